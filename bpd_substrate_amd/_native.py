@@ -1,0 +1,93 @@
+"""Loading of the in-tree native libraries, with ctypes signatures.
+
+The argtypes follow the reference's own ctypes declarations (every pointer
+c_void_p, every size c_int, void returns): bench/verify_quant_gpu.py:27-42,
+bench/bench_gpu_sweep.py:6-20, bench/bench_dequant_gpu_h2h.py:5-13,
+bench/test_gemm_q8_0_tiles.py:42-69.
+There is no fallback: if libbpdq_hip.so is missing the import of the GPU entry
+points fails with an error naming the build command.
+"""
+import ctypes
+import os
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+HIP_LIB = os.path.join(PKG, "libbpdq_hip.so")
+SYNTH_LIB = os.path.join(PKG, "libbpdq_synth.so")
+
+P, I, F = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
+
+# name -> (restype, argtypes); the full exported surface of include/bpdq.h
+HIP_SIGNATURES = {
+    "bpd_gpu_last_error": (I, []),
+    "bpd_gpu_last_error_message": (ctypes.c_char_p, []),
+    "bpd_gpu_set_stream": (None, [P]),
+    "bpd_dequant_q4k_gpu": (None, [P, P, I]),
+    "bpd_qmatmul_q4k_gpu": (None, [P, P, P, I, I]),
+    "qgpu_alloc": (P, [I]),
+    "qgpu_free": (None, [P]),
+    "qgpu_h2d": (None, [P, P, I]),
+    "qgpu_d2h": (None, [P, P, I]),
+    "qgpu_sync": (None, []),
+    "dequant_v1_256": (None, [P, P, I]),
+    "dequant_v1_128": (None, [P, P, I]),
+    "dequant_v1_64": (None, [P, P, I]),
+    "dequant_v1_32": (None, [P, P, I]),
+    "dequant_ilp2": (None, [P, P, I]),
+    "dequant_multi2": (None, [P, P, I]),
+    "dequant_multi4": (None, [P, P, I]),
+    "dequant_multi8": (None, [P, P, I]),
+    "sgpu_alloc": (P, [I]),
+    "sgpu_free": (None, [P]),
+    "sgpu_h2d": (None, [P, P, I]),
+    "sgpu_d2h": (None, [P, P, I]),
+    "sgpu_sync": (None, []),
+    "run_llamacpp": (None, [P, P, I]),
+    "run_bpd": (None, [P, P, I]),
+    "galloc": (P, [I]),
+    "gfree": (None, [P]),
+    "gh2d": (None, [P, P, I]),
+    "gd2h": (None, [P, P, I]),
+    "gsync": (None, []),
+    "bpd_dequant_q4k_gguf_gpu": (None, [P, P, I]),
+    "bpd_quant_q8_k_gpu": (None, [P, P, I]),
+    "bpd_qmatmul_q4k_q8k_gpu": (None, [P, P, P, I, I]),
+    "bpd_qmatmul_q4k_q8k_gguf_gpu": (None, [P, P, P, I, I]),
+    "bpd_dequant_q8_0_gpu": (None, [P, P, I]),
+    "bpd_embed_lookup_q8_0_gpu": (None, [P, P, P, I, I]),
+    "bpd_quant_q8_0_gpu": (None, [P, P, I]),
+    "bpd_qmatmul_q8_0_dispatch_gpu": (None, [P, P, P, I, I, I]),
+    "bpd_qmatmul_q8_0_llamafile_gpu": (None, [P, P, P, I, I, I]),
+}
+
+SYNTH_SIGNATURES = {
+    "bpdq_synth_key": (ctypes.c_uint64, [ctypes.c_uint64, ctypes.c_uint64]),
+    "bpdq_synth_q4k": (None, [P, ctypes.c_int64, ctypes.c_uint64, ctypes.c_double, ctypes.c_double, I]),
+    "bpdq_synth_q8_0": (None, [P, ctypes.c_int64, ctypes.c_uint64, ctypes.c_double, I]),
+    "bpdq_synth_normal_f32": (None, [P, ctypes.c_int64, ctypes.c_uint64, ctypes.c_double, I]),
+    "bpdq_synth_bytes": (None, [P, ctypes.c_int64, ctypes.c_uint64, I]),
+}
+
+_cache = {}
+
+
+def _load(path, sigs, what):
+    if path in _cache:
+        return _cache[path]
+    if not os.path.exists(path):
+        raise RuntimeError(f"{what} is not built ({path} missing): run `python -m bpd_substrate_amd.build`")
+    lib = ctypes.CDLL(path)
+    for name, (res, args) in sigs.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _cache[path] = lib
+    return lib
+
+
+def load_hip():
+    """The gfx950 library (libbpdq_hip.so). Raises if it has not been built."""
+    return _load(HIP_LIB, HIP_SIGNATURES, "libbpdq_hip.so")
+
+
+def load_synth():
+    return _load(SYNTH_LIB, SYNTH_SIGNATURES, "libbpdq_synth.so")

@@ -1,0 +1,303 @@
+// abi.hip — the exported C ABI (include/bpdq.h): argument validation, error
+// recording, stream selection and the launches.  Nothing here computes on the
+// CPU: every numeric result comes from a gfx950 kernel.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+
+#include "../../include/bpdq.h"
+#include "bpdq_launch.h"
+
+namespace {
+
+thread_local int g_err = BPDQ_OK;
+thread_local char g_msg[256] = "";
+hipStream_t g_stream = nullptr;
+
+void set_err(int code, const char* fn, const char* what) {
+    if (g_err == BPDQ_OK) g_err = code;
+    std::snprintf(g_msg, sizeof g_msg, "%s: %s", fn, what);
+}
+
+bool hip_ok(hipError_t e, const char* fn) {
+    if (e == hipSuccess) return true;
+    set_err(BPDQ_ERR_HIP, fn, hipGetErrorString(e));
+    return false;
+}
+
+// After a launch: report launch-configuration errors without synchronizing.
+void check_launch(const char* fn) { hip_ok(hipGetLastError(), fn); }
+
+bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+// Validation shared by the entry points.  Returns false (and records why) if
+// nothing should be launched; `empty` is set when there is no work.
+struct Check {
+    const char* fn;
+    bool ok = true;
+    explicit Check(const char* f) : fn(f) {}
+    Check& nonneg(int v, const char* name) {
+        if (ok && v < 0) fail(BPDQ_ERR_SHAPE, name, "is negative");
+        return *this;
+    }
+    Check& multiple(int v, int m, const char* name) {
+        if (ok && v % m != 0) {
+            char buf[96];
+            std::snprintf(buf, sizeof buf, "%s=%d is not a multiple of %d", name, v, m);
+            set_err(BPDQ_ERR_SHAPE, fn, buf);
+            ok = false;
+        }
+        return *this;
+    }
+    Check& ptr(const void* p, uintptr_t align, const char* name) {
+        if (!ok) return *this;
+        if (p == nullptr) fail(BPDQ_ERR_NULL, name, "is NULL");
+        else if (!aligned(p, align)) {
+            char buf[96];
+            std::snprintf(buf, sizeof buf, "%s is not %d-byte aligned", name, (int)align);
+            set_err(BPDQ_ERR_ALIGN, fn, buf);
+            ok = false;
+        }
+        return *this;
+    }
+    void fail(int code, const char* name, const char* what) {
+        char buf[96];
+        std::snprintf(buf, sizeof buf, "%s %s", name, what);
+        set_err(code, fn, buf);
+        ok = false;
+    }
+};
+
+// Device workspace for the quantized activations of the llamafile path (the
+// reference mallocs it per call, bench/bpd_cpu.c:4441).  Grown on demand;
+// calls that overlap on different streams must not share it.
+std::mutex g_ws_mu;
+void* g_ws = nullptr;
+size_t g_ws_bytes = 0;
+
+void* workspace(size_t bytes, const char* fn) {
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    if (bytes <= g_ws_bytes) return g_ws;
+    if (g_ws) {
+        if (!hip_ok(hipDeviceSynchronize(), fn)) return nullptr;
+        (void)hipFree(g_ws);
+        g_ws = nullptr;
+        g_ws_bytes = 0;
+    }
+    if (hipMalloc(&g_ws, bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        set_err(BPDQ_ERR_ALLOC, fn, "workspace allocation failed");
+        g_ws = nullptr;
+        return nullptr;
+    }
+    g_ws_bytes = bytes;
+    return g_ws;
+}
+
+void dequant_q4k(const uint8_t* q, float* out, int nb, int order, const char* fn) {
+    Check c(fn);
+    c.nonneg(nb, "n_blocks");
+    if (!c.ok || nb == 0) return;
+    c.ptr(q, 16, "q").ptr(out, 16, "out");
+    if (!c.ok) return;
+    bpdq::launch_dequant_q4k(q, out, nb, order, g_stream);
+    check_launch(fn);
+}
+
+void* alloc(int bytes, const char* fn) {
+    if (bytes < 0) {
+        set_err(BPDQ_ERR_SHAPE, fn, "bytes is negative");
+        return nullptr;
+    }
+    if (bytes == 0) return nullptr;
+    void* p = nullptr;
+    if (hipMalloc(&p, (size_t)bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        set_err(BPDQ_ERR_ALLOC, fn, "hipMalloc failed");
+        return nullptr;
+    }
+    return p;
+}
+
+void copy(void* dst, const void* src, int bytes, hipMemcpyKind kind, const char* fn) {
+    Check c(fn);
+    c.nonneg(bytes, "bytes");
+    if (!c.ok || bytes == 0) return;
+    c.ptr(dst, 1, "dst").ptr(src, 1, "src");
+    if (!c.ok) return;
+    hip_ok(hipMemcpy(dst, src, (size_t)bytes, kind), fn);
+}
+
+void q4k_q8k(const uint8_t* w, const uint8_t* xq, float* y, int M, int K, int order, const char* fn) {
+    Check c(fn);
+    c.nonneg(M, "M").nonneg(K, "K").multiple(K, 256, "K");
+    if (!c.ok || M == 0) return;
+    c.ptr(y, 4, "y");
+    if (K > 0) c.ptr(w, 16, "w").ptr(xq, 4, "xq");
+    if (!c.ok) return;
+    bpdq::launch_qmatmul_q4k_q8k(w, xq, y, M, K, order, g_stream);
+    check_launch(fn);
+}
+
+}  // namespace
+
+extern "C" {
+
+int bpd_gpu_last_error(void) {
+    const int e = g_err;
+    g_err = BPDQ_OK;
+    return e;
+}
+
+const char* bpd_gpu_last_error_message(void) { return g_msg; }
+
+void bpd_gpu_set_stream(void* s) { g_stream = static_cast<hipStream_t>(s); }
+
+// ---- Q4_K -------------------------------------------------------------------
+void bpd_dequant_q4k_gpu(const uint8_t* q, float* out, int n_blocks) {
+    dequant_q4k(q, out, n_blocks, 0, "bpd_dequant_q4k_gpu");
+}
+
+void bpd_dequant_q4k_gguf_gpu(const uint8_t* q, float* out, int n_blocks) {
+    dequant_q4k(q, out, n_blocks, 1, "bpd_dequant_q4k_gguf_gpu");
+}
+
+void bpd_qmatmul_q4k_gpu(const uint8_t* w, const float* x, float* y, int M, int K) {
+    const char* fn = "bpd_qmatmul_q4k_gpu";
+    Check c(fn);
+    c.nonneg(M, "M").nonneg(K, "K").multiple(K, 256, "K");
+    if (!c.ok || M == 0) return;
+    c.ptr(y, 4, "y");
+    if (K > 0) c.ptr(w, 16, "w").ptr(x, 4, "x");
+    if (!c.ok) return;
+    bpdq::launch_qmatmul_q4k_chain(w, x, y, M, K, g_stream);
+    check_launch(fn);
+}
+
+void bpd_quant_q8_k_gpu(const float* x, uint8_t* y, int n) {
+    const char* fn = "bpd_quant_q8_k_gpu";
+    Check c(fn);
+    c.nonneg(n, "n").multiple(n, 256, "n");
+    if (!c.ok || n == 0) return;
+    c.ptr(x, 16, "x").ptr(y, 4, "y");
+    if (!c.ok) return;
+    bpdq::launch_quant_q8k(x, y, n, g_stream);
+    check_launch(fn);
+}
+
+void bpd_qmatmul_q4k_q8k_gpu(const uint8_t* w, const uint8_t* xq, float* y, int M, int K) {
+    q4k_q8k(w, xq, y, M, K, 0, "bpd_qmatmul_q4k_q8k_gpu");
+}
+
+void bpd_qmatmul_q4k_q8k_gguf_gpu(const uint8_t* w, const uint8_t* xq, float* y, int M, int K) {
+    q4k_q8k(w, xq, y, M, K, 1, "bpd_qmatmul_q4k_q8k_gguf_gpu");
+}
+
+void* qgpu_alloc(int bytes) { return alloc(bytes, "qgpu_alloc"); }
+void qgpu_free(void* p) {
+    if (p) hip_ok(hipFree(p), "qgpu_free");
+}
+void qgpu_h2d(void* d, const void* s, int bytes) { copy(d, s, bytes, hipMemcpyHostToDevice, "qgpu_h2d"); }
+void qgpu_d2h(void* d, const void* s, int bytes) { copy(d, s, bytes, hipMemcpyDeviceToHost, "qgpu_d2h"); }
+void qgpu_sync(void) { hip_ok(hipDeviceSynchronize(), "qgpu_sync"); }
+
+// ---- sweep / head-to-head aliases ---------------------------------------------
+void dequant_v1_256(const uint8_t* q, float* o, int nb) { dequant_q4k(q, o, nb, 0, "dequant_v1_256"); }
+void dequant_v1_128(const uint8_t* q, float* o, int nb) { dequant_q4k(q, o, nb, 0, "dequant_v1_128"); }
+void dequant_v1_64(const uint8_t* q, float* o, int nb) { dequant_q4k(q, o, nb, 0, "dequant_v1_64"); }
+void dequant_v1_32(const uint8_t* q, float* o, int nb) { dequant_q4k(q, o, nb, 0, "dequant_v1_32"); }
+void dequant_ilp2(const uint8_t* q, float* o, int nb) { dequant_q4k(q, o, nb, 0, "dequant_ilp2"); }
+void dequant_multi2(const uint8_t* q, float* o, int nb) { dequant_q4k(q, o, nb, 0, "dequant_multi2"); }
+void dequant_multi4(const uint8_t* q, float* o, int nb) { dequant_q4k(q, o, nb, 0, "dequant_multi4"); }
+void dequant_multi8(const uint8_t* q, float* o, int nb) { dequant_q4k(q, o, nb, 0, "dequant_multi8"); }
+void* sgpu_alloc(int bytes) { return alloc(bytes, "sgpu_alloc"); }
+void sgpu_free(void* p) {
+    if (p) hip_ok(hipFree(p), "sgpu_free");
+}
+void sgpu_h2d(void* d, const void* s, int bytes) { copy(d, s, bytes, hipMemcpyHostToDevice, "sgpu_h2d"); }
+void sgpu_d2h(void* d, const void* s, int bytes) { copy(d, s, bytes, hipMemcpyDeviceToHost, "sgpu_d2h"); }
+void sgpu_sync(void) { hip_ok(hipDeviceSynchronize(), "sgpu_sync"); }
+
+void run_llamacpp(const void* q, float* o, int nb) {
+    dequant_q4k(static_cast<const uint8_t*>(q), o, nb, 1, "run_llamacpp");
+}
+void run_bpd(const void* q, float* o, int nb) { dequant_q4k(static_cast<const uint8_t*>(q), o, nb, 1, "run_bpd"); }
+void* galloc(int bytes) { return alloc(bytes, "galloc"); }
+void gfree(void* p) {
+    if (p) hip_ok(hipFree(p), "gfree");
+}
+void gh2d(void* d, const void* s, int bytes) { copy(d, s, bytes, hipMemcpyHostToDevice, "gh2d"); }
+void gd2h(void* d, const void* s, int bytes) { copy(d, s, bytes, hipMemcpyDeviceToHost, "gd2h"); }
+void gsync(void) { hip_ok(hipDeviceSynchronize(), "gsync"); }
+
+// ---- Q8_0 ---------------------------------------------------------------------
+void bpd_dequant_q8_0_gpu(const uint8_t* raw, float* out, int n_blocks) {
+    const char* fn = "bpd_dequant_q8_0_gpu";
+    Check c(fn);
+    c.nonneg(n_blocks, "n_blocks");
+    if (!c.ok || n_blocks == 0) return;
+    c.ptr(raw, 1, "raw").ptr(out, 4, "out");
+    if (!c.ok) return;
+    bpdq::launch_dequant_q8_0(raw, out, n_blocks, g_stream);
+    check_launch(fn);
+}
+
+void bpd_embed_lookup_q8_0_gpu(const uint8_t* table, const int32_t* ids, float* out, int n_tokens, int embed_dim) {
+    const char* fn = "bpd_embed_lookup_q8_0_gpu";
+    Check c(fn);
+    c.nonneg(n_tokens, "n_tokens").nonneg(embed_dim, "embed_dim").multiple(embed_dim, 32, "embed_dim");
+    if (!c.ok || n_tokens == 0 || embed_dim == 0) return;
+    c.ptr(table, 1, "table").ptr(ids, 4, "token_ids").ptr(out, 4, "out");
+    if (!c.ok) return;
+    bpdq::launch_embed_q8_0(table, ids, out, n_tokens, embed_dim, g_stream);
+    check_launch(fn);
+}
+
+void bpd_quant_q8_0_gpu(const float* x, uint8_t* y, int n_elements) {
+    const char* fn = "bpd_quant_q8_0_gpu";
+    Check c(fn);
+    c.nonneg(n_elements, "n_elements").multiple(n_elements, 32, "n_elements");
+    if (!c.ok || n_elements == 0) return;
+    c.ptr(x, 4, "x").ptr(y, 1, "y");
+    if (!c.ok) return;
+    bpdq::launch_quant_q8_0(x, y, n_elements, g_stream);
+    check_launch(fn);
+}
+
+void bpd_qmatmul_q8_0_dispatch_gpu(const uint8_t* Wq, const uint8_t* Xq, float* out, int m_weight, int m_tokens,
+                                   int K) {
+    const char* fn = "bpd_qmatmul_q8_0_dispatch_gpu";
+    Check c(fn);
+    c.nonneg(m_weight, "m_weight").nonneg(m_tokens, "m_tokens").nonneg(K, "K").multiple(K, 32, "K");
+    if (!c.ok || m_weight == 0 || m_tokens == 0) return;
+    c.ptr(out, 4, "out");
+    if (K > 0) c.ptr(Wq, 1, "W_q8_0").ptr(Xq, 1, "X_q8_0");
+    if (!c.ok) return;
+    bpdq::launch_q8_0_dispatch_T(Wq, Xq, out, m_weight, m_tokens, K, g_stream);
+    check_launch(fn);
+}
+
+void bpd_qmatmul_q8_0_llamafile_gpu(const uint8_t* W, const float* X, float* out, int m_weight, int m_tokens, int K) {
+    const char* fn = "bpd_qmatmul_q8_0_llamafile_gpu";
+    Check c(fn);
+    c.nonneg(m_weight, "m_weight").nonneg(m_tokens, "m_tokens").nonneg(K, "K").multiple(K, 32, "K");
+    if (!c.ok || m_weight == 0 || m_tokens == 0) return;
+    c.ptr(out, 4, "out");
+    if (K > 0) c.ptr(W, 1, "W_q8_0").ptr(X, 4, "X_f32");
+    if (!c.ok) return;
+    const size_t xq_bytes = (size_t)m_tokens * (size_t)(K / 32) * 34;
+    uint8_t* xq = nullptr;
+    if (xq_bytes > 0) {
+        xq = static_cast<uint8_t*>(workspace(xq_bytes, fn));
+        if (!xq) return;
+        // K % 32 == 0, so the flat m_tokens*K array quantizes to the same blocks as row by row.
+        bpdq::launch_quant_q8_0(X, xq, (int64_t)m_tokens * K, g_stream);
+        check_launch(fn);
+    }
+    bpdq::launch_q8_0_dispatch_T(W, xq, out, m_weight, m_tokens, K, g_stream);
+    check_launch(fn);
+}
+
+}  // extern "C"

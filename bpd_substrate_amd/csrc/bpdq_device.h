@@ -1,0 +1,76 @@
+// bpdq_device.h — device helpers shared by the gfx950 kernels.
+//
+// All kernels are compiled with -ffp-contract=off: every fp32 expression is the
+// sequence of IEEE operations written, and an FMA appears only where fmaf() is
+// called explicitly (and only where it is provably equal to the unfused form).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace bpdq {
+
+constexpr int kQ4KBytes = 144;   // {f16 d, f16 dmin, u8 scales[12], u8 qs[128]}
+constexpr int kQ8KBytes = 292;   // {f32 d, i8 qs[256], i16 bsums[16]}
+constexpr int kQ80Bytes = 34;    // {f16 d, i8 qs[32]}
+
+// IEEE binary16 -> binary32 (v_cvt_f32_f16): exact for every finite input and
+// for +/-0 and +/-Inf.  NaN stays NaN.
+__device__ __forceinline__ float f16_ieee(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(h & 0xFFFFu));
+}
+
+// The decode of /root/reference/bench/bench_dequant_gpu_h2h.cu:14-19: both
+// zeros -> +0.0, exponent 31 (Inf or NaN) -> +/-Inf, all else exact.
+__device__ __forceinline__ float f16_h2h(uint32_t h) {
+    h &= 0xFFFFu;
+    if ((h & 0x7FFFu) == 0) return 0.0f;
+    if ((h & 0x7C00u) == 0x7C00u) return (h & 0x8000u) ? -__builtin_inff() : __builtin_inff();
+    return f16_ieee(h);
+}
+
+// 6-bit scale and min of sub-block j from the 12 scale bytes held in three
+// dwords s0 = bytes 0..3, s1 = bytes 4..7, s2 = bytes 8..11
+// (layout of /root/reference/bench/bpd_quant.c:56-62).
+__device__ __forceinline__ void q4k_scale_min(uint32_t s0, uint32_t s1, uint32_t s2, int j, int& sc, int& m) {
+    if (j < 4) {
+        const int sh = 8 * j;
+        sc = (int)((s0 >> sh) & 63u);
+        m = (int)((s1 >> sh) & 63u);
+    } else {
+        const int sh = 8 * (j - 4);
+        sc = (int)(((s2 >> sh) & 15u) | (((s0 >> (sh + 6)) & 3u) << 4));
+        m = (int)(((s2 >> (sh + 4)) & 15u) | (((s1 >> (sh + 6)) & 3u) << 4));
+    }
+}
+
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// Cross-lane moves inside a wave64.
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, true);
+}
+__device__ __forceinline__ float xor_f(float v, int mask) { return __shfl_xor(v, mask, 64); }
+__device__ __forceinline__ int xor_i(int v, int mask) { return __shfl_xor(v, mask, 64); }
+
+// Sum of an int over each aligned group of 8 lanes (exact; order irrelevant).
+__device__ __forceinline__ int sum8_i(int v) {
+    v += dpp_i<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_i<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_i<0x141>(v);  // row_half_mirror: lane i <-> 7-i inside each 8
+    return v;
+}
+
+__device__ __forceinline__ uint32_t ld_u32(const uint8_t* p) {
+    uint32_t v;
+    __builtin_memcpy(&v, p, 4);
+    return v;
+}
+
+__device__ __forceinline__ uint4 ld_u128(const uint8_t* p) {
+    return *reinterpret_cast<const uint4*>(p);
+}
+
+}  // namespace bpdq

@@ -1,0 +1,22 @@
+// bpdq_launch.h — host-side launchers of the gfx950 kernels (internal to
+// libbpdq_hip.so; the exported C ABI is include/bpdq.h).  Callers have already
+// validated every argument: shapes, multiples, pointer alignment.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace bpdq {
+
+void launch_dequant_q4k(const uint8_t* q, float* out, int n_blocks, int order, hipStream_t s);
+void launch_qmatmul_q4k_chain(const uint8_t* w, const float* x, float* y, int M, int K, hipStream_t s);
+void launch_quant_q8k(const float* x, uint8_t* y, int n, hipStream_t s);
+void launch_qmatmul_q4k_q8k(const uint8_t* w, const uint8_t* xq, float* y, int M, int K, int order, hipStream_t s);
+
+void launch_dequant_q8_0(const uint8_t* raw, float* out, int n_blocks, hipStream_t s);
+void launch_embed_q8_0(const uint8_t* table, const int32_t* ids, float* out, int n_tokens, int embed_dim,
+                       hipStream_t s);
+void launch_quant_q8_0(const float* x, uint8_t* y, int64_t n_elements, hipStream_t s);
+void launch_q8_0_dispatch_T(const uint8_t* Wq, const uint8_t* Xq, float* out, int m_weight, int m_tokens, int K,
+                            hipStream_t s);
+
+}  // namespace bpdq

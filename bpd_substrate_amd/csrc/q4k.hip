@@ -1,0 +1,252 @@
+// q4k.hip — Q4_K super-block kernels for gfx950.
+//
+//   k_dequant_q4k<ORDER>   Q4_K -> fp32, bpd element map or GGUF element map
+//   k_qmatmul_q4k_chain    reference-order GEMV with fp32 x (one fp32 chain per row)
+//   k_quant_q8k            fp32 -> Q8_K activation blocks
+//   k_q4k_q8k_gemv<ORDER,R> Q4_K x Q8_K GEMV, integer sub-block sums + fixed fp32 tree
+#include "bpdq_device.h"
+#include "bpdq_launch.h"
+
+namespace bpdq {
+
+// ----------------------------------------------------------------------------
+// Dequant.  Thread t (0..31) of a Q4_K block owns qs dword t (bytes 4t..4t+3)
+// and writes its 4 low nibbles and its 4 high nibbles as two float4 stores.
+//   bpd map  (bench/bpd_quant.c:68-72):   low -> 32(t/4)+4(t%4), high = low+16,
+//                                          both in sub-block t/4
+//   GGUF map (bench_dequant_gpu_h2h.cu:31-46): low -> 64(t/8)+4(t%8), high = low+32,
+//                                          sub-blocks 2(t/8) and 2(t/8)+1
+// y = RN(d*sc*q - dmin*m): d*sc and (d*sc)*q are exact in fp32, so
+// fmaf(d*sc, q, -dmin*m) equals the reference's multiply-then-subtract bit for bit.
+// ----------------------------------------------------------------------------
+template <int ORDER>
+__global__ __launch_bounds__(256) void k_dequant_q4k(const uint8_t* __restrict__ q, float* __restrict__ out,
+                                                     int n_blocks) {
+    const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t b = g >> 5;
+    const int t = (int)(g & 31);
+    if (b >= n_blocks) return;
+    const uint8_t* blk = q + b * kQ4KBytes;
+    const uint4 hdr = ld_u128(blk);
+    const uint32_t qw = ld_u32(blk + 16 + 4 * t);
+    float d, dmin;
+    int j_lo, j_hi, e_lo, e_hi;
+    if (ORDER == 0) {
+        d = f16_ieee(hdr.x);
+        dmin = f16_ieee(hdr.x >> 16);
+        j_lo = j_hi = t >> 2;
+        e_lo = 32 * (t >> 2) + 4 * (t & 3);
+        e_hi = e_lo + 16;
+    } else {
+        d = f16_h2h(hdr.x);
+        dmin = f16_h2h(hdr.x >> 16);
+        j_lo = 2 * (t >> 3);
+        j_hi = j_lo + 1;
+        e_lo = 64 * (t >> 3) + 4 * (t & 7);
+        e_hi = e_lo + 32;
+    }
+    int sc, m;
+    q4k_scale_min(hdr.y, hdr.z, hdr.w, j_lo, sc, m);
+    const float s_lo = d * (float)sc, m_lo = dmin * (float)m;
+    q4k_scale_min(hdr.y, hdr.z, hdr.w, j_hi, sc, m);
+    const float s_hi = d * (float)sc, m_hi = dmin * (float)m;
+    const uint32_t lo = qw & 0x0F0F0F0Fu, hi = (qw >> 4) & 0x0F0F0F0Fu;
+    float4 vlo, vhi;
+    vlo.x = fmaf(s_lo, (float)(lo & 0xFFu), -m_lo);
+    vlo.y = fmaf(s_lo, (float)((lo >> 8) & 0xFFu), -m_lo);
+    vlo.z = fmaf(s_lo, (float)((lo >> 16) & 0xFFu), -m_lo);
+    vlo.w = fmaf(s_lo, (float)(lo >> 24), -m_lo);
+    vhi.x = fmaf(s_hi, (float)(hi & 0xFFu), -m_hi);
+    vhi.y = fmaf(s_hi, (float)((hi >> 8) & 0xFFu), -m_hi);
+    vhi.z = fmaf(s_hi, (float)((hi >> 16) & 0xFFu), -m_hi);
+    vhi.w = fmaf(s_hi, (float)(hi >> 24), -m_hi);
+    float* y = out + b * 256;
+    *reinterpret_cast<float4*>(y + e_lo) = vlo;
+    *reinterpret_cast<float4*>(y + e_hi) = vhi;
+}
+
+void launch_dequant_q4k(const uint8_t* q, float* out, int n_blocks, int order, hipStream_t s) {
+    const int64_t threads = (int64_t)n_blocks * 32;
+    const dim3 grid((unsigned)((threads + 255) / 256));
+    if (order == 0)
+        hipLaunchKernelGGL(k_dequant_q4k<0>, grid, dim3(256), 0, s, q, out, n_blocks);
+    else
+        hipLaunchKernelGGL(k_dequant_q4k<1>, grid, dim3(256), 0, s, q, out, n_blocks);
+}
+
+// ----------------------------------------------------------------------------
+// Reference-order GEMV with fp32 x (bench/bpd_quant.c:88-109): one lane per row
+// runs y = (((0 + w0*x0) + w1*x1) + ...) over k in bpd element order, each
+// product and each sum rounded once.  Rows are independent, so this is
+// bit-identical to the CPU reference; the chain itself is serial by definition.
+// ----------------------------------------------------------------------------
+__global__ __launch_bounds__(64) void k_qmatmul_q4k_chain(const uint8_t* __restrict__ w, const float* __restrict__ x,
+                                                          float* __restrict__ y, int M, int nb) {
+    const int row = blockIdx.x * 64 + threadIdx.x;
+    if (row >= M) return;
+    const uint8_t* rp = w + (int64_t)row * nb * kQ4KBytes;
+    float sum = 0.0f;
+    for (int b = 0; b < nb; b++) {
+        const uint8_t* blk = rp + (int64_t)b * kQ4KBytes;
+        const uint4 hdr = ld_u128(blk);
+        const float d = f16_ieee(hdr.x), dmin = f16_ieee(hdr.x >> 16);
+        const float* xb = x + (int64_t)b * 256;
+        for (int j = 0; j < 8; j++) {
+            int sc, m;
+            q4k_scale_min(hdr.y, hdr.z, hdr.w, j, sc, m);
+            const float scale = d * (float)sc, mn = dmin * (float)m;
+            const uint4 qv = ld_u128(blk + 16 + 16 * j);
+            const uint32_t qd[4] = {qv.x, qv.y, qv.z, qv.w};
+#pragma unroll
+            for (int k = 0; k < 16; k++) {
+                const float v = fmaf(scale, (float)((qd[k >> 2] >> (8 * (k & 3))) & 15u), -mn);
+                sum = sum + v * xb[32 * j + k];
+            }
+#pragma unroll
+            for (int k = 0; k < 16; k++) {
+                const float v = fmaf(scale, (float)((qd[k >> 2] >> (8 * (k & 3) + 4)) & 15u), -mn);
+                sum = sum + v * xb[32 * j + 16 + k];
+            }
+        }
+    }
+    y[row] = sum;
+}
+
+void launch_qmatmul_q4k_chain(const uint8_t* w, const float* x, float* y, int M, int K, hipStream_t s) {
+    hipLaunchKernelGGL(k_qmatmul_q4k_chain, dim3((M + 63) / 64), dim3(64), 0, s, w, x, y, M, K / 256);
+}
+
+// ----------------------------------------------------------------------------
+// Q8_K quantizer: one wave per 256-element block, lane l holds elements 4l..4l+3.
+// d = RN(amax/127), id = amax ? RN(127/amax) : 0, q = rint(RN(x*id)),
+// bsums[g] = sum of q[16g..16g+15] (lanes 4g..4g+3).
+// ----------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_quant_q8k(const float* __restrict__ x, uint8_t* __restrict__ y, int nb) {
+    const int lane = threadIdx.x & 63;
+    const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (b >= nb) return;
+    const float4 v = *reinterpret_cast<const float4*>(x + (int64_t)b * 256 + 4 * lane);
+    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+#pragma unroll
+    for (int mask = 1; mask < 64; mask <<= 1) amax = fmaxf(amax, xor_f(amax, mask));
+    const float d = amax / 127.0f;
+    const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+    const int q0 = (int)__builtin_rintf(v.x * id), q1 = (int)__builtin_rintf(v.y * id);
+    const int q2 = (int)__builtin_rintf(v.z * id), q3 = (int)__builtin_rintf(v.w * id);
+    uint8_t* yb = y + (int64_t)b * kQ8KBytes;
+    const uint32_t packed = (uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) | ((uint32_t)(q2 & 0xFF) << 16) |
+                            ((uint32_t)(q3 & 0xFF) << 24);
+    *reinterpret_cast<uint32_t*>(yb + 4 + 4 * lane) = packed;
+    int s = q0 + q1 + q2 + q3;
+    s += dpp_i<0xB1>(s);
+    s += dpp_i<0x4E>(s);
+    if ((lane & 3) == 0) *reinterpret_cast<int16_t*>(yb + 260 + 2 * (lane >> 2)) = (int16_t)s;
+    if (lane == 0) *reinterpret_cast<float*>(yb) = d;
+}
+
+void launch_quant_q8k(const float* x, uint8_t* y, int n, hipStream_t s) {
+    const int nb = n / 256;
+    hipLaunchKernelGGL(k_quant_q8k, dim3((nb + 3) / 4), dim3(256), 0, s, x, y, nb);
+}
+
+// ----------------------------------------------------------------------------
+// Q4_K x Q8_K GEMV.  A wave covers R rows.  Lane (q = lane/8, c = lane%8) owns
+// qs bytes 16c..16c+15 of super-block 8t+q in every block-group t: one 16-B load
+// per lane, so a wave instruction reads the qs of 8 consecutive super-blocks.
+//   bpd map: those 16 bytes are exactly sub-block c (low nibbles with x[32c+k],
+//            high nibbles with x[32c+16+k]).
+//   GGUF map: low nibbles are elements 64(c/2)+16(c%2)+k of sub-block 2(c/2),
+//            high nibbles the same +32, of sub-block 2(c/2)+1.
+// Integer partials are summed exactly over the 8 lanes of a super-block; the
+// fp32 combine and the per-row tree are the fixed order documented in
+// the C restatement: slot sums s_q from +0.0 over b = q mod 8 ascending, then
+// ((s0+s1)+(s2+s3)) + ((s4+s5)+(s6+s7)) as an xor-8/16/32 butterfly.
+// ----------------------------------------------------------------------------
+template <int ORDER, int R>
+__global__ __launch_bounds__(256) void k_q4k_q8k_gemv(const uint8_t* __restrict__ w, const uint8_t* __restrict__ xq,
+                                                      float* __restrict__ y, int M, int nb) {
+    const int lane = threadIdx.x & 63;
+    const int q = lane >> 3, c = lane & 7;
+    const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
+    if (row0 >= M) return;
+    const int64_t row_bytes = (int64_t)nb * kQ4KBytes;
+    float s[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) s[r] = 0.0f;
+
+    for (int t = 0; t * 8 < nb; t++) {
+        const int b = t * 8 + q;
+        const bool valid = b < nb;
+        const int bb = valid ? b : nb - 1;
+        const uint8_t* xb = xq + (int64_t)bb * kQ8KBytes;
+        const float dy = *reinterpret_cast<const float*>(xb);
+        const uint32_t bs = ld_u32(xb + 260 + 4 * c);
+        const int bsum = (int)(int16_t)(bs & 0xFFFFu) + (int)(int16_t)(bs >> 16);
+        uint32_t xl[4], xh[4];
+        {
+            const int off_lo = ORDER == 0 ? 32 * c : 64 * (c >> 1) + 16 * (c & 1);
+            const int off_hi = ORDER == 0 ? 32 * c + 16 : off_lo + 32;
+            const uint8_t* p = xb + 4;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                xl[k] = ld_u32(p + off_lo + 4 * k);
+                xh[k] = ld_u32(p + off_hi + 4 * k);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const int row = min(row0 + r, M - 1);
+            const uint8_t* blk = w + (int64_t)row * row_bytes + (int64_t)bb * kQ4KBytes;
+            const uint4 hdr = ld_u128(blk);
+            const uint4 qv = ld_u128(blk + 16 + 16 * c);
+            const uint32_t qd[4] = {qv.x, qv.y, qv.z, qv.w};
+            int s_lo = 0, s_hi = 0;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                s_lo = sdot4(qd[k] & 0x0F0F0F0Fu, xl[k], s_lo);
+                s_hi = sdot4((qd[k] >> 4) & 0x0F0F0F0Fu, xh[k], s_hi);
+            }
+            int sc, m, isum;
+            if (ORDER == 0) {
+                q4k_scale_min(hdr.y, hdr.z, hdr.w, c, sc, m);
+                isum = sc * (s_lo + s_hi);
+            } else {
+                int sc2, m2;
+                q4k_scale_min(hdr.y, hdr.z, hdr.w, 2 * (c >> 1), sc, m2);
+                q4k_scale_min(hdr.y, hdr.z, hdr.w, 2 * (c >> 1) + 1, sc2, m2);
+                isum = sc * s_lo + sc2 * s_hi;
+                q4k_scale_min(hdr.y, hdr.z, hdr.w, c, sc2, m);
+            }
+            int msum = m * bsum;
+            isum = sum8_i(isum);
+            msum = sum8_i(msum);
+            const float dd = f16_ieee(hdr.x) * dy;
+            const float dm = f16_ieee(hdr.x >> 16) * dy;
+            const float a = dd * (float)isum;
+            const float mm = dm * (float)msum;
+            const float cb = a - mm;
+            if (valid) s[r] = s[r] + cb;
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        float v = s[r];
+        v = v + xor_f(v, 8);
+        v = v + xor_f(v, 16);
+        v = v + xor_f(v, 32);
+        if (lane == 0 && row0 + r < M) y[row0 + r] = v;
+    }
+}
+
+void launch_qmatmul_q4k_q8k(const uint8_t* w, const uint8_t* xq, float* y, int M, int K, int order, hipStream_t s) {
+    constexpr int R = 4;
+    const int nb = K / 256;
+    const int waves = (M + R - 1) / R;
+    const dim3 grid((waves + 3) / 4);
+    if (order == 0)
+        hipLaunchKernelGGL((k_q4k_q8k_gemv<0, R>), grid, dim3(256), 0, s, w, xq, y, M, nb);
+    else
+        hipLaunchKernelGGL((k_q4k_q8k_gemv<1, R>), grid, dim3(256), 0, s, w, xq, y, M, nb);
+}
+
+}  // namespace bpdq

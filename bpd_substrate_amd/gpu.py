@@ -1,0 +1,165 @@
+"""Host-side mirror of the reference's GPU entry points, over libbpdq_hip.so.
+
+Two layers:
+
+* `call(name, *args)` — the C ABI exactly as the reference's ctypes callers
+  use it (bench/verify_quant_gpu.py:27-42 and friends): device pointers as ints,
+  sizes as ints.  Torch tensors are accepted wherever a pointer is and are
+  passed as their data_ptr().  After the call the library's error slot is read
+  and a BpdqError is raised if the arguments were rejected or HIP failed.
+* tensor helpers (`dequant_q4k`, `qmatmul_q4k_q8k`, ...) that allocate the
+  outputs as torch tensors on the current device and launch on torch's current
+  stream.
+
+Nothing here computes on the CPU: if libbpdq_hip.so is not built, every entry
+point raises.
+"""
+import ctypes
+
+from . import formats
+from ._native import load_hip
+
+
+class BpdqError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"bpdq error {code}: {msg}")
+        self.code = code
+
+
+def lib():
+    return load_hip()
+
+
+def _ptr(a):
+    if a is None:
+        return None
+    if isinstance(a, int):
+        return a
+    if hasattr(a, "data_ptr"):
+        return a.data_ptr()
+    if isinstance(a, ctypes.c_void_p):
+        return a.value
+    raise TypeError(f"cannot pass {type(a).__name__} as a device pointer")
+
+
+def check():
+    """Raise BpdqError if the last call on this thread recorded an error."""
+    L = lib()
+    code = L.bpd_gpu_last_error()
+    if code:
+        raise BpdqError(code, L.bpd_gpu_last_error_message().decode())
+
+
+def call(name, *args):
+    """Call an exported entry point by name; pointers may be tensors."""
+    fn = getattr(lib(), name)
+    conv = [_ptr(a) if not isinstance(a, (float,)) else a for a in args]
+    res = fn(*conv)
+    check()
+    return res
+
+
+def _use_torch_stream():
+    import torch
+
+    lib().bpd_gpu_set_stream(torch.cuda.current_stream().cuda_stream)
+
+
+def _empty(n, dtype, like):
+    import torch
+
+    return torch.empty(n, dtype=dtype, device=like.device)
+
+
+# ---------------------------------------------------------------- Q4_K / Q8_K
+
+def dequant_q4k(q, order=formats.ORDER_BPD, out=None):
+    """q: uint8 device tensor of n_blocks*144 bytes -> fp32 tensor [n_blocks*256]."""
+    import torch
+
+    nb = q.numel() // formats.Q4K_BYTES
+    out = _empty(nb * 256, torch.float32, q) if out is None else out
+    _use_torch_stream()
+    call("bpd_dequant_q4k_gpu" if order == formats.ORDER_BPD else "bpd_dequant_q4k_gguf_gpu", q, out, nb)
+    return out
+
+
+def qmatmul_q4k(w, x, M, K, out=None):
+    """Reference-order GEMV, fp32 x (bit-identical to bpd_qmatmul_q4k)."""
+    import torch
+
+    out = _empty(M, torch.float32, x) if out is None else out
+    _use_torch_stream()
+    call("bpd_qmatmul_q4k_gpu", w, x, out, M, K)
+    return out
+
+
+def quant_q8_k(x, out=None):
+    import torch
+
+    n = x.numel()
+    out = _empty(n // formats.Q8K_ELEMS * formats.Q8K_BYTES, torch.uint8, x) if out is None else out
+    _use_torch_stream()
+    call("bpd_quant_q8_k_gpu", x, out, n)
+    return out
+
+
+def qmatmul_q4k_q8k(w, xq, M, K, order=formats.ORDER_BPD, out=None):
+    import torch
+
+    out = _empty(M, torch.float32, xq) if out is None else out
+    _use_torch_stream()
+    call("bpd_qmatmul_q4k_q8k_gpu" if order == formats.ORDER_BPD else "bpd_qmatmul_q4k_q8k_gguf_gpu",
+         w, xq, out, M, K)
+    return out
+
+
+# ---------------------------------------------------------------- Q8_0
+
+def dequant_q8_0(raw, out=None):
+    import torch
+
+    nb = raw.numel() // formats.Q8_0_BYTES
+    out = _empty(nb * 32, torch.float32, raw) if out is None else out
+    _use_torch_stream()
+    call("bpd_dequant_q8_0_gpu", raw, out, nb)
+    return out
+
+
+def embed_lookup_q8_0(table, ids, embed_dim, out=None):
+    import torch
+
+    n = ids.numel()
+    out = _empty(n * embed_dim, torch.float32, table) if out is None else out
+    _use_torch_stream()
+    call("bpd_embed_lookup_q8_0_gpu", table, ids, out, n, embed_dim)
+    return out
+
+
+def quant_q8_0(x, out=None):
+    import torch
+
+    n = x.numel()
+    out = _empty(n // 32 * 34, torch.uint8, x) if out is None else out
+    _use_torch_stream()
+    call("bpd_quant_q8_0_gpu", x, out, n)
+    return out
+
+
+def qmatmul_q8_0_dispatch(Wq, Xq, m_weight, m_tokens, K, out=None):
+    """out[token * m_weight + row] in the AVX1 llamafile tile order."""
+    import torch
+
+    out = _empty(m_tokens * m_weight, torch.float32, Wq) if out is None else out
+    _use_torch_stream()
+    call("bpd_qmatmul_q8_0_dispatch_gpu", Wq, Xq, out, m_weight, m_tokens, K)
+    return out
+
+
+def qmatmul_q8_0_llamafile(W, X, m_weight, m_tokens, K, out=None):
+    import torch
+
+    out = _empty(m_tokens * m_weight, torch.float32, W) if out is None else out
+    _use_torch_stream()
+    call("bpd_qmatmul_q8_0_llamafile_gpu", W, X, out, m_weight, m_tokens, K)
+    return out

@@ -1,0 +1,114 @@
+/* bpdq.h — C ABI of libbpdq_hip.so, the gfx950 (MI355X) implementation of the
+ * bpd-substrate quantized-inference path.
+ *
+ * Conventions, kept from the reference's ctypes surface:
+ *   - every tensor argument is a device pointer (qgpu_alloc, hipMalloc, or a
+ *     torch-ROCm tensor's data_ptr()); sizes are C int; functions return void;
+ *   - GGUF block bytes are consumed unchanged: Q4_K 144 B / 256 elements,
+ *     Q8_0 34 B / 32 elements, rows stored with K contiguous;
+ *   - kernels are launched asynchronously on the current stream (the null
+ *     stream unless bpd_gpu_set_stream() chose another), like the reference's
+ *     <<<grid, block>>> launches; qgpu_h2d/qgpu_d2h are synchronous copies.
+ * Unlike the reference, every entry point validates its arguments first.  A
+ * NULL pointer with a non-empty size, a negative size, K that is not a multiple
+ * of the block length, or a misaligned pointer launches nothing, leaves the
+ * outputs untouched and records an error code readable with bpd_gpu_last_error().
+ * Pointer alignment required: Q4_K tensors 16 B; fp32 vectors of
+ * bpd_quant_q8_k_gpu 16 B; every other fp32 / Q8_K pointer 4 B; Q8_0 bytes 1 B.
+ *
+ * Citations are /root/reference/<file>:<line> of the interface each entry
+ * point replaces.
+ */
+#ifndef BPDQ_H
+#define BPDQ_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- error reporting (no counterpart in the reference, whose CUDA calls are
+ *      never checked: bench/bpd_quant_gpu.cu:162-176) ---------------------- */
+#define BPDQ_OK 0
+#define BPDQ_ERR_NULL 1   /* NULL pointer for a non-empty tensor */
+#define BPDQ_ERR_SHAPE 2  /* negative size or K not a multiple of the block length */
+#define BPDQ_ERR_ALIGN 3  /* pointer alignment below what the kernel loads with */
+#define BPDQ_ERR_HIP 4    /* the HIP runtime reported an error (launch, copy, sync) */
+#define BPDQ_ERR_ALLOC 5  /* device allocation failed */
+/* First error recorded on the calling thread since the previous call; clears it. */
+int bpd_gpu_last_error(void);
+/* Text of the most recent error on the calling thread ("" if none). */
+const char* bpd_gpu_last_error_message(void);
+/* Launch stream for every later call (a hipStream_t; NULL = the null stream). */
+void bpd_gpu_set_stream(void* hip_stream);
+
+/* ---- Q4_K: bench/bpd_quant_gpu.cu:160-178 ------------------------------- */
+/* out[256 b + e] = dequant of Q4_K block b in the bpd element map
+ * (bench/bpd_quant_gpu.cu:162-164, math of bench/bpd_quant.c:41-81); 0 ULP. */
+void bpd_dequant_q4k_gpu(const uint8_t* q_dev, float* out_dev, int n_blocks);
+/* y[M] = W_q4k[M,K] x_f32[K] with the reference CPU order of bench/bpd_quant.c:88-109
+ * (a sequential fp32 chain per row): bit-identical to bpd_qmatmul_q4k.
+ * Replaces bench/bpd_quant_gpu.cu:166-169. */
+void bpd_qmatmul_q4k_gpu(const uint8_t* w_dev, const float* x_dev, float* y_dev, int M, int K);
+void* qgpu_alloc(int bytes);                                  /* bench/bpd_quant_gpu.cu:172 */
+void qgpu_free(void* p);                                      /* :173 */
+void qgpu_h2d(void* dst_dev, const void* src_host, int bytes); /* :174 */
+void qgpu_d2h(void* dst_host, const void* src_dev, int bytes); /* :175 */
+void qgpu_sync(void);                                         /* :176 */
+
+/* ---- aliases of the launch-sweep library, bench/bpd_quant_gpu_sweep.cu:131-151.
+ * All eight produce the full bpd-order dequant (the reference's v1<128/64/32>
+ * left elements unwritten, bench/bpd_quant_gpu_sweep.cu:39-41). */
+void dequant_v1_256(const uint8_t* q, float* o, int nb);
+void dequant_v1_128(const uint8_t* q, float* o, int nb);
+void dequant_v1_64(const uint8_t* q, float* o, int nb);
+void dequant_v1_32(const uint8_t* q, float* o, int nb);
+void dequant_ilp2(const uint8_t* q, float* o, int nb);
+void dequant_multi2(const uint8_t* q, float* o, int nb);
+void dequant_multi4(const uint8_t* q, float* o, int nb);
+void dequant_multi8(const uint8_t* q, float* o, int nb);
+void* sgpu_alloc(int bytes);
+void sgpu_free(void* p);
+void sgpu_h2d(void* d, const void* s, int bytes);
+void sgpu_d2h(void* d, const void* s, int bytes);
+void sgpu_sync(void);
+
+/* ---- aliases of the head-to-head library, bench/bench_dequant_gpu_h2h.cu:74-82:
+ * GGUF (llama.cpp) element map with that file's f16 decode. */
+void run_llamacpp(const void* q, float* o, int nb);
+void run_bpd(const void* q, float* o, int nb);
+void* galloc(int bytes);
+void gfree(void* p);
+void gh2d(void* d, const void* s, int bytes);
+void gd2h(void* d, const void* s, int bytes);
+void gsync(void);
+
+/* ---- new Q4_K / Q8_K entry points (the reference has no Q8_K code:
+ *      docs/llama-kernel-audit.md:65; block size lib/gguf_emit_manifest.pl:142) */
+/* GGUF element map (bench/bench_dequant_gpu_h2h.cu:27-48). */
+void bpd_dequant_q4k_gguf_gpu(const uint8_t* q_dev, float* out_dev, int n_blocks);
+/* x[n] fp32 -> n/256 Q8_K blocks {f32 d; i8 qs[256]; i16 bsums[16]} (292 B). */
+void bpd_quant_q8_k_gpu(const float* x_dev, uint8_t* y_q8k_dev, int n);
+/* y[M] = W_q4k[M,K] . x_q8k[K]: exact integer sub-block sums, fixed fp32 tree
+ * (bpd element map / GGUF element map). */
+void bpd_qmatmul_q4k_q8k_gpu(const uint8_t* w_dev, const uint8_t* xq8k_dev, float* y_dev, int M, int K);
+void bpd_qmatmul_q4k_q8k_gguf_gpu(const uint8_t* w_dev, const uint8_t* xq8k_dev, float* y_dev, int M, int K);
+
+/* ---- Q8_0 on the GPU, same signatures as the CPU functions they mirror ---- */
+void bpd_dequant_q8_0_gpu(const uint8_t* raw_dev, float* out_dev, int n_blocks);           /* bench/bpd_cpu.c:3960 */
+/* ids must index rows of the table (0 <= id < rows); bench/bpd_cpu.c:4002 */
+void bpd_embed_lookup_q8_0_gpu(const uint8_t* table_dev, const int32_t* ids_dev, float* out_dev, int n_tokens,
+                               int embed_dim);
+void bpd_quant_q8_0_gpu(const float* x_dev, uint8_t* y_dev, int n_elements);                /* bench/bpd_cpu.c:4106 */
+/* out[token * m_weight + row], AVX1 llamafile tile order: bit-identical to
+ * bpd_qmatmul_q8_0_dispatch_cpu of the -mavx build (bench/bpd_gemm_q8_0_cpu.c:159). */
+void bpd_qmatmul_q8_0_dispatch_gpu(const uint8_t* Wq_dev, const uint8_t* Xq_dev, float* out_dev, int m_weight,
+                                   int m_tokens, int K);
+/* quantize X (fp32, m_tokens x K) then the dispatcher (bench/bpd_cpu.c:4429-4452). */
+void bpd_qmatmul_q8_0_llamafile_gpu(const uint8_t* W_dev, const float* X_dev, float* out_dev, int m_weight,
+                                    int m_tokens, int K);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* BPDQ_H */

@@ -1,0 +1,529 @@
+/* bpdq_oracle.c — CPU restatement of the reference Q4_K / Q8_0 arithmetic.
+ *
+ * TEST INFRASTRUCTURE ONLY: this is the checker the HIP kernels are compared
+ * against, and the CPU baseline bench.py times.  Nothing in the product library
+ * links or calls it.  Build with gcc -O2 -ffp-contract=off (no -march, no
+ * -ffast-math): every fp32 operation below is one IEEE binary32 operation
+ * rounded to nearest even, in the order written.
+ *
+ * Each function cites the reference code (/root/reference/<file>:<line>) whose
+ * operation order it restates.  The Q8_K quantizer and the Q4_K x Q8_K dot have
+ * no reference code (the reference lists Q8_K only by size,
+ * lib/gguf_emit_manifest.pl:130,142); their order is defined here and shared
+ * with the GPU kernel:
+ *
+ *   per super-block b of a row (256 elements, sub-blocks j = 0..7):
+ *     S_j  = sum over the 32 elements of sub-block j of q4 * q8   (exact int)
+ *     I_b  = sum_j sc_j * S_j                                       (exact int32)
+ *     Mn_b = sum_j m_j * (bsums[2j] + bsums[2j+1])                  (exact int32)
+ *     c_b  = RN( RN(RN(d*dy) * float(I_b)) - RN(RN(dmin*dy) * float(Mn_b)) )
+ *   per row, with nb super-blocks:
+ *     s_q  = +0.0;  for b = q, q+8, q+16, ... < nb:  s_q = RN(s_q + c_b)   (q = 0..7)
+ *     y    = RN( RN(RN(s0+s1) + RN(s2+s3)) + RN(RN(s4+s5) + RN(s6+s7)) )
+ */
+#include "bpdq_oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ---------------------------------------------------------------- f16 ---- */
+
+/* bench/bpd_quant.c:25-38 (same arithmetic: bench/bpd_quant_gpu.cu:19-30,
+ * bench/bpd_gemm_q8_0_cpu.c:13-26).  mant/1024 and the ldexpf scaling are exact,
+ * so every finite input decodes to its exact value; NaN decodes to +/-NAN. */
+float bpdq_o_f16_ldexp(uint16_t h) {
+    uint32_t s = (h >> 15) & 1u, e = (h >> 10) & 31u, m = h & 1023u;
+    float r;
+    if (e == 0) r = m ? ldexpf((float)m, -24) : 0.0f;
+    else if (e == 31) r = m ? NAN : INFINITY;
+    else r = ldexpf((float)(m | 1024u), (int)e - 25);
+    return s ? -r : r;
+}
+
+/* bench/bpd_cpu.c:3928-3958.  The magic-number form yields the exact value for
+ * finite inputs and, for NaN, the f16 payload shifted up with the quiet bit set
+ * (the multiply by 2^-112 quiets a signalling NaN). */
+float bpdq_o_f16_magic(uint16_t h) {
+    uint32_t s = (uint32_t)(h & 0x8000u) << 16, e = (h >> 10) & 31u, m = h & 1023u, bits;
+    if (e == 31) {
+        bits = s | 0x7F800000u | (m << 13) | (m ? 0x400000u : 0u);
+    } else {
+        float v = e ? ldexpf((float)(m | 1024u), (int)e - 25) : ldexpf((float)m, -24);
+        memcpy(&bits, &v, 4);
+        bits |= s;
+    }
+    float r;
+    memcpy(&r, &bits, 4);
+    return r;
+}
+
+/* bench/bench_dequant_gpu_h2h.cu:14-19: +/-0 both decode to +0.0, NaN decodes
+ * to +/-Inf, everything else exactly. */
+float bpdq_o_f16_h2h(uint16_t h) {
+    uint32_t s = (h >> 15) & 1u, e = (h >> 10) & 31u, m = h & 1023u;
+    if (e == 0 && m == 0) return 0.0f;
+    if (e == 31) return s ? -INFINITY : INFINITY;
+    float v = e ? ldexpf((float)(m | 1024u), (int)e - 25) : ldexpf((float)m, -24);
+    return s ? -v : v;
+}
+
+/* bench/bpd_cpu.c:4049-4104: binary32 -> binary16, round to nearest even,
+ * overflow -> Inf, NaN -> exponent 31 with the top mantissa bits and bit 0 set. */
+uint16_t bpdq_o_f32_to_f16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    uint32_t sign = (x >> 16) & 0x8000u, ef = (x >> 23) & 0xFFu, mf = x & 0x7FFFFFu;
+    if (ef == 0xFFu) return (uint16_t)(sign | 0x7C00u | (mf ? ((mf >> 13) | 1u) : 0u));
+    int32_t eh = (int32_t)ef - 112;
+    if (eh >= 31) return (uint16_t)(sign | 0x7C00u);
+    if (eh <= 0) {
+        if (eh < -10) return (uint16_t)sign;
+        uint32_t full = mf | 0x800000u;
+        int sh = 14 - eh;
+        uint32_t q = full >> sh;
+        uint32_t rb = (full >> (sh - 1)) & 1u;
+        uint32_t st = (full & ((1u << (sh - 1)) - 1u)) != 0u;
+        if (rb && (st || (q & 1u))) q++;
+        return (uint16_t)(sign | q);
+    }
+    uint32_t q = mf >> 13;
+    uint32_t rb = (mf >> 12) & 1u, st = (mf & 0xFFFu) != 0u;
+    if (rb && (st || (q & 1u))) {
+        q++;
+        if (q == 0x400u) {
+            q = 0;
+            eh++;
+            if (eh >= 31) return (uint16_t)(sign | 0x7C00u);
+        }
+    }
+    return (uint16_t)(sign | ((uint32_t)eh << 10) | q);
+}
+
+static inline uint16_t rd16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
+/* ---------------------------------------------------------------- Q4_K --- */
+
+/* 6-bit scale/min of sub-block j: bench/bpd_quant.c:56-62. */
+static inline void q4k_scale_min(const uint8_t* s, int j, int* sc, int* m) {
+    if (j < 4) {
+        *sc = s[j] & 63;
+        *m = s[j + 4] & 63;
+    } else {
+        *sc = (s[j + 4] & 15) | ((s[j - 4] >> 6) << 4);
+        *m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+    }
+}
+
+/* bench/bpd_quant.c:41-74: element 32j+k <- low nibble of qs[16j+k],
+ * element 32j+16+k <- high nibble; y = RN(d*sc*q - dmin*m). */
+static void dq_block_bpd(const uint8_t* blk, float* out) {
+    float d = bpdq_o_f16_ldexp(rd16(blk)), dmin = bpdq_o_f16_ldexp(rd16(blk + 2));
+    const uint8_t* s = blk + 4;
+    const uint8_t* qs = blk + 16;
+    for (int j = 0; j < 8; j++) {
+        int sc, m;
+        q4k_scale_min(s, j, &sc, &m);
+        float scale = d * (float)sc, mn = dmin * (float)m;
+        for (int k = 0; k < 16; k++) {
+            uint8_t byte = qs[16 * j + k];
+            out[32 * j + k] = scale * (float)(byte & 15) - mn;
+            out[32 * j + 16 + k] = scale * (float)(byte >> 4) - mn;
+        }
+    }
+}
+
+void bpdq_o_dequant_q4k(const uint8_t* q, float* out, int n_blocks) {
+    for (int b = 0; b < n_blocks; b++) dq_block_bpd(q + (size_t)b * 144, out + (size_t)b * 256);
+}
+
+/* bench/bench_dequant_gpu_h2h.cu:27-48: for i in 0..3, l in 0..31:
+ * element 64i+l <- low(qs[32i+l]) with sub-block 2i,
+ * element 64i+32+l <- high(qs[32i+l]) with sub-block 2i+1; h2h f16 decode. */
+void bpdq_o_dequant_q4k_gguf(const uint8_t* q, float* out, int n_blocks) {
+    for (int b = 0; b < n_blocks; b++) {
+        const uint8_t* blk = q + (size_t)b * 144;
+        float* y = out + (size_t)b * 256;
+        float dall = bpdq_o_f16_h2h(rd16(blk)), dmin = bpdq_o_f16_h2h(rd16(blk + 2));
+        for (int i = 0; i < 4; i++) {
+            int sc, m;
+            q4k_scale_min(blk + 4, 2 * i, &sc, &m);
+            float d1 = dall * (float)sc, m1 = dmin * (float)m;
+            q4k_scale_min(blk + 4, 2 * i + 1, &sc, &m);
+            float d2 = dall * (float)sc, m2 = dmin * (float)m;
+            const uint8_t* qs = blk + 16 + 32 * i;
+            for (int l = 0; l < 32; l++) {
+                y[64 * i + l] = d1 * (float)(qs[l] & 15) - m1;
+                y[64 * i + 32 + l] = d2 * (float)(qs[l] >> 4) - m2;
+            }
+        }
+    }
+}
+
+/* bench/bpd_quant.c:88-109: sequential fp32 chain from +0.0 over k in element order. */
+void bpdq_o_qmatmul_q4k(const uint8_t* w, const float* x, float* y, int M, int K) {
+    int nb = K / 256;
+    float buf[256];
+    for (int r = 0; r < M; r++) {
+        float sum = 0.0f;
+        const uint8_t* row = w + (size_t)r * nb * 144;
+        for (int b = 0; b < nb; b++) {
+            dq_block_bpd(row + (size_t)b * 144, buf);
+            const float* xp = x + (size_t)b * 256;
+            for (int k = 0; k < 256; k++) sum = sum + buf[k] * xp[k];
+        }
+        y[r] = sum;
+    }
+}
+
+/* bench/bpd_quant.c:114-137: C[r,c] = sequential chain over k of deq(A)[r,k]*B[k,c]. */
+void bpdq_o_qmm_q4k(const uint8_t* A, const float* B, float* C, int M, int N, int K) {
+    int nb = K / 256;
+    float buf[256];
+    for (int r = 0; r < M; r++) {
+        const uint8_t* row = A + (size_t)r * nb * 144;
+        for (int c = 0; c < N; c++) C[(size_t)r * N + c] = 0.0f;
+        for (int b = 0; b < nb; b++) {
+            dq_block_bpd(row + (size_t)b * 144, buf);
+            for (int k = 0; k < 256; k++) {
+                float a = buf[k];
+                const float* brow = B + ((size_t)b * 256 + k) * N;
+                for (int c = 0; c < N; c++) C[(size_t)r * N + c] = C[(size_t)r * N + c] + a * brow[c];
+            }
+        }
+    }
+}
+
+/* ---------------------------------------------------------------- Q8_K --- */
+
+/* Q8_K quantizer (no reference code).  Mirrors the Q8_0 rule of
+ * bench/bpd_cpu.c:4106-4136 at 256 elements with an fp32 scale:
+ * d = RN(amax/127), id = amax ? RN(127/amax) : 0, q = rint(RN(x*id)),
+ * bsums[g] = sum of q over elements 16g..16g+15. */
+void bpdq_o_quant_q8_k(const float* x, uint8_t* y, int n) {
+    int nb = n / 256;
+    for (int b = 0; b < nb; b++) {
+        const float* xb = x + (size_t)b * 256;
+        uint8_t* yb = y + (size_t)b * 292;
+        float amax = 0.0f;
+        for (int j = 0; j < 256; j++) {
+            float v = xb[j];
+            float av = v < 0 ? -v : v;
+            if (av > amax) amax = av;
+        }
+        float d = amax / 127.0f;
+        float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+        memcpy(yb, &d, 4);
+        int8_t* qs = (int8_t*)(yb + 4);
+        for (int j = 0; j < 256; j++) qs[j] = (int8_t)rintf(xb[j] * id);
+        for (int g = 0; g < 16; g++) {
+            int s = 0;
+            for (int j = 0; j < 16; j++) s += qs[16 * g + j];
+            int16_t s16 = (int16_t)s;
+            memcpy(yb + 260 + 2 * g, &s16, 2);
+        }
+    }
+}
+
+void bpdq_o_q4k_q8k_block_ints(const uint8_t* wblk, const uint8_t* xblk, int order, int32_t* I, int32_t* Mn) {
+    const uint8_t* s = wblk + 4;
+    const uint8_t* qs = wblk + 16;
+    const int8_t* xq = (const int8_t*)(xblk + 4);
+    int32_t S[8] = {0};
+    if (order == 0) {
+        for (int j = 0; j < 8; j++)
+            for (int k = 0; k < 16; k++)
+                S[j] += (qs[16 * j + k] & 15) * xq[32 * j + k] + (qs[16 * j + k] >> 4) * xq[32 * j + 16 + k];
+    } else {
+        for (int i = 0; i < 4; i++)
+            for (int l = 0; l < 32; l++) {
+                S[2 * i] += (qs[32 * i + l] & 15) * xq[64 * i + l];
+                S[2 * i + 1] += (qs[32 * i + l] >> 4) * xq[64 * i + 32 + l];
+            }
+    }
+    int32_t isum = 0, msum = 0;
+    for (int j = 0; j < 8; j++) {
+        int sc, m;
+        q4k_scale_min(s, j, &sc, &m);
+        int16_t b0, b1;
+        memcpy(&b0, xblk + 260 + 4 * j, 2);
+        memcpy(&b1, xblk + 262 + 4 * j, 2);
+        isum += sc * S[j];
+        msum += m * ((int32_t)b0 + (int32_t)b1);
+    }
+    *I = isum;
+    *Mn = msum;
+}
+
+static float q4k_q8k_row(const uint8_t* row, const uint8_t* xq, int nb, int order) {
+    float s[8];
+    for (int q = 0; q < 8; q++) s[q] = 0.0f;
+    for (int b = 0; b < nb; b++) {
+        const uint8_t* wb = row + (size_t)b * 144;
+        const uint8_t* xb = xq + (size_t)b * 292;
+        int32_t I, Mn;
+        bpdq_o_q4k_q8k_block_ints(wb, xb, order, &I, &Mn);
+        float dy;
+        memcpy(&dy, xb, 4);
+        float dd = bpdq_o_f16_magic(rd16(wb)) * dy;
+        float dm = bpdq_o_f16_magic(rd16(wb + 2)) * dy;
+        float a = dd * (float)I;
+        float m = dm * (float)Mn;
+        float c = a - m;
+        s[b & 7] = s[b & 7] + c;
+    }
+    float t0 = s[0] + s[1], t1 = s[2] + s[3], t2 = s[4] + s[5], t3 = s[6] + s[7];
+    return (t0 + t1) + (t2 + t3);
+}
+
+void bpdq_o_qmatmul_q4k_q8k(const uint8_t* w, const uint8_t* xq, float* y, int M, int K, int order) {
+    int nb = K / 256;
+    for (int r = 0; r < M; r++) y[r] = q4k_q8k_row(w + (size_t)r * nb * 144, xq, nb, order);
+}
+
+/* ---------------------------------------------------------------- Q8_0 --- */
+
+/* bench/bpd_cpu.c:3960-3973 */
+void bpdq_o_dequant_q8_0(const uint8_t* raw, float* out, int n_blocks) {
+    for (int b = 0; b < n_blocks; b++) {
+        const uint8_t* blk = raw + (size_t)b * 34;
+        float d = bpdq_o_f16_magic(rd16(blk));
+        const int8_t* qs = (const int8_t*)(blk + 2);
+        for (int i = 0; i < 32; i++) out[(size_t)b * 32 + i] = (float)qs[i] * d;
+    }
+}
+
+/* bench/bpd_cpu.c:4002-4013 */
+void bpdq_o_embed_lookup_q8_0(const uint8_t* table, const int32_t* ids, float* out, int n_tokens, int embed_dim) {
+    int bpr = embed_dim / 32;
+    for (int t = 0; t < n_tokens; t++)
+        bpdq_o_dequant_q8_0(table + (size_t)ids[t] * bpr * 34, out + (size_t)t * embed_dim, bpr);
+}
+
+/* bench/bpd_cpu.c:4106-4136 */
+void bpdq_o_quant_q8_0(const float* x, uint8_t* y, int n_elements) {
+    int nb = n_elements / 32;
+    for (int i = 0; i < nb; i++) {
+        const float* xb = x + (size_t)i * 32;
+        uint8_t* yb = y + (size_t)i * 34;
+        float amax = 0.0f;
+        for (int j = 0; j < 32; j++) {
+            float v = xb[j];
+            float av = v < 0 ? -v : v;
+            if (av > amax) amax = av;
+        }
+        uint16_t dh = bpdq_o_f32_to_f16(amax / 127.0f);
+        yb[0] = (uint8_t)(dh & 0xFF);
+        yb[1] = (uint8_t)(dh >> 8);
+        float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+        int8_t* qs = (int8_t*)(yb + 2);
+        for (int j = 0; j < 32; j++) qs[j] = (int8_t)rintf(xb[j] * id);
+    }
+}
+
+/* SSSE3 _mm_sign_epi8 + _mm_maddubs_epi16 + _mm_madd_epi16(1) on four bytes,
+ * with the weight byte as the sign source (bench/bpd_cpu.c:4166-4170,
+ * bench/bpd_gemm_q8_0_cpu.c:58-66).  Equals the true dot product unless an
+ * activation byte is -128 against a negative weight (the negation wraps). */
+static inline int32_t sse_quad(const int8_t* w, const int8_t* a) {
+    int32_t pair[2];
+    for (int h = 0; h < 2; h++) {
+        int32_t t = 0;
+        for (int u = 0; u < 2; u++) {
+            int wi = w[2 * h + u], ai = a[2 * h + u];
+            int ua = wi < 0 ? -wi : wi;                                   /* |w|, 128 for -128 */
+            int sb = wi < 0 ? (int)(int8_t)(uint8_t)(-ai) : (wi == 0 ? 0 : ai);
+            t += ua * sb;
+        }
+        if (t > 32767) t = 32767;
+        if (t < -32768) t = -32768;
+        pair[h] = t;
+    }
+    return pair[0] + pair[1];
+}
+
+static inline float hsum8(const float* a) {
+    /* bench/bpd_cpu.c:4200-4206 */
+    return ((a[0] + a[4]) + (a[2] + a[6])) + ((a[1] + a[5]) + (a[3] + a[7]));
+}
+
+static inline int32_t dot32(const int8_t* w, const int8_t* a) {
+    int32_t s = 0;
+    for (int j = 0; j < 32; j++) s += (int32_t)w[j] * (int32_t)a[j];
+    return s;
+}
+
+/* Scalar order S: bench/bpd_cpu.c:4263-4280 and bench/bpd_gemm_q8_0_cpu.c:112-128. */
+float bpdq_o_qdot_q8_0_S(const uint8_t* w, const uint8_t* a, int n_blocks) {
+    float sumf = 0.0f;
+    for (int ib = 0; ib < n_blocks; ib++) {
+        const uint8_t* wb = w + (size_t)ib * 34;
+        const uint8_t* ab = a + (size_t)ib * 34;
+        int32_t sumi = dot32((const int8_t*)(wb + 2), (const int8_t*)(ab + 2));
+        float delta = bpdq_o_f16_magic(rd16(wb)) * bpdq_o_f16_magic(rd16(ab));
+        sumf = sumf + (float)sumi * delta;
+    }
+    return sumf;
+}
+
+float bpdq_o_cell_q8_0_S(const uint8_t* w, const uint8_t* a, int n_blocks) {
+    return bpdq_o_qdot_q8_0_S(w, a, n_blocks);
+}
+
+/* AVX1 pair order P: bench/bpd_cpu.c:4208-4259. */
+float bpdq_o_qdot_q8_0_P(const uint8_t* w, const uint8_t* a, int n_blocks) {
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int ib = 0;
+    for (; ib + 1 < n_blocks; ib += 2) {
+        for (int h = 0; h < 2; h++) {
+            const uint8_t* wb = w + (size_t)(ib + h) * 34;
+            const uint8_t* ab = a + (size_t)(ib + h) * 34;
+            const int8_t* wq = (const int8_t*)(wb + 2);
+            const int8_t* aq = (const int8_t*)(ab + 2);
+            float delta = bpdq_o_f16_magic(rd16(wb)) * bpdq_o_f16_magic(rd16(ab));
+            for (int i = 0; i < 4; i++) {
+                int32_t p = sse_quad(wq + 4 * i, aq + 4 * i) + sse_quad(wq + 16 + 4 * i, aq + 16 + 4 * i);
+                float prod = delta * (float)p;
+                acc[4 * h + i] = prod + acc[4 * h + i];
+            }
+        }
+    }
+    float sumf = hsum8(acc);
+    for (; ib < n_blocks; ib++) {
+        const uint8_t* wb = w + (size_t)ib * 34;
+        const uint8_t* ab = a + (size_t)ib * 34;
+        int32_t sumi = dot32((const int8_t*)(wb + 2), (const int8_t*)(ab + 2));
+        float delta = bpdq_o_f16_magic(rd16(wb)) * bpdq_o_f16_magic(rd16(ab));
+        sumf = sumf + (float)sumi * delta;
+    }
+    return sumf;
+}
+
+/* AVX1 llamafile tile order T, one output cell: bench/bpd_gemm_q8_0_cpu.c:32-86.
+ * Lane L accumulates the 4-element partial of elements 4L..4L+3 of every block. */
+float bpdq_o_cell_q8_0_T(const uint8_t* w, const uint8_t* a, int n_blocks) {
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int l = 0; l < n_blocks; l++) {
+        const uint8_t* ab = a + (size_t)l * 34;
+        const uint8_t* wb = w + (size_t)l * 34;
+        float Bd = bpdq_o_f16_ldexp(rd16(ab));
+        float Ad = bpdq_o_f16_ldexp(rd16(wb));
+        float scale = Ad * Bd;
+        for (int L = 0; L < 8; L++) {
+            int32_t p = sse_quad((const int8_t*)(wb + 2) + 4 * L, (const int8_t*)(ab + 2) + 4 * L);
+            float prod = scale * (float)p;
+            acc[L] = prod + acc[L];
+        }
+    }
+    return hsum8(acc);
+}
+
+/* bench/bpd_gemm_q8_0_cpu.c:159-207: every cell of out[token * m_weight + row]
+ * is one tile cell; the tile shape never changes a cell's bits. */
+void bpdq_o_dispatch_q8_0(const uint8_t* Wq, const uint8_t* Xq, float* out, int m_weight, int m_tokens, int K, int order) {
+    int k = K / 32;
+    size_t bpr = (size_t)k * 34;
+    for (int t = 0; t < m_tokens; t++)
+        for (int r = 0; r < m_weight; r++) {
+            const uint8_t* wr = Wq + (size_t)r * bpr;
+            const uint8_t* xr = Xq + (size_t)t * bpr;
+            out[(size_t)t * m_weight + r] = order == 'T' ? bpdq_o_cell_q8_0_T(wr, xr, k) : bpdq_o_cell_q8_0_S(wr, xr, k);
+        }
+}
+
+/* bench/bpd_cpu.c:4295-4315: out[m * N + n] = qdot(W row n, quant(X row m)). */
+void bpdq_o_qmatmul_q8_0(const uint8_t* W, const float* X, float* out, int M, int N, int K, int order) {
+    int nb = K / 32;
+    size_t bpr = (size_t)nb * 34;
+    uint8_t* Xq = (uint8_t*)malloc((size_t)M * bpr + 1);
+    if (!Xq) return;
+    for (int m = 0; m < M; m++) bpdq_o_quant_q8_0(X + (size_t)m * K, Xq + (size_t)m * bpr, K);
+    for (int m = 0; m < M; m++)
+        for (int n = 0; n < N; n++)
+            out[(size_t)m * N + n] = order == 'P' ? bpdq_o_qdot_q8_0_P(W + (size_t)n * bpr, Xq + (size_t)m * bpr, nb)
+                                                  : bpdq_o_qdot_q8_0_S(W + (size_t)n * bpr, Xq + (size_t)m * bpr, nb);
+    free(Xq);
+}
+
+/* bench/bpd_cpu.c:4429-4452 (AVX1: quantize X, then the dispatcher, order T) and
+ * :4455-4458 (scalar build: bpd_qmatmul_q8_0_cpu(W, X, out, mt, mw, K), order S). */
+void bpdq_o_qmatmul_q8_0_llamafile(const uint8_t* W, const float* X, float* out, int m_weight, int m_tokens, int K, int order) {
+    if (order != 'T') {
+        bpdq_o_qmatmul_q8_0(W, X, out, m_tokens, m_weight, K, 'S');
+        return;
+    }
+    int k = K / 32;
+    size_t bpr = (size_t)k * 34;
+    uint8_t* Xq = (uint8_t*)malloc((size_t)m_tokens * bpr + 1);
+    if (!Xq) return;
+    for (int i = 0; i < m_tokens; i++) bpdq_o_quant_q8_0(X + (size_t)i * K, Xq + (size_t)i * bpr, K);
+    bpdq_o_dispatch_q8_0(W, Xq, out, m_weight, m_tokens, K, 'T');
+    free(Xq);
+}
+
+/* ------------------------------------------------- multi-threaded wrappers */
+
+typedef struct {
+    int kind, order, K, mw, mt;
+    const uint8_t* a;
+    const uint8_t* b;
+    float* out;
+    int r0, r1;
+} mt_job;
+
+static void* mt_run(void* p) {
+    mt_job* j = (mt_job*)p;
+    if (j->kind == 0) {
+        bpdq_o_dequant_q4k(j->a + (size_t)j->r0 * 144, j->out + (size_t)j->r0 * 256, j->r1 - j->r0);
+    } else if (j->kind == 1) {
+        int nb = j->K / 256;
+        for (int r = j->r0; r < j->r1; r++) j->out[r] = q4k_q8k_row(j->a + (size_t)r * nb * 144, j->b, nb, j->order);
+    } else {
+        int k = j->K / 32;
+        size_t bpr = (size_t)k * 34;
+        for (int t = 0; t < j->mt; t++)
+            for (int r = j->r0; r < j->r1; r++)
+                j->out[(size_t)t * j->mw + r] = j->order == 'T' ? bpdq_o_cell_q8_0_T(j->a + (size_t)r * bpr, j->b + (size_t)t * bpr, k)
+                                                                : bpdq_o_cell_q8_0_S(j->a + (size_t)r * bpr, j->b + (size_t)t * bpr, k);
+    }
+    return NULL;
+}
+
+static void mt_launch(mt_job proto, int n, int nthreads) {
+    enum { MAXT = 256 };
+    if (nthreads < 1) nthreads = 1;
+    if (nthreads > MAXT) nthreads = MAXT;
+    if (nthreads > n) nthreads = n > 0 ? n : 1;
+    mt_job jobs[MAXT];
+    pthread_t th[MAXT];
+    int ok[MAXT];
+    for (int t = 0; t < nthreads; t++) {
+        jobs[t] = proto;
+        jobs[t].r0 = (int)((long long)n * t / nthreads);
+        jobs[t].r1 = (int)((long long)n * (t + 1) / nthreads);
+        ok[t] = t > 0 && pthread_create(&th[t], NULL, mt_run, &jobs[t]) == 0;
+        if (t > 0 && !ok[t]) mt_run(&jobs[t]);
+    }
+    mt_run(&jobs[0]);
+    for (int t = 1; t < nthreads; t++)
+        if (ok[t]) pthread_join(th[t], NULL);
+}
+
+void bpdq_o_dequant_q4k_mt(const uint8_t* q, float* out, int n_blocks, int nthreads) {
+    mt_job p = {0};
+    p.kind = 0; p.a = q; p.out = out;
+    mt_launch(p, n_blocks, nthreads);
+}
+
+void bpdq_o_qmatmul_q4k_q8k_mt(const uint8_t* w, const uint8_t* xq, float* y, int M, int K, int order, int nthreads) {
+    mt_job p = {0};
+    p.kind = 1; p.a = w; p.b = xq; p.out = y; p.K = K; p.order = order;
+    mt_launch(p, M, nthreads);
+}
+
+void bpdq_o_dispatch_q8_0_mt(const uint8_t* Wq, const uint8_t* Xq, float* out, int m_weight, int m_tokens, int K, int order, int nthreads) {
+    mt_job p = {0};
+    p.kind = 2; p.a = Wq; p.b = Xq; p.out = out; p.K = K; p.order = order; p.mw = m_weight; p.mt = m_tokens;
+    mt_launch(p, m_weight, nthreads);
+}

@@ -1,0 +1,60 @@
+/* bpdq_oracle.h — CPU restatement of the reference quantized path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load liboracle.so, and only as the checker
+ * or the timed CPU baseline.  The product path (libbpdq_hip.so) never calls it.
+ *
+ * Citations are /root/reference/<file>:<line>.
+ */
+#ifndef BPDQ_ORACLE_H
+#define BPDQ_ORACLE_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* binary16 decode, three reference variants (identical on finite inputs). */
+float bpdq_o_f16_ldexp(uint16_t h);   /* bench/bpd_quant.c:25-38 (NaN -> +/-0x7FC00000) */
+float bpdq_o_f16_magic(uint16_t h);   /* bench/bpd_cpu.c:3928-3958 (NaN payload kept) */
+float bpdq_o_f16_h2h(uint16_t h);     /* bench/bench_dequant_gpu_h2h.cu:14-19 (NaN -> +/-Inf) */
+uint16_t bpdq_o_f32_to_f16(float f);  /* bench/bpd_cpu.c:4049-4104 */
+
+/* Q4_K (144 B / 256 elements) */
+void bpdq_o_dequant_q4k(const uint8_t* q, float* out, int n_blocks);       /* bench/bpd_quant.c:41-81 */
+void bpdq_o_dequant_q4k_gguf(const uint8_t* q, float* out, int n_blocks);  /* bench/bench_dequant_gpu_h2h.cu:27-48 */
+void bpdq_o_qmatmul_q4k(const uint8_t* w, const float* x, float* y, int M, int K);            /* bench/bpd_quant.c:88-109 */
+void bpdq_o_qmm_q4k(const uint8_t* A, const float* B, float* C, int M, int N, int K);          /* bench/bpd_quant.c:114-137 */
+
+/* Q8_K (292 B / 256 elements: f32 d, i8 qs[256], i16 bsums[16]) — no reference code exists. */
+void bpdq_o_quant_q8_k(const float* x, uint8_t* y, int n);
+/* y[r] = sum of Q4_K row r times Q8_K x; order 0 = bpd element map, 1 = GGUF element map. */
+void bpdq_o_qmatmul_q4k_q8k(const uint8_t* w, const uint8_t* xq, float* y, int M, int K, int order);
+/* exact per-super-block integer sums for one (row, block): I = sum sc_j S_j, Mn = sum m_j bsum_j */
+void bpdq_o_q4k_q8k_block_ints(const uint8_t* wblk, const uint8_t* xblk, int order, int32_t* I, int32_t* Mn);
+
+/* Q8_0 (34 B / 32 elements) */
+void bpdq_o_dequant_q8_0(const uint8_t* raw, float* out, int n_blocks);                      /* bench/bpd_cpu.c:3960-3973 */
+void bpdq_o_embed_lookup_q8_0(const uint8_t* table, const int32_t* ids, float* out, int n_tokens, int embed_dim); /* :4002-4013 */
+void bpdq_o_quant_q8_0(const float* x, uint8_t* y, int n_elements);                        /* bench/bpd_cpu.c:4106-4136 */
+float bpdq_o_qdot_q8_0_S(const uint8_t* w, const uint8_t* a, int n_blocks);                 /* bench/bpd_cpu.c:4263-4280 */
+float bpdq_o_qdot_q8_0_P(const uint8_t* w, const uint8_t* a, int n_blocks);                 /* bench/bpd_cpu.c:4208-4259 */
+float bpdq_o_cell_q8_0_T(const uint8_t* w, const uint8_t* a, int n_blocks);                 /* bench/bpd_gemm_q8_0_cpu.c:32-86 */
+float bpdq_o_cell_q8_0_S(const uint8_t* w, const uint8_t* a, int n_blocks);                 /* bench/bpd_gemm_q8_0_cpu.c:102-131 */
+/* order: 'T' (AVX1 build tiles) or 'S' (scalar build tiles); out[token * m_weight + row]. */
+void bpdq_o_dispatch_q8_0(const uint8_t* Wq, const uint8_t* Xq, float* out, int m_weight, int m_tokens, int K, int order); /* bench/bpd_gemm_q8_0_cpu.c:159-207 */
+/* order: 'P' (AVX1 qdot) or 'S'; out[m * N + n]. */
+void bpdq_o_qmatmul_q8_0(const uint8_t* W, const float* X, float* out, int M, int N, int K, int order); /* bench/bpd_cpu.c:4295-4315 */
+/* order: 'T' (AVX1 build) or 'S' (scalar build redirect, bench/bpd_cpu.c:4455-4458). */
+void bpdq_o_qmatmul_q8_0_llamafile(const uint8_t* W, const float* X, float* out, int m_weight, int m_tokens, int K, int order); /* :4429-4452 */
+
+/* Row-range parallel wrappers for the CPU baseline: every row's bits are those of
+ * the single-threaded function. */
+void bpdq_o_dequant_q4k_mt(const uint8_t* q, float* out, int n_blocks, int nthreads);
+void bpdq_o_qmatmul_q4k_q8k_mt(const uint8_t* w, const uint8_t* xq, float* y, int M, int K, int order, int nthreads);
+void bpdq_o_dispatch_q8_0_mt(const uint8_t* Wq, const uint8_t* Xq, float* out, int m_weight, int m_tokens, int K, int order, int nthreads);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,79 @@
+"""GPU parity of the Q8_0 kernels against the C oracle, through the C ABI.
+
+dequant, embed lookup and the quantizer are bit-exact with bench/bpd_cpu.c; the
+dispatcher and the llamafile path are bit-exact with the AVX1 build's tile
+order T (bench/bpd_gemm_q8_0_cpu.c:32-86).  Int8 values stay in [-127, 127],
+the range every Q8_0 quantizer produces.
+"""
+import numpy as np
+import pytest
+
+from bpd_substrate_amd import gpu, synth
+from helpers import assert_bits_equal, to_np
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _d(a, dev):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+@pytest.mark.parametrize("n_blocks", [1, 3, 128 * 448])
+def test_dequant_q8_0(dev, n_blocks):
+    raw = synth.q8_0(n_blocks, 32, synth.key(42, 4))
+    assert_bits_equal(to_np(gpu.dequant_q8_0(_d(raw, dev))), O.dequant_q8_0(raw), "dequant_q8_0")
+
+
+def test_dequant_q8_0_subnormal_scale(dev):
+    # tests/check_dequant_subnormal.py:9-31: f16 0x00c2 times int8 1 = 194 * 2^-24
+    blk = np.array([0xC2, 0x00] + [1] * 32, np.uint8)
+    got = to_np(gpu.dequant_q8_0(_d(blk, dev)))
+    assert np.all(got == np.float32(194 * 2.0 ** -24))
+
+
+def test_embed_lookup_q8_0(dev):
+    table = synth.q8_0(100, 4096, synth.key(42, 5))
+    ids = np.array([3, 0, 99, 3, 57], np.int32)
+    got = to_np(gpu.embed_lookup_q8_0(_d(table, dev), _d(ids, dev), 4096))
+    assert_bits_equal(got, O.embed_lookup_q8_0(table, ids, 4096), "embed lookup")
+
+
+@pytest.mark.parametrize("n", [32, 4096, 14336, 512 * 4096])
+def test_quant_q8_0(dev, n):
+    x = synth.normal_f32(n, synth.key(42, 6))
+    got = to_np(gpu.quant_q8_0(_d(x, dev)))
+    want = O.quant_q8_0(x)
+    assert np.array_equal(got, want), f"Q8_0 bytes differ at {np.flatnonzero(got != want)[:8]}"
+
+
+def test_quant_q8_0_edges(dev):
+    x = np.zeros(6 * 32, np.float32)
+    x[32:64] = np.arange(32, dtype=np.float32) - 15.5          # ties at x*id = k + 0.5
+    x[64:96] = 6.0e-5 * (np.arange(32) - 16)                    # d in the f16 subnormal range
+    x[96:128] = 1.0e5                                           # d = 787.4 -> f16 rounding
+    x[128:160] = 9.0e6                                          # amax/127 > 65504: d -> f16 Inf
+    x[160] = -0.0
+    got = to_np(gpu.quant_q8_0(_d(x, dev)))
+    want = O.quant_q8_0(x)
+    assert np.array_equal(got, want), f"bytes differ at {np.flatnonzero(got != want)[:8]}"
+
+
+@pytest.mark.parametrize("mw,mt,K", [(14336, 1, 4096), (4096, 1, 14336), (4, 2, 128), (7, 5, 128),
+                                     (9, 7, 128), (2048, 2, 2048), (1, 1, 32), (13, 3, 4096 + 32)])
+def test_dispatch_tile_order(dev, mw, mt, K):
+    W = synth.q8_0(mw, K, synth.key(42, 7))
+    X = synth.normal_f32(mt * K, synth.key(42, 8))
+    Xq = O.quant_q8_0(X)
+    got = to_np(gpu.qmatmul_q8_0_dispatch(_d(W, dev), _d(Xq, dev), mw, mt, K))
+    assert_bits_equal(got, O.dispatch_q8_0(W, Xq, mw, mt, K, "T"), f"dispatch {mw}x{mt}x{K}")
+
+
+@pytest.mark.parametrize("mw,mt,K", [(14336, 1, 4096), (64, 4, 256), (6, 3, 96)])
+def test_llamafile_path(dev, mw, mt, K):
+    W = synth.q8_0(mw, K, synth.key(42, 9))
+    X = synth.normal_f32(mt * K, synth.key(42, 10))
+    got = to_np(gpu.qmatmul_q8_0_llamafile(_d(W, dev), _d(X, dev), mw, mt, K))
+    assert_bits_equal(got, O.qmatmul_q8_0_llamafile(W, X, mw, mt, K, "T"), "llamafile")
