@@ -112,10 +112,10 @@ def main():
     emb(h["emb_table"].ctypes.data, h["emb_ids"].ctypes.data, h["emb_out"].ctypes.data, 4, 64)
     # one row-row dot with an odd block count (pair loop + tail)
     h["dot_w"] = q8_0_blocks_random(7, synth.key(42, 33))
-    h["dot_a"] = q8_0_blocks_random(7, synth.key(42, 34))
+    h["dot_act"] = q8_0_blocks_random(7, synth.key(42, 34))
     for k, L in (("s", RS), ("a", RA)):
         f = bind(L, "bpd_qdot_q8_0_q8_0_cpu", [P, P, I], ctypes.c_float)
-        h[f"dot_{k}"] = np.array([f(h["dot_w"].ctypes.data, h["dot_a"].ctypes.data, 7)], np.float32)
+        h[f"dot_{k}"] = np.array([f(h["dot_w"].ctypes.data, h["dot_act"].ctypes.data, 7)], np.float32)
     # dispatcher: 9 weight rows x 7 token rows, K = 128 (tiles 4+4+1 x 4+2+1)
     mw, mt, Kd = 9, 7, 128
     h["disp_W"] = q8_0_blocks_random(mw * Kd // 32, synth.key(42, 35))

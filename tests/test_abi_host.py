@@ -1,0 +1,134 @@
+"""CPU-only checks of the C ABI and the host code (no kernel is launched).
+
+* libbpdq_hip.so loads and exports every function include/bpdq.h declares, and
+  the Python signature table covers exactly that set.
+* Argument validation rejects bad calls before any HIP call: error code set,
+  message set, nothing launched.  (Each call below fails validation, so it
+  runs safely without a GPU.)
+* The synthetic generator is deterministic and chunking-invariant.
+* bench.py refuses more than one GPU.
+"""
+import os
+import re
+import subprocess
+import sys
+
+import numpy as np
+import pytest
+
+from bpd_substrate_amd import _native, formats, synth
+from bpd_substrate_amd import gpu
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_functions():
+    src = open(os.path.join(ROOT, "include", "bpdq.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    names = re.findall(r"^\s*(?:const\s+)?[A-Za-z_][\w\s\*]*?\b([a-z_][a-z0-9_]*)\s*\(", src, flags=re.M)
+    return sorted(set(n for n in names if n not in ("defined",)))
+
+
+def test_header_matches_exports_and_signatures():
+    names = header_functions()
+    assert len(names) >= 39
+    lib = _native.load_hip()
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in include/bpdq.h but not exported"
+    assert sorted(_native.HIP_SIGNATURES) == names
+
+
+def test_exported_symbols_are_exactly_the_header(tmp_path):
+    out = subprocess.run(["nm", "-D", "--defined-only", _native.HIP_LIB], capture_output=True, text=True).stdout
+    exported = {l.split()[-1] for l in out.splitlines() if " T " in l}
+    ours = {n for n in exported if not n.startswith(("_", "__hip"))}
+    assert set(header_functions()) <= ours
+
+
+def _err(expected):
+    L = _native.load_hip()
+    code = L.bpd_gpu_last_error()
+    msg = L.bpd_gpu_last_error_message().decode()
+    assert code == expected, (code, msg)
+    assert L.bpd_gpu_last_error() == 0  # cleared by the read
+    return msg
+
+
+def test_validation_rejects_before_launch():
+    L = _native.load_hip()
+    L.bpd_gpu_last_error()
+    L.bpd_qmatmul_q4k_q8k_gpu(None, None, None, 4, 300)
+    assert "multiple of 256" in _err(2)
+    L.bpd_qmatmul_q4k_q8k_gpu(None, None, None, -1, 256)
+    _err(2)
+    L.bpd_qmatmul_q4k_q8k_gpu(0x1000, None, 0x2000, 4, 256)
+    assert "NULL" in _err(1)
+    L.bpd_qmatmul_q4k_q8k_gpu(0x1004, 0x2000, 0x3000, 4, 256)
+    assert "aligned" in _err(3)
+    L.bpd_dequant_q4k_gpu(None, None, -3)
+    _err(2)
+    L.bpd_dequant_q4k_gpu(0x1008, 0x2000, 5)
+    _err(3)
+    L.bpd_quant_q8_k_gpu(0x1000, 0x2000, 100)
+    _err(2)
+    L.bpd_quant_q8_0_gpu(0x1000, 0x2000, 33)
+    _err(2)
+    L.bpd_qmatmul_q8_0_dispatch_gpu(0x1000, 0x2000, 0x3000, 4, 1, 48)
+    _err(2)
+    L.bpd_qmatmul_q8_0_llamafile_gpu(0x1000, 0x2001, 0x3000, 4, 1, 64)
+    _err(3)
+    L.bpd_embed_lookup_q8_0_gpu(0x1000, None, 0x3000, 2, 64)
+    _err(1)
+    assert L.qgpu_alloc(-5) is None
+    _err(2)
+    L.qgpu_h2d(None, None, -1)
+    _err(2)
+
+
+def test_empty_calls_are_no_ops():
+    L = _native.load_hip()
+    L.bpd_gpu_last_error()
+    L.bpd_dequant_q4k_gpu(None, None, 0)
+    L.bpd_qmatmul_q4k_q8k_gpu(None, None, None, 0, 4096)
+    L.bpd_quant_q8_0_gpu(None, None, 0)
+    assert L.qgpu_alloc(0) is None
+    assert L.bpd_gpu_last_error() == 0
+
+
+def test_gpu_wrapper_raises():
+    with pytest.raises(gpu.BpdqError) as e:
+        gpu.call("bpd_qmatmul_q4k_gpu", None, None, None, 3, 100)
+    assert e.value.code == 2
+
+
+def test_synth_deterministic_and_chunk_invariant():
+    L = _native.load_synth()
+    k = synth.key(42, 5)
+    a = np.empty(1000 * 144, np.uint8)
+    b = np.empty(1000 * 144, np.uint8)
+    L.bpdq_synth_q4k(a.ctypes.data, 1000, k, 0.02, 0.01, 1)
+    L.bpdq_synth_q4k(b.ctypes.data, 1000, k, 0.02, 0.01, 7)
+    assert np.array_equal(a, b)
+    # block 500 alone equals block 500 of the run
+    c = np.empty(144 * 1000, np.uint8)
+    L.bpdq_synth_q4k(c.ctypes.data, 1000, k, 0.02, 0.01, 3)
+    assert np.array_equal(a[500 * 144:501 * 144], c[500 * 144:501 * 144])
+    x1 = synth.normal_f32(50001, synth.key(1, 1))
+    assert abs(float(x1.mean())) < 0.02 and abs(float(x1.std()) - 1) < 0.02
+
+
+def test_synth_distributions_match_configs():
+    q = synth.q4k(4096, 256, synth.key(42, 0)).reshape(-1, 144)
+    d = q[:, 0:2].copy().view(np.float16).astype(np.float64).ravel()
+    dm = q[:, 2:4].copy().view(np.float16).astype(np.float64).ravel()
+    assert np.all(d >= 0) and abs(np.sqrt(np.mean(d ** 2)) - 0.02) < 0.002
+    assert np.all(dm >= 0) and abs(np.sqrt(np.mean(dm ** 2)) - 0.01) < 0.001
+    w = synth.q8_0(4096, 32, synth.key(42, 1)).reshape(-1, 34)
+    v = w[:, 2:].view(np.int8)
+    assert v.min() == -127 and v.max() == 127
+    assert formats.q4k_bytes(14336, 4096) == 33030144
+
+
+def test_bench_refuses_multi_gpu():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True, text=True)
+    assert r.returncode == 2 and "one GPU" in r.stderr

@@ -1,0 +1,237 @@
+"""Pin the C oracle to the reference's own C code.
+
+1. Golden vectors (tests/golden/*.npz, written by tests/golden/make_golden.py
+   from the reference C compiled from source): always run.
+2. SHA-256 of the reference's outputs at the BASELINE config sizes
+   (tests/golden/hashes.json): always run.
+3. Direct comparison with oracle/_ref/*.so on fresh inputs, including the
+   AVX1 sign/maddubs quirk on int8 = -128: run where oracle/_ref is built.
+"""
+import ctypes
+import hashlib
+import json
+import os
+
+import numpy as np
+import pytest
+
+from bpd_substrate_amd import synth
+from helpers import assert_bits_equal
+from oracle import oracle as O
+
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+P, I = ctypes.c_void_p, ctypes.c_int
+
+
+def sha(a):
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+@pytest.fixture(scope="module")
+def g4():
+    return dict(np.load(os.path.join(GOLD, "q4k.npz")))
+
+
+@pytest.fixture(scope="module")
+def g8():
+    return dict(np.load(os.path.join(GOLD, "q8_0.npz")))
+
+
+@pytest.fixture(scope="module")
+def hashes():
+    with open(os.path.join(GOLD, "hashes.json")) as f:
+        return json.load(f)
+
+
+# ------------------------------------------------------------ golden vectors
+
+def test_golden_q4k_dequant(g4):
+    assert_bits_equal(O.dequant_q4k(g4["synth_q"]), g4["synth_deq"], "synthetic blocks")
+    assert_bits_equal(O.dequant_q4k(g4["rand_q"]), g4["rand_deq"], "random-byte blocks")
+
+
+def test_golden_q4k_gemv_and_gemm(g4):
+    assert_bits_equal(O.qmatmul_q4k(g4["mm_w"], g4["mm_x"], 8, 512), g4["mm_y"], "bpd_qmatmul_q4k")
+    assert_bits_equal(O.qmm_q4k(g4["qmm_A"], g4["qmm_B"], 3, 5, 256), g4["qmm_C"], "bpd_qmm_q4k")
+
+
+def test_golden_q8_0_quant(g8):
+    # both builds share the quantizer source, so both fixtures must agree too
+    assert np.array_equal(g8["quant_y_s"], g8["quant_y_a"])
+    assert np.array_equal(O.quant_q8_0(g8["quant_x"]), g8["quant_y_s"])
+
+
+def test_golden_q8_0_dequant_and_embed(g8):
+    assert_bits_equal(O.dequant_q8_0(g8["deq_raw"]), g8["deq_out"], "dequant")
+    assert_bits_equal(O.embed_lookup_q8_0(g8["emb_table"], g8["emb_ids"], 64), g8["emb_out"], "embed")
+
+
+def test_golden_q8_0_dot_orders(g8):
+    w, a = g8["dot_w"], g8["dot_act"]
+    assert_bits_equal(np.float32(O.lib().bpdq_o_qdot_q8_0_S(w.ctypes.data, a.ctypes.data, 7)), g8["dot_s"][0], "S")
+    assert_bits_equal(np.float32(O.lib().bpdq_o_qdot_q8_0_P(w.ctypes.data, a.ctypes.data, 7)), g8["dot_a"][0], "P")
+
+
+def test_golden_q8_0_dispatch(g8):
+    W, X = g8["disp_W"], g8["disp_X"]
+    assert_bits_equal(O.dispatch_q8_0(W, X, 9, 7, 128, "T"), g8["disp_a"], "AVX1 tiles (T)")
+    assert_bits_equal(O.dispatch_q8_0(W, X, 9, 7, 128, "S"), g8["disp_s"], "scalar tiles (S)")
+
+
+def test_golden_q8_0_llamafile_and_qmatmul(g8):
+    W, X = g8["lf_W"], g8["lf_X"]
+    assert_bits_equal(O.qmatmul_q8_0_llamafile(W, X, 6, 3, 96, "T"), g8["lf_a"], "llamafile AVX1")
+    assert_bits_equal(O.qmatmul_q8_0_llamafile(W, X, 6, 3, 96, "S"), g8["lf_s"], "llamafile scalar build")
+    assert_bits_equal(O.qmatmul_q8_0(W, X, 3, 6, 96, "P"), g8["qm_a"], "qmatmul AVX1 (P)")
+    assert_bits_equal(O.qmatmul_q8_0(W, X, 3, 6, 96, "S"), g8["qm_s"], "qmatmul scalar (S)")
+
+
+# ------------------------------------------------------ full-size hashes
+
+def test_synth_inputs_are_the_hashed_ones(hashes):
+    w0 = synth.q4k(4096, 4096, synth.key(42, synth.STREAM["cfg0_w"]))
+    assert sha(w0) == hashes["input cfg0_w q4k 4096x4096"]
+    assert sha(synth.normal_f32(4096, synth.key(42, synth.STREAM["cfg1_x"]))) == hashes["input cfg1_x f32[4096]"]
+    wm = synth.q4k(14336, 4096, synth.key(42, synth.STREAM["metric_w"]))
+    assert sha(wm) == hashes["input metric_w q4k 14336x4096"]
+
+
+def test_full_size_q4k_outputs_match_reference_hashes(hashes):
+    w0 = synth.q4k(4096, 4096, synth.key(42, synth.STREAM["cfg0_w"]))
+    assert sha(O.dequant_q4k_mt(w0, 8)) == hashes["ref bpd_dequant_q4k cfg0"]
+    x1 = synth.normal_f32(4096, synth.key(42, synth.STREAM["cfg1_x"]))
+    assert sha(O.qmatmul_q4k(w0, x1, 4096, 4096)) == hashes["ref bpd_qmatmul_q4k cfg0_w . cfg1_x"]
+
+
+@pytest.mark.parametrize("name,rows,k", [("up", 14336, 4096), ("down", 4096, 14336)])
+def test_full_size_q8_0_outputs_match_reference_hashes(hashes, name, rows, k):
+    W = synth.q8_0(rows, k, synth.key(42, synth.STREAM[f"cfg2_{name}"]))
+    X = synth.normal_f32(k, synth.key(42, synth.STREAM[f"cfg2_x_{name}"]))
+    assert sha(W) == hashes[f"input cfg2_{name} q8_0 {rows}x{k}"]
+    Xq = O.quant_q8_0(X)
+    assert sha(Xq) == hashes[f"ref bpd_quant_q8_0_cpu cfg2_x_{name}"]
+    assert sha(O.dispatch_q8_0(W, Xq, rows, 1, k, "T", nthreads=8)) == hashes[f"ref avx dispatch cfg2_{name}"]
+
+
+# ------------------------------------------- direct comparison with the reference
+
+def _need(kind):
+    lib = O.ref(kind)
+    if lib is None:
+        pytest.skip("oracle/_ref not built here (needs /root/reference): covered by the golden vectors")
+    return lib
+
+
+def _bind(lib, name, args, res=None):
+    f = getattr(lib, name)
+    f.argtypes, f.restype = args, res
+    return f
+
+
+def _q8_random(n_blocks, key):
+    raw = synth.random_bytes(n_blocks * 34, key).reshape(n_blocks, 34)
+    sc = synth.q8_0(n_blocks, 32, key ^ 0x99).reshape(n_blocks, 34)[:, :2]
+    raw[:, :2] = sc
+    return raw.reshape(-1).copy()
+
+
+def test_ref_dequant_random_bytes_many():
+    R = _need("quant")
+    f = _bind(R, "bpd_dequant_q4k", [P, P, I])
+    q = synth.random_bytes(20000 * 144, synth.key(3, 3))
+    out = np.empty(20000 * 256, np.float32)
+    f(q.ctypes.data, out.ctypes.data, 20000)
+    assert_bits_equal(O.dequant_q4k(q), out, "random bytes")  # NaN bits included
+
+
+def test_ref_f16_exhaustive_through_dequant():
+    # a block with d = h, sc = 1, all nibbles 1, dmin = 0 dequantizes to exactly d:
+    # all 65536 binary16 patterns through the reference's half_to_float
+    R = _need("quant")
+    f = _bind(R, "bpd_dequant_q4k", [P, P, I])
+    blocks = np.zeros((65536, 144), np.uint8)
+    h = np.arange(65536, dtype=np.uint32)
+    blocks[:, 0], blocks[:, 1] = h & 0xFF, h >> 8
+    blocks[:, 4:8] = 1                       # sc_0..3 = 1 (m = 0)
+    blocks[:, 12:16] = 1                     # sc_4..7 low bits = 1
+    blocks[:, 16:] = 0x11
+    out = np.empty(65536 * 256, np.float32)
+    f(blocks.ctypes.data, out.ctypes.data, 65536)
+    mine = np.array([O.lib().bpdq_o_f16_ldexp(int(v)) for v in range(65536)], np.float32)
+    # d*1*1 - 0*0 = d except that (-0)*1 - 0 = -0 and NaN stays NaN
+    assert_bits_equal(out.reshape(65536, 256)[:, 0], mine * np.float32(1) - np.float32(0), "half_to_float")
+
+
+def test_ref_q8_0_quant_and_dequant_random():
+    RS = _need("scalar")
+    fq = _bind(RS, "bpd_quant_q8_0_cpu", [P, P, I])
+    x = synth.normal_f32(1 << 16, synth.key(5, 5)) * np.float32(3.0)
+    x[::97] *= np.float32(1e-6)
+    y = np.empty(x.size // 32 * 34, np.uint8)
+    fq(x.ctypes.data, y.ctypes.data, x.size)
+    assert np.array_equal(O.quant_q8_0(x), y)
+    fd = _bind(RS, "bpd_dequant_q8_0_cpu", [P, P, I])
+    raw = _q8_random(4096, synth.key(5, 6))
+    out = np.empty(4096 * 32, np.float32)
+    fd(raw.ctypes.data, out.ctypes.data, 4096)
+    assert_bits_equal(O.dequant_q8_0(raw), out, "dequant")
+
+
+@pytest.mark.parametrize("nb", [1, 2, 7, 64, 129])
+def test_ref_qdot_orders_full_int8_range(nb):
+    RS, RA = _need("scalar"), _need("avx")
+    w, a = _q8_random(nb, synth.key(6, nb)), _q8_random(nb, synth.key(7, nb))
+    for lib, fn in ((RS, "bpdq_o_qdot_q8_0_S"), (RA, "bpdq_o_qdot_q8_0_P")):
+        f = _bind(lib, "bpd_qdot_q8_0_q8_0_cpu", [P, P, I], ctypes.c_float)
+        want = np.float32(f(w.ctypes.data, a.ctypes.data, nb))
+        got = np.float32(getattr(O.lib(), fn)(w.ctypes.data, a.ctypes.data, nb))
+        assert_bits_equal(got, want, fn)
+
+
+@pytest.mark.parametrize("mw,mt,K", [(9, 7, 128), (4, 2, 128), (17, 5, 4096), (1, 1, 32)])
+def test_ref_dispatch_and_all_nine_tiles(mw, mt, K):
+    RS, RA = _need("scalar"), _need("avx")
+    W, X = _q8_random(mw * K // 32, synth.key(8, mw)), _q8_random(mt * K // 32, synth.key(9, mt))
+    for lib, order in ((RA, "T"), (RS, "S")):
+        f = _bind(lib, "bpd_qmatmul_q8_0_dispatch_cpu", [P, P, P, I, I, I])
+        out = np.empty(mw * mt, np.float32)
+        f(W.ctypes.data, X.ctypes.data, out.ctypes.data, mw, mt, K)
+        assert_bits_equal(O.dispatch_q8_0(W, X, mw, mt, K, order), out, f"dispatch {order}")
+        # tiling invariance: each tile kernel on the top-left RM x RN corner
+        bpr = K // 32 * 34
+        for rm in (1, 2, 4):
+            for rn in (1, 2, 4):
+                if rm > mw or rn > mt:
+                    continue
+                t = _bind(lib, f"bpd_gemm_q8_0_{rm}_{rn}_cpu", [P, P, I, I, I, P, I])
+                tile = np.zeros(rn * mw, np.float32)
+                t(W.ctypes.data, X.ctypes.data, K // 32, bpr, bpr, tile.ctypes.data, mw)
+                want = out.reshape(mt, mw)[:rn, :rm]
+                assert_bits_equal(tile.reshape(rn, mw)[:, :rm], want, f"tile {rm}x{rn} {order}")
+
+
+def test_ref_llamafile_and_qmatmul_builds():
+    RS, RA = _need("scalar"), _need("avx")
+    mw, mt, K = 12, 5, 256
+    W = synth.q8_0(mw, K, synth.key(10, 1))
+    X = synth.normal_f32(mt * K, synth.key(10, 2))
+    for lib, order in ((RA, "T"), (RS, "S")):
+        f = _bind(lib, "bpd_qmatmul_q8_0_llamafile_cpu", [P, P, P, I, I, I])
+        out = np.empty(mw * mt, np.float32)
+        f(W.ctypes.data, X.ctypes.data, out.ctypes.data, mw, mt, K)
+        assert_bits_equal(O.qmatmul_q8_0_llamafile(W, X, mw, mt, K, order), out, f"llamafile {order}")
+    for lib, order in ((RA, "P"), (RS, "S")):
+        f = _bind(lib, "bpd_qmatmul_q8_0_cpu", [P, P, P, I, I, I])
+        out = np.empty(mw * mt, np.float32)
+        f(W.ctypes.data, X.ctypes.data, out.ctypes.data, mt, mw, K)
+        assert_bits_equal(O.qmatmul_q8_0(W, X, mt, mw, K, order), out, f"qmatmul {order}")
+
+
+def test_ref_qmm_q4k_random():
+    R = _need("quant")
+    f = _bind(R, "bpd_qmm_q4k", [P, P, P, I, I, I])
+    A = synth.q4k(5, 512, synth.key(11, 1))
+    B = synth.normal_f32(512 * 7, synth.key(11, 2))
+    C = np.empty(35, np.float32)
+    f(A.ctypes.data, B.ctypes.data, C.ctypes.data, 5, 7, 512)
+    assert_bits_equal(O.qmm_q4k(A, B, 5, 7, 512), C, "qmm")
