@@ -3,13 +3,17 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
 
-A step is one Q4_K x Q8_K GEMV at M=14336, K=4096 (the metric workload), with
-the weight, the Q8_K activation and the output already resident in HBM.
-Weights rotate over >= 16 distinct copies (> 512 MB) so the 256 MB MALL cannot
-serve them.  The timed launches are captured once in a HIP graph and replayed,
-so the host's launch rate cannot hide the kernel time; HIP events on that
-stream bracket the timed region (whole-job throughput) and, in a second pass,
-each launch (kernel roofline).  Prints ONE JSON line.
+A step is one Q4_K x Q8_K GEMV at M=14336, K=4096 (the metric workload) with
+the weight, the Q8_K activation and the output already resident in HBM.  The
+weight rotates over >= 16 distinct copies (> 512 MB) so the 256 MB MALL cannot
+serve it.  The K timed launches are captured once in a HIP graph and replayed;
+HIP events on the graph's stream bracket the timed region, so the host's
+launch rate cannot hide or inflate kernel time.  `value` and
+`roofline.achieved` are the algorithmic bytes of one GEMV divided by the timed
+region / K.  The same method times, on the same rotating copies, a plain
+streaming read of the weight's bytes (the single-launch HBM read floor of this
+size on this device), the cfg0 dequant and the cfg2 Q8_0 GEMVs.  Prints ONE
+JSON line.
 """
 import argparse
 import json
@@ -24,13 +28,13 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 M, K = 14336, 4096
-Q8K_BLOCKS = K // 256
 W_BYTES = M * (K // 256) * 144                    # 33,030,144
-X_BYTES = Q8K_BLOCKS * 292                        # 4,672
+X_BYTES = (K // 256) * 292                        # 4,672
 Y_BYTES = M * 4                                   # 57,344
 ALG_BYTES = W_BYTES + X_BYTES + Y_BYTES           # 33,092,160 per GEMV
 DQ_BLOCKS = 4096 * 4096 // 256                    # cfg0: 65,536 Q4_K blocks
 DQ_BYTES = DQ_BLOCKS * 144 + DQ_BLOCKS * 256 * 4  # 76,546,048 per dequant
+Q80_SHAPES = {"up": (14336, 4096), "down": (4096, 14336)}
 
 
 def parse():
@@ -40,6 +44,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--copies", type=int, default=16)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-extra", action="store_true", help="metric GEMV only")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     return ap.parse_args()
 
@@ -48,44 +53,35 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def graph_of(fn, stream, torch):
-    """Capture fn() (a sequence of library launches) into a CUDA/HIP graph."""
-    from bpd_substrate_amd import gpu
+class Timer:
+    """Capture a list of library launches into one graph and time its replay."""
 
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.stream(stream):
-        with torch.cuda.graph(g, stream=stream):
-            gpu.lib().bpd_gpu_set_stream(torch.cuda.current_stream().cuda_stream)
-            fn()
-        gpu.lib().bpd_gpu_set_stream(stream.cuda_stream)
-    return g
+    def __init__(self, torch, lib, stream):
+        self.torch, self.lib, self.stream = torch, lib, stream
 
-
-def time_graph(g, stream, torch):
-    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    with torch.cuda.stream(stream):  # replay() launches on the current stream
-        s.record(stream)
-        g.replay()
-        e.record(stream)
-    e.synchronize()
-    return s.elapsed_time(e)  # ms
-
-
-def per_launch_ms(launch, n, stream, torch):
-    """Average duration of single launches, each bracketed by its own events."""
-    from bpd_substrate_amd import gpu
-
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
-    torch.cuda.synchronize()
-    gpu.lib().bpd_gpu_set_stream(stream.cuda_stream)
-    for i in range(n):
-        evs[i][0].record(stream)
-        launch(i)
-        evs[i][1].record(stream)
-    torch.cuda.synchronize()
-    t = np.array([a.elapsed_time(b) for a, b in evs])
-    return float(np.median(t)), float(np.mean(t))
+    def us_per_launch(self, launches, repeats=3):
+        torch = self.torch
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(self.stream):
+            with torch.cuda.graph(g, stream=self.stream):
+                self.lib.bpd_gpu_set_stream(self.stream.cuda_stream)
+                for fn in launches:
+                    fn()
+            self.lib.bpd_gpu_set_stream(self.stream.cuda_stream)
+        best = None
+        for i in range(repeats + 1):
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            with torch.cuda.stream(self.stream):
+                s.record(self.stream)
+                g.replay()
+                e.record(self.stream)
+            e.synchronize()
+            ms = s.elapsed_time(e)
+            if i > 0:  # the first replay warms the graph
+                best = ms if best is None else min(best, ms)
+        del g
+        return best * 1e3 / len(launches)
 
 
 def cpu_baseline(w_host, x_host, seconds):
@@ -131,8 +127,9 @@ def cpu_baseline(w_host, x_host, seconds):
     dt = (time.perf_counter() - t0) / n
     cpu_bytes = W_BYTES + K * 4 + Y_BYTES
     return {"value": round(cpu_bytes / dt / 1e9, 3), "unit": "GB/s", "cores": nthreads, "kind": kind,
-            "sample": f"{n} full {M}x{K} fp32-x GEMVs (bpd_qmatmul_q4k, -O2) in {n * dt:.1f} s, "
-                      f"{dt * 1e3:.1f} ms each"}, y
+            "sample": f"{n} full {M}x{K} fp32-x GEMVs of bpd_qmatmul_q4k (reference C, -O2, rows split over "
+                      f"{nthreads} threads) in {n * dt:.1f} s, {dt * 1e3:.2f} ms each; bytes counted as for the "
+                      f"GPU metric with fp32 x"}, y
 
 
 def load_traffic():
@@ -157,6 +154,7 @@ def main():
     torch.cuda.set_device(dev)
     L = gpu.lib()
     stream = torch.cuda.Stream()
+    T = Timer(torch, L, stream)
 
     log("generating the 14336x4096 Q4_K weight and x")
     w_host = synth.q4k(M, K, synth.key(42, synth.STREAM["metric_w"]))
@@ -167,47 +165,35 @@ def main():
     x = torch.from_numpy(x_host).to(dev)
     xq = torch.empty(X_BYTES, dtype=torch.uint8, device=dev)
     y = torch.empty(M, dtype=torch.float32, device=dev)
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
     L.bpd_gpu_set_stream(stream.cuda_stream)
     with torch.cuda.stream(stream):
         gpu.call("bpd_quant_q8_k_gpu", x, xq, K)
     torch.cuda.synchronize()
+    wp = [t.data_ptr() for t in ws]
 
     def gemv(i):
-        L.bpd_qmatmul_q4k_q8k_gpu(ws[i % copies].data_ptr(), xq.data_ptr(), y.data_ptr(), M, K)
+        return lambda: L.bpd_qmatmul_q4k_q8k_gpu(wp[i % copies], xq.data_ptr(), y.data_ptr(), M, K)
 
-    # warmup (eager) then check the library accepted every launch
-    L.bpd_gpu_set_stream(stream.cuda_stream)
     for i in range(a.warmup):
-        gemv(i)
+        gemv(i)()
     torch.cuda.synchronize()
     gpu.check()
 
-    log(f"capturing {a.steps} GEMVs over {copies} weight copies ({copies * W_BYTES / 2**20:.0f} MiB)")
-    g = graph_of(lambda: [gemv(i) for i in range(a.steps)], stream, torch)
+    log(f"timing {a.steps} GEMVs over {copies} weight copies ({copies * W_BYTES / 2**20:.0f} MiB)")
+    us = T.us_per_launch([gemv(i) for i in range(a.steps)])
     gpu.check()
-    time_graph(g, stream, torch)  # graph warmup
-    total_ms = min(time_graph(g, stream, torch) for _ in range(3))
-    ms_per_step = total_ms / a.steps
-    value = ALG_BYTES / (ms_per_step * 1e-3) / 1e9
+    ms_per_step = us * 1e-3
+    value = ALG_BYTES / (us * 1e-6) / 1e9
 
-    n_single = min(a.steps, 400)
-    k_med, k_mean = per_launch_ms(gemv, n_single, stream, torch)
-    achieved = ALG_BYTES / (k_mean * 1e-3) / 1e9
-
-    # Q4_K dequant (cfg0) on rotating copies, same method
-    log("dequant 4096x4096 (cfg0)")
-    dq_in = synth.q4k(DQ_BLOCKS, 256, synth.key(42, synth.STREAM["cfg0_w"]))
-    dq_q = [torch.from_numpy(dq_in).to(dev) for _ in range(8)]
-    dq_o = [torch.empty(DQ_BLOCKS * 256, dtype=torch.float32, device=dev) for _ in range(8)]
-    gd = graph_of(lambda: [L.bpd_dequant_q4k_gpu(dq_q[i % 8].data_ptr(), dq_o[i % 8].data_ptr(), DQ_BLOCKS)
-                           for i in range(200)], stream, torch)
-    time_graph(gd, stream, torch)
-    dq_ms = min(time_graph(gd, stream, torch) for _ in range(3)) / 200
-    gpu.check()
+    # single-launch streaming-read floor for the same bytes, same copies
+    rd_us = T.us_per_launch([(lambda i=i: L.bpdq_stream_read_gpu(wp[i % copies], W_BYTES // 16, sink.data_ptr()))
+                             for i in range(a.steps)])
+    rd_gbs = W_BYTES / (rd_us * 1e-6) / 1e9
 
     result = {
         "metric": "Q4_K GEMV HBM GB/s (% of peak) at 14336x4096; dequant Gelem/s; ULP vs ref",
-        "value": round(value, 2),
+        "value": round(value, 1),
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": a.steps,
@@ -219,27 +205,58 @@ def main():
         "dtype": "int8 dot4 / fp32 (Q4_K x Q8_K)",
         "data": "synthetic (seeded splitmix64 Q4_K blocks per BASELINE config; x ~ N(0,1) -> Q8_K)",
         "config": {"workload": "Q4_K x Q8_K GEMV, M=14336, K=4096, batch 1 (BASELINE metric shape)",
-                   "weight_copies": copies, "timing": "HIP graph of `steps` launches; events on its stream"},
+                   "weight_copies": copies, "timing": "HIP graph of `steps` launches, events on its stream"},
         "pct_of_peak": round(100 * value / HBM_PEAK_GBS, 2),
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": load_traffic(),
+        "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": load_traffic(),
                      "kernel": "k_q4k_q8k_gemv", "alg_bytes_per_launch": ALG_BYTES,
-                     "launch_ms_mean": round(k_mean, 6), "launch_ms_median": round(k_med, 6)},
-        "dequant_cfg0": {"us": round(dq_ms * 1e3, 3), "gelem_s": round(DQ_BLOCKS * 256 / (dq_ms * 1e-3) / 1e9, 1),
-                         "gb_s": round(DQ_BYTES / (dq_ms * 1e-3) / 1e9, 1)},
+                     "launch_us": round(us, 3),
+                     "stream_read_floor": {"us": round(rd_us, 3), "gb_s": round(rd_gbs, 1),
+                                           "frac_of_floor": round(rd_us / us, 4)}},
     }
+
+    if not a.no_extra:
+        log("dequant 4096x4096 (cfg0) and Q8_0 GEMVs (cfg2)")
+        dq_in = torch.from_numpy(synth.q4k(DQ_BLOCKS, 256, synth.key(42, synth.STREAM["cfg0_w"]))).to(dev)
+        dq_q = [dq_in] + [dq_in.clone() for _ in range(7)]
+        dq_o = [torch.empty(DQ_BLOCKS * 256, dtype=torch.float32, device=dev) for _ in range(8)]
+        dq_us = T.us_per_launch([(lambda i=i: L.bpd_dequant_q4k_gpu(dq_q[i % 8].data_ptr(), dq_o[i % 8].data_ptr(),
+                                                                   DQ_BLOCKS)) for i in range(400)])
+        result["dequant_cfg0"] = {"us": round(dq_us, 3), "gelem_s": round(DQ_BLOCKS * 256 / dq_us / 1e3, 1),
+                                  "gb_s": round(DQ_BYTES / dq_us / 1e3, 1),
+                                  "frac_hbm": round(DQ_BYTES / dq_us / 1e3 / HBM_PEAK_GBS, 4)}
+        del dq_q, dq_o, dq_in
+        q_us = T.us_per_launch([(lambda: L.bpd_quant_q8_k_gpu(x.data_ptr(), xq.data_ptr(), K))] * 200)
+        result["quant_q8_k_4096_us"] = round(q_us, 3)
+        for name, (rows, k) in Q80_SHAPES.items():
+            W = torch.from_numpy(synth.q8_0(rows, k, synth.key(42, synth.STREAM[f"cfg2_{name}"]))).to(dev)
+            n_c = max(16, -(-512 * 2**20 // W.numel()))
+            Ws = [W] + [W.clone() for _ in range(n_c - 1)]
+            X = torch.from_numpy(synth.normal_f32(k, synth.key(42, synth.STREAM[f"cfg2_x_{name}"]))).to(dev)
+            Xq = gpu.quant_q8_0(X)
+            out = torch.empty(rows, dtype=torch.float32, device=dev)
+            torch.cuda.synchronize()
+            u = T.us_per_launch([(lambda i=i: L.bpd_qmatmul_q8_0_dispatch_gpu(Ws[i % n_c].data_ptr(), Xq.data_ptr(),
+                                                                             out.data_ptr(), rows, 1, k))
+                                 for i in range(400)])
+            alg = W.numel() + Xq.numel() + rows * 4
+            result[f"q8_0_gemv_{rows}x{k}"] = {"us": round(u, 3), "gb_s": round(alg / u / 1e3, 1),
+                                              "frac_hbm": round(alg / u / 1e3 / HBM_PEAK_GBS, 4),
+                                              "order": "llamafile tile (T), bit-exact"}
+            del Ws, W
+        gpu.check()
 
     if not a.no_cpu:
         log("CPU baseline (reference C bpd_qmatmul_q4k)")
         cb, y_cpu = cpu_baseline(w_host, x_host, a.cpu_seconds)
         result["cpu_baseline"] = cb
-        # the GPU reference-order entry point must reproduce the CPU reference bit for bit
+        # the GPU reference-order entry point reproduces the CPU reference bit for bit
         y_chain = torch.empty(M, dtype=torch.float32, device=dev)
         with torch.cuda.stream(stream):
             gpu.call("bpd_qmatmul_q4k_gpu", w0, x, y_chain, M, K)
         torch.cuda.synchronize()
         diff = int(np.count_nonzero(y_chain.cpu().numpy().view(np.uint32) != y_cpu.view(np.uint32)))
-        result["ulp_vs_ref"] = {"bpd_qmatmul_q4k_gpu_vs_reference_C_rows_differing": diff}
+        result["ulp_vs_ref"] = {"bpd_qmatmul_q4k_gpu_rows_differing_from_reference_C": diff, "of_rows": M}
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)

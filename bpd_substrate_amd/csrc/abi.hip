@@ -300,4 +300,16 @@ void bpd_qmatmul_q8_0_llamafile_gpu(const uint8_t* W, const float* X, float* out
     check_launch(fn);
 }
 
+// ---- measurement helper ---------------------------------------------------------
+void bpdq_stream_read_gpu(const uint8_t* p, int n16, uint32_t* sink) {
+    const char* fn = "bpdq_stream_read_gpu";
+    Check c(fn);
+    c.nonneg(n16, "n16");
+    if (!c.ok || n16 == 0) return;
+    c.ptr(p, 16, "p").ptr(sink, 4, "sink");
+    if (!c.ok) return;
+    bpdq::launch_stream_read(p, n16, sink, g_stream);
+    check_launch(fn);
+}
+
 }  // extern "C"

@@ -30,17 +30,17 @@ __device__ __forceinline__ float f16_h2h(uint32_t h) {
 
 // 6-bit scale and min of sub-block j from the 12 scale bytes held in three
 // dwords s0 = bytes 0..3, s1 = bytes 4..7, s2 = bytes 8..11
-// (layout of /root/reference/bench/bpd_quant.c:56-62).
+// (layout of /root/reference/bench/bpd_quant.c:56-62):
+//   j < 4 : sc = s[j] & 63,                         m = s[j+4] & 63
+//   j >= 4: sc = (s[j+4] & 15) | ((s[j-4] >> 6) << 4), m = (s[j+4] >> 4) | ((s[j] >> 6) << 4)
+// Both halves are computed and selected, so a lane-varying j never becomes a branch.
 __device__ __forceinline__ void q4k_scale_min(uint32_t s0, uint32_t s1, uint32_t s2, int j, int& sc, int& m) {
-    if (j < 4) {
-        const int sh = 8 * j;
-        sc = (int)((s0 >> sh) & 63u);
-        m = (int)((s1 >> sh) & 63u);
-    } else {
-        const int sh = 8 * (j - 4);
-        sc = (int)(((s2 >> sh) & 15u) | (((s0 >> (sh + 6)) & 3u) << 4));
-        m = (int)(((s2 >> (sh + 4)) & 15u) | (((s1 >> (sh + 6)) & 3u) << 4));
-    }
+    const uint32_t sh = 8u * (uint32_t)(j & 3);
+    const uint32_t a = s0 >> sh, b = s1 >> sh, h = s2 >> sh;
+    const uint32_t sc_hi = (h & 15u) | ((a >> 2) & 0x30u);
+    const uint32_t m_hi = ((h >> 4) & 15u) | ((b >> 2) & 0x30u);
+    sc = (int)(j < 4 ? (a & 63u) : sc_hi);
+    m = (int)(j < 4 ? (b & 63u) : m_hi);
 }
 
 __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {

@@ -162,70 +162,122 @@ void launch_quant_q8k(const float* x, uint8_t* y, int n, hipStream_t s) {
 // the C restatement: slot sums s_q from +0.0 over b = q mod 8 ascending, then
 // ((s0+s1)+(s2+s3)) + ((s4+s5)+(s6+s7)) as an xor-8/16/32 butterfly.
 // ----------------------------------------------------------------------------
-template <int ORDER, int R>
-__global__ __launch_bounds__(256) void k_q4k_q8k_gemv(const uint8_t* __restrict__ w, const uint8_t* __restrict__ xq,
-                                                      float* __restrict__ y, int M, int nb) {
+// Per-lane activation operands of one super-block: the 32 q8 values that meet
+// this lane's 32 nibbles, the lane's pair of bsums, and the block scale.
+struct XOps {
+    uint32_t lo[4], hi[4];
+    int bsum;
+    float dy;
+};
+
+// x operands of one super-block for lane c (xb = the Q8_K block).
+template <int ORDER>
+__device__ __forceinline__ XOps load_x(const uint8_t* __restrict__ xb, int c) {
+    XOps o;
+    o.dy = *reinterpret_cast<const float*>(xb);
+    const uint32_t bs = ld_u32(xb + 260 + 4 * c);
+    o.bsum = (int)(int16_t)(bs & 0xFFFFu) + (int)(int16_t)(bs >> 16);
+    const int off_lo = ORDER == 0 ? 32 * c : 64 * (c >> 1) + 16 * (c & 1);
+    const int off_hi = ORDER == 0 ? 32 * c + 16 : off_lo + 32;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        o.lo[k] = ld_u32(xb + 4 + off_lo + 4 * k);
+        o.hi[k] = ld_u32(xb + 4 + off_hi + 4 * k);
+    }
+    return o;
+}
+
+// The 16 header bytes {d, dmin, scales[12]} of a super-block: lane c of a slot
+// loaded dword (c & 3); four quad broadcasts give every lane all four dwords.
+__device__ __forceinline__ uint4 bcast_header(uint32_t mine) {
+    uint4 h;
+    h.x = (uint32_t)__builtin_amdgcn_mov_dpp((int)mine, 0x00, 0xF, 0xF, false);  // quad_perm [0,0,0,0]
+    h.y = (uint32_t)__builtin_amdgcn_mov_dpp((int)mine, 0x55, 0xF, 0xF, false);  // quad_perm [1,1,1,1]
+    h.z = (uint32_t)__builtin_amdgcn_mov_dpp((int)mine, 0xAA, 0xF, 0xF, false);  // quad_perm [2,2,2,2]
+    h.w = (uint32_t)__builtin_amdgcn_mov_dpp((int)mine, 0xFF, 0xF, 0xF, false);  // quad_perm [3,3,3,3]
+    return h;
+}
+
+// Contribution c_b of one super-block (same value in all 8 lanes of the slot).
+// |S| <= 32*15*127 and sc, m <= 63, so the 24-bit multiplies are exact.
+template <int ORDER>
+__device__ __forceinline__ float block_contrib(const uint4& hdr, const uint4& qv, const XOps& x, int c) {
+    const uint32_t qd[4] = {qv.x, qv.y, qv.z, qv.w};
+    int s_lo = 0, s_hi = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        s_lo = sdot4(qd[k] & 0x0F0F0F0Fu, x.lo[k], s_lo);
+        s_hi = sdot4((qd[k] >> 4) & 0x0F0F0F0Fu, x.hi[k], s_hi);
+    }
+    int sc, m, isum;
+    if (ORDER == 0) {
+        q4k_scale_min(hdr.y, hdr.z, hdr.w, c, sc, m);
+        isum = __mul24(sc, s_lo + s_hi);
+    } else {
+        int sc2, m2;
+        q4k_scale_min(hdr.y, hdr.z, hdr.w, 2 * (c >> 1), sc, m2);
+        q4k_scale_min(hdr.y, hdr.z, hdr.w, 2 * (c >> 1) + 1, sc2, m2);
+        isum = __mul24(sc, s_lo) + __mul24(sc2, s_hi);
+        q4k_scale_min(hdr.y, hdr.z, hdr.w, c, sc2, m);
+    }
+    int msum = __mul24(m, x.bsum);
+    isum = sum8_i(isum);
+    msum = sum8_i(msum);
+    const float dd = f16_ieee(hdr.x) * x.dy;
+    const float dm = f16_ieee(hdr.x >> 16) * x.dy;
+    const float a = dd * (float)isum;
+    const float mm = dm * (float)msum;
+    return a - mm;
+}
+
+// R rows per wave, WPB waves per workgroup; each pass issues the loads of G
+// block-groups x R rows (a 16-byte qs load and a header dword per lane each)
+// before computing any of them, so every wave keeps its whole share of the
+// stream in flight.  Rows past M reuse row M-1 and slots past nb reuse block
+// nb-1 (their results are discarded), so every address stays in the tensors.
+template <int ORDER, int R, int G, int WPB>
+__global__ __launch_bounds__(64 * WPB) void k_q4k_q8k_gemv(const uint8_t* __restrict__ w,
+                                                           const uint8_t* __restrict__ xq, float* __restrict__ y,
+                                                           int M, int nb) {
     const int lane = threadIdx.x & 63;
     const int q = lane >> 3, c = lane & 7;
-    const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
+    // the wave index is uniform across the wave; saying so keeps row offsets scalar
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int row0 = (blockIdx.x * WPB + wave) * R;
     if (row0 >= M) return;
     const int64_t row_bytes = (int64_t)nb * kQ4KBytes;
+    const int ngroups = (nb + 7) >> 3;
     float s[R];
 #pragma unroll
     for (int r = 0; r < R; r++) s[r] = 0.0f;
 
-    for (int t = 0; t * 8 < nb; t++) {
-        const int b = t * 8 + q;
-        const bool valid = b < nb;
-        const int bb = valid ? b : nb - 1;
-        const uint8_t* xb = xq + (int64_t)bb * kQ8KBytes;
-        const float dy = *reinterpret_cast<const float*>(xb);
-        const uint32_t bs = ld_u32(xb + 260 + 4 * c);
-        const int bsum = (int)(int16_t)(bs & 0xFFFFu) + (int)(int16_t)(bs >> 16);
-        uint32_t xl[4], xh[4];
-        {
-            const int off_lo = ORDER == 0 ? 32 * c : 64 * (c >> 1) + 16 * (c & 1);
-            const int off_hi = ORDER == 0 ? 32 * c + 16 : off_lo + 32;
-            const uint8_t* p = xb + 4;
+    for (int t0 = 0; t0 < ngroups; t0 += G) {
+        uint32_t hw[G][R];
+        uint4 qv[G][R];
+        XOps x[G];
+        bool valid[G];
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
-                xl[k] = ld_u32(p + off_lo + 4 * k);
-                xh[k] = ld_u32(p + off_hi + 4 * k);
+        for (int g = 0; g < G; g++) {
+            const int b = (t0 + g) * 8 + q;
+            valid[g] = b < nb;
+            const int bb = valid[g] ? b : nb - 1;
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const uint8_t* blk = w + (int64_t)min(row0 + r, M - 1) * row_bytes + (int64_t)bb * kQ4KBytes;
+                qv[g][r] = ld_u128(blk + 16 + 16 * c);
+                hw[g][r] = ld_u32(blk + 4 * (c & 3));
             }
+            x[g] = load_x<ORDER>(xq + (int64_t)bb * kQ8KBytes, c);
         }
+        // every load of the pass is issued before any of its data is used
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-            const int row = min(row0 + r, M - 1);
-            const uint8_t* blk = w + (int64_t)row * row_bytes + (int64_t)bb * kQ4KBytes;
-            const uint4 hdr = ld_u128(blk);
-            const uint4 qv = ld_u128(blk + 16 + 16 * c);
-            const uint32_t qd[4] = {qv.x, qv.y, qv.z, qv.w};
-            int s_lo = 0, s_hi = 0;
+        for (int g = 0; g < G; g++) {
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
-                s_lo = sdot4(qd[k] & 0x0F0F0F0Fu, xl[k], s_lo);
-                s_hi = sdot4((qd[k] >> 4) & 0x0F0F0F0Fu, xh[k], s_hi);
+            for (int r = 0; r < R; r++) {
+                const float cb = block_contrib<ORDER>(bcast_header(hw[g][r]), qv[g][r], x[g], c);
+                if (valid[g]) s[r] = s[r] + cb;
             }
-            int sc, m, isum;
-            if (ORDER == 0) {
-                q4k_scale_min(hdr.y, hdr.z, hdr.w, c, sc, m);
-                isum = sc * (s_lo + s_hi);
-            } else {
-                int sc2, m2;
-                q4k_scale_min(hdr.y, hdr.z, hdr.w, 2 * (c >> 1), sc, m2);
-                q4k_scale_min(hdr.y, hdr.z, hdr.w, 2 * (c >> 1) + 1, sc2, m2);
-                isum = sc * s_lo + sc2 * s_hi;
-                q4k_scale_min(hdr.y, hdr.z, hdr.w, c, sc2, m);
-            }
-            int msum = m * bsum;
-            isum = sum8_i(isum);
-            msum = sum8_i(msum);
-            const float dd = f16_ieee(hdr.x) * dy;
-            const float dm = f16_ieee(hdr.x >> 16) * dy;
-            const float a = dd * (float)isum;
-            const float mm = dm * (float)msum;
-            const float cb = a - mm;
-            if (valid) s[r] = s[r] + cb;
         }
     }
 #pragma unroll
@@ -238,15 +290,30 @@ __global__ __launch_bounds__(256) void k_q4k_q8k_gemv(const uint8_t* __restrict_
     }
 }
 
-void launch_qmatmul_q4k_q8k(const uint8_t* w, const uint8_t* xq, float* y, int M, int K, int order, hipStream_t s) {
-    constexpr int R = 4;
-    const int nb = K / 256;
+template <int ORDER, int R, int G, int WPB>
+static void launch_gemv(const uint8_t* w, const uint8_t* xq, float* y, int M, int nb, hipStream_t s) {
     const int waves = (M + R - 1) / R;
-    const dim3 grid((waves + 3) / 4);
-    if (order == 0)
-        hipLaunchKernelGGL((k_q4k_q8k_gemv<0, R>), grid, dim3(256), 0, s, w, xq, y, M, nb);
+    hipLaunchKernelGGL((k_q4k_q8k_gemv<ORDER, R, G, WPB>), dim3((waves + WPB - 1) / WPB), dim3(64 * WPB), 0, s, w,
+                       xq, y, M, nb);
+}
+
+template <int ORDER>
+static void launch_gemv_order(const uint8_t* w, const uint8_t* xq, float* y, int M, int nb, hipStream_t s) {
+    const int ngroups = (nb + 7) / 8;
+    // shapes measured on MI355X: 2 rows x 2 block-groups per pass; wider
+    // workgroups pay off when the row is long (several passes per wave)
+    if (ngroups <= 2)
+        launch_gemv<ORDER, 2, 2, 4>(w, xq, y, M, nb, s);
     else
-        hipLaunchKernelGGL((k_q4k_q8k_gemv<1, R>), grid, dim3(256), 0, s, w, xq, y, M, nb);
+        launch_gemv<ORDER, 2, 2, 8>(w, xq, y, M, nb, s);
+}
+
+void launch_qmatmul_q4k_q8k(const uint8_t* w, const uint8_t* xq, float* y, int M, int K, int order, hipStream_t s) {
+    const int nb = K / 256;
+    if (order == 0)
+        launch_gemv_order<0>(w, xq, y, M, nb, s);
+    else
+        launch_gemv_order<1>(w, xq, y, M, nb, s);
 }
 
 }  // namespace bpdq

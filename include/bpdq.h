@@ -108,6 +108,13 @@ void bpd_qmatmul_q8_0_dispatch_gpu(const uint8_t* Wq_dev, const uint8_t* Xq_dev,
 void bpd_qmatmul_q8_0_llamafile_gpu(const uint8_t* W_dev, const float* X_dev, float* out_dev, int m_weight,
                                     int m_tokens, int K);
 
+/* ---- measurement helper (no counterpart in the reference) -------------------
+ * Reads n16 16-byte chunks at p once, as fast as a plain streaming kernel can,
+ * and writes *sink only if the data XORs to a magic value.  bench.py uses it for
+ * the single-launch HBM read floor of a given size, and it is the known-traffic
+ * kernel that calibrates rocprofv3's FETCH_SIZE counter. */
+void bpdq_stream_read_gpu(const uint8_t* p, int n16, uint32_t* sink);
+
 #ifdef __cplusplus
 }
 #endif
