@@ -82,7 +82,95 @@ void launch_quant_q8_0(const float* x, uint8_t* y, int64_t n_elements, hipStream
 // [-127, 127] (it wraps only for an activation byte of -128 against a
 // negative weight, which no Q8_0 quantizer produces).
 // A wave holds 8 rows of one token; grid.y = tokens.
+//
+// The chain over blocks is serial, so the kernel hides memory latency by
+// software pipelining: each lane prefetches the weight dword and scale of the
+// next U blocks while it accumulates the current U.  The token's activation row
+// is staged once per workgroup in LDS, its 32 quants 4-byte aligned per block
+// and its scale decoded to fp32, so each step reads x with two LDS broadcasts.
 // ----------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) {
+    uint16_t v;
+    __builtin_memcpy(&v, p, 2);
+    return v;
+}
+
+template <int U>
+struct WBatch {
+    uint32_t q[U];   // weight bytes 2+4L..5+4L of block b
+    uint32_t d[U];   // weight scale (binary16 bits) of block b
+};
+
+// wbase: wave-uniform pointer to the wave's first row; voff: this lane's row
+// offset within the wave plus 2 + 4L (lane-constant).  Addresses are then
+// "scalar base + 32-bit lane offset + immediate", one instruction per load.
+template <int U>
+__device__ __forceinline__ void load_batch(WBatch<U>& w, const uint8_t* __restrict__ wbase, uint32_t voff,
+                                           uint32_t doff, int b0, int nb) {
+    // Blocks past the end of the row repeat block nb-1 (their steps are skipped).
+    // The clamp is wave-uniform, so each address stays scalar base + lane offset.
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const uint8_t* bu = wbase + (int64_t)min(b0 + u, nb - 1) * kQ80Bytes;
+        w.q[u] = ld_u32(bu + voff);
+        w.d[u] = ld_u16(bu + doff);
+    }
+}
+
+template <int U>
+__device__ __forceinline__ float accumulate_batch(const WBatch<U>& w, const uint32_t* __restrict__ xs,
+                                                  const float* __restrict__ xd, int L, int b0, int nb, float acc) {
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const int b = b0 + u;
+        if (b < nb) {
+            const float scale = f16_ieee(w.d[u]) * xd[b];
+            const int p = sdot4(w.q[u], xs[b * 8 + L], 0);
+            const float prod = scale * (float)p;
+            acc = prod + acc;
+        }
+    }
+    return acc;
+}
+
+template <int U, int WPB>
+__global__ __launch_bounds__(64 * WPB) void k_q8_0_gemv_T(const uint8_t* __restrict__ W, const uint8_t* __restrict__ Xq,
+                                                          float* __restrict__ out, int m_weight, int nb) {
+    extern __shared__ uint32_t lds[];
+    uint32_t* xs = lds;                                   // [nb][8] activation quants
+    float* xd = reinterpret_cast<float*>(lds + nb * 8);   // [nb] activation scales
+    const int lane = threadIdx.x & 63;
+    const int L = lane & 7;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int row = (blockIdx.x * WPB + wave) * 8 + (lane >> 3);
+    const int tok = blockIdx.y;
+    const int64_t bpr = (int64_t)nb * kQ80Bytes;
+    const int row0 = (blockIdx.x * WPB + wave) * 8;
+    const uint8_t* wbase = W + (int64_t)row0 * bpr;
+    const uint32_t doff = (uint32_t)((min(row, m_weight - 1) - row0) * bpr);
+    const uint32_t voff = doff + 2 + 4 * L;
+
+    WBatch<U> a, b;
+    load_batch<U>(a, wbase, voff, doff, 0, nb);
+    const uint8_t* xr = Xq + (int64_t)tok * bpr;
+    for (int i = threadIdx.x; i < nb * 8; i += 64 * WPB) xs[i] = ld_u32(xr + (int64_t)(i >> 3) * kQ80Bytes + 2 + 4 * (i & 7));
+    for (int i = threadIdx.x; i < nb; i += 64 * WPB) xd[i] = f16_ieee(ld_u16(xr + (int64_t)i * kQ80Bytes));
+    __syncthreads();
+
+    float acc = 0.0f;
+    for (int b0 = 0; b0 < nb; b0 += 2 * U) {
+        if (b0 + U < nb) load_batch<U>(b, wbase, voff, doff, b0 + U, nb);
+        acc = accumulate_batch<U>(a, xs, xd, L, b0, nb, acc);
+        if (b0 + 2 * U < nb) load_batch<U>(a, wbase, voff, doff, b0 + 2 * U, nb);
+        acc = accumulate_batch<U>(b, xs, xd, L, b0 + U, nb, acc);
+    }
+    acc = acc + xor_f(acc, 4);
+    acc = acc + xor_f(acc, 2);
+    acc = acc + xor_f(acc, 1);
+    if (L == 0 && row < m_weight) out[(int64_t)tok * m_weight + row] = acc;
+}
+
+// Plain form of the same order for activation rows too long to stage in LDS.
 __global__ __launch_bounds__(256) void k_q8_0_gemm_T(const uint8_t* __restrict__ W, const uint8_t* __restrict__ Xq,
                                                      float* __restrict__ out, int m_weight, int nb) {
     const int lane = threadIdx.x & 63;
@@ -117,7 +205,19 @@ void launch_q8_0_dispatch_T(const uint8_t* Wq, const uint8_t* Xq, float* out, in
                             hipStream_t s) {
     const int nb = K / 32;
     const int waves = (m_weight + 7) / 8;
-    hipLaunchKernelGGL(k_q8_0_gemm_T, dim3((waves + 3) / 4, m_tokens), dim3(256), 0, s, Wq, Xq, out, m_weight, nb);
+    const size_t lds = (size_t)nb * 36;
+    if (lds > 64 * 1024) {
+        hipLaunchKernelGGL(k_q8_0_gemm_T, dim3((waves + 3) / 4, m_tokens), dim3(256), 0, s, Wq, Xq, out, m_weight, nb);
+        return;
+    }
+    // shapes measured on MI355X: 16-block batches and 4 waves per workgroup when
+    // there are many waves; fewer, longer chains prefer 32-block batches, 2 waves
+    if (waves * m_tokens >= 1024)
+        hipLaunchKernelGGL((k_q8_0_gemv_T<16, 4>), dim3((waves + 3) / 4, m_tokens), dim3(256), lds, s, Wq, Xq, out,
+                           m_weight, nb);
+    else
+        hipLaunchKernelGGL((k_q8_0_gemv_T<32, 2>), dim3((waves + 1) / 2, m_tokens), dim3(128), lds, s, Wq, Xq, out,
+                           m_weight, nb);
 }
 
 }  // namespace bpdq
