@@ -244,6 +244,19 @@ def main():
                                               "frac_hbm": round(alg / u / 1e3 / HBM_PEAK_GBS, 4),
                                               "order": "llamafile tile (T), bit-exact"}
             del Ws, W
+        # cfg4: batched prefill, 512 tokens x 4096 x 14336 rows, order S on int8 MFMA
+        W = torch.from_numpy(synth.q8_0(14336, 4096, synth.key(42, synth.STREAM["cfg2_up"]))).to(dev)
+        X = torch.from_numpy(synth.normal_f32(512 * 4096, synth.key(42, synth.STREAM["cfg4_x"]))).to(dev)
+        Xq = gpu.quant_q8_0(X)
+        out = torch.empty(512 * 14336, dtype=torch.float32, device=dev)
+        torch.cuda.synchronize()
+        u = T.us_per_launch([(lambda: L.bpd_qmatmul_q8_0_dispatch_s_gpu(W.data_ptr(), Xq.data_ptr(), out.data_ptr(),
+                                                                         14336, 512, 4096))] * 20)
+        ops = 2.0 * 512 * 4096 * 14336
+        result["prefill_q8_0_cfg4"] = {"us": round(u, 2), "tops": round(ops / u / 1e6, 1),
+                                       "frac_int8_mfma": round(ops / u / 1e6 / 5000.0, 4),
+                                       "order": "scalar S, bit-exact vs the -O2 reference build"}
+        del W, X, Xq, out
         gpu.check()
 
     if not a.no_cpu:

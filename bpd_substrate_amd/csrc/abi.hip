@@ -300,6 +300,39 @@ void bpd_qmatmul_q8_0_llamafile_gpu(const uint8_t* W, const float* X, float* out
     check_launch(fn);
 }
 
+void bpd_qmatmul_q8_0_dispatch_s_gpu(const uint8_t* Wq, const uint8_t* Xq, float* out, int m_weight, int m_tokens,
+                                     int K) {
+    const char* fn = "bpd_qmatmul_q8_0_dispatch_s_gpu";
+    Check c(fn);
+    c.nonneg(m_weight, "m_weight").nonneg(m_tokens, "m_tokens").nonneg(K, "K").multiple(K, 32, "K");
+    if (!c.ok || m_weight == 0 || m_tokens == 0) return;
+    c.ptr(out, 4, "out");
+    if (K > 0) c.ptr(Wq, 1, "W_q8_0").ptr(Xq, 1, "X_q8_0");
+    if (!c.ok) return;
+    bpdq::launch_q8_0_gemm_S(Wq, Xq, out, m_weight, m_tokens, K, g_stream);
+    check_launch(fn);
+}
+
+void bpd_qmatmul_q8_0_llamafile_s_gpu(const uint8_t* W, const float* X, float* out, int m_weight, int m_tokens,
+                                      int K) {
+    const char* fn = "bpd_qmatmul_q8_0_llamafile_s_gpu";
+    Check c(fn);
+    c.nonneg(m_weight, "m_weight").nonneg(m_tokens, "m_tokens").nonneg(K, "K").multiple(K, 32, "K");
+    if (!c.ok || m_weight == 0 || m_tokens == 0) return;
+    c.ptr(out, 4, "out");
+    if (K > 0) c.ptr(W, 1, "W_q8_0").ptr(X, 4, "X_f32");
+    if (!c.ok) return;
+    const size_t xq_bytes = (size_t)m_tokens * (size_t)(K / 32) * 34;
+    uint8_t* xq = nullptr;
+    if (xq_bytes > 0) {
+        xq = static_cast<uint8_t*>(workspace(xq_bytes, fn));
+        if (!xq) return;
+        bpdq::launch_quant_q8_0(X, xq, (int64_t)m_tokens * K, g_stream);
+    }
+    bpdq::launch_q8_0_gemm_S(W, xq, out, m_weight, m_tokens, K, g_stream);
+    check_launch(fn);
+}
+
 // ---- measurement helper ---------------------------------------------------------
 void bpdq_stream_read_gpu(const uint8_t* p, int n16, uint32_t* sink) {
     const char* fn = "bpdq_stream_read_gpu";

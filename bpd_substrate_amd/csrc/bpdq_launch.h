@@ -19,6 +19,8 @@ void launch_quant_q8_0(const float* x, uint8_t* y, int64_t n_elements, hipStream
 void launch_q8_0_dispatch_T(const uint8_t* Wq, const uint8_t* Xq, float* out, int m_weight, int m_tokens, int K,
                             hipStream_t s);
 
+void launch_q8_0_gemm_S(const uint8_t* Wq, const uint8_t* Xq, float* out, int m_weight, int m_tokens, int K,
+                        hipStream_t s);
 void launch_stream_read(const uint8_t* p, int64_t n16, uint32_t* sink, hipStream_t s);
 
 }  // namespace bpdq

@@ -10,64 +10,56 @@
 namespace bpdq {
 
 // ----------------------------------------------------------------------------
-// Dequant.  Thread t (0..31) of a Q4_K block owns qs dword t (bytes 4t..4t+3)
-// and writes its 4 low nibbles and its 4 high nibbles as two float4 stores.
-//   bpd map  (bench/bpd_quant.c:68-72):   low -> 32(t/4)+4(t%4), high = low+16,
-//                                          both in sub-block t/4
-//   GGUF map (bench_dequant_gpu_h2h.cu:31-46): low -> 64(t/8)+4(t%8), high = low+32,
-//                                          sub-blocks 2(t/8) and 2(t/8)+1
+// Dequant.  One wave per Q4_K block; lane l writes elements 4l..4l+3, so each
+// wave store is one contiguous 1 KB line of output.  The four elements come
+// from the low or the high nibbles of one qs dword:
+//   bpd map  (bench/bpd_quant.c:68-72): sub-block j = l/8, qs dword 4j + l%4,
+//            high nibbles when bit 2 of l is set
+//   GGUF map (bench_dequant_gpu_h2h.cu:31-46): group i = l/16, qs dword 8i + l%8,
+//            high nibbles (sub-block 2i+1) when bit 3 of l is set, else sub-block 2i
 // y = RN(d*sc*q - dmin*m): d*sc and (d*sc)*q are exact in fp32, so
 // fmaf(d*sc, q, -dmin*m) equals the reference's multiply-then-subtract bit for bit.
+// The output is written with non-temporal stores: nothing re-reads it here, and
+// skipping the cache allocation lifts the write stream from ~4.7 to ~6.4 TB/s.
 // ----------------------------------------------------------------------------
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
 template <int ORDER>
 __global__ __launch_bounds__(256) void k_dequant_q4k(const uint8_t* __restrict__ q, float* __restrict__ out,
                                                      int n_blocks) {
-    const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    const int64_t b = g >> 5;
-    const int t = (int)(g & 31);
+    const int lane = threadIdx.x & 63;
+    const int64_t b = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (b >= n_blocks) return;
+    int dw, j, hi;
+    if (ORDER == 0) {
+        j = lane >> 3;
+        dw = 4 * j + (lane & 3);
+        hi = (lane >> 2) & 1;
+    } else {
+        const int i = lane >> 4;
+        dw = 8 * i + (lane & 7);
+        hi = (lane >> 3) & 1;
+        j = 2 * i + hi;
+    }
     const uint8_t* blk = q + b * kQ4KBytes;
     const uint4 hdr = ld_u128(blk);
-    const uint32_t qw = ld_u32(blk + 16 + 4 * t);
-    float d, dmin;
-    int j_lo, j_hi, e_lo, e_hi;
-    if (ORDER == 0) {
-        d = f16_ieee(hdr.x);
-        dmin = f16_ieee(hdr.x >> 16);
-        j_lo = j_hi = t >> 2;
-        e_lo = 32 * (t >> 2) + 4 * (t & 3);
-        e_hi = e_lo + 16;
-    } else {
-        d = f16_h2h(hdr.x);
-        dmin = f16_h2h(hdr.x >> 16);
-        j_lo = 2 * (t >> 3);
-        j_hi = j_lo + 1;
-        e_lo = 64 * (t >> 3) + 4 * (t & 7);
-        e_hi = e_lo + 32;
-    }
+    const uint32_t qw = ld_u32(blk + 16 + 4 * dw);
+    const float d = ORDER == 0 ? f16_ieee(hdr.x) : f16_h2h(hdr.x);
+    const float dmin = ORDER == 0 ? f16_ieee(hdr.x >> 16) : f16_h2h(hdr.x >> 16);
     int sc, m;
-    q4k_scale_min(hdr.y, hdr.z, hdr.w, j_lo, sc, m);
-    const float s_lo = d * (float)sc, m_lo = dmin * (float)m;
-    q4k_scale_min(hdr.y, hdr.z, hdr.w, j_hi, sc, m);
-    const float s_hi = d * (float)sc, m_hi = dmin * (float)m;
-    const uint32_t lo = qw & 0x0F0F0F0Fu, hi = (qw >> 4) & 0x0F0F0F0Fu;
-    float4 vlo, vhi;
-    vlo.x = fmaf(s_lo, (float)(lo & 0xFFu), -m_lo);
-    vlo.y = fmaf(s_lo, (float)((lo >> 8) & 0xFFu), -m_lo);
-    vlo.z = fmaf(s_lo, (float)((lo >> 16) & 0xFFu), -m_lo);
-    vlo.w = fmaf(s_lo, (float)(lo >> 24), -m_lo);
-    vhi.x = fmaf(s_hi, (float)(hi & 0xFFu), -m_hi);
-    vhi.y = fmaf(s_hi, (float)((hi >> 8) & 0xFFu), -m_hi);
-    vhi.z = fmaf(s_hi, (float)((hi >> 16) & 0xFFu), -m_hi);
-    vhi.w = fmaf(s_hi, (float)(hi >> 24), -m_hi);
-    float* y = out + b * 256;
-    *reinterpret_cast<float4*>(y + e_lo) = vlo;
-    *reinterpret_cast<float4*>(y + e_hi) = vhi;
+    q4k_scale_min(hdr.y, hdr.z, hdr.w, j, sc, m);
+    const float s = d * (float)sc, mn = dmin * (float)m;
+    const uint32_t nib = (hi ? (qw >> 4) : qw) & 0x0F0F0F0Fu;
+    f32x4 v;
+    v.x = fmaf(s, (float)(nib & 0xFFu), -mn);
+    v.y = fmaf(s, (float)((nib >> 8) & 0xFFu), -mn);
+    v.z = fmaf(s, (float)((nib >> 16) & 0xFFu), -mn);
+    v.w = fmaf(s, (float)(nib >> 24), -mn);
+    __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(out + b * 256 + 4 * lane));
 }
 
 void launch_dequant_q4k(const uint8_t* q, float* out, int n_blocks, int order, hipStream_t s) {
-    const int64_t threads = (int64_t)n_blocks * 32;
-    const dim3 grid((unsigned)((threads + 255) / 256));
+    const dim3 grid((unsigned)(((int64_t)n_blocks + 3) / 4));
     if (order == 0)
         hipLaunchKernelGGL(k_dequant_q4k<0>, grid, dim3(256), 0, s, q, out, n_blocks);
     else

@@ -145,9 +145,11 @@ __global__ __launch_bounds__(64 * WPB) void k_q8_0_gemv_T(const uint8_t* __restr
     const int row = (blockIdx.x * WPB + wave) * 8 + (lane >> 3);
     const int tok = blockIdx.y;
     const int64_t bpr = (int64_t)nb * kQ80Bytes;
-    const int row0 = (blockIdx.x * WPB + wave) * 8;
+    // A wave past the last row (the workgroup's spare waves) reads row m_weight-1;
+    // base and lane offsets are clamped so every address stays inside W.
+    const int row0 = min((blockIdx.x * WPB + wave) * 8, m_weight - 1);
     const uint8_t* wbase = W + (int64_t)row0 * bpr;
-    const uint32_t doff = (uint32_t)((min(row, m_weight - 1) - row0) * bpr);
+    const uint32_t doff = (uint32_t)((max(min(row, m_weight - 1), row0) - row0) * bpr);
     const uint32_t voff = doff + 2 + 4 * L;
 
     WBatch<U> a, b;
@@ -201,9 +203,23 @@ __global__ __launch_bounds__(256) void k_q8_0_gemm_T(const uint8_t* __restrict__
     if (L == 0 && row < m_weight) out[(int64_t)tok * m_weight + row] = acc;
 }
 
+// Every cell of an empty (K = 0) product is the empty sum, +0.0.
+__global__ __launch_bounds__(256) void k_fill_zero(float* __restrict__ out, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) out[i] = 0.0f;
+}
+
+void launch_fill_zero(float* out, int64_t n, hipStream_t s) {
+    if (n > 0) hipLaunchKernelGGL(k_fill_zero, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, out, n);
+}
+
 void launch_q8_0_dispatch_T(const uint8_t* Wq, const uint8_t* Xq, float* out, int m_weight, int m_tokens, int K,
                             hipStream_t s) {
     const int nb = K / 32;
+    if (nb == 0) {  // the kernels below index block nb-1
+        launch_fill_zero(out, (int64_t)m_weight * m_tokens, s);
+        return;
+    }
     const int waves = (m_weight + 7) / 8;
     const size_t lds = (size_t)nb * 36;
     if (lds > 64 * 1024) {
@@ -218,6 +234,178 @@ void launch_q8_0_dispatch_T(const uint8_t* Wq, const uint8_t* Xq, float* out, in
     else
         hipLaunchKernelGGL((k_q8_0_gemv_T<32, 2>), dim3((waves + 1) / 2, m_tokens), dim3(128), lds, s, Wq, Xq, out,
                            m_weight, nb);
+}
+
+}  // namespace bpdq
+
+namespace bpdq {
+
+// ----------------------------------------------------------------------------
+// Prefill GEMM in the scalar order S (bench/bpd_gemm_q8_0_cpu.c:102-131,
+// bench/bpd_cpu.c:4263-4280): per output cell
+//   acc = +0.0;  for b in blocks: acc = RN(acc + RN(float(S_b) * RN(Ad_b * Bd_b)))
+// with S_b the exact int32 dot of the cell's two 32-element blocks.  One K step
+// of v_mfma_i32_32x32x32_i8 covers exactly one Q8_0 block, so with a zero
+// accumulator it yields S_b for a 32 x 32 tile of cells; the fp32 epilogue then
+// applies the block's scale in order.  Bit-identical to the scalar (-O2) build
+// of bpd_qmatmul_q8_0_dispatch_cpu / bpd_qmatmul_q8_0_llamafile_cpu.
+//
+// Workgroup: 4 waves in 2 x 2, tile 128 weight rows x 128 tokens; each wave
+// 64 x 64 = 2 x 2 MFMA tiles.  Blocks are staged KB at a time through LDS
+// (double buffered), quants 32-byte aligned per (row, block), scales as fp32.
+// A lane feeds row (lane % 32) of A and column (lane % 32) of B with the same
+// 16-byte half of the block (lane / 32), so every K index of A meets the same K
+// index of B.  Output lane layout of a 32x32 tile: register r of lane l holds
+// row 8(r/4) + 4(l/32) + r%4, column l%32.
+// ----------------------------------------------------------------------------
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kGT = 128;  // tile rows = tile tokens
+constexpr int kGB = 4;    // blocks per LDS stage
+
+struct GemmLds {
+    uint8_t aq[2][kGB][kGT][32];
+    uint8_t bq[2][kGB][kGT][32];
+    float ad[2][kGB][kGT];
+    float bd[2][kGB][kGT];
+};
+
+// One (row, block) of a Q8_0 matrix: scale bits and the 32 quants.
+struct BlkRegs {
+    uint32_t d;
+    uint32_t q[8];
+};
+
+__device__ __forceinline__ void load_blk(BlkRegs& r, const uint8_t* __restrict__ p) {
+    r.d = ld_u16(p);
+#pragma unroll
+    for (int j = 0; j < 8; j++) r.q[j] = ld_u32(p + 2 + 4 * j);
+}
+
+// Thread t stages pairs t, t+256 of A (row-major over 128 rows x kGB blocks) and
+// the same of B.
+__device__ __forceinline__ void stage_load(BlkRegs (&ra)[2], BlkRegs (&rb)[2], const uint8_t* __restrict__ W,
+                                           const uint8_t* __restrict__ X, int m0, int n0, int m_weight,
+                                           int m_tokens, int b0, int nb, int64_t bpr) {
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int p = threadIdx.x + 256 * i;
+        const int rr = p & (kGT - 1), u = p >> 7;
+        const int blk = min(b0 + u, nb - 1);
+        load_blk(ra[i], W + (int64_t)min(m0 + rr, m_weight - 1) * bpr + (int64_t)blk * kQ80Bytes);
+        load_blk(rb[i], X + (int64_t)min(n0 + rr, m_tokens - 1) * bpr + (int64_t)blk * kQ80Bytes);
+    }
+}
+
+__device__ __forceinline__ void stage_store(GemmLds& s, int buf, const BlkRegs (&ra)[2], const BlkRegs (&rb)[2]) {
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int p = threadIdx.x + 256 * i;
+        const int rr = p & (kGT - 1), u = p >> 7;
+        uint4* qa = reinterpret_cast<uint4*>(s.aq[buf][u][rr]);
+        qa[0] = make_uint4(ra[i].q[0], ra[i].q[1], ra[i].q[2], ra[i].q[3]);
+        qa[1] = make_uint4(ra[i].q[4], ra[i].q[5], ra[i].q[6], ra[i].q[7]);
+        uint4* qb = reinterpret_cast<uint4*>(s.bq[buf][u][rr]);
+        qb[0] = make_uint4(rb[i].q[0], rb[i].q[1], rb[i].q[2], rb[i].q[3]);
+        qb[1] = make_uint4(rb[i].q[4], rb[i].q[5], rb[i].q[6], rb[i].q[7]);
+        s.ad[buf][u][rr] = f16_ieee(ra[i].d);
+        s.bd[buf][u][rr] = f16_ieee(rb[i].d);
+    }
+}
+
+__global__ __launch_bounds__(256) void k_q8_0_gemm_S(const uint8_t* __restrict__ W, const uint8_t* __restrict__ X,
+                                                     float* __restrict__ out, int m_weight, int m_tokens, int nb) {
+    __shared__ GemmLds s;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int wr = wave >> 1, wc = wave & 1;
+    const int m0 = blockIdx.x * kGT, n0 = blockIdx.y * kGT;
+    const int64_t bpr = (int64_t)nb * kQ80Bytes;
+    const int col = lane & 31, half = lane >> 5;
+
+    float acc[2][2][16];
+#pragma unroll
+    for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+        for (int ct = 0; ct < 2; ct++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[rt][ct][r] = 0.0f;
+
+    BlkRegs ra[2], rb[2];
+    const int nstages = (nb + kGB - 1) / kGB;
+    stage_load(ra, rb, W, X, m0, n0, m_weight, m_tokens, 0, nb, bpr);
+    stage_store(s, 0, ra, rb);
+    __syncthreads();
+
+    for (int st = 0; st < nstages; st++) {
+        const int buf = st & 1;
+        if (st + 1 < nstages) stage_load(ra, rb, W, X, m0, n0, m_weight, m_tokens, (st + 1) * kGB, nb, bpr);
+        for (int u = 0; u < kGB; u++) {
+            if (st * kGB + u >= nb) break;
+            i32x4 fa[2], fb[2];
+#pragma unroll
+            for (int rt = 0; rt < 2; rt++)
+                fa[rt] = *reinterpret_cast<const i32x4*>(&s.aq[buf][u][wr * 64 + rt * 32 + col][16 * half]);
+#pragma unroll
+            for (int ct = 0; ct < 2; ct++)
+                fb[ct] = *reinterpret_cast<const i32x4*>(&s.bq[buf][u][wc * 64 + ct * 32 + col][16 * half]);
+            float bd[2];
+#pragma unroll
+            for (int ct = 0; ct < 2; ct++) bd[ct] = s.bd[buf][u][wc * 64 + ct * 32 + col];
+#pragma unroll
+            for (int rt = 0; rt < 2; rt++) {
+                float ad[16];
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    const float4 v = *reinterpret_cast<const float4*>(&s.ad[buf][u][wr * 64 + rt * 32 + 8 * g + 4 * half]);
+                    ad[4 * g + 0] = v.x;
+                    ad[4 * g + 1] = v.y;
+                    ad[4 * g + 2] = v.z;
+                    ad[4 * g + 3] = v.w;
+                }
+#pragma unroll
+                for (int ct = 0; ct < 2; ct++) {
+                    const i32x16 zero = {0};
+                    const i32x16 sb = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[rt], fb[ct], zero, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const float delta = ad[r] * bd[ct];
+                        const float prod = (float)sb[r] * delta;
+                        acc[rt][ct][r] = acc[rt][ct][r] + prod;
+                    }
+                }
+            }
+        }
+        if (st + 1 < nstages) {
+            __syncthreads();  // everyone is done reading the buffer about to be overwritten
+            stage_store(s, buf ^ 1, ra, rb);
+        }
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int rt = 0; rt < 2; rt++)
+#pragma unroll
+        for (int ct = 0; ct < 2; ct++) {
+            const int tok = n0 + wc * 64 + ct * 32 + col;
+            if (tok >= m_tokens) continue;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int row = m0 + wr * 64 + rt * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+                if (row < m_weight) out[(int64_t)tok * m_weight + row] = acc[rt][ct][r];
+            }
+        }
+}
+
+void launch_q8_0_gemm_S(const uint8_t* Wq, const uint8_t* Xq, float* out, int m_weight, int m_tokens, int K,
+                        hipStream_t s) {
+    if (K / 32 == 0) {  // the kernel indexes block nb-1
+        launch_fill_zero(out, (int64_t)m_weight * m_tokens, s);
+        return;
+    }
+    const dim3 grid((m_weight + kGT - 1) / kGT, (m_tokens + kGT - 1) / kGT);
+    hipLaunchKernelGGL(k_q8_0_gemm_S, grid, dim3(256), 0, s, Wq, Xq, out, m_weight, m_tokens, K / 32);
 }
 
 }  // namespace bpdq

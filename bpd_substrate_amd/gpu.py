@@ -163,3 +163,22 @@ def qmatmul_q8_0_llamafile(W, X, m_weight, m_tokens, K, out=None):
     _use_torch_stream()
     call("bpd_qmatmul_q8_0_llamafile_gpu", W, X, out, m_weight, m_tokens, K)
     return out
+
+
+def qmatmul_q8_0_dispatch_s(Wq, Xq, m_weight, m_tokens, K, out=None):
+    """out[token * m_weight + row] in the scalar order S (int8 MFMA prefill GEMM)."""
+    import torch
+
+    out = _empty(m_tokens * m_weight, torch.float32, Wq) if out is None else out
+    _use_torch_stream()
+    call("bpd_qmatmul_q8_0_dispatch_s_gpu", Wq, Xq, out, m_weight, m_tokens, K)
+    return out
+
+
+def qmatmul_q8_0_llamafile_s(W, X, m_weight, m_tokens, K, out=None):
+    import torch
+
+    out = _empty(m_tokens * m_weight, torch.float32, W) if out is None else out
+    _use_torch_stream()
+    call("bpd_qmatmul_q8_0_llamafile_s_gpu", W, X, out, m_weight, m_tokens, K)
+    return out

@@ -167,6 +167,31 @@ def main():
         out = np.empty(rows, np.float32)
         f(W.ctypes.data, Xq.ctypes.data, out.ctypes.data, rows, 1, k)
         H[f"ref avx dispatch cfg2_{name}"] = sha(out)
+    # cfg4: prefill, W as cfg2 up (14336 x 4096), X 512 x 4096 -> Q8_0, scalar build (order S);
+    # the reference dispatcher is run on token ranges in parallel (rows of out are independent)
+    import threading
+
+    W = synth.q8_0(14336, 4096, synth.key(42, synth.STREAM["cfg2_up"]))
+    X = synth.normal_f32(512 * 4096, synth.key(42, synth.STREAM["cfg4_x"]))
+    H["input cfg4_x f32[512x4096]"] = sha(X)
+    qs = bind(RS, "bpd_quant_q8_0_cpu", [P, P, I])
+    Xq = np.empty(512 * 128 * 34, np.uint8)
+    qs(X.ctypes.data, Xq.ctypes.data, X.size)
+    H["ref bpd_quant_q8_0_cpu cfg4_x"] = sha(Xq)
+    f = bind(RS, "bpd_qmatmul_q8_0_dispatch_cpu", [P, P, P, I, I, I])
+    out = np.empty(512 * 14336, np.float32)
+    nt = 16
+
+    def part(i):
+        t0, t1 = 512 * i // nt, 512 * (i + 1) // nt
+        f(W.ctypes.data, Xq.ctypes.data + t0 * 128 * 34, out.ctypes.data + t0 * 14336 * 4, 14336, t1 - t0, 4096)
+
+    ths = [threading.Thread(target=part, args=(i,)) for i in range(nt)]
+    for t in ths:
+        t.start()
+    for t in ths:
+        t.join()
+    H["ref scalar dispatch cfg4 512x14336x4096"] = sha(out)
     with open(os.path.join(OUT, "hashes.json"), "w") as fh:
         json.dump(H, fh, indent=1, sort_keys=True)
     print("wrote", os.listdir(OUT))

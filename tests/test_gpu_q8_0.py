@@ -77,3 +77,59 @@ def test_llamafile_path(dev, mw, mt, K):
     X = synth.normal_f32(mt * K, synth.key(42, 10))
     got = to_np(gpu.qmatmul_q8_0_llamafile(_d(W, dev), _d(X, dev), mw, mt, K))
     assert_bits_equal(got, O.qmatmul_q8_0_llamafile(W, X, mw, mt, K, "T"), "llamafile")
+
+
+# ------------------------------------------------- prefill GEMM, scalar order S (int8 MFMA)
+
+@pytest.mark.parametrize("mw,mt,K", [(4, 2, 128), (7, 5, 128), (130, 129, 4096 + 32), (1, 1, 32), (256, 256, 64),
+                                     (300, 17, 224), (2048, 64, 2048)])
+def test_dispatch_scalar_order(dev, mw, mt, K):
+    W = synth.q8_0(mw, K, synth.key(43, 7))
+    X = synth.normal_f32(mt * K, synth.key(43, 8))
+    Xq = O.quant_q8_0(X)
+    got = to_np(gpu.qmatmul_q8_0_dispatch_s(_d(W, dev), _d(Xq, dev), mw, mt, K))
+    assert_bits_equal(got, O.dispatch_q8_0(W, Xq, mw, mt, K, "S", nthreads=8), f"S-order {mw}x{mt}x{K}")
+
+
+def test_llamafile_scalar_build_path(dev):
+    mw, mt, K = 96, 40, 512
+    W = synth.q8_0(mw, K, synth.key(43, 9))
+    X = synth.normal_f32(mt * K, synth.key(43, 10))
+    got = to_np(gpu.qmatmul_q8_0_llamafile_s(_d(W, dev), _d(X, dev), mw, mt, K))
+    assert_bits_equal(got, O.qmatmul_q8_0_llamafile(W, X, mw, mt, K, "S"), "llamafile, scalar build")
+
+
+def test_prefill_cfg4_full_size_matches_reference_hash(dev):
+    # BASELINE cfg4: W = cfg2 up (14336 x 4096), X = 512 x 4096 N(0,1) -> Q8_0; the expected
+    # SHA-256 is that of the reference's scalar-build dispatcher output (tests/golden/make_golden.py)
+    import hashlib
+    import json
+    import os
+
+    hashes = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "hashes.json")))
+    W = synth.q8_0(14336, 4096, synth.key(42, synth.STREAM["cfg2_up"]))
+    X = synth.normal_f32(512 * 4096, synth.key(42, synth.STREAM["cfg4_x"]))
+    Xq = gpu.quant_q8_0(_d(X, dev))
+    assert hashlib.sha256(to_np(Xq).tobytes()).hexdigest() == hashes["ref bpd_quant_q8_0_cpu cfg4_x"]
+    out = to_np(gpu.qmatmul_q8_0_dispatch_s(_d(W, dev), Xq, 14336, 512, 4096))
+    assert hashlib.sha256(out.tobytes()).hexdigest() == hashes["ref scalar dispatch cfg4 512x14336x4096"]
+
+
+def test_empty_k_gives_zero_cells(dev):
+    import torch
+
+    for name in ("bpd_qmatmul_q8_0_dispatch_gpu", "bpd_qmatmul_q8_0_dispatch_s_gpu"):
+        out = torch.full((3 * 5,), float("nan"), device=dev)
+        gpu.call(name, None, None, out, 5, 3, 0)
+        torch.cuda.synchronize()
+        assert to_np(out).view(np.uint32).tolist() == [0] * 15, name
+
+
+@pytest.mark.parametrize("mw", [7, 15, 17, 23])
+def test_dispatch_spare_waves(dev, mw):
+    # row counts that leave whole waves of the last workgroup past the end of W
+    K = 256
+    W = synth.q8_0(mw, K, synth.key(44, mw))
+    Xq = O.quant_q8_0(synth.normal_f32(K, synth.key(44, 1)))
+    got = to_np(gpu.qmatmul_q8_0_dispatch(_d(W, dev), _d(Xq, dev), mw, 1, K))
+    assert_bits_equal(got, O.dispatch_q8_0(W, Xq, mw, 1, K, "T"), f"spare waves mw={mw}")

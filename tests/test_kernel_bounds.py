@@ -1,0 +1,149 @@
+"""Host-side replay of the kernels' launch geometry and address arithmetic.
+
+For every shape the GPU tests use (and edge shapes: one row, spare waves in the
+last workgroup, K = 0, ragged tails) this recomputes, lane by lane, the byte
+ranges each kernel reads and writes and checks they stay inside the tensors.
+It mirrors the index formulas of bpd_substrate_amd/csrc/*.hip and the launch
+choices of their launchers; a change there must be mirrored here.  No GPU.
+"""
+import numpy as np
+import pytest
+
+Q4K, Q8K, Q80 = 144, 292, 34
+
+
+def lanes():
+    return np.arange(64)
+
+
+# ---------------------------------------------------------------- Q4_K x Q8_K GEMV
+
+def q4k_gemv_shape(nb):
+    ngroups = (nb + 7) // 8
+    return (2, 2, 4) if ngroups <= 2 else (2, 2, 8)
+
+
+@pytest.mark.parametrize("M,K", [(4096, 4096), (14336, 4096), (4096, 14336), (1024, 4096), (1, 256), (5, 512),
+                                 (13, 2304), (9, 2304), (3, 0), (64, 1024), (77, 512)])
+def test_q4k_q8k_gemv_in_bounds(M, K):
+    nb = K // 256
+    R, G, WPB = q4k_gemv_shape(nb)
+    waves = (M + R - 1) // R
+    grid = (waves + WPB - 1) // WPB
+    w_size, x_size, y_size = M * nb * Q4K, nb * Q8K, M * 4
+    l = lanes()
+    q, c = l >> 3, l & 7
+    ngroups = (nb + 7) >> 3
+    for blk in sorted({0, grid - 1}):
+        for wave in range(WPB):
+            row0 = (blk * WPB + wave) * R
+            if row0 >= M:
+                continue
+            for t0 in range(0, ngroups, G):
+                for g in range(G):
+                    b = (t0 + g) * 8 + q
+                    bb = np.where(b < nb, b, nb - 1)
+                    for r in range(R):
+                        base = min(row0 + r, M - 1) * nb * Q4K + bb * Q4K
+                        assert (base + 16 + 16 * c + 16).max() <= w_size and base.min() >= 0
+                        assert (base + 4 * (c & 3) + 4).max() <= w_size
+                    xb = bb * Q8K
+                    # (offset, bytes) of every x access: dy, bsum pair, low and high quants of both maps
+                    for off, size in ((0, 4), (260 + 4 * c, 4), (4 + 32 * c, 16), (4 + 32 * c + 16, 16),
+                                      (4 + 64 * (c >> 1) + 16 * (c & 1), 16),
+                                      (4 + 64 * (c >> 1) + 16 * (c & 1) + 32, 16)):
+                        assert np.max(xb + off + size) <= x_size and np.min(xb + off) >= 0
+            for r in range(R):
+                if row0 + r < M:
+                    assert (row0 + r) * 4 + 4 <= y_size
+
+
+# ---------------------------------------------------------------- dequant
+
+@pytest.mark.parametrize("nb", [1, 7, 33, 65536, 4096])
+def test_dequant_in_bounds(nb):
+    grid = (nb + 3) // 4
+    for blk in {0, grid - 1}:
+        for wave in range(4):
+            b = blk * 4 + wave
+            if b >= nb:
+                continue
+            l = lanes()
+            assert b * Q4K + 16 + 4 * 31 + 4 <= nb * Q4K
+            assert (b * 256 + 4 * l + 4).max() <= nb * 256
+
+
+# ---------------------------------------------------------------- Q8_0 tile-order GEMV
+
+def q8_gemv_config(mw, mt, K):
+    nb = K // 32
+    waves = (mw + 7) // 8
+    if nb == 0:
+        return None
+    if nb * 36 > 64 * 1024:
+        return ("plain", 4, 1)
+    if waves * mt >= 1024:
+        return ("pipelined", 4, 16)
+    return ("pipelined", 2, 32)
+
+
+@pytest.mark.parametrize("mw,mt,K", [(14336, 1, 4096), (4096, 1, 14336), (4, 2, 128), (7, 5, 128), (9, 7, 128),
+                                     (2048, 2, 2048), (1, 1, 32), (13, 3, 4128), (64, 4, 256), (6, 3, 96),
+                                     (3, 1, 64), (17, 1, 32), (15, 1, 256), (23, 1, 256), (7, 1, 256)])
+def test_q8_0_gemv_T_in_bounds(mw, mt, K):
+    cfg = q8_gemv_config(mw, mt, K)
+    nb = K // 32
+    bpr = nb * Q80
+    w_size, x_size, out_size = mw * bpr, mt * bpr, mw * mt * 4
+    if cfg is None:
+        return
+    kind, WPB, U = cfg
+    waves = (mw + 7) // 8
+    grid = (waves + WPB - 1) // WPB if kind == "pipelined" else (waves + 3) // 4
+    l = lanes()
+    L = l & 7
+    for blk in sorted({0, grid - 1}):
+        for wave in range(WPB):
+            row = (blk * WPB + wave) * 8 + (l >> 3)
+            if kind == "plain":
+                continue
+            row0 = min((blk * WPB + wave) * 8, mw - 1)
+            doff = (np.maximum(np.minimum(row, mw - 1), row0) - row0) * bpr
+            assert doff.min() >= 0
+            voff = doff + 2 + 4 * L
+            for b0 in range(0, nb + 2 * U, U):
+                for u in range(U):
+                    b = min(b0 + u, nb - 1)
+                    base = row0 * bpr + b * Q80
+                    assert (base + voff + 4).max() <= w_size and (base + doff).min() >= 0
+                    assert (base + doff + 2).max() <= w_size
+            for tok in range(mt):
+                assert tok * bpr + (nb - 1) * Q80 + 2 + 28 + 4 <= x_size
+                ok = row < mw
+                assert ((tok * mw + row[ok]) * 4 + 4).max(initial=0) <= out_size
+
+
+# ---------------------------------------------------------------- Q8_0 S-order GEMM (MFMA)
+
+@pytest.mark.parametrize("mw,mt,K", [(14336, 512, 4096), (4, 2, 128), (7, 5, 128), (130, 129, 4096 + 32),
+                                     (1, 1, 32), (256, 256, 64), (300, 17, 224)])
+def test_q8_0_gemm_S_in_bounds(mw, mt, K):
+    nb = K // 32
+    if nb == 0:
+        return
+    bpr = nb * Q80
+    gx, gy = (mw + 127) // 128, (mt + 127) // 128
+    t = np.arange(256)
+    for bx in {0, gx - 1}:
+        for by in {0, gy - 1}:
+            m0, n0 = bx * 128, by * 128
+            for b0 in range(0, nb + 4, 4):
+                for i in range(2):
+                    p = t + 256 * i
+                    rr, u = p & 127, p >> 7
+                    blk = np.minimum(b0 + u, nb - 1)
+                    wa = np.minimum(m0 + rr, mw - 1) * bpr + blk * Q80
+                    xa = np.minimum(n0 + rr, mt - 1) * bpr + blk * Q80
+                    assert wa.min() >= 0 and (wa + 34).max() <= mw * bpr
+                    assert xa.min() >= 0 and (xa + 34).max() <= mt * bpr
+                    assert u.max() < 4 and rr.max() < 128
