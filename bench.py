@@ -132,6 +132,39 @@ def cpu_baseline(w_host, x_host, seconds):
                       f"GPU metric with fp32 x"}, y
 
 
+def decode_chain(torch, L, T, dev, gpu, synth, n_layers=32, tokens=10):
+    """BASELINE cfg3: the GEMV portion of a 32-layer Mistral-7B-shaped decode step,
+    Q4_K weights (each tensor its own seed), activations N(0,1) -> Q8_K."""
+    from bpd_substrate_amd import decode
+
+    log(f"decode chain: generating {n_layers} layers of Q4_K weights")
+    d = decode.Dims()
+    e, kv, ff = d.n_embd, d.n_kv, d.ff
+    layers, acts = [], []
+    for i in range(n_layers):
+        k = lambda t: synth.key(42, 1000 + 8 * i + t)
+        shapes = dict(q=(e, e), k=(kv, e), v=(kv, e), o=(e, e), gate=(ff, e), up=(ff, e), down=(e, ff))
+        layers.append(decode.LayerWeights(**{n: torch.from_numpy(synth.q4k(m, kk, k(t))).to(dev)
+                                             for t, (n, (m, kk)) in enumerate(shapes.items())}))
+        acts.append([torch.from_numpy(synth.normal_f32(n, synth.key(43, 10 * i + j))).to(dev)
+                     for j, n in enumerate((e, e, e, ff))])
+    chain = decode.GemvChain(layers, d, dev)
+    torch.cuda.synchronize()
+    L.bpd_gpu_set_stream(T.stream.cuda_stream)
+    chain.step(acts)
+    torch.cuda.synchronize()
+    gpu.check()
+    us = T.us_per_launch([lambda: chain.step(acts)] * tokens)  # us per token
+    wb = chain.weight_bytes()
+    gpu.check()
+    out = {"us_per_token": round(us, 1), "tokens_per_s": round(1e6 / us, 1), "weight_bytes": wb,
+           "gb_s": round(wb / us / 1e3, 1), "frac_hbm": round(wb / us / 1e3 / HBM_PEAK_GBS, 4),
+           "launches_per_token": 8 * n_layers,
+           "roofline_us_per_token": round(wb / HBM_PEAK_GBS / 1e3, 1)}
+    del chain, layers, acts
+    return out
+
+
 def load_traffic():
     p = os.path.join(ROOT, "profiles", "q4k_q8k_gemv_14336x4096_traffic.json")
     if not os.path.exists(p):
@@ -258,6 +291,7 @@ def main():
                                        "order": "scalar S, bit-exact vs the -O2 reference build"}
         del W, X, Xq, out
         gpu.check()
+        result["decode_cfg3"] = decode_chain(torch, L, T, dev, gpu, synth)
 
     if not a.no_cpu:
         log("CPU baseline (reference C bpd_qmatmul_q4k)")

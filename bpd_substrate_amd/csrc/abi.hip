@@ -195,6 +195,29 @@ void bpd_qmatmul_q4k_q8k_gguf_gpu(const uint8_t* w, const uint8_t* xq, float* y,
     q4k_q8k(w, xq, y, M, K, 1, "bpd_qmatmul_q4k_q8k_gguf_gpu");
 }
 
+void bpd_qmatmul_q4k_q8k_multi_gpu(const uint8_t* const* w_list, float* const* y_list, const int* M_list, int n,
+                                   const uint8_t* xq, int K) {
+    const char* fn = "bpd_qmatmul_q4k_q8k_multi_gpu";
+    Check c(fn);
+    if (n < 0 || n > 4) c.fail(BPDQ_ERR_SHAPE, "n", "is outside 0..4");
+    c.nonneg(K, "K").multiple(K, 256, "K");
+    if (!c.ok || n == 0) return;
+    c.ptr(w_list, 1, "w_list").ptr(y_list, 1, "y_list").ptr(M_list, 1, "M_list");
+    if (!c.ok) return;
+    int rows = 0;
+    for (int i = 0; i < n && c.ok; i++) {
+        c.nonneg(M_list[i], "M_list[i]");
+        if (!c.ok || M_list[i] == 0) continue;
+        rows += M_list[i];
+        c.ptr(y_list[i], 4, "y_list[i]");
+        if (K > 0) c.ptr(w_list[i], 16, "w_list[i]");
+    }
+    if (K > 0) c.ptr(xq, 4, "xq");
+    if (!c.ok || rows == 0) return;
+    bpdq::launch_qmatmul_q4k_q8k_multi(w_list, y_list, M_list, n, xq, K, 0, g_stream);
+    check_launch(fn);
+}
+
 void* qgpu_alloc(int bytes) { return alloc(bytes, "qgpu_alloc"); }
 void qgpu_free(void* p) {
     if (p) hip_ok(hipFree(p), "qgpu_free");

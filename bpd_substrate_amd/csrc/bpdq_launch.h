@@ -12,6 +12,9 @@ void launch_qmatmul_q4k_chain(const uint8_t* w, const float* x, float* y, int M,
 void launch_quant_q8k(const float* x, uint8_t* y, int n, hipStream_t s);
 void launch_qmatmul_q4k_q8k(const uint8_t* w, const uint8_t* xq, float* y, int M, int K, int order, hipStream_t s);
 
+void launch_qmatmul_q4k_q8k_multi(const uint8_t* const* w, float* const* y, const int* M, int n, const uint8_t* xq,
+                                  int K, int order, hipStream_t s);
+
 void launch_dequant_q8_0(const uint8_t* raw, float* out, int n_blocks, hipStream_t s);
 void launch_embed_q8_0(const uint8_t* table, const int32_t* ids, float* out, int n_tokens, int embed_dim,
                        hipStream_t s);

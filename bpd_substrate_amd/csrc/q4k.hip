@@ -222,21 +222,16 @@ __device__ __forceinline__ float block_contrib(const uint4& hdr, const uint4& qv
     return a - mm;
 }
 
-// R rows per wave, WPB waves per workgroup; each pass issues the loads of G
-// block-groups x R rows (a 16-byte qs load and a header dword per lane each)
-// before computing any of them, so every wave keeps its whole share of the
-// stream in flight.  Rows past M reuse row M-1 and slots past nb reuse block
-// nb-1 (their results are discarded), so every address stays in the tensors.
-template <int ORDER, int R, int G, int WPB>
-__global__ __launch_bounds__(64 * WPB) void k_q4k_q8k_gemv(const uint8_t* __restrict__ w,
-                                                           const uint8_t* __restrict__ xq, float* __restrict__ y,
-                                                           int M, int nb) {
+// One wave's R rows: each pass issues the loads of G block-groups x R rows (a
+// 16-byte qs load and a header dword per lane each) before computing any of
+// them, so every wave keeps its whole share of the stream in flight.  Rows past
+// M reuse row M-1 and slots past nb reuse block nb-1 (their results are
+// discarded), so every address stays in the tensors.  row0 < M.
+template <int ORDER, int R, int G>
+__device__ __forceinline__ void gemv_rows(const uint8_t* __restrict__ w, const uint8_t* __restrict__ xq,
+                                          float* __restrict__ y, int M, int nb, int row0) {
     const int lane = threadIdx.x & 63;
     const int q = lane >> 3, c = lane & 7;
-    // the wave index is uniform across the wave; saying so keeps row offsets scalar
-    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int row0 = (blockIdx.x * WPB + wave) * R;
-    if (row0 >= M) return;
     const int64_t row_bytes = (int64_t)nb * kQ4KBytes;
     const int ngroups = (nb + 7) >> 3;
     float s[R];
@@ -282,6 +277,44 @@ __global__ __launch_bounds__(64 * WPB) void k_q4k_q8k_gemv(const uint8_t* __rest
     }
 }
 
+// R rows per wave, WPB waves per workgroup.
+template <int ORDER, int R, int G, int WPB>
+__global__ __launch_bounds__(64 * WPB) void k_q4k_q8k_gemv(const uint8_t* __restrict__ w,
+                                                           const uint8_t* __restrict__ xq, float* __restrict__ y,
+                                                           int M, int nb) {
+    // the wave index is uniform across the wave; saying so keeps row offsets scalar
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int row0 = (blockIdx.x * WPB + wave) * R;
+    if (row0 >= M) return;
+    gemv_rows<ORDER, R, G>(w, xq, y, M, nb, row0);
+}
+
+// Up to kMulti matrices that share one activation vector (Q/K/V, gate/up) in
+// one launch: waves are numbered across the matrices, matrix i owning waves
+// [first[i], first[i+1]).  Each row is computed exactly as the single-matrix
+// kernel computes it.
+constexpr int kMulti = 4;
+struct MultiArgs {
+    const uint8_t* w[kMulti];
+    float* y[kMulti];
+    int M[kMulti];
+    int first[kMulti + 1];
+};
+
+template <int ORDER, int R, int G, int WPB>
+__global__ __launch_bounds__(64 * WPB) void k_q4k_q8k_gemv_multi(MultiArgs a, const uint8_t* __restrict__ xq, int nb) {
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int gw = blockIdx.x * WPB + wave;
+    int i = 0;
+#pragma unroll
+    for (int k = 1; k < kMulti; k++)
+        if (gw >= a.first[k]) i = k;
+    if (gw >= a.first[kMulti]) return;
+    const int row0 = (gw - a.first[i]) * R;
+    if (row0 >= a.M[i]) return;
+    gemv_rows<ORDER, R, G>(a.w[i], xq, a.y[i], a.M[i], nb, row0);
+}
+
 template <int ORDER, int R, int G, int WPB>
 static void launch_gemv(const uint8_t* w, const uint8_t* xq, float* y, int M, int nb, hipStream_t s) {
     const int waves = (M + R - 1) / R;
@@ -306,6 +339,37 @@ void launch_qmatmul_q4k_q8k(const uint8_t* w, const uint8_t* xq, float* y, int M
         launch_gemv_order<0>(w, xq, y, M, nb, s);
     else
         launch_gemv_order<1>(w, xq, y, M, nb, s);
+}
+
+template <int ORDER, int WPB>
+static void launch_multi(const MultiArgs& a, const uint8_t* xq, int nb, hipStream_t s) {
+    const int waves = a.first[kMulti];
+    hipLaunchKernelGGL((k_q4k_q8k_gemv_multi<ORDER, 2, 2, WPB>), dim3((waves + WPB - 1) / WPB), dim3(64 * WPB), 0, s,
+                       a, xq, nb);
+}
+
+void launch_qmatmul_q4k_q8k_multi(const uint8_t* const* w, float* const* y, const int* M, int n, const uint8_t* xq,
+                                  int K, int order, hipStream_t s) {
+    constexpr int R = 2;
+    MultiArgs a;
+    int waves = 0;
+    for (int i = 0; i < kMulti; i++) {
+        const bool used = i < n;
+        a.w[i] = used ? w[i] : nullptr;
+        a.y[i] = used ? y[i] : nullptr;
+        a.M[i] = used ? M[i] : 0;
+        a.first[i] = waves;
+        waves += used ? (M[i] + R - 1) / R : 0;
+    }
+    a.first[kMulti] = waves;
+    if (waves == 0) return;
+    const int nb = K / 256;
+    const bool long_rows = (nb + 7) / 8 > 2;
+    if (order == 0) {
+        if (long_rows) launch_multi<0, 8>(a, xq, nb, s); else launch_multi<0, 4>(a, xq, nb, s);
+    } else {
+        if (long_rows) launch_multi<1, 8>(a, xq, nb, s); else launch_multi<1, 4>(a, xq, nb, s);
+    }
 }
 
 }  // namespace bpdq

@@ -114,6 +114,21 @@ def qmatmul_q4k_q8k(w, xq, M, K, order=formats.ORDER_BPD, out=None):
     return out
 
 
+def qmatmul_q4k_q8k_multi(ws, xq, Ms, K, outs=None):
+    """Up to four Q4_K GEMVs sharing the activation xq, in one launch."""
+    import torch
+
+    n = len(ws)
+    outs = [_empty(m, torch.float32, xq) for m in Ms] if outs is None else outs
+    w_arr = (ctypes.c_void_p * n)(*[_ptr(w) for w in ws])
+    y_arr = (ctypes.c_void_p * n)(*[_ptr(y) for y in outs])
+    m_arr = (ctypes.c_int * n)(*Ms)
+    _use_torch_stream()
+    call("bpd_qmatmul_q4k_q8k_multi_gpu", ctypes.addressof(w_arr), ctypes.addressof(y_arr), ctypes.addressof(m_arr),
+         n, xq, K)
+    return outs
+
+
 # ---------------------------------------------------------------- Q8_0
 
 def dequant_q8_0(raw, out=None):

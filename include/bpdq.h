@@ -94,6 +94,13 @@ void bpd_quant_q8_k_gpu(const float* x_dev, uint8_t* y_q8k_dev, int n);
 void bpd_qmatmul_q4k_q8k_gpu(const uint8_t* w_dev, const uint8_t* xq8k_dev, float* y_dev, int M, int K);
 void bpd_qmatmul_q4k_q8k_gguf_gpu(const uint8_t* w_dev, const uint8_t* xq8k_dev, float* y_dev, int M, int K);
 
+/* n (0..4) Q4_K matrices sharing one Q8_K activation, in one launch: y_list[i][M_list[i]] =
+ * W_i . xq8k, each bit-identical to bpd_qmatmul_q4k_q8k_gpu on that matrix.  w_list, y_list and
+ * M_list are host arrays (of device pointers).  For the Q/K/V and gate/up GEMVs of a decode step
+ * (bench/bpd_cpu.c:5642-5727 issues them as separate calls). */
+void bpd_qmatmul_q4k_q8k_multi_gpu(const uint8_t* const* w_list, float* const* y_list, const int* M_list, int n,
+                                   const uint8_t* xq8k_dev, int K);
+
 /* ---- Q8_0 on the GPU, same signatures as the CPU functions they mirror ---- */
 void bpd_dequant_q8_0_gpu(const uint8_t* raw_dev, float* out_dev, int n_blocks);           /* bench/bpd_cpu.c:3960 */
 /* ids must index rows of the table (0 <= id < rows); bench/bpd_cpu.c:4002 */
