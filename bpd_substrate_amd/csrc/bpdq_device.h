@@ -52,6 +52,21 @@ template <int CTRL>
 __device__ __forceinline__ int dpp_i(int v) {
     return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, true);
 }
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+// v_permlane32_swap: afterwards a's lanes 32-63 hold b's old lanes 0-31 and b's
+// lanes 0-31 hold a's old lanes 32-63 (the other halves are unchanged).
+__device__ __forceinline__ void swap32(uint32_t& a, uint32_t& b) {
+    typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2 r = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+    a = r.x;
+    b = r.y;
+}
 __device__ __forceinline__ float xor_f(float v, int mask) { return __shfl_xor(v, mask, 64); }
 __device__ __forceinline__ int xor_i(int v, int mask) { return __shfl_xor(v, mask, 64); }
 

@@ -267,18 +267,140 @@ __device__ __forceinline__ void gemv_rows(const uint8_t* __restrict__ w, const u
             }
         }
     }
+    // slot q lives in lanes 8q..8q+7: row_mirror pairs slots q and q^1, then the
+    // four pair sums are lanes 0, 16, 32, 48
 #pragma unroll
     for (int r = 0; r < R; r++) {
         float v = s[r];
-        v = v + xor_f(v, 8);
-        v = v + xor_f(v, 16);
-        v = v + xor_f(v, 32);
-        if (lane == 0 && row0 + r < M) y[row0 + r] = v;
+        v = v + dpp_f<0x140>(v);
+        const float p01 = readlane_f(v, 0), p23 = readlane_f(v, 16);
+        const float p45 = readlane_f(v, 32), p67 = readlane_f(v, 48);
+        if (lane == 0 && row0 + r < M) y[row0 + r] = (p01 + p23) + (p45 + p67);
     }
 }
 
+// ----------------------------------------------------------------------------
+// The same GEMV with 4 lanes per super-block: lane (bl = lane/4, c4 = lane%4)
+// takes qs chunks c4 and c4+4 of super-block 16t+bl, so the header broadcast,
+// the scale decode and the fp32 combine are shared by two chunks and a wave
+// pass covers 16 super-blocks.  The qs are loaded as in gemv_rows (instruction
+// A: all 8 chunks of blocks 16t..16t+7, B: of blocks 16t+8..16t+15, chunk
+// 4(lane/32)+c4) and one v_permlane32_swap per dword pairs them up.  Integer
+// sums are the same integers and the fp32 order is the same order, so the
+// output equals gemv_rows bit for bit.  Fewer VALU per block pays off on
+// shorter matrices and on long rows.
+// ----------------------------------------------------------------------------
+template <int ORDER>
+__device__ __forceinline__ float block4_contrib(const uint4& hdr, const uint32_t (&qd0)[4], const uint32_t (&qd1)[4],
+                                                const XOps& x0, const XOps& x1, int c4) {
+    int S[4] = {0, 0, 0, 0};  // low and high nibbles of chunks c4 and c4+4
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        S[0] = sdot4(qd0[k] & 0x0F0F0F0Fu, x0.lo[k], S[0]);
+        S[1] = sdot4((qd0[k] >> 4) & 0x0F0F0F0Fu, x0.hi[k], S[1]);
+        S[2] = sdot4(qd1[k] & 0x0F0F0F0Fu, x1.lo[k], S[2]);
+        S[3] = sdot4((qd1[k] >> 4) & 0x0F0F0F0Fu, x1.hi[k], S[3]);
+    }
+    // byte c4 of the scale dwords gives (sc, m) of sub-blocks c4 and c4+4
+    const uint32_t a = hdr.y >> (8 * c4), b = hdr.z >> (8 * c4), h = hdr.w >> (8 * c4);
+    const int m0 = (int)(b & 63u), m1 = (int)(((h >> 4) & 15u) | ((b >> 2) & 0x30u));
+    int isum;
+    if (ORDER == 0) {
+        const int sc0 = (int)(a & 63u), sc1 = (int)((h & 15u) | ((a >> 2) & 0x30u));
+        isum = __mul24(sc0, S[0] + S[1]) + __mul24(sc1, S[2] + S[3]);
+    } else {
+        // GGUF: chunk c covers halves of sub-blocks 2(c/2) (low) and 2(c/2)+1 (high)
+        const int i0 = 2 * (c4 >> 1);
+        int s0, s1, s2, s3, unused;
+        q4k_scale_min(hdr.y, hdr.z, hdr.w, i0, s0, unused);
+        q4k_scale_min(hdr.y, hdr.z, hdr.w, i0 + 1, s1, unused);
+        q4k_scale_min(hdr.y, hdr.z, hdr.w, i0 + 4, s2, unused);
+        q4k_scale_min(hdr.y, hdr.z, hdr.w, i0 + 5, s3, unused);
+        isum = __mul24(s0, S[0]) + __mul24(s1, S[1]) + __mul24(s2, S[2]) + __mul24(s3, S[3]);
+    }
+    int msum = __mul24(m0, x0.bsum) + __mul24(m1, x1.bsum);
+    isum += dpp_i<0xB1>(isum);
+    isum += dpp_i<0x4E>(isum);
+    msum += dpp_i<0xB1>(msum);
+    msum += dpp_i<0x4E>(msum);
+    const float dd = f16_ieee(hdr.x) * x0.dy;
+    const float dm = f16_ieee(hdr.x >> 16) * x0.dy;
+    const float av = dd * (float)isum;
+    const float mm = dm * (float)msum;
+    return av - mm;
+}
+
+template <int ORDER, int R>
+__device__ __forceinline__ void gemv4_rows(const uint8_t* __restrict__ w, const uint8_t* __restrict__ xq,
+                                           float* __restrict__ y, int M, int nb, int row0) {
+    const int lane = threadIdx.x & 63;
+    const int bl = lane >> 2, c4 = lane & 3;
+    const int chunk = 4 * (lane >> 5) + c4;
+    const uint32_t row_bytes = (uint32_t)nb * kQ4KBytes;
+    const int ngroups = (nb + 15) >> 4;
+    float s[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) s[r] = 0.0f;
+
+    for (int t = 0; t < ngroups; t++) {
+        const int b = 16 * t + bl;
+        const bool valid = b < nb, valid_hi = b + 8 < nb;
+        const uint32_t boff = (uint32_t)min(b, nb - 1) * kQ4KBytes;
+        const uint32_t offA = (uint32_t)min(16 * t + (bl & 7), nb - 1) * kQ4KBytes + 16 + 16 * chunk;
+        const uint32_t offB = (uint32_t)min(16 * t + 8 + (bl & 7), nb - 1) * kQ4KBytes + 16 + 16 * chunk;
+        uint4 qa[R], qb[R];
+        uint32_t hw[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const uint8_t* rp = w + (size_t)min(row0 + r, M - 1) * row_bytes;
+            qa[r] = ld_u128(rp + offA);
+            qb[r] = ld_u128(rp + offB);
+            hw[r] = ld_u32(rp + boff + 4 * c4);
+        }
+        const uint8_t* xb = xq + (size_t)min(b, nb - 1) * kQ8KBytes;
+        const XOps x0 = load_x<ORDER>(xb, c4);
+        const XOps x1 = load_x<ORDER>(xb, c4 + 4);
+        // every load of the pass is issued before any of its data is used
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            uint32_t qd0[4] = {qa[r].x, qa[r].y, qa[r].z, qa[r].w};
+            uint32_t qd1[4] = {qb[r].x, qb[r].y, qb[r].z, qb[r].w};
+#pragma unroll
+            for (int k = 0; k < 4; k++) swap32(qd0[k], qd1[k]);
+            const float c = block4_contrib<ORDER>(bcast_header(hw[r]), qd0, qd1, x0, x1, c4);
+            uint32_t c_lo = __float_as_uint(c), c_hi = c_lo;
+            swap32(c_lo, c_hi);  // lanes 0-31: c_hi = contribution of block b+8
+            float v = s[r];
+            if (valid) v = v + c;
+            if (valid_hi) v = v + __uint_as_float(c_hi);
+            s[r] = v;
+        }
+    }
+    // slot q lives in lanes 4q..4q+3 (q < 8): row_half_mirror pairs slots q and
+    // q^1, row_mirror the pairs, and lanes 0 and 16 hold the two halves
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        float v = s[r];
+        v = v + dpp_f<0x141>(v);
+        v = v + dpp_f<0x140>(v);
+        const float lo = readlane_f(v, 0), hi = readlane_f(v, 16);
+        if (lane == 0 && row0 + r < M) y[row0 + r] = lo + hi;
+    }
+}
+
+// KIND 0: gemv_rows (8 lanes per super-block), KIND 1: gemv4_rows.
+template <int KIND, int ORDER, int R, int G>
+__device__ __forceinline__ void rows(const uint8_t* __restrict__ w, const uint8_t* __restrict__ xq,
+                                     float* __restrict__ y, int M, int nb, int row0) {
+    if (KIND == 0)
+        gemv_rows<ORDER, R, G>(w, xq, y, M, nb, row0);
+    else
+        gemv4_rows<ORDER, R>(w, xq, y, M, nb, row0);
+}
+
 // R rows per wave, WPB waves per workgroup.
-template <int ORDER, int R, int G, int WPB>
+template <int KIND, int ORDER, int R, int G, int WPB>
 __global__ __launch_bounds__(64 * WPB) void k_q4k_q8k_gemv(const uint8_t* __restrict__ w,
                                                            const uint8_t* __restrict__ xq, float* __restrict__ y,
                                                            int M, int nb) {
@@ -286,7 +408,7 @@ __global__ __launch_bounds__(64 * WPB) void k_q4k_q8k_gemv(const uint8_t* __rest
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int row0 = (blockIdx.x * WPB + wave) * R;
     if (row0 >= M) return;
-    gemv_rows<ORDER, R, G>(w, xq, y, M, nb, row0);
+    rows<KIND, ORDER, R, G>(w, xq, y, M, nb, row0);
 }
 
 // Up to kMulti matrices that share one activation vector (Q/K/V, gate/up) in
@@ -301,7 +423,7 @@ struct MultiArgs {
     int first[kMulti + 1];
 };
 
-template <int ORDER, int R, int G, int WPB>
+template <int KIND, int ORDER, int R, int G, int WPB>
 __global__ __launch_bounds__(64 * WPB) void k_q4k_q8k_gemv_multi(MultiArgs a, const uint8_t* __restrict__ xq, int nb) {
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int gw = blockIdx.x * WPB + wave;
@@ -312,25 +434,40 @@ __global__ __launch_bounds__(64 * WPB) void k_q4k_q8k_gemv_multi(MultiArgs a, co
     if (gw >= a.first[kMulti]) return;
     const int row0 = (gw - a.first[i]) * R;
     if (row0 >= a.M[i]) return;
-    gemv_rows<ORDER, R, G>(a.w[i], xq, a.y[i], a.M[i], nb, row0);
+    rows<KIND, ORDER, R, G>(a.w[i], xq, a.y[i], a.M[i], nb, row0);
 }
 
-template <int ORDER, int R, int G, int WPB>
+// Launch shapes, measured on MI355X (one graph of back-to-back launches over
+// weights that do not fit the MALL):
+//   kWide  8 lanes/block, 2 rows x 2 block-groups per wave, 4 waves: best for
+//          many short rows (14336x4096: 7.37 us vs 7.75 for k4Row2)
+//   k4Row1 4 lanes/block, 1 row per wave, 8 waves: best up to ~8K rows of
+//          K <= 4096 (4096x4096: 3.87 us vs 4.00; 1024x4096: 2.85 vs 3.05)
+//   k4Row2 4 lanes/block, 2 rows per wave, 4 waves: best for long rows
+//          (4096x14336: 8.13 us vs 8.57)
+enum GemvShape { kWide, k4Row1, k4Row2 };
+
+static GemvShape choose_shape(int rows, int nb) {
+    if (nb > 16) return k4Row2;
+    return rows <= 8192 ? k4Row1 : kWide;
+}
+
+static int shape_rows_per_wave(GemvShape sh) { return sh == k4Row1 ? 1 : 2; }
+
+template <int KIND, int ORDER, int R, int G, int WPB>
 static void launch_gemv(const uint8_t* w, const uint8_t* xq, float* y, int M, int nb, hipStream_t s) {
     const int waves = (M + R - 1) / R;
-    hipLaunchKernelGGL((k_q4k_q8k_gemv<ORDER, R, G, WPB>), dim3((waves + WPB - 1) / WPB), dim3(64 * WPB), 0, s, w,
-                       xq, y, M, nb);
+    hipLaunchKernelGGL((k_q4k_q8k_gemv<KIND, ORDER, R, G, WPB>), dim3((waves + WPB - 1) / WPB), dim3(64 * WPB), 0,
+                       s, w, xq, y, M, nb);
 }
 
 template <int ORDER>
 static void launch_gemv_order(const uint8_t* w, const uint8_t* xq, float* y, int M, int nb, hipStream_t s) {
-    const int ngroups = (nb + 7) / 8;
-    // shapes measured on MI355X: 2 rows x 2 block-groups per pass; wider
-    // workgroups pay off when the row is long (several passes per wave)
-    if (ngroups <= 2)
-        launch_gemv<ORDER, 2, 2, 4>(w, xq, y, M, nb, s);
-    else
-        launch_gemv<ORDER, 2, 2, 8>(w, xq, y, M, nb, s);
+    switch (choose_shape(M, nb)) {
+        case kWide: launch_gemv<0, ORDER, 2, 2, 4>(w, xq, y, M, nb, s); break;
+        case k4Row1: launch_gemv<1, ORDER, 1, 1, 8>(w, xq, y, M, nb, s); break;
+        case k4Row2: launch_gemv<1, ORDER, 2, 1, 4>(w, xq, y, M, nb, s); break;
+    }
 }
 
 void launch_qmatmul_q4k_q8k(const uint8_t* w, const uint8_t* xq, float* y, int M, int K, int order, hipStream_t s) {
@@ -341,16 +478,29 @@ void launch_qmatmul_q4k_q8k(const uint8_t* w, const uint8_t* xq, float* y, int M
         launch_gemv_order<1>(w, xq, y, M, nb, s);
 }
 
-template <int ORDER, int WPB>
+template <int KIND, int ORDER, int R, int G, int WPB>
 static void launch_multi(const MultiArgs& a, const uint8_t* xq, int nb, hipStream_t s) {
     const int waves = a.first[kMulti];
-    hipLaunchKernelGGL((k_q4k_q8k_gemv_multi<ORDER, 2, 2, WPB>), dim3((waves + WPB - 1) / WPB), dim3(64 * WPB), 0, s,
-                       a, xq, nb);
+    hipLaunchKernelGGL((k_q4k_q8k_gemv_multi<KIND, ORDER, R, G, WPB>), dim3((waves + WPB - 1) / WPB),
+                       dim3(64 * WPB), 0, s, a, xq, nb);
+}
+
+template <int ORDER>
+static void launch_multi_order(const MultiArgs& a, GemvShape sh, const uint8_t* xq, int nb, hipStream_t s) {
+    switch (sh) {
+        case kWide: launch_multi<0, ORDER, 2, 2, 4>(a, xq, nb, s); break;
+        case k4Row1: launch_multi<1, ORDER, 1, 1, 8>(a, xq, nb, s); break;
+        case k4Row2: launch_multi<1, ORDER, 2, 1, 4>(a, xq, nb, s); break;
+    }
 }
 
 void launch_qmatmul_q4k_q8k_multi(const uint8_t* const* w, float* const* y, const int* M, int n, const uint8_t* xq,
                                   int K, int order, hipStream_t s) {
-    constexpr int R = 2;
+    const int nb = K / 256;
+    int total = 0;
+    for (int i = 0; i < n; i++) total += M[i];
+    const GemvShape sh = choose_shape(total, nb);
+    const int R = shape_rows_per_wave(sh);
     MultiArgs a;
     int waves = 0;
     for (int i = 0; i < kMulti; i++) {
@@ -363,13 +513,10 @@ void launch_qmatmul_q4k_q8k_multi(const uint8_t* const* w, float* const* y, cons
     }
     a.first[kMulti] = waves;
     if (waves == 0) return;
-    const int nb = K / 256;
-    const bool long_rows = (nb + 7) / 8 > 2;
-    if (order == 0) {
-        if (long_rows) launch_multi<0, 8>(a, xq, nb, s); else launch_multi<0, 4>(a, xq, nb, s);
-    } else {
-        if (long_rows) launch_multi<1, 8>(a, xq, nb, s); else launch_multi<1, 4>(a, xq, nb, s);
-    }
+    if (order == 0)
+        launch_multi_order<0>(a, sh, xq, nb, s);
+    else
+        launch_multi_order<1>(a, sh, xq, nb, s);
 }
 
 }  // namespace bpdq

@@ -18,44 +18,76 @@ def lanes():
 
 # ---------------------------------------------------------------- Q4_K x Q8_K GEMV
 
-def q4k_gemv_shape(nb):
-    ngroups = (nb + 7) // 8
-    return (2, 2, 4) if ngroups <= 2 else (2, 2, 8)
+def q4k_gemv_shape(rows, nb):
+    """(kind, R, G, WPB) as chosen by choose_shape() in q4k.hip."""
+    if nb > 16:
+        return (1, 2, 1, 4)
+    return (1, 1, 1, 8) if rows <= 8192 else (0, 2, 2, 4)
+
+
+def x_accesses(c):
+    """(offset, bytes) of every Q8_K access load_x makes for chunk c (both element maps)."""
+    return ((0, 4), (260 + 4 * c, 4), (4 + 32 * c, 16), (4 + 32 * c + 16, 16),
+            (4 + 64 * (c >> 1) + 16 * (c & 1), 16), (4 + 64 * (c >> 1) + 16 * (c & 1) + 32, 16))
+
+
+def check_wide(M, nb, row0, R, G):
+    w_size, x_size = M * nb * Q4K, nb * Q8K
+    l = lanes()
+    q, c = l >> 3, l & 7
+    for t0 in range(0, (nb + 7) >> 3, G):
+        for g in range(G):
+            b = (t0 + g) * 8 + q
+            bb = np.where(b < nb, b, nb - 1)
+            for r in range(R):
+                base = min(row0 + r, M - 1) * nb * Q4K + bb * Q4K
+                assert (base + 16 + 16 * c + 16).max() <= w_size and base.min() >= 0
+                assert (base + 4 * (c & 3) + 4).max() <= w_size
+            for off, size in x_accesses(c):
+                assert np.max(bb * Q8K + off + size) <= x_size and np.min(bb * Q8K + off) >= 0
+
+
+def check_four(M, nb, row0, R):
+    w_size, x_size = M * nb * Q4K, nb * Q8K
+    l = lanes()
+    bl, c4 = l >> 2, l & 3
+    chunk = 4 * (l >> 5) + c4
+    assert chunk.max() < 8
+    for t in range((nb + 15) >> 4):
+        b = 16 * t + bl
+        bb = np.minimum(b, nb - 1)
+        off_a = np.minimum(16 * t + (bl & 7), nb - 1) * Q4K + 16 + 16 * chunk
+        off_b = np.minimum(16 * t + 8 + (bl & 7), nb - 1) * Q4K + 16 + 16 * chunk
+        for r in range(R):
+            rb = min(row0 + r, M - 1) * nb * Q4K
+            for off in (off_a, off_b):
+                assert (rb + off + 16).max() <= w_size and (rb + off).min() >= 0
+            assert (rb + bb * Q4K + 4 * c4 + 4).max() <= w_size
+        for c in (c4, c4 + 4):
+            for off, size in x_accesses(c):
+                assert np.max(bb * Q8K + off + size) <= x_size and np.min(bb * Q8K + off) >= 0
 
 
 @pytest.mark.parametrize("M,K", [(4096, 4096), (14336, 4096), (4096, 14336), (1024, 4096), (1, 256), (5, 512),
-                                 (13, 2304), (9, 2304), (3, 0), (64, 1024), (77, 512)])
-def test_q4k_q8k_gemv_in_bounds(M, K):
+                                 (13, 2304), (9, 2304), (3, 0), (64, 1024), (77, 512), (6144, 4096), (28672, 4096),
+                                 (8193, 4096), (17, 4352), (2, 14336)])
+@pytest.mark.parametrize("force", [None, (0, 2, 2, 4), (1, 1, 1, 8), (1, 2, 1, 4)])
+def test_q4k_q8k_gemv_in_bounds(M, K, force):
     nb = K // 256
-    R, G, WPB = q4k_gemv_shape(nb)
+    if nb == 0:
+        return  # no block-group pass runs: the kernels read nothing and write y = +0.0
+    kind, R, G, WPB = force or q4k_gemv_shape(M, nb)
     waves = (M + R - 1) // R
     grid = (waves + WPB - 1) // WPB
-    w_size, x_size, y_size = M * nb * Q4K, nb * Q8K, M * 4
-    l = lanes()
-    q, c = l >> 3, l & 7
-    ngroups = (nb + 7) >> 3
     for blk in sorted({0, grid - 1}):
         for wave in range(WPB):
             row0 = (blk * WPB + wave) * R
             if row0 >= M:
                 continue
-            for t0 in range(0, ngroups, G):
-                for g in range(G):
-                    b = (t0 + g) * 8 + q
-                    bb = np.where(b < nb, b, nb - 1)
-                    for r in range(R):
-                        base = min(row0 + r, M - 1) * nb * Q4K + bb * Q4K
-                        assert (base + 16 + 16 * c + 16).max() <= w_size and base.min() >= 0
-                        assert (base + 4 * (c & 3) + 4).max() <= w_size
-                    xb = bb * Q8K
-                    # (offset, bytes) of every x access: dy, bsum pair, low and high quants of both maps
-                    for off, size in ((0, 4), (260 + 4 * c, 4), (4 + 32 * c, 16), (4 + 32 * c + 16, 16),
-                                      (4 + 64 * (c >> 1) + 16 * (c & 1), 16),
-                                      (4 + 64 * (c >> 1) + 16 * (c & 1) + 32, 16)):
-                        assert np.max(xb + off + size) <= x_size and np.min(xb + off) >= 0
+            (check_wide(M, nb, row0, R, G) if kind == 0 else check_four(M, nb, row0, R))
             for r in range(R):
                 if row0 + r < M:
-                    assert (row0 + r) * 4 + 4 <= y_size
+                    assert (row0 + r) * 4 + 4 <= M * 4
 
 
 # ---------------------------------------------------------------- dequant
