@@ -148,20 +148,28 @@ def decode_chain(torch, L, T, dev, gpu, synth, n_layers=32, tokens=10):
                                              for t, (n, (m, kk)) in enumerate(shapes.items())}))
         acts.append([torch.from_numpy(synth.normal_f32(n, synth.key(43, 10 * i + j))).to(dev)
                      for j, n in enumerate((e, e, e, ff))])
-    chain = decode.GemvChain(layers, d, dev)
-    torch.cuda.synchronize()
-    L.bpd_gpu_set_stream(T.stream.cuda_stream)
-    chain.step(acts)
-    torch.cuda.synchronize()
-    gpu.check()
-    us = T.us_per_launch([lambda: chain.step(acts)] * tokens)  # us per token
-    wb = chain.weight_bytes()
-    gpu.check()
-    out = {"us_per_token": round(us, 1), "tokens_per_s": round(1e6 / us, 1), "weight_bytes": wb,
-           "gb_s": round(wb / us / 1e3, 1), "frac_hbm": round(wb / us / 1e3 / HBM_PEAK_GBS, 4),
-           "launches_per_token": 8 * n_layers,
-           "roofline_us_per_token": round(wb / HBM_PEAK_GBS / 1e3, 1)}
-    del chain, layers, acts
+    out = {}
+    for fused in (True, False):
+        chain = decode.GemvChain(layers, d, dev, fused=fused)
+        torch.cuda.synchronize()
+        L.bpd_gpu_set_stream(T.stream.cuda_stream)
+        chain.step(acts)
+        torch.cuda.synchronize()
+        gpu.check()
+        us = T.us_per_launch([lambda: chain.step(acts)] * tokens)  # us per token
+        wb = chain.weight_bytes()
+        gpu.check()
+        r = {"us_per_token": round(us, 1), "tokens_per_s": round(1e6 / us, 1), "weight_bytes": wb,
+             "gb_s": round(wb / us / 1e3, 1), "frac_hbm": round(wb / us / 1e3 / HBM_PEAK_GBS, 4),
+             "launches_per_token": (4 if fused else 8) * n_layers,
+             "roofline_us_per_token": round(wb / HBM_PEAK_GBS / 1e3, 1)}
+        if fused:
+            out = r
+            out["quantization"] = "Q8_K of each activation inside its GEMV kernel"
+        else:
+            out["separate_quant_launches"] = {k: r[k] for k in ("us_per_token", "tokens_per_s", "launches_per_token")}
+        del chain
+    del layers, acts
     return out
 
 

@@ -141,6 +141,45 @@ void q4k_q8k(const uint8_t* w, const uint8_t* xq, float* y, int M, int K, int or
     check_launch(fn);
 }
 
+// List arguments of the multi-matrix GEMVs.  Returns true when there is work.
+bool check_multi(Check& c, const uint8_t* const* w_list, float* const* y_list, const int* M_list, int n, int K) {
+    if (n < 0 || n > 4) c.fail(BPDQ_ERR_SHAPE, "n", "is outside 0..4");
+    c.nonneg(K, "K").multiple(K, 256, "K");
+    if (!c.ok || n == 0) return false;
+    c.ptr(w_list, 1, "w_list").ptr(y_list, 1, "y_list").ptr(M_list, 1, "M_list");
+    if (!c.ok) return false;
+    int rows = 0;
+    for (int i = 0; i < n && c.ok; i++) {
+        c.nonneg(M_list[i], "M_list[i]");
+        if (!c.ok || M_list[i] == 0) continue;
+        rows += M_list[i];
+        c.ptr(y_list[i], 4, "y_list[i]");
+        if (K > 0) c.ptr(w_list[i], 16, "w_list[i]");
+    }
+    return c.ok && rows > 0;
+}
+
+// Q4_K x Q8_K(x) with the quantization of fp32 x inside the GEMV kernel.
+// Beyond the fused kernel's K it quantizes into the workspace first (same bits).
+void fused(const uint8_t* const* w_list, float* const* y_list, const int* M_list, int n, const float* x, int K,
+           const char* fn) {
+    Check c(fn);
+    if (!check_multi(c, w_list, y_list, M_list, n, K)) return;
+    if (K > 0) c.ptr(x, 16, "x");
+    if (!c.ok) return;
+    if (K == 0) {
+        bpdq::launch_qmatmul_q4k_q8k_multi(w_list, y_list, M_list, n, nullptr, 0, 0, g_stream);
+    } else if (K <= bpdq::fused_max_k()) {
+        bpdq::launch_qmatmul_q4k_fused_multi(w_list, y_list, M_list, n, x, K, 0, g_stream);
+    } else {
+        uint8_t* xq = static_cast<uint8_t*>(workspace((size_t)(K / 256) * 292, fn));
+        if (!xq) return;
+        bpdq::launch_quant_q8k(x, xq, K, g_stream);
+        bpdq::launch_qmatmul_q4k_q8k_multi(w_list, y_list, M_list, n, xq, K, 0, g_stream);
+    }
+    check_launch(fn);
+}
+
 }  // namespace
 
 extern "C" {
@@ -199,23 +238,20 @@ void bpd_qmatmul_q4k_q8k_multi_gpu(const uint8_t* const* w_list, float* const* y
                                    const uint8_t* xq, int K) {
     const char* fn = "bpd_qmatmul_q4k_q8k_multi_gpu";
     Check c(fn);
-    if (n < 0 || n > 4) c.fail(BPDQ_ERR_SHAPE, "n", "is outside 0..4");
-    c.nonneg(K, "K").multiple(K, 256, "K");
-    if (!c.ok || n == 0) return;
-    c.ptr(w_list, 1, "w_list").ptr(y_list, 1, "y_list").ptr(M_list, 1, "M_list");
-    if (!c.ok) return;
-    int rows = 0;
-    for (int i = 0; i < n && c.ok; i++) {
-        c.nonneg(M_list[i], "M_list[i]");
-        if (!c.ok || M_list[i] == 0) continue;
-        rows += M_list[i];
-        c.ptr(y_list[i], 4, "y_list[i]");
-        if (K > 0) c.ptr(w_list[i], 16, "w_list[i]");
-    }
+    if (!check_multi(c, w_list, y_list, M_list, n, K)) return;
     if (K > 0) c.ptr(xq, 4, "xq");
-    if (!c.ok || rows == 0) return;
+    if (!c.ok) return;
     bpdq::launch_qmatmul_q4k_q8k_multi(w_list, y_list, M_list, n, xq, K, 0, g_stream);
     check_launch(fn);
+}
+
+void bpd_qmatmul_q4k_q8k_fused_multi_gpu(const uint8_t* const* w_list, float* const* y_list, const int* M_list, int n,
+                                         const float* x, int K) {
+    fused(w_list, y_list, M_list, n, x, K, "bpd_qmatmul_q4k_q8k_fused_multi_gpu");
+}
+
+void bpd_qmatmul_q4k_q8k_fused_gpu(const uint8_t* w, const float* x, float* y, int M, int K) {
+    fused(&w, &y, &M, 1, x, K, "bpd_qmatmul_q4k_q8k_fused_gpu");
 }
 
 void* qgpu_alloc(int bytes) { return alloc(bytes, "qgpu_alloc"); }

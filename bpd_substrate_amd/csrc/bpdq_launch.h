@@ -14,6 +14,11 @@ void launch_qmatmul_q4k_q8k(const uint8_t* w, const uint8_t* xq, float* y, int M
 
 void launch_qmatmul_q4k_q8k_multi(const uint8_t* const* w, float* const* y, const int* M, int n, const uint8_t* xq,
                                   int K, int order, hipStream_t s);
+// The fused-quantization GEMV handles K <= fused_max_k(); beyond it callers
+// quantize into a buffer and use launch_qmatmul_q4k_q8k_multi.
+int fused_max_k();
+void launch_qmatmul_q4k_fused_multi(const uint8_t* const* w, float* const* y, const int* M, int n, const float* x,
+                                    int K, int order, hipStream_t s);
 
 void launch_dequant_q8_0(const uint8_t* raw, float* out, int n_blocks, hipStream_t s);
 void launch_embed_q8_0(const uint8_t* table, const int32_t* ids, float* out, int n_tokens, int embed_dim,

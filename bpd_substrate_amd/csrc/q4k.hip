@@ -222,39 +222,86 @@ __device__ __forceinline__ float block_contrib(const uint4& hdr, const uint4& qv
     return a - mm;
 }
 
+// x operands of chunk c of super-block b, from the Q8_K vector in global
+// memory (LX = false) or from the workgroup's LDS copy of it (LX = true: kXS
+// bytes per block, qs at 0, the 16 int16 bsums at 256, d at 288).
+constexpr int kXS = 304;
+
+template <int ORDER, bool LX>
+__device__ __forceinline__ XOps get_x(const uint8_t* __restrict__ xsrc, int b, int c) {
+    if (!LX) return load_x<ORDER>(xsrc + (int64_t)b * kQ8KBytes, c);
+    const uint8_t* xb = xsrc + b * kXS;
+    const int off_lo = ORDER == 0 ? 32 * c : 64 * (c >> 1) + 16 * (c & 1);
+    const int off_hi = ORDER == 0 ? 32 * c + 16 : off_lo + 32;
+    const uint4 lo = *reinterpret_cast<const uint4*>(xb + off_lo);
+    const uint4 hi = *reinterpret_cast<const uint4*>(xb + off_hi);
+    const uint32_t bs = *reinterpret_cast<const uint32_t*>(xb + 256 + 4 * c);
+    XOps o;
+    o.lo[0] = lo.x; o.lo[1] = lo.y; o.lo[2] = lo.z; o.lo[3] = lo.w;
+    o.hi[0] = hi.x; o.hi[1] = hi.y; o.hi[2] = hi.z; o.hi[3] = hi.w;
+    o.bsum = (int)(int16_t)(bs & 0xFFFFu) + (int)(int16_t)(bs >> 16);
+    o.dy = *reinterpret_cast<const float*>(xb + 288);
+    return o;
+}
+
+// Weight operands of one pass of gemv_rows: qs chunk and header dword of
+// G block-groups x R rows.
+template <int R, int G>
+struct WideW {
+    uint4 qv[G][R];
+    uint32_t hw[G][R];
+};
+
+template <int R, int G>
+__device__ __forceinline__ void wide_load_g(WideW<R, G>& W, int g, const uint8_t* __restrict__ w, int M, int nb,
+                                            int row0, int t0) {
+    const int lane = threadIdx.x & 63;
+    const int q = lane >> 3, c = lane & 7;
+    const int64_t row_bytes = (int64_t)nb * kQ4KBytes;
+    const int b = (t0 + g) * 8 + q;
+    const int bb = b < nb ? b : nb - 1;
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const uint8_t* blk = w + (int64_t)min(row0 + r, M - 1) * row_bytes + (int64_t)bb * kQ4KBytes;
+        W.qv[g][r] = ld_u128(blk + 16 + 16 * c);
+        W.hw[g][r] = ld_u32(blk + 4 * (c & 3));
+    }
+}
+
 // One wave's R rows: each pass issues the loads of G block-groups x R rows (a
 // 16-byte qs load and a header dword per lane each) before computing any of
 // them, so every wave keeps its whole share of the stream in flight.  Rows past
 // M reuse row M-1 and slots past nb reuse block nb-1 (their results are
-// discarded), so every address stays in the tensors.  row0 < M.
-template <int ORDER, int R, int G>
-__device__ __forceinline__ void gemv_rows(const uint8_t* __restrict__ w, const uint8_t* __restrict__ xq,
-                                          float* __restrict__ y, int M, int nb, int row0) {
+// discarded), so every address stays in the tensors.  row0 < M.  With PRE the
+// weights of the first pass were loaded by the caller into `pre`.
+template <int ORDER, int R, int G, bool LX, bool PRE>
+__device__ __forceinline__ void gemv_rows(const uint8_t* __restrict__ w, const uint8_t* __restrict__ xsrc,
+                                          float* __restrict__ y, int M, int nb, int row0, const WideW<R, G>& pre) {
     const int lane = threadIdx.x & 63;
     const int q = lane >> 3, c = lane & 7;
-    const int64_t row_bytes = (int64_t)nb * kQ4KBytes;
     const int ngroups = (nb + 7) >> 3;
     float s[R];
 #pragma unroll
     for (int r = 0; r < R; r++) s[r] = 0.0f;
 
     for (int t0 = 0; t0 < ngroups; t0 += G) {
-        uint32_t hw[G][R];
-        uint4 qv[G][R];
+        WideW<R, G> W;
         XOps x[G];
         bool valid[G];
 #pragma unroll
         for (int g = 0; g < G; g++) {
             const int b = (t0 + g) * 8 + q;
             valid[g] = b < nb;
-            const int bb = valid[g] ? b : nb - 1;
+            if (PRE && t0 == 0) {
 #pragma unroll
-            for (int r = 0; r < R; r++) {
-                const uint8_t* blk = w + (int64_t)min(row0 + r, M - 1) * row_bytes + (int64_t)bb * kQ4KBytes;
-                qv[g][r] = ld_u128(blk + 16 + 16 * c);
-                hw[g][r] = ld_u32(blk + 4 * (c & 3));
+                for (int r = 0; r < R; r++) {
+                    W.qv[g][r] = pre.qv[g][r];
+                    W.hw[g][r] = pre.hw[g][r];
+                }
+            } else {
+                wide_load_g<R, G>(W, g, w, M, nb, row0, t0);
             }
-            x[g] = load_x<ORDER>(xq + (int64_t)bb * kQ8KBytes, c);
+            x[g] = get_x<ORDER, LX>(xsrc, valid[g] ? b : nb - 1, c);
         }
         // every load of the pass is issued before any of its data is used
         __builtin_amdgcn_sched_barrier(0);
@@ -262,7 +309,7 @@ __device__ __forceinline__ void gemv_rows(const uint8_t* __restrict__ w, const u
         for (int g = 0; g < G; g++) {
 #pragma unroll
             for (int r = 0; r < R; r++) {
-                const float cb = block_contrib<ORDER>(bcast_header(hw[g][r]), qv[g][r], x[g], c);
+                const float cb = block_contrib<ORDER>(bcast_header(W.hw[g][r]), W.qv[g][r], x[g], c);
                 if (valid[g]) s[r] = s[r] + cb;
             }
         }
@@ -330,13 +377,36 @@ __device__ __forceinline__ float block4_contrib(const uint4& hdr, const uint32_t
     return av - mm;
 }
 
-template <int ORDER, int R>
-__device__ __forceinline__ void gemv4_rows(const uint8_t* __restrict__ w, const uint8_t* __restrict__ xq,
-                                           float* __restrict__ y, int M, int nb, int row0) {
+// Weight operands of one pass of gemv4_rows.
+template <int R>
+struct FourW {
+    uint4 qa[R], qb[R];
+    uint32_t hw[R];
+};
+
+template <int R>
+__device__ __forceinline__ void four_load(FourW<R>& W, const uint8_t* __restrict__ w, int M, int nb, int row0, int t) {
     const int lane = threadIdx.x & 63;
     const int bl = lane >> 2, c4 = lane & 3;
     const int chunk = 4 * (lane >> 5) + c4;
     const uint32_t row_bytes = (uint32_t)nb * kQ4KBytes;
+    const uint32_t boff = (uint32_t)min(16 * t + bl, nb - 1) * kQ4KBytes;
+    const uint32_t offA = (uint32_t)min(16 * t + (bl & 7), nb - 1) * kQ4KBytes + 16 + 16 * chunk;
+    const uint32_t offB = (uint32_t)min(16 * t + 8 + (bl & 7), nb - 1) * kQ4KBytes + 16 + 16 * chunk;
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const uint8_t* rp = w + (size_t)min(row0 + r, M - 1) * row_bytes;
+        W.qa[r] = ld_u128(rp + offA);
+        W.qb[r] = ld_u128(rp + offB);
+        W.hw[r] = ld_u32(rp + boff + 4 * c4);
+    }
+}
+
+template <int ORDER, int R, bool LX, bool PRE>
+__device__ __forceinline__ void gemv4_rows(const uint8_t* __restrict__ w, const uint8_t* __restrict__ xsrc,
+                                           float* __restrict__ y, int M, int nb, int row0, const FourW<R>& pre) {
+    const int lane = threadIdx.x & 63;
+    const int bl = lane >> 2, c4 = lane & 3;
     const int ngroups = (nb + 15) >> 4;
     float s[R];
 #pragma unroll
@@ -345,30 +415,23 @@ __device__ __forceinline__ void gemv4_rows(const uint8_t* __restrict__ w, const 
     for (int t = 0; t < ngroups; t++) {
         const int b = 16 * t + bl;
         const bool valid = b < nb, valid_hi = b + 8 < nb;
-        const uint32_t boff = (uint32_t)min(b, nb - 1) * kQ4KBytes;
-        const uint32_t offA = (uint32_t)min(16 * t + (bl & 7), nb - 1) * kQ4KBytes + 16 + 16 * chunk;
-        const uint32_t offB = (uint32_t)min(16 * t + 8 + (bl & 7), nb - 1) * kQ4KBytes + 16 + 16 * chunk;
-        uint4 qa[R], qb[R];
-        uint32_t hw[R];
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            const uint8_t* rp = w + (size_t)min(row0 + r, M - 1) * row_bytes;
-            qa[r] = ld_u128(rp + offA);
-            qb[r] = ld_u128(rp + offB);
-            hw[r] = ld_u32(rp + boff + 4 * c4);
-        }
-        const uint8_t* xb = xq + (size_t)min(b, nb - 1) * kQ8KBytes;
-        const XOps x0 = load_x<ORDER>(xb, c4);
-        const XOps x1 = load_x<ORDER>(xb, c4 + 4);
+        FourW<R> W;
+        if (PRE && t == 0)
+            W = pre;
+        else
+            four_load<R>(W, w, M, nb, row0, t);
+        const int bb = min(b, nb - 1);
+        const XOps x0 = get_x<ORDER, LX>(xsrc, bb, c4);
+        const XOps x1 = get_x<ORDER, LX>(xsrc, bb, c4 + 4);
         // every load of the pass is issued before any of its data is used
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            uint32_t qd0[4] = {qa[r].x, qa[r].y, qa[r].z, qa[r].w};
-            uint32_t qd1[4] = {qb[r].x, qb[r].y, qb[r].z, qb[r].w};
+            uint32_t qd0[4] = {W.qa[r].x, W.qa[r].y, W.qa[r].z, W.qa[r].w};
+            uint32_t qd1[4] = {W.qb[r].x, W.qb[r].y, W.qb[r].z, W.qb[r].w};
 #pragma unroll
             for (int k = 0; k < 4; k++) swap32(qd0[k], qd1[k]);
-            const float c = block4_contrib<ORDER>(bcast_header(hw[r]), qd0, qd1, x0, x1, c4);
+            const float c = block4_contrib<ORDER>(bcast_header(W.hw[r]), qd0, qd1, x0, x1, c4);
             uint32_t c_lo = __float_as_uint(c), c_hi = c_lo;
             swap32(c_lo, c_hi);  // lanes 0-31: c_hi = contribution of block b+8
             float v = s[r];
@@ -390,13 +453,32 @@ __device__ __forceinline__ void gemv4_rows(const uint8_t* __restrict__ w, const 
 }
 
 // KIND 0: gemv_rows (8 lanes per super-block), KIND 1: gemv4_rows.
-template <int KIND, int ORDER, int R, int G>
-__device__ __forceinline__ void rows(const uint8_t* __restrict__ w, const uint8_t* __restrict__ xq,
-                                     float* __restrict__ y, int M, int nb, int row0) {
-    if (KIND == 0)
-        gemv_rows<ORDER, R, G>(w, xq, y, M, nb, row0);
+template <int KIND, int R, int G>
+struct PassW;
+template <int R, int G>
+struct PassW<0, R, G> { using type = WideW<R, G>; };
+template <int R, int G>
+struct PassW<1, R, G> { using type = FourW<R>; };
+
+template <int KIND, int R, int G>
+__device__ __forceinline__ void load_first(typename PassW<KIND, R, G>::type& W, const uint8_t* __restrict__ w, int M,
+                                           int nb, int row0) {
+    if constexpr (KIND == 0) {
+#pragma unroll
+        for (int g = 0; g < G; g++) wide_load_g<R, G>(W, g, w, M, nb, row0, 0);
+    } else {
+        four_load<R>(W, w, M, nb, row0, 0);
+    }
+}
+
+template <int KIND, int ORDER, int R, int G, bool LX = false, bool PRE = false>
+__device__ __forceinline__ void rows(const uint8_t* __restrict__ w, const uint8_t* __restrict__ xsrc,
+                                     float* __restrict__ y, int M, int nb, int row0,
+                                     const typename PassW<KIND, R, G>::type& pre) {
+    if constexpr (KIND == 0)
+        gemv_rows<ORDER, R, G, LX, PRE>(w, xsrc, y, M, nb, row0, pre);
     else
-        gemv4_rows<ORDER, R>(w, xq, y, M, nb, row0);
+        gemv4_rows<ORDER, R, LX, PRE>(w, xsrc, y, M, nb, row0, pre);
 }
 
 // R rows per wave, WPB waves per workgroup.
@@ -408,7 +490,8 @@ __global__ __launch_bounds__(64 * WPB) void k_q4k_q8k_gemv(const uint8_t* __rest
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int row0 = (blockIdx.x * WPB + wave) * R;
     if (row0 >= M) return;
-    rows<KIND, ORDER, R, G>(w, xq, y, M, nb, row0);
+    typename PassW<KIND, R, G>::type unused;
+    rows<KIND, ORDER, R, G>(w, xq, y, M, nb, row0, unused);
 }
 
 // Up to kMulti matrices that share one activation vector (Q/K/V, gate/up) in
@@ -421,6 +504,8 @@ struct MultiArgs {
     float* y[kMulti];
     int M[kMulti];
     int first[kMulti + 1];
+    int safe;  // a matrix with M > 0
+    int rows;  // total rows
 };
 
 template <int KIND, int ORDER, int R, int G, int WPB>
@@ -434,7 +519,8 @@ __global__ __launch_bounds__(64 * WPB) void k_q4k_q8k_gemv_multi(MultiArgs a, co
     if (gw >= a.first[kMulti]) return;
     const int row0 = (gw - a.first[i]) * R;
     if (row0 >= a.M[i]) return;
-    rows<KIND, ORDER, R, G>(a.w[i], xq, a.y[i], a.M[i], nb, row0);
+    typename PassW<KIND, R, G>::type unused;
+    rows<KIND, ORDER, R, G>(a.w[i], xq, a.y[i], a.M[i], nb, row0, unused);
 }
 
 // Launch shapes, measured on MI355X (one graph of back-to-back launches over
@@ -494,14 +580,16 @@ static void launch_multi_order(const MultiArgs& a, GemvShape sh, const uint8_t* 
     }
 }
 
-void launch_qmatmul_q4k_q8k_multi(const uint8_t* const* w, float* const* y, const int* M, int n, const uint8_t* xq,
-                                  int K, int order, hipStream_t s) {
-    const int nb = K / 256;
-    int total = 0;
-    for (int i = 0; i < n; i++) total += M[i];
-    const GemvShape sh = choose_shape(total, nb);
-    const int R = shape_rows_per_wave(sh);
+// Wave numbering of a multi launch for the shape that choose_shape picks.
+static MultiArgs make_multi_args(const uint8_t* const* w, float* const* y, const int* M, int n, int nb) {
     MultiArgs a;
+    a.rows = 0;
+    a.safe = 0;
+    for (int i = 0; i < n; i++) {
+        a.rows += M[i];
+        if (M[i] > 0 && M[a.safe] == 0) a.safe = i;
+    }
+    const int R = shape_rows_per_wave(choose_shape(a.rows, nb));
     int waves = 0;
     for (int i = 0; i < kMulti; i++) {
         const bool used = i < n;
@@ -512,11 +600,160 @@ void launch_qmatmul_q4k_q8k_multi(const uint8_t* const* w, float* const* y, cons
         waves += used ? (M[i] + R - 1) / R : 0;
     }
     a.first[kMulti] = waves;
-    if (waves == 0) return;
+    return a;
+}
+
+void launch_qmatmul_q4k_q8k_multi(const uint8_t* const* w, float* const* y, const int* M, int n, const uint8_t* xq,
+                                  int K, int order, hipStream_t s) {
+    const int nb = K / 256;
+    const MultiArgs a = make_multi_args(w, y, M, n, nb);
+    if (a.first[kMulti] == 0) return;
+    const GemvShape sh = choose_shape(a.rows, nb);
     if (order == 0)
         launch_multi_order<0>(a, sh, xq, nb, s);
     else
         launch_multi_order<1>(a, sh, xq, nb, s);
+}
+
+// ----------------------------------------------------------------------------
+// GEMV with the Q8_K quantization of an fp32 x fused in: every workgroup
+// quantizes all of x into LDS (the same arithmetic as k_quant_q8k, so the
+// Q8_K bytes are identical), then runs the GEMV of its rows reading x from LDS.
+// Order of work per wave: issue the fp32 x loads of its quantization share,
+// issue the weight loads of its first pass, quantize as soon as x arrives
+// (x loads were issued first, so waiting for them does not wait for the
+// weights), barrier, GEMV.  The weight stream is in flight while x is
+// quantized, so the quantization hides behind HBM latency instead of costing
+// a launch.  y equals quant_q8_k followed by the Q8_K GEMV bit for bit.
+//
+// Quantization share: 16 lanes per Q8_K block (the block is one DPP row), lane
+// li holds elements 16li..16li+15 = bsum group li; a workgroup covers 4*WPB
+// blocks per iteration, IT iterations.
+// ----------------------------------------------------------------------------
+template <int IT>
+struct XPre {
+    float4 v[IT][4];
+};
+
+template <int WPB, int IT>
+__device__ __forceinline__ void x32_load(XPre<IT>& P, const float* __restrict__ x, int nb) {
+    const int tid = threadIdx.x, gq = tid >> 4, li = tid & 15;
+#pragma unroll
+    for (int it = 0; it < IT; it++) {
+        const int b = min(it * 4 * WPB + gq, nb - 1);
+        const float* xb = x + (int64_t)b * 256 + 16 * li;
+#pragma unroll
+        for (int k = 0; k < 4; k++) P.v[it][k] = *reinterpret_cast<const float4*>(xb + 4 * k);
+    }
+}
+
+template <int WPB, int IT>
+__device__ __forceinline__ void x32_quantize(const XPre<IT>& P, uint8_t* __restrict__ xl, int nb) {
+    const int tid = threadIdx.x, gq = tid >> 4, li = tid & 15;
+#pragma unroll
+    for (int it = 0; it < IT; it++) {
+        const int b = it * 4 * WPB + gq;
+        float e[16];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            e[4 * k] = P.v[it][k].x;
+            e[4 * k + 1] = P.v[it][k].y;
+            e[4 * k + 2] = P.v[it][k].z;
+            e[4 * k + 3] = P.v[it][k].w;
+        }
+        float amax = fabsf(e[0]);
+#pragma unroll
+        for (int k = 1; k < 16; k++) amax = fmaxf(amax, fabsf(e[k]));
+        amax = fmaxf(amax, dpp_f<0xB1>(amax));   // quad_perm [1,0,3,2]
+        amax = fmaxf(amax, dpp_f<0x4E>(amax));   // quad_perm [2,3,0,1]
+        amax = fmaxf(amax, dpp_f<0x141>(amax));  // row_half_mirror
+        amax = fmaxf(amax, dpp_f<0x140>(amax));  // row_mirror: the whole 16-lane row
+        const float d = amax / 127.0f;
+        const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+        uint32_t pk[4] = {0u, 0u, 0u, 0u};
+        int bsum = 0;
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            const int qv = (int)__builtin_rintf(e[k] * id);
+            bsum += qv;
+            pk[k >> 2] |= (uint32_t)(qv & 0xFF) << (8 * (k & 3));
+        }
+        if (b < nb) {
+            uint8_t* xb = xl + b * kXS;
+            *reinterpret_cast<uint4*>(xb + 16 * li) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+            *reinterpret_cast<int16_t*>(xb + 256 + 2 * li) = (int16_t)bsum;
+            if (li == 0) *reinterpret_cast<float*>(xb + 288) = d;
+        }
+    }
+}
+
+// Matrix index and first row of wave gw in a MultiArgs launch; waves past the
+// last row get (safe, 0) so that their first-pass loads stay in a real tensor.
+__device__ __forceinline__ bool wave_rows(const MultiArgs& a, int gw, int R, int& i, int& row0) {
+    i = 0;
+#pragma unroll
+    for (int k = 1; k < kMulti; k++)
+        if (gw >= a.first[k]) i = k;
+    row0 = (gw - a.first[i]) * R;
+    const bool has = gw < a.first[kMulti] && row0 < a.M[i];
+    if (!has) {
+        i = a.safe;
+        row0 = 0;
+    }
+    return has;
+}
+
+template <int KIND, int ORDER, int R, int G, int WPB, int IT>
+__global__ __launch_bounds__(64 * WPB) void k_q4k_fused_gemv(MultiArgs a, const float* __restrict__ x, int nb) {
+    extern __shared__ __align__(16) uint8_t xl[];
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    int i, row0;
+    const bool has = wave_rows(a, blockIdx.x * WPB + wave, R, i, row0);
+    XPre<IT> P;
+    x32_load<WPB, IT>(P, x, nb);
+    typename PassW<KIND, R, G>::type pre;
+    load_first<KIND, R, G>(pre, a.w[i], a.M[i], nb, row0);
+    __builtin_amdgcn_sched_barrier(0);
+    x32_quantize<WPB, IT>(P, xl, nb);
+    __syncthreads();
+    if (!has) return;
+    rows<KIND, ORDER, R, G, true, true>(a.w[i], xl, a.y[i], a.M[i], nb, row0, pre);
+}
+
+template <int KIND, int ORDER, int R, int G, int WPB, int IT>
+static void launch_fused(const MultiArgs& a, const float* x, int nb, hipStream_t s) {
+    const int waves = a.first[kMulti];
+    hipLaunchKernelGGL((k_q4k_fused_gemv<KIND, ORDER, R, G, WPB, IT>), dim3((waves + WPB - 1) / WPB),
+                       dim3(64 * WPB), (size_t)nb * kXS, s, a, x, nb);
+}
+
+template <int ORDER>
+static void launch_fused_order(const MultiArgs& a, GemvShape sh, const float* x, int nb, hipStream_t s) {
+    // IT = quantization iterations: 4*WPB blocks each
+    switch (sh) {
+        case kWide: launch_fused<0, ORDER, 2, 2, 4, 1>(a, x, nb, s); break;
+        case k4Row1: launch_fused<1, ORDER, 1, 1, 8, 1>(a, x, nb, s); break;
+        case k4Row2:
+            if (nb <= 32)
+                launch_fused<1, ORDER, 2, 1, 8, 1>(a, x, nb, s);
+            else
+                launch_fused<1, ORDER, 2, 1, 8, 2>(a, x, nb, s);
+            break;
+    }
+}
+
+int fused_max_k() { return 64 * 256; }
+
+void launch_qmatmul_q4k_fused_multi(const uint8_t* const* w, float* const* y, const int* M, int n, const float* x,
+                                    int K, int order, hipStream_t s) {
+    const int nb = K / 256;
+    MultiArgs a = make_multi_args(w, y, M, n, nb);
+    if (a.first[kMulti] == 0) return;
+    const GemvShape sh = choose_shape(a.rows, nb);
+    if (order == 0)
+        launch_fused_order<0>(a, sh, x, nb, s);
+    else
+        launch_fused_order<1>(a, sh, x, nb, s);
 }
 
 }  // namespace bpdq

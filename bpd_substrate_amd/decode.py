@@ -4,10 +4,14 @@ Per layer this issues the seven weight GEMVs of the reference's block
 (bench/bpd_cpu.c:5642-5733: Q, K, V, O, gate, up, down) as Q4_K x Q8_K GEMVs,
 each activation quantized to Q8_K first:
 
-    xa = Q8_K(attn_in)   ->  q, k, v = Wq xa, Wk xa, Wv xa      (one fused launch)
+    xa = Q8_K(attn_in)   ->  q, k, v = Wq xa, Wk xa, Wv xa      (one multi-matrix launch)
     xo = Q8_K(attn_out)  ->  o = Wo xo
-    xf = Q8_K(ffn_in)    ->  g, u = Wgate xf, Wup xf            (one fused launch)
+    xf = Q8_K(ffn_in)    ->  g, u = Wgate xf, Wup xf            (one multi-matrix launch)
     xh = Q8_K(ffn_mid)   ->  d = Wdown xh
+
+With fused=True (the default) each quantization happens inside the GEMV kernel
+that consumes it (bpd_qmatmul_q4k_q8k_fused*_gpu): 4 launches per layer instead
+of 8, same bits.
 
 The norms, RoPE, attention and SwiGLU between them are not part of this path
 (the activations are inputs), which makes this the GEMV portion a decode step
@@ -44,12 +48,13 @@ class Dims:
 class GemvChain:
     """Buffers and launch sequence for the decode-step GEMV chain."""
 
-    def __init__(self, layers, dims=Dims(), device=None):
+    def __init__(self, layers, dims=Dims(), device=None, fused=True):
         import torch
 
         self.L = load_hip()
         self.layers = layers
         self.d = dims
+        self.fused = fused
         dev = device or layers[0].q.device
         e, kv, ff = dims.n_embd, dims.n_kv, dims.ff
         q8k = lambda n: torch.empty(n // formats.Q8K_ELEMS * formats.Q8K_BYTES, dtype=torch.uint8, device=dev)
@@ -58,25 +63,26 @@ class GemvChain:
         self.out = [dict(q=f32(e), k=f32(kv), v=f32(kv), o=f32(e), gate=f32(ff), up=f32(ff), down=f32(e))
                     for _ in layers]
 
-    def _multi(self, ws, ys, Ms, xq, K):
-        n = len(ws)
+    def _gemv(self, ws, ys, Ms, x, xq, K):
+        """GEMVs of the weights ws on the fp32 activation x (xq: its Q8_K buffer)."""
+        L, n = self.L, len(ws)
         w_arr = (ctypes.c_void_p * n)(*[w.data_ptr() for w in ws])
         y_arr = (ctypes.c_void_p * n)(*[y.data_ptr() for y in ys])
         m_arr = (ctypes.c_int * n)(*Ms)
-        self.L.bpd_qmatmul_q4k_q8k_multi_gpu(w_arr, y_arr, m_arr, n, xq.data_ptr(), K)
+        if self.fused:
+            L.bpd_qmatmul_q4k_q8k_fused_multi_gpu(w_arr, y_arr, m_arr, n, x.data_ptr(), K)
+        else:
+            L.bpd_quant_q8_k_gpu(x.data_ptr(), xq.data_ptr(), K)
+            L.bpd_qmatmul_q4k_q8k_multi_gpu(w_arr, y_arr, m_arr, n, xq.data_ptr(), K)
 
     def layer(self, i, attn_in, attn_out, ffn_in, ffn_mid):
         """Launch layer i's chain (asynchronous, on the library's current stream)."""
-        L, d, w, o = self.L, self.d, self.layers[i], self.out[i]
+        d, w, o = self.d, self.layers[i], self.out[i]
         e, kv, ff = d.n_embd, d.n_kv, d.ff
-        L.bpd_quant_q8_k_gpu(attn_in.data_ptr(), self.xa.data_ptr(), e)
-        self._multi([w.q, w.k, w.v], [o["q"], o["k"], o["v"]], [e, kv, kv], self.xa, e)
-        L.bpd_quant_q8_k_gpu(attn_out.data_ptr(), self.xo.data_ptr(), e)
-        L.bpd_qmatmul_q4k_q8k_gpu(w.o.data_ptr(), self.xo.data_ptr(), o["o"].data_ptr(), e, e)
-        L.bpd_quant_q8_k_gpu(ffn_in.data_ptr(), self.xf.data_ptr(), e)
-        self._multi([w.gate, w.up], [o["gate"], o["up"]], [ff, ff], self.xf, e)
-        L.bpd_quant_q8_k_gpu(ffn_mid.data_ptr(), self.xh.data_ptr(), ff)
-        L.bpd_qmatmul_q4k_q8k_gpu(w.down.data_ptr(), self.xh.data_ptr(), o["down"].data_ptr(), e, ff)
+        self._gemv([w.q, w.k, w.v], [o["q"], o["k"], o["v"]], [e, kv, kv], attn_in, self.xa, e)
+        self._gemv([w.o], [o["o"]], [e], attn_out, self.xo, e)
+        self._gemv([w.gate, w.up], [o["gate"], o["up"]], [ff, ff], ffn_in, self.xf, e)
+        self._gemv([w.down], [o["down"]], [e], ffn_mid, self.xh, ff)
 
     def step(self, acts):
         """One token: every layer's chain; acts[i] = (attn_in, attn_out, ffn_in, ffn_mid)."""

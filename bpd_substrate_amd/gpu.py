@@ -116,16 +116,34 @@ def qmatmul_q4k_q8k(w, xq, M, K, order=formats.ORDER_BPD, out=None):
 
 def qmatmul_q4k_q8k_multi(ws, xq, Ms, K, outs=None):
     """Up to four Q4_K GEMVs sharing the activation xq, in one launch."""
+    return _multi("bpd_qmatmul_q4k_q8k_multi_gpu", ws, xq, Ms, K, outs)
+
+
+def qmatmul_q4k_q8k_fused(w, x, M, K, out=None):
+    """Q4_K x Q8_K(x) for fp32 x, quantized inside the GEMV kernel (bits equal quant + GEMV)."""
+    import torch
+
+    out = _empty(M, torch.float32, x) if out is None else out
+    _use_torch_stream()
+    call("bpd_qmatmul_q4k_q8k_fused_gpu", w, x, out, M, K)
+    return out
+
+
+def qmatmul_q4k_q8k_fused_multi(ws, x, Ms, K, outs=None):
+    """Up to four Q4_K GEMVs of one fp32 activation, quantized in-kernel, in one launch."""
+    return _multi("bpd_qmatmul_q4k_q8k_fused_multi_gpu", ws, x, Ms, K, outs)
+
+
+def _multi(name, ws, x, Ms, K, outs):
     import torch
 
     n = len(ws)
-    outs = [_empty(m, torch.float32, xq) for m in Ms] if outs is None else outs
+    outs = [_empty(m, torch.float32, x) for m in Ms] if outs is None else outs
     w_arr = (ctypes.c_void_p * n)(*[_ptr(w) for w in ws])
     y_arr = (ctypes.c_void_p * n)(*[_ptr(y) for y in outs])
     m_arr = (ctypes.c_int * n)(*Ms)
     _use_torch_stream()
-    call("bpd_qmatmul_q4k_q8k_multi_gpu", ctypes.addressof(w_arr), ctypes.addressof(y_arr), ctypes.addressof(m_arr),
-         n, xq, K)
+    call(name, ctypes.addressof(w_arr), ctypes.addressof(y_arr), ctypes.addressof(m_arr), n, x, K)
     return outs
 
 

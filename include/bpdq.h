@@ -101,6 +101,15 @@ void bpd_qmatmul_q4k_q8k_gguf_gpu(const uint8_t* w_dev, const uint8_t* xq8k_dev,
 void bpd_qmatmul_q4k_q8k_multi_gpu(const uint8_t* const* w_list, float* const* y_list, const int* M_list, int n,
                                    const uint8_t* xq8k_dev, int K);
 
+/* The two above with the activation given as fp32 x[K] (16-byte aligned): the kernel quantizes x
+ * to Q8_K itself, so y is bit-identical to bpd_quant_q8_k_gpu followed by
+ * bpd_qmatmul_q4k_q8k_gpu / _multi_gpu, in one launch instead of two.  For a decode step, which
+ * re-quantizes every activation before its GEMVs (bench/bpd_cpu.c:5642-5733 quantizes inside
+ * each bpd_qmatmul_q8_0_llamafile_cpu call, bench/bpd_cpu.c:4429-4452). */
+void bpd_qmatmul_q4k_q8k_fused_gpu(const uint8_t* w_dev, const float* x_dev, float* y_dev, int M, int K);
+void bpd_qmatmul_q4k_q8k_fused_multi_gpu(const uint8_t* const* w_list, float* const* y_list, const int* M_list,
+                                         int n, const float* x_dev, int K);
+
 /* ---- Q8_0 on the GPU, same signatures as the CPU functions they mirror ---- */
 void bpd_dequant_q8_0_gpu(const uint8_t* raw_dev, float* out_dev, int n_blocks);           /* bench/bpd_cpu.c:3960 */
 /* ids must index rows of the table (0 <= id < rows); bench/bpd_cpu.c:4002 */

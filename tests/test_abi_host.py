@@ -79,6 +79,19 @@ def test_validation_rejects_before_launch():
     _err(3)
     L.bpd_embed_lookup_q8_0_gpu(0x1000, None, 0x3000, 2, 64)
     _err(1)
+    # fused-quantization GEMVs: fp32 x must be 16-byte aligned, list sizes 0..4
+    L.bpd_qmatmul_q4k_q8k_fused_gpu(0x1000, 0x2004, 0x3000, 4, 256)
+    assert "x is not 16-byte aligned" in _err(3)
+    L.bpd_qmatmul_q4k_q8k_fused_gpu(0x1000, 0x2000, 0x3000, 4, 200)
+    _err(2)
+    import ctypes
+    w_arr, y_arr, m_arr = (ctypes.c_void_p * 5)(), (ctypes.c_void_p * 5)(), (ctypes.c_int * 5)()
+    L.bpd_qmatmul_q4k_q8k_fused_multi_gpu(w_arr, y_arr, m_arr, 5, 0x2000, 256)
+    assert "outside 0..4" in _err(2)
+    m_arr[0] = 3
+    w_arr[0], y_arr[0] = 0x1000, None
+    L.bpd_qmatmul_q4k_q8k_fused_multi_gpu(w_arr, y_arr, m_arr, 1, 0x2000, 256)
+    assert "y_list[i]" in _err(1)
     assert L.qgpu_alloc(-5) is None
     _err(2)
     L.qgpu_h2d(None, None, -1)

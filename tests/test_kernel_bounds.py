@@ -179,3 +179,31 @@ def test_q8_0_gemm_S_in_bounds(mw, mt, K):
                     assert wa.min() >= 0 and (wa + 34).max() <= mw * bpr
                     assert xa.min() >= 0 and (xa + 34).max() <= mt * bpr
                     assert u.max() < 4 and rr.max() < 128
+
+
+# ---------------------------------------------------------------- fused Q8_K quantization prologue
+
+def fused_config(rows, nb):
+    """(WPB, IT) of launch_fused_order in q4k.hip."""
+    kind, R, G, WPB = q4k_gemv_shape(rows, nb)
+    if kind == 0:
+        return 4, 1
+    if R == 1:
+        return 8, 1
+    return 8, 1 if nb <= 32 else 2
+
+
+@pytest.mark.parametrize("rows", [1, 300, 8192, 8193, 14336, 28672])
+def test_fused_quantization_covers_x_and_stays_in_bounds(rows):
+    for nb in range(1, 65):  # fused_max_k() = 64 * 256
+        WPB, IT = fused_config(rows, nb)
+        assert IT * 4 * WPB >= nb, "some Q8_K block would never be quantized"
+        tid = np.arange(64 * WPB)
+        gq, li = tid >> 4, tid & 15
+        for it in range(IT):
+            b = np.minimum(it * 4 * WPB + gq, nb - 1)
+            assert ((b * 256 + 16 * li + 16) <= nb * 256).all() and (b >= 0).all()
+            bw = it * 4 * WPB + gq
+            ok = bw < nb
+            assert ((bw[ok] * 304 + 16 * li[ok] + 16) <= nb * 304).all()
+            assert ((bw[ok] * 304 + 288 + 4) <= nb * 304).all()
