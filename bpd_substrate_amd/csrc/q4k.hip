@@ -580,8 +580,14 @@ static void launch_multi_order(const MultiArgs& a, GemvShape sh, const uint8_t* 
     }
 }
 
-// Wave numbering of a multi launch for the shape that choose_shape picks.
-static MultiArgs make_multi_args(const uint8_t* const* w, float* const* y, const int* M, int n, int nb) {
+static int total_rows(const int* M, int n) {
+    int rows = 0;
+    for (int i = 0; i < n; i++) rows += M[i];
+    return rows;
+}
+
+// Wave numbering of a multi launch with R rows per wave.
+static MultiArgs make_multi_args(const uint8_t* const* w, float* const* y, const int* M, int n, int R) {
     MultiArgs a;
     a.rows = 0;
     a.safe = 0;
@@ -589,7 +595,6 @@ static MultiArgs make_multi_args(const uint8_t* const* w, float* const* y, const
         a.rows += M[i];
         if (M[i] > 0 && M[a.safe] == 0) a.safe = i;
     }
-    const int R = shape_rows_per_wave(choose_shape(a.rows, nb));
     int waves = 0;
     for (int i = 0; i < kMulti; i++) {
         const bool used = i < n;
@@ -606,9 +611,9 @@ static MultiArgs make_multi_args(const uint8_t* const* w, float* const* y, const
 void launch_qmatmul_q4k_q8k_multi(const uint8_t* const* w, float* const* y, const int* M, int n, const uint8_t* xq,
                                   int K, int order, hipStream_t s) {
     const int nb = K / 256;
-    const MultiArgs a = make_multi_args(w, y, M, n, nb);
+    const GemvShape sh = choose_shape(total_rows(M, n), nb);
+    const MultiArgs a = make_multi_args(w, y, M, n, shape_rows_per_wave(sh));
     if (a.first[kMulti] == 0) return;
-    const GemvShape sh = choose_shape(a.rows, nb);
     if (order == 0)
         launch_multi_order<0>(a, sh, xq, nb, s);
     else
@@ -727,33 +732,25 @@ static void launch_fused(const MultiArgs& a, const float* x, int nb, hipStream_t
                        dim3(64 * WPB), (size_t)nb * kXS, s, a, x, nb);
 }
 
-template <int ORDER>
-static void launch_fused_order(const MultiArgs& a, GemvShape sh, const float* x, int nb, hipStream_t s) {
-    // IT = quantization iterations: 4*WPB blocks each
-    switch (sh) {
-        case kWide: launch_fused<0, ORDER, 2, 2, 4, 1>(a, x, nb, s); break;
-        case k4Row1: launch_fused<1, ORDER, 1, 1, 8, 1>(a, x, nb, s); break;
-        case k4Row2:
-            if (nb <= 32)
-                launch_fused<1, ORDER, 2, 1, 8, 1>(a, x, nb, s);
-            else
-                launch_fused<1, ORDER, 2, 1, 8, 2>(a, x, nb, s);
-            break;
-    }
-}
-
+// Fused shapes, measured on MI355X for the decode-chain GEMVs (one graph of
+// back-to-back launches, weights beyond the MALL): K <= 4096 takes the 8-lane
+// kernel with 4 waves (QKV 6144x4096: 5.14 us vs 5.44 for k4Row1; O 4096x4096:
+// 4.36 vs 4.40; gate+up 2x14336x4096: 14.24), longer rows the 4-lane kernel
+// with one row per wave and 16 waves (4096x14336: 9.20 us vs 9.50 for 2 rows x
+// 8 waves).  IT = 1: 4*WPB Q8_K blocks per quantization pass cover nb.
 int fused_max_k() { return 64 * 256; }
 
 void launch_qmatmul_q4k_fused_multi(const uint8_t* const* w, float* const* y, const int* M, int n, const float* x,
                                     int K, int order, hipStream_t s) {
     const int nb = K / 256;
-    MultiArgs a = make_multi_args(w, y, M, n, nb);
+    const bool wide = nb <= 16;
+    const MultiArgs a = make_multi_args(w, y, M, n, wide ? 2 : 1);
     if (a.first[kMulti] == 0) return;
-    const GemvShape sh = choose_shape(a.rows, nb);
-    if (order == 0)
-        launch_fused_order<0>(a, sh, x, nb, s);
-    else
-        launch_fused_order<1>(a, sh, x, nb, s);
+    if (order == 0) {
+        if (wide) launch_fused<0, 0, 2, 2, 4, 1>(a, x, nb, s); else launch_fused<1, 0, 1, 1, 16, 1>(a, x, nb, s);
+    } else {
+        if (wide) launch_fused<0, 1, 2, 2, 4, 1>(a, x, nb, s); else launch_fused<1, 1, 1, 1, 16, 1>(a, x, nb, s);
+    }
 }
 
 }  // namespace bpdq

@@ -71,7 +71,7 @@ def check_four(M, nb, row0, R):
 @pytest.mark.parametrize("M,K", [(4096, 4096), (14336, 4096), (4096, 14336), (1024, 4096), (1, 256), (5, 512),
                                  (13, 2304), (9, 2304), (3, 0), (64, 1024), (77, 512), (6144, 4096), (28672, 4096),
                                  (8193, 4096), (17, 4352), (2, 14336)])
-@pytest.mark.parametrize("force", [None, (0, 2, 2, 4), (1, 1, 1, 8), (1, 2, 1, 4)])
+@pytest.mark.parametrize("force", [None, (0, 2, 2, 4), (1, 1, 1, 8), (1, 2, 1, 4), (1, 1, 1, 16)])
 def test_q4k_q8k_gemv_in_bounds(M, K, force):
     nb = K // 256
     if nb == 0:
@@ -184,13 +184,8 @@ def test_q8_0_gemm_S_in_bounds(mw, mt, K):
 # ---------------------------------------------------------------- fused Q8_K quantization prologue
 
 def fused_config(rows, nb):
-    """(WPB, IT) of launch_fused_order in q4k.hip."""
-    kind, R, G, WPB = q4k_gemv_shape(rows, nb)
-    if kind == 0:
-        return 4, 1
-    if R == 1:
-        return 8, 1
-    return 8, 1 if nb <= 32 else 2
+    """(WPB, IT) of launch_qmatmul_q4k_fused_multi in q4k.hip."""
+    return (4, 1) if nb <= 16 else (16, 1)
 
 
 @pytest.mark.parametrize("rows", [1, 300, 8192, 8193, 14336, 28672])
