@@ -260,6 +260,7 @@ namespace bpdq {
 // ----------------------------------------------------------------------------
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kGT = 128;  // tile rows = tile tokens
 constexpr int kGB = 4;    // blocks per LDS stage
@@ -350,28 +351,26 @@ __global__ __launch_bounds__(256) void k_q8_0_gemm_S(const uint8_t* __restrict__
 #pragma unroll
             for (int ct = 0; ct < 2; ct++)
                 fb[ct] = *reinterpret_cast<const i32x4*>(&s.bq[buf][u][wc * 64 + ct * 32 + col][16 * half]);
-            float bd[2];
+            // scale products RN(Ad*Bd) of every cell as a rank-1 fp32 MFMA: lanes 0-31
+            // give K index 0 (row / column scale), lanes 32-63 K index 1 (zero), so
+            // D = Ad*Bd + 0*0 + 0, rounded once.  |Ad*Bd| >= 2^-48 or 0 (f16 inputs),
+            // never an fp32 subnormal.
+            float av[2], bv[2];
 #pragma unroll
-            for (int ct = 0; ct < 2; ct++) bd[ct] = s.bd[buf][u][wc * 64 + ct * 32 + col];
+            for (int rt = 0; rt < 2; rt++) av[rt] = half ? 0.0f : s.ad[buf][u][wr * 64 + rt * 32 + col];
+#pragma unroll
+            for (int ct = 0; ct < 2; ct++) bv[ct] = half ? 0.0f : s.bd[buf][u][wc * 64 + ct * 32 + col];
 #pragma unroll
             for (int rt = 0; rt < 2; rt++) {
-                float ad[16];
-#pragma unroll
-                for (int g = 0; g < 4; g++) {
-                    const float4 v = *reinterpret_cast<const float4*>(&s.ad[buf][u][wr * 64 + rt * 32 + 8 * g + 4 * half]);
-                    ad[4 * g + 0] = v.x;
-                    ad[4 * g + 1] = v.y;
-                    ad[4 * g + 2] = v.z;
-                    ad[4 * g + 3] = v.w;
-                }
 #pragma unroll
                 for (int ct = 0; ct < 2; ct++) {
                     const i32x16 zero = {0};
+                    const f32x16 fzero = {0.0f};
                     const i32x16 sb = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[rt], fb[ct], zero, 0, 0, 0);
+                    const f32x16 delta = __builtin_amdgcn_mfma_f32_32x32x2f32(av[rt], bv[ct], fzero, 0, 0, 0);
 #pragma unroll
                     for (int r = 0; r < 16; r++) {
-                        const float delta = ad[r] * bd[ct];
-                        const float prod = (float)sb[r] * delta;
+                        const float prod = (float)sb[r] * delta[r];
                         acc[rt][ct][r] = acc[rt][ct][r] + prod;
                     }
                 }
@@ -398,6 +397,130 @@ __global__ __launch_bounds__(256) void k_q8_0_gemm_S(const uint8_t* __restrict__
         }
 }
 
+// ----------------------------------------------------------------------------
+// The same GEMM when K is a multiple of 128 and W, X are 4-byte aligned, with
+// coalesced staging and more waves.  A half-stage is 4 blocks; its bytes of one
+// row are 136 contiguous bytes, and thread t stages blocks 2p, 2p+1 (p = t%2)
+// of row (t/2)%128 of W (t < 256) or X: 68 contiguous bytes, 17 dword loads.
+// In registers block 2p's scale is the low half of dword 0 and its quants start
+// 2 bytes into dword 0 (one v_alignbit per dword); block 2p+1's scale is the
+// high half of dword 8, its quants dwords 9..16.  Two LDS slots alternate:
+// while one is computed, the next half-stage is loaded and written to the
+// other, one barrier per half-stage.  8 waves (4 x 2) each own 32 weight rows x
+// 64 tokens (two 32x32 MFMA tiles), so two workgroups (16 waves) share a CU
+// and the MFMA latency of one wave hides behind the fp32 epilogue of others.
+// ----------------------------------------------------------------------------
+constexpr int kGH = 4;  // blocks per half-stage
+
+struct __align__(16) GemmLdsH {
+    uint8_t q[2][2][kGH][kGT][32];  // [slot][W / X][block][row][quants]
+    float d[2][2][kGH][kGT];
+};
+
+__device__ __forceinline__ void half_load(uint32_t (&raw)[17], const uint8_t* __restrict__ W,
+                                          const uint8_t* __restrict__ X, int m0, int n0, int m_weight, int m_tokens,
+                                          int b0, int64_t bpr) {
+    const int t = threadIdx.x, row = (t >> 1) & (kGT - 1), p = t & 1;
+    const uint8_t* src = t < 2 * kGT ? W + (int64_t)min(m0 + row, m_weight - 1) * bpr
+                                     : X + (int64_t)min(n0 + row, m_tokens - 1) * bpr;
+    src += (int64_t)(b0 + 2 * p) * kQ80Bytes;
+#pragma unroll
+    for (int k = 0; k < 17; k++) raw[k] = *reinterpret_cast<const uint32_t*>(src + 4 * k);
+}
+
+__device__ __forceinline__ void half_store(GemmLdsH& s, int slot, const uint32_t (&d)[17]) {
+    const int t = threadIdx.x, mat = t >> 8, row = (t >> 1) & (kGT - 1), p = t & 1;
+    uint32_t q[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) q[k] = __builtin_amdgcn_alignbit(d[k + 1], d[k], 16);
+    uint4* dst = reinterpret_cast<uint4*>(s.q[slot][mat][2 * p][row]);
+    dst[0] = make_uint4(q[0], q[1], q[2], q[3]);
+    dst[1] = make_uint4(q[4], q[5], q[6], q[7]);
+    dst = reinterpret_cast<uint4*>(s.q[slot][mat][2 * p + 1][row]);
+    dst[0] = make_uint4(d[9], d[10], d[11], d[12]);
+    dst[1] = make_uint4(d[13], d[14], d[15], d[16]);
+    s.d[slot][mat][2 * p][row] = f16_ieee(d[0] & 0xFFFFu);
+    s.d[slot][mat][2 * p + 1][row] = f16_ieee(d[8] >> 16);
+}
+
+__global__ __launch_bounds__(512, 2) void k_q8_0_gemm_SH(const uint8_t* __restrict__ W,
+                                                         const uint8_t* __restrict__ X, float* __restrict__ out,
+                                                         int m_weight, int m_tokens, int nb) {
+    __shared__ GemmLdsH s;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int wr = wave >> 1, wc = wave & 1;
+    const int m0 = blockIdx.x * kGT, n0 = blockIdx.y * kGT;
+    const int64_t bpr = (int64_t)nb * kQ80Bytes;
+    const int col = lane & 31, half = lane >> 5;
+    const int ra = wr * 32 + col;
+    const uint32_t kmask = half ? 0u : 0xFFFFFFFFu;  // K index 1 of the scale MFMA is zero
+
+    float acc[2][16];
+#pragma unroll
+    for (int ct = 0; ct < 2; ct++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[ct][r] = 0.0f;
+
+    uint32_t raw[17];
+    const int nh = nb / kGH;
+    half_load(raw, W, X, m0, n0, m_weight, m_tokens, 0, bpr);
+    half_store(s, 0, raw);
+    __syncthreads();
+
+    for (int h = 0; h < nh; h++) {
+        const int slot = h & 1;
+        if (h + 1 < nh) half_load(raw, W, X, m0, n0, m_weight, m_tokens, (h + 1) * kGH, bpr);
+#pragma unroll 1
+        for (int u = 0; u < kGH; u++) {
+            const i32x4 fa = *reinterpret_cast<const i32x4*>(&s.q[slot][0][u][ra][16 * half]);
+            // scale products RN(Ad*Bd) as a rank-1 fp32 MFMA: lanes 0-31 give K index 0
+            // (row / column scale), lanes 32-63 K index 1 (zero), so D = Ad*Bd + 0*0 + 0
+            // is rounded once; |Ad*Bd| >= 2^-48 or 0 (f16 inputs), never fp32-subnormal
+            const float av = __uint_as_float(__float_as_uint(s.d[slot][0][u][ra]) & kmask);
+#pragma unroll
+            for (int ct = 0; ct < 2; ct++) {
+                const int cb = wc * 64 + ct * 32 + col;
+                const i32x4 fb = *reinterpret_cast<const i32x4*>(&s.q[slot][1][u][cb][16 * half]);
+                const float bv = __uint_as_float(__float_as_uint(s.d[slot][1][u][cb]) & kmask);
+                const i32x16 zero = {0};
+                const f32x16 fzero = {0.0f};
+                const i32x16 sb = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa, fb, zero, 0, 0, 0);
+                const f32x16 delta = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, fzero, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const float prod = (float)sb[r] * delta[r];
+                    acc[ct][r] = acc[ct][r] + prod;
+                }
+            }
+        }
+        // the other slot was last read before the previous barrier
+        if (h + 1 < nh) half_store(s, slot ^ 1, raw);
+        __syncthreads();
+    }
+
+    // register r of lane l is row 8(r/4) + 4(l/32) + r%4 of the tile: runs of 4 rows
+    const bool full_rows = m0 + wr * 32 + 32 <= m_weight && (m_weight & 3) == 0;
+#pragma unroll
+    for (int ct = 0; ct < 2; ct++) {
+        const int tok = n0 + wc * 64 + ct * 32 + col;
+        if (tok >= m_tokens) continue;
+        float* o = out + (int64_t)tok * m_weight + m0 + wr * 32 + 4 * half;
+        if (full_rows) {
+#pragma unroll
+            for (int g = 0; g < 4; g++)
+                *reinterpret_cast<float4*>(o + 8 * g) =
+                    make_float4(acc[ct][4 * g], acc[ct][4 * g + 1], acc[ct][4 * g + 2], acc[ct][4 * g + 3]);
+        } else {
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int row = m0 + wr * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+                if (row < m_weight) o[8 * (r >> 2) + (r & 3)] = acc[ct][r];
+            }
+        }
+    }
+}
+
 void launch_q8_0_gemm_S(const uint8_t* Wq, const uint8_t* Xq, float* out, int m_weight, int m_tokens, int K,
                         hipStream_t s) {
     if (K / 32 == 0) {  // the kernel indexes block nb-1
@@ -405,7 +528,12 @@ void launch_q8_0_gemm_S(const uint8_t* Wq, const uint8_t* Xq, float* out, int m_
         return;
     }
     const dim3 grid((m_weight + kGT - 1) / kGT, (m_tokens + kGT - 1) / kGT);
-    hipLaunchKernelGGL(k_q8_0_gemm_S, grid, dim3(256), 0, s, Wq, Xq, out, m_weight, m_tokens, K / 32);
+    const bool aligned = K % 128 == 0 && (reinterpret_cast<uintptr_t>(Wq) & 3) == 0 &&
+                         (reinterpret_cast<uintptr_t>(Xq) & 3) == 0;
+    if (aligned)
+        hipLaunchKernelGGL(k_q8_0_gemm_SH, grid, dim3(512), 0, s, Wq, Xq, out, m_weight, m_tokens, K / 32);
+    else
+        hipLaunchKernelGGL(k_q8_0_gemm_S, grid, dim3(256), 0, s, Wq, Xq, out, m_weight, m_tokens, K / 32);
 }
 
 }  // namespace bpdq
