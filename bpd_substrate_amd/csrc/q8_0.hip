@@ -399,58 +399,73 @@ __global__ __launch_bounds__(256) void k_q8_0_gemm_S(const uint8_t* __restrict__
 
 // ----------------------------------------------------------------------------
 // The same GEMM when K is a multiple of 128 and W, X are 4-byte aligned, with
-// coalesced staging and more waves.  A half-stage is 4 blocks; its bytes of one
-// row are 136 contiguous bytes, and thread t stages blocks 2p, 2p+1 (p = t%2)
-// of row (t/2)%128 of W (t < 256) or X: 68 contiguous bytes, 17 dword loads.
-// In registers block 2p's scale is the low half of dword 0 and its quants start
-// 2 bytes into dword 0 (one v_alignbit per dword); block 2p+1's scale is the
-// high half of dword 8, its quants dwords 9..16.  Two LDS slots alternate:
-// while one is computed, the next half-stage is loaded and written to the
-// other, one barrier per half-stage.  8 waves (4 x 2) each own 32 weight rows x
-// 64 tokens (two 32x32 MFMA tiles), so two workgroups (16 waves) share a CU
-// and the MFMA latency of one wave hides behind the fp32 epilogue of others.
+// coalesced staging and more waves.  A workgroup owns 32*RT weight rows x 128
+// tokens; its 2*RT waves each own 32 rows x 64 tokens (two 32x32 MFMA tiles).
+// A half-stage is 4 blocks: the bytes of one row are 136 contiguous bytes, and
+// thread pair (2r, 2r+1) stages them for row r of W (first 32*RT rows) or of X
+// (next 128): thread p of the pair takes blocks 2p, 2p+1 = 68 contiguous bytes
+// in 17 dword loads.  In registers block 2p's scale is the low half of dword 0
+// and its quants start 2 bytes into dword 0 (one v_alignbit per dword); block
+// 2p+1's scale is the high half of dword 8, its quants dwords 9..16.  Two LDS
+// slots alternate: while one is computed, the next half-stage is loaded and
+// written to the other, one barrier per half-stage.  Many waves per CU let the
+// MFMA latency of one wave hide behind the fp32 epilogue of others.
 // ----------------------------------------------------------------------------
 constexpr int kGH = 4;  // blocks per half-stage
 
+template <int RT>
 struct __align__(16) GemmLdsH {
-    uint8_t q[2][2][kGH][kGT][32];  // [slot][W / X][block][row][quants]
-    float d[2][2][kGH][kGT];
+    uint8_t qa[2][kGH][32 * RT][32];  // [slot][block][weight row][quants]
+    uint8_t qb[2][kGH][kGT][32];      // [slot][block][token][quants]
+    float da[2][kGH][32 * RT];
+    float db[2][kGH][kGT];
 };
 
+template <int RT>
 __device__ __forceinline__ void half_load(uint32_t (&raw)[17], const uint8_t* __restrict__ W,
                                           const uint8_t* __restrict__ X, int m0, int n0, int m_weight, int m_tokens,
                                           int b0, int64_t bpr) {
-    const int t = threadIdx.x, row = (t >> 1) & (kGT - 1), p = t & 1;
-    const uint8_t* src = t < 2 * kGT ? W + (int64_t)min(m0 + row, m_weight - 1) * bpr
-                                     : X + (int64_t)min(n0 + row, m_tokens - 1) * bpr;
+    // threads past the last staged row repeat its loads (the store skips them)
+    const int t = min((int)threadIdx.x, 64 * RT + 2 * kGT - 1), p = t & 1;
+    const bool wrow = t < 64 * RT;
+    const int row = wrow ? t >> 1 : (t - 64 * RT) >> 1;
+    const uint8_t* src = wrow ? W + (int64_t)min(m0 + row, m_weight - 1) * bpr
+                              : X + (int64_t)min(n0 + row, m_tokens - 1) * bpr;
     src += (int64_t)(b0 + 2 * p) * kQ80Bytes;
 #pragma unroll
     for (int k = 0; k < 17; k++) raw[k] = *reinterpret_cast<const uint32_t*>(src + 4 * k);
 }
 
-__device__ __forceinline__ void half_store(GemmLdsH& s, int slot, const uint32_t (&d)[17]) {
-    const int t = threadIdx.x, mat = t >> 8, row = (t >> 1) & (kGT - 1), p = t & 1;
+template <int RT>
+__device__ __forceinline__ void half_store(GemmLdsH<RT>& s, int slot, const uint32_t (&d)[17]) {
+    const int t = threadIdx.x, p = t & 1;
+    if (t >= 64 * RT + 2 * kGT) return;
+    const bool wrow = t < 64 * RT;
+    const int row = wrow ? t >> 1 : (t - 64 * RT) >> 1;
     uint32_t q[8];
 #pragma unroll
     for (int k = 0; k < 8; k++) q[k] = __builtin_amdgcn_alignbit(d[k + 1], d[k], 16);
-    uint4* dst = reinterpret_cast<uint4*>(s.q[slot][mat][2 * p][row]);
-    dst[0] = make_uint4(q[0], q[1], q[2], q[3]);
-    dst[1] = make_uint4(q[4], q[5], q[6], q[7]);
-    dst = reinterpret_cast<uint4*>(s.q[slot][mat][2 * p + 1][row]);
-    dst[0] = make_uint4(d[9], d[10], d[11], d[12]);
-    dst[1] = make_uint4(d[13], d[14], d[15], d[16]);
-    s.d[slot][mat][2 * p][row] = f16_ieee(d[0] & 0xFFFFu);
-    s.d[slot][mat][2 * p + 1][row] = f16_ieee(d[8] >> 16);
+    uint4* d0 = reinterpret_cast<uint4*>(wrow ? s.qa[slot][2 * p][row] : s.qb[slot][2 * p][row]);
+    uint4* d1 = reinterpret_cast<uint4*>(wrow ? s.qa[slot][2 * p + 1][row] : s.qb[slot][2 * p + 1][row]);
+    d0[0] = make_uint4(q[0], q[1], q[2], q[3]);
+    d0[1] = make_uint4(q[4], q[5], q[6], q[7]);
+    d1[0] = make_uint4(d[9], d[10], d[11], d[12]);
+    d1[1] = make_uint4(d[13], d[14], d[15], d[16]);
+    float* ds0 = wrow ? &s.da[slot][2 * p][row] : &s.db[slot][2 * p][row];
+    float* ds1 = wrow ? &s.da[slot][2 * p + 1][row] : &s.db[slot][2 * p + 1][row];
+    *ds0 = f16_ieee(d[0] & 0xFFFFu);
+    *ds1 = f16_ieee(d[8] >> 16);
 }
 
-__global__ __launch_bounds__(512, 2) void k_q8_0_gemm_SH(const uint8_t* __restrict__ W,
-                                                         const uint8_t* __restrict__ X, float* __restrict__ out,
-                                                         int m_weight, int m_tokens, int nb) {
-    __shared__ GemmLdsH s;
+template <int RT>
+__global__ __launch_bounds__(128 * RT) void k_q8_0_gemm_SH(const uint8_t* __restrict__ W,
+                                                           const uint8_t* __restrict__ X, float* __restrict__ out,
+                                                           int m_weight, int m_tokens, int nb) {
+    __shared__ GemmLdsH<RT> s;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int wr = wave >> 1, wc = wave & 1;
-    const int m0 = blockIdx.x * kGT, n0 = blockIdx.y * kGT;
+    const int m0 = blockIdx.x * 32 * RT, n0 = blockIdx.y * kGT;
     const int64_t bpr = (int64_t)nb * kQ80Bytes;
     const int col = lane & 31, half = lane >> 5;
     const int ra = wr * 32 + col;
@@ -464,25 +479,25 @@ __global__ __launch_bounds__(512, 2) void k_q8_0_gemm_SH(const uint8_t* __restri
 
     uint32_t raw[17];
     const int nh = nb / kGH;
-    half_load(raw, W, X, m0, n0, m_weight, m_tokens, 0, bpr);
-    half_store(s, 0, raw);
+    half_load<RT>(raw, W, X, m0, n0, m_weight, m_tokens, 0, bpr);
+    half_store<RT>(s, 0, raw);
     __syncthreads();
 
     for (int h = 0; h < nh; h++) {
         const int slot = h & 1;
-        if (h + 1 < nh) half_load(raw, W, X, m0, n0, m_weight, m_tokens, (h + 1) * kGH, bpr);
+        if (h + 1 < nh) half_load<RT>(raw, W, X, m0, n0, m_weight, m_tokens, (h + 1) * kGH, bpr);
 #pragma unroll 1
         for (int u = 0; u < kGH; u++) {
-            const i32x4 fa = *reinterpret_cast<const i32x4*>(&s.q[slot][0][u][ra][16 * half]);
+            const i32x4 fa = *reinterpret_cast<const i32x4*>(&s.qa[slot][u][ra][16 * half]);
             // scale products RN(Ad*Bd) as a rank-1 fp32 MFMA: lanes 0-31 give K index 0
             // (row / column scale), lanes 32-63 K index 1 (zero), so D = Ad*Bd + 0*0 + 0
             // is rounded once; |Ad*Bd| >= 2^-48 or 0 (f16 inputs), never fp32-subnormal
-            const float av = __uint_as_float(__float_as_uint(s.d[slot][0][u][ra]) & kmask);
+            const float av = __uint_as_float(__float_as_uint(s.da[slot][u][ra]) & kmask);
 #pragma unroll
             for (int ct = 0; ct < 2; ct++) {
                 const int cb = wc * 64 + ct * 32 + col;
-                const i32x4 fb = *reinterpret_cast<const i32x4*>(&s.q[slot][1][u][cb][16 * half]);
-                const float bv = __uint_as_float(__float_as_uint(s.d[slot][1][u][cb]) & kmask);
+                const i32x4 fb = *reinterpret_cast<const i32x4*>(&s.qb[slot][u][cb][16 * half]);
+                const float bv = __uint_as_float(__float_as_uint(s.db[slot][u][cb]) & kmask);
                 const i32x16 zero = {0};
                 const f32x16 fzero = {0.0f};
                 const i32x16 sb = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa, fb, zero, 0, 0, 0);
@@ -495,7 +510,7 @@ __global__ __launch_bounds__(512, 2) void k_q8_0_gemm_SH(const uint8_t* __restri
             }
         }
         // the other slot was last read before the previous barrier
-        if (h + 1 < nh) half_store(s, slot ^ 1, raw);
+        if (h + 1 < nh) half_store<RT>(s, slot ^ 1, raw);
         __syncthreads();
     }
 
@@ -530,10 +545,14 @@ void launch_q8_0_gemm_S(const uint8_t* Wq, const uint8_t* Xq, float* out, int m_
     const dim3 grid((m_weight + kGT - 1) / kGT, (m_tokens + kGT - 1) / kGT);
     const bool aligned = K % 128 == 0 && (reinterpret_cast<uintptr_t>(Wq) & 3) == 0 &&
                          (reinterpret_cast<uintptr_t>(Xq) & 3) == 0;
-    if (aligned)
-        hipLaunchKernelGGL(k_q8_0_gemm_SH, grid, dim3(512), 0, s, Wq, Xq, out, m_weight, m_tokens, K / 32);
-    else
+    if (!aligned) {
         hipLaunchKernelGGL(k_q8_0_gemm_S, grid, dim3(256), 0, s, Wq, Xq, out, m_weight, m_tokens, K / 32);
+        return;
+    }
+    // 128 weight rows per workgroup, two 512-thread workgroups per CU.  (224 rows,
+    // one 896-thread workgroup per CU, balances cfg4's 14336 rows over 256 CUs
+    // exactly but measured slower: 150.9 us vs 146.)
+    hipLaunchKernelGGL(k_q8_0_gemm_SH<4>, grid, dim3(512), 0, s, Wq, Xq, out, m_weight, m_tokens, K / 32);
 }
 
 }  // namespace bpdq

@@ -207,19 +207,23 @@ def test_fused_quantization_covers_x_and_stays_in_bounds(rows):
 # ---------------------------------------------------------------- Q8_0 S-order GEMM, coalesced staging
 
 @pytest.mark.parametrize("mw,mt,K", [(14336, 512, 4096), (130, 129, 4096), (1, 1, 128), (300, 17, 384), (256, 256, 128),
-                                     (7, 5, 14336)])
-def test_q8_0_gemm_SH_in_bounds(mw, mt, K):
+                                     (7, 5, 14336), (225, 3, 256)])
+@pytest.mark.parametrize("RT", [4])
+def test_q8_0_gemm_SH_in_bounds(mw, mt, K, RT):
     assert K % 128 == 0  # the launcher's condition for this kernel
     nb = K // 32
     bpr = nb * Q80
-    t = np.arange(512)
-    row, p, mat = (t >> 1) & 127, t & 1, t >> 8
-    for bx in {0, (mw + 127) // 128 - 1}:
+    t = np.minimum(np.arange(128 * RT), 64 * RT + 255)
+    p, wrow = t & 1, t < 64 * RT
+    row = np.where(wrow, t >> 1, (t - 64 * RT) >> 1)
+    assert row.max() < max(32 * RT, 128)
+    rows = 32 * RT
+    for bx in {0, (mw + rows - 1) // rows - 1}:
         for by in {0, (mt + 127) // 128 - 1}:
-            m0, n0 = bx * 128, by * 128
+            m0, n0 = bx * rows, by * 128
             for b0 in range(0, nb, 4):
-                r = np.where(mat == 0, np.minimum(m0 + row, mw - 1), np.minimum(n0 + row, mt - 1))
-                size = np.where(mat == 0, mw * bpr, mt * bpr)
+                r = np.where(wrow, np.minimum(m0 + row, mw - 1), np.minimum(n0 + row, mt - 1))
+                size = np.where(wrow, mw * bpr, mt * bpr)
                 src = r * bpr + (b0 + 2 * p) * Q80
                 assert (src >= 0).all() and ((src + 4 * 16 + 4) <= size).all()
                 assert ((b0 + 2 * p + 1) < nb).all()  # both staged blocks exist
