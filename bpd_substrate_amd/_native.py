@@ -54,6 +54,10 @@ HIP_SIGNATURES = {
     "bpd_qmatmul_q4k_q8k_gguf_gpu": (None, [P, P, P, I, I]),
     "bpd_qmatmul_q4k_q8k_multi_gpu": (None, [P, P, P, I, P, I]),
     "bpd_qmatmul_q4k_q8k_fused_gpu": (None, [P, P, P, I, I]),
+    "bpd_dequant_q6k_gpu": (None, [P, P, I]),
+    "bpd_dequant_q6k_gguf_gpu": (None, [P, P, I]),
+    "bpd_qmatmul_q6k_q8k_gpu": (None, [P, P, P, I, I]),
+    "bpd_qmatmul_q6k_q8k_gguf_gpu": (None, [P, P, P, I, I]),
     "bpd_qmatmul_q4k_q8k_fused_multi_gpu": (None, [P, P, P, I, P, I]),
     "bpd_dequant_q8_0_gpu": (None, [P, P, I]),
     "bpd_embed_lookup_q8_0_gpu": (None, [P, P, P, I, I]),

@@ -130,6 +130,27 @@ void copy(void* dst, const void* src, int bytes, hipMemcpyKind kind, const char*
     hip_ok(hipMemcpy(dst, src, (size_t)bytes, kind), fn);
 }
 
+void dequant_q6k(const uint8_t* q, float* out, int nb, int order, const char* fn) {
+    Check c(fn);
+    c.nonneg(nb, "n_blocks");
+    if (!c.ok || nb == 0) return;
+    c.ptr(q, 2, "q").ptr(out, 16, "out");
+    if (!c.ok) return;
+    bpdq::launch_dequant_q6k(q, out, nb, order, g_stream);
+    check_launch(fn);
+}
+
+void q6k_q8k(const uint8_t* w, const uint8_t* xq, float* y, int M, int K, int order, const char* fn) {
+    Check c(fn);
+    c.nonneg(M, "M").nonneg(K, "K").multiple(K, 256, "K");
+    if (!c.ok || M == 0) return;
+    c.ptr(y, 4, "y");
+    if (K > 0) c.ptr(w, 2, "w").ptr(xq, 4, "xq");
+    if (!c.ok) return;
+    bpdq::launch_qmatmul_q6k_q8k(w, xq, y, M, K, order, g_stream);
+    check_launch(fn);
+}
+
 void q4k_q8k(const uint8_t* w, const uint8_t* xq, float* y, int M, int K, int order, const char* fn) {
     Check c(fn);
     c.nonneg(M, "M").nonneg(K, "K").multiple(K, 256, "K");
@@ -252,6 +273,20 @@ void bpd_qmatmul_q4k_q8k_fused_multi_gpu(const uint8_t* const* w_list, float* co
 
 void bpd_qmatmul_q4k_q8k_fused_gpu(const uint8_t* w, const float* x, float* y, int M, int K) {
     fused(&w, &y, &M, 1, x, K, "bpd_qmatmul_q4k_q8k_fused_gpu");
+}
+
+// ---- Q6_K --------------------------------------------------------------------
+void bpd_dequant_q6k_gpu(const uint8_t* q, float* out, int n_blocks) {
+    dequant_q6k(q, out, n_blocks, 0, "bpd_dequant_q6k_gpu");
+}
+void bpd_dequant_q6k_gguf_gpu(const uint8_t* q, float* out, int n_blocks) {
+    dequant_q6k(q, out, n_blocks, 1, "bpd_dequant_q6k_gguf_gpu");
+}
+void bpd_qmatmul_q6k_q8k_gpu(const uint8_t* w, const uint8_t* xq, float* y, int M, int K) {
+    q6k_q8k(w, xq, y, M, K, 0, "bpd_qmatmul_q6k_q8k_gpu");
+}
+void bpd_qmatmul_q6k_q8k_gguf_gpu(const uint8_t* w, const uint8_t* xq, float* y, int M, int K) {
+    q6k_q8k(w, xq, y, M, K, 1, "bpd_qmatmul_q6k_q8k_gguf_gpu");
 }
 
 void* qgpu_alloc(int bytes) { return alloc(bytes, "qgpu_alloc"); }

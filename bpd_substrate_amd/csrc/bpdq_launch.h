@@ -20,6 +20,9 @@ int fused_max_k();
 void launch_qmatmul_q4k_fused_multi(const uint8_t* const* w, float* const* y, const int* M, int n, const float* x,
                                     int K, int order, hipStream_t s);
 
+void launch_dequant_q6k(const uint8_t* q, float* out, int n_blocks, int order, hipStream_t s);
+void launch_qmatmul_q6k_q8k(const uint8_t* w, const uint8_t* xq, float* y, int M, int K, int order, hipStream_t s);
+
 void launch_dequant_q8_0(const uint8_t* raw, float* out, int n_blocks, hipStream_t s);
 void launch_embed_q8_0(const uint8_t* table, const int32_t* ids, float* out, int n_tokens, int embed_dim,
                        hipStream_t s);

@@ -147,6 +147,30 @@ def _multi(name, ws, x, Ms, K, outs):
     return outs
 
 
+# ---------------------------------------------------------------- Q6_K
+
+def dequant_q6k(q, order=formats.ORDER_BPD, out=None):
+    """q: uint8 device tensor of n_blocks*210 bytes -> fp32 [n_blocks*256].  ORDER_BPD is the
+    reference's map (inference/llamatov_helpers.py:161-179), ORDER_GGUF llama.cpp's."""
+    import torch
+
+    nb = q.numel() // 210
+    out = _empty(nb * 256, torch.float32, q) if out is None else out
+    _use_torch_stream()
+    call("bpd_dequant_q6k_gpu" if order == formats.ORDER_BPD else "bpd_dequant_q6k_gguf_gpu", q, out, nb)
+    return out
+
+
+def qmatmul_q6k_q8k(w, xq, M, K, order=formats.ORDER_BPD, out=None):
+    import torch
+
+    out = _empty(M, torch.float32, xq) if out is None else out
+    _use_torch_stream()
+    call("bpd_qmatmul_q6k_q8k_gpu" if order == formats.ORDER_BPD else "bpd_qmatmul_q6k_q8k_gguf_gpu",
+         w, xq, out, M, K)
+    return out
+
+
 # ---------------------------------------------------------------- Q8_0
 
 def dequant_q8_0(raw, out=None):

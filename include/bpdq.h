@@ -110,6 +110,19 @@ void bpd_qmatmul_q4k_q8k_fused_gpu(const uint8_t* w_dev, const float* x_dev, flo
 void bpd_qmatmul_q4k_q8k_fused_multi_gpu(const uint8_t* const* w_list, float* const* y_list, const int* M_list,
                                          int n, const float* x_dev, int K);
 
+/* ---- Q6_K (210-byte blocks: ql[128], qh[64], int8 sc[16], f16 d) ----
+ * The reference has Q6_K only as Python: inference/llamatov_helpers.py:161-179 dequantizes
+ * it to fp32, with its own element map (element 2i / 2i+1 = low / high nibble of ql[i],
+ * element 4j+k = bits 2k..2k+1 of qh[j]).  The _gguf_ forms use the GGUF (llama.cpp
+ * dequantize_row_q6_K) map.  Q6_K pointers need 2-byte alignment. */
+void bpd_dequant_q6k_gpu(const uint8_t* q_dev, float* out_dev, int n_blocks);
+void bpd_dequant_q6k_gguf_gpu(const uint8_t* q_dev, float* out_dev, int n_blocks);
+/* y[M] = W_q6k[M,K] . x_q8k[K]: exact integer group sums, then the fp32 order of
+ * bpd_qmatmul_q4k_q8k_gpu (no reference code: the reference never multiplies Q6_K
+ * without dequantizing it first). */
+void bpd_qmatmul_q6k_q8k_gpu(const uint8_t* w_dev, const uint8_t* xq8k_dev, float* y_dev, int M, int K);
+void bpd_qmatmul_q6k_q8k_gguf_gpu(const uint8_t* w_dev, const uint8_t* xq8k_dev, float* y_dev, int M, int K);
+
 /* ---- Q8_0 on the GPU, same signatures as the CPU functions they mirror ---- */
 void bpd_dequant_q8_0_gpu(const uint8_t* raw_dev, float* out_dev, int n_blocks);           /* bench/bpd_cpu.c:3960 */
 /* ids must index rows of the table (0 <= id < rows); bench/bpd_cpu.c:4002 */

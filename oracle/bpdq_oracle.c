@@ -282,6 +282,102 @@ void bpdq_o_qmatmul_q4k_q8k(const uint8_t* w, const uint8_t* xq, float* y, int M
     for (int r = 0; r < M; r++) y[r] = q4k_q8k_row(w + (size_t)r * nb * 144, xq, nb, order);
 }
 
+/* ---------------------------------------------------------------- Q6_K --- */
+
+/* Q6_K block, 210 B per 256 elements: ql[128] (low 4 bits), qh[64] (high 2
+ * bits), sc[16] (int8, one per 16 elements), d (f16 at byte 208).
+ * q = (low | high << 4) - 32.  Element maps:
+ *   order 0, inference/llamatov_helpers.py:161-179: element 2i takes the low
+ *     nibble of ql[i], 2i+1 its high nibble; element 4j+k takes bits 2k..2k+1
+ *     of qh[j];
+ *   order 1, the GGUF layout of llama.cpp's dequantize_row_q6_K (ggml-quants.c,
+ *     the llama.cpp build 5311 the reference audits, docs/llama-kernel-audit.md:11):
+ *     in half h (ql += 64h, qh += 32h), for l < 32: element l takes ql[l] low and
+ *     qh[l] bits 0-1, l+32 ql[l+32] low and bits 2-3, l+64 ql[l] high and bits
+ *     4-5, l+96 ql[l+32] high and bits 6-7.
+ * In both maps element e uses scale sc[e/16]. */
+void bpdq_o_q6k_quants(const uint8_t* blk, int order, int8_t* q) {
+    const uint8_t* ql = blk;
+    const uint8_t* qh = blk + 128;
+    if (order == 0) {
+        for (int i = 0; i < 128; i++) {
+            int e0 = 2 * i, e1 = 2 * i + 1;
+            q[e0] = (int8_t)(((ql[i] & 15) | (((qh[e0 / 4] >> (2 * (e0 % 4))) & 3) << 4)) - 32);
+            q[e1] = (int8_t)(((ql[i] >> 4) | (((qh[e1 / 4] >> (2 * (e1 % 4))) & 3) << 4)) - 32);
+        }
+    } else {
+        for (int h = 0; h < 2; h++) {
+            const uint8_t* L = ql + 64 * h;
+            const uint8_t* H = qh + 32 * h;
+            int8_t* o = q + 128 * h;
+            for (int l = 0; l < 32; l++) {
+                o[l] = (int8_t)(((L[l] & 15) | (((H[l] >> 0) & 3) << 4)) - 32);
+                o[l + 32] = (int8_t)(((L[l + 32] & 15) | (((H[l] >> 2) & 3) << 4)) - 32);
+                o[l + 64] = (int8_t)(((L[l] >> 4) | (((H[l] >> 4) & 3) << 4)) - 32);
+                o[l + 96] = (int8_t)(((L[l + 32] >> 4) | (((H[l] >> 6) & 3) << 4)) - 32);
+            }
+        }
+    }
+}
+
+/* y = (d * sc) * q in fp32: d*sc is exact (11 x 8 bits), so one rounding,
+ * as the float32 numpy of inference/llamatov_helpers.py:177-178 and the C of
+ * dequantize_row_q6_K.  The scale is decoded with NaN payloads kept. */
+void bpdq_o_dequant_q6k(const uint8_t* q, float* out, int n_blocks, int order) {
+    for (int b = 0; b < n_blocks; b++) {
+        const uint8_t* blk = q + (size_t)b * 210;
+        const int8_t* sc = (const int8_t*)(blk + 192);
+        float d = bpdq_o_f16_magic(rd16(blk + 208));
+        int8_t qq[256];
+        bpdq_o_q6k_quants(blk, order, qq);
+        for (int e = 0; e < 256; e++) {
+            float ds = d * (float)sc[e / 16];
+            out[(size_t)b * 256 + e] = ds * (float)qq[e];
+        }
+    }
+}
+
+/* Q6_K x Q8_K (no reference code; the reference dequantizes Q6_K to fp32 in
+ * Python): I_b = sum over the 16 groups g of sc[g] * sum_{e in g} q_e * x_e,
+ * exact in int32; c_b = RN(RN(d*dy) * float(I_b)); then the fixed fp32 order of
+ * the Q4_K x Q8_K GEMV: slot sums s_q from +0.0 over b = q mod 8 ascending,
+ * y = ((s0+s1)+(s2+s3)) + ((s4+s5)+(s6+s7)). */
+int32_t bpdq_o_q6k_q8k_block_int(const uint8_t* wblk, const uint8_t* xblk, int order) {
+    int8_t qq[256];
+    bpdq_o_q6k_quants(wblk, order, qq);
+    const int8_t* sc = (const int8_t*)(wblk + 192);
+    const int8_t* xq = (const int8_t*)(xblk + 4);
+    int32_t I = 0;
+    for (int g = 0; g < 16; g++) {
+        int32_t S = 0;
+        for (int k = 0; k < 16; k++) S += qq[16 * g + k] * xq[16 * g + k];
+        I += sc[g] * S;
+    }
+    return I;
+}
+
+static float q6k_q8k_row(const uint8_t* row, const uint8_t* xq, int nb, int order) {
+    float s[8];
+    for (int q = 0; q < 8; q++) s[q] = 0.0f;
+    for (int b = 0; b < nb; b++) {
+        const uint8_t* wb = row + (size_t)b * 210;
+        const uint8_t* xb = xq + (size_t)b * 292;
+        int32_t I = bpdq_o_q6k_q8k_block_int(wb, xb, order);
+        float dy;
+        memcpy(&dy, xb, 4);
+        float dd = bpdq_o_f16_magic(rd16(wb + 208)) * dy;
+        float c = dd * (float)I;
+        s[b & 7] = s[b & 7] + c;
+    }
+    float t0 = s[0] + s[1], t1 = s[2] + s[3], t2 = s[4] + s[5], t3 = s[6] + s[7];
+    return (t0 + t1) + (t2 + t3);
+}
+
+void bpdq_o_qmatmul_q6k_q8k(const uint8_t* w, const uint8_t* xq, float* y, int M, int K, int order) {
+    int nb = K / 256;
+    for (int r = 0; r < M; r++) y[r] = q6k_q8k_row(w + (size_t)r * nb * 210, xq, nb, order);
+}
+
 /* ---------------------------------------------------------------- Q8_0 --- */
 
 /* bench/bpd_cpu.c:3960-3973 */
@@ -479,6 +575,9 @@ static void* mt_run(void* p) {
     } else if (j->kind == 1) {
         int nb = j->K / 256;
         for (int r = j->r0; r < j->r1; r++) j->out[r] = q4k_q8k_row(j->a + (size_t)r * nb * 144, j->b, nb, j->order);
+    } else if (j->kind == 3) {
+        int nb = j->K / 256;
+        for (int r = j->r0; r < j->r1; r++) j->out[r] = q6k_q8k_row(j->a + (size_t)r * nb * 210, j->b, nb, j->order);
     } else {
         int k = j->K / 32;
         size_t bpr = (size_t)k * 34;
@@ -526,4 +625,10 @@ void bpdq_o_dispatch_q8_0_mt(const uint8_t* Wq, const uint8_t* Xq, float* out, i
     mt_job p = {0};
     p.kind = 2; p.a = Wq; p.b = Xq; p.out = out; p.K = K; p.order = order; p.mw = m_weight; p.mt = m_tokens;
     mt_launch(p, m_weight, nthreads);
+}
+
+void bpdq_o_qmatmul_q6k_q8k_mt(const uint8_t* w, const uint8_t* xq, float* y, int M, int K, int order, int nthreads) {
+    mt_job p = {0};
+    p.kind = 3; p.a = w; p.b = xq; p.out = y; p.K = K; p.order = order;
+    mt_launch(p, M, nthreads);
 }

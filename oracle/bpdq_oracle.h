@@ -34,6 +34,12 @@ void bpdq_o_qmatmul_q4k_q8k(const uint8_t* w, const uint8_t* xq, float* y, int M
 void bpdq_o_q4k_q8k_block_ints(const uint8_t* wblk, const uint8_t* xblk, int order, int32_t* I, int32_t* Mn);
 
 /* Q8_0 (34 B / 32 elements) */
+/* Q6_K (210 B / 256): order 0 = inference/llamatov_helpers.py:161-179, order 1 = GGUF (llama.cpp) */
+void bpdq_o_q6k_quants(const uint8_t* blk, int order, int8_t* q);
+void bpdq_o_dequant_q6k(const uint8_t* q, float* out, int n_blocks, int order);
+int32_t bpdq_o_q6k_q8k_block_int(const uint8_t* wblk, const uint8_t* xblk, int order);
+void bpdq_o_qmatmul_q6k_q8k(const uint8_t* w, const uint8_t* xq, float* y, int M, int K, int order);
+
 void bpdq_o_dequant_q8_0(const uint8_t* raw, float* out, int n_blocks);                      /* bench/bpd_cpu.c:3960-3973 */
 void bpdq_o_embed_lookup_q8_0(const uint8_t* table, const int32_t* ids, float* out, int n_tokens, int embed_dim); /* :4002-4013 */
 void bpdq_o_quant_q8_0(const float* x, uint8_t* y, int n_elements);                        /* bench/bpd_cpu.c:4106-4136 */
@@ -52,6 +58,7 @@ void bpdq_o_qmatmul_q8_0_llamafile(const uint8_t* W, const float* X, float* out,
  * the single-threaded function. */
 void bpdq_o_dequant_q4k_mt(const uint8_t* q, float* out, int n_blocks, int nthreads);
 void bpdq_o_qmatmul_q4k_q8k_mt(const uint8_t* w, const uint8_t* xq, float* y, int M, int K, int order, int nthreads);
+void bpdq_o_qmatmul_q6k_q8k_mt(const uint8_t* w, const uint8_t* xq, float* y, int M, int K, int order, int nthreads);
 void bpdq_o_dispatch_q8_0_mt(const uint8_t* Wq, const uint8_t* Xq, float* out, int m_weight, int m_tokens, int K, int order, int nthreads);
 
 #ifdef __cplusplus

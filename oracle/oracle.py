@@ -33,6 +33,11 @@ _SIGS = {
     "bpdq_o_quant_q8_k": (None, [P, P, I]),
     "bpdq_o_qmatmul_q4k_q8k": (None, [P, P, P, I, I, I]),
     "bpdq_o_q4k_q8k_block_ints": (None, [P, P, I, P, P]),
+    "bpdq_o_q6k_quants": (None, [P, I, P]),
+    "bpdq_o_dequant_q6k": (None, [P, P, I, I]),
+    "bpdq_o_q6k_q8k_block_int": (ctypes.c_int32, [P, P, I]),
+    "bpdq_o_qmatmul_q6k_q8k": (None, [P, P, P, I, I, I]),
+    "bpdq_o_qmatmul_q6k_q8k_mt": (None, [P, P, P, I, I, I, I]),
     "bpdq_o_dequant_q8_0": (None, [P, P, I]),
     "bpdq_o_embed_lookup_q8_0": (None, [P, P, P, I, I]),
     "bpdq_o_quant_q8_0": (None, [P, P, I]),
@@ -125,6 +130,32 @@ def block_ints(wblk, xblk, order=0):
     I_, M_ = ctypes.c_int32(), ctypes.c_int32()
     lib().bpdq_o_q4k_q8k_block_ints(_p(wblk), _p(xblk), order, ctypes.addressof(I_), ctypes.addressof(M_))
     return I_.value, M_.value
+
+
+def q6k_quants(blk, order=0):
+    q = np.empty(256, np.int8)
+    lib().bpdq_o_q6k_quants(_p(blk), order, _p(q))
+    return q
+
+
+def dequant_q6k(q, order=0):
+    nb = q.size // 210
+    out = np.empty(nb * 256, np.float32)
+    lib().bpdq_o_dequant_q6k(_p(q), _p(out), nb, order)
+    return out
+
+
+def q6k_block_int(wblk, xblk, order=0):
+    return int(lib().bpdq_o_q6k_q8k_block_int(_p(wblk), _p(xblk), order))
+
+
+def qmatmul_q6k_q8k(w, xq, M, K, order=0, nthreads=1):
+    y = np.empty(M, np.float32)
+    if nthreads > 1:
+        lib().bpdq_o_qmatmul_q6k_q8k_mt(_p(w), _p(xq), _p(y), M, K, order, nthreads)
+    else:
+        lib().bpdq_o_qmatmul_q6k_q8k(_p(w), _p(xq), _p(y), M, K, order)
+    return y
 
 
 def dequant_q8_0(raw):

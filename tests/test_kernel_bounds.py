@@ -227,3 +227,63 @@ def test_q8_0_gemm_SH_in_bounds(mw, mt, K, RT):
                 src = r * bpr + (b0 + 2 * p) * Q80
                 assert (src >= 0).all() and ((src + 4 * 16 + 4) <= size).all()
                 assert ((b0 + 2 * p + 1) < nb).all()  # both staged blocks exist
+
+
+# ---------------------------------------------------------------- Q6_K
+
+Q6K = 210
+
+
+@pytest.mark.parametrize("nb", [1, 3, 5, 4096])
+@pytest.mark.parametrize("order", [0, 1])
+def test_dequant_q6k_in_bounds(nb, order):
+    l = lanes()
+    for b in {0, nb - 1}:
+        base = b * Q6K
+        if order == 0:
+            spans = [(2 * l, 2), (128 + l, 1)]
+        else:
+            e0 = 4 * l
+            h, r = e0 >> 7, e0 & 127
+            quarter, idx = r >> 5, r & 31
+            spans = [(64 * h + 32 * (quarter & 1) + idx, 4), (128 + 32 * h + idx, 4)]
+        spans += [(192 + (l >> 2), 1), (np.full(64, 208), 2)]
+        for off, size in spans:
+            assert (base + off + size).max() <= nb * Q6K and (base + off).min() >= 0
+            assert (off + size).max() <= Q6K          # never reads into the next block
+
+
+@pytest.mark.parametrize("M,K", [(1, 256), (5, 512), (64, 4096), (17, 14336), (3, 2304), (3, 0)])
+@pytest.mark.parametrize("order", [0, 1])
+def test_q6k_gemv_in_bounds(M, K, order):
+    nb = K // 256
+    if nb == 0:
+        return
+    R, WPB = 2, 4
+    waves = (M + R - 1) // R
+    grid = (waves + WPB - 1) // WPB
+    c = lanes() & 7
+    if order == 0:
+        w_spans = [(16 * c, 16), (128 + 8 * c, 8), (192 + 2 * c, 1), (192 + 2 * c + 1, 1), (np.full(64, 208), 2)]
+        x_spans = [(4 + 32 * c + 4 * j, 4) for j in range(8)]
+        groups = [2 * c, 2 * c + 1]
+    else:
+        h, p = c >> 2, c & 3
+        e0 = 128 * h + 16 * p
+        w_spans = [(64 * h + 16 * p, 16), (128 + 32 * h + 16 * (p & 1), 16), (192 + 8 * h + p, 1),
+                   (192 + 8 * h + p + 4, 1), (np.full(64, 208), 2)]
+        x_spans = [(4 + e0 + 4 * k, 4) for k in range(4)] + [(4 + e0 + 64 + 4 * k, 4) for k in range(4)]
+        groups = [8 * h + p, 8 * h + p + 4]
+    x_spans += [(260 + 2 * g, 2) for g in groups] + [(np.zeros(64, int), 4)]
+    for off, size in w_spans:
+        assert (off + size).max() <= Q6K
+    for off, size in x_spans:
+        assert (off + size).max() <= Q8K
+    assert all(np.max(g) < 16 for g in groups)
+    for blk in sorted({0, grid - 1}):
+        for wave in range(WPB):
+            row0 = (blk * WPB + wave) * R
+            if row0 >= M:
+                continue
+            for r in range(R):
+                assert min(row0 + r, M - 1) < M
