@@ -54,6 +54,8 @@ HIP_SIGNATURES = {
     "bpd_qmatmul_q4k_q8k_gguf_gpu": (None, [P, P, P, I, I]),
     "bpd_qmatmul_q4k_q8k_multi_gpu": (None, [P, P, P, I, P, I]),
     "bpd_qmatmul_q4k_q8k_fused_gpu": (None, [P, P, P, I, I]),
+    "bpd_q8_pad64_from_f32_gpu": (None, [P, P, I, I]),
+    "bpd_qmatmul_q8_pad64_gpu": (None, [P, P, P, I, I, I]),
     "bpd_dequant_q6k_gpu": (None, [P, P, I]),
     "bpd_dequant_q6k_gguf_gpu": (None, [P, P, I]),
     "bpd_qmatmul_q6k_q8k_gpu": (None, [P, P, P, I, I]),

@@ -289,6 +289,30 @@ void bpd_qmatmul_q6k_q8k_gguf_gpu(const uint8_t* w, const uint8_t* xq, float* y,
     q6k_q8k(w, xq, y, M, K, 1, "bpd_qmatmul_q6k_q8k_gguf_gpu");
 }
 
+// ---- Q8 padded 64-byte layout (the reference's dp4a weight layout) -----------
+void bpd_q8_pad64_from_f32_gpu(const float* x, uint8_t* out, int N, int K) {
+    const char* fn = "bpd_q8_pad64_from_f32_gpu";
+    Check c(fn);
+    c.nonneg(N, "N").nonneg(K, "K").multiple(K, 32, "K");
+    if (!c.ok || N == 0 || K == 0) return;
+    c.ptr(x, 4, "x").ptr(out, 4, "out");
+    if (!c.ok) return;
+    bpdq::launch_q8_pad64(x, out, N, K, g_stream);
+    check_launch(fn);
+}
+
+void bpd_qmatmul_q8_pad64_gpu(const uint8_t* Wp, const uint8_t* Xq, float* out, int m_weight, int m_tokens, int K) {
+    const char* fn = "bpd_qmatmul_q8_pad64_gpu";
+    Check c(fn);
+    c.nonneg(m_weight, "m_weight").nonneg(m_tokens, "m_tokens").nonneg(K, "K").multiple(K, 32, "K");
+    if (!c.ok || m_weight == 0 || m_tokens == 0) return;
+    c.ptr(out, 4, "out");
+    if (K > 0) c.ptr(Wp, 4, "W_pad64").ptr(Xq, 1, "X_q8_0");
+    if (!c.ok) return;
+    bpdq::launch_q8_pad64_dispatch_T(Wp, Xq, out, m_weight, m_tokens, K, g_stream);
+    check_launch(fn);
+}
+
 void* qgpu_alloc(int bytes) { return alloc(bytes, "qgpu_alloc"); }
 void qgpu_free(void* p) {
     if (p) hip_ok(hipFree(p), "qgpu_free");

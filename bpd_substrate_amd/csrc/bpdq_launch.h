@@ -29,6 +29,9 @@ void launch_embed_q8_0(const uint8_t* table, const int32_t* ids, float* out, int
 void launch_quant_q8_0(const float* x, uint8_t* y, int64_t n_elements, hipStream_t s);
 void launch_q8_0_dispatch_T(const uint8_t* Wq, const uint8_t* Xq, float* out, int m_weight, int m_tokens, int K,
                             hipStream_t s);
+void launch_q8_pad64(const float* x, uint8_t* out, int N, int K, hipStream_t s);
+void launch_q8_pad64_dispatch_T(const uint8_t* Wp, const uint8_t* Xq, float* out, int m_weight, int m_tokens, int K,
+                                hipStream_t s);
 
 void launch_q8_0_gemm_S(const uint8_t* Wq, const uint8_t* Xq, float* out, int m_weight, int m_tokens, int K,
                         hipStream_t s);

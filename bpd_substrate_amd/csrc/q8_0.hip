@@ -104,14 +104,14 @@ struct WBatch {
 // wbase: wave-uniform pointer to the wave's first row; voff: this lane's row
 // offset within the wave plus 2 + 4L (lane-constant).  Addresses are then
 // "scalar base + 32-bit lane offset + immediate", one instruction per load.
-template <int U>
+template <int U, int LAYOUT>
 __device__ __forceinline__ void load_batch(WBatch<U>& w, const uint8_t* __restrict__ wbase, uint32_t voff,
-                                           uint32_t doff, int b0, int nb) {
+                                           uint32_t doff, int b0, int nb, int64_t bstride) {
     // Blocks past the end of the row repeat block nb-1 (their steps are skipped).
     // The clamp is wave-uniform, so each address stays scalar base + lane offset.
 #pragma unroll
     for (int u = 0; u < U; u++) {
-        const uint8_t* bu = wbase + (int64_t)min(b0 + u, nb - 1) * kQ80Bytes;
+        const uint8_t* bu = wbase + (int64_t)min(b0 + u, nb - 1) * (LAYOUT == 0 ? (int64_t)kQ80Bytes : bstride);
         w.q[u] = ld_u32(bu + voff);
         w.d[u] = ld_u16(bu + doff);
     }
@@ -133,7 +133,11 @@ __device__ __forceinline__ float accumulate_batch(const WBatch<U>& w, const uint
     return acc;
 }
 
-template <int U, int WPB>
+// LAYOUT 0: W is rows of 34-byte Q8_0 blocks.  LAYOUT 1: W is the padded
+// block-major layout of inference/llamatov_c_inference.py:88-100, records of 64
+// bytes [block][row] with d at bytes 0-1 and the quants at 4-35; the cells and
+// their order are the same.
+template <int U, int WPB, int LAYOUT = 0>
 __global__ __launch_bounds__(64 * WPB) void k_q8_0_gemv_T(const uint8_t* __restrict__ W, const uint8_t* __restrict__ Xq,
                                                           float* __restrict__ out, int m_weight, int nb) {
     extern __shared__ uint32_t lds[];
@@ -145,15 +149,16 @@ __global__ __launch_bounds__(64 * WPB) void k_q8_0_gemv_T(const uint8_t* __restr
     const int row = (blockIdx.x * WPB + wave) * 8 + (lane >> 3);
     const int tok = blockIdx.y;
     const int64_t bpr = (int64_t)nb * kQ80Bytes;
+    const int64_t wrow = LAYOUT == 0 ? bpr : 64, bstride = LAYOUT == 0 ? kQ80Bytes : (int64_t)m_weight * 64;
     // A wave past the last row (the workgroup's spare waves) reads row m_weight-1;
     // base and lane offsets are clamped so every address stays inside W.
     const int row0 = min((blockIdx.x * WPB + wave) * 8, m_weight - 1);
-    const uint8_t* wbase = W + (int64_t)row0 * bpr;
-    const uint32_t doff = (uint32_t)((max(min(row, m_weight - 1), row0) - row0) * bpr);
-    const uint32_t voff = doff + 2 + 4 * L;
+    const uint8_t* wbase = W + (int64_t)row0 * wrow;
+    const uint32_t doff = (uint32_t)((max(min(row, m_weight - 1), row0) - row0) * wrow);
+    const uint32_t voff = doff + (LAYOUT == 0 ? 2 : 4) + 4 * L;
 
     WBatch<U> a, b;
-    load_batch<U>(a, wbase, voff, doff, 0, nb);
+    load_batch<U, LAYOUT>(a, wbase, voff, doff, 0, nb, bstride);
     const uint8_t* xr = Xq + (int64_t)tok * bpr;
     for (int i = threadIdx.x; i < nb * 8; i += 64 * WPB) xs[i] = ld_u32(xr + (int64_t)(i >> 3) * kQ80Bytes + 2 + 4 * (i & 7));
     for (int i = threadIdx.x; i < nb; i += 64 * WPB) xd[i] = f16_ieee(ld_u16(xr + (int64_t)i * kQ80Bytes));
@@ -161,9 +166,9 @@ __global__ __launch_bounds__(64 * WPB) void k_q8_0_gemv_T(const uint8_t* __restr
 
     float acc = 0.0f;
     for (int b0 = 0; b0 < nb; b0 += 2 * U) {
-        if (b0 + U < nb) load_batch<U>(b, wbase, voff, doff, b0 + U, nb);
+        if (b0 + U < nb) load_batch<U, LAYOUT>(b, wbase, voff, doff, b0 + U, nb, bstride);
         acc = accumulate_batch<U>(a, xs, xd, L, b0, nb, acc);
-        if (b0 + 2 * U < nb) load_batch<U>(a, wbase, voff, doff, b0 + 2 * U, nb);
+        if (b0 + 2 * U < nb) load_batch<U, LAYOUT>(a, wbase, voff, doff, b0 + 2 * U, nb, bstride);
         acc = accumulate_batch<U>(b, xs, xd, L, b0 + U, nb, acc);
     }
     acc = acc + xor_f(acc, 4);
@@ -173,6 +178,7 @@ __global__ __launch_bounds__(64 * WPB) void k_q8_0_gemv_T(const uint8_t* __restr
 }
 
 // Plain form of the same order for activation rows too long to stage in LDS.
+template <int LAYOUT = 0>
 __global__ __launch_bounds__(256) void k_q8_0_gemm_T(const uint8_t* __restrict__ W, const uint8_t* __restrict__ Xq,
                                                      float* __restrict__ out, int m_weight, int nb) {
     const int lane = threadIdx.x & 63;
@@ -182,13 +188,13 @@ __global__ __launch_bounds__(256) void k_q8_0_gemm_T(const uint8_t* __restrict__
     if ((row & ~7) >= m_weight) return;
     const int rr = min(row, m_weight - 1);
     const int64_t bpr = (int64_t)nb * kQ80Bytes;
-    const uint8_t* wr = W + (int64_t)rr * bpr;
+    const uint8_t* wr = W + (int64_t)rr * (LAYOUT == 0 ? bpr : 64);
     const uint8_t* xr = Xq + (int64_t)tok * bpr;
     float acc = 0.0f;
     for (int b = 0; b < nb; b++) {
-        const uint8_t* wb = wr + (int64_t)b * kQ80Bytes;
+        const uint8_t* wb = wr + (int64_t)b * (LAYOUT == 0 ? (int64_t)kQ80Bytes : (int64_t)m_weight * 64);
         const uint8_t* xb = xr + (int64_t)b * kQ80Bytes;
-        const uint32_t wv = ld_u32(wb + 2 + 4 * L);
+        const uint32_t wv = ld_u32(wb + (LAYOUT == 0 ? 2 : 4) + 4 * L);
         const uint32_t xv = ld_u32(xb + 2 + 4 * L);
         const float Ad = f16_ieee((uint32_t)wb[0] | ((uint32_t)wb[1] << 8));
         const float Bd = f16_ieee((uint32_t)xb[0] | ((uint32_t)xb[1] << 8));
@@ -213,8 +219,9 @@ void launch_fill_zero(float* out, int64_t n, hipStream_t s) {
     if (n > 0) hipLaunchKernelGGL(k_fill_zero, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, out, n);
 }
 
-void launch_q8_0_dispatch_T(const uint8_t* Wq, const uint8_t* Xq, float* out, int m_weight, int m_tokens, int K,
-                            hipStream_t s) {
+template <int LAYOUT>
+static void dispatch_T(const uint8_t* Wq, const uint8_t* Xq, float* out, int m_weight, int m_tokens, int K,
+                       hipStream_t s) {
     const int nb = K / 32;
     if (nb == 0) {  // the kernels below index block nb-1
         launch_fill_zero(out, (int64_t)m_weight * m_tokens, s);
@@ -223,17 +230,64 @@ void launch_q8_0_dispatch_T(const uint8_t* Wq, const uint8_t* Xq, float* out, in
     const int waves = (m_weight + 7) / 8;
     const size_t lds = (size_t)nb * 36;
     if (lds > 64 * 1024) {
-        hipLaunchKernelGGL(k_q8_0_gemm_T, dim3((waves + 3) / 4, m_tokens), dim3(256), 0, s, Wq, Xq, out, m_weight, nb);
+        hipLaunchKernelGGL(k_q8_0_gemm_T<LAYOUT>, dim3((waves + 3) / 4, m_tokens), dim3(256), 0, s, Wq, Xq, out,
+                           m_weight, nb);
         return;
     }
     // shapes measured on MI355X: 16-block batches and 4 waves per workgroup when
     // there are many waves; fewer, longer chains prefer 32-block batches, 2 waves
     if (waves * m_tokens >= 1024)
-        hipLaunchKernelGGL((k_q8_0_gemv_T<16, 4>), dim3((waves + 3) / 4, m_tokens), dim3(256), lds, s, Wq, Xq, out,
-                           m_weight, nb);
+        hipLaunchKernelGGL((k_q8_0_gemv_T<16, 4, LAYOUT>), dim3((waves + 3) / 4, m_tokens), dim3(256), lds, s, Wq, Xq,
+                           out, m_weight, nb);
     else
-        hipLaunchKernelGGL((k_q8_0_gemv_T<32, 2>), dim3((waves + 1) / 2, m_tokens), dim3(128), lds, s, Wq, Xq, out,
-                           m_weight, nb);
+        hipLaunchKernelGGL((k_q8_0_gemv_T<32, 2, LAYOUT>), dim3((waves + 1) / 2, m_tokens), dim3(128), lds, s, Wq,
+                           Xq, out, m_weight, nb);
+}
+
+void launch_q8_0_dispatch_T(const uint8_t* Wq, const uint8_t* Xq, float* out, int m_weight, int m_tokens, int K,
+                            hipStream_t s) {
+    dispatch_T<0>(Wq, Xq, out, m_weight, m_tokens, K, s);
+}
+
+void launch_q8_pad64_dispatch_T(const uint8_t* Wp, const uint8_t* Xq, float* out, int m_weight, int m_tokens, int K,
+                                hipStream_t s) {
+    dispatch_T<1>(Wp, Xq, out, m_weight, m_tokens, K, s);
+}
+
+// ----------------------------------------------------------------------------
+// fp32 [N, K] -> the padded Q8 layout of inference/llamatov_c_inference.py:88-100:
+// per (row n, block b) of 32 values, d = RN(max(amax, 1e-10) / 127) (float32),
+// q = clip(round-half-even(RN(x / d)), -128, 127), record (b, n) at byte
+// (b*N + n)*64 = {f16(d) RNE, 0, 0, q[32], 28 zero bytes}.  32 lanes per record
+// (lane = element), so the reads of consecutive records are contiguous.
+// ----------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_q8_pad64(const float* __restrict__ x, uint8_t* __restrict__ out, int N,
+                                                  int nb) {
+    const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t rec = g >> 5;  // n * nb + b: the 32 lanes of a record stay together
+    const int e = (int)(g & 31);
+    if (rec >= (int64_t)N * nb) return;
+    const int64_t n = rec / nb, b = rec - n * nb;
+    const float v = x[rec * 32 + e];
+    float amax = fabsf(v);
+#pragma unroll
+    for (int mask = 1; mask < 32; mask <<= 1) amax = fmaxf(amax, xor_f(amax, mask));
+    amax = fmaxf(amax, 1e-10f);
+    const float d = amax / 127.0f;
+    const float qf = fminf(fmaxf(__builtin_rintf(v / d), -128.0f), 127.0f);
+    uint8_t* o = out + (b * N + n) * 64;
+    o[4 + e] = (uint8_t)(int8_t)(int)qf;
+    if (e < 28) o[36 + e] = 0;
+    if (e == 0) {
+        const uint16_t h = __builtin_bit_cast(uint16_t, (_Float16)d);
+        *reinterpret_cast<uint32_t*>(o) = (uint32_t)h;
+    }
+}
+
+void launch_q8_pad64(const float* x, uint8_t* out, int N, int K, hipStream_t s) {
+    const int64_t threads = (int64_t)N * (K / 32) * 32;
+    if (threads == 0) return;
+    hipLaunchKernelGGL(k_q8_pad64, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, x, out, N, K / 32);
 }
 
 }  // namespace bpdq

@@ -147,6 +147,28 @@ def _multi(name, ws, x, Ms, K, outs):
     return outs
 
 
+# ---------------------------------------------------------------- padded Q8 layout
+
+def q8_pad64(x, N, K, out=None):
+    """fp32 [N, K] -> uint8 [K/32 * N * 64] in the layout of q8_pad64_coalesced
+    (inference/llamatov_c_inference.py:88-100)."""
+    import torch
+
+    out = _empty(K // 32 * N * 64, torch.uint8, x) if out is None else out
+    _use_torch_stream()
+    call("bpd_q8_pad64_from_f32_gpu", x, out, N, K)
+    return out
+
+
+def qmatmul_q8_pad64(Wp, Xq, m_weight, m_tokens, K, out=None):
+    import torch
+
+    out = _empty(m_tokens * m_weight, torch.float32, Xq) if out is None else out
+    _use_torch_stream()
+    call("bpd_qmatmul_q8_pad64_gpu", Wp, Xq, out, m_weight, m_tokens, K)
+    return out
+
+
 # ---------------------------------------------------------------- Q6_K
 
 def dequant_q6k(q, order=formats.ORDER_BPD, out=None):

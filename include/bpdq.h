@@ -110,6 +110,17 @@ void bpd_qmatmul_q4k_q8k_fused_gpu(const uint8_t* w_dev, const float* x_dev, flo
 void bpd_qmatmul_q4k_q8k_fused_multi_gpu(const uint8_t* const* w_list, float* const* y_list, const int* M_list,
                                          int n, const float* x_dev, int K);
 
+/* ---- the padded Q8 weight layout of the reference's dp4a GPU path ----
+ * fp32 x[N][K] -> [K/32][N][64] bytes, record (b, n) = {f16 d, 0, 0, int8 q[32], 28 zero bytes}
+ * with d = RN(max(amax, 1e-10)/127) and q = clip(round-half-even(RN(x/d)), -128, 127):
+ * q8_pad64_coalesced (inference/llamatov_c_inference.py:88-100), done on the GPU at load time. */
+void bpd_q8_pad64_from_f32_gpu(const float* x_dev, uint8_t* out_dev, int N, int K);
+/* The Q8_0 tile-order T product (bpd_qmatmul_q8_0_dispatch_gpu) with W in that layout:
+ * out[token * m_weight + row], bit-identical to the dispatcher on the same (d, q) in 34-byte
+ * Q8_0 rows.  Xq: m_tokens rows of Q8_0 blocks. */
+void bpd_qmatmul_q8_pad64_gpu(const uint8_t* W_pad64_dev, const uint8_t* Xq_dev, float* out_dev, int m_weight,
+                              int m_tokens, int K);
+
 /* ---- Q6_K (210-byte blocks: ql[128], qh[64], int8 sc[16], f16 d) ----
  * The reference has Q6_K only as Python: inference/llamatov_helpers.py:161-179 dequantizes
  * it to fp32, with its own element map (element 2i / 2i+1 = low / high nibble of ql[i],

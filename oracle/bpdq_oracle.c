@@ -558,6 +558,38 @@ void bpdq_o_qmatmul_q8_0_llamafile(const uint8_t* W, const float* X, float* out,
     free(Xq);
 }
 
+/* -------------------------------------------------- padded Q8 layout --- */
+
+/* q8_pad64_coalesced, inference/llamatov_c_inference.py:88-100, in float32 as
+ * numpy evaluates it (NEP 50: float32 array op Python float stays float32):
+ * amax = max(max|x|, 1e-10f); d = amax / 127; q = clip(rint(x / d), -128, 127)
+ * (np.round is round-half-even, as rintf in the default mode); d stored as RNE
+ * binary16; record (b, n) at byte (b*N + n)*64 = {d16, 0, 0, q[32], 0 x 28}. */
+void bpdq_o_q8_pad64(const float* x, uint8_t* out, int N, int K) {
+    int nb = K / 32;
+    for (int n = 0; n < N; n++)
+        for (int b = 0; b < nb; b++) {
+            const float* xb = x + (size_t)n * K + (size_t)b * 32;
+            uint8_t* o = out + ((size_t)b * N + n) * 64;
+            float amax = 0.0f;
+            for (int j = 0; j < 32; j++) {
+                float a = fabsf(xb[j]);
+                if (a > amax) amax = a;
+            }
+            if (amax < 1e-10f) amax = 1e-10f;
+            float d = amax / 127.0f;
+            memset(o, 0, 64);
+            uint16_t h = bpdq_o_f32_to_f16(d);
+            memcpy(o, &h, 2);
+            for (int j = 0; j < 32; j++) {
+                float q = rintf(xb[j] / d);
+                if (q < -128.0f) q = -128.0f;
+                if (q > 127.0f) q = 127.0f;
+                o[4 + j] = (uint8_t)(int8_t)q;
+            }
+        }
+}
+
 /* ------------------------------------------------- multi-threaded wrappers */
 
 typedef struct {

@@ -40,6 +40,8 @@ void bpdq_o_dequant_q6k(const uint8_t* q, float* out, int n_blocks, int order);
 int32_t bpdq_o_q6k_q8k_block_int(const uint8_t* wblk, const uint8_t* xblk, int order);
 void bpdq_o_qmatmul_q6k_q8k(const uint8_t* w, const uint8_t* xq, float* y, int M, int K, int order);
 
+void bpdq_o_q8_pad64(const float* x, uint8_t* out, int N, int K);   /* inference/llamatov_c_inference.py:88-100 */
+
 void bpdq_o_dequant_q8_0(const uint8_t* raw, float* out, int n_blocks);                      /* bench/bpd_cpu.c:3960-3973 */
 void bpdq_o_embed_lookup_q8_0(const uint8_t* table, const int32_t* ids, float* out, int n_tokens, int embed_dim); /* :4002-4013 */
 void bpdq_o_quant_q8_0(const float* x, uint8_t* y, int n_elements);                        /* bench/bpd_cpu.c:4106-4136 */

@@ -33,6 +33,7 @@ _SIGS = {
     "bpdq_o_quant_q8_k": (None, [P, P, I]),
     "bpdq_o_qmatmul_q4k_q8k": (None, [P, P, P, I, I, I]),
     "bpdq_o_q4k_q8k_block_ints": (None, [P, P, I, P, P]),
+    "bpdq_o_q8_pad64": (None, [P, P, I, I]),
     "bpdq_o_q6k_quants": (None, [P, I, P]),
     "bpdq_o_dequant_q6k": (None, [P, P, I, I]),
     "bpdq_o_q6k_q8k_block_int": (ctypes.c_int32, [P, P, I]),
@@ -130,6 +131,12 @@ def block_ints(wblk, xblk, order=0):
     I_, M_ = ctypes.c_int32(), ctypes.c_int32()
     lib().bpdq_o_q4k_q8k_block_ints(_p(wblk), _p(xblk), order, ctypes.addressof(I_), ctypes.addressof(M_))
     return I_.value, M_.value
+
+
+def q8_pad64(x, N, K):
+    out = np.empty(K // 32 * N * 64, np.uint8)
+    lib().bpdq_o_q8_pad64(_p(np.ascontiguousarray(x, np.float32)), _p(out), N, K)
+    return out
 
 
 def q6k_quants(blk, order=0):

@@ -287,3 +287,43 @@ def test_q6k_gemv_in_bounds(M, K, order):
                 continue
             for r in range(R):
                 assert min(row0 + r, M - 1) < M
+
+
+@pytest.mark.parametrize("mw,mt,K", [(4096, 1, 14336), (14336, 1, 4096), (13, 3, 160), (8, 1, 32), (9, 2, 64), (7, 5, 128)])
+def test_q8_pad64_gemv_in_bounds(mw, mt, K):
+    """k_q8_0_gemv_T<.., 1> / k_q8_0_gemm_T<1>: W records (b, n) at (b*mw + n)*64."""
+    cfg = q8_gemv_config(mw, mt, K)
+    if cfg is None:
+        return
+    nb = K // 32
+    w_size = nb * mw * 64
+    kind, WPB, U = cfg
+    waves = (mw + 7) // 8
+    grid = (waves + WPB - 1) // WPB if kind == "pipelined" else (waves + 3) // 4
+    l = lanes()
+    L = l & 7
+    for blk in sorted({0, grid - 1}):
+        for wave in range(WPB):
+            row = (blk * WPB + wave) * 8 + (l >> 3)
+            row0 = min((blk * WPB + wave) * 8, mw - 1)
+            doff = (np.maximum(np.minimum(row, mw - 1), row0) - row0) * 64
+            voff = doff + 4 + 4 * L
+            for b0 in range(0, nb + 2 * U, U):
+                for u in range(U):
+                    b = min(b0 + u, nb - 1)
+                    base = row0 * 64 + b * mw * 64
+                    assert (base + voff + 4).max() <= w_size and (base + doff).min() >= 0
+                    assert (base + doff + 2).max() <= w_size
+
+
+@pytest.mark.parametrize("N,K", [(1, 32), (7, 96), (300, 4096)])
+def test_q8_pad64_conversion_in_bounds(N, K):
+    nb = K // 32
+    g = np.arange(((N * nb * 32 + 255) // 256) * 256)
+    rec, e = g >> 5, g & 31
+    live = rec < N * nb
+    rec, e = rec[live], e[live]
+    n, b = rec // nb, rec % nb
+    assert ((rec * 32 + e) < N * K).all()
+    o = (b * N + n) * 64
+    assert ((o + 4 + e) < N * nb * 64).all() and ((o + 36 + np.minimum(e, 27)) < N * nb * 64).all()
