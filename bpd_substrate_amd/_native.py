@@ -69,6 +69,17 @@ HIP_SIGNATURES = {
     "bpd_qmatmul_q8_0_dispatch_s_gpu": (None, [P, P, P, I, I, I]),
     "bpd_qmatmul_q8_0_llamafile_s_gpu": (None, [P, P, P, I, I, I]),
     "bpdq_stream_read_gpu": (None, [P, I, P]),
+    # include/bpdq_llama.h; the struct arguments are passed by address
+    # (inference/llamatov_c_inference.py:66-83 declares them POINTER(struct))
+    "generate_token": (I, [P, P, P, P, I, P, P, P, P, I, I]),
+    "gpu_alloc": (P, [I]),
+    "gpu_copy_h2d": (None, [P, P, I]),
+    "gpu_copy_d2h": (None, [P, P, I]),
+    "gpu_sync": (None, []),
+    "gpu_free": (None, [P]),
+    "bpd_llama_step_gpu": (I, [I, P, P, P, P, I, P, P, P, P, I, I]),
+    "bpd_residual_rmsnorm_gpu": (None, [P, P, P, P, P, P, I, F]),
+    "bpd_expf_gpu": (None, [P, P, I]),
 }
 
 SYNTH_SIGNATURES = {

@@ -203,6 +203,12 @@ void fused(const uint8_t* const* w_list, float* const* y_list, const int* M_list
 
 }  // namespace
 
+namespace bpdq {
+void abi_error(int code, const char* fn, const char* what) { set_err(code, fn, what); }
+bool abi_hip_ok(hipError_t e, const char* fn) { return hip_ok(e, fn); }
+hipStream_t abi_stream() { return g_stream; }
+}  // namespace bpdq
+
 extern "C" {
 
 int bpd_gpu_last_error(void) {

@@ -88,4 +88,23 @@ __device__ __forceinline__ uint4 ld_u128(const uint8_t* p) {
     return *reinterpret_cast<const uint4*>(p);
 }
 
+// Q8_0 quantization of one 32-element block held by 32 consecutive lanes of a
+// wave (lane = element e, all 32 active), as bpd_quant_q8_0_cpu
+// (/root/reference/bench/bpd_cpu.c:4106-4136) computes it: amax is exact in any
+// order (NaN never wins, as with its `av > max` test); d = RN(amax/127) is stored
+// as an RNE binary16 (v_cvt_f16_f32); id = RN(127/amax); q = rint(RN(v*id)).
+__device__ __forceinline__ void q8_0_lane_store(float v, uint8_t* __restrict__ yb, int e) {
+    float amax = fabsf(v);
+#pragma unroll
+    for (int mask = 1; mask < 32; mask <<= 1) amax = fmaxf(amax, xor_f(amax, mask));
+    const float d = amax / 127.0f;
+    const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+    yb[2 + e] = (uint8_t)(int8_t)(int)__builtin_rintf(v * id);
+    if (e == 0) {
+        const uint16_t h = __builtin_bit_cast(uint16_t, (_Float16)d);
+        yb[0] = (uint8_t)(h & 0xFF);
+        yb[1] = (uint8_t)(h >> 8);
+    }
+}
+
 }  // namespace bpdq

@@ -7,6 +7,12 @@
 
 namespace bpdq {
 
+// Error recording (read back with bpd_gpu_last_error) and the launch stream of
+// the exported ABI, for entry points defined outside abi.hip.
+void abi_error(int code, const char* fn, const char* what);
+bool abi_hip_ok(hipError_t e, const char* fn);
+hipStream_t abi_stream();
+
 void launch_dequant_q4k(const uint8_t* q, float* out, int n_blocks, int order, hipStream_t s);
 void launch_qmatmul_q4k_chain(const uint8_t* w, const float* x, float* y, int M, int K, hipStream_t s);
 void launch_quant_q8k(const float* x, uint8_t* y, int n, hipStream_t s);

@@ -1,0 +1,699 @@
+// llama.hip — the decode step of a llama-family model on gfx950
+// (include/bpdq_llama.h): kernels, the per-step launch sequence, and the
+// generate_token ABI of inference/llamatov_c_inference.py:15-83.
+//
+//   k_residual_rmsnorm  x = x_in (+ add); h = rmsnorm(x) * w; Q8_0(h)   one workgroup
+//   k_rope_kv           q/k/v bias, RoPE (NORM pairs) on q and k, K/V cache row write
+//   k_attn_decode       one workgroup per query head: scores, softmax, P.V, Q8_0(out)
+//   k_swiglu            silu(gate) * up, Q8_0
+//   k_argmax            first index of the maximum logit
+//   k_gemv_f32          fp32 head (tied embeddings)
+// The seven GEMVs of a layer are the padded-Q8 tile-order product (q8_0.hip) or
+// the fused Q4_K x Q8_K product (q4k.hip).
+//
+// Every fp32 operation follows the reference's CPU block in order
+// (bench/bpd_cpu.c:5611-5737 and the helpers it calls), so with Q8 weights the
+// step is bit-identical to it:
+//   - sums that the reference runs sequentially (an attention score over
+//     head_dim, the softmax denominator, each output of P.V) run sequentially
+//     here, in one lane, in the same order;
+//   - max, amax and argmax are exact in any order;
+//   - expf is the libm method restated in bpdq_math.h; cos/sin of the rotary
+//     angles come from the host's libm (sincosf, which is what the reference's
+//     compiled cosf/sinf pair calls) through a kernel argument;
+//   - the RMSNorm sum of squares is binary64 like the reference's; its
+//     parallel sum is used only when an error bound proves it gives the same
+//     fp32 mean as the reference's sequential binary64 sum.
+#include <climits>
+#include <cmath>
+#include <cstdio>
+#include <mutex>
+
+#include "../../include/bpdq.h"
+#include "../../include/bpdq_llama.h"
+#include "bpdq_device.h"
+#include "bpdq_launch.h"
+#include "bpdq_math.h"
+
+namespace bpdq {
+
+constexpr int kNormThreads = 1024;
+constexpr int kMaxEmbd = 16384;  // the residual row stays in LDS (64 KB)
+constexpr int kMaxHeadDim = 256;
+constexpr int kAttnThreads = 256;
+constexpr int kMaxCtx = 32768;  // one head's scores stay in LDS (128 KB)
+
+// ----------------------------------------------------------------------------
+// Residual add + RMSNorm + Q8_0, one workgroup for the whole row
+// (bpd_add_f32_cpu, bench/bpd_cpu.c:5466; bpd_rmsnorm_llama_cpu, :4959-4986):
+//   x = x_in + add;  mean = (float)(sum_i (double)x_i^2 / n)   (sequential in the reference)
+//   scale = 1 / sqrtf(mean + eps);  h_i = (x_i * scale) * w_i.
+// The squares are exact in binary64.  Any summation order of n non-negative
+// terms is within (n-1) 2^-53 S of the exact sum S, so the reference's
+// sequential sum lies within E = 4 n 2^-53 S_tree of this kernel's tree sum.
+// If (float)((S_tree - E)/n) == (float)((S_tree + E)/n), rounding monotonicity
+// pins the reference's mean to that value; otherwise lane 0 redoes the
+// reference's sequential sum from the row kept in LDS.
+// ----------------------------------------------------------------------------
+template <int NT>
+__global__ __launch_bounds__(NT) void k_residual_rmsnorm(const float* x_in, const float* __restrict__ add,
+                                                         float* x_out, const float* __restrict__ w,
+                                                         float* __restrict__ h, uint8_t* __restrict__ xq, int n,
+                                                         float eps) {
+    extern __shared__ float xs[];
+    __shared__ double wsum[NT / 64];
+    __shared__ float sh_scale;
+    const int tid = threadIdx.x;
+    double s = 0.0;
+    for (int i = tid; i < n; i += NT) {
+        float v = x_in[i];
+        if (add != nullptr) v = v + add[i];
+        xs[i] = v;
+        if (x_out != nullptr) x_out[i] = v;
+        s += (double)v * (double)v;
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m, 64);
+    if ((tid & 63) == 0) wsum[tid >> 6] = s;
+    __syncthreads();
+    if (tid == 0) {
+        double S = 0.0;
+        for (int i = 0; i < NT / 64; i++) S += wsum[i];
+        const double dn = (double)n;
+        const double err = S * (4.0 * dn * 0x1p-53);
+        const float lo = (float)((S - err) / dn), hi = (float)((S + err) / dn);
+        float mean = lo;
+        if (!(lo == hi)) {
+            double q = 0.0;
+            for (int i = 0; i < n; i++) q += (double)xs[i] * (double)xs[i];
+            mean = (float)(q / dn);
+        }
+        sh_scale = 1.0f / sqrtf(mean + eps);
+    }
+    __syncthreads();
+    const float scale = sh_scale;
+    // n and NT are multiples of 32: each Q8_0 block is 32 lanes of one wave
+    for (int i = tid; i < n; i += NT) {
+        const float y = (xs[i] * scale) * w[i];
+        if (h != nullptr) h[i] = y;
+        if (xq != nullptr) q8_0_lane_store(y, xq + (int64_t)(i >> 5) * kQ80Bytes, i & 31);
+    }
+}
+
+// ----------------------------------------------------------------------------
+// Bias, RoPE and the K/V cache write (bpd_rope_norm_freqs_cpu,
+// bench/bpd_cpu.c:5146-5184 without frequency factors; bpd_kv_cache_write_cpu,
+// :5204-5222).  NORM pairs: pair j of a head rotates elements 2j and 2j+1 by
+// angle pos * theta_scale^j, whose cos/sin the host computed:
+//   y0 = x0*c - x1*s,  y1 = x0*s + x1*c   (each product rounded, then the sum).
+// Thread i: a q pair, a k pair (also written to the cache), or a v element.
+// ----------------------------------------------------------------------------
+struct RopeTab {
+    float c[kMaxHeadDim / 2];
+    float s[kMaxHeadDim / 2];
+};
+
+__global__ __launch_bounds__(256) void k_rope_kv(float* __restrict__ q, float* __restrict__ k, float* __restrict__ v,
+                                                 const float* __restrict__ bq, const float* __restrict__ bk,
+                                                 const float* __restrict__ bv, float* __restrict__ kc,
+                                                 float* __restrict__ vc, int nq_pairs, int nk_pairs, int nv, int half,
+                                                 RopeTab tab) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < nq_pairs + nk_pairs) {
+        const bool isq = i < nq_pairs;
+        const int p = isq ? i : i - nq_pairs;
+        float* t = isq ? q : k;
+        const float* b = isq ? bq : bk;
+        const int e = 2 * p, j = p % half;
+        float x0 = t[e], x1 = t[e + 1];
+        if (b != nullptr) {
+            x0 = x0 + b[e];
+            x1 = x1 + b[e + 1];
+        }
+        const float c = tab.c[j], s = tab.s[j];
+        const float y0 = x0 * c - x1 * s;
+        const float y1 = x0 * s + x1 * c;
+        t[e] = y0;
+        t[e + 1] = y1;
+        if (!isq) {
+            kc[e] = y0;
+            kc[e + 1] = y1;
+        }
+    } else if (i < nq_pairs + nk_pairs + nv) {
+        const int j = i - nq_pairs - nk_pairs;
+        float val = v[j];
+        if (bv != nullptr) {
+            val = val + bv[j];
+            v[j] = val;
+        }
+        vc[j] = val;
+    }
+}
+
+// ----------------------------------------------------------------------------
+// Decode attention for query head blockIdx.x over cache rows 0..n-1
+// (bpd_gqa_attn_cpu, bench/bpd_cpu.c:5370-5440, post-scaled batch softmax):
+//   s_j = sum_d q_d k_jd (sequential over d);  v_j = s_j * scale
+//   m = max(-1e38, v_j);  e_j = expf(v_j - m);  S = sum_j e_j (sequential over j)
+//   w_j = e_j * (S == 0 ? 0 : 1/S);  out_d = sum_j v_jd w_j (sequential over j)
+// Scores and weights live in LDS.  The reference also visits rows n..max_seq-1
+// with weight exp(-1e38 - m) = 0; for finite cache contents those add exact
+// zeros, so stopping at n gives the same bits.
+// ----------------------------------------------------------------------------
+template <int NT>
+__global__ __launch_bounds__(NT) void k_attn_decode(const float* __restrict__ q, const float* __restrict__ kc,
+                                                    const float* __restrict__ vc, float* __restrict__ out,
+                                                    uint8_t* __restrict__ xq, int group, int row, int D, int n,
+                                                    float scale) {
+    extern __shared__ float e[];
+    __shared__ float4 qs4[kMaxHeadDim / 4];
+    __shared__ float red[NT / 64];
+    __shared__ float sh_max, sh_inv;
+    const int tid = threadIdx.x, head = blockIdx.x, kvh = head / group;
+    float* qs = reinterpret_cast<float*>(qs4);
+    for (int d = tid; d < D; d += NT) qs[d] = q[(int64_t)head * D + d];
+    __syncthreads();
+    const float* kbase = kc + (int64_t)kvh * D;
+    float m = -1e38f;
+    for (int j = tid; j < n; j += NT) {
+        const float4* kr = reinterpret_cast<const float4*>(kbase + (int64_t)j * row);
+        float s = 0.0f;
+        for (int d4 = 0; d4 < D / 4; d4++) {
+            const float4 kv = kr[d4];
+            const float4 qv = qs4[d4];
+            s = s + qv.x * kv.x;
+            s = s + qv.y * kv.y;
+            s = s + qv.z * kv.z;
+            s = s + qv.w * kv.w;
+        }
+        const float sv = s * scale;
+        e[j] = sv;
+        m = sv > m ? sv : m;
+    }
+#pragma unroll
+    for (int mask = 32; mask >= 1; mask >>= 1) {
+        const float o = xor_f(m, mask);
+        m = o > m ? o : m;
+    }
+    if ((tid & 63) == 0) red[tid >> 6] = m;
+    __syncthreads();
+    if (tid == 0) {
+        float mm = red[0];
+        for (int w = 1; w < NT / 64; w++) mm = red[w] > mm ? red[w] : mm;
+        sh_max = mm;
+    }
+    __syncthreads();
+    const float mx = sh_max;
+    for (int j = tid; j < n; j += NT) e[j] = expf_libm(e[j] - mx);
+    __syncthreads();
+    if (tid == 0) {
+        float sum = 0.0f;
+#pragma unroll 8
+        for (int j = 0; j < n; j++) sum = sum + e[j];
+        sh_inv = sum == 0.0f ? 0.0f : 1.0f / sum;
+    }
+    __syncthreads();
+    const float inv = sh_inv;
+    for (int j = tid; j < n; j += NT) e[j] = e[j] * inv;
+    __syncthreads();
+    // D <= NT and D % 32 == 0: lanes d < D are whole 32-lane Q8_0 blocks
+    const int d = tid;
+    if (d < D) {
+        const float* vcol = vc + (int64_t)kvh * D + d;
+        float acc = 0.0f;
+#pragma unroll 8
+        for (int j = 0; j < n; j++) acc = acc + vcol[(int64_t)j * row] * e[j];
+        const int64_t o = (int64_t)head * D + d;
+        out[o] = acc;
+        if (xq != nullptr) q8_0_lane_store(acc, xq + (o >> 5) * kQ80Bytes, d & 31);
+    }
+}
+
+// ----------------------------------------------------------------------------
+// SwiGLU (bpd_swiglu_fuse_cpu, bench/bpd_cpu.c:5504-5507):
+//   y = (g / (1 + expf(-g))) * u, written over gate, and Q8_0(y).
+// ----------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_swiglu(float* gate, const float* __restrict__ up, uint8_t* __restrict__ xq,
+                                                int F) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= F) return;  // F % 32 == 0: whole Q8_0 blocks leave together
+    const float g = gate[i];
+    const float y = (g / (1.0f + expf_libm(-g))) * up[i];
+    gate[i] = y;
+    if (xq != nullptr) q8_0_lane_store(y, xq + (int64_t)(i >> 5) * kQ80Bytes, i & 31);
+}
+
+// ----------------------------------------------------------------------------
+// Argmax (bpd_argmax_dim_cpu, bench/bpd_cpu.c:4512-4526): best = x[0], then
+// x[k] replaces it when x[k] > best.  So the result is the first index of the
+// largest non-NaN value (+0 and -0 tie), or 0 when x[0] is NaN.
+// ----------------------------------------------------------------------------
+__device__ __forceinline__ bool argmax_beats(float b, int bi, float a, int ai) {
+    if (bi == INT_MAX) return false;
+    if (ai == INT_MAX) return true;
+    return b > a || (b == a && bi < ai);
+}
+
+template <int NT>
+__global__ __launch_bounds__(NT) void k_argmax(const float* __restrict__ x, int n, int32_t* __restrict__ out) {
+    __shared__ float bv[NT / 64];
+    __shared__ int bi[NT / 64];
+    const int tid = threadIdx.x;
+    float best = 0.0f;
+    int idx = INT_MAX;  // no candidate yet
+    for (int i = tid; i < n; i += NT) {
+        const float v = x[i];
+        if (v == v && (idx == INT_MAX || v > best)) {
+            best = v;
+            idx = i;
+        }
+    }
+#pragma unroll
+    for (int mask = 32; mask >= 1; mask >>= 1) {
+        const float ob = xor_f(best, mask);
+        const int oi = xor_i(idx, mask);
+        if (argmax_beats(ob, oi, best, idx)) {
+            best = ob;
+            idx = oi;
+        }
+    }
+    if ((tid & 63) == 0) {
+        bv[tid >> 6] = best;
+        bi[tid >> 6] = idx;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < NT / 64; w++)
+            if (argmax_beats(bv[w], bi[w], best, idx)) {
+                best = bv[w];
+                idx = bi[w];
+            }
+        const float x0 = x[0];
+        out[0] = (!(x0 == x0) || idx == INT_MAX) ? 0 : idx;
+    }
+}
+
+// ----------------------------------------------------------------------------
+// fp32 head y[N] = W[N][K] h (the reference driver's weight-tied fallback,
+// inference/llamatov_c_inference.py:179-186; its library has no source).
+// Order: lane l sums W[r][l + 64 i] * h[l + 64 i] over i from +0.0, then the
+// lanes combine by xor-32, 16, 8, 4, 2, 1 steps (p_l = p_l + p_{l^m}).
+// ----------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_gemv_f32(const float* __restrict__ W, const float* __restrict__ x,
+                                                  float* __restrict__ y, int N, int K) {
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= N) return;
+    const float* wr = W + (int64_t)r * K;
+    float acc = 0.0f;
+    for (int k = lane; k < K; k += 64) acc = acc + wr[k] * x[k];
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) acc = acc + xor_f(acc, m);
+    if (lane == 0) y[r] = acc;
+}
+
+__global__ __launch_bounds__(256) void k_expf(const float* __restrict__ x, float* __restrict__ y, int n) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) y[i] = expf_libm(x[i]);
+}
+
+// ---------------------------------------------------------------------------- host side
+
+namespace {
+
+// The kernels that take more than 64 KB of dynamic LDS say so once per process.
+bool lds_limits_set(const char* fn) {
+    static std::once_flag once;
+    static hipError_t err = hipSuccess;
+    std::call_once(once, [] {
+        err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_decode<kAttnThreads>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, kMaxCtx * 4);
+        if (err == hipSuccess)
+            err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_residual_rmsnorm<kNormThreads>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, kMaxEmbd * 4);
+    });
+    return abi_hip_ok(err, fn);
+}
+
+void launch_norm(const float* x_in, const float* add, float* x_out, const float* w, float* h, uint8_t* xq, int n,
+                 float eps, hipStream_t s) {
+    hipLaunchKernelGGL(k_residual_rmsnorm<kNormThreads>, dim3(1), dim3(kNormThreads), (size_t)n * 4, s, x_in, add,
+                       x_out, w, h, xq, n, eps);
+}
+
+// Rotation table for `pos`: pair j turns by pos * theta_scale^j, the angle
+// accumulated in fp32 exactly as the reference's loop does
+// (theta_scale = powf(base, -2/n_dims); theta *= theta_scale after each pair).
+// sincosf through a pointer, so the compiler neither folds nor reorders it.
+void rope_table(RopeTab& t, int pos, int head_dim, float base) {
+    static void (*volatile sc)(float, float*, float*) = sincosf;
+    static float (*volatile pw)(float, float) = powf;
+    const float theta_scale = pw(base, -2.0f / (float)head_dim);
+    float theta = (float)pos;
+    for (int j = 0; j < head_dim / 2; j++) {
+        sc(theta, &t.s[j], &t.c[j]);
+        theta *= theta_scale;
+    }
+}
+
+// Device workspace of the quantized activations (Q8_0 rows, or Q8_K when a Q4_K
+// GEMV is too long for the fused kernel).  Grown on demand.
+std::mutex g_ws_mu;
+void* g_ws = nullptr;
+size_t g_ws_bytes = 0;
+
+uint8_t* step_workspace(size_t bytes, const char* fn) {
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    if (bytes <= g_ws_bytes) return static_cast<uint8_t*>(g_ws);
+    if (g_ws) {
+        if (!abi_hip_ok(hipDeviceSynchronize(), fn)) return nullptr;
+        (void)hipFree(g_ws);
+        g_ws = nullptr;
+        g_ws_bytes = 0;
+    }
+    if (hipMalloc(&g_ws, bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        abi_error(BPDQ_ERR_ALLOC, fn, "workspace allocation failed");
+        g_ws = nullptr;
+        return nullptr;
+    }
+    g_ws_bytes = bytes;
+    return static_cast<uint8_t*>(g_ws);
+}
+
+struct V {
+    const char* fn;
+    bool ok = true;
+    void fail(int code, const char* what) {
+        if (ok) abi_error(code, fn, what);
+        ok = false;
+    }
+    void need(bool cond, int code, const char* what) {
+        if (!cond) fail(code, what);
+    }
+    void ptr(const void* p, uintptr_t align, const char* name) {
+        if (!ok) return;
+        char buf[128];
+        if (p == nullptr) {
+            std::snprintf(buf, sizeof buf, "%s is NULL", name);
+            fail(BPDQ_ERR_NULL, buf);
+        } else if ((reinterpret_cast<uintptr_t>(p) & (align - 1)) != 0) {
+            std::snprintf(buf, sizeof buf, "%s is not %d-byte aligned", name, (int)align);
+            fail(BPDQ_ERR_ALIGN, buf);
+        }
+    }
+    void dims(int got_k, int want_k, int got_n, int want_n, int layer, const char* name) {
+        if (!ok || (got_k == want_k && got_n == want_n)) return;
+        char buf[160];
+        std::snprintf(buf, sizeof buf, "layer %d %s is %d x %d (K x N), expected %d x %d", layer, name, got_k, got_n,
+                      want_k, want_n);
+        fail(BPDQ_ERR_SHAPE, buf);
+    }
+};
+
+struct Geometry {
+    int E, H, HKV, D, F, L;
+};
+
+bool validate(V& v, int fmt, const LayerWeights* layers, const ModelConfig* cfg, const WorkBuffers* buf,
+              const KVCache* kv, int pos, const void* emb, const void* out_norm, const void* lm_w,
+              const void* lm_f32, int lm_K, int lm_N, Geometry& g) {
+    v.need(fmt == BPDQ_W_Q8_PAD64 || fmt == BPDQ_W_Q4K || fmt == BPDQ_W_Q4K_GGUF, BPDQ_ERR_SHAPE,
+           "unknown weight_format");
+    v.ptr(cfg, 1, "cfg");
+    v.ptr(buf, 1, "buf");
+    if (!v.ok) return false;
+    g = Geometry{cfg->n_embd, cfg->n_head, cfg->n_head_kv, cfg->head_dim, cfg->ff_dim, cfg->n_layers};
+    const int blk = fmt == BPDQ_W_Q8_PAD64 ? 32 : 256;
+    v.need(g.L >= 0, BPDQ_ERR_SHAPE, "n_layers is negative");
+    v.need(g.H > 0 && g.HKV > 0 && g.H % g.HKV == 0, BPDQ_ERR_SHAPE,
+           "n_head and n_head_kv must be positive, n_head a multiple of n_head_kv");
+    v.need(g.D > 0 && g.D % 32 == 0 && g.D <= kMaxHeadDim, BPDQ_ERR_SHAPE,
+           "head_dim must be a multiple of 32 and at most 256");
+    v.need(g.E == g.H * g.D, BPDQ_ERR_SHAPE, "n_embd must equal n_head * head_dim");
+    v.need(g.E > 0 && g.E % blk == 0 && g.E <= kMaxEmbd, BPDQ_ERR_SHAPE,
+           "n_embd must be a positive multiple of the weight block length, at most 16384");
+    v.need(g.F > 0 && g.F % blk == 0, BPDQ_ERR_SHAPE, "ff_dim must be a positive multiple of the weight block length");
+    v.need(cfg->max_seq > 0 && cfg->max_seq <= kMaxCtx, BPDQ_ERR_SHAPE, "max_seq must be in 1..32768");
+    v.need(pos >= 0 && pos < cfg->max_seq, BPDQ_ERR_SHAPE, "position must be in 0..max_seq-1");
+    v.need(lm_K == g.E, BPDQ_ERR_SHAPE, "lm_K must equal n_embd");
+    v.need(lm_N > 0, BPDQ_ERR_SHAPE, "lm_N must be positive");
+    if (!v.ok) return false;
+    const uintptr_t wal = fmt == BPDQ_W_Q8_PAD64 ? 4 : 16;
+    v.ptr(emb, 4, "embedding");
+    v.ptr(out_norm, 4, "output_norm_w");
+    if (lm_w != nullptr)
+        v.ptr(lm_w, wal, "lm_head");
+    else
+        v.ptr(lm_f32, 4, "lm_f32 (lm_head is NULL)");
+    const void* bufs[11] = {buf->x, buf->h, buf->q, buf->k, buf->v, buf->attn_out,
+                            buf->gate, buf->up, buf->ffn, buf->logits, buf->argmax_result};
+    static const char* names[11] = {"buf.x", "buf.h", "buf.q", "buf.k", "buf.v", "buf.attn_out",
+                                    "buf.gate", "buf.up", "buf.ffn", "buf.logits", "buf.argmax_result"};
+    for (int i = 0; i < 11; i++) v.ptr(bufs[i], 16, names[i]);
+    if (g.L > 0) {
+        v.ptr(layers, 1, "layers");
+        v.ptr(kv, 1, "kv");
+        if (v.ok) {
+            v.ptr(kv->k_cache, 1, "kv.k_cache");
+            v.ptr(kv->v_cache, 1, "kv.v_cache");
+        }
+    }
+    for (int l = 0; l < g.L && v.ok; l++) {
+        const LayerWeights& w = layers[l];
+        const int qd = g.H * g.D, kd = g.HKV * g.D;
+        v.dims(w.q_K, g.E, w.q_N, qd, l, "q");
+        v.dims(w.k_K, g.E, w.k_N, kd, l, "k");
+        v.dims(w.v_K, g.E, w.v_N, kd, l, "v");
+        v.dims(w.o_K, qd, w.o_N, g.E, l, "o");
+        v.dims(w.gate_K, g.E, w.gate_N, g.F, l, "gate");
+        v.dims(w.up_K, g.E, w.up_N, g.F, l, "up");
+        v.dims(w.down_K, g.F, w.down_N, g.E, l, "down");
+        const void* mats[7] = {w.q, w.k, w.v, w.o, w.gate, w.up, w.down};
+        static const char* mnames[7] = {"q", "k", "v", "o", "gate", "up", "down"};
+        for (int i = 0; i < 7; i++) v.ptr(mats[i], wal, mnames[i]);
+        v.ptr(w.attn_norm, 4, "attn_norm");
+        v.ptr(w.ffn_norm, 4, "ffn_norm");
+        if (w.q_bias) v.ptr(w.q_bias, 4, "q_bias");
+        if (w.k_bias) v.ptr(w.k_bias, 4, "k_bias");
+        if (w.v_bias) v.ptr(w.v_bias, 4, "v_bias");
+        v.ptr(kv->k_cache[l], 16, "kv.k_cache[layer]");
+        v.ptr(kv->v_cache[l], 16, "kv.v_cache[layer]");
+    }
+    return v.ok;
+}
+
+// One GEMV y[N] = W[N][K] a[K]: padded Q8 reads the Q8_0 bytes aq of a; Q4_K
+// takes fp32 a (and quantizes it to Q8_K inside the kernel when K allows).
+struct Gemv {
+    int fmt;
+    uint8_t* q8k;  // Q8_K staging for K beyond the fused kernel
+    hipStream_t s;
+    void run(int n, const void* const* w, float* const* y, const int* N, const float* a, const uint8_t* aq,
+             int K) const {
+        if (fmt == BPDQ_W_Q8_PAD64) {
+            for (int i = 0; i < n; i++)
+                launch_q8_pad64_dispatch_T(static_cast<const uint8_t*>(w[i]), aq, y[i], N[i], 1, K, s);
+            return;
+        }
+        const int order = fmt == BPDQ_W_Q4K_GGUF ? 1 : 0;
+        const uint8_t* wl[4];
+        for (int i = 0; i < n; i++) wl[i] = static_cast<const uint8_t*>(w[i]);
+        if (K <= fused_max_k()) {
+            launch_qmatmul_q4k_fused_multi(wl, y, N, n, a, K, order, s);
+        } else {
+            launch_quant_q8k(a, q8k, K, s);
+            launch_qmatmul_q4k_q8k_multi(wl, y, N, n, q8k, K, order, s);
+        }
+    }
+};
+
+bool enqueue_step(int fmt, const LayerWeights* layers, const ModelConfig* cfg, const WorkBuffers* buf,
+                  const KVCache* kv, int pos, const void* emb, const void* out_norm, const void* lm_w,
+                  const void* lm_f32, int lm_K, int lm_N, const char* fn) {
+    V v{fn};
+    Geometry g{};
+    if (!validate(v, fmt, layers, cfg, buf, kv, pos, emb, out_norm, lm_w, lm_f32, lm_K, lm_N, g)) return false;
+    if (!lds_limits_set(fn)) return false;
+    const bool q8 = fmt == BPDQ_W_Q8_PAD64;
+    const size_t q8e = (size_t)(g.E / 32) * kQ80Bytes, q8f = (size_t)(g.F / 32) * kQ80Bytes;
+    const int kmax = g.F > g.E ? g.F : g.E;
+    const size_t q8k = kmax > fused_max_k() ? (size_t)(kmax / 256) * kQ8KBytes : 0;
+    uint8_t* ws = step_workspace((q8 ? 2 * q8e + q8f : 0) + q8k + 256, fn);
+    if (ws == nullptr) return false;
+    uint8_t* xq_e = q8 ? ws : nullptr;
+    uint8_t* xq_a = q8 ? ws + q8e : nullptr;
+    uint8_t* xq_f = q8 ? ws + 2 * q8e : nullptr;
+    const Gemv gemv{fmt, ws + (q8 ? 2 * q8e + q8f : 0), abi_stream()};
+    const hipStream_t s = gemv.s;
+
+    float* x = static_cast<float*>(buf->x);
+    float* h = static_cast<float*>(buf->h);
+    float* qb = static_cast<float*>(buf->q);
+    float* kb = static_cast<float*>(buf->k);
+    float* vb = static_cast<float*>(buf->v);
+    float* att = static_cast<float*>(buf->attn_out);
+    float* gate = static_cast<float*>(buf->gate);
+    float* up = static_cast<float*>(buf->up);
+    float* ffn = static_cast<float*>(buf->ffn);
+    float* logits = static_cast<float*>(buf->logits);
+    const int row = g.HKV * g.D, n_ctx = pos + 1;
+    const float scale = 1.0f / sqrtf((float)g.D);
+    RopeTab tab;
+    if (g.L > 0) rope_table(tab, pos, g.D, cfg->rope_theta);
+
+    const float* xin = static_cast<const float*>(emb);
+    const float* add = nullptr;
+    for (int l = 0; l < g.L; l++) {
+        const LayerWeights& w = layers[l];
+        launch_norm(xin, add, x, static_cast<const float*>(w.attn_norm), h, xq_e, g.E, cfg->eps, s);
+        xin = x;
+        {
+            const void* ws3[3] = {w.q, w.k, w.v};
+            float* ys3[3] = {qb, kb, vb};
+            const int ns3[3] = {w.q_N, w.k_N, w.v_N};
+            gemv.run(3, ws3, ys3, ns3, h, xq_e, g.E);
+        }
+        float* kc = static_cast<float*>(kv->k_cache[l]) + (int64_t)pos * row;
+        float* vc = static_cast<float*>(kv->v_cache[l]) + (int64_t)pos * row;
+        const int nq = g.H * g.D / 2, nk = row / 2, nv = row;
+        hipLaunchKernelGGL(k_rope_kv, dim3((nq + nk + nv + 255) / 256), dim3(256), 0, s, qb, kb, vb,
+                           static_cast<const float*>(w.q_bias), static_cast<const float*>(w.k_bias),
+                           static_cast<const float*>(w.v_bias), kc, vc, nq, nk, nv, g.D / 2, tab);
+        hipLaunchKernelGGL(k_attn_decode<kAttnThreads>, dim3(g.H), dim3(kAttnThreads), (size_t)n_ctx * 4, s, qb,
+                           static_cast<const float*>(kv->k_cache[l]), static_cast<const float*>(kv->v_cache[l]), att,
+                           xq_a, g.H / g.HKV, row, g.D, n_ctx, scale);
+        {
+            const void* wo[1] = {w.o};
+            float* yo[1] = {ffn};
+            const int no[1] = {w.o_N};
+            gemv.run(1, wo, yo, no, att, xq_a, g.H * g.D);
+        }
+        launch_norm(x, ffn, x, static_cast<const float*>(w.ffn_norm), h, xq_e, g.E, cfg->eps, s);
+        {
+            const void* wgu[2] = {w.gate, w.up};
+            float* ygu[2] = {gate, up};
+            const int ngu[2] = {w.gate_N, w.up_N};
+            gemv.run(2, wgu, ygu, ngu, h, xq_e, g.E);
+        }
+        hipLaunchKernelGGL(k_swiglu, dim3((g.F + 255) / 256), dim3(256), 0, s, gate, up, xq_f, g.F);
+        {
+            const void* wd[1] = {w.down};
+            float* yd[1] = {ffn};
+            const int nd[1] = {w.down_N};
+            gemv.run(1, wd, yd, nd, gate, xq_f, g.F);
+        }
+        add = ffn;
+    }
+    launch_norm(xin, add, x, static_cast<const float*>(out_norm), h, xq_e, g.E, cfg->eps, s);
+    if (lm_w != nullptr) {
+        const void* wl[1] = {lm_w};
+        float* yl[1] = {logits};
+        const int nl[1] = {lm_N};
+        gemv.run(1, wl, yl, nl, h, xq_e, g.E);
+    } else {
+        hipLaunchKernelGGL(k_gemv_f32, dim3((lm_N + 3) / 4), dim3(256), 0, s, static_cast<const float*>(lm_f32), h,
+                           logits, lm_N, g.E);
+    }
+    hipLaunchKernelGGL(k_argmax<1024>, dim3(1), dim3(1024), 0, s, logits, lm_N,
+                       static_cast<int32_t*>(buf->argmax_result));
+    return abi_hip_ok(hipGetLastError(), fn);
+}
+
+}  // namespace
+}  // namespace bpdq
+
+extern "C" {
+
+int generate_token(const LayerWeights* layers, const ModelConfig* cfg, const WorkBuffers* buf, const KVCache* kv,
+                   int position, const void* embedding, const void* output_norm_w, const void* lm_head,
+                   const void* lm_f32, int lm_K, int lm_N) {
+    const char* fn = "generate_token";
+    if (!bpdq::enqueue_step(BPDQ_W_Q8_PAD64, layers, cfg, buf, kv, position, embedding, output_norm_w, lm_head,
+                            lm_f32, lm_K, lm_N, fn))
+        return -1;
+    int32_t tok = -1;
+    const hipStream_t s = bpdq::abi_stream();
+    if (!bpdq::abi_hip_ok(hipMemcpyAsync(&tok, buf->argmax_result, 4, hipMemcpyDeviceToHost, s), fn)) return -1;
+    if (!bpdq::abi_hip_ok(hipStreamSynchronize(s), fn)) return -1;
+    return tok;
+}
+
+int bpd_llama_step_gpu(int weight_format, const LayerWeights* layers, const ModelConfig* cfg,
+                       const WorkBuffers* buf, const KVCache* kv, int position, const void* embedding,
+                       const void* output_norm_w, const void* lm_head, const void* lm_f32, int lm_K, int lm_N) {
+    return bpdq::enqueue_step(weight_format, layers, cfg, buf, kv, position, embedding, output_norm_w, lm_head,
+                              lm_f32, lm_K, lm_N, "bpd_llama_step_gpu")
+               ? 0
+               : -1;
+}
+
+void* gpu_alloc(int bytes) {
+    const char* fn = "gpu_alloc";
+    if (bytes < 0) {
+        bpdq::abi_error(BPDQ_ERR_SHAPE, fn, "bytes is negative");
+        return nullptr;
+    }
+    void* p = nullptr;
+    if (hipMalloc(&p, bytes > 0 ? (size_t)bytes : 1) != hipSuccess) {
+        (void)hipGetLastError();
+        bpdq::abi_error(BPDQ_ERR_ALLOC, fn, "hipMalloc failed");
+        return nullptr;
+    }
+    return p;
+}
+
+void gpu_free(void* p) {
+    if (p != nullptr) bpdq::abi_hip_ok(hipFree(p), "gpu_free");
+}
+
+static void gpu_copy(void* dst, const void* src, int bytes, hipMemcpyKind kind, const char* fn) {
+    if (bytes < 0) {
+        bpdq::abi_error(BPDQ_ERR_SHAPE, fn, "bytes is negative");
+        return;
+    }
+    if (bytes == 0) return;
+    if (dst == nullptr || src == nullptr) {
+        bpdq::abi_error(BPDQ_ERR_NULL, fn, "NULL pointer");
+        return;
+    }
+    bpdq::abi_hip_ok(hipMemcpy(dst, src, (size_t)bytes, kind), fn);
+}
+
+void gpu_copy_h2d(void* dst, const void* src, int bytes) {
+    gpu_copy(dst, src, bytes, hipMemcpyHostToDevice, "gpu_copy_h2d");
+}
+void gpu_copy_d2h(void* dst, const void* src, int bytes) {
+    gpu_copy(dst, src, bytes, hipMemcpyDeviceToHost, "gpu_copy_d2h");
+}
+void gpu_sync(void) { bpdq::abi_hip_ok(hipDeviceSynchronize(), "gpu_sync"); }
+
+void bpd_residual_rmsnorm_gpu(const float* x_in, const float* add, float* x_out, const float* w, float* h,
+                              uint8_t* xq, int n, float eps) {
+    const char* fn = "bpd_residual_rmsnorm_gpu";
+    bpdq::V v{fn};
+    v.need(n > 0 && n % 32 == 0 && n <= bpdq::kMaxEmbd, BPDQ_ERR_SHAPE,
+           "n must be a positive multiple of 32, at most 16384");
+    v.ptr(x_in, 4, "x_in");
+    v.ptr(w, 4, "w");
+    if (add) v.ptr(add, 4, "add");
+    if (x_out) v.ptr(x_out, 4, "x_out");
+    if (h) v.ptr(h, 4, "h");
+    if (!v.ok || !bpdq::lds_limits_set(fn)) return;
+    bpdq::launch_norm(x_in, add, x_out, w, h, xq, n, eps, bpdq::abi_stream());
+    bpdq::abi_hip_ok(hipGetLastError(), fn);
+}
+
+void bpd_expf_gpu(const float* x, float* y, int n) {
+    const char* fn = "bpd_expf_gpu";
+    bpdq::V v{fn};
+    v.need(n >= 0, BPDQ_ERR_SHAPE, "n is negative");
+    if (!v.ok || n == 0) return;
+    v.ptr(x, 4, "x");
+    v.ptr(y, 4, "y");
+    if (!v.ok) return;
+    hipLaunchKernelGGL(bpdq::k_expf, dim3((n + 255) / 256), dim3(256), 0, bpdq::abi_stream(), x, y, n);
+    bpdq::abi_hip_ok(hipGetLastError(), fn);
+}
+
+}  // extern "C"

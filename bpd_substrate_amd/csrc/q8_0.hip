@@ -42,28 +42,14 @@ void launch_embed_q8_0(const uint8_t* table, const int32_t* ids, float* out, int
                        embed_dim);
 }
 
-// Q8_0 quantizer: 32 lanes per block (two blocks per wave), lane = element.
-// amax is exact whatever the reduction order; d = RN(amax/127) is stored as an
-// RNE binary16 (v_cvt_f16_f32); id = RN(127/amax); q = rint(RN(x*id)).
+// Q8_0 quantizer: 32 lanes per block (two blocks per wave), lane = element
+// (q8_0_lane_store).
 __global__ __launch_bounds__(256) void k_quant_q8_0(const float* __restrict__ x, uint8_t* __restrict__ y,
                                                     int64_t n_blocks) {
     const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int64_t b = g >> 5;
-    const int e = (int)(g & 31);
     if (b >= n_blocks) return;
-    const float v = x[g];
-    float amax = fabsf(v);
-#pragma unroll
-    for (int mask = 1; mask < 32; mask <<= 1) amax = fmaxf(amax, xor_f(amax, mask));
-    const float d = amax / 127.0f;
-    const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
-    uint8_t* yb = y + b * kQ80Bytes;
-    yb[2 + e] = (uint8_t)(int8_t)(int)__builtin_rintf(v * id);
-    if (e == 0) {
-        const uint16_t h = __builtin_bit_cast(uint16_t, (_Float16)d);
-        yb[0] = (uint8_t)(h & 0xFF);
-        yb[1] = (uint8_t)(h >> 8);
-    }
+    q8_0_lane_store(x[g], y + b * kQ80Bytes, (int)(g & 31));
 }
 
 void launch_quant_q8_0(const float* x, uint8_t* y, int64_t n_elements, hipStream_t s) {

@@ -28,3 +28,21 @@ def q8_0_bytes(rows: int, k: int) -> int:
 
 def q8k_bytes(rows: int, k: int) -> int:
     return rows * (k // Q8K_ELEMS) * Q8K_BYTES
+
+
+PAD64_BYTES = 64  # record {f16 d, 0, 0, i8 q[32], 28 zero bytes}
+
+
+def q8_0_rows_to_pad64(rows, n: int, k: int):
+    """Q8_0 rows [n][k/32][34] -> the padded layout [k/32][n][64] of
+    q8_pad64_coalesced (inference/llamatov_c_inference.py:88-100): a byte
+    relayout of the same (d, q) pairs, so a GGUF Q8_0 tensor feeds
+    generate_token without requantization."""
+    import numpy as np
+
+    nb = k // Q8_0_ELEMS
+    src = np.asarray(rows, dtype=np.uint8).reshape(n, nb, Q8_0_BYTES)
+    out = np.zeros((nb, n, PAD64_BYTES), np.uint8)
+    out[:, :, 0:2] = src[:, :, 0:2].transpose(1, 0, 2)
+    out[:, :, 4:36] = src[:, :, 2:34].transpose(1, 0, 2)
+    return out.reshape(-1)

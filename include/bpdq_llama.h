@@ -1,0 +1,148 @@
+/* bpdq_llama.h — the decode step of a llama-family model, part of
+ * libbpdq_hip.so (gfx950 / MI355X).
+ *
+ * The structs and generate_token() are the ABI the reference's GPU driver binds
+ * with ctypes (inference/llamatov_c_inference.py:15-83); the reference ships no
+ * source for the library behind it.  What one step computes is the reference's
+ * CPU transformer block, bpd_llama_block_cpu (bench/bpd_cpu.c:5611-5737), and the
+ * head of bpd_llama_forward_cpu (:5740-5798), for one token at `position`:
+ *
+ *   per layer: h = rmsnorm(x) * attn_norm            (bpd_rmsnorm_llama_cpu, :4959)
+ *              q, k, v = Wq h, Wk h, Wv h (+ bias)    (Q8_0 activations, tile order T)
+ *              q, k = rope_norm(q, k, position)       (bpd_rope_norm_freqs_cpu, :5146)
+ *              K/V cache[position] = k, v             (bpd_kv_cache_write_cpu, :5204)
+ *              a = softmax(q k^T / sqrt(D)) v          (bpd_gqa_attn_cpu, :5370)
+ *              x = x + Wo a
+ *              h = rmsnorm(x) * ffn_norm
+ *              x = x + Wdown (silu(Wgate h) * Wup h)  (bpd_swiglu_fuse_cpu, :5504)
+ *   then       logits = W_lm (rmsnorm(x) * out_norm),  token = argmax (:4512)
+ *
+ * With Q8_0 weights in the padded layout, every fp32 operation happens in the
+ * reference's order, including libm's expf, cosf and sinf, so logits and the
+ * token are bit-identical to the reference's CPU block built for AVX (whose
+ * Q8_0 product is the llamafile tile order).  Conditions: head_dim a multiple
+ * of 32 and at most 256, n_head a multiple of n_head_kv, n_embd = n_head *
+ * head_dim, every K a multiple of 32 (256 for Q4_K), n_embd <= 16384, and
+ * K/V cache rows [0, position) written by earlier steps and finite.
+ *
+ * Differences from the reference's block, by design:
+ *   - attention reads cache rows 0..position only; the reference scores all
+ *     max_seq rows and masks the rest to weight 0, which adds exact zeros when
+ *     those rows hold finite values;
+ *   - RoPE has no frequency factors (the ABI carries none) and rope_dim = head_dim;
+ *   - q/k/v biases (the qwen2 fields) are added to the projection before RoPE,
+ *     as in llama.cpp's qwen2 graph; the reference block has no biases.
+ * Calls run on the stream of bpd_gpu_set_stream() (include/bpdq.h); errors are
+ * recorded for bpd_gpu_last_error().  The library keeps one device workspace
+ * for the quantized activations: steps that overlap on different streams race.
+ */
+#ifndef BPDQ_LLAMA_H
+#define BPDQ_LLAMA_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* inference/llamatov_c_inference.py:15-31.  Weight pointers are device
+ * pointers.  X_K is the input width (reduction length) and X_N the number of
+ * output rows of matrix X: y[X_N] = W_X[X_N, X_K] h[X_K]. */
+typedef struct {
+    void* attn_norm; /* fp32 [n_embd] */
+    void* q;
+    void* k;
+    void* v;
+    void* o;
+    void* ffn_norm; /* fp32 [n_embd] */
+    void* gate;
+    void* up;
+    void* down;
+    int q_K, q_N, k_K, k_N, v_K, v_N, o_K, o_N;
+    int gate_K, gate_N, up_K, up_N, down_K, down_N;
+    void* q_bias; /* fp32 [q_N] or NULL */
+    void* k_bias; /* fp32 [k_N] or NULL */
+    void* v_bias; /* fp32 [v_N] or NULL */
+} LayerWeights;
+
+/* :33-43 */
+typedef struct {
+    int n_layers, n_embd, n_head, n_head_kv, head_dim, ff_dim, vocab_size, max_seq;
+    float eps, rope_theta;
+} ModelConfig;
+
+/* :45-51: two host arrays of n_layers device pointers, each to an fp32
+ * [max_seq][n_head_kv * head_dim] cache. */
+typedef struct {
+    void** k_cache;
+    void** v_cache;
+} KVCache;
+
+/* :53-59: device buffers, fp32 unless noted: x, h, q, attn_out, ffn [n_embd];
+ * k, v [n_head_kv * head_dim]; gate, up [ff_dim]; logits [lm_N];
+ * argmax_result: one int32.  After a step, x holds the residual stream after
+ * the last layer, h the final normed x, logits the head's output. */
+typedef struct {
+    void* x;
+    void* h;
+    void* q;
+    void* k;
+    void* v;
+    void* attn_out;
+    void* gate;
+    void* up;
+    void* ffn;
+    void* logits;
+    void* argmax_result;
+} WorkBuffers;
+
+/* :62-78.  One decode step.  `embedding` is the fp32 [n_embd] input row on the
+ * device; layer and head weights are in the padded Q8 layout of
+ * bpd_q8_pad64_from_f32_gpu (records [K/32][N][64]), or, with lm_head NULL,
+ * the head is lm_f32: fp32 [lm_N][lm_K] row-major.  Returns the argmax token
+ * (waits for the step to finish), or -1 after recording an error. */
+int generate_token(const LayerWeights* layers, const ModelConfig* cfg, const WorkBuffers* buf, const KVCache* kv,
+                   int position, const void* embedding, const void* output_norm_w, const void* lm_head,
+                   const void* lm_f32, int lm_K, int lm_N);
+
+/* :79-83.  gpu_alloc returns NULL on failure; copies are synchronous. */
+void* gpu_alloc(int bytes);
+void gpu_copy_h2d(void* dst_dev, const void* src_host, int bytes);
+void gpu_copy_d2h(void* dst_host, const void* src_dev, int bytes);
+void gpu_sync(void);
+/* No counterpart in the reference (its driver never frees). */
+void gpu_free(void* p);
+
+/* ---- the same step for other weight formats, enqueued without waiting ----
+ * No counterpart in the reference.  weight_format applies to the seven layer
+ * matrices and lm_head:
+ *   BPDQ_W_Q8_PAD64   the padded Q8 layout above (generate_token's format);
+ *   BPDQ_W_Q4K        Q4_K GGUF bytes [N][K/256][144], bpd element map;
+ *   BPDQ_W_Q4K_GGUF   Q4_K, GGUF (llama.cpp) element map.
+ * With Q4_K weights each GEMV is the Q4_K x Q8_K product with the activation
+ * quantized to Q8_K inside the kernel (bpd_qmatmul_q4k_q8k_fused_multi_gpu);
+ * Q/K/V and gate/up are single launches.  The token is left in
+ * buf->argmax_result; returns 0, or -1 after recording an error.  For HIP
+ * graph capture and timing loops. */
+#define BPDQ_W_Q8_PAD64 0
+#define BPDQ_W_Q4K 1
+#define BPDQ_W_Q4K_GGUF 2
+int bpd_llama_step_gpu(int weight_format, const LayerWeights* layers, const ModelConfig* cfg,
+                       const WorkBuffers* buf, const KVCache* kv, int position, const void* embedding,
+                       const void* output_norm_w, const void* lm_head, const void* lm_f32, int lm_K, int lm_N);
+
+/* ---- single steps of the decode step, for parity tests ----
+ * x_out = x_in (+ add); h = rmsnorm(x_out) * w; xq = Q8_0(h) when xq != NULL
+ * (bpd_rmsnorm_llama_cpu, bench/bpd_cpu.c:4959-4986, with the residual add of
+ * bpd_add_f32_cpu, :5466, in front).  The sum of squares is accumulated in
+ * binary64 as the reference does; when the parallel sum cannot prove that the
+ * reference's sequential binary64 sum rounds to the same fp32 mean, the kernel
+ * recomputes it sequentially. */
+void bpd_residual_rmsnorm_gpu(const float* x_in, const float* add, float* x_out, const float* w, float* h,
+                              uint8_t* xq, int n, float eps);
+/* expf of the decode step (the platform libm's, see bpdq_math.h) on n values. */
+void bpd_expf_gpu(const float* x, float* y, int n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -664,3 +664,272 @@ void bpdq_o_qmatmul_q6k_q8k_mt(const uint8_t* w, const uint8_t* xq, float* y, in
     p.kind = 3; p.a = w; p.b = xq; p.out = y; p.K = K; p.order = order;
     mt_launch(p, M, nthreads);
 }
+
+/* ==========================================================================
+ * The decode step.
+ * ========================================================================== */
+
+/* expf by the method the C library uses on x86-64 glibc with FMA (Szabolcs
+ * Nagy's table-driven expf, ARM optimized-routines math/expf.c): see
+ * bpd_substrate_amd/csrc/bpdq_math.h, whose device code runs the same steps. */
+static const uint64_t expf_tab[32] = {
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
+};
+
+void bpdq_o_expf_table(uint64_t* out) { memcpy(out, expf_tab, sizeof expf_tab); }
+
+float bpdq_o_expf_nagy(float x) {
+    const double N = 32.0, InvLn2N = 0x1.71547652b82fep+0 * N, Shift = 0x1.8p+52;
+    const double C0 = 0x1.c6af84b912394p-5 / (N * N * N), C1 = 0x1.ebfce50fac4f3p-3 / (N * N),
+                 C2 = 0x1.62e42ff0c52d6p-1 / N;
+    uint32_t ux;
+    memcpy(&ux, &x, 4);
+    const uint32_t abstop = (ux >> 20) & 0x7ffu;
+    if (abstop >= 0x42bu) {
+        if (ux == 0xff800000u) return 0.0f;
+        if (abstop >= 0x7f8u) return x + x;
+        if (x > 0x1.62e42ep6f) return INFINITY;
+        if (x < -0x1.9fe368p6f) return 0.0f;
+    }
+    const double xd = (double)x;
+    double kd = fma(InvLn2N, xd, Shift);
+    uint64_t ki;
+    memcpy(&ki, &kd, 8);
+    kd -= Shift;
+    const double r = fma(InvLn2N, xd, -kd);
+    const uint64_t t = expf_tab[ki & 31] + (ki << 47);
+    double s;
+    memcpy(&s, &t, 8);
+    const double z = fma(C0, r, C1);
+    const double r2 = r * r;
+    double y = fma(C2, r, 1.0);
+    y = fma(z, r2, y);
+    y = y * s;
+    return (float)y;
+}
+
+typedef struct {
+    uint32_t start, step;
+    uint64_t bad;
+    uint32_t first_bad;
+} expf_job;
+
+static float (*volatile libm_expf)(float) = expf;
+
+static void* expf_run(void* p) {
+    expf_job* j = (expf_job*)p;
+    for (uint64_t u = j->start; u <= 0xFFFFFFFFull; u += j->step) {
+        float x;
+        const uint32_t v = (uint32_t)u;
+        memcpy(&x, &v, 4);
+        if (x != x) continue;
+        const float a = libm_expf(x), b = bpdq_o_expf_nagy(x);
+        if (memcmp(&a, &b, 4) != 0) {
+            if (j->bad == 0) j->first_bad = v;
+            j->bad++;
+        }
+    }
+    return NULL;
+}
+
+uint64_t bpdq_o_expf_mismatches(int nthreads, uint32_t stride, uint32_t* first_bad) {
+    enum { MAXJ = 64 };
+    if (nthreads < 1) nthreads = 1;
+    if (nthreads > MAXJ) nthreads = MAXJ;
+    if (stride < 1) stride = 1;
+    expf_job jobs[MAXJ];
+    pthread_t th[MAXJ];
+    int ok[MAXJ];
+    for (int t = 0; t < nthreads; t++) {
+        jobs[t].start = (uint32_t)t * stride;
+        jobs[t].step = (uint32_t)nthreads * stride;
+        jobs[t].bad = 0;
+        jobs[t].first_bad = 0;
+        ok[t] = t > 0 && pthread_create(&th[t], NULL, expf_run, &jobs[t]) == 0;
+    }
+    for (int t = 1; t < nthreads; t++)
+        if (!ok[t]) expf_run(&jobs[t]);
+    expf_run(&jobs[0]);
+    uint64_t bad = 0;
+    *first_bad = 0;
+    for (int t = 0; t < nthreads; t++) {
+        if (ok[t]) pthread_join(th[t], NULL);
+        if (jobs[t].bad && !bad) *first_bad = jobs[t].first_bad;
+        bad += jobs[t].bad;
+    }
+    return bad;
+}
+
+void bpdq_o_libm_expf(const float* x, float* y, int n) {
+    for (int i = 0; i < n; i++) y[i] = libm_expf(x[i]);
+}
+
+/* bench/bpd_cpu.c:4959-4986 */
+void bpdq_o_rmsnorm(const float* x, const float* w, float* y, int n, float eps) {
+    double sum = 0.0;
+    for (int i = 0; i < n; i++) sum += (double)x[i] * (double)x[i];
+    const float mean = (float)(sum / n);
+    const float scale = 1.0f / sqrtf(mean + eps);
+    for (int i = 0; i < n; i++) y[i] = x[i] * scale * w[i];
+}
+
+/* bench/bpd_cpu.c:5146-5184 (NORM pairs), no frequency factors, n_dims = head_dim. */
+void bpdq_o_rope_norm(float* t, int n_heads, int head_dim, int pos, float base) {
+    const float theta_scale = powf(base, -2.0f / (float)head_dim);
+    for (int hh = 0; hh < n_heads; hh++) {
+        float* p = t + (size_t)hh * head_dim;
+        float theta = (float)pos;
+        for (int i0 = 0; i0 < head_dim; i0 += 2) {
+            const float c = cosf(theta), s = sinf(theta);
+            const float x0 = p[i0], x1 = p[i0 + 1];
+            p[i0] = x0 * c - x1 * s;
+            p[i0 + 1] = x0 * s + x1 * c;
+            theta *= theta_scale;
+        }
+    }
+}
+
+/* bench/bpd_cpu.c:5370-5440 for one query token at position pos, over all
+ * max_seq cache rows with the causal mask (rows > pos weigh exp(-1e38 - max)). */
+void bpdq_o_gqa_attn(const float* q, const float* kc, const float* vc, float* out, int max_seq, int pos, int H,
+                     int HKV, int D, float scale) {
+    const int grp = H / HKV, row = HKV * D;
+    float* sc = (float*)malloc(sizeof(float) * (size_t)max_seq);
+    for (int h = 0; h < H; h++) {
+        const int kvh = h / grp;
+        const float* pq = q + (size_t)h * D;
+        for (int j = 0; j < max_seq; j++) {
+            const float* pk = kc + (size_t)j * row + (size_t)kvh * D;
+            float s = 0.0f;
+            for (int d = 0; d < D; d++) s += pq[d] * pk[d];
+            sc[j] = s;
+        }
+        float mx = -1e38f;
+        for (int j = 0; j < max_seq; j++) {
+            const float sv = j <= pos ? sc[j] * scale : -1e38f;
+            sc[j] = sv;
+            if (sv > mx) mx = sv;
+        }
+        float sum = 0.0f;
+        for (int j = 0; j < max_seq; j++) {
+            const float e = expf(sc[j] - mx);
+            sc[j] = e;
+            sum += e;
+        }
+        const float inv = sum == 0.0f ? 0.0f : 1.0f / sum;
+        for (int j = 0; j < max_seq; j++) sc[j] *= inv;
+        float* o = out + (size_t)h * D;
+        for (int d = 0; d < D; d++) o[d] = 0.0f;
+        for (int j = 0; j < max_seq; j++) {
+            const float* pv = vc + (size_t)j * row + (size_t)kvh * D;
+            for (int d = 0; d < D; d++) o[d] += pv[d] * sc[j];
+        }
+    }
+    free(sc);
+}
+
+/* bench/bpd_cpu.c:5504-5507 */
+void bpdq_o_swiglu(const float* g, const float* u, float* y, int n) {
+    for (int i = 0; i < n; i++) y[i] = (g[i] / (1.0f + expf(-g[i]))) * u[i];
+}
+
+/* bench/bpd_cpu.c:4512-4526 */
+int bpdq_o_argmax(const float* x, int n) {
+    float best = x[0];
+    int bi = 0;
+    for (int k = 1; k < n; k++)
+        if (x[k] > best) {
+            best = x[k];
+            bi = k;
+        }
+    return bi;
+}
+
+/* The fp32 head of the decode step (no reference source): lane l of a 64-wide
+ * wave sums W[r][l + 64 i] * x[l + 64 i] over i, then xor-32..1 pair sums. */
+void bpdq_o_gemv_f32_wave(const float* W, const float* x, float* y, int N, int K) {
+    for (int r = 0; r < N; r++) {
+        float p[64];
+        for (int l = 0; l < 64; l++) {
+            float a = 0.0f;
+            for (int k = l; k < K; k += 64) a = a + W[(size_t)r * K + k] * x[k];
+            p[l] = a;
+        }
+        for (int m = 32; m >= 1; m >>= 1) {
+            float t[64];
+            for (int l = 0; l < 64; l++) t[l] = p[l] + p[l ^ m];
+            memcpy(p, t, sizeof p);
+        }
+        y[r] = p[0];
+    }
+}
+
+/* y[N] = W[N][K] a[K] in the step's weight format. */
+static void step_gemv(int fmt, const uint8_t* W, const float* a, float* y, int N, int K) {
+    if (fmt == 0) {
+        uint8_t* aq = (uint8_t*)malloc((size_t)(K / 32) * 34);
+        bpdq_o_quant_q8_0(a, aq, K);
+        bpdq_o_dispatch_q8_0(W, aq, y, N, 1, K, 'T');
+        free(aq);
+    } else {
+        uint8_t* aq = (uint8_t*)malloc((size_t)(K / 256) * 292);
+        bpdq_o_quant_q8_k(a, aq, K);
+        bpdq_o_qmatmul_q4k_q8k(W, aq, y, N, K, fmt == 2 ? 1 : 0);
+        free(aq);
+    }
+}
+
+/* The composition of bpd_llama_block_cpu (bench/bpd_cpu.c:5611-5737) over the
+ * layers and the head of bpd_llama_forward_cpu (:5779-5792) for one token. */
+int bpdq_o_llama_step(int fmt, const bpdq_o_layer* layers, const bpdq_o_cfg* cfg, float* const* k_cache,
+                      float* const* v_cache, int pos, const float* emb, const float* out_norm, const uint8_t* lm,
+                      const float* lm_f32, int lm_N, float* x, float* h, float* logits) {
+    const int E = cfg->n_embd, H = cfg->n_head, HKV = cfg->n_head_kv, D = cfg->head_dim, F = cfg->ff_dim;
+    const int row = HKV * D;
+    float* q = (float*)malloc(sizeof(float) * (size_t)H * D);
+    float* k = (float*)malloc(sizeof(float) * (size_t)row);
+    float* v = (float*)malloc(sizeof(float) * (size_t)row);
+    float* att = (float*)malloc(sizeof(float) * (size_t)H * D);
+    float* t = (float*)malloc(sizeof(float) * (size_t)E);
+    float* g = (float*)malloc(sizeof(float) * (size_t)F);
+    float* u = (float*)malloc(sizeof(float) * (size_t)F);
+    memcpy(x, emb, sizeof(float) * (size_t)E);
+    const float scale = 1.0f / sqrtf((float)D);
+    for (int l = 0; l < cfg->n_layers; l++) {
+        const bpdq_o_layer* w = &layers[l];
+        bpdq_o_rmsnorm(x, w->attn_norm, h, E, cfg->eps);
+        step_gemv(fmt, w->q, h, q, H * D, E);
+        step_gemv(fmt, w->k, h, k, row, E);
+        step_gemv(fmt, w->v, h, v, row, E);
+        if (w->q_bias) for (int i = 0; i < H * D; i++) q[i] = q[i] + w->q_bias[i];
+        if (w->k_bias) for (int i = 0; i < row; i++) k[i] = k[i] + w->k_bias[i];
+        if (w->v_bias) for (int i = 0; i < row; i++) v[i] = v[i] + w->v_bias[i];
+        bpdq_o_rope_norm(q, H, D, pos, cfg->rope_theta);
+        bpdq_o_rope_norm(k, HKV, D, pos, cfg->rope_theta);
+        memcpy(k_cache[l] + (size_t)pos * row, k, sizeof(float) * (size_t)row);
+        memcpy(v_cache[l] + (size_t)pos * row, v, sizeof(float) * (size_t)row);
+        bpdq_o_gqa_attn(q, k_cache[l], v_cache[l], att, cfg->max_seq, pos, H, HKV, D, scale);
+        step_gemv(fmt, w->o, att, t, E, H * D);
+        for (int i = 0; i < E; i++) x[i] = x[i] + t[i];
+        bpdq_o_rmsnorm(x, w->ffn_norm, h, E, cfg->eps);
+        step_gemv(fmt, w->gate, h, g, F, E);
+        step_gemv(fmt, w->up, h, u, F, E);
+        bpdq_o_swiglu(g, u, g, F);
+        step_gemv(fmt, w->down, g, t, E, F);
+        for (int i = 0; i < E; i++) x[i] = x[i] + t[i];
+    }
+    bpdq_o_rmsnorm(x, out_norm, h, E, cfg->eps);
+    if (lm)
+        step_gemv(fmt, lm, h, logits, lm_N, E);
+    else
+        bpdq_o_gemv_f32_wave(lm_f32, h, logits, lm_N, E);
+    free(q); free(k); free(v); free(att); free(t); free(g); free(u);
+    return bpdq_o_argmax(logits, lm_N);
+}

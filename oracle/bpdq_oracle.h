@@ -56,6 +56,36 @@ void bpdq_o_qmatmul_q8_0(const uint8_t* W, const float* X, float* out, int M, in
 /* order: 'T' (AVX1 build) or 'S' (scalar build redirect, bench/bpd_cpu.c:4455-4458). */
 void bpdq_o_qmatmul_q8_0_llamafile(const uint8_t* W, const float* X, float* out, int m_weight, int m_tokens, int K, int order); /* :4429-4452 */
 
+/* ---- the decode step (bench/bpd_cpu.c:5611-5798) ---- */
+/* expf by glibc's method (ARM optimized-routines expf, FMA variant); the table it uses. */
+float bpdq_o_expf_nagy(float x);
+void bpdq_o_expf_table(uint64_t* out32);
+/* Inputs u = k*stride (k >= 0, u < 2^32, not NaN) where bpdq_o_expf_nagy and libm's expf differ. */
+uint64_t bpdq_o_expf_mismatches(int nthreads, uint32_t stride, uint32_t* first_bad);
+void bpdq_o_libm_expf(const float* x, float* y, int n);
+void bpdq_o_rmsnorm(const float* x, const float* w, float* y, int n, float eps);           /* :4959-4986 */
+void bpdq_o_rope_norm(float* t, int n_heads, int head_dim, int pos, float base);          /* :5146-5184 */
+void bpdq_o_gqa_attn(const float* q, const float* kc, const float* vc, float* out, int max_seq, int pos, int H,
+                     int HKV, int D, float scale);                                        /* :5370-5440 */
+void bpdq_o_swiglu(const float* g, const float* u, float* y, int n);                      /* :5504-5507 */
+int bpdq_o_argmax(const float* x, int n);                                                 /* :4512-4526 */
+void bpdq_o_gemv_f32_wave(const float* W, const float* x, float* y, int N, int K);
+typedef struct {
+    const float* attn_norm;
+    const uint8_t *q, *k, *v, *o;
+    const float* ffn_norm;
+    const uint8_t *gate, *up, *down;
+    const float *q_bias, *k_bias, *v_bias;
+} bpdq_o_layer;
+typedef struct {
+    int n_layers, n_embd, n_head, n_head_kv, head_dim, ff_dim, max_seq;
+    float eps, rope_theta;
+} bpdq_o_cfg;
+/* fmt 0: Q8_0 rows, tile order T; 1 / 2: Q4_K (bpd / GGUF map) x Q8_K.  lm NULL: lm_f32 head. */
+int bpdq_o_llama_step(int fmt, const bpdq_o_layer* layers, const bpdq_o_cfg* cfg, float* const* k_cache,
+                      float* const* v_cache, int pos, const float* emb, const float* out_norm, const uint8_t* lm,
+                      const float* lm_f32, int lm_N, float* x, float* h, float* logits);
+
 /* Row-range parallel wrappers for the CPU baseline: every row's bits are those of
  * the single-threaded function. */
 void bpdq_o_dequant_q4k_mt(const uint8_t* q, float* out, int n_blocks, int nthreads);

@@ -52,6 +52,17 @@ _SIGS = {
     "bpdq_o_dequant_q4k_mt": (None, [P, P, I, I]),
     "bpdq_o_qmatmul_q4k_q8k_mt": (None, [P, P, P, I, I, I, I]),
     "bpdq_o_dispatch_q8_0_mt": (None, [P, P, P, I, I, I, I, I]),
+    "bpdq_o_expf_nagy": (F, [F]),
+    "bpdq_o_expf_table": (None, [P]),
+    "bpdq_o_expf_mismatches": (ctypes.c_uint64, [I, ctypes.c_uint32, P]),
+    "bpdq_o_libm_expf": (None, [P, P, I]),
+    "bpdq_o_rmsnorm": (None, [P, P, P, I, F]),
+    "bpdq_o_rope_norm": (None, [P, I, I, I, F]),
+    "bpdq_o_gqa_attn": (None, [P, P, P, P, I, I, I, I, I, F]),
+    "bpdq_o_swiglu": (None, [P, P, P, I]),
+    "bpdq_o_argmax": (I, [P, I]),
+    "bpdq_o_gemv_f32_wave": (None, [P, P, P, I, I]),
+    "bpdq_o_llama_step": (I, [I, P, P, P, P, I, P, P, P, P, I, P, P, P]),
 }
 
 _lib = None
@@ -210,3 +221,148 @@ def dequant_q4k_mt(q, nthreads):
     out = np.empty(nb * 256, np.float32)
     lib().bpdq_o_dequant_q4k_mt(_p(q), _p(out), nb, nthreads)
     return out
+
+
+# ------------------------------------------------------------------ the decode step
+
+def expf_nagy(x):
+    return np.float32(lib().bpdq_o_expf_nagy(float(np.float32(x))))
+
+
+def expf_table():
+    t = np.empty(32, np.uint64)
+    lib().bpdq_o_expf_table(_p(t))
+    return t
+
+
+def expf_mismatches(nthreads=8, stride=1):
+    """(count, first input bits) of non-NaN inputs k*stride where the restated
+    expf and libm's differ."""
+    first = ctypes.c_uint32()
+    n = lib().bpdq_o_expf_mismatches(nthreads, stride, ctypes.addressof(first))
+    return n, first.value
+
+
+def libm_expf(x):
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    lib().bpdq_o_libm_expf(_p(x), _p(y), x.size)
+    return y
+
+
+def rmsnorm(x, w, eps):
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    lib().bpdq_o_rmsnorm(_p(x), _p(np.ascontiguousarray(w, np.float32)), _p(y), x.size, eps)
+    return y
+
+
+def rope_norm(t, n_heads, head_dim, pos, base):
+    t = np.array(t, np.float32)
+    lib().bpdq_o_rope_norm(_p(t), n_heads, head_dim, pos, base)
+    return t
+
+
+def gqa_attn(q, kc, vc, max_seq, pos, H, HKV, D, scale):
+    out = np.empty(H * D, np.float32)
+    lib().bpdq_o_gqa_attn(_p(q), _p(kc), _p(vc), _p(out), max_seq, pos, H, HKV, D, scale)
+    return out
+
+
+def swiglu(g, u):
+    y = np.empty_like(g)
+    lib().bpdq_o_swiglu(_p(g), _p(u), _p(y), g.size)
+    return y
+
+
+def argmax(x):
+    return lib().bpdq_o_argmax(_p(np.ascontiguousarray(x, np.float32)), x.size)
+
+
+def gemv_f32_wave(W, x, N, K):
+    y = np.empty(N, np.float32)
+    lib().bpdq_o_gemv_f32_wave(_p(W), _p(x), _p(y), N, K)
+    return y
+
+
+class _OLayer(ctypes.Structure):
+    _fields_ = [(n, P) for n in ("attn_norm", "q", "k", "v", "o", "ffn_norm", "gate", "up", "down",
+                                 "q_bias", "k_bias", "v_bias")]
+
+
+class _OCfg(ctypes.Structure):
+    _fields_ = [(n, I) for n in ("n_layers", "n_embd", "n_head", "n_head_kv", "head_dim", "ff_dim", "max_seq")] + \
+        [("eps", F), ("rope_theta", F)]
+
+
+def _addr(a):
+    return None if a is None else a.ctypes.data
+
+
+def llama_step(fmt, layers, cfg, k_cache, v_cache, pos, emb, out_norm, lm, lm_f32, lm_N):
+    """One decode step of the restatement (bpdq_o_llama_step).  layers: dicts of
+    numpy arrays (Q8_0 rows for fmt 0, Q4_K for 1/2); k_cache, v_cache: lists
+    of fp32 [max_seq * HKV * D] arrays, updated in place.
+    Returns (token, x, h, logits)."""
+    E = cfg["n_embd"]
+    arr = (_OLayer * max(1, len(layers)))()
+    for i, lw in enumerate(layers):
+        for n, _ in _OLayer._fields_:
+            setattr(arr[i], n, _addr(lw.get(n)))
+    c = _OCfg(*(cfg[n] for n, _ in _OCfg._fields_))
+    kp = (P * max(1, len(k_cache)))(*[_p(t) for t in k_cache])
+    vp = (P * max(1, len(v_cache)))(*[_p(t) for t in v_cache])
+    x, h, logits = np.empty(E, np.float32), np.empty(E, np.float32), np.empty(lm_N, np.float32)
+    tok = lib().bpdq_o_llama_step(fmt, ctypes.addressof(arr), ctypes.addressof(c), kp, vp, pos, _p(emb),
+                                  _p(out_norm), _addr(lm), _addr(lm_f32), lm_N, _p(x), _p(h), _p(logits))
+    return tok, x, h, logits
+
+
+# The reference's own block, compiled from bench/bpd_cpu.c into oracle/_ref.
+class RefLlamaConfig(ctypes.Structure):      # bench/bpd_cpu.c:5556-5570
+    _fields_ = [(n, I) for n in ("n_layers", "n_heads", "n_kv_heads", "head_dim", "embed_dim", "ffn_dim",
+                                 "vocab_size", "max_seq_len")] + \
+        [("rms_eps", F), ("rope_base", F), ("rope_dim", I), ("kv_cache_f16", I)]
+
+
+class RefLayerWeights(ctypes.Structure):     # bench/bpd_cpu.c:5585-5595
+    _fields_ = [(n, P) for n in ("attn_norm_w", "w_q", "w_k", "w_v", "w_o", "ffn_norm_w", "w_gate", "w_up",
+                                 "w_down")]
+
+
+def ref_llama_step(layers, cfg, k_cache, v_cache, pos, emb, out_norm, lm, lm_N, kind="avx"):
+    """One token through the reference's bpd_llama_block_cpu per layer
+    (bench/bpd_cpu.c:5611-5737), then the head of bpd_llama_forward_cpu
+    (:5779-5792: bpd_rmsnorm_llama_cpu, bpd_qmatmul_q8_0_llamafile_cpu,
+    bpd_argmax_dim_cpu), with an fp32 cache per layer.  (The forward itself
+    steps its per-layer cache pointer in uint16_t units, :5771-5773, which
+    overlaps fp32 layers; the composition here gives each layer its own.)
+    Returns (token, x, h, logits), or None if oracle/_ref is not built."""
+    R = ref(kind)
+    if R is None:
+        return None
+    for name, args in (("bpd_llama_block_cpu", [P, P, P, P, I, I, P, P, P, P, P, P]),
+                       ("bpd_rmsnorm_llama_cpu", [P, P, P, I, I, F]),
+                       ("bpd_qmatmul_q8_0_llamafile_cpu", [P, P, P, I, I, I]),
+                       ("bpd_argmax_dim_cpu", [P, P, I, I, I])):
+        f = getattr(R, name)
+        f.argtypes, f.restype = args, None
+    E, H, HKV, D, F_ = (cfg[n] for n in ("n_embd", "n_head", "n_head_kv", "head_dim", "ff_dim"))
+    c = RefLlamaConfig(cfg["n_layers"], H, HKV, D, E, F_, lm_N, cfg["max_seq"], cfg["eps"], cfg["rope_theta"],
+                       D, 0)
+    x = np.array(emb, np.float32)
+    big = max(E, F_, H * D)
+    s1, s2, s3 = (np.zeros(big, np.float32) for _ in range(3))
+    pos_ids = np.array([pos], np.int32)
+    for l, lw in enumerate(layers):
+        w = RefLayerWeights(*(_addr(lw[n]) for n in ("attn_norm", "q", "k", "v", "o", "ffn_norm", "gate", "up",
+                                                     "down")))
+        R.bpd_llama_block_cpu(_p(x), ctypes.addressof(w), ctypes.addressof(c), _p(pos_ids), 1, pos, _p(k_cache[l]),
+                              _p(v_cache[l]), _p(s1), _p(s2), _p(s3), None)
+    h = np.empty(E, np.float32)
+    R.bpd_rmsnorm_llama_cpu(_p(x), _p(out_norm), _p(h), 1, E, cfg["eps"])
+    logits = np.empty(lm_N, np.float32)
+    R.bpd_qmatmul_q8_0_llamafile_cpu(_p(lm), _p(h), _p(logits), lm_N, 1, E)
+    tok = np.zeros(1, np.int64)
+    R.bpd_argmax_dim_cpu(_p(logits), _p(tok), 1, lm_N, 1)
+    return int(tok[0]), x, h, logits

@@ -23,7 +23,8 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
 def header_functions():
-    src = open(os.path.join(ROOT, "include", "bpdq.h")).read()
+    inc = os.path.join(ROOT, "include")
+    src = "".join(open(os.path.join(inc, f)).read() for f in sorted(os.listdir(inc)) if f.endswith(".h"))
     src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
     names = re.findall(r"^\s*(?:const\s+)?[A-Za-z_][\w\s\*]*?\b([a-z_][a-z0-9_]*)\s*\(", src, flags=re.M)
     return sorted(set(n for n in names if n not in ("defined",)))
@@ -145,3 +146,50 @@ def test_synth_distributions_match_configs():
 def test_bench_refuses_multi_gpu():
     r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True, text=True)
     assert r.returncode == 2 and "one GPU" in r.stderr
+
+
+def test_decode_step_validation_before_launch():
+    """generate_token / bpd_llama_step_gpu reject bad structs before any HIP call."""
+    import ctypes
+
+    from bpd_substrate_amd import llama
+
+    L = _native.load_hip()
+    L.bpd_gpu_last_error()
+    assert L.generate_token(None, None, None, None, 0, None, None, None, None, 64, 100) == -1
+    assert "cfg is NULL" in _err(1)
+    cfg = llama.ModelConfig(1, 256, 4, 2, 64, 512, 100, 64, 1e-5, 10000.0)
+    bufs = llama.WorkBuffers(*[0x10000 * (i + 1) for i in range(11)])
+    a = (ctypes.addressof(cfg), ctypes.addressof(bufs))
+    for field, val, text in (("head_dim", 48, "head_dim"), ("n_head_kv", 3, "n_head_kv"), ("max_seq", 0, "max_seq"),
+                             ("n_embd", 320, "n_embd")):
+        old = getattr(cfg, field)
+        setattr(cfg, field, val)
+        assert L.generate_token(None, a[0], a[1], None, 0, 0x1000, 0x2000, 0x3000, None, 256, 100) == -1
+        assert text in _err(2)
+        setattr(cfg, field, old)
+    assert L.generate_token(None, a[0], a[1], None, 64, 0x1000, 0x2000, 0x3000, None, 256, 100) == -1
+    assert "position" in _err(2)
+    assert L.generate_token(None, a[0], a[1], None, 0, 0x1000, 0x2000, None, None, 256, 100) == -1
+    assert "lm_f32" in _err(1)
+    bufs.k = 0x10004
+    assert L.generate_token(None, a[0], a[1], None, 0, 0x1000, 0x2000, 0x3000, None, 256, 100) == -1
+    assert "buf.k is not 16-byte aligned" in _err(3)
+    bufs.k = 0x20000
+    assert L.generate_token(None, a[0], a[1], None, 0, 0x1000, 0x2000, 0x3000, None, 256, 100) == -1
+    assert "layers is NULL" in _err(1)
+    lw = (llama.LayerWeights * 1)()
+    kp = (ctypes.c_void_p * 1)(0x40000)
+    kv = llama.KVCache(ctypes.cast(kp, ctypes.POINTER(ctypes.c_void_p)), ctypes.cast(kp, ctypes.POINTER(ctypes.c_void_p)))
+    assert L.generate_token(ctypes.addressof(lw), a[0], a[1], ctypes.addressof(kv), 0, 0x1000, 0x2000, 0x3000, None,
+                            256, 100) == -1
+    assert "layer 0 q is 0 x 0" in _err(2)
+    assert L.bpd_llama_step_gpu(7, None, a[0], a[1], None, 0, 0x1000, 0x2000, 0x3000, None, 256, 100) == -1
+    assert "weight_format" in _err(2)
+    cfg.n_embd, cfg.n_head = 256, 4
+    assert L.bpd_llama_step_gpu(llama.W_Q4K, None, a[0], a[1], None, 0, 0x1000, 0x2000, 0x3000, None, 256, 100) == -1
+    assert "ff_dim" not in _err(1)
+    L.bpd_residual_rmsnorm_gpu(0x1000, None, None, 0x2000, None, None, 48, 1e-5)
+    assert "multiple of 32" in _err(2)
+    assert L.gpu_alloc(-1) is None
+    _err(2)

@@ -1,0 +1,157 @@
+"""GPU parity of the decode step (include/bpdq_llama.h) through the C ABI.
+
+* bpd_expf_gpu equals libm's expf on a strided sweep of all binary32 inputs;
+* bpd_residual_rmsnorm_gpu equals the reference's rmsnorm (and the Q8_0
+  quantizer) bit-for-bit, including the input whose parallel sum disagrees
+  with the sequential one;
+* generate_token, with Q8_0 weights in the padded layout, equals the
+  reference's own bpd_llama_block_cpu composition from oracle/_ref bit-for-bit
+  (token, logits, x, h, K/V caches) step after step, for several GQA shapes;
+* the fp32 head, q/k/v biases, long contexts and the Q4_K formats equal the
+  restatement bpdq_o_llama_step bit-for-bit.
+Bar: bit-exact everywhere.
+"""
+import numpy as np
+import pytest
+import torch
+
+import llama_model as LM
+from bpd_substrate_amd import gpu, llama
+from helpers import assert_bits_equal, to_np
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _d(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def test_expf_sweep(dev):
+    u = np.arange(0, 2 ** 32, 251, dtype=np.uint64).astype(np.uint32)
+    x = u.view(np.float32)
+    x = x[~np.isnan(x)]
+    want = O.libm_expf(x)
+    y = torch.empty(x.size, dtype=torch.float32, device=dev)
+    gpu._use_torch_stream()
+    gpu.call("bpd_expf_gpu", _d(x, dev), y, x.size)
+    assert_bits_equal(to_np(y), want, "expf")
+
+
+def _norm(dev, x, add, w, eps, with_q):
+    n = x.size
+    xo = torch.empty(n, dtype=torch.float32, device=dev)
+    h = torch.empty(n, dtype=torch.float32, device=dev)
+    xq = torch.empty(n // 32 * 34, dtype=torch.uint8, device=dev) if with_q else None
+    gpu._use_torch_stream()
+    gpu.call("bpd_residual_rmsnorm_gpu", _d(x, dev), None if add is None else _d(add, dev), xo, _d(w, dev), h, xq,
+             n, float(eps))
+    torch.cuda.synchronize()
+    return to_np(xo), to_np(h), None if xq is None else to_np(xq)
+
+
+@pytest.mark.parametrize("n", [32, 64, 1024, 4096, 14336, 16384])
+def test_residual_rmsnorm(dev, n):
+    x = LM.synth.normal_f32(n, LM.synth.key(21, n)) * 2.0
+    a = LM.synth.normal_f32(n, LM.synth.key(22, n))
+    w = LM._norm_w(n, LM.synth.key(23, n))
+    xo, h, xq = _norm(dev, x, a, w, 1e-5, True)
+    s = x + a
+    assert_bits_equal(xo, s, "residual")
+    want = O.rmsnorm(s, w, 1e-5)
+    assert_bits_equal(h, want, f"rmsnorm n={n}")
+    assert np.array_equal(xq, O.quant_q8_0(want)), "Q8_0 of the normed row"
+
+
+def test_rmsnorm_sequential_fallback(dev):
+    from test_oracle_llama import rmsnorm_hard_case
+
+    x = rmsnorm_hard_case()
+    for w in (np.ones(64, np.float32), LM._norm_w(64, LM.synth.key(24, 1))):
+        _, h, _ = _norm(dev, x, None, w, 0.0, False)
+        assert_bits_equal(h, O.rmsnorm(x, w, 0.0), "rmsnorm hard case")
+    # the same case inside a long row, several times over
+    big = np.tile(x, 64)
+    w = LM._norm_w(big.size, LM.synth.key(24, 2))
+    _, h, _ = _norm(dev, big, None, w, 1e-6, False)
+    assert_bits_equal(h, O.rmsnorm(big, w, 1e-6), "rmsnorm hard case x64")
+
+
+def _gpu_model(cfg, layers, head, fmt, dev):
+    dl, on, lm, lmf = LM.to_device(cfg, layers, head, fmt, dev)
+    return llama.DecodeModel(cfg, dl, on, lm_head=lm, lm_f32=lmf, fmt=fmt, device=dev)
+
+
+def _check_step(m, got_tok, want, l_caches, pos, what):
+    tok, x, h, logits = want
+    assert got_tok == tok, f"{what}: token {got_tok} != {tok} at position {pos}"
+    assert_bits_equal(to_np(m.buf_t["logits"]), logits, f"{what} logits at {pos}")
+    assert_bits_equal(to_np(m.buf_t["x"]), x, f"{what} x at {pos}")
+    assert_bits_equal(to_np(m.buf_t["h"]), h, f"{what} h at {pos}")
+    kc, vc = l_caches
+    for l in range(len(kc)):
+        assert_bits_equal(to_np(m.k_cache[l]), kc[l], f"{what} K cache layer {l}")
+        assert_bits_equal(to_np(m.v_cache[l]), vc[l], f"{what} V cache layer {l}")
+
+
+@pytest.mark.parametrize("shape", [dict(), dict(H=8, HKV=8, D=32), dict(H=4, HKV=1, D=128, E=512, F=256),
+                                   dict(H=2, HKV=1, D=256, E=512, F=1024, L=3)])
+def test_generate_token_equals_reference_block(dev, shape):
+    cfg = LM.config(**shape)
+    layers, head = LM.make(cfg, 0, seed=3)
+    m = _gpu_model(cfg, layers, head, llama.W_Q8_PAD64, dev)
+    kr, vr = LM.caches(cfg)
+    for pos, e in enumerate(LM.embeddings(cfg, 6)):
+        print(f"generate_token {shape} position {pos}", flush=True)
+        want = O.ref_llama_step(layers, cfg, kr, vr, pos, e, head["out_norm"], head["lm"], cfg["vocab_size"])
+        if want is None:
+            pytest.skip("oracle/_ref not built")
+        tok = m.step(_d(e, dev), pos)
+        _check_step(m, tok, want, (kr, vr), pos, "generate_token")
+
+
+@pytest.mark.parametrize("fmt", [llama.W_Q8_PAD64, llama.W_Q4K, llama.W_Q4K_GGUF])
+@pytest.mark.parametrize("variant", ["plain", "bias", "f32_head"])
+def test_step_equals_restatement(dev, fmt, variant):
+    cfg = LM.config(L=2)
+    layers, head = LM.make(cfg, fmt, seed=4, bias=variant == "bias", f32_head=variant == "f32_head")
+    m = _gpu_model(cfg, layers, head, fmt, dev)
+    ko, vo = LM.caches(cfg)
+    for pos, e in enumerate(LM.embeddings(cfg, 4, seed=8)):
+        print(f"step fmt={fmt} {variant} position {pos}", flush=True)
+        want = O.llama_step(fmt, layers, cfg, ko, vo, pos, e, head["out_norm"], head["lm"], head["lm_f32"],
+                            cfg["vocab_size"])
+        tok = m.step(_d(e, dev), pos)
+        _check_step(m, tok, want, (ko, vo), pos, f"fmt {fmt} {variant}")
+
+
+@pytest.mark.parametrize("pos", [255, 2047])
+def test_long_context(dev, pos):
+    """Rows 0..pos-1 of the caches hold the same random finite data on both
+    sides; one step at `pos` then attends over pos+1 rows."""
+    cfg = LM.config(L=1, max_seq=2048, E=256, H=4, HKV=2, D=64)
+    layers, head = LM.make(cfg, 0, seed=5)
+    m = _gpu_model(cfg, layers, head, llama.W_Q8_PAD64, dev)
+    ko, vo = LM.caches(cfg)
+    row = cfg["n_head_kv"] * cfg["head_dim"]
+    for l in range(cfg["n_layers"]):
+        ko[l][:pos * row] = LM.synth.normal_f32(pos * row, LM.synth.key(31, l))
+        vo[l][:pos * row] = LM.synth.normal_f32(pos * row, LM.synth.key(32, l))
+        m.k_cache[l].copy_(_d(ko[l], dev))
+        m.v_cache[l].copy_(_d(vo[l], dev))
+    e = LM.embeddings(cfg, 1, seed=9)[0]
+    want = O.llama_step(0, layers, cfg, ko, vo, pos, e, head["out_norm"], head["lm"], None, cfg["vocab_size"])
+    tok = m.step(_d(e, dev), pos)
+    _check_step(m, tok, want, (ko, vo), pos, "long context")
+
+
+def test_rejects_bad_config(dev):
+    cfg = LM.config()
+    layers, head = LM.make(cfg, 0, seed=6)
+    m = _gpu_model(cfg, layers, head, llama.W_Q8_PAD64, dev)
+    e = _d(LM.embeddings(cfg, 1)[0], dev)
+    with pytest.raises(gpu.BpdqError, match="position"):
+        m.step(e, cfg["max_seq"])
+    m.layers[1].down_N = 128
+    with pytest.raises(gpu.BpdqError, match="layer 1 down"):
+        m.step(e, 0)
