@@ -132,12 +132,12 @@ def cpu_baseline(w_host, x_host, seconds):
                       f"GPU metric with fp32 x"}, y
 
 
-def decode_chain(torch, L, T, dev, gpu, synth, n_layers=32, tokens=10):
-    """BASELINE cfg3: the GEMV portion of a 32-layer Mistral-7B-shaped decode step,
-    Q4_K weights (each tensor its own seed), activations N(0,1) -> Q8_K."""
+def cfg3_layers(torch, dev, synth, n_layers=32):
+    """Q4_K weights of a 32-layer Mistral-7B-shaped model (each tensor its own
+    seed) and N(0,1) activations for the GEMV chain."""
     from bpd_substrate_amd import decode
 
-    log(f"decode chain: generating {n_layers} layers of Q4_K weights")
+    log(f"cfg3: generating {n_layers} layers of Q4_K weights")
     d = decode.Dims()
     e, kv, ff = d.n_embd, d.n_kv, d.ff
     layers, acts = [], []
@@ -148,6 +148,16 @@ def decode_chain(torch, L, T, dev, gpu, synth, n_layers=32, tokens=10):
                                              for t, (n, (m, kk)) in enumerate(shapes.items())}))
         acts.append([torch.from_numpy(synth.normal_f32(n, synth.key(43, 10 * i + j))).to(dev)
                      for j, n in enumerate((e, e, e, ff))])
+    return layers, acts
+
+
+def decode_chain(torch, L, T, dev, gpu, layers, acts, tokens=10):
+    """BASELINE cfg3: the GEMV portion of a 32-layer Mistral-7B-shaped decode step,
+    Q4_K weights, activations N(0,1) -> Q8_K."""
+    from bpd_substrate_amd import decode
+
+    d = decode.Dims()
+    n_layers = len(layers)
     out = {}
     for fused in (True, False):
         chain = decode.GemvChain(layers, d, dev, fused=fused)
@@ -169,7 +179,46 @@ def decode_chain(torch, L, T, dev, gpu, synth, n_layers=32, tokens=10):
         else:
             out["separate_quant_launches"] = {k: r[k] for k in ("us_per_token", "tokens_per_s", "launches_per_token")}
         del chain
-    del layers, acts
+    return out
+
+
+def decode_step(torch, L, T, dev, gpu, synth, layers, tokens=10, max_seq=4096, vocab=32000):
+    """BASELINE cfg3 as a whole decode step (bpd_llama_step_gpu): the chain's
+    Q4_K weights plus RMSNorm, RoPE, the fp32 K/V cache, GQA attention,
+    SwiGLU, a Q4_K head of `vocab` rows and argmax, one token at a time.
+    Timed at short context (positions 0..tokens-1) and after 2048 cached rows."""
+    from bpd_substrate_amd import llama
+
+    E, H, HKV, D, F = 4096, 32, 8, 128, 14336
+    cfg = dict(n_layers=len(layers), n_embd=E, n_head=H, n_head_kv=HKV, head_dim=D, ff_dim=F, vocab_size=vocab,
+               max_seq=max_seq, eps=1e-5, rope_theta=1e6)
+    norm = lambda t: torch.from_numpy(1.0 + 0.1 * synth.normal_f32(E, synth.key(44, t))).to(dev)
+    dl = [dict(attn_norm=norm(2 * i), ffn_norm=norm(2 * i + 1), **{n: getattr(lw, n) for n in llama.MATRICES})
+          for i, lw in enumerate(layers)]
+    lm = torch.from_numpy(synth.q4k(vocab, E, synth.key(44, 999))).to(dev)
+    m = llama.DecodeModel(cfg, dl, norm(998), lm_head=lm, fmt=llama.W_Q4K, device=dev)
+    embs = [torch.from_numpy(synth.normal_f32(E, synth.key(45, t))).to(dev) for t in range(tokens)]
+    with torch.cuda.stream(T.stream):
+        m.step(embs[0], 0)  # allocates the step workspace before any capture
+    torch.cuda.synchronize()
+    gpu.check()
+    wb = sum(t.numel() for lw in layers for t in (getattr(lw, n) for n in llama.MATRICES)) + lm.numel()
+    out = {"weight_bytes": wb, "vocab": vocab, "max_seq": max_seq, "launches_per_token": 9 * len(layers) + 3}
+    for pos0 in (0, 2048):
+        us = T.us_per_launch([(lambda t=t: m.enqueue(embs[t], pos0 + t)) for t in range(tokens)])
+        gpu.check()
+        out[f"pos{pos0}"] = {"us_per_token": round(us, 1), "tokens_per_s": round(1e6 / us, 1),
+                             "weight_gb_s": round(wb / us / 1e3, 1),
+                             "frac_hbm": round(wb / us / 1e3 / HBM_PEAK_GBS, 4)}
+    # the reference driver's pattern: one synchronous generate-style call per token, no graph
+    with torch.cuda.stream(T.stream):
+        t0 = time.perf_counter()
+        for t in range(tokens):
+            m.step(embs[t], t)
+        eager = (time.perf_counter() - t0) / tokens * 1e6
+    out["eager_sync_us_per_token"] = round(eager, 1)
+    out["roofline_us_per_token"] = round(wb / HBM_PEAK_GBS / 1e3, 1)
+    del m, dl, lm
     return out
 
 
@@ -299,7 +348,10 @@ def main():
                                        "order": "scalar S, bit-exact vs the -O2 reference build"}
         del W, X, Xq, out
         gpu.check()
-        result["decode_cfg3"] = decode_chain(torch, L, T, dev, gpu, synth)
+        layers, acts = cfg3_layers(torch, dev, synth)
+        result["decode_cfg3"] = decode_chain(torch, L, T, dev, gpu, layers, acts)
+        result["decode_cfg3"]["full_step"] = decode_step(torch, L, T, dev, gpu, synth, layers)
+        del layers, acts
 
     if not a.no_cpu:
         log("CPU baseline (reference C bpd_qmatmul_q4k)")
