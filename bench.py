@@ -203,7 +203,7 @@ def decode_step(torch, L, T, dev, gpu, synth, layers, tokens=10, max_seq=4096, v
     torch.cuda.synchronize()
     gpu.check()
     wb = sum(t.numel() for lw in layers for t in (getattr(lw, n) for n in llama.MATRICES)) + lm.numel()
-    out = {"weight_bytes": wb, "vocab": vocab, "max_seq": max_seq, "launches_per_token": 9 * len(layers) + 3}
+    out = {"weight_bytes": wb, "vocab": vocab, "max_seq": max_seq, "launches_per_token": 7 * len(layers) + 3}
     for pos0 in (0, 2048):
         us = T.us_per_launch([(lambda t=t: m.enqueue(embs[t], pos0 + t)) for t in range(tokens)])
         gpu.check()

@@ -107,4 +107,23 @@ __device__ __forceinline__ void q8_0_lane_store(float v, uint8_t* __restrict__ y
     }
 }
 
+// The same bytes from 8 consecutive lanes holding 4 elements each (lane g of
+// the aligned group holds elements 4g..4g+3).  yb is a 34-byte record, so only
+// 2-byte aligned: the quants go out as two 16-bit stores per lane.
+__device__ __forceinline__ void q8_0_quad_store(float4 v, uint8_t* __restrict__ yb, int g) {
+    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+#pragma unroll
+    for (int mask = 1; mask < 8; mask <<= 1) amax = fmaxf(amax, xor_f(amax, mask));
+    const float d = amax / 127.0f;
+    const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+    const uint32_t q0 = (uint32_t)(int)__builtin_rintf(v.x * id) & 0xFFu;
+    const uint32_t q1 = (uint32_t)(int)__builtin_rintf(v.y * id) & 0xFFu;
+    const uint32_t q2 = (uint32_t)(int)__builtin_rintf(v.z * id) & 0xFFu;
+    const uint32_t q3 = (uint32_t)(int)__builtin_rintf(v.w * id) & 0xFFu;
+    uint16_t* p = reinterpret_cast<uint16_t*>(yb + 2 + 4 * g);
+    p[0] = (uint16_t)(q0 | (q1 << 8));
+    p[1] = (uint16_t)(q2 | (q3 << 8));
+    if (g == 0) *reinterpret_cast<uint16_t*>(yb) = __builtin_bit_cast(uint16_t, (_Float16)d);
+}
+
 }  // namespace bpdq

@@ -25,6 +25,10 @@ void launch_qmatmul_q4k_q8k_multi(const uint8_t* const* w, float* const* y, cons
 int fused_max_k();
 void launch_qmatmul_q4k_fused_multi(const uint8_t* const* w, float* const* y, const int* M, int n, const float* x,
                                     int K, int order, hipStream_t s);
+// Gate and up (M rows each, K <= fused_max_k()) with the fp32 activation x:
+// y[r] = silu(gate_r) * up_r, gate_r and up_r as the fused GEMV computes them.
+void launch_qmatmul_q4k_fused_swiglu(const uint8_t* w_gate, const uint8_t* w_up, float* y, int M, const float* x,
+                                     int K, int order, hipStream_t s);
 
 void launch_dequant_q6k(const uint8_t* q, float* out, int n_blocks, int order, hipStream_t s);
 void launch_qmatmul_q6k_q8k(const uint8_t* w, const uint8_t* xq, float* y, int M, int K, int order, hipStream_t s);

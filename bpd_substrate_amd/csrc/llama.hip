@@ -3,9 +3,10 @@
 // generate_token ABI of inference/llamatov_c_inference.py:15-83.
 //
 //   k_residual_rmsnorm  x = x_in (+ add); h = rmsnorm(x) * w; Q8_0(h)   one workgroup
-//   k_rope_kv           q/k/v bias, RoPE (NORM pairs) on q and k, K/V cache row write
-//   k_attn_decode       one workgroup per query head: scores, softmax, P.V, Q8_0(out)
-//   k_swiglu            silu(gate) * up, Q8_0
+//   k_attn_decode       one workgroup per query head: q/k/v bias, RoPE (NORM pairs),
+//                       the K/V cache row write, scores, softmax, P.V, Q8_0(out)
+//   k_swiglu            silu(gate) * up, Q8_0 (padded Q8 weights; with Q4_K the
+//                       gate/up GEMV applies it to its own outputs)
 //   k_argmax            first index of the maximum logit
 //   k_gemv_f32          fp32 head (tied embeddings)
 // The seven GEMVs of a layer are the padded-Q8 tile-order product (q8_0.hip) or
@@ -38,6 +39,7 @@
 namespace bpdq {
 
 constexpr int kNormThreads = 1024;
+constexpr int kNormChunks = 16384 / (4 * kNormThreads);  // float4 chunks per thread for n <= kMaxEmbd
 constexpr int kMaxEmbd = 16384;  // the residual row stays in LDS (64 KB)
 constexpr int kMaxHeadDim = 256;
 constexpr int kAttnThreads = 256;
@@ -55,22 +57,43 @@ constexpr int kMaxCtx = 32768;  // one head's scores stay in LDS (128 KB)
 // pins the reference's mean to that value; otherwise lane 0 redoes the
 // reference's sequential sum from the row kept in LDS.
 // ----------------------------------------------------------------------------
-template <int NT>
+// Thread t holds float4 chunks t, t + NT, ... of the row (MAXC at most), with
+// the norm weight loaded alongside.  Q8_0 blocks are 8 consecutive lanes.
+template <int NT, int MAXC>
 __global__ __launch_bounds__(NT) void k_residual_rmsnorm(const float* x_in, const float* __restrict__ add,
                                                          float* x_out, const float* __restrict__ w,
                                                          float* __restrict__ h, uint8_t* __restrict__ xq, int n,
                                                          float eps) {
-    extern __shared__ float xs[];
+    extern __shared__ float4 xs4[];
     __shared__ double wsum[NT / 64];
     __shared__ float sh_scale;
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, nc = n >> 2;
+    const float4* x4 = reinterpret_cast<const float4*>(x_in);
+    const float4* a4 = reinterpret_cast<const float4*>(add);
+    const float4* w4 = reinterpret_cast<const float4*>(w);
+    float4 v[MAXC], wv[MAXC];
+#pragma unroll
+    for (int j = 0; j < MAXC; j++) {
+        const int c = tid + j * NT;
+        if (c < nc) {
+            v[j] = x4[c];
+            wv[j] = w4[c];
+            if (add != nullptr) {
+                const float4 a = a4[c];
+                v[j] = make_float4(v[j].x + a.x, v[j].y + a.y, v[j].z + a.z, v[j].w + a.w);
+            }
+        }
+    }
     double s = 0.0;
-    for (int i = tid; i < n; i += NT) {
-        float v = x_in[i];
-        if (add != nullptr) v = v + add[i];
-        xs[i] = v;
-        if (x_out != nullptr) x_out[i] = v;
-        s += (double)v * (double)v;
+#pragma unroll
+    for (int j = 0; j < MAXC; j++) {
+        const int c = tid + j * NT;
+        if (c < nc) {
+            xs4[c] = v[j];
+            if (x_out != nullptr) reinterpret_cast<float4*>(x_out)[c] = v[j];
+            s += (double)v[j].x * v[j].x + (double)v[j].y * v[j].y + (double)v[j].z * v[j].z +
+                 (double)v[j].w * v[j].w;
+        }
     }
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m, 64);
@@ -84,6 +107,7 @@ __global__ __launch_bounds__(NT) void k_residual_rmsnorm(const float* x_in, cons
         const float lo = (float)((S - err) / dn), hi = (float)((S + err) / dn);
         float mean = lo;
         if (!(lo == hi)) {
+            const float* xs = reinterpret_cast<const float*>(xs4);
             double q = 0.0;
             for (int i = 0; i < n; i++) q += (double)xs[i] * (double)xs[i];
             mean = (float)(q / dn);
@@ -92,101 +116,115 @@ __global__ __launch_bounds__(NT) void k_residual_rmsnorm(const float* x_in, cons
     }
     __syncthreads();
     const float scale = sh_scale;
-    // n and NT are multiples of 32: each Q8_0 block is 32 lanes of one wave
-    for (int i = tid; i < n; i += NT) {
-        const float y = (xs[i] * scale) * w[i];
-        if (h != nullptr) h[i] = y;
-        if (xq != nullptr) q8_0_lane_store(y, xq + (int64_t)(i >> 5) * kQ80Bytes, i & 31);
+#pragma unroll
+    for (int j = 0; j < MAXC; j++) {
+        const int c = tid + j * NT;
+        if (c < nc) {
+            const float4 x = v[j], ww = wv[j];
+            const float4 y = make_float4((x.x * scale) * ww.x, (x.y * scale) * ww.y, (x.z * scale) * ww.z,
+                                         (x.w * scale) * ww.w);
+            if (h != nullptr) reinterpret_cast<float4*>(h)[c] = y;
+            // n % 32 == 0 and NT % 8 == 0: the 8 chunks of a block are 8 aligned lanes
+            if (xq != nullptr) q8_0_quad_store(y, xq + (int64_t)(c >> 3) * kQ80Bytes, c & 7);
+        }
     }
 }
 
 // ----------------------------------------------------------------------------
-// Bias, RoPE and the K/V cache write (bpd_rope_norm_freqs_cpu,
-// bench/bpd_cpu.c:5146-5184 without frequency factors; bpd_kv_cache_write_cpu,
-// :5204-5222).  NORM pairs: pair j of a head rotates elements 2j and 2j+1 by
-// angle pos * theta_scale^j, whose cos/sin the host computed:
-//   y0 = x0*c - x1*s,  y1 = x0*s + x1*c   (each product rounded, then the sum).
-// Thread i: a q pair, a k pair (also written to the cache), or a v element.
+// Decode attention of query head blockIdx.x at position pos, with the bias,
+// RoPE and K/V cache write of the new row folded in:
+//   bias: q, k, v = projection + bias (when given), before RoPE;
+//   RoPE (bpd_rope_norm_freqs_cpu, bench/bpd_cpu.c:5146-5184, no frequency
+//     factors): pair j of a head rotates elements 2j, 2j+1 by pos*theta_scale^j,
+//     y0 = x0*c - x1*s, y1 = x0*s + x1*c (each product rounded, then the sum),
+//     cos/sin from the host;
+//   the new k and v rows go to cache row pos (bpd_kv_cache_write_cpu, :5204),
+//     written by the first query head of each group; every head of the group
+//     takes row pos from its own LDS copy, so no head reads a row another
+//     workgroup is writing;
+//   attention (bpd_gqa_attn_cpu, :5370-5440, post-scaled batch softmax) over
+//     rows 0..pos:
+//   s_j = sum_d q_d k_jd (sequential over d);  v_j = s_j * scale
+//   m = max(-1e38, v_j);  e_j = expf(v_j - m);  S = sum_j e_j (sequential over j)
+//   w_j = e_j * (S == 0 ? 0 : 1/S);  out_d = sum_j v_jd w_j (sequential over j)
+// The reference also visits rows pos+1..max_seq-1 with weight exp(-1e38 - m) =
+// 0; for finite cache contents those add exact zeros, so stopping at pos gives
+// the same bits.  Scores live in LDS.
 // ----------------------------------------------------------------------------
 struct RopeTab {
     float c[kMaxHeadDim / 2];
     float s[kMaxHeadDim / 2];
 };
 
-__global__ __launch_bounds__(256) void k_rope_kv(float* __restrict__ q, float* __restrict__ k, float* __restrict__ v,
-                                                 const float* __restrict__ bq, const float* __restrict__ bk,
-                                                 const float* __restrict__ bv, float* __restrict__ kc,
-                                                 float* __restrict__ vc, int nq_pairs, int nk_pairs, int nv, int half,
-                                                 RopeTab tab) {
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i < nq_pairs + nk_pairs) {
-        const bool isq = i < nq_pairs;
-        const int p = isq ? i : i - nq_pairs;
-        float* t = isq ? q : k;
-        const float* b = isq ? bq : bk;
-        const int e = 2 * p, j = p % half;
-        float x0 = t[e], x1 = t[e + 1];
-        if (b != nullptr) {
-            x0 = x0 + b[e];
-            x1 = x1 + b[e + 1];
-        }
-        const float c = tab.c[j], s = tab.s[j];
-        const float y0 = x0 * c - x1 * s;
-        const float y1 = x0 * s + x1 * c;
-        t[e] = y0;
-        t[e + 1] = y1;
-        if (!isq) {
-            kc[e] = y0;
-            kc[e + 1] = y1;
-        }
-    } else if (i < nq_pairs + nk_pairs + nv) {
-        const int j = i - nq_pairs - nk_pairs;
-        float val = v[j];
-        if (bv != nullptr) {
-            val = val + bv[j];
-            v[j] = val;
-        }
-        vc[j] = val;
-    }
-}
-
-// ----------------------------------------------------------------------------
-// Decode attention for query head blockIdx.x over cache rows 0..n-1
-// (bpd_gqa_attn_cpu, bench/bpd_cpu.c:5370-5440, post-scaled batch softmax):
-//   s_j = sum_d q_d k_jd (sequential over d);  v_j = s_j * scale
-//   m = max(-1e38, v_j);  e_j = expf(v_j - m);  S = sum_j e_j (sequential over j)
-//   w_j = e_j * (S == 0 ? 0 : 1/S);  out_d = sum_j v_jd w_j (sequential over j)
-// Scores and weights live in LDS.  The reference also visits rows n..max_seq-1
-// with weight exp(-1e38 - m) = 0; for finite cache contents those add exact
-// zeros, so stopping at n gives the same bits.
-// ----------------------------------------------------------------------------
 template <int NT>
-__global__ __launch_bounds__(NT) void k_attn_decode(const float* __restrict__ q, const float* __restrict__ kc,
-                                                    const float* __restrict__ vc, float* __restrict__ out,
-                                                    uint8_t* __restrict__ xq, int group, int row, int D, int n,
-                                                    float scale) {
+__global__ __launch_bounds__(NT) void k_attn_decode(const float* __restrict__ q, const float* __restrict__ knew,
+                                                    const float* __restrict__ vnew, const float* __restrict__ bq,
+                                                    const float* __restrict__ bk, const float* __restrict__ bv,
+                                                    float* __restrict__ kc, float* __restrict__ vc,
+                                                    float* __restrict__ out, uint8_t* __restrict__ xq, int group,
+                                                    int row, int D, int pos, float scale, RopeTab tab) {
     extern __shared__ float e[];
-    __shared__ float4 qs4[kMaxHeadDim / 4];
+    __shared__ float4 qs4[kMaxHeadDim / 4], ks4[kMaxHeadDim / 4], vs4[kMaxHeadDim / 4];
     __shared__ float red[NT / 64];
-    __shared__ float sh_max, sh_inv;
-    const int tid = threadIdx.x, head = blockIdx.x, kvh = head / group;
+    __shared__ float sh_inv;
+    const int tid = threadIdx.x, head = blockIdx.x, kvh = head / group, n = pos + 1;
     float* qs = reinterpret_cast<float*>(qs4);
-    for (int d = tid; d < D; d += NT) qs[d] = q[(int64_t)head * D + d];
+    float* ks = reinterpret_cast<float*>(ks4);
+    float* vs = reinterpret_cast<float*>(vs4);
+    const int64_t qo = (int64_t)head * D, ko = (int64_t)kvh * D;
+    for (int p = tid; p < D / 2; p += NT) {
+        const int i = 2 * p;
+        const float c = tab.c[p], sn = tab.s[p];
+        float x0 = q[qo + i], x1 = q[qo + i + 1];
+        float k0 = knew[ko + i], k1 = knew[ko + i + 1];
+        if (bq != nullptr) {
+            x0 = x0 + bq[qo + i];
+            x1 = x1 + bq[qo + i + 1];
+        }
+        if (bk != nullptr) {
+            k0 = k0 + bk[ko + i];
+            k1 = k1 + bk[ko + i + 1];
+        }
+        qs[i] = x0 * c - x1 * sn;
+        qs[i + 1] = x0 * sn + x1 * c;
+        ks[i] = k0 * c - k1 * sn;
+        ks[i + 1] = k0 * sn + k1 * c;
+    }
+    for (int d = tid; d < D; d += NT) {
+        float vv = vnew[ko + d];
+        if (bv != nullptr) vv = vv + bv[ko + d];
+        vs[d] = vv;
+    }
     __syncthreads();
-    const float* kbase = kc + (int64_t)kvh * D;
+    if (head % group == 0)
+        for (int d = tid; d < D; d += NT) {
+            kc[(int64_t)pos * row + ko + d] = ks[d];
+            vc[(int64_t)pos * row + ko + d] = vs[d];
+        }
     float m = -1e38f;
     for (int j = tid; j < n; j += NT) {
-        const float4* kr = reinterpret_cast<const float4*>(kbase + (int64_t)j * row);
-        float s = 0.0f;
-        for (int d4 = 0; d4 < D / 4; d4++) {
-            const float4 kv = kr[d4];
-            const float4 qv = qs4[d4];
-            s = s + qv.x * kv.x;
-            s = s + qv.y * kv.y;
-            s = s + qv.z * kv.z;
-            s = s + qv.w * kv.w;
+        const float4* kr = reinterpret_cast<const float4*>(kc + (int64_t)j * row + ko);
+        float sc = 0.0f;
+        if (j < pos) {
+            for (int d4 = 0; d4 < D / 4; d4++) {
+                const float4 kv = kr[d4];
+                const float4 qv = qs4[d4];
+                sc = sc + qv.x * kv.x;
+                sc = sc + qv.y * kv.y;
+                sc = sc + qv.z * kv.z;
+                sc = sc + qv.w * kv.w;
+            }
+        } else {
+            for (int d4 = 0; d4 < D / 4; d4++) {
+                const float4 kv = ks4[d4];
+                const float4 qv = qs4[d4];
+                sc = sc + qv.x * kv.x;
+                sc = sc + qv.y * kv.y;
+                sc = sc + qv.z * kv.z;
+                sc = sc + qv.w * kv.w;
+            }
         }
-        const float sv = s * scale;
+        const float sv = sc * scale;
         e[j] = sv;
         m = sv > m ? sv : m;
     }
@@ -197,13 +235,9 @@ __global__ __launch_bounds__(NT) void k_attn_decode(const float* __restrict__ q,
     }
     if ((tid & 63) == 0) red[tid >> 6] = m;
     __syncthreads();
-    if (tid == 0) {
-        float mm = red[0];
-        for (int w = 1; w < NT / 64; w++) mm = red[w] > mm ? red[w] : mm;
-        sh_max = mm;
-    }
-    __syncthreads();
-    const float mx = sh_max;
+    float mx = red[0];
+#pragma unroll
+    for (int w = 1; w < NT / 64; w++) mx = red[w] > mx ? red[w] : mx;
     for (int j = tid; j < n; j += NT) e[j] = expf_libm(e[j] - mx);
     __syncthreads();
     if (tid == 0) {
@@ -214,16 +248,15 @@ __global__ __launch_bounds__(NT) void k_attn_decode(const float* __restrict__ q,
     }
     __syncthreads();
     const float inv = sh_inv;
-    for (int j = tid; j < n; j += NT) e[j] = e[j] * inv;
-    __syncthreads();
     // D <= NT and D % 32 == 0: lanes d < D are whole 32-lane Q8_0 blocks
     const int d = tid;
     if (d < D) {
-        const float* vcol = vc + (int64_t)kvh * D + d;
+        const float* vcol = vc + ko + d;
         float acc = 0.0f;
 #pragma unroll 8
-        for (int j = 0; j < n; j++) acc = acc + vcol[(int64_t)j * row] * e[j];
-        const int64_t o = (int64_t)head * D + d;
+        for (int j = 0; j < pos; j++) acc = acc + vcol[(int64_t)j * row] * (e[j] * inv);
+        acc = acc + vs[d] * (e[pos] * inv);
+        const int64_t o = qo + d;
         out[o] = acc;
         if (xq != nullptr) q8_0_lane_store(acc, xq + (o >> 5) * kQ80Bytes, d & 31);
     }
@@ -329,7 +362,7 @@ bool lds_limits_set(const char* fn) {
         err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_decode<kAttnThreads>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, kMaxCtx * 4);
         if (err == hipSuccess)
-            err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_residual_rmsnorm<kNormThreads>),
+            err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_residual_rmsnorm<kNormThreads, kNormChunks>),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, kMaxEmbd * 4);
     });
     return abi_hip_ok(err, fn);
@@ -337,7 +370,8 @@ bool lds_limits_set(const char* fn) {
 
 void launch_norm(const float* x_in, const float* add, float* x_out, const float* w, float* h, uint8_t* xq, int n,
                  float eps, hipStream_t s) {
-    hipLaunchKernelGGL(k_residual_rmsnorm<kNormThreads>, dim3(1), dim3(kNormThreads), (size_t)n * 4, s, x_in, add,
+    hipLaunchKernelGGL((k_residual_rmsnorm<kNormThreads, kNormChunks>), dim3(1), dim3(kNormThreads), (size_t)n * 4, s,
+                       x_in, add,
                        x_out, w, h, xq, n, eps);
 }
 
@@ -440,8 +474,8 @@ bool validate(V& v, int fmt, const LayerWeights* layers, const ModelConfig* cfg,
     v.need(lm_N > 0, BPDQ_ERR_SHAPE, "lm_N must be positive");
     if (!v.ok) return false;
     const uintptr_t wal = fmt == BPDQ_W_Q8_PAD64 ? 4 : 16;
-    v.ptr(emb, 4, "embedding");
-    v.ptr(out_norm, 4, "output_norm_w");
+    v.ptr(emb, 16, "embedding");
+    v.ptr(out_norm, 16, "output_norm_w");
     if (lm_w != nullptr)
         v.ptr(lm_w, wal, "lm_head");
     else
@@ -472,8 +506,8 @@ bool validate(V& v, int fmt, const LayerWeights* layers, const ModelConfig* cfg,
         const void* mats[7] = {w.q, w.k, w.v, w.o, w.gate, w.up, w.down};
         static const char* mnames[7] = {"q", "k", "v", "o", "gate", "up", "down"};
         for (int i = 0; i < 7; i++) v.ptr(mats[i], wal, mnames[i]);
-        v.ptr(w.attn_norm, 4, "attn_norm");
-        v.ptr(w.ffn_norm, 4, "ffn_norm");
+        v.ptr(w.attn_norm, 16, "attn_norm");
+        v.ptr(w.ffn_norm, 16, "ffn_norm");
         if (w.q_bias) v.ptr(w.q_bias, 4, "q_bias");
         if (w.k_bias) v.ptr(w.k_bias, 4, "k_bias");
         if (w.v_bias) v.ptr(w.v_bias, 4, "v_bias");
@@ -484,7 +518,7 @@ bool validate(V& v, int fmt, const LayerWeights* layers, const ModelConfig* cfg,
 }
 
 // One GEMV y[N] = W[N][K] a[K]: padded Q8 reads the Q8_0 bytes aq of a; Q4_K
-// takes fp32 a (and quantizes it to Q8_K inside the kernel when K allows).
+// takes fp32 a and quantizes it to Q8_K inside the kernel.
 struct Gemv {
     int fmt;
     uint8_t* q8k;  // Q8_K staging for K beyond the fused kernel
@@ -508,94 +542,110 @@ struct Gemv {
     }
 };
 
+struct StepCtx {
+    Geometry g;
+    const ModelConfig* cfg;
+    const KVCache* kv;
+    int pos;
+    hipStream_t s;
+    RopeTab tab;
+    float *x, *h, *qb, *kb, *vb, *att, *gate, *up, *ffn;
+    uint8_t *xq_e, *xq_a, *xq_f;  // Q8_0 activations (padded Q8 weights only, else NULL)
+};
+
+// The layers.  The residual add is the first step of each RMSNorm kernel; the
+// norm, attention and SwiGLU kernels also write the Q8_0 bytes of their outputs
+// when the GEMVs take Q8_0 activations.  On return (xin, add) is the residual
+// stream as x + add.
+void run_layers(const StepCtx& c, const Gemv& gemv, const LayerWeights* layers, const float*& xin,
+                const float*& add) {
+    const Geometry& g = c.g;
+    const int row = g.HKV * g.D, n_ctx = c.pos + 1;
+    for (int l = 0; l < g.L; l++) {
+        const LayerWeights& w = layers[l];
+        launch_norm(xin, add, c.x, static_cast<const float*>(w.attn_norm), c.h, c.xq_e, g.E, c.cfg->eps, c.s);
+        xin = c.x;
+        const void* wqkv[3] = {w.q, w.k, w.v};
+        float* yqkv[3] = {c.qb, c.kb, c.vb};
+        const int nqkv[3] = {w.q_N, w.k_N, w.v_N};
+        gemv.run(3, wqkv, yqkv, nqkv, c.h, c.xq_e, g.E);
+        hipLaunchKernelGGL(k_attn_decode<kAttnThreads>, dim3(g.H), dim3(kAttnThreads), (size_t)n_ctx * 4, c.s, c.qb,
+                           c.kb, c.vb, static_cast<const float*>(w.q_bias), static_cast<const float*>(w.k_bias),
+                           static_cast<const float*>(w.v_bias), static_cast<float*>(c.kv->k_cache[l]),
+                           static_cast<float*>(c.kv->v_cache[l]), c.att, c.xq_a, g.H / g.HKV, row, g.D, c.pos,
+                           1.0f / sqrtf((float)g.D), c.tab);
+        const void* wo[1] = {w.o};
+        float* yo[1] = {c.ffn};
+        const int no[1] = {w.o_N};
+        gemv.run(1, wo, yo, no, c.att, c.xq_a, g.H * g.D);
+        launch_norm(c.x, c.ffn, c.x, static_cast<const float*>(w.ffn_norm), c.h, c.xq_e, g.E, c.cfg->eps, c.s);
+        if (gemv.fmt == BPDQ_W_Q8_PAD64) {
+            const void* wgu[2] = {w.gate, w.up};
+            float* ygu[2] = {c.gate, c.up};
+            const int ngu[2] = {w.gate_N, w.up_N};
+            gemv.run(2, wgu, ygu, ngu, c.h, c.xq_e, g.E);
+            hipLaunchKernelGGL(k_swiglu, dim3((g.F + 255) / 256), dim3(256), 0, c.s, c.gate, c.up, c.xq_f, g.F);
+        } else {  // n_embd <= fused_max_k(): gate/up with SwiGLU in the epilogue, into gate
+            launch_qmatmul_q4k_fused_swiglu(static_cast<const uint8_t*>(w.gate), static_cast<const uint8_t*>(w.up),
+                                            c.gate, g.F, c.h, g.E, gemv.fmt == BPDQ_W_Q4K_GGUF ? 1 : 0, c.s);
+        }
+        const void* wd[1] = {w.down};
+        float* yd[1] = {c.ffn};
+        const int nd[1] = {w.down_N};
+        gemv.run(1, wd, yd, nd, c.gate, c.xq_f, g.F);
+        add = c.ffn;
+    }
+}
+
 bool enqueue_step(int fmt, const LayerWeights* layers, const ModelConfig* cfg, const WorkBuffers* buf,
                   const KVCache* kv, int pos, const void* emb, const void* out_norm, const void* lm_w,
                   const void* lm_f32, int lm_K, int lm_N, const char* fn) {
     V v{fn};
-    Geometry g{};
+    StepCtx c{};
+    Geometry& g = c.g;
     if (!validate(v, fmt, layers, cfg, buf, kv, pos, emb, out_norm, lm_w, lm_f32, lm_K, lm_N, g)) return false;
     if (!lds_limits_set(fn)) return false;
     const bool q8 = fmt == BPDQ_W_Q8_PAD64;
     const size_t q8e = (size_t)(g.E / 32) * kQ80Bytes, q8f = (size_t)(g.F / 32) * kQ80Bytes;
+    const size_t front = q8 ? (2 * q8e + q8f + 255) & ~(size_t)255 : 0;
     const int kmax = g.F > g.E ? g.F : g.E;
     const size_t q8k = kmax > fused_max_k() ? (size_t)(kmax / 256) * kQ8KBytes : 0;
-    uint8_t* ws = step_workspace((q8 ? 2 * q8e + q8f : 0) + q8k + 256, fn);
+    uint8_t* ws = step_workspace(front + q8k + 256, fn);
     if (ws == nullptr) return false;
-    uint8_t* xq_e = q8 ? ws : nullptr;
-    uint8_t* xq_a = q8 ? ws + q8e : nullptr;
-    uint8_t* xq_f = q8 ? ws + 2 * q8e : nullptr;
-    const Gemv gemv{fmt, ws + (q8 ? 2 * q8e + q8f : 0), abi_stream()};
-    const hipStream_t s = gemv.s;
-
-    float* x = static_cast<float*>(buf->x);
-    float* h = static_cast<float*>(buf->h);
-    float* qb = static_cast<float*>(buf->q);
-    float* kb = static_cast<float*>(buf->k);
-    float* vb = static_cast<float*>(buf->v);
-    float* att = static_cast<float*>(buf->attn_out);
-    float* gate = static_cast<float*>(buf->gate);
-    float* up = static_cast<float*>(buf->up);
-    float* ffn = static_cast<float*>(buf->ffn);
+    const Gemv gemv{fmt, ws + front, abi_stream()};
+    c.cfg = cfg;
+    c.kv = kv;
+    c.pos = pos;
+    c.s = gemv.s;
+    c.x = static_cast<float*>(buf->x);
+    c.h = static_cast<float*>(buf->h);
+    c.qb = static_cast<float*>(buf->q);
+    c.kb = static_cast<float*>(buf->k);
+    c.vb = static_cast<float*>(buf->v);
+    c.att = static_cast<float*>(buf->attn_out);
+    c.gate = static_cast<float*>(buf->gate);
+    c.up = static_cast<float*>(buf->up);
+    c.ffn = static_cast<float*>(buf->ffn);
+    c.xq_e = q8 ? ws : nullptr;
+    c.xq_a = q8 ? ws + q8e : nullptr;
+    c.xq_f = q8 ? ws + 2 * q8e : nullptr;
+    if (g.L > 0) rope_table(c.tab, pos, g.D, cfg->rope_theta);
     float* logits = static_cast<float*>(buf->logits);
-    const int row = g.HKV * g.D, n_ctx = pos + 1;
-    const float scale = 1.0f / sqrtf((float)g.D);
-    RopeTab tab;
-    if (g.L > 0) rope_table(tab, pos, g.D, cfg->rope_theta);
 
     const float* xin = static_cast<const float*>(emb);
     const float* add = nullptr;
-    for (int l = 0; l < g.L; l++) {
-        const LayerWeights& w = layers[l];
-        launch_norm(xin, add, x, static_cast<const float*>(w.attn_norm), h, xq_e, g.E, cfg->eps, s);
-        xin = x;
-        {
-            const void* ws3[3] = {w.q, w.k, w.v};
-            float* ys3[3] = {qb, kb, vb};
-            const int ns3[3] = {w.q_N, w.k_N, w.v_N};
-            gemv.run(3, ws3, ys3, ns3, h, xq_e, g.E);
-        }
-        float* kc = static_cast<float*>(kv->k_cache[l]) + (int64_t)pos * row;
-        float* vc = static_cast<float*>(kv->v_cache[l]) + (int64_t)pos * row;
-        const int nq = g.H * g.D / 2, nk = row / 2, nv = row;
-        hipLaunchKernelGGL(k_rope_kv, dim3((nq + nk + nv + 255) / 256), dim3(256), 0, s, qb, kb, vb,
-                           static_cast<const float*>(w.q_bias), static_cast<const float*>(w.k_bias),
-                           static_cast<const float*>(w.v_bias), kc, vc, nq, nk, nv, g.D / 2, tab);
-        hipLaunchKernelGGL(k_attn_decode<kAttnThreads>, dim3(g.H), dim3(kAttnThreads), (size_t)n_ctx * 4, s, qb,
-                           static_cast<const float*>(kv->k_cache[l]), static_cast<const float*>(kv->v_cache[l]), att,
-                           xq_a, g.H / g.HKV, row, g.D, n_ctx, scale);
-        {
-            const void* wo[1] = {w.o};
-            float* yo[1] = {ffn};
-            const int no[1] = {w.o_N};
-            gemv.run(1, wo, yo, no, att, xq_a, g.H * g.D);
-        }
-        launch_norm(x, ffn, x, static_cast<const float*>(w.ffn_norm), h, xq_e, g.E, cfg->eps, s);
-        {
-            const void* wgu[2] = {w.gate, w.up};
-            float* ygu[2] = {gate, up};
-            const int ngu[2] = {w.gate_N, w.up_N};
-            gemv.run(2, wgu, ygu, ngu, h, xq_e, g.E);
-        }
-        hipLaunchKernelGGL(k_swiglu, dim3((g.F + 255) / 256), dim3(256), 0, s, gate, up, xq_f, g.F);
-        {
-            const void* wd[1] = {w.down};
-            float* yd[1] = {ffn};
-            const int nd[1] = {w.down_N};
-            gemv.run(1, wd, yd, nd, gate, xq_f, g.F);
-        }
-        add = ffn;
-    }
-    launch_norm(xin, add, x, static_cast<const float*>(out_norm), h, xq_e, g.E, cfg->eps, s);
+    run_layers(c, gemv, layers, xin, add);
+    launch_norm(xin, add, c.x, static_cast<const float*>(out_norm), c.h, c.xq_e, g.E, cfg->eps, c.s);
     if (lm_w != nullptr) {
         const void* wl[1] = {lm_w};
         float* yl[1] = {logits};
         const int nl[1] = {lm_N};
-        gemv.run(1, wl, yl, nl, h, xq_e, g.E);
+        gemv.run(1, wl, yl, nl, c.h, c.xq_e, g.E);
     } else {
-        hipLaunchKernelGGL(k_gemv_f32, dim3((lm_N + 3) / 4), dim3(256), 0, s, static_cast<const float*>(lm_f32), h,
-                           logits, lm_N, g.E);
+        hipLaunchKernelGGL(k_gemv_f32, dim3((lm_N + 3) / 4), dim3(256), 0, c.s, static_cast<const float*>(lm_f32),
+                           c.h, logits, lm_N, g.E);
     }
-    hipLaunchKernelGGL(k_argmax<1024>, dim3(1), dim3(1024), 0, s, logits, lm_N,
+    hipLaunchKernelGGL(k_argmax<1024>, dim3(1), dim3(1024), 0, c.s, logits, lm_N,
                        static_cast<int32_t*>(buf->argmax_result));
     return abi_hip_ok(hipGetLastError(), fn);
 }
@@ -674,11 +724,11 @@ void bpd_residual_rmsnorm_gpu(const float* x_in, const float* add, float* x_out,
     bpdq::V v{fn};
     v.need(n > 0 && n % 32 == 0 && n <= bpdq::kMaxEmbd, BPDQ_ERR_SHAPE,
            "n must be a positive multiple of 32, at most 16384");
-    v.ptr(x_in, 4, "x_in");
-    v.ptr(w, 4, "w");
-    if (add) v.ptr(add, 4, "add");
-    if (x_out) v.ptr(x_out, 4, "x_out");
-    if (h) v.ptr(h, 4, "h");
+    v.ptr(x_in, 16, "x_in");
+    v.ptr(w, 16, "w");
+    if (add) v.ptr(add, 16, "add");
+    if (x_out) v.ptr(x_out, 16, "x_out");
+    if (h) v.ptr(h, 16, "h");
     if (!v.ok || !bpdq::lds_limits_set(fn)) return;
     bpdq::launch_norm(x_in, add, x_out, w, h, xq, n, eps, bpdq::abi_stream());
     bpdq::abi_hip_ok(hipGetLastError(), fn);

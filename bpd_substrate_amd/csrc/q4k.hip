@@ -6,6 +6,7 @@
 //   k_q4k_q8k_gemv<ORDER,R> Q4_K x Q8_K GEMV, integer sub-block sums + fixed fp32 tree
 #include "bpdq_device.h"
 #include "bpdq_launch.h"
+#include "bpdq_math.h"
 
 namespace bpdq {
 
@@ -252,9 +253,10 @@ struct WideW {
     uint32_t hw[G][R];
 };
 
-template <int R, int G>
+// PAIR (R = 2): the wave's two rows are row row0 of w and row row0 of w1.
+template <int R, int G, bool PAIR = false>
 __device__ __forceinline__ void wide_load_g(WideW<R, G>& W, int g, const uint8_t* __restrict__ w, int M, int nb,
-                                            int row0, int t0) {
+                                            int row0, int t0, const uint8_t* __restrict__ w1 = nullptr) {
     const int lane = threadIdx.x & 63;
     const int q = lane >> 3, c = lane & 7;
     const int64_t row_bytes = (int64_t)nb * kQ4KBytes;
@@ -262,7 +264,9 @@ __device__ __forceinline__ void wide_load_g(WideW<R, G>& W, int g, const uint8_t
     const int bb = b < nb ? b : nb - 1;
 #pragma unroll
     for (int r = 0; r < R; r++) {
-        const uint8_t* blk = w + (int64_t)min(row0 + r, M - 1) * row_bytes + (int64_t)bb * kQ4KBytes;
+        const uint8_t* base = PAIR && r == 1 ? w1 : w;
+        const int row = PAIR ? row0 : min(row0 + r, M - 1);
+        const uint8_t* blk = base + (int64_t)row * row_bytes + (int64_t)bb * kQ4KBytes;
         W.qv[g][r] = ld_u128(blk + 16 + 16 * c);
         W.hw[g][r] = ld_u32(blk + 4 * (c & 3));
     }
@@ -274,9 +278,16 @@ __device__ __forceinline__ void wide_load_g(WideW<R, G>& W, int g, const uint8_t
 // M reuse row M-1 and slots past nb reuse block nb-1 (their results are
 // discarded), so every address stays in the tensors.  row0 < M.  With PRE the
 // weights of the first pass were loaded by the caller into `pre`.
-template <int ORDER, int R, int G, bool LX, bool PRE>
+//
+// PAIR (R = 2): the rows are row0 of w (gate) and row0 of w1 (up), and the
+// wave stores y[row0] = (g / (1 + expf(-g))) * u, the SwiGLU of the two
+// (bench/bpd_cpu.c:5504-5507) on the bit-exact g and u.
+__device__ __forceinline__ float silu_mul(float g, float u) { return (g / (1.0f + expf_libm(-g))) * u; }
+
+template <int ORDER, int R, int G, bool LX, bool PRE, bool PAIR = false>
 __device__ __forceinline__ void gemv_rows(const uint8_t* __restrict__ w, const uint8_t* __restrict__ xsrc,
-                                          float* __restrict__ y, int M, int nb, int row0, const WideW<R, G>& pre) {
+                                          float* __restrict__ y, int M, int nb, int row0, const WideW<R, G>& pre,
+                                          const uint8_t* __restrict__ w1 = nullptr) {
     const int lane = threadIdx.x & 63;
     const int q = lane >> 3, c = lane & 7;
     const int ngroups = (nb + 7) >> 3;
@@ -299,7 +310,7 @@ __device__ __forceinline__ void gemv_rows(const uint8_t* __restrict__ w, const u
                     W.hw[g][r] = pre.hw[g][r];
                 }
             } else {
-                wide_load_g<R, G>(W, g, w, M, nb, row0, t0);
+                wide_load_g<R, G, PAIR>(W, g, w, M, nb, row0, t0, w1);
             }
             x[g] = get_x<ORDER, LX>(xsrc, valid[g] ? b : nb - 1, c);
         }
@@ -316,14 +327,17 @@ __device__ __forceinline__ void gemv_rows(const uint8_t* __restrict__ w, const u
     }
     // slot q lives in lanes 8q..8q+7: row_mirror pairs slots q and q^1, then the
     // four pair sums are lanes 0, 16, 32, 48
+    float out[R];
 #pragma unroll
     for (int r = 0; r < R; r++) {
         float v = s[r];
         v = v + dpp_f<0x140>(v);
         const float p01 = readlane_f(v, 0), p23 = readlane_f(v, 16);
         const float p45 = readlane_f(v, 32), p67 = readlane_f(v, 48);
-        if (lane == 0 && row0 + r < M) y[row0 + r] = (p01 + p23) + (p45 + p67);
+        out[r] = (p01 + p23) + (p45 + p67);
+        if (!PAIR && lane == 0 && row0 + r < M) y[row0 + r] = out[r];
     }
+    if (PAIR && lane == 0) y[row0] = silu_mul(out[0], out[R - 1]);
 }
 
 // ----------------------------------------------------------------------------
@@ -730,6 +744,51 @@ static void launch_fused(const MultiArgs& a, const float* x, int nb, hipStream_t
     const int waves = a.first[kMulti];
     hipLaunchKernelGGL((k_q4k_fused_gemv<KIND, ORDER, R, G, WPB, IT>), dim3((waves + WPB - 1) / WPB),
                        dim3(64 * WPB), (size_t)nb * kXS, s, a, x, nb);
+}
+
+// Gate and up in one launch with SwiGLU in the epilogue: wave w computes row w
+// of both matrices (the 8-lane kernel, two rows per wave) from the shared
+// fp32 x, quantized to Q8_K in LDS as in k_q4k_fused_gemv, and stores
+// y[w] = silu(gate_w) * up_w.  gate_w and up_w are the bits the plain GEMV
+// gives, so y equals the GEMVs followed by bpd_swiglu_fuse_cpu's arithmetic.
+template <int ORDER, int G, int WPB>
+__global__ __launch_bounds__(64 * WPB) void k_q4k_fused_swiglu(const uint8_t* __restrict__ wg,
+                                                              const uint8_t* __restrict__ wu, float* __restrict__ y,
+                                                              int M, const float* __restrict__ x, int nb) {
+    extern __shared__ __align__(16) uint8_t xl[];
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int row = blockIdx.x * WPB + wave;
+    const bool has = row < M;
+    const int row0 = has ? row : 0;
+    XPre<1> P;
+    x32_load<WPB, 1>(P, x, nb);
+    WideW<2, G> pre;
+#pragma unroll
+    for (int g = 0; g < G; g++) wide_load_g<2, G, true>(pre, g, wg, M, nb, row0, 0, wu);
+    __builtin_amdgcn_sched_barrier(0);
+    x32_quantize<WPB, 1>(P, xl, nb);
+    __syncthreads();
+    if (!has) return;
+    gemv_rows<ORDER, 2, G, true, true, true>(wg, xl, y, M, nb, row0, pre, wu);
+}
+
+template <int ORDER, int WPB>
+static void launch_swiglu(const uint8_t* wg, const uint8_t* wu, float* y, int M, const float* x, int nb,
+                          hipStream_t s) {
+    hipLaunchKernelGGL((k_q4k_fused_swiglu<ORDER, 2, WPB>), dim3((M + WPB - 1) / WPB), dim3(64 * WPB),
+                       (size_t)nb * kXS, s, wg, wu, y, M, x, nb);
+}
+
+// One quantization pass covers 4*WPB blocks: 4 waves up to K = 4096, 16 up to
+// fused_max_k().
+void launch_qmatmul_q4k_fused_swiglu(const uint8_t* wg, const uint8_t* wu, float* y, int M, const float* x, int K,
+                                     int order, hipStream_t s) {
+    const int nb = K / 256;
+    if (nb <= 16) {
+        if (order == 0) launch_swiglu<0, 4>(wg, wu, y, M, x, nb, s); else launch_swiglu<1, 4>(wg, wu, y, M, x, nb, s);
+    } else {
+        if (order == 0) launch_swiglu<0, 16>(wg, wu, y, M, x, nb, s); else launch_swiglu<1, 16>(wg, wu, y, M, x, nb, s);
+    }
 }
 
 // Fused shapes, measured on MI355X for the decode-chain GEMVs (one graph of

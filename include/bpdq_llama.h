@@ -96,7 +96,8 @@ typedef struct {
 } WorkBuffers;
 
 /* :62-78.  One decode step.  `embedding` is the fp32 [n_embd] input row on the
- * device; layer and head weights are in the padded Q8 layout of
+ * device (16-byte aligned, as are the norm weights, the work buffers and the
+ * caches); layer and head weights are in the padded Q8 layout of
  * bpd_q8_pad64_from_f32_gpu (records [K/32][N][64]), or, with lm_head NULL,
  * the head is lm_f32: fp32 [lm_N][lm_K] row-major.  Returns the argmax token
  * (waits for the step to finish), or -1 after recording an error. */
@@ -120,7 +121,9 @@ void gpu_free(void* p);
  *   BPDQ_W_Q4K_GGUF   Q4_K, GGUF (llama.cpp) element map.
  * With Q4_K weights each GEMV is the Q4_K x Q8_K product with the activation
  * quantized to Q8_K inside the kernel (bpd_qmatmul_q4k_q8k_fused_multi_gpu);
- * Q/K/V and gate/up are single launches.  The token is left in
+ * Q/K/V is one launch, and gate/up one launch that applies SwiGLU to its own
+ * outputs (gate holds silu(gate) * up afterwards; up is not written).  The
+ * token is left in
  * buf->argmax_result; returns 0, or -1 after recording an error.  For HIP
  * graph capture and timing loops. */
 #define BPDQ_W_Q8_PAD64 0
@@ -136,7 +139,7 @@ int bpd_llama_step_gpu(int weight_format, const LayerWeights* layers, const Mode
  * bpd_add_f32_cpu, :5466, in front).  The sum of squares is accumulated in
  * binary64 as the reference does; when the parallel sum cannot prove that the
  * reference's sequential binary64 sum rounds to the same fp32 mean, the kernel
- * recomputes it sequentially. */
+ * recomputes it sequentially.  fp32 pointers 16-byte aligned. */
 void bpd_residual_rmsnorm_gpu(const float* x_in, const float* add, float* x_out, const float* w, float* h,
                               uint8_t* xq, int n, float eps);
 /* expf of the decode step (the platform libm's, see bpdq_math.h) on n values. */

@@ -155,3 +155,25 @@ def test_rejects_bad_config(dev):
     m.layers[1].down_N = 128
     with pytest.raises(gpu.BpdqError, match="layer 1 down"):
         m.step(e, 0)
+
+
+@pytest.mark.parametrize("fmt", [llama.W_Q8_PAD64, llama.W_Q4K])
+def test_step_norm_fallback_row(dev, fmt):
+    """An embedding whose squares sum differently in a tree and in sequence
+    (x_0^2/n a binary32 midpoint, 255 squares of 2^-54): layer 0's RMSNorm must
+    take the sequential fallback of the norm kernel, with either weight format."""
+    cfg = LM.config(L=1)
+    e = np.full(cfg["n_embd"], 2.0 ** -27, np.float32)
+    e[0] = 1 + 2.0 ** -12
+    # every kernel's bound check fails here: (S -+ E)/n straddle an fp32 rounding boundary
+    S = float(np.sum(e.astype(np.float64) ** 2))
+    E = S * 4 * e.size * 2.0 ** -53
+    assert np.float32((S - E) / e.size) != np.float32((S + E) / e.size)
+    layers, head = LM.make(cfg, fmt, seed=12)
+    for lw in layers:
+        lw["attn_norm"] = np.ones(cfg["n_embd"], np.float32)
+    m = _gpu_model(cfg, layers, head, fmt, dev)
+    ko, vo = LM.caches(cfg)
+    want = O.llama_step(fmt, layers, cfg, ko, vo, 0, e, head["out_norm"], head["lm"], None, cfg["vocab_size"])
+    tok = m.step(_d(e, dev), 0)
+    _check_step(m, tok, want, (ko, vo), 0, f"fallback row fmt {fmt}")
