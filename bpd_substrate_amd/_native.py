@@ -80,6 +80,7 @@ HIP_SIGNATURES = {
     "bpd_llama_step_gpu": (I, [I, P, P, P, P, I, P, P, P, P, I, I]),
     "bpd_residual_rmsnorm_gpu": (None, [P, P, P, P, P, P, I, F]),
     "bpd_expf_gpu": (None, [P, P, I]),
+    "bpd_argmax_gpu": (None, [P, I, P]),
 }
 
 SYNTH_SIGNATURES = {

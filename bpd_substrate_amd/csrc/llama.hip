@@ -3,8 +3,12 @@
 // generate_token ABI of inference/llamatov_c_inference.py:15-83.
 //
 //   k_residual_rmsnorm  x = x_in (+ add); h = rmsnorm(x) * w; Q8_0(h)   one workgroup
-//   k_attn_decode       one workgroup per query head: q/k/v bias, RoPE (NORM pairs),
-//                       the K/V cache row write, scores, softmax, P.V, Q8_0(out)
+//   k_attn_small        attention for pos < 64: one workgroup per query head does q/k/v
+//                       bias, RoPE (NORM pairs), the K/V cache row write, scores,
+//                       softmax, P.V and Q8_0(out)
+//   k_attn_scores       longer contexts: bias, RoPE, cache row write and the scores,
+//                       spread over (head, 256-row) workgroups
+//   k_attn_pv           longer contexts: softmax and P.V per (head, 32 columns)
 //   k_swiglu            silu(gate) * up, Q8_0 (padded Q8 weights; with Q4_K the
 //                       gate/up GEMV applies it to its own outputs)
 //   k_argmax            first index of the maximum logit
@@ -38,11 +42,11 @@
 
 namespace bpdq {
 
-constexpr int kNormThreads = 1024;
-constexpr int kNormChunks = 16384 / (4 * kNormThreads);  // float4 chunks per thread for n <= kMaxEmbd
 constexpr int kMaxEmbd = 16384;  // the residual row stays in LDS (64 KB)
+constexpr int kNormThreads = 1024;
+constexpr int kNormChunks = kMaxEmbd / (4 * kNormThreads);  // float4 chunks per thread
 constexpr int kMaxHeadDim = 256;
-constexpr int kAttnThreads = 256;
+constexpr int kPvThreads = 256;
 constexpr int kMaxCtx = 32768;  // one head's scores stay in LDS (128 KB)
 
 // ----------------------------------------------------------------------------
@@ -156,88 +160,270 @@ struct RopeTab {
     float s[kMaxHeadDim / 2];
 };
 
-template <int NT>
-__global__ __launch_bounds__(NT) void k_attn_decode(const float* __restrict__ q, const float* __restrict__ knew,
-                                                    const float* __restrict__ vnew, const float* __restrict__ bq,
-                                                    const float* __restrict__ bk, const float* __restrict__ bv,
-                                                    float* __restrict__ kc, float* __restrict__ vc,
-                                                    float* __restrict__ out, uint8_t* __restrict__ xq, int group,
-                                                    int row, int D, int pos, float scale, RopeTab tab) {
-    extern __shared__ float e[];
-    __shared__ float4 qs4[kMaxHeadDim / 4], ks4[kMaxHeadDim / 4], vs4[kMaxHeadDim / 4];
-    __shared__ float red[NT / 64];
-    __shared__ float sh_inv;
-    const int tid = threadIdx.x, head = blockIdx.x, kvh = head / group, n = pos + 1;
-    float* qs = reinterpret_cast<float*>(qs4);
-    float* ks = reinterpret_cast<float*>(ks4);
-    float* vs = reinterpret_cast<float*>(vs4);
-    const int64_t qo = (int64_t)head * D, ko = (int64_t)kvh * D;
-    for (int p = tid; p < D / 2; p += NT) {
+struct AttnIn {
+    const float *q, *knew, *vnew;  // projections of this token (before bias and RoPE)
+    const float *bq, *bk, *bv;     // biases or NULL
+    float *kc, *vc;                // this layer's caches, [max_seq][row]
+    int group, row, D, pos;
+    float scale;
+};
+
+// Bias + RoPE of query head `head` into qs and, with `with_kv`, of the new k
+// row into ks and the new v row into vs (all LDS).
+__device__ __forceinline__ void rope_rows(const AttnIn& a, const RopeTab& tab, int head, int kvh, float* qs,
+                                          float* ks, float* vs, bool with_kv) {
+    const int64_t qo = (int64_t)head * a.D, ko = (int64_t)kvh * a.D;
+    for (int p = threadIdx.x; p < a.D / 2; p += blockDim.x) {
         const int i = 2 * p;
         const float c = tab.c[p], sn = tab.s[p];
-        float x0 = q[qo + i], x1 = q[qo + i + 1];
-        float k0 = knew[ko + i], k1 = knew[ko + i + 1];
-        if (bq != nullptr) {
-            x0 = x0 + bq[qo + i];
-            x1 = x1 + bq[qo + i + 1];
-        }
-        if (bk != nullptr) {
-            k0 = k0 + bk[ko + i];
-            k1 = k1 + bk[ko + i + 1];
+        float x0 = a.q[qo + i], x1 = a.q[qo + i + 1];
+        if (a.bq != nullptr) {
+            x0 = x0 + a.bq[qo + i];
+            x1 = x1 + a.bq[qo + i + 1];
         }
         qs[i] = x0 * c - x1 * sn;
         qs[i + 1] = x0 * sn + x1 * c;
-        ks[i] = k0 * c - k1 * sn;
-        ks[i + 1] = k0 * sn + k1 * c;
-    }
-    for (int d = tid; d < D; d += NT) {
-        float vv = vnew[ko + d];
-        if (bv != nullptr) vv = vv + bv[ko + d];
-        vs[d] = vv;
-    }
-    __syncthreads();
-    if (head % group == 0)
-        for (int d = tid; d < D; d += NT) {
-            kc[(int64_t)pos * row + ko + d] = ks[d];
-            vc[(int64_t)pos * row + ko + d] = vs[d];
-        }
-    float m = -1e38f;
-    for (int j = tid; j < n; j += NT) {
-        const float4* kr = reinterpret_cast<const float4*>(kc + (int64_t)j * row + ko);
-        float sc = 0.0f;
-        if (j < pos) {
-            for (int d4 = 0; d4 < D / 4; d4++) {
-                const float4 kv = kr[d4];
-                const float4 qv = qs4[d4];
-                sc = sc + qv.x * kv.x;
-                sc = sc + qv.y * kv.y;
-                sc = sc + qv.z * kv.z;
-                sc = sc + qv.w * kv.w;
+        if (with_kv) {
+            float k0 = a.knew[ko + i], k1 = a.knew[ko + i + 1];
+            if (a.bk != nullptr) {
+                k0 = k0 + a.bk[ko + i];
+                k1 = k1 + a.bk[ko + i + 1];
             }
-        } else {
-            for (int d4 = 0; d4 < D / 4; d4++) {
-                const float4 kv = ks4[d4];
-                const float4 qv = qs4[d4];
-                sc = sc + qv.x * kv.x;
-                sc = sc + qv.y * kv.y;
-                sc = sc + qv.z * kv.z;
-                sc = sc + qv.w * kv.w;
-            }
+            ks[i] = k0 * c - k1 * sn;
+            ks[i + 1] = k0 * sn + k1 * c;
         }
-        const float sv = sc * scale;
-        e[j] = sv;
-        m = sv > m ? sv : m;
     }
+    if (with_kv)
+        for (int d = threadIdx.x; d < a.D; d += blockDim.x) {
+            float vv = a.vnew[ko + d];
+            if (a.bv != nullptr) vv = vv + a.bv[ko + d];
+            vs[d] = vv;
+        }
+}
+
+// Cache row pos of the new k and v, written by the first query head of the group.
+__device__ __forceinline__ void write_new_row(const AttnIn& a, int head, int kvh, const float* ks, const float* vs) {
+    if (head % a.group != 0) return;
+    const int64_t o = (int64_t)a.pos * a.row + (int64_t)kvh * a.D;
+    for (int d = threadIdx.x; d < a.D; d += blockDim.x) {
+        a.kc[o + d] = ks[d];
+        a.vc[o + d] = vs[d];
+    }
+}
+
+// Sequential dot products of q with one k row: s = s + q_d * k_d, d ascending.
+__device__ __forceinline__ float dot_step(float s, float4 q, float4 k) {
+    s = s + q.x * k.x;
+    s = s + q.y * k.y;
+    s = s + q.z * k.z;
+    return s + q.w * k.w;
+}
+template <int D4>
+__device__ __forceinline__ float dot_regs(const float4* qs4, const float4 (&k)[D4]) {
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < D4; i++) s = dot_step(s, qs4[i], k[i]);
+    return s;
+}
+__device__ __forceinline__ float dot_ptr(const float4* qs4, const float4* k, int D4) {
+    float s = 0.0f;
+#pragma unroll 8
+    for (int i = 0; i < D4; i++) s = dot_step(s, qs4[i], k[i]);
+    return s;
+}
+
+// Block-wide max of the scaled scores, as the reference's scan keeps it
+// (start at -1e38, take v when v > max): exact in any order.
+template <int NT>
+__device__ __forceinline__ float block_max(float m, float* red) {
 #pragma unroll
     for (int mask = 32; mask >= 1; mask >>= 1) {
         const float o = xor_f(m, mask);
         m = o > m ? o : m;
     }
-    if ((tid & 63) == 0) red[tid >> 6] = m;
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
     __syncthreads();
     float mx = red[0];
 #pragma unroll
     for (int w = 1; w < NT / 64; w++) mx = red[w] > mx ? red[w] : mx;
+    return mx;
+}
+
+// ----------------------------------------------------------------------------
+// Short contexts (pos < 64, head_dim DT <= 128): one workgroup per query head.
+// Every cache load is issued at entry: thread j < pos loads k row j into
+// registers, and the V rows 0..pos-1 go to LDS, so the kernel waits for memory
+// once.  Then RoPE, scores, max, exps, the sequential softmax sum (lane 0) and
+// the sequential P.V chains (lane d) from LDS.
+// ----------------------------------------------------------------------------
+constexpr int kSmallCtx = 64;
+
+template <int DT>
+__global__ __launch_bounds__(256) void k_attn_small(AttnIn a, RopeTab tab, float* __restrict__ out,
+                                                    uint8_t* __restrict__ xq) {
+    constexpr int NT = 256, D4 = DT / 4, VU = (kSmallCtx * D4 + NT - 1) / NT;
+    __shared__ float4 qs4[D4], ks4[D4], vs4[D4];
+    __shared__ float4 V4[kSmallCtx * D4];
+    __shared__ float e[kSmallCtx];
+    __shared__ float red[NT / 64];
+    __shared__ float sh_inv;
+    const int tid = threadIdx.x, head = blockIdx.x, kvh = head / a.group, pos = a.pos, n = pos + 1;
+    const int64_t ko = (int64_t)kvh * DT;
+    float4 kr[D4];
+    if (tid < pos) {
+        const float4* p = reinterpret_cast<const float4*>(a.kc + (int64_t)tid * a.row + ko);
+#pragma unroll
+        for (int i = 0; i < D4; i++) kr[i] = p[i];
+    }
+#pragma unroll
+    for (int u = 0; u < VU; u++) {
+        const int f = tid + u * NT, r = f / D4;
+        if (r < pos) V4[f] = *reinterpret_cast<const float4*>(a.vc + (int64_t)r * a.row + ko + 4 * (f % D4));
+    }
+    float* qs = reinterpret_cast<float*>(qs4);
+    float* ks = reinterpret_cast<float*>(ks4);
+    float* vs = reinterpret_cast<float*>(vs4);
+    rope_rows(a, tab, head, kvh, qs, ks, vs, true);
+    __syncthreads();
+    write_new_row(a, head, kvh, ks, vs);
+    float m = -1e38f;
+    if (tid < n) {
+        const float sc = tid < pos ? dot_regs<D4>(qs4, kr) : dot_ptr(qs4, ks4, D4);
+        const float sv = sc * a.scale;
+        e[tid] = sv;
+        m = sv;
+    }
+    const float mx = block_max<NT>(m, red);
+    if (tid < n) e[tid] = expf_libm(e[tid] - mx);
+    __syncthreads();
+    if (tid == 0) {
+        float sum = 0.0f;
+        for (int j = 0; j < n; j++) sum = sum + e[j];
+        sh_inv = sum == 0.0f ? 0.0f : 1.0f / sum;
+    }
+    __syncthreads();
+    if (tid < DT) {
+        const float inv = sh_inv;
+        const float* Vf = reinterpret_cast<const float*>(V4);
+        float acc = 0.0f;
+        for (int j = 0; j < pos; j++) acc = acc + Vf[j * DT + tid] * (e[j] * inv);
+        acc = acc + vs[tid] * (e[pos] * inv);
+        const int64_t o = (int64_t)head * DT + tid;
+        out[o] = acc;
+        if (xq != nullptr) q8_0_lane_store(acc, xq + (o >> 5) * kQ80Bytes, tid & 31);
+    }
+}
+
+// ----------------------------------------------------------------------------
+// Longer contexts, two kernels.
+// k_attn_scores, grid (heads, ceil(n/256)): thread j of the grid's row range
+// computes v_j = (q . k_j) * scale for one row (its k row loaded whole into
+// registers when head_dim is DT) into sc[head][j]; the workgroup holding row pos
+// also ropes the new k row, scores it from LDS and, for the first head of each
+// group, writes the new k and v rows to the caches.
+// ----------------------------------------------------------------------------
+template <int DT>
+__global__ __launch_bounds__(256) void k_attn_scores(AttnIn a, RopeTab tab, float* __restrict__ sc, int ld) {
+    __shared__ float4 qs4[kMaxHeadDim / 4], ks4[kMaxHeadDim / 4], vs4[kMaxHeadDim / 4];
+    const int tid = threadIdx.x, head = blockIdx.x, kvh = head / a.group, pos = a.pos;
+    const int j = blockIdx.y * 256 + tid, D4 = a.D / 4;
+    const bool last = blockIdx.y == gridDim.y - 1;  // the block holding row pos
+    const int64_t ko = (int64_t)kvh * a.D;
+    constexpr int KR = DT > 0 ? DT / 4 : 1;
+    float4 kr[KR];
+    if (DT > 0 && j < pos) {
+        const float4* p = reinterpret_cast<const float4*>(a.kc + (int64_t)j * a.row + ko);
+#pragma unroll
+        for (int i = 0; i < KR; i++) kr[i] = p[i];
+    }
+    rope_rows(a, tab, head, kvh, reinterpret_cast<float*>(qs4), reinterpret_cast<float*>(ks4),
+              reinterpret_cast<float*>(vs4), last);
+    __syncthreads();
+    if (last) write_new_row(a, head, kvh, reinterpret_cast<float*>(ks4), reinterpret_cast<float*>(vs4));
+    if (j > pos) return;
+    float s;
+    if (j == pos)
+        s = dot_ptr(qs4, ks4, D4);
+    else if (DT > 0)
+        s = dot_regs<KR>(qs4, kr);
+    else
+        s = dot_ptr(qs4, reinterpret_cast<const float4*>(a.kc + (int64_t)j * a.row + ko), D4);
+    sc[(int64_t)head * ld + j] = s * a.scale;
+}
+
+// k_attn_pv, grid (heads, head_dim/32): softmax and P.V for 32 output columns
+// d0..d0+31 of one head.  The scores go to LDS; max, exps and w_j = e_j * inv
+// are parallel, the softmax sum runs in lane 0 and each output's chain in lane
+// d - d0 of wave 0, all in the reference's order.  The V columns stream
+// through a two-slot LDS ring of 64-row chunks: every thread keeps the loads of
+// the next 8 chunks in flight in registers and writes one chunk per step, one
+// barrier per chunk, so the chains read LDS instead of waiting on HBM.
+// ----------------------------------------------------------------------------
+constexpr int kPvRows = 64;   // rows per chunk
+constexpr int kPvAhead = 8;   // chunks in flight
+
+struct PvPipe {
+    const float* vbase;  // V column d0 of the head's kv row 0
+    int row, n, nch, tid;
+    bool chain;
+    const float* w;      // softmax weights in LDS
+};
+
+// Load of chunk c's share of thread tid: float4 number f = tid + k*NT is row
+// c*64 + f/8, columns d0 + 4(f%8)..+3; rows past n repeat row n-1 (never read
+// by the chains, so every load stays in the cache rows already written).
+template <int NT>
+__device__ __forceinline__ float4 pv_load(const PvPipe& p, int c, int k) {
+    const int f = p.tid + k * NT, r = min(c * kPvRows + f / 8, p.n - 1);
+    return *reinterpret_cast<const float4*>(p.vbase + (int64_t)r * p.row + 4 * (f % 8));
+}
+
+// Chunk c = c0 + U: its registers go to ring slot c&1 and are refilled with
+// chunk c + 8; barrier; lanes 0..31 of wave 0 extend their chains over its rows.
+// U is a template argument so that pf is indexed by constants only.
+template <int U, int NT, int PER>
+__device__ __forceinline__ void pv_chunk(const PvPipe& p, float4 (&pf)[kPvAhead * PER], float4 (*ring)[kPvRows * 8],
+                                         int c0, float& acc) {
+    const int c = c0 + U;
+    if (c < p.nch) {
+#pragma unroll
+        for (int k = 0; k < PER; k++) {
+            ring[c & 1][p.tid + k * NT] = pf[U * PER + k];
+            pf[U * PER + k] = pv_load<NT>(p, c + kPvAhead, k);
+        }
+    }
+    __syncthreads();
+    if (p.chain && c < p.nch) {
+        const float* col = reinterpret_cast<const float*>(ring[c & 1]) + p.tid;
+        const int rows = min(kPvRows, p.n - c * kPvRows);
+        const float* w = p.w + c * kPvRows;
+        for (int r = 0; r < rows; r++) acc = acc + col[32 * r] * w[r];
+    }
+}
+
+template <int NT>
+__global__ __launch_bounds__(NT) void k_attn_pv(AttnIn a, const float* __restrict__ sc, int ld,
+                                                float* __restrict__ out, uint8_t* __restrict__ xq) {
+    constexpr int PER = kPvRows * 8 / NT;  // float4 of a chunk per thread (a chunk: 64 rows x 8 float4)
+    extern __shared__ float e[];
+    __shared__ float4 ring[2][kPvRows * 8];
+    __shared__ float red[NT / 64];
+    __shared__ float sh_inv;
+    const int tid = threadIdx.x, head = blockIdx.x, kvh = head / a.group, n = a.pos + 1;
+    const int d0 = 32 * blockIdx.y, nch = (n + kPvRows - 1) / kPvRows;
+    const PvPipe pp{a.vc + (int64_t)kvh * a.D + d0, a.row, n, nch, tid, tid < 32, e};
+    float4 pf[kPvAhead * PER];
+#pragma unroll
+    for (int c = 0; c < kPvAhead; c++)
+#pragma unroll
+        for (int k = 0; k < PER; k++) pf[c * PER + k] = pv_load<NT>(pp, c, k);
+    float m = -1e38f;
+    for (int j = tid; j < n; j += NT) {
+        const float sv = sc[(int64_t)head * ld + j];
+        e[j] = sv;
+        m = sv > m ? sv : m;
+    }
+    const float mx = block_max<NT>(m, red);
     for (int j = tid; j < n; j += NT) e[j] = expf_libm(e[j] - mx);
     __syncthreads();
     if (tid == 0) {
@@ -248,17 +434,23 @@ __global__ __launch_bounds__(NT) void k_attn_decode(const float* __restrict__ q,
     }
     __syncthreads();
     const float inv = sh_inv;
-    // D <= NT and D % 32 == 0: lanes d < D are whole 32-lane Q8_0 blocks
-    const int d = tid;
-    if (d < D) {
-        const float* vcol = vc + ko + d;
-        float acc = 0.0f;
-#pragma unroll 8
-        for (int j = 0; j < pos; j++) acc = acc + vcol[(int64_t)j * row] * (e[j] * inv);
-        acc = acc + vs[d] * (e[pos] * inv);
-        const int64_t o = qo + d;
+    for (int j = tid; j < n; j += NT) e[j] = e[j] * inv;
+    float acc = 0.0f;
+    static_assert(kPvAhead == 8, "one pv_chunk call per chunk in flight");
+    for (int c0 = 0; c0 < nch; c0 += kPvAhead) {
+        pv_chunk<0, NT, PER>(pp, pf, ring, c0, acc);
+        pv_chunk<1, NT, PER>(pp, pf, ring, c0, acc);
+        pv_chunk<2, NT, PER>(pp, pf, ring, c0, acc);
+        pv_chunk<3, NT, PER>(pp, pf, ring, c0, acc);
+        pv_chunk<4, NT, PER>(pp, pf, ring, c0, acc);
+        pv_chunk<5, NT, PER>(pp, pf, ring, c0, acc);
+        pv_chunk<6, NT, PER>(pp, pf, ring, c0, acc);
+        pv_chunk<7, NT, PER>(pp, pf, ring, c0, acc);
+    }
+    if (pp.chain) {
+        const int64_t o = (int64_t)head * a.D + d0 + tid;
         out[o] = acc;
-        if (xq != nullptr) q8_0_lane_store(acc, xq + (o >> 5) * kQ80Bytes, d & 31);
+        if (xq != nullptr) q8_0_lane_store(acc, xq + (o >> 5) * kQ80Bytes, tid & 31);
     }
 }
 
@@ -287,20 +479,43 @@ __device__ __forceinline__ bool argmax_beats(float b, int bi, float a, int ai) {
     return b > a || (b == a && bi < ai);
 }
 
+__device__ __forceinline__ void argmax_take(float v, int i, float& best, int& idx) {
+    if (v == v && (idx == INT_MAX || v > best)) {
+        best = v;
+        idx = i;
+    }
+}
+
+// Each thread scans float4 chunks t, t + NT, ... (8 loads in flight), then the
+// n % 4 tail, so it meets its indices in increasing order and keeps the first
+// of equal values; lanes and waves then combine by (value, lower index).
 template <int NT>
 __global__ __launch_bounds__(NT) void k_argmax(const float* __restrict__ x, int n, int32_t* __restrict__ out) {
     __shared__ float bv[NT / 64];
     __shared__ int bi[NT / 64];
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, nc = n >> 2;
+    const float4* x4 = reinterpret_cast<const float4*>(x);
     float best = 0.0f;
     int idx = INT_MAX;  // no candidate yet
-    for (int i = tid; i < n; i += NT) {
-        const float v = x[i];
-        if (v == v && (idx == INT_MAX || v > best)) {
-            best = v;
-            idx = i;
+    for (int c0 = tid; c0 < nc; c0 += 8 * NT) {
+        float4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int c = c0 + u * NT;
+            v[u] = c < nc ? x4[c] : make_float4(__builtin_nanf(""), 0.0f, 0.0f, 0.0f);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int c = c0 + u * NT;
+            if (c < nc) {
+                argmax_take(v[u].x, 4 * c, best, idx);
+                argmax_take(v[u].y, 4 * c + 1, best, idx);
+                argmax_take(v[u].z, 4 * c + 2, best, idx);
+                argmax_take(v[u].w, 4 * c + 3, best, idx);
+            }
         }
     }
+    if (tid < (n & 3)) argmax_take(x[4 * nc + tid], 4 * nc + tid, best, idx);
 #pragma unroll
     for (int mask = 32; mask >= 1; mask >>= 1) {
         const float ob = xor_f(best, mask);
@@ -359,7 +574,7 @@ bool lds_limits_set(const char* fn) {
     static std::once_flag once;
     static hipError_t err = hipSuccess;
     std::call_once(once, [] {
-        err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_decode<kAttnThreads>),
+        err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_pv<kPvThreads>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, kMaxCtx * 4);
         if (err == hipSuccess)
             err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_residual_rmsnorm<kNormThreads, kNormChunks>),
@@ -550,8 +765,35 @@ struct StepCtx {
     hipStream_t s;
     RopeTab tab;
     float *x, *h, *qb, *kb, *vb, *att, *gate, *up, *ffn;
+    float* scores;      // [n_head][max_seq] scaled scores of the long-context attention
+    float attn_scale;   // 1 / sqrtf(head_dim), as the reference computes it
     uint8_t *xq_e, *xq_a, *xq_f;  // Q8_0 activations (padded Q8 weights only, else NULL)
 };
+
+// Attention over n_ctx = pos + 1 rows: one kernel while the context is short
+// and head_dim is 32, 64 or 128, else scores and softmax/P.V as two kernels.
+void attention(const StepCtx& c, const AttnIn& ai, int n_ctx) {
+    const Geometry& g = c.g;
+    if (n_ctx <= kSmallCtx && (g.D == 32 || g.D == 64 || g.D == 128)) {
+        if (g.D == 128)
+            hipLaunchKernelGGL(k_attn_small<128>, dim3(g.H), dim3(256), 0, c.s, ai, c.tab, c.att, c.xq_a);
+        else if (g.D == 64)
+            hipLaunchKernelGGL(k_attn_small<64>, dim3(g.H), dim3(256), 0, c.s, ai, c.tab, c.att, c.xq_a);
+        else
+            hipLaunchKernelGGL(k_attn_small<32>, dim3(g.H), dim3(256), 0, c.s, ai, c.tab, c.att, c.xq_a);
+        return;
+    }
+    const dim3 gs(g.H, (n_ctx + 255) / 256);
+    const int ld = c.cfg->max_seq;
+    if (g.D == 128)
+        hipLaunchKernelGGL(k_attn_scores<128>, gs, dim3(256), 0, c.s, ai, c.tab, c.scores, ld);
+    else if (g.D == 64)
+        hipLaunchKernelGGL(k_attn_scores<64>, gs, dim3(256), 0, c.s, ai, c.tab, c.scores, ld);
+    else
+        hipLaunchKernelGGL(k_attn_scores<0>, gs, dim3(256), 0, c.s, ai, c.tab, c.scores, ld);
+    hipLaunchKernelGGL(k_attn_pv<kPvThreads>, dim3(g.H, g.D / 32), dim3(kPvThreads), (size_t)n_ctx * 4, c.s, ai,
+                       c.scores, ld, c.att, c.xq_a);
+}
 
 // The layers.  The residual add is the first step of each RMSNorm kernel; the
 // norm, attention and SwiGLU kernels also write the Q8_0 bytes of their outputs
@@ -569,11 +811,11 @@ void run_layers(const StepCtx& c, const Gemv& gemv, const LayerWeights* layers, 
         float* yqkv[3] = {c.qb, c.kb, c.vb};
         const int nqkv[3] = {w.q_N, w.k_N, w.v_N};
         gemv.run(3, wqkv, yqkv, nqkv, c.h, c.xq_e, g.E);
-        hipLaunchKernelGGL(k_attn_decode<kAttnThreads>, dim3(g.H), dim3(kAttnThreads), (size_t)n_ctx * 4, c.s, c.qb,
-                           c.kb, c.vb, static_cast<const float*>(w.q_bias), static_cast<const float*>(w.k_bias),
-                           static_cast<const float*>(w.v_bias), static_cast<float*>(c.kv->k_cache[l]),
-                           static_cast<float*>(c.kv->v_cache[l]), c.att, c.xq_a, g.H / g.HKV, row, g.D, c.pos,
-                           1.0f / sqrtf((float)g.D), c.tab);
+        const AttnIn ai{c.qb, c.kb, c.vb,
+                        static_cast<const float*>(w.q_bias), static_cast<const float*>(w.k_bias),
+                        static_cast<const float*>(w.v_bias), static_cast<float*>(c.kv->k_cache[l]),
+                        static_cast<float*>(c.kv->v_cache[l]), g.H / g.HKV, row, g.D, c.pos, c.attn_scale};
+        attention(c, ai, n_ctx);
         const void* wo[1] = {w.o};
         float* yo[1] = {c.ffn};
         const int no[1] = {w.o_N};
@@ -610,12 +852,16 @@ bool enqueue_step(int fmt, const LayerWeights* layers, const ModelConfig* cfg, c
     const size_t front = q8 ? (2 * q8e + q8f + 255) & ~(size_t)255 : 0;
     const int kmax = g.F > g.E ? g.F : g.E;
     const size_t q8k = kmax > fused_max_k() ? (size_t)(kmax / 256) * kQ8KBytes : 0;
-    uint8_t* ws = step_workspace(front + q8k + 256, fn);
+    const size_t q8k_end = (front + q8k + 255) & ~(size_t)255;
+    const size_t sc_bytes = (size_t)g.H * cfg->max_seq * 4;
+    uint8_t* ws = step_workspace(q8k_end + sc_bytes, fn);
     if (ws == nullptr) return false;
     const Gemv gemv{fmt, ws + front, abi_stream()};
     c.cfg = cfg;
     c.kv = kv;
     c.pos = pos;
+    c.scores = reinterpret_cast<float*>(ws + q8k_end);
+    c.attn_scale = 1.0f / sqrtf((float)g.D);
     c.s = gemv.s;
     c.x = static_cast<float*>(buf->x);
     c.h = static_cast<float*>(buf->h);
@@ -731,6 +977,17 @@ void bpd_residual_rmsnorm_gpu(const float* x_in, const float* add, float* x_out,
     if (h) v.ptr(h, 16, "h");
     if (!v.ok || !bpdq::lds_limits_set(fn)) return;
     bpdq::launch_norm(x_in, add, x_out, w, h, xq, n, eps, bpdq::abi_stream());
+    bpdq::abi_hip_ok(hipGetLastError(), fn);
+}
+
+void bpd_argmax_gpu(const float* x, int n, int32_t* out) {
+    const char* fn = "bpd_argmax_gpu";
+    bpdq::V v{fn};
+    v.need(n > 0, BPDQ_ERR_SHAPE, "n must be positive");
+    v.ptr(x, 16, "x");
+    v.ptr(out, 4, "out");
+    if (!v.ok) return;
+    hipLaunchKernelGGL(bpdq::k_argmax<1024>, dim3(1), dim3(1024), 0, bpdq::abi_stream(), x, n, out);
     bpdq::abi_hip_ok(hipGetLastError(), fn);
 }
 

@@ -142,6 +142,10 @@ int bpd_llama_step_gpu(int weight_format, const LayerWeights* layers, const Mode
  * recomputes it sequentially.  fp32 pointers 16-byte aligned. */
 void bpd_residual_rmsnorm_gpu(const float* x_in, const float* add, float* x_out, const float* w, float* h,
                               uint8_t* xq, int n, float eps);
+/* out[0] = the step's argmax of x[n] (bpd_argmax_dim_cpu, bench/bpd_cpu.c:4512-4526,
+ * with outer = inner = 1): first index of the largest non-NaN value, 0 when x[0]
+ * is NaN.  x 16-byte aligned. */
+void bpd_argmax_gpu(const float* x, int n, int32_t* out);
 /* expf of the decode step (the platform libm's, see bpdq_math.h) on n values. */
 void bpd_expf_gpu(const float* x, float* y, int n);
 

@@ -125,11 +125,13 @@ def test_step_equals_restatement(dev, fmt, variant):
         _check_step(m, tok, want, (ko, vo), pos, f"fmt {fmt} {variant}")
 
 
-@pytest.mark.parametrize("pos", [255, 2047])
-def test_long_context(dev, pos):
+@pytest.mark.parametrize("D,pos", [(64, 63), (64, 64), (64, 255), (64, 2047), (128, 63), (128, 300),
+                                   (256, 40), (32, 1000)])
+def test_long_context(dev, D, pos):
     """Rows 0..pos-1 of the caches hold the same random finite data on both
-    sides; one step at `pos` then attends over pos+1 rows."""
-    cfg = LM.config(L=1, max_seq=2048, E=256, H=4, HKV=2, D=64)
+    sides; one step at `pos` then attends over pos+1 rows (one attention kernel
+    up to 64 rows for head_dim <= 128, the scores + P.V pair beyond)."""
+    cfg = LM.config(L=1, max_seq=2048, E=4 * D, H=4, HKV=2, D=D)
     layers, head = LM.make(cfg, 0, seed=5)
     m = _gpu_model(cfg, layers, head, llama.W_Q8_PAD64, dev)
     ko, vo = LM.caches(cfg)
@@ -177,3 +179,27 @@ def test_step_norm_fallback_row(dev, fmt):
     want = O.llama_step(fmt, layers, cfg, ko, vo, 0, e, head["out_norm"], head["lm"], None, cfg["vocab_size"])
     tok = m.step(_d(e, dev), 0)
     _check_step(m, tok, want, (ko, vo), 0, f"fallback row fmt {fmt}")
+
+
+@pytest.mark.parametrize("n", [1, 3, 4, 7, 1000, 4097, 32000, 128256])
+def test_argmax_equals_reference(dev, n):
+    rng = np.random.default_rng(n)
+    cases = [rng.normal(0, 1, n).astype(np.float32), np.zeros(n, np.float32),
+             np.round(rng.normal(0, 2, n)).astype(np.float32)]        # many ties
+    x = rng.normal(0, 1, n).astype(np.float32)
+    x[rng.integers(0, n, max(1, n // 10))] = np.nan                  # NaNs anywhere
+    cases.append(x)
+    x = cases[0].copy()
+    x[0] = np.nan                                                     # NaN first: index 0
+    cases.append(x)
+    x = -np.zeros(n, np.float32)
+    x[n // 2] = 0.0                                                   # +0 does not beat -0
+    cases.append(x)
+    x = np.full(n, -np.inf, np.float32)
+    x[-1] = -1e30                                                     # last element, tail lane
+    cases.append(x)
+    out = torch.zeros(1, dtype=torch.int32, device=dev)
+    for i, x in enumerate(cases):
+        gpu._use_torch_stream()
+        gpu.call("bpd_argmax_gpu", _d(x, dev), n, out)
+        assert int(out.item()) == O.argmax(x), (n, i)
