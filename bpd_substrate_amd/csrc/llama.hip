@@ -249,6 +249,28 @@ __device__ __forceinline__ float block_max(float m, float* red) {
     return mx;
 }
 
+// The softmax denominator in one lane: sum = sum + e_j for j = 0..n-1, read
+// from LDS four at a time with 8 reads in flight (e 16-byte aligned).
+__device__ __forceinline__ float seq_sum(const float* __restrict__ e, int n) {
+    const float4* e4 = reinterpret_cast<const float4*>(e);
+    float sum = 0.0f;
+    int j = 0;
+    for (; j + 32 <= n; j += 32) {
+        float4 v[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = e4[j / 4 + i];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            sum = sum + v[i].x;
+            sum = sum + v[i].y;
+            sum = sum + v[i].z;
+            sum = sum + v[i].w;
+        }
+    }
+    for (; j < n; j++) sum = sum + e[j];
+    return sum;
+}
+
 // ----------------------------------------------------------------------------
 // Short contexts (pos < 64, head_dim DT <= 128): one workgroup per query head.
 // Every cache load is issued at entry: thread j < pos loads k row j into
@@ -264,7 +286,7 @@ __global__ __launch_bounds__(256) void k_attn_small(AttnIn a, RopeTab tab, float
     constexpr int NT = 256, D4 = DT / 4, VU = (kSmallCtx * D4 + NT - 1) / NT;
     __shared__ float4 qs4[D4], ks4[D4], vs4[D4];
     __shared__ float4 V4[kSmallCtx * D4];
-    __shared__ float e[kSmallCtx];
+    __shared__ __align__(16) float e[kSmallCtx];
     __shared__ float red[NT / 64];
     __shared__ float sh_inv;
     const int tid = threadIdx.x, head = blockIdx.x, kvh = head / a.group, pos = a.pos, n = pos + 1;
@@ -297,8 +319,7 @@ __global__ __launch_bounds__(256) void k_attn_small(AttnIn a, RopeTab tab, float
     if (tid < n) e[tid] = expf_libm(e[tid] - mx);
     __syncthreads();
     if (tid == 0) {
-        float sum = 0.0f;
-        for (int j = 0; j < n; j++) sum = sum + e[j];
+        const float sum = seq_sum(e, n);
         sh_inv = sum == 0.0f ? 0.0f : 1.0f / sum;
     }
     __syncthreads();
@@ -361,6 +382,7 @@ __global__ __launch_bounds__(256) void k_attn_scores(AttnIn a, RopeTab tab, floa
 // ----------------------------------------------------------------------------
 constexpr int kPvRows = 64;   // rows per chunk
 constexpr int kPvAhead = 8;   // chunks in flight
+constexpr int kPvLd = kPvRows + 4;  // ring row pitch in floats: column d of a chunk is one padded row
 
 struct PvPipe {
     const float* vbase;  // V column d0 of the head's kv row 0
@@ -378,26 +400,48 @@ __device__ __forceinline__ float4 pv_load(const PvPipe& p, int c, int k) {
     return *reinterpret_cast<const float4*>(p.vbase + (int64_t)r * p.row + 4 * (f % 8));
 }
 
-// Chunk c = c0 + U: its registers go to ring slot c&1 and are refilled with
-// chunk c + 8; barrier; lanes 0..31 of wave 0 extend their chains over its rows.
-// U is a template argument so that pf is indexed by constants only.
+// Chunk c = c0 + U: its registers, times their rows' weights, go to ring slot
+// c&1 (the reference's RN(v_jd * w_j)), transposed so that column d is one
+// padded LDS row, and are refilled with chunk c + 8; barrier; lane d - d0 of
+// wave 0 reads its 64 products as 16 float4 and extends its chain,
+// acc = RN(acc + p_j), rows in order.  U is a template argument so that pf is
+// indexed by constants only.
 template <int U, int NT, int PER>
-__device__ __forceinline__ void pv_chunk(const PvPipe& p, float4 (&pf)[kPvAhead * PER], float4 (*ring)[kPvRows * 8],
+__device__ __forceinline__ void pv_chunk(const PvPipe& p, float4 (&pf)[kPvAhead * PER], float (*ring)[32 * kPvLd],
                                          int c0, float& acc) {
     const int c = c0 + U;
     if (c < p.nch) {
 #pragma unroll
         for (int k = 0; k < PER; k++) {
-            ring[c & 1][p.tid + k * NT] = pf[U * PER + k];
+            const int f = p.tid + k * NT, rr = f / 8, q4 = 4 * (f % 8), r = c * kPvRows + rr;
+            const float w = r < p.n ? p.w[r] : 0.0f;
+            const float4 v = pf[U * PER + k];
+            float* dst = ring[c & 1] + q4 * kPvLd + rr;
+            dst[0] = v.x * w;
+            dst[kPvLd] = v.y * w;
+            dst[2 * kPvLd] = v.z * w;
+            dst[3 * kPvLd] = v.w * w;
             pf[U * PER + k] = pv_load<NT>(p, c + kPvAhead, k);
         }
     }
     __syncthreads();
     if (p.chain && c < p.nch) {
-        const float* col = reinterpret_cast<const float*>(ring[c & 1]) + p.tid;
+        const float* col = ring[c & 1] + p.tid * kPvLd;
         const int rows = min(kPvRows, p.n - c * kPvRows);
-        const float* w = p.w + c * kPvRows;
-        for (int r = 0; r < rows; r++) acc = acc + col[32 * r] * w[r];
+        if (rows == kPvRows) {
+            float4 t[kPvRows / 4];
+#pragma unroll
+            for (int i = 0; i < kPvRows / 4; i++) t[i] = reinterpret_cast<const float4*>(col)[i];
+#pragma unroll
+            for (int i = 0; i < kPvRows / 4; i++) {
+                acc = acc + t[i].x;
+                acc = acc + t[i].y;
+                acc = acc + t[i].z;
+                acc = acc + t[i].w;
+            }
+        } else {
+            for (int r = 0; r < rows; r++) acc = acc + col[r];
+        }
     }
 }
 
@@ -405,36 +449,48 @@ template <int NT>
 __global__ __launch_bounds__(NT) void k_attn_pv(AttnIn a, const float* __restrict__ sc, int ld,
                                                 float* __restrict__ out, uint8_t* __restrict__ xq) {
     constexpr int PER = kPvRows * 8 / NT;  // float4 of a chunk per thread (a chunk: 64 rows x 8 float4)
-    extern __shared__ float e[];
-    __shared__ float4 ring[2][kPvRows * 8];
+    extern __shared__ float4 e4dyn[];
+    float* e = reinterpret_cast<float*>(e4dyn);
+    __shared__ __align__(16) float ring[2][32 * kPvLd];
     __shared__ float red[NT / 64];
     __shared__ float sh_inv;
     const int tid = threadIdx.x, head = blockIdx.x, kvh = head / a.group, n = a.pos + 1;
     const int d0 = 32 * blockIdx.y, nch = (n + kPvRows - 1) / kPvRows;
+    // the scores first, 8 loads in flight (loads complete in order, so anything
+    // issued before them would be waited for too), then the first V chunks,
+    // which stream in while the softmax runs
+    float m = -1e38f;
+    const float* scr = sc + (int64_t)head * ld;
+    for (int j0 = tid; j0 < n; j0 += 8 * NT) {
+        float t[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) t[u] = scr[min(j0 + u * NT, n - 1)];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int j = j0 + u * NT;
+            if (j < n) {
+                e[j] = t[u];
+                m = t[u] > m ? t[u] : m;
+            }
+        }
+    }
     const PvPipe pp{a.vc + (int64_t)kvh * a.D + d0, a.row, n, nch, tid, tid < 32, e};
     float4 pf[kPvAhead * PER];
 #pragma unroll
     for (int c = 0; c < kPvAhead; c++)
 #pragma unroll
         for (int k = 0; k < PER; k++) pf[c * PER + k] = pv_load<NT>(pp, c, k);
-    float m = -1e38f;
-    for (int j = tid; j < n; j += NT) {
-        const float sv = sc[(int64_t)head * ld + j];
-        e[j] = sv;
-        m = sv > m ? sv : m;
-    }
     const float mx = block_max<NT>(m, red);
     for (int j = tid; j < n; j += NT) e[j] = expf_libm(e[j] - mx);
     __syncthreads();
     if (tid == 0) {
-        float sum = 0.0f;
-#pragma unroll 8
-        for (int j = 0; j < n; j++) sum = sum + e[j];
+        const float sum = seq_sum(e, n);
         sh_inv = sum == 0.0f ? 0.0f : 1.0f / sum;
     }
     __syncthreads();
     const float inv = sh_inv;
     for (int j = tid; j < n; j += NT) e[j] = e[j] * inv;
+    __syncthreads();  // the producers read other threads' weights
     float acc = 0.0f;
     static_assert(kPvAhead == 8, "one pv_chunk call per chunk in flight");
     for (int c0 = 0; c0 < nch; c0 += kPvAhead) {
