@@ -3,8 +3,13 @@
 //   k_dequant_q8_0        Q8_0 -> fp32                       (bench/bpd_cpu.c:3960-3973)
 //   k_embed_q8_0          row gather + dequant               (bench/bpd_cpu.c:4002-4013)
 //   k_quant_q8_0          fp32 -> Q8_0                       (bench/bpd_cpu.c:4106-4136)
-//   k_q8_0_gemm_T         Q8_0 x Q8_0 cells in the AVX1 llamafile tile order
-//                         (bench/bpd_gemm_q8_0_cpu.c:32-86), any number of tokens
+//   k_q8_0_gemv_T         Q8_0 x Q8_0 cells in the AVX1 llamafile tile order
+//                         (bench/bpd_gemm_q8_0_cpu.c:32-86), pipelined chains
+//   k_q8_0_gemv_TP        the same cells, block products by producer waves and the
+//                         chains from LDS (few rows, long rows)
+//   k_q8_0_gemm_T         the same cells, plain, for rows too long to stage
+//   k_q8_pad64            fp32 -> the padded Q8 layout (inference/llamatov_c_inference.py:88-100)
+//   k_q8_0_gemm_S(H)      the scalar order S on int8 MFMA (prefill)
 #include "bpdq_device.h"
 #include "bpdq_launch.h"
 
@@ -119,6 +124,35 @@ __device__ __forceinline__ float accumulate_batch(const WBatch<U>& w, const uint
     return acc;
 }
 
+// The token's activation row into LDS: xs[b*8 + L] = quant dword L of block b,
+// xd[b] = its scale as fp32.  Each pass issues all its loads (8 per thread)
+// before storing any, so staging costs one memory latency per 8*NT dwords
+// instead of one per loop trip.
+template <int NT>
+__device__ __forceinline__ void stage_x(uint32_t* __restrict__ xs, float* __restrict__ xd,
+                                        const uint8_t* __restrict__ xr, int nb) {
+    const int n = nb * 8;
+    for (int i0 = threadIdx.x; i0 < n; i0 += 8 * NT) {
+        uint32_t v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int i = min(i0 + u * NT, n - 1);
+            v[u] = ld_u32(xr + (int64_t)(i >> 3) * kQ80Bytes + 2 + 4 * (i & 7));
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (i0 + u * NT < n) xs[i0 + u * NT] = v[u];
+    }
+    for (int i0 = threadIdx.x; i0 < nb; i0 += 8 * NT) {
+        uint32_t v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = ld_u16(xr + (int64_t)min(i0 + u * NT, nb - 1) * kQ80Bytes);
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+            if (i0 + u * NT < nb) xd[i0 + u * NT] = f16_ieee(v[u]);
+    }
+}
+
 // LAYOUT 0: W is rows of 34-byte Q8_0 blocks.  LAYOUT 1: W is the padded
 // block-major layout of inference/llamatov_c_inference.py:88-100, records of 64
 // bytes [block][row] with d at bytes 0-1 and the quants at 4-35; the cells and
@@ -145,9 +179,7 @@ __global__ __launch_bounds__(64 * WPB) void k_q8_0_gemv_T(const uint8_t* __restr
 
     WBatch<U> a, b;
     load_batch<U, LAYOUT>(a, wbase, voff, doff, 0, nb, bstride);
-    const uint8_t* xr = Xq + (int64_t)tok * bpr;
-    for (int i = threadIdx.x; i < nb * 8; i += 64 * WPB) xs[i] = ld_u32(xr + (int64_t)(i >> 3) * kQ80Bytes + 2 + 4 * (i & 7));
-    for (int i = threadIdx.x; i < nb; i += 64 * WPB) xd[i] = f16_ieee(ld_u16(xr + (int64_t)i * kQ80Bytes));
+    stage_x<64 * WPB>(xs, xd, Xq + (int64_t)tok * bpr, nb);
     __syncthreads();
 
     float acc = 0.0f;
@@ -161,6 +193,161 @@ __global__ __launch_bounds__(64 * WPB) void k_q8_0_gemv_T(const uint8_t* __restr
     acc = acc + xor_f(acc, 2);
     acc = acc + xor_f(acc, 1);
     if (L == 0 && row < m_weight) out[(int64_t)tok * m_weight + row] = acc;
+}
+
+// ----------------------------------------------------------------------------
+// The same order T with the memory latency taken off the chains: a workgroup
+// holds 8 weight rows of one token and has 5 waves.  Waves 1-4 (producers)
+// compute the block products RN(RN(Ad*Bd) * float(p_L)) of 32-block chunks,
+// one lane per (row, block) of a chunk, all 8 partials L of it from the block's
+// 34 bytes (8 dword loads and one 16-bit load, re-aligned with v_alignbit for
+// even blocks of the 34-byte layout), with the loads of the next 8 chunks in
+// flight in registers, and write them to a two-slot LDS array; wave 0
+// (consumer) lane (row, L) runs the reference's accumulator chain
+// acc_L = prod + acc_L over the products in block order, and combines the 8
+// lanes of a row as k_q8_0_gemv_T does.  The chain lanes only add, so the
+// kernel streams the weights at the rate the producers keep in flight instead
+// of one load latency per block.  One barrier per chunk.
+// ----------------------------------------------------------------------------
+constexpr int kTpChunk = 32;          // blocks per chunk
+constexpr int kTpLd = kTpChunk + 4;   // product row pitch (floats), float4-aligned
+constexpr int kTpAhead = 8;           // chunks in flight per producer lane
+
+struct TpLoad {
+    uint32_t w[8];  // LAYOUT 1 and odd blocks: quant dwords; even blocks: raw dwords from the block start
+    uint32_t e;     // the 16-bit word w leaves out: the scale, or (even blocks) quant bytes 30-31 of L = 7
+};
+
+struct TpLane {
+    const uint8_t* rowbase;  // this producer lane's weight row, block 0
+    int64_t bstride;         // bytes from block b to block b+1 of the row
+    int j, row8, nb;         // block within a chunk, row within the workgroup * 8
+};
+
+template <int LAYOUT>
+__device__ __forceinline__ void tp_load(TpLoad& t, const TpLane& p, int c) {
+    const int b = min(c * kTpChunk + p.j, p.nb - 1);
+    const uint8_t* blk = p.rowbase + (int64_t)b * p.bstride;
+    if (LAYOUT == 1 || (b & 1)) {
+        // quant dword L at byte 2+4L (34-byte blocks, odd b: 4-byte aligned) or 4+4L (padded)
+        const uint8_t* qp = blk + (LAYOUT == 0 ? 2 : 4);
+#pragma unroll
+        for (int k = 0; k < 8; k++) t.w[k] = ld_u32(qp + 4 * k);
+        t.e = ld_u16(blk);
+    } else {
+        // even b of the 34-byte layout: dwords at the (aligned) block start, then bytes 32-33
+#pragma unroll
+        for (int k = 0; k < 8; k++) t.w[k] = ld_u32(blk + 4 * k);
+        t.e = ld_u16(blk + 32);
+    }
+}
+
+template <int LAYOUT>
+__device__ __forceinline__ void tp_products(const TpLoad& t, const TpLane& p, float* __restrict__ prod,
+                                            const uint32_t* __restrict__ xs, const float* __restrict__ xd, int c) {
+    const int b = c * kTpChunk + p.j;
+    if (b >= p.nb) return;
+    const bool aligned = LAYOUT == 1 || (b & 1);
+    const uint32_t dbits = aligned ? t.e : (t.w[0] & 0xFFFFu);
+    const float scale = f16_ieee(dbits) * xd[b];
+#pragma unroll
+    for (int L = 0; L < 8; L++) {
+        uint32_t q;
+        if (aligned)
+            q = t.w[L];
+        else
+            q = __builtin_amdgcn_alignbit(L < 7 ? t.w[L + 1] : t.e, t.w[L], 16);
+        const int s = sdot4(q, xs[b * 8 + L], 0);
+        prod[(p.row8 + L) * kTpLd + p.j] = scale * (float)s;
+    }
+}
+
+// Step c = c0 + U: producers turn chunk c+1 (register slot (U+1)%8) into
+// products and refill that slot with chunk c+9; the consumer adds chunk c.
+// U is a template argument so that the register slots are indexed by constants.
+template <int U, int LAYOUT>
+__device__ __forceinline__ void tp_step(TpLoad (&regs)[kTpAhead], const TpLane& p, bool producer,
+                                        float (*prod)[64 * kTpLd], const uint32_t* __restrict__ xs,
+                                        const float* __restrict__ xd, int c0, int nch, float& acc) {
+    constexpr int S = (U + 1) % kTpAhead;
+    const int c = c0 + U;
+    if (producer && c + 1 < nch) {
+        tp_products<LAYOUT>(regs[S], p, prod[(c + 1) & 1], xs, xd, c + 1);
+        if (c + 1 + kTpAhead < nch) tp_load<LAYOUT>(regs[S], p, c + 1 + kTpAhead);
+    }
+    if (!producer && c < nch) {
+        const float* f = prod[c & 1] + threadIdx.x * kTpLd;
+        const int nblk = min(kTpChunk, p.nb - c * kTpChunk);
+        if (nblk == kTpChunk) {
+            float4 t[kTpChunk / 4];
+#pragma unroll
+            for (int i = 0; i < kTpChunk / 4; i++) t[i] = reinterpret_cast<const float4*>(f)[i];
+#pragma unroll
+            for (int i = 0; i < kTpChunk / 4; i++) {
+                acc = t[i].x + acc;
+                acc = t[i].y + acc;
+                acc = t[i].z + acc;
+                acc = t[i].w + acc;
+            }
+        } else {
+            for (int j = 0; j < nblk; j++) acc = f[j] + acc;
+        }
+    }
+    __syncthreads();
+}
+
+template <int LAYOUT>
+__global__ __launch_bounds__(320) void k_q8_0_gemv_TP(const uint8_t* __restrict__ W, const uint8_t* __restrict__ Xq,
+                                                       float* __restrict__ out, int m_weight, int nb) {
+    extern __shared__ uint32_t lds[];
+    uint32_t* xs = lds;                                   // [nb][8] activation quants
+    float* xd = reinterpret_cast<float*>(lds + nb * 8);   // [nb] activation scales
+    __shared__ __align__(16) float prod[2][64 * kTpLd];
+    const int tid = threadIdx.x, tok = blockIdx.y, row0 = blockIdx.x * 8;
+    const bool producer = tid >= 64;
+    const int pp = producer ? tid - 64 : 0;
+    TpLane p;
+    p.j = pp & 31;
+    p.row8 = (pp >> 5) * 8;
+    p.nb = nb;
+    const int row = min(row0 + (pp >> 5), m_weight - 1);  // rows past the end reuse the last row (outputs discarded)
+    p.rowbase = W + (int64_t)row * (LAYOUT == 0 ? (int64_t)nb * kQ80Bytes : 64);
+    p.bstride = LAYOUT == 0 ? kQ80Bytes : (int64_t)m_weight * 64;
+    const int nch = (nb + kTpChunk - 1) / kTpChunk;
+    // loads return in order, so: chunk 0, then the activation row (the first
+    // barrier waits for it), then the rest of the prefetch
+    TpLoad regs[kTpAhead];
+    if (producer) {
+#pragma unroll
+        for (int c = 0; c < kTpAhead; c++)
+            if (c < nch) tp_load<LAYOUT>(regs[c], p, c);
+    }
+    stage_x<320>(xs, xd, Xq + (int64_t)tok * nb * kQ80Bytes, nb);
+    __syncthreads();
+    if (producer) {
+        tp_products<LAYOUT>(regs[0], p, prod[0], xs, xd, 0);
+        if (kTpAhead < nch) tp_load<LAYOUT>(regs[0], p, kTpAhead);
+    }
+    __syncthreads();
+    float acc = 0.0f;
+    static_assert(kTpAhead == 8, "one tp_step per register slot");
+    for (int c0 = 0; c0 < nch; c0 += kTpAhead) {
+        tp_step<0, LAYOUT>(regs, p, producer, prod, xs, xd, c0, nch, acc);
+        tp_step<1, LAYOUT>(regs, p, producer, prod, xs, xd, c0, nch, acc);
+        tp_step<2, LAYOUT>(regs, p, producer, prod, xs, xd, c0, nch, acc);
+        tp_step<3, LAYOUT>(regs, p, producer, prod, xs, xd, c0, nch, acc);
+        tp_step<4, LAYOUT>(regs, p, producer, prod, xs, xd, c0, nch, acc);
+        tp_step<5, LAYOUT>(regs, p, producer, prod, xs, xd, c0, nch, acc);
+        tp_step<6, LAYOUT>(regs, p, producer, prod, xs, xd, c0, nch, acc);
+        tp_step<7, LAYOUT>(regs, p, producer, prod, xs, xd, c0, nch, acc);
+    }
+    if (!producer) {
+        acc = acc + xor_f(acc, 4);
+        acc = acc + xor_f(acc, 2);
+        acc = acc + xor_f(acc, 1);
+        const int orow = row0 + (tid >> 3);
+        if ((tid & 7) == 0 && orow < m_weight) out[(int64_t)tok * m_weight + orow] = acc;
+    }
 }
 
 // Plain form of the same order for activation rows too long to stage in LDS.
@@ -220,11 +407,17 @@ static void dispatch_T(const uint8_t* Wq, const uint8_t* Xq, float* out, int m_w
                            m_weight, nb);
         return;
     }
-    // shapes measured on MI355X: 16-block batches and 4 waves per workgroup when
-    // there are many waves; fewer, longer chains prefer 32-block batches, 2 waves
+    // shapes measured on MI355X (graph, weights beyond the MALL): with many waves
+    // the pipelined kernel with 16-block batches and 4 waves per workgroup
+    // (14336x4096: 20.4 us vs 37.3 for the producer/consumer kernel); with fewer
+    // waves the producer/consumer kernel (4096x14336: 24.8 us vs 38.6 for 32-block
+    // batches; 4096x4096: 10.4 vs 13.1; 1024x4096: 7.0 vs 12.5)
     if (waves * m_tokens >= 1024)
         hipLaunchKernelGGL((k_q8_0_gemv_T<16, 4, LAYOUT>), dim3((waves + 3) / 4, m_tokens), dim3(256), lds, s, Wq, Xq,
                            out, m_weight, nb);
+    else if (lds + sizeof(float) * 2 * 64 * kTpLd <= 64 * 1024)
+        hipLaunchKernelGGL((k_q8_0_gemv_TP<LAYOUT>), dim3((m_weight + 7) / 8, m_tokens), dim3(320), lds, s, Wq, Xq, out,
+                           m_weight, nb);
     else
         hipLaunchKernelGGL((k_q8_0_gemv_T<32, 2, LAYOUT>), dim3((waves + 1) / 2, m_tokens), dim3(128), lds, s, Wq,
                            Xq, out, m_weight, nb);

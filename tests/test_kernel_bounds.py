@@ -116,7 +116,34 @@ def q8_gemv_config(mw, mt, K):
         return ("plain", 4, 1)
     if waves * mt >= 1024:
         return ("pipelined", 4, 16)
+    if nb * 36 + 2 * 64 * 36 * 4 <= 64 * 1024:
+        return ("producer", 5, 32)
     return ("pipelined", 2, 32)
+
+
+def check_producer(mw, mt, nb, layout, w_size):
+    """k_q8_0_gemv_TP: producer lane p of workgroup g reads block min(c*32 + p%32,
+    nb-1) of row min(8g + p/32, mw-1) for chunks c < nch, bytes [blk, blk+34)
+    (34-byte blocks: 8 dwords from blk+2 for odd b, from blk for even b, plus a
+    16-bit word at blk or blk+32) or [blk, blk+36) (padded records)."""
+    nch = (nb + 31) // 32
+    groups = (mw + 7) // 8
+    p = np.arange(256)
+    for g in sorted({0, groups - 1}):
+        row = np.minimum(8 * g + (p >> 5), mw - 1)
+        for c in range(nch):
+            b = np.minimum(c * 32 + (p & 31), nb - 1)
+            if layout == 0:
+                blk = row * nb * Q80 + b * Q80
+                lo, hi = blk, blk + 34
+            else:
+                blk = b * mw * 64 + row * 64
+                lo, hi = blk, blk + 36
+            assert lo.min() >= 0 and hi.max() <= w_size
+        # products: (row8 + L) * 36 + j inside the two 64 x 36 slots; consumer lane t reads t*36 .. +32
+        assert ((p >> 5) * 8 + 7) .max() * 36 + 31 < 64 * 36
+        orow = 8 * g + (np.arange(64) >> 3)
+        assert ((orow[orow < mw]) * 4 + 4).max(initial=0) <= mw * 4
 
 
 @pytest.mark.parametrize("mw,mt,K", [(14336, 1, 4096), (4096, 1, 14336), (4, 2, 128), (7, 5, 128), (9, 7, 128),
@@ -130,6 +157,11 @@ def test_q8_0_gemv_T_in_bounds(mw, mt, K):
     if cfg is None:
         return
     kind, WPB, U = cfg
+    if kind == "producer":
+        check_producer(mw, mt, nb, 0, w_size)
+        for tok in range(mt):
+            assert tok * bpr + (nb - 1) * Q80 + 2 + 28 + 4 <= x_size
+        return
     waves = (mw + 7) // 8
     grid = (waves + WPB - 1) // WPB if kind == "pipelined" else (waves + 3) // 4
     l = lanes()
@@ -298,6 +330,9 @@ def test_q8_pad64_gemv_in_bounds(mw, mt, K):
     nb = K // 32
     w_size = nb * mw * 64
     kind, WPB, U = cfg
+    if kind == "producer":
+        check_producer(mw, mt, nb, 1, w_size)
+        return
     waves = (mw + 7) // 8
     grid = (waves + WPB - 1) // WPB if kind == "pipelined" else (waves + 3) // 4
     l = lanes()
