@@ -316,13 +316,16 @@ __global__ __launch_bounds__(320) void k_q8_0_gemv_TP(const uint8_t* __restrict_
     const int nch = (nb + kTpChunk - 1) / kTpChunk;
     // loads return in order, so: chunk 0, then the activation row (the first
     // barrier waits for it), then the rest of the prefetch
+    // the activation row first (an L2 hit for every workgroup but the first few),
+    // then the weight prefetch: loads return in order, so staging issued after
+    // the prefetch would wait for all of it
+    stage_x<320>(xs, xd, Xq + (int64_t)tok * nb * kQ80Bytes, nb);
     TpLoad regs[kTpAhead];
     if (producer) {
 #pragma unroll
         for (int c = 0; c < kTpAhead; c++)
             if (c < nch) tp_load<LAYOUT>(regs[c], p, c);
     }
-    stage_x<320>(xs, xd, Xq + (int64_t)tok * nb * kQ80Bytes, nb);
     __syncthreads();
     if (producer) {
         tp_products<LAYOUT>(regs[0], p, prod[0], xs, xd, 0);
@@ -409,9 +412,9 @@ static void dispatch_T(const uint8_t* Wq, const uint8_t* Xq, float* out, int m_w
     }
     // shapes measured on MI355X (graph, weights beyond the MALL): with many waves
     // the pipelined kernel with 16-block batches and 4 waves per workgroup
-    // (14336x4096: 20.4 us vs 37.3 for the producer/consumer kernel); with fewer
-    // waves the producer/consumer kernel (4096x14336: 24.8 us vs 38.6 for 32-block
-    // batches; 4096x4096: 10.4 vs 13.1; 1024x4096: 7.0 vs 12.5)
+    // (14336x4096: 20.1 us vs 32.0 for the producer/consumer kernel); with fewer
+    // waves the producer/consumer kernel (4096x14336: 24.2 us vs 38.4 for 32-block
+    // batches; 4096x4096: 9.2 vs 13.0; 1024x4096: 6.7 vs 12.5)
     if (waves * m_tokens >= 1024)
         hipLaunchKernelGGL((k_q8_0_gemv_T<16, 4, LAYOUT>), dim3((waves + 3) / 4, m_tokens), dim3(256), lds, s, Wq, Xq,
                            out, m_weight, nb);
