@@ -8,7 +8,8 @@
 //                       softmax, P.V and Q8_0(out)
 //   k_attn_scores       longer contexts: bias, RoPE, cache row write and the scores,
 //                       spread over (head, 256-row) workgroups
-//   k_attn_pv           longer contexts: softmax and P.V per (head, 32 columns)
+//   k_attn_pv           longer contexts: softmax and P.V per (head, 32 columns), one
+//                       wave running the chains while four stream V
 //   k_swiglu            silu(gate) * up, Q8_0 (padded Q8 weights; with Q4_K the
 //                       gate/up GEMV applies it to its own outputs)
 //   k_argmax            first index of the maximum logit
@@ -46,7 +47,6 @@ constexpr int kMaxEmbd = 16384;  // the residual row stays in LDS (64 KB)
 constexpr int kNormThreads = 1024;
 constexpr int kNormChunks = kMaxEmbd / (4 * kNormThreads);  // float4 chunks per thread
 constexpr int kMaxHeadDim = 256;
-constexpr int kPvThreads = 256;
 constexpr int kMaxCtx = 32768;  // one head's scores stay in LDS (128 KB)
 
 // ----------------------------------------------------------------------------
@@ -249,27 +249,46 @@ __device__ __forceinline__ float block_max(float m, float* red) {
     return mx;
 }
 
-// The softmax denominator in one lane: sum = sum + e_j for j = 0..n-1, read
-// from LDS four at a time with 8 reads in flight (e 16-byte aligned).
-__device__ __forceinline__ float seq_sum(const float* __restrict__ e, int n) {
-    const float4* e4 = reinterpret_cast<const float4*>(e);
-    float sum = 0.0f;
-    int j = 0;
-    for (; j + 32 <= n; j += 32) {
-        float4 v[8];
+// The softmax denominator in one lane: sum = sum + e_j for j = 0..n-1.  The
+// caller pads e with -0.0 up to n32 = a multiple of 32; sum + -0.0 == sum for
+// every sum (signed zeros and NaN included), so the padding changes no bit.
+// e is read from LDS in groups of 32 (8 float4, e 16-byte aligned), the next
+// group's reads issued before the current group's adds; sched_barrier keeps the
+// compiler from sinking those reads below the adds.
+__device__ __forceinline__ void sum_group(float& sum, const float4 (&v)[8]) {
 #pragma unroll
-        for (int i = 0; i < 8; i++) v[i] = e4[j / 4 + i];
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            sum = sum + v[i].x;
-            sum = sum + v[i].y;
-            sum = sum + v[i].z;
-            sum = sum + v[i].w;
-        }
+    for (int i = 0; i < 8; i++) {
+        sum = sum + v[i].x;
+        sum = sum + v[i].y;
+        sum = sum + v[i].z;
+        sum = sum + v[i].w;
     }
-    for (; j < n; j++) sum = sum + e[j];
+}
+__device__ __forceinline__ void read_group(float4 (&v)[8], const float4* e4, int g) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = e4[g * 8 + i];
+}
+__device__ __forceinline__ float seq_sum(const float* __restrict__ e, int n32) {
+    const float4* e4 = reinterpret_cast<const float4*>(e);
+    const int ng = n32 / 32;
+    float sum = 0.0f;
+    if (ng == 0) return sum;
+    float4 a[8], b[8];
+    read_group(a, e4, 0);
+    for (int g = 0; g < ng; g += 2) {
+        read_group(b, e4, g + 1 < ng ? g + 1 : g);  // past the end: a re-read, never added
+        __builtin_amdgcn_sched_barrier(0);
+        sum_group(sum, a);
+        __builtin_amdgcn_sched_barrier(0);
+        if (g + 1 >= ng) break;
+        read_group(a, e4, g + 2 < ng ? g + 2 : g + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        sum_group(sum, b);
+        __builtin_amdgcn_sched_barrier(0);
+    }
     return sum;
 }
+__host__ __device__ constexpr int pad32(int n) { return (n + 31) & ~31; }
 
 // ----------------------------------------------------------------------------
 // Short contexts (pos < 64, head_dim DT <= 128): one workgroup per query head.
@@ -316,10 +335,13 @@ __global__ __launch_bounds__(256) void k_attn_small(AttnIn a, RopeTab tab, float
         m = sv;
     }
     const float mx = block_max<NT>(m, red);
-    if (tid < n) e[tid] = expf_libm(e[tid] - mx);
+    if (tid < n)
+        e[tid] = expf_libm(e[tid] - mx);
+    else if (tid < pad32(n))
+        e[tid] = -0.0f;
     __syncthreads();
     if (tid == 0) {
-        const float sum = seq_sum(e, n);
+        const float sum = seq_sum(e, pad32(n));
         sh_inv = sum == 0.0f ? 0.0f : 1.0f / sum;
     }
     __syncthreads();
@@ -372,90 +394,115 @@ __global__ __launch_bounds__(256) void k_attn_scores(AttnIn a, RopeTab tab, floa
     sc[(int64_t)head * ld + j] = s * a.scale;
 }
 
-// k_attn_pv, grid (heads, head_dim/32): softmax and P.V for 32 output columns
-// d0..d0+31 of one head.  The scores go to LDS; max, exps and w_j = e_j * inv
-// are parallel, the softmax sum runs in lane 0 and each output's chain in lane
-// d - d0 of wave 0, all in the reference's order.  The V columns stream
-// through a two-slot LDS ring of 64-row chunks: every thread keeps the loads of
-// the next 8 chunks in flight in registers and writes one chunk per step, one
-// barrier per chunk, so the chains read LDS instead of waiting on HBM.
+// k_attn_pv, grid (heads * head_dim/32): softmax and P.V for 32 output columns
+// d0..d0+31 of one head, in the reference's order.  The scores go to LDS; max,
+// exps and the weights w_j = e_j * inv are parallel; the softmax sum runs in
+// lane 0 and each output's chain acc = RN(acc + RN(v_jd * w_j)) in lane d - d0
+// of wave 0.  Wave 0 does nothing else during P.V: waves 1-4 (the producers)
+// stream the V columns through a two-slot LDS ring of ROWS-row chunks.  Every
+// producer keeps the loads of the next AHEAD chunks in flight in registers and
+// writes one chunk of products per step, transposed so that column d of a
+// chunk is one padded LDS row; one barrier per chunk.  Rows past n get -0.0,
+// which leaves the chain unchanged (acc + -0.0 == acc), so every chunk is read
+// as whole float4.
 // ----------------------------------------------------------------------------
-constexpr int kPvRows = 64;   // rows per chunk
-constexpr int kPvAhead = 8;   // chunks in flight
-constexpr int kPvLd = kPvRows + 4;  // ring row pitch in floats: column d of a chunk is one padded row
+constexpr int kPvProd = 256;               // producer threads
+constexpr int kPvThreads = 64 + kPvProd;   // wave 0 runs the chains
+constexpr int kPvBigMin = 1024;            // 128-row chunks from here ...
+constexpr int kPvBigMax = 16384;           // ... up to here (LDS: ring + scores)
+
+template <int ROWS>
+struct PvShape {
+    static constexpr int LD = ROWS + 4;             // ring row pitch in floats
+    static constexpr int PER = ROWS * 8 / kPvProd;  // float4 of a chunk per producer (ROWS x 8 float4)
+    static constexpr int AHEAD = 512 / ROWS;        // chunks in flight: 64 KB per workgroup
+};
+// LDS: the ring, the padded scores and a few words
+static_assert(kMaxCtx % 32 == 0 && 2 * 32 * PvShape<64>::LD * 4 + kMaxCtx * 4 + 64 <= 160 * 1024,
+              "k_attn_pv<64> LDS");
+static_assert(kPvBigMax % 32 == 0 && 2 * 32 * PvShape<128>::LD * 4 + kPvBigMax * 4 + 64 <= 160 * 1024,
+              "k_attn_pv<128> LDS");
 
 struct PvPipe {
     const float* vbase;  // V column d0 of the head's kv row 0
-    int row, n, nch, tid;
-    bool chain;
-    const float* w;      // softmax weights in LDS
+    int row, n, nch, tid;  // tid: producer number, or the chain lane
+    const float* e;      // exps in LDS
+    float inv;
 };
 
-// Load of chunk c's share of thread tid: float4 number f = tid + k*NT is row
-// c*64 + f/8, columns d0 + 4(f%8)..+3; rows past n repeat row n-1 (never read
-// by the chains, so every load stays in the cache rows already written).
-template <int NT>
+// Load of chunk c's share of producer tid: float4 number f = tid + k*256 is
+// row c*ROWS + f/8, columns d0 + 4(f%8)..+3; rows past n repeat row n-1 (never
+// used, so every load stays in the cache rows already written).
+template <int ROWS>
 __device__ __forceinline__ float4 pv_load(const PvPipe& p, int c, int k) {
-    const int f = p.tid + k * NT, r = min(c * kPvRows + f / 8, p.n - 1);
+    const int f = p.tid + k * kPvProd, r = min(c * ROWS + f / 8, p.n - 1);
     return *reinterpret_cast<const float4*>(p.vbase + (int64_t)r * p.row + 4 * (f % 8));
 }
 
-// Chunk c = c0 + U: its registers, times their rows' weights, go to ring slot
-// c&1 (the reference's RN(v_jd * w_j)), transposed so that column d is one
-// padded LDS row, and are refilled with chunk c + 8; barrier; lane d - d0 of
-// wave 0 reads its 64 products as 16 float4 and extends its chain,
-// acc = RN(acc + p_j), rows in order.  U is a template argument so that pf is
-// indexed by constants only.
-template <int U, int NT, int PER>
-__device__ __forceinline__ void pv_chunk(const PvPipe& p, float4 (&pf)[kPvAhead * PER], float (*ring)[32 * kPvLd],
+// Step c = c0 + U (pf slot U holds chunk c; U is a template argument so that pf
+// is indexed by constants only): the producers write chunk c's products to
+// ring slot c&1 and refill with chunk c + AHEAD; barrier; the chain lanes add
+// the chunk's ROWS products in row order.  Slot c&1 is written again at step
+// c+2, after the barrier of step c+1, which the chain reaches only once it has
+// added chunk c.
+template <int U, int ROWS>
+__device__ __forceinline__ void pv_chunk(const PvPipe& p, bool prod, bool chain,
+                                         float4 (&pf)[PvShape<ROWS>::AHEAD * PvShape<ROWS>::PER], float* ring,
                                          int c0, float& acc) {
+    constexpr int PER = PvShape<ROWS>::PER, LD = PvShape<ROWS>::LD;
     const int c = c0 + U;
-    if (c < p.nch) {
+    if (c >= p.nch) return;  // uniform over the workgroup
+    float* slot = ring + (c & 1) * 32 * LD;
+    if (prod) {
 #pragma unroll
         for (int k = 0; k < PER; k++) {
-            const int f = p.tid + k * NT, rr = f / 8, q4 = 4 * (f % 8), r = c * kPvRows + rr;
-            const float w = r < p.n ? p.w[r] : 0.0f;
+            const int f = p.tid + k * kPvProd, rr = f / 8, r = c * ROWS + rr;
             const float4 v = pf[U * PER + k];
-            float* dst = ring[c & 1] + q4 * kPvLd + rr;
-            dst[0] = v.x * w;
-            dst[kPvLd] = v.y * w;
-            dst[2 * kPvLd] = v.z * w;
-            dst[3 * kPvLd] = v.w * w;
-            pf[U * PER + k] = pv_load<NT>(p, c + kPvAhead, k);
+            float* dst = slot + 4 * (f % 8) * LD + rr;
+            if (r < p.n) {
+                const float w = p.e[r] * p.inv;  // the reference's scores[j] *= inv_sum
+                dst[0] = v.x * w;
+                dst[LD] = v.y * w;
+                dst[2 * LD] = v.z * w;
+                dst[3 * LD] = v.w * w;
+            } else {
+                dst[0] = -0.0f;
+                dst[LD] = -0.0f;
+                dst[2 * LD] = -0.0f;
+                dst[3 * LD] = -0.0f;
+            }
+            pf[U * PER + k] = pv_load<ROWS>(p, c + PvShape<ROWS>::AHEAD, k);
         }
     }
     __syncthreads();
-    if (p.chain && c < p.nch) {
-        const float* col = ring[c & 1] + p.tid * kPvLd;
-        const int rows = min(kPvRows, p.n - c * kPvRows);
-        if (rows == kPvRows) {
-            float4 t[kPvRows / 4];
+    if (chain) {
+        const float4* col = reinterpret_cast<const float4*>(slot + p.tid * LD);
+        float4 t[ROWS / 4];
 #pragma unroll
-            for (int i = 0; i < kPvRows / 4; i++) t[i] = reinterpret_cast<const float4*>(col)[i];
+        for (int i = 0; i < ROWS / 4; i++) t[i] = col[i];
 #pragma unroll
-            for (int i = 0; i < kPvRows / 4; i++) {
-                acc = acc + t[i].x;
-                acc = acc + t[i].y;
-                acc = acc + t[i].z;
-                acc = acc + t[i].w;
-            }
-        } else {
-            for (int r = 0; r < rows; r++) acc = acc + col[r];
+        for (int i = 0; i < ROWS / 4; i++) {
+            acc = acc + t[i].x;
+            acc = acc + t[i].y;
+            acc = acc + t[i].z;
+            acc = acc + t[i].w;
         }
     }
 }
 
-template <int NT>
-__global__ __launch_bounds__(NT) void k_attn_pv(AttnIn a, const float* __restrict__ sc, int ld,
-                                                float* __restrict__ out, uint8_t* __restrict__ xq) {
-    constexpr int PER = kPvRows * 8 / NT;  // float4 of a chunk per thread (a chunk: 64 rows x 8 float4)
+template <int ROWS>
+__global__ __launch_bounds__(kPvThreads) void k_attn_pv(AttnIn a, const float* __restrict__ sc, int ld,
+                                                        float* __restrict__ out, uint8_t* __restrict__ xq) {
+    constexpr int NT = kPvThreads, PER = PvShape<ROWS>::PER, AHEAD = PvShape<ROWS>::AHEAD;
+    static_assert(AHEAD == 4 || AHEAD == 8, "one pv_chunk call per chunk in flight");
     extern __shared__ float4 e4dyn[];
-    float* e = reinterpret_cast<float*>(e4dyn);
-    __shared__ __align__(16) float ring[2][32 * kPvLd];
+    float* e = reinterpret_cast<float*>(e4dyn);  // pad32(n) floats
+    __shared__ __align__(16) float ring[2 * 32 * PvShape<ROWS>::LD];
     __shared__ float red[NT / 64];
     __shared__ float sh_inv;
-    const int tid = threadIdx.x, head = blockIdx.x, kvh = head / a.group, n = a.pos + 1;
-    const int d0 = 32 * blockIdx.y, nch = (n + kPvRows - 1) / kPvRows;
+    const int H = a.row / a.D * a.group, head = blockIdx.x % H, d0 = 32 * (blockIdx.x / H);
+    const int tid = threadIdx.x, kvh = head / a.group, n = a.pos + 1, nch = (n + ROWS - 1) / ROWS;
+    const bool prod = tid >= 64, chain = tid < 32;
     // the scores first, 8 loads in flight (loads complete in order, so anything
     // issued before them would be waited for too), then the first V chunks,
     // which stream in while the softmax runs
@@ -474,36 +521,37 @@ __global__ __launch_bounds__(NT) void k_attn_pv(AttnIn a, const float* __restric
             }
         }
     }
-    const PvPipe pp{a.vc + (int64_t)kvh * a.D + d0, a.row, n, nch, tid, tid < 32, e};
-    float4 pf[kPvAhead * PER];
+    PvPipe pp{a.vc + (int64_t)kvh * a.D + d0, a.row, n, nch, prod ? tid - 64 : tid, e, 0.0f};
+    float4 pf[AHEAD * PER];
+    if (prod) {
 #pragma unroll
-    for (int c = 0; c < kPvAhead; c++)
+        for (int c = 0; c < AHEAD; c++)
 #pragma unroll
-        for (int k = 0; k < PER; k++) pf[c * PER + k] = pv_load<NT>(pp, c, k);
+            for (int k = 0; k < PER; k++) pf[c * PER + k] = pv_load<ROWS>(pp, c, k);
+    }
     const float mx = block_max<NT>(m, red);
-    for (int j = tid; j < n; j += NT) e[j] = expf_libm(e[j] - mx);
+    for (int j = tid; j < pad32(n); j += NT) e[j] = j < n ? expf_libm(e[j] - mx) : -0.0f;
     __syncthreads();
     if (tid == 0) {
-        const float sum = seq_sum(e, n);
+        const float sum = seq_sum(e, pad32(n));
         sh_inv = sum == 0.0f ? 0.0f : 1.0f / sum;
     }
     __syncthreads();
-    const float inv = sh_inv;
-    for (int j = tid; j < n; j += NT) e[j] = e[j] * inv;
-    __syncthreads();  // the producers read other threads' weights
+    pp.inv = sh_inv;
     float acc = 0.0f;
-    static_assert(kPvAhead == 8, "one pv_chunk call per chunk in flight");
-    for (int c0 = 0; c0 < nch; c0 += kPvAhead) {
-        pv_chunk<0, NT, PER>(pp, pf, ring, c0, acc);
-        pv_chunk<1, NT, PER>(pp, pf, ring, c0, acc);
-        pv_chunk<2, NT, PER>(pp, pf, ring, c0, acc);
-        pv_chunk<3, NT, PER>(pp, pf, ring, c0, acc);
-        pv_chunk<4, NT, PER>(pp, pf, ring, c0, acc);
-        pv_chunk<5, NT, PER>(pp, pf, ring, c0, acc);
-        pv_chunk<6, NT, PER>(pp, pf, ring, c0, acc);
-        pv_chunk<7, NT, PER>(pp, pf, ring, c0, acc);
+    for (int c0 = 0; c0 < nch; c0 += AHEAD) {
+        pv_chunk<0, ROWS>(pp, prod, chain, pf, ring, c0, acc);
+        pv_chunk<1, ROWS>(pp, prod, chain, pf, ring, c0, acc);
+        pv_chunk<2, ROWS>(pp, prod, chain, pf, ring, c0, acc);
+        pv_chunk<3, ROWS>(pp, prod, chain, pf, ring, c0, acc);
+        if constexpr (AHEAD == 8) {
+            pv_chunk<4, ROWS>(pp, prod, chain, pf, ring, c0, acc);
+            pv_chunk<5, ROWS>(pp, prod, chain, pf, ring, c0, acc);
+            pv_chunk<6, ROWS>(pp, prod, chain, pf, ring, c0, acc);
+            pv_chunk<7, ROWS>(pp, prod, chain, pf, ring, c0, acc);
+        }
     }
-    if (pp.chain) {
+    if (chain) {
         const int64_t o = (int64_t)head * a.D + d0 + tid;
         out[o] = acc;
         if (xq != nullptr) q8_0_lane_store(acc, xq + (o >> 5) * kQ80Bytes, tid & 31);
@@ -630,8 +678,11 @@ bool lds_limits_set(const char* fn) {
     static std::once_flag once;
     static hipError_t err = hipSuccess;
     std::call_once(once, [] {
-        err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_pv<kPvThreads>),
+        err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_pv<64>),
                                   hipFuncAttributeMaxDynamicSharedMemorySize, kMaxCtx * 4);
+        if (err == hipSuccess)
+            err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_pv<128>),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, kPvBigMax * 4);
         if (err == hipSuccess)
             err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_residual_rmsnorm<kNormThreads, kNormChunks>),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, kMaxEmbd * 4);
@@ -847,8 +898,14 @@ void attention(const StepCtx& c, const AttnIn& ai, int n_ctx) {
         hipLaunchKernelGGL(k_attn_scores<64>, gs, dim3(256), 0, c.s, ai, c.tab, c.scores, ld);
     else
         hipLaunchKernelGGL(k_attn_scores<0>, gs, dim3(256), 0, c.s, ai, c.tab, c.scores, ld);
-    hipLaunchKernelGGL(k_attn_pv<kPvThreads>, dim3(g.H, g.D / 32), dim3(kPvThreads), (size_t)n_ctx * 4, c.s, ai,
-                       c.scores, ld, c.att, c.xq_a);
+    // e holds pad32(n_ctx) <= kMaxCtx floats (kMaxCtx % 32 == 0); with 128-row
+    // chunks n_ctx <= kPvBigMax, so the ring and the scores fit in 160 KB
+    const dim3 gp(g.H * (g.D / 32));
+    const size_t lds = (size_t)pad32(n_ctx) * 4;
+    if (n_ctx >= kPvBigMin && n_ctx <= kPvBigMax)
+        hipLaunchKernelGGL(k_attn_pv<128>, gp, dim3(kPvThreads), lds, c.s, ai, c.scores, ld, c.att, c.xq_a);
+    else
+        hipLaunchKernelGGL(k_attn_pv<64>, gp, dim3(kPvThreads), lds, c.s, ai, c.scores, ld, c.att, c.xq_a);
 }
 
 // The layers.  The residual add is the first step of each RMSNorm kernel; the

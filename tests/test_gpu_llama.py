@@ -126,12 +126,14 @@ def test_step_equals_restatement(dev, fmt, variant):
 
 
 @pytest.mark.parametrize("D,pos", [(64, 63), (64, 64), (64, 255), (64, 2047), (128, 63), (128, 300),
-                                   (256, 40), (32, 1000)])
+                                   (256, 40), (32, 1000), (64, 1023), (128, 1100), (32, 16383), (32, 16500)])
 def test_long_context(dev, D, pos):
     """Rows 0..pos-1 of the caches hold the same random finite data on both
     sides; one step at `pos` then attends over pos+1 rows (one attention kernel
-    up to 64 rows for head_dim <= 128, the scores + P.V pair beyond)."""
-    cfg = LM.config(L=1, max_seq=2048, E=4 * D, H=4, HKV=2, D=D)
+    up to 64 rows for head_dim <= 128, the scores + P.V pair beyond, whose P.V
+    streams V in 128-row chunks for 1024..16384 rows and 64-row chunks
+    otherwise; the cases cover whole and partial last chunks of both)."""
+    cfg = LM.config(L=1, max_seq=max(2048, pos + 1), E=4 * D, H=4, HKV=2, D=D)
     layers, head = LM.make(cfg, 0, seed=5)
     m = _gpu_model(cfg, layers, head, llama.W_Q8_PAD64, dev)
     ko, vo = LM.caches(cfg)
