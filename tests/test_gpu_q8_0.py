@@ -62,7 +62,11 @@ def test_quant_q8_0_edges(dev):
 
 
 @pytest.mark.parametrize("mw,mt,K", [(14336, 1, 4096), (4096, 1, 14336), (4, 2, 128), (7, 5, 128),
-                                     (9, 7, 128), (2048, 2, 2048), (1, 1, 32), (13, 3, 4096 + 32)])
+                                     (9, 7, 128), (2048, 2, 2048), (1, 1, 32), (13, 3, 4096 + 32),
+                                     # the wide-load kernel: 32-row and 16-row workgroups, a
+                                     # partial last workgroup, each activation register count
+                                     (8192, 2, 1024), (8200, 3, 8192), (2048, 1, 8192), (9000, 1, 2048),
+                                     (2056, 1, 16384)])
 def test_dispatch_tile_order(dev, mw, mt, K):
     W = synth.q8_0(mw, K, synth.key(42, 7))
     X = synth.normal_f32(mt * K, synth.key(42, 8))
@@ -123,6 +127,22 @@ def test_empty_k_gives_zero_cells(dev):
         gpu.call(name, None, None, out, 5, 3, 0)
         torch.cuda.synchronize()
         assert to_np(out).view(np.uint32).tolist() == [0] * 15, name
+
+
+def test_dispatch_unaligned_weights_take_the_dword_kernels(dev):
+    # W at an address 2 mod 16: the wide-load kernel needs 16-byte rows, so the
+    # dispatcher must take k_q8_0_gemv_T, with the same bits
+    import torch
+
+    mw, mt, K = 8192, 1, 1024
+    W = synth.q8_0(mw, K, synth.key(45, 1))
+    Xq = O.quant_q8_0(synth.normal_f32(mt * K, synth.key(45, 2)))
+    buf = torch.zeros(W.size + 16, dtype=torch.uint8, device=dev)
+    buf[2:2 + W.size].copy_(_d(W, dev))
+    out = torch.empty(mw * mt, dtype=torch.float32, device=dev)
+    gpu._use_torch_stream()
+    gpu.call("bpd_qmatmul_q8_0_dispatch_gpu", buf.data_ptr() + 2, _d(Xq, dev), out, mw, mt, K)
+    assert_bits_equal(to_np(out), O.dispatch_q8_0(W, Xq, mw, mt, K, "T"), "unaligned W")
 
 
 @pytest.mark.parametrize("mw", [7, 15, 17, 23])

@@ -107,11 +107,68 @@ def test_dequant_in_bounds(nb):
 
 # ---------------------------------------------------------------- Q8_0 tile-order GEMV
 
+def q8_wide_config(mw, nb):
+    """(R, AHEAD, XR) of k_q8_0_gemv_W as launch_wide() in q8_0.hip picks it for a
+    16-byte aligned W, or None."""
+    if nb == 0 or nb % 32 != 0:
+        return None
+    big = mw >= 8192
+    if not big and not (mw >= 2048 and nb >= 256):
+        return None
+    R, AHEAD = (32, 2) if big else (16, 4)
+    NT = 128 * (R // 8)
+    XR = next((x for x in ((2, 4, 8, 16) if R == 32 else (4, 8, 16)) if nb * 8 <= x * NT), None)
+    if XR is None or nb > 2 * NT or nb * 36 + 2 * R * 1104 > 160 * 1024:
+        return None
+    return R, AHEAD, XR
+
+
+def check_wide_q8(mw, mt, nb, w_size, x_size, out_size):
+    """k_q8_0_gemv_W: loader thread lt of workgroup g reads 16-byte piece
+    f = min(lt + k*LT, R*68 - 1) -- row f/68, bytes 1088c + 16(f%68) of that row
+    (rows past mw re-read row mw-1) -- for chunks c < nb/32 and writes it at
+    (f/68)*1104 + 16(f%68) of a ring slot; chain lane (row, L) reads the row
+    chunk's bytes [34bb+2+4L, +4) (even bb: [34bb+4L, 34bb+4L+8)) and the scale at
+    34bb; the activation is quant dword min(i, 8nb-1) and scale min(j, nb-1)."""
+    R, AHEAD, XR = q8_wide_config(mw, nb)
+    NT, LT, PIECES = 128 * (R // 8), 64 * (R // 8), R * 68
+    PER = -(-PIECES // LT)
+    bpr, nch = nb * Q80, nb // 32
+    lt = np.arange(LT)
+    groups = -(-mw // R)
+    for g in sorted({0, groups - 1}):
+        row0 = g * R
+        row0c = min(row0, mw - 1)
+        for k in range(PER):
+            f = np.minimum(lt + k * LT, PIECES - 1)
+            r, pc = f // 68, f % 68
+            off = (np.minimum(row0 + r, mw - 1) - row0c) * bpr + 16 * pc
+            for c in (0, nch - 1):
+                a = row0c * bpr + off + c * 1088
+                assert a.min() >= 0 and (a + 16).max() <= w_size
+            dst = r * 1104 + 16 * pc
+            assert (dst + 16).max() <= R * 1104
+    L = np.arange(8)
+    for bb in range(32):
+        o = 34 * bb + 2 + 4 * L
+        lo, hi = (o - 2, o + 6) if bb % 2 == 0 else (o, o + 4)
+        assert lo.min() >= 0 and hi.max() <= 1088 and 34 * bb + 2 <= 1088
+    i = np.minimum(np.arange(XR * NT), nb * 8 - 1)
+    j = np.minimum(np.arange(2 * NT), nb - 1)
+    for tok in range(mt):
+        assert tok * bpr + ((i >> 3) * Q80 + 2 + 4 * (i & 7) + 4).max() <= x_size
+        assert tok * bpr + (j * Q80 + 2).max() <= x_size
+    assert (mt - 1) * mw * 4 + mw * 4 <= out_size
+    assert nb * 36 + 2 * R * 1104 <= 160 * 1024
+
+
 def q8_gemv_config(mw, mt, K):
     nb = K // 32
     waves = (mw + 7) // 8
     if nb == 0:
         return None
+    if q8_wide_config(mw, nb) is not None:
+        return ("wide", 0, 0)
     if nb * 36 > 64 * 1024:
         return ("plain", 4, 1)
     if waves * mt >= 1024:
@@ -148,7 +205,9 @@ def check_producer(mw, mt, nb, layout, w_size):
 
 @pytest.mark.parametrize("mw,mt,K", [(14336, 1, 4096), (4096, 1, 14336), (4, 2, 128), (7, 5, 128), (9, 7, 128),
                                      (2048, 2, 2048), (1, 1, 32), (13, 3, 4128), (64, 4, 256), (6, 3, 96),
-                                     (3, 1, 64), (17, 1, 32), (15, 1, 256), (23, 1, 256), (7, 1, 256)])
+                                     (3, 1, 64), (17, 1, 32), (15, 1, 256), (23, 1, 256), (7, 1, 256),
+                                     (8192, 2, 1024), (8200, 3, 8192), (2048, 1, 8192), (9000, 1, 2048),
+                                     (14336, 4, 4096), (2056, 1, 16384), (8192, 1, 32768)])
 def test_q8_0_gemv_T_in_bounds(mw, mt, K):
     cfg = q8_gemv_config(mw, mt, K)
     nb = K // 32
@@ -157,6 +216,9 @@ def test_q8_0_gemv_T_in_bounds(mw, mt, K):
     if cfg is None:
         return
     kind, WPB, U = cfg
+    if kind == "wide":
+        check_wide_q8(mw, mt, nb, w_size, x_size, out_size)
+        return
     if kind == "producer":
         check_producer(mw, mt, nb, 0, w_size)
         for tok in range(mt):
