@@ -7,7 +7,7 @@
 //                       bias, RoPE (NORM pairs), the K/V cache row write, scores,
 //                       softmax, P.V and Q8_0(out)
 //   k_attn_scores       longer contexts: bias, RoPE, cache row write and the scores,
-//                       spread over (head, 256-row) workgroups
+//                       per (kv head, 64 rows), the k rows read once into LDS
 //   k_attn_pv           longer contexts: softmax and P.V per (head, 32 columns), one
 //                       wave running the chains while four stream V
 //   k_swiglu            silu(gate) * up, Q8_0 (padded Q8 weights; with Q4_K the
@@ -168,21 +168,23 @@ struct AttnIn {
     float scale;
 };
 
-// Bias + RoPE of query head `head` into qs and, with `with_kv`, of the new k
-// row into ks and the new v row into vs (all LDS).
+// Bias + RoPE of query head `head` into qs (unless NULL) and, with `with_kv`,
+// of the new k row into ks and the new v row into vs (all LDS).
 __device__ __forceinline__ void rope_rows(const AttnIn& a, const RopeTab& tab, int head, int kvh, float* qs,
                                           float* ks, float* vs, bool with_kv) {
     const int64_t qo = (int64_t)head * a.D, ko = (int64_t)kvh * a.D;
     for (int p = threadIdx.x; p < a.D / 2; p += blockDim.x) {
         const int i = 2 * p;
         const float c = tab.c[p], sn = tab.s[p];
-        float x0 = a.q[qo + i], x1 = a.q[qo + i + 1];
-        if (a.bq != nullptr) {
-            x0 = x0 + a.bq[qo + i];
-            x1 = x1 + a.bq[qo + i + 1];
+        if (qs != nullptr) {
+            float x0 = a.q[qo + i], x1 = a.q[qo + i + 1];
+            if (a.bq != nullptr) {
+                x0 = x0 + a.bq[qo + i];
+                x1 = x1 + a.bq[qo + i + 1];
+            }
+            qs[i] = x0 * c - x1 * sn;
+            qs[i + 1] = x0 * sn + x1 * c;
         }
-        qs[i] = x0 * c - x1 * sn;
-        qs[i + 1] = x0 * sn + x1 * c;
         if (with_kv) {
             float k0 = a.knew[ko + i], k1 = a.knew[ko + i + 1];
             if (a.bk != nullptr) {
@@ -359,39 +361,78 @@ __global__ __launch_bounds__(256) void k_attn_small(AttnIn a, RopeTab tab, float
 
 // ----------------------------------------------------------------------------
 // Longer contexts, two kernels.
-// k_attn_scores, grid (heads, ceil(n/256)): thread j of the grid's row range
-// computes v_j = (q . k_j) * scale for one row (its k row loaded whole into
-// registers when head_dim is DT) into sc[head][j]; the workgroup holding row pos
-// also ropes the new k row, scores it from LDS and, for the first head of each
-// group, writes the new k and v rows to the caches.
+// k_attn_scores, grid (kv heads * ceil(n/64)), one wave per query head of the
+// kv head's group: the workgroup loads k rows 64b .. 64b+63 once, coalesced,
+// into LDS (rows at a padded pitch), and lane j of wave h computes
+// v_j = (q_h . k_j) * scale, the dot sequential over d, into sc[h][j].  The
+// block holding row pos ropes the new k row into its LDS row (the cache row is
+// not read) and writes the new k and v rows to the caches, once per kv head.
 // ----------------------------------------------------------------------------
+constexpr int kScoreRows = 64;
+constexpr int kMaxGroup = 8;  // waves per workgroup; larger groups loop over their heads
+
+__host__ __device__ constexpr int score_pitch(int D) { return D + 4; }  // floats: rows 4 banks apart
+
 template <int DT>
-__global__ __launch_bounds__(256) void k_attn_scores(AttnIn a, RopeTab tab, float* __restrict__ sc, int ld) {
-    __shared__ float4 qs4[kMaxHeadDim / 4], ks4[kMaxHeadDim / 4], vs4[kMaxHeadDim / 4];
-    const int tid = threadIdx.x, head = blockIdx.x, kvh = head / a.group, pos = a.pos;
-    const int j = blockIdx.y * 256 + tid, D4 = a.D / 4;
-    const bool last = blockIdx.y == gridDim.y - 1;  // the block holding row pos
-    const int64_t ko = (int64_t)kvh * a.D;
-    constexpr int KR = DT > 0 ? DT / 4 : 1;
-    float4 kr[KR];
-    if (DT > 0 && j < pos) {
-        const float4* p = reinterpret_cast<const float4*>(a.kc + (int64_t)j * a.row + ko);
-#pragma unroll
-        for (int i = 0; i < KR; i++) kr[i] = p[i];
+__global__ __launch_bounds__(64 * kMaxGroup) void k_attn_scores(AttnIn a, RopeTab tab, float* __restrict__ sc, int ld) {
+    extern __shared__ float4 sm4[];
+    const int D = DT > 0 ? DT : a.D, D4 = D / 4, P4 = score_pitch(D) / 4, G = a.group;
+    const int pos = a.pos, nb = (pos + kScoreRows) / kScoreRows;
+    const int kvh = blockIdx.x / nb, yb = blockIdx.x % nb, j0 = yb * kScoreRows;
+    const int nw = blockDim.x >> 6, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    float4* kt = sm4;                        // [64][P4] the block's k rows
+    float4* qs4 = kt + kScoreRows * P4;      // [G][D4] q of the group's heads
+    float4* ks4 = qs4 + G * D4;              // the new k row
+    float4* vs4 = ks4 + D4;                  // the new v row
+    const bool last = yb == nb - 1;          // the block holding row pos
+    const int64_t ko = (int64_t)kvh * D;
+    // k rows j0 .. min(j0+63, pos-1): float4 i of row r at kt[r*P4 + i]
+    const int rows = min(kScoreRows, pos - j0);
+    for (int f = threadIdx.x; f < rows * D4; f += blockDim.x) {
+        const int r = f / D4, i = f % D4;
+        kt[r * P4 + i] = *reinterpret_cast<const float4*>(a.kc + (int64_t)(j0 + r) * a.row + ko + 4 * i);
     }
-    rope_rows(a, tab, head, kvh, reinterpret_cast<float*>(qs4), reinterpret_cast<float*>(ks4),
-              reinterpret_cast<float*>(vs4), last);
+    // bias + RoPE of the group's q heads in one pass (their loads in flight together),
+    // then of the new k and v rows in the block holding row pos
+    float* qs = reinterpret_cast<float*>(qs4);
+    const int half = D / 2;
+    for (int pp = threadIdx.x; pp < G * half; pp += blockDim.x) {
+        const int h = pp / half, pr = pp % half, i = 2 * pr;
+        const int64_t qo = (int64_t)(kvh * G + h) * D + i;
+        float x0 = a.q[qo], x1 = a.q[qo + 1];
+        if (a.bq != nullptr) {
+            x0 = x0 + a.bq[qo];
+            x1 = x1 + a.bq[qo + 1];
+        }
+        const float c = tab.c[pr], sn = tab.s[pr];
+        qs[h * D + i] = x0 * c - x1 * sn;
+        qs[h * D + i + 1] = x0 * sn + x1 * c;
+    }
+    if (last) rope_rows(a, tab, kvh * G, kvh, nullptr, reinterpret_cast<float*>(ks4), reinterpret_cast<float*>(vs4), true);
     __syncthreads();
-    if (last) write_new_row(a, head, kvh, reinterpret_cast<float*>(ks4), reinterpret_cast<float*>(vs4));
+    if (last) {
+        const int64_t o = (int64_t)pos * a.row + ko;
+        const float* ks = reinterpret_cast<const float*>(ks4);
+        const float* vs = reinterpret_cast<const float*>(vs4);
+        for (int d = threadIdx.x; d < D; d += blockDim.x) {
+            a.kc[o + d] = ks[d];
+            a.vc[o + d] = vs[d];
+        }
+    }
+    const int j = j0 + lane;
     if (j > pos) return;
-    float s;
-    if (j == pos)
-        s = dot_ptr(qs4, ks4, D4);
-    else if (DT > 0)
-        s = dot_regs<KR>(qs4, kr);
-    else
-        s = dot_ptr(qs4, reinterpret_cast<const float4*>(a.kc + (int64_t)j * a.row + ko), D4);
-    sc[(int64_t)head * ld + j] = s * a.scale;
+    const float4* kr = j == pos ? ks4 : kt + lane * P4;
+    for (int h = wave; h < G; h += nw) {
+        const float4* q = qs4 + h * D4;
+        float s = 0.0f;
+        if (DT > 0) {
+#pragma unroll 8
+            for (int i = 0; i < DT / 4; i++) s = dot_step(s, q[i], kr[i]);
+        } else {
+            for (int i = 0; i < D4; i++) s = dot_step(s, q[i], kr[i]);
+        }
+        sc[(int64_t)(kvh * G + h) * ld + j] = s * a.scale;
+    }
 }
 
 // k_attn_pv, grid (heads * head_dim/32): softmax and P.V for 32 output columns
@@ -683,6 +724,13 @@ bool lds_limits_set(const char* fn) {
         if (err == hipSuccess)
             err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_pv<128>),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, kPvBigMax * 4);
+        // the scores kernel's LDS: the k tile plus q of up to n_embd / head_dim heads
+        for (const void* f : {reinterpret_cast<const void*>(&k_attn_scores<128>),
+                              reinterpret_cast<const void*>(&k_attn_scores<64>),
+                              reinterpret_cast<const void*>(&k_attn_scores<0>)})
+            if (err == hipSuccess)
+                err = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                          (kScoreRows * score_pitch(kMaxHeadDim) + kMaxEmbd + 2 * kMaxHeadDim) * 4);
         if (err == hipSuccess)
             err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_residual_rmsnorm<kNormThreads, kNormChunks>),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, kMaxEmbd * 4);
@@ -890,14 +938,16 @@ void attention(const StepCtx& c, const AttnIn& ai, int n_ctx) {
             hipLaunchKernelGGL(k_attn_small<32>, dim3(g.H), dim3(256), 0, c.s, ai, c.tab, c.att, c.xq_a);
         return;
     }
-    const dim3 gs(g.H, (n_ctx + 255) / 256);
-    const int ld = c.cfg->max_seq;
+    const int ld = c.cfg->max_seq, group = g.H / g.HKV;
+    const dim3 gs(g.HKV * ((n_ctx + kScoreRows - 1) / kScoreRows)), ts(64 * (group < kMaxGroup ? group : kMaxGroup));
+    // k tile, q of the group's heads, new k and v rows: <= (64 * 260 + 16384 + 512) * 4 bytes
+    const size_t slds = ((size_t)kScoreRows * score_pitch(g.D) + (size_t)(group + 2) * g.D) * 4;
     if (g.D == 128)
-        hipLaunchKernelGGL(k_attn_scores<128>, gs, dim3(256), 0, c.s, ai, c.tab, c.scores, ld);
+        hipLaunchKernelGGL(k_attn_scores<128>, gs, ts, slds, c.s, ai, c.tab, c.scores, ld);
     else if (g.D == 64)
-        hipLaunchKernelGGL(k_attn_scores<64>, gs, dim3(256), 0, c.s, ai, c.tab, c.scores, ld);
+        hipLaunchKernelGGL(k_attn_scores<64>, gs, ts, slds, c.s, ai, c.tab, c.scores, ld);
     else
-        hipLaunchKernelGGL(k_attn_scores<0>, gs, dim3(256), 0, c.s, ai, c.tab, c.scores, ld);
+        hipLaunchKernelGGL(k_attn_scores<0>, gs, ts, slds, c.s, ai, c.tab, c.scores, ld);
     // e holds pad32(n_ctx) <= kMaxCtx floats (kMaxCtx % 32 == 0); with 128-row
     // chunks n_ctx <= kPvBigMax, so the ring and the scores fit in 160 KB
     const dim3 gp(g.H * (g.D / 32));

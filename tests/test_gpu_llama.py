@@ -125,16 +125,20 @@ def test_step_equals_restatement(dev, fmt, variant):
         _check_step(m, tok, want, (ko, vo), pos, f"fmt {fmt} {variant}")
 
 
-@pytest.mark.parametrize("D,pos", [(64, 63), (64, 64), (64, 255), (64, 2047), (128, 63), (128, 300),
-                                   (256, 40), (32, 1000), (64, 1023), (128, 1100), (32, 16383), (32, 16500)])
-def test_long_context(dev, D, pos):
+@pytest.mark.parametrize("D,pos,H,HKV,bias", [
+    (64, 63, 4, 2, False), (64, 64, 4, 2, False), (64, 255, 4, 2, False), (64, 2047, 4, 2, False),
+    (128, 63, 4, 2, False), (128, 300, 4, 2, False), (256, 40, 4, 2, False), (32, 1000, 4, 2, False),
+    (64, 1023, 4, 2, False), (128, 1100, 4, 2, False), (32, 16383, 4, 2, False), (32, 16500, 4, 2, False),
+    # q/k/v biases; GQA groups of 1 and of 16 (the scores kernel's waves then loop over heads)
+    (64, 300, 4, 2, True), (32, 200, 4, 4, False), (32, 130, 16, 1, True)])
+def test_long_context(dev, D, pos, H, HKV, bias):
     """Rows 0..pos-1 of the caches hold the same random finite data on both
     sides; one step at `pos` then attends over pos+1 rows (one attention kernel
     up to 64 rows for head_dim <= 128, the scores + P.V pair beyond, whose P.V
     streams V in 128-row chunks for 1024..16384 rows and 64-row chunks
     otherwise; the cases cover whole and partial last chunks of both)."""
-    cfg = LM.config(L=1, max_seq=max(2048, pos + 1), E=4 * D, H=4, HKV=2, D=D)
-    layers, head = LM.make(cfg, 0, seed=5)
+    cfg = LM.config(L=1, max_seq=max(2048, pos + 1), E=H * D, H=H, HKV=HKV, D=D)
+    layers, head = LM.make(cfg, 0, seed=5, bias=bias)
     m = _gpu_model(cfg, layers, head, llama.W_Q8_PAD64, dev)
     ko, vo = LM.caches(cfg)
     row = cfg["n_head_kv"] * cfg["head_dim"]
