@@ -126,4 +126,26 @@ __device__ __forceinline__ void q8_0_quad_store(float4 v, uint8_t* __restrict__ 
     if (g == 0) *reinterpret_cast<uint16_t*>(yb) = __builtin_bit_cast(uint16_t, (_Float16)d);
 }
 
+// One Q8_K block {f32 d, i8 qs[256], i16 bsums[16]} from one whole wave, lane l
+// holding elements 4l..4l+3: amax over the block (exact in any order), d =
+// amax / 127, id = 127 / amax (0 when amax is 0), q = rint(x * id), bsums of
+// 16 consecutive q.  yb is 4-byte aligned.
+__device__ __forceinline__ void q8k_wave_store(float4 v, uint8_t* __restrict__ yb, int lane) {
+    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+#pragma unroll
+    for (int mask = 1; mask < 64; mask <<= 1) amax = fmaxf(amax, xor_f(amax, mask));
+    const float d = amax / 127.0f;
+    const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+    const int q0 = (int)__builtin_rintf(v.x * id), q1 = (int)__builtin_rintf(v.y * id);
+    const int q2 = (int)__builtin_rintf(v.z * id), q3 = (int)__builtin_rintf(v.w * id);
+    const uint32_t packed = (uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) | ((uint32_t)(q2 & 0xFF) << 16) |
+                            ((uint32_t)(q3 & 0xFF) << 24);
+    *reinterpret_cast<uint32_t*>(yb + 4 + 4 * lane) = packed;
+    int s = q0 + q1 + q2 + q3;
+    s += dpp_i<0xB1>(s);
+    s += dpp_i<0x4E>(s);
+    if ((lane & 3) == 0) *reinterpret_cast<int16_t*>(yb + 260 + 2 * (lane >> 2)) = (int16_t)s;
+    if (lane == 0) *reinterpret_cast<float*>(yb) = d;
+}
+
 }  // namespace bpdq

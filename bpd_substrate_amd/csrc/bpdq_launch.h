@@ -29,6 +29,9 @@ void launch_qmatmul_q4k_fused_multi(const uint8_t* const* w, float* const* y, co
 // y[r] = silu(gate_r) * up_r, gate_r and up_r as the fused GEMV computes them.
 void launch_qmatmul_q4k_fused_swiglu(const uint8_t* w_gate, const uint8_t* w_up, float* y, int M, const float* x,
                                      int K, int order, hipStream_t s);
+// The same from a Q8_K activation xq (K <= 4096).
+void launch_qmatmul_q4k_swiglu_q8k(const uint8_t* w_gate, const uint8_t* w_up, float* y, int M, const uint8_t* xq,
+                                   int K, int order, hipStream_t s);
 
 void launch_dequant_q6k(const uint8_t* q, float* out, int n_blocks, int order, hipStream_t s);
 void launch_qmatmul_q6k_q8k(const uint8_t* w, const uint8_t* xq, float* y, int M, int K, int order, hipStream_t s);

@@ -63,11 +63,14 @@ constexpr int kMaxCtx = 32768;  // one head's scores stay in LDS (128 KB)
 // ----------------------------------------------------------------------------
 // Thread t holds float4 chunks t, t + NT, ... of the row (MAXC at most), with
 // the norm weight loaded alongside.  Q8_0 blocks are 8 consecutive lanes.
+// xk (or NULL) receives Q8_K blocks of h, the bytes k_quant_q8k writes: chunk
+// c of a thread is lane c % 64 of block c / 64, so each block is one whole wave
+// (n % 256 == 0 when xk is given).
 template <int NT, int MAXC>
 __global__ __launch_bounds__(NT) void k_residual_rmsnorm(const float* x_in, const float* __restrict__ add,
                                                          float* x_out, const float* __restrict__ w,
-                                                         float* __restrict__ h, uint8_t* __restrict__ xq, int n,
-                                                         float eps) {
+                                                         float* __restrict__ h, uint8_t* __restrict__ xq,
+                                                         uint8_t* __restrict__ xk, int n, float eps) {
     extern __shared__ float4 xs4[];
     __shared__ double wsum[NT / 64];
     __shared__ float sh_scale;
@@ -130,6 +133,7 @@ __global__ __launch_bounds__(NT) void k_residual_rmsnorm(const float* x_in, cons
             if (h != nullptr) reinterpret_cast<float4*>(h)[c] = y;
             // n % 32 == 0 and NT % 8 == 0: the 8 chunks of a block are 8 aligned lanes
             if (xq != nullptr) q8_0_quad_store(y, xq + (int64_t)(c >> 3) * kQ80Bytes, c & 7);
+            if (xk != nullptr) q8k_wave_store(y, xk + (int64_t)(c >> 6) * kQ8KBytes, c & 63);
         }
     }
 }
@@ -739,10 +743,9 @@ bool lds_limits_set(const char* fn) {
 }
 
 void launch_norm(const float* x_in, const float* add, float* x_out, const float* w, float* h, uint8_t* xq, int n,
-                 float eps, hipStream_t s) {
+                 float eps, hipStream_t s, uint8_t* xk = nullptr) {
     hipLaunchKernelGGL((k_residual_rmsnorm<kNormThreads, kNormChunks>), dim3(1), dim3(kNormThreads), (size_t)n * 4, s,
-                       x_in, add,
-                       x_out, w, h, xq, n, eps);
+                       x_in, add, x_out, w, h, xq, xk, n, eps);
 }
 
 // Rotation table for `pos`: pair j turns by pos * theta_scale^j, the angle
@@ -923,6 +926,7 @@ struct StepCtx {
     float* scores;      // [n_head][max_seq] scaled scores of the long-context attention
     float attn_scale;   // 1 / sqrtf(head_dim), as the reference computes it
     uint8_t *xq_e, *xq_a, *xq_f;  // Q8_0 activations (padded Q8 weights only, else NULL)
+    uint8_t* xk;  // Q8_K of the normed row (Q4_K weights, n_embd <= 4096, else NULL)
 };
 
 // Attention over n_ctx = pos + 1 rows: one kernel while the context is short
@@ -968,12 +972,18 @@ void run_layers(const StepCtx& c, const Gemv& gemv, const LayerWeights* layers, 
     const int row = g.HKV * g.D, n_ctx = c.pos + 1;
     for (int l = 0; l < g.L; l++) {
         const LayerWeights& w = layers[l];
-        launch_norm(xin, add, c.x, static_cast<const float*>(w.attn_norm), c.h, c.xq_e, g.E, c.cfg->eps, c.s);
+        launch_norm(xin, add, c.x, static_cast<const float*>(w.attn_norm), c.h, c.xq_e, g.E, c.cfg->eps, c.s, c.xk);
         xin = c.x;
         const void* wqkv[3] = {w.q, w.k, w.v};
         float* yqkv[3] = {c.qb, c.kb, c.vb};
         const int nqkv[3] = {w.q_N, w.k_N, w.v_N};
-        gemv.run(3, wqkv, yqkv, nqkv, c.h, c.xq_e, g.E);
+        if (c.xk != nullptr) {  // the norm wrote h's Q8_K once: the plain GEMV reads it
+            const uint8_t* wl[3] = {static_cast<const uint8_t*>(w.q), static_cast<const uint8_t*>(w.k),
+                                    static_cast<const uint8_t*>(w.v)};
+            launch_qmatmul_q4k_q8k_multi(wl, yqkv, nqkv, 3, c.xk, g.E, gemv.fmt == BPDQ_W_Q4K_GGUF ? 1 : 0, c.s);
+        } else {
+            gemv.run(3, wqkv, yqkv, nqkv, c.h, c.xq_e, g.E);
+        }
         const AttnIn ai{c.qb, c.kb, c.vb,
                         static_cast<const float*>(w.q_bias), static_cast<const float*>(w.k_bias),
                         static_cast<const float*>(w.v_bias), static_cast<float*>(c.kv->k_cache[l]),
@@ -983,8 +993,11 @@ void run_layers(const StepCtx& c, const Gemv& gemv, const LayerWeights* layers, 
         float* yo[1] = {c.ffn};
         const int no[1] = {w.o_N};
         gemv.run(1, wo, yo, no, c.att, c.xq_a, g.H * g.D);
-        launch_norm(c.x, c.ffn, c.x, static_cast<const float*>(w.ffn_norm), c.h, c.xq_e, g.E, c.cfg->eps, c.s);
-        if (gemv.fmt == BPDQ_W_Q8_PAD64) {
+        launch_norm(c.x, c.ffn, c.x, static_cast<const float*>(w.ffn_norm), c.h, c.xq_e, g.E, c.cfg->eps, c.s, c.xk);
+        if (c.xk != nullptr) {
+            launch_qmatmul_q4k_swiglu_q8k(static_cast<const uint8_t*>(w.gate), static_cast<const uint8_t*>(w.up),
+                                          c.gate, g.F, c.xk, g.E, gemv.fmt == BPDQ_W_Q4K_GGUF ? 1 : 0, c.s);
+        } else if (gemv.fmt == BPDQ_W_Q8_PAD64) {
             const void* wgu[2] = {w.gate, w.up};
             float* ygu[2] = {c.gate, c.up};
             const int ngu[2] = {w.gate_N, w.up_N};
@@ -1015,7 +1028,10 @@ bool enqueue_step(int fmt, const LayerWeights* layers, const ModelConfig* cfg, c
     const size_t front = q8 ? (2 * q8e + q8f + 255) & ~(size_t)255 : 0;
     const int kmax = g.F > g.E ? g.F : g.E;
     const size_t q8k = kmax > fused_max_k() ? (size_t)(kmax / 256) * kQ8KBytes : 0;
-    const size_t q8k_end = (front + q8k + 255) & ~(size_t)255;
+    // with Q4_K weights and n_embd <= 4096 the norms write h's Q8_K once for the
+    // Q/K/V and gate/up GEMVs (measured 1,515 -> 1,500 us/token at cfg3)
+    const size_t xk_bytes = !q8 && g.E <= 4096 ? ((size_t)(g.E / 256) * kQ8KBytes + 255) & ~(size_t)255 : 0;
+    const size_t q8k_end = ((front + q8k + 255) & ~(size_t)255) + xk_bytes;
     const size_t sc_bytes = (size_t)g.H * cfg->max_seq * 4;
     uint8_t* ws = step_workspace(q8k_end + sc_bytes, fn);
     if (ws == nullptr) return false;
@@ -1038,6 +1054,7 @@ bool enqueue_step(int fmt, const LayerWeights* layers, const ModelConfig* cfg, c
     c.xq_e = q8 ? ws : nullptr;
     c.xq_a = q8 ? ws + q8e : nullptr;
     c.xq_f = q8 ? ws + 2 * q8e : nullptr;
+    c.xk = xk_bytes ? ws + q8k_end - xk_bytes : nullptr;
     if (g.L > 0) rope_table(c.tab, pos, g.D, cfg->rope_theta);
     float* logits = static_cast<float*>(buf->logits);
 

@@ -119,22 +119,7 @@ __global__ __launch_bounds__(256) void k_quant_q8k(const float* __restrict__ x, 
     const int b = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (b >= nb) return;
     const float4 v = *reinterpret_cast<const float4*>(x + (int64_t)b * 256 + 4 * lane);
-    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-#pragma unroll
-    for (int mask = 1; mask < 64; mask <<= 1) amax = fmaxf(amax, xor_f(amax, mask));
-    const float d = amax / 127.0f;
-    const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
-    const int q0 = (int)__builtin_rintf(v.x * id), q1 = (int)__builtin_rintf(v.y * id);
-    const int q2 = (int)__builtin_rintf(v.z * id), q3 = (int)__builtin_rintf(v.w * id);
-    uint8_t* yb = y + (int64_t)b * kQ8KBytes;
-    const uint32_t packed = (uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) | ((uint32_t)(q2 & 0xFF) << 16) |
-                            ((uint32_t)(q3 & 0xFF) << 24);
-    *reinterpret_cast<uint32_t*>(yb + 4 + 4 * lane) = packed;
-    int s = q0 + q1 + q2 + q3;
-    s += dpp_i<0xB1>(s);
-    s += dpp_i<0x4E>(s);
-    if ((lane & 3) == 0) *reinterpret_cast<int16_t*>(yb + 260 + 2 * (lane >> 2)) = (int16_t)s;
-    if (lane == 0) *reinterpret_cast<float*>(yb) = d;
+    q8k_wave_store(v, y + (int64_t)b * kQ8KBytes, lane);
 }
 
 void launch_quant_q8k(const float* x, uint8_t* y, int n, hipStream_t s) {
@@ -751,32 +736,55 @@ static void launch_fused(const MultiArgs& a, const float* x, int nb, hipStream_t
 // fp32 x, quantized to Q8_K in LDS as in k_q4k_fused_gemv, and stores
 // y[w] = silu(gate_w) * up_w.  gate_w and up_w are the bits the plain GEMV
 // gives, so y equals the GEMVs followed by bpd_swiglu_fuse_cpu's arithmetic.
-template <int ORDER, int G, int WPB>
+// QX: x is already Q8_K (xq), read from global memory, with no quantization pass.
+template <int ORDER, int G, int WPB, bool QX = false>
 __global__ __launch_bounds__(64 * WPB) void k_q4k_fused_swiglu(const uint8_t* __restrict__ wg,
                                                               const uint8_t* __restrict__ wu, float* __restrict__ y,
-                                                              int M, const float* __restrict__ x, int nb) {
+                                                              int M, const float* __restrict__ x,
+                                                              const uint8_t* __restrict__ xq, int nb) {
     extern __shared__ __align__(16) uint8_t xl[];
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int row = blockIdx.x * WPB + wave;
     const bool has = row < M;
     const int row0 = has ? row : 0;
-    XPre<1> P;
-    x32_load<WPB, 1>(P, x, nb);
-    WideW<2, G> pre;
+    if constexpr (QX) {
+        if (!has) return;
+        WideW<2, G> pre;
 #pragma unroll
-    for (int g = 0; g < G; g++) wide_load_g<2, G, true>(pre, g, wg, M, nb, row0, 0, wu);
-    __builtin_amdgcn_sched_barrier(0);
-    x32_quantize<WPB, 1>(P, xl, nb);
-    __syncthreads();
-    if (!has) return;
-    gemv_rows<ORDER, 2, G, true, true, true>(wg, xl, y, M, nb, row0, pre, wu);
+        for (int g = 0; g < G; g++) wide_load_g<2, G, true>(pre, g, wg, M, nb, row0, 0, wu);
+        gemv_rows<ORDER, 2, G, false, true, true>(wg, xq, y, M, nb, row0, pre, wu);
+    } else {
+        XPre<1> P;
+        x32_load<WPB, 1>(P, x, nb);
+        WideW<2, G> pre;
+#pragma unroll
+        for (int g = 0; g < G; g++) wide_load_g<2, G, true>(pre, g, wg, M, nb, row0, 0, wu);
+        __builtin_amdgcn_sched_barrier(0);
+        x32_quantize<WPB, 1>(P, xl, nb);
+        __syncthreads();
+        if (!has) return;
+        gemv_rows<ORDER, 2, G, true, true, true>(wg, xl, y, M, nb, row0, pre, wu);
+    }
 }
 
 template <int ORDER, int WPB>
 static void launch_swiglu(const uint8_t* wg, const uint8_t* wu, float* y, int M, const float* x, int nb,
                           hipStream_t s) {
     hipLaunchKernelGGL((k_q4k_fused_swiglu<ORDER, 2, WPB>), dim3((M + WPB - 1) / WPB), dim3(64 * WPB),
-                       (size_t)nb * kXS, s, wg, wu, y, M, x, nb);
+                       (size_t)nb * kXS, s, wg, wu, y, M, x, nullptr, nb);
+}
+
+// Gate and up from a Q8_K activation (K <= 4096), as launch_qmatmul_q4k_fused_swiglu
+// computes them after quantizing.
+void launch_qmatmul_q4k_swiglu_q8k(const uint8_t* wg, const uint8_t* wu, float* y, int M, const uint8_t* xq, int K,
+                                   int order, hipStream_t s) {
+    const int nb = K / 256;
+    if (order == 0)
+        hipLaunchKernelGGL((k_q4k_fused_swiglu<0, 2, 4, true>), dim3((M + 3) / 4), dim3(256), 0, s, wg, wu, y, M,
+                           nullptr, xq, nb);
+    else
+        hipLaunchKernelGGL((k_q4k_fused_swiglu<1, 2, 4, true>), dim3((M + 3) / 4), dim3(256), 0, s, wg, wu, y, M,
+                           nullptr, xq, nb);
 }
 
 // One quantization pass covers 4*WPB blocks: 4 waves up to K = 4096, 16 up to
