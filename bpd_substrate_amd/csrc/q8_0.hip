@@ -559,7 +559,8 @@ void launch_fill_zero(float* out, int64_t n, hipStream_t s) {
 template <int R, int AHEAD>
 static const void* wide_kernel(int nb) {
     constexpr int NT = WShape<R>::NT;
-    if (nb * 8 <= 2 * NT && R == 32) return reinterpret_cast<const void*>(&k_q8_0_gemv_W<R, AHEAD, 2>);
+    if constexpr (R == 32)
+        if (nb * 8 <= 2 * NT) return reinterpret_cast<const void*>(&k_q8_0_gemv_W<R, AHEAD, 2>);
     if (nb * 8 <= 4 * NT) return reinterpret_cast<const void*>(&k_q8_0_gemv_W<R, AHEAD, 4>);
     if (nb * 8 <= 8 * NT) return reinterpret_cast<const void*>(&k_q8_0_gemv_W<R, AHEAD, 8>);
     if (nb * 8 <= 16 * NT) return reinterpret_cast<const void*>(&k_q8_0_gemv_W<R, AHEAD, 16>);
