@@ -7,8 +7,8 @@
 //                         (bench/bpd_gemm_q8_0_cpu.c:32-86), pipelined chains
 //   k_q8_0_gemv_TP        the same cells, block products by producer waves and the
 //                         chains from LDS (few rows, long rows)
-//   k_q8_0_gemv_W         the same cells, rows streamed as 16-byte lanes through LDS
-//                         by loader waves, chains from LDS (cfg2 shapes)
+//   k_q8_0_gemv_V         the same cells, each wave streaming its 8 rows as 16-byte
+//                         lanes through its own LDS slot (cfg2 shapes)
 //   k_q8_0_gemm_T         the same cells, plain, for rows too long to stage
 //   k_q8_pad64            fp32 -> the padded Q8 layout (inference/llamatov_c_inference.py:88-100)
 //   k_q8_0_gemm_S(H)      the scalar order S on int8 MFMA (prefill)
@@ -358,48 +358,57 @@ __global__ __launch_bounds__(320) void k_q8_0_gemv_TP(const uint8_t* __restrict_
 }
 
 // ----------------------------------------------------------------------------
-// The same order T for 34-byte rows read as 16-byte lanes.  The loads of
+// The same order T for 34-byte rows read as 16-byte lanes, one wave per 8 rows
+// with nothing shared between the waves but the activation row.  The loads of
 // k_q8_0_gemv_T (a dword and a 16-bit word per lane and block) reach 3.6 TB/s
 // at the cfg2 shapes even without arithmetic; 16-byte lanes over the same
-// bytes reach 5.9.  A workgroup holds R rows of one token and 2R/8 waves:
-// waves R/8.. (loaders) stream the rows in chunks of 32 blocks -- 1088 bytes
-// of a row, 68 aligned 16-byte pieces -- keeping AHEAD chunks in flight in
-// registers and writing one chunk per step into a two-slot LDS ring (rows at
-// a 1104-byte pitch); waves 0..R/8-1 (chains) run k_q8_0_gemv_T's lanes: lane
-// (row, L) takes the dword at byte 34b + 2 + 4L of its row's chunk (two
-// aligned LDS dwords and v_alignbit for even b) and the 16-bit scale at 34b,
-// and extends acc_L = RN(RN(RN(Ad*Bd) * float(p_L)) + acc_L) in block order.
-// The activation row is loaded into registers before the weights (loads
-// return in order) and written to LDS when it arrives.  The products, their
-// order and the final combine are k_q8_0_gemv_T's, so the bits are too.
-// Needs nb % 32 == 0 and W 16-byte aligned (rows are then 16-byte aligned).
+// bytes reach 5.9.  Each wave streams its 8 rows in chunks of 32 blocks (1088
+// bytes of a row, 68 aligned 16-byte pieces, 544 pieces for the 8 rows: 9
+// loads per lane, the 9th on lanes 0..31) with AHEAD chunks in flight in
+// registers, and stages the current chunk in a private LDS slot (rows at a
+// 1248-byte pitch, 312 dwords = 56 mod 64, so the 8 rows' dword windows fall
+// in disjoint banks).  The wave then forms the chunk's 8 x 32 scale products
+// RN(Ad*Bd) once (4 per lane) and lane (row, L) runs k_q8_0_gemv_T's chain
+// acc_L = RN(RN(RN(Ad*Bd) * float(p_L)) + acc_L) over the 32 blocks in order:
+// quant dword at byte 34b + 2 + 4L (two aligned LDS dwords and v_alignbit for
+// even b), the activation dwords four blocks at a time from an L-major copy.
+// A wave only waits for its own loads and LDS writes (in-order LDS queue), so
+// the one workgroup barrier is the one after the activation row is staged.
+// The products, their order and the final combine are k_q8_0_gemv_T's, so the
+// bits are too.  Needs nb % 32 == 0 and W 16-byte aligned.
 // ----------------------------------------------------------------------------
-typedef uint32_t w_u32x4 __attribute__((ext_vector_type(4)));  // native vector: stays in VGPRs
-constexpr int kWChunk = 32;                  // blocks per chunk
-constexpr int kWRowB = kWChunk * kQ80Bytes;  // 1088 bytes of a row per chunk
-constexpr int kWPieces = kWRowB / 16;        // 68 aligned 16-byte pieces
-constexpr int kWPitch = kWRowB + 16;         // LDS row pitch: rows 4 banks apart
-constexpr int kWXD = 2;                      // activation scales per thread
+typedef uint32_t v_u32x4 __attribute__((ext_vector_type(4)));  // native vectors: stay in VGPRs
+typedef float v_f32x4 __attribute__((ext_vector_type(4)));
+constexpr int kVChunk = 32;                  // blocks per chunk
+constexpr int kVRowB = kVChunk * kQ80Bytes;  // 1088 bytes of a row per chunk
+constexpr int kVPieces = kVRowB / 16;        // 68 aligned 16-byte pieces
+constexpr int kVPitch = 1248;                // LDS row pitch, bytes
+constexpr int kVWavePieces = 8 * kVPieces;   // 544 pieces per wave and chunk
+constexpr int kVPer = (kVWavePieces + 63) / 64;  // loads per lane and chunk
+constexpr int kVScP = kVChunk + 4;           // scale-product row pitch, floats
+constexpr int kVSlot = 8 * kVPitch + 8 * kVScP * 4;  // LDS bytes per wave
+constexpr int kVAhead = 2;                   // chunks in flight per wave
 
-template <int R>
-struct WShape {
-    static constexpr int CW = R / 8;                                  // chain waves = loader waves
-    static constexpr int NT = 128 * CW;                               // threads
-    static constexpr int LT = 64 * CW;                                // loader threads
-    static constexpr int PIECES = R * kWPieces;                       // 16-byte pieces of a chunk
-    static constexpr int PER = (PIECES + LT - 1) / LT;                // pieces per loader thread
-    static constexpr size_t RING = 2 * (size_t)R * kWPitch;           // LDS bytes of the ring
-};
+__host__ __device__ constexpr int v_xpitch(int nb) { return nb + 4; }  // dwords: the 8 L rows 4 banks apart
+__host__ __device__ constexpr size_t v_lds_bytes(int nb, int nw) {
+    return (size_t)(8 * v_xpitch(nb) + nb) * 4 + (size_t)nw * kVSlot;
+}
 
-template <int PER>
-__device__ __forceinline__ void w_load(w_u32x4 (&v)[PER], const uint8_t* __restrict__ wbase,
-                                       const uint32_t (&off)[PER], int c) {
+// the wave's own LDS writes complete before its later reads (and the compiler
+// keeps them in that order)
+__device__ __forceinline__ void v_lds_order() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+__device__ __forceinline__ bool v_piece(int lane, int k) { return k < kVPer - 1 || lane + 64 * k < kVWavePieces; }
+
+__device__ __forceinline__ void v_load(v_u32x4 (&v)[kVPer], const uint8_t* __restrict__ wbase,
+                                       const uint32_t (&off)[kVPer], int c, int lane) {
 #pragma unroll
-    for (int k = 0; k < PER; k++) v[k] = *reinterpret_cast<const w_u32x4*>(wbase + off[k] + (uint32_t)c * kWRowB);
+    for (int k = 0; k < kVPer; k++)
+        if (v_piece(lane, k)) v[k] = *reinterpret_cast<const v_u32x4*>(wbase + off[k] + (uint32_t)c * kVRowB);
 }
 
 // dword at byte 34 bb + 2 + 4L of a row's chunk in LDS: 4-aligned for odd bb, 2 mod 4 for even bb
-__device__ __forceinline__ uint32_t w_quants(const uint8_t* rowp, int bb, int L) {
+__device__ __forceinline__ uint32_t v_quants(const uint8_t* rowp, int bb, int L) {
     const int o = bb * kQ80Bytes + 2 + 4 * L;
     if (bb & 1) return *reinterpret_cast<const uint32_t*>(rowp + o);
     const uint32_t lo = *reinterpret_cast<const uint32_t*>(rowp + o - 2);
@@ -407,110 +416,106 @@ __device__ __forceinline__ uint32_t w_quants(const uint8_t* rowp, int bb, int L)
     return __builtin_amdgcn_alignbit(hi, lo, 16);
 }
 
-// chain lane (row, L) over the 32 blocks of chunk c: k_q8_0_gemv_T's steps
-__device__ __forceinline__ float w_chain(const uint8_t* rowp, const uint32_t* __restrict__ xs,
-                                         const float* __restrict__ xd, int c, int L, float acc) {
-#pragma unroll 8
-    for (int bb = 0; bb < kWChunk; bb++) {
-        const int b = c * kWChunk + bb;
-        const uint32_t q = w_quants(rowp, bb, L);
-        const uint32_t d = *reinterpret_cast<const uint16_t*>(rowp + bb * kQ80Bytes);
-        const float scale = f16_ieee(d) * xd[b];
-        const int p = sdot4(q, xs[b * 8 + L], 0);
-        const float prod = scale * (float)p;
-        acc = prod + acc;
-    }
-    return acc;
-}
-
-// Step c = c0 + U (pf slot U holds chunk c; U is a template argument so that pf
-// is indexed by constants only): the loaders write chunk c to ring slot c&1 and
-// refill slot U with chunk c + AHEAD; barrier; the chains take chunk c.  Slot
-// c&1 is written again at step c+2, after the barrier of step c+1, which the
-// chain waves reach only once they are done with chunk c.
-template <int U, int R, int AHEAD>
-__device__ __forceinline__ void w_step(w_u32x4 (&pf)[AHEAD][WShape<R>::PER], uint8_t* ring,
-                                       const uint8_t* __restrict__ wbase, const uint32_t (&off)[WShape<R>::PER],
-                                       const uint32_t (&dst)[WShape<R>::PER], bool loader, int lt, int c0, int nch,
-                                       int rr, const uint32_t* xs, const float* xd, int L, float& acc) {
-    using S = WShape<R>;
+// Chunk c = c0 + U (register slot U holds it; U is a template argument so that
+// the slots are indexed by constants): stage it, refill slot U with chunk
+// c + kVAhead, scale products, chains.
+template <int U>
+__device__ __forceinline__ void v_step(v_u32x4 (&pf)[kVAhead][kVPer], uint8_t* slot, float* sc,
+                                       const uint8_t* __restrict__ wbase, const uint32_t (&off)[kVPer],
+                                       const uint32_t (&dst)[kVPer], int lane, int c0, int nch,
+                                       const uint32_t* __restrict__ xs, const float* __restrict__ xd, int xp,
+                                       float& acc) {
     const int c = c0 + U;
-    if (c >= nch) return;  // uniform over the workgroup
-    uint8_t* slot = ring + (c & 1) * R * kWPitch;
-    if (loader) {
+    if (c >= nch) return;  // uniform over the wave
 #pragma unroll
-        for (int k = 0; k < S::PER; k++)
-            if (lt + k * S::LT < S::PIECES) *reinterpret_cast<w_u32x4*>(slot + dst[k]) = pf[U][k];
-        if (c + AHEAD < nch) w_load<S::PER>(pf[U], wbase, off, c + AHEAD);
+    for (int k = 0; k < kVPer; k++)
+        if (v_piece(lane, k)) *reinterpret_cast<v_u32x4*>(slot + dst[k]) = pf[U][k];
+    if (c + kVAhead < nch) v_load(pf[U], wbase, off, c + kVAhead, lane);
+    v_lds_order();
+#pragma unroll
+    for (int t = 0; t < 8 * kVChunk / 64; t++) {
+        const int j = lane + 64 * t, r = j / kVChunk, bb = j % kVChunk;
+        const uint32_t ad = *reinterpret_cast<const uint16_t*>(slot + r * kVPitch + bb * kQ80Bytes);
+        sc[r * kVScP + bb] = f16_ieee(ad) * xd[c * kVChunk + bb];
     }
-    __syncthreads();
-    if (!loader) acc = w_chain(slot + rr * kWPitch, xs, xd, c, L, acc);
+    v_lds_order();
+    const int L = lane & 7, rr = lane >> 3;
+    const uint8_t* rowp = slot + rr * kVPitch;
+    const uint32_t* xl = xs + L * xp + c * kVChunk;
+    const float* sr = sc + rr * kVScP;
+#pragma unroll
+    for (int b4 = 0; b4 < kVChunk; b4 += 4) {
+        const v_u32x4 xq = *reinterpret_cast<const v_u32x4*>(xl + b4);
+        const v_f32x4 s4 = *reinterpret_cast<const v_f32x4*>(sr + b4);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int p = sdot4(v_quants(rowp, b4 + j, L), xq[j], 0);
+            const float prod = s4[j] * (float)p;
+            acc = prod + acc;
+        }
+    }
 }
 
-template <int R, int AHEAD, int XR>
-__global__ __launch_bounds__(WShape<R>::NT) void k_q8_0_gemv_W(const uint8_t* __restrict__ W,
-                                                              const uint8_t* __restrict__ Xq,
-                                                              float* __restrict__ out, int m_weight, int nb) {
-    using S = WShape<R>;
-    static_assert(AHEAD == 2 || AHEAD == 4, "one w_step call per chunk in flight");
-    extern __shared__ uint32_t lds[];
-    uint32_t* xs = lds;                                       // [nb][8] activation quants
-    float* xd = reinterpret_cast<float*>(lds + nb * 8);       // [nb] activation scales
-    uint8_t* ring = reinterpret_cast<uint8_t*>(lds + nb * 9);
-    const int tid = threadIdx.x, tok = blockIdx.y, row0 = blockIdx.x * R, nch = nb / kWChunk;
+// NW waves of 8 rows per workgroup; x quants in XR dwords per thread (nb*8 <= XR*64*NW).
+template <int NW, int XR>
+__global__ __launch_bounds__(64 * NW) void k_q8_0_gemv_V(const uint8_t* __restrict__ W,
+                                                        const uint8_t* __restrict__ Xq, float* __restrict__ out,
+                                                        int m_weight, int nb) {
+    static_assert(kVAhead == 2, "one v_step call per chunk in flight");
+    constexpr int NT = 64 * NW;
+    extern __shared__ __align__(16) uint32_t lds[];
+    const int xp = v_xpitch(nb);
+    uint32_t* xs = lds;                                          // [8][xp]: quant dword L of block b at L*xp + b
+    float* xd = reinterpret_cast<float*>(lds + 8 * xp);          // [nb] activation scales
+    const int tid = threadIdx.x, lane = tid & 63, tok = blockIdx.y;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    uint8_t* slot = reinterpret_cast<uint8_t*>(lds + 8 * xp + nb) + wave * kVSlot;
+    float* sc = reinterpret_cast<float*>(slot + 8 * kVPitch);    // [8][kVScP] scale products
+    const int row0 = (blockIdx.x * NW + wave) * 8, nch = nb / kVChunk;
     const int64_t bpr = (int64_t)nb * kQ80Bytes;
-    const bool loader = tid >= S::LT;
-    const int lt = tid - S::LT;
     // rows past m_weight re-read row m_weight-1 (their cells are not written)
     const int row0c = min(row0, m_weight - 1);
     const uint8_t* wbase = W + (int64_t)row0c * bpr;
-    // the activation row: quant dword i = 8b + L and scale b, into registers first
+    // the activation row into registers first (loads return in order)
     const uint8_t* xr = Xq + (int64_t)tok * bpr;
-    uint32_t xq[XR], xh[kWXD];
+    constexpr int XD = (XR + 7) / 8;  // nb <= XD * NT scales
+    uint32_t xq[XR], xh[XD];
 #pragma unroll
     for (int u = 0; u < XR; u++) {
-        const int i = min(tid + u * S::NT, nb * 8 - 1);
+        const int i = min(tid + u * NT, nb * 8 - 1);
         xq[u] = ld_u32(xr + (int64_t)(i >> 3) * kQ80Bytes + 2 + 4 * (i & 7));
     }
 #pragma unroll
-    for (int u = 0; u < kWXD; u++) xh[u] = ld_u16(xr + (int64_t)min(tid + u * S::NT, nb - 1) * kQ80Bytes);
-    // loader piece k of this thread: f = lt + k*LT is row f/68, piece f%68
-    uint32_t off[S::PER], dst[S::PER];
-    w_u32x4 pf[AHEAD][S::PER];
-    if (loader) {
+    for (int u = 0; u < XD; u++) xh[u] = ld_u16(xr + (int64_t)min(tid + u * NT, nb - 1) * kQ80Bytes);
+    // piece k of this lane: f = lane + 64k is row f/68, piece f%68 of the chunk
+    uint32_t off[kVPer], dst[kVPer];
 #pragma unroll
-        for (int k = 0; k < S::PER; k++) {
-            const int f = min(lt + k * S::LT, S::PIECES - 1), r = f / kWPieces, p = f % kWPieces;
-            off[k] = (uint32_t)((min(row0 + r, m_weight - 1) - row0c) * bpr) + 16u * p;
-            dst[k] = (uint32_t)(r * kWPitch + 16 * p);
-        }
-#pragma unroll
-        for (int a = 0; a < AHEAD; a++)
-            if (a < nch) w_load<S::PER>(pf[a], wbase, off, a);
+    for (int k = 0; k < kVPer; k++) {
+        const int f = min(lane + 64 * k, kVWavePieces - 1), r = f / kVPieces, p = f % kVPieces;
+        off[k] = (uint32_t)((min(row0 + r, m_weight - 1) - row0c) * bpr) + 16u * p;
+        dst[k] = (uint32_t)(r * kVPitch + 16 * p);
     }
+    v_u32x4 pf[kVAhead][kVPer];
+#pragma unroll
+    for (int a = 0; a < kVAhead; a++)
+        if (a < nch) v_load(pf[a], wbase, off, a, lane);
 #pragma unroll
     for (int u = 0; u < XR; u++)
-        if (tid + u * S::NT < nb * 8) xs[tid + u * S::NT] = xq[u];
+        if (tid + u * NT < nb * 8) xs[((tid + u * NT) & 7) * xp + ((tid + u * NT) >> 3)] = xq[u];
 #pragma unroll
-    for (int u = 0; u < kWXD; u++)
-        if (tid + u * S::NT < nb) xd[tid + u * S::NT] = f16_ieee(xh[u]);
-    const int lane = tid & 63, L = lane & 7, rr = (tid >> 6) * 8 + (lane >> 3);  // chain waves: tid < LT
+    for (int u = 0; u < XD; u++)
+        if (tid + u * NT < nb) xd[tid + u * NT] = f16_ieee(xh[u]);
+    __syncthreads();
     float acc = 0.0f;
-    for (int c0 = 0; c0 < nch; c0 += AHEAD) {
-        w_step<0, R, AHEAD>(pf, ring, wbase, off, dst, loader, lt, c0, nch, rr, xs, xd, L, acc);
-        w_step<1, R, AHEAD>(pf, ring, wbase, off, dst, loader, lt, c0, nch, rr, xs, xd, L, acc);
-        if constexpr (AHEAD == 4) {
-            w_step<2, R, AHEAD>(pf, ring, wbase, off, dst, loader, lt, c0, nch, rr, xs, xd, L, acc);
-            w_step<3, R, AHEAD>(pf, ring, wbase, off, dst, loader, lt, c0, nch, rr, xs, xd, L, acc);
-        }
+    for (int c0 = 0; c0 < nch; c0 += kVAhead) {
+        v_step<0>(pf, slot, sc, wbase, off, dst, lane, c0, nch, xs, xd, xp, acc);
+        v_step<1>(pf, slot, sc, wbase, off, dst, lane, c0, nch, xs, xd, xp, acc);
     }
-    if (!loader) {
-        acc = acc + xor_f(acc, 4);
-        acc = acc + xor_f(acc, 2);
-        acc = acc + xor_f(acc, 1);
-        const int row = row0 + rr;
-        if (L == 0 && row < m_weight) out[(int64_t)tok * m_weight + row] = acc;
-    }
+    acc = acc + xor_f(acc, 4);
+    acc = acc + xor_f(acc, 2);
+    acc = acc + xor_f(acc, 1);
+    const int row = row0 + (lane >> 3);
+    if ((lane & 7) == 0 && row < m_weight) out[(int64_t)tok * m_weight + row] = acc;
 }
 
 // Plain form of the same order for activation rows too long to stage in LDS.
@@ -555,48 +560,57 @@ void launch_fill_zero(float* out, int64_t n, hipStream_t s) {
     if (n > 0) hipLaunchKernelGGL(k_fill_zero, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, out, n);
 }
 
-// k_q8_0_gemv_W for LAYOUT 0: x quants in XR dwords per thread (nb*8 <= XR*NT).
-template <int R, int AHEAD>
-static const void* wide_kernel(int nb) {
-    constexpr int NT = WShape<R>::NT;
-    if constexpr (R == 32)
-        if (nb * 8 <= 2 * NT) return reinterpret_cast<const void*>(&k_q8_0_gemv_W<R, AHEAD, 2>);
-    if (nb * 8 <= 4 * NT) return reinterpret_cast<const void*>(&k_q8_0_gemv_W<R, AHEAD, 4>);
-    if (nb * 8 <= 8 * NT) return reinterpret_cast<const void*>(&k_q8_0_gemv_W<R, AHEAD, 8>);
-    if (nb * 8 <= 16 * NT) return reinterpret_cast<const void*>(&k_q8_0_gemv_W<R, AHEAD, 16>);
+// k_q8_0_gemv_V with NW waves per workgroup for nb blocks, or NULL when the
+// activation row does not fit XR <= 32 dwords per thread.
+template <int NW>
+static const void* v_kernel(int nb) {
+    constexpr int NT = 64 * NW;
+    if (nb * 8 <= 2 * NT) return reinterpret_cast<const void*>(&k_q8_0_gemv_V<NW, 2>);
+    if (nb * 8 <= 4 * NT) return reinterpret_cast<const void*>(&k_q8_0_gemv_V<NW, 4>);
+    if (nb * 8 <= 8 * NT) return reinterpret_cast<const void*>(&k_q8_0_gemv_V<NW, 8>);
+    if (nb * 8 <= 16 * NT) return reinterpret_cast<const void*>(&k_q8_0_gemv_V<NW, 16>);
+    if (nb * 8 <= 32 * NT) return reinterpret_cast<const void*>(&k_q8_0_gemv_V<NW, 32>);
     return nullptr;
 }
 
 // The wide-load kernel where it is measured faster (MI355X, graph, weights
-// beyond the MALL): 14336x4096 17.7 us (k_q8_0_gemv_T<16,4>: 19.8) and at 4
-// tokens 50.1 us (52.3) with R = 32; 4096x14336 20.2 us (k_q8_0_gemv_TP: 24.1)
-// with R = 16.  At 4096x4096 and below the kernels of dispatch_T are as fast or
-// faster.  Returns false when the shape or W's alignment does not fit.
+// beyond the MALL), by 8-row waves w = ceil(m_weight/8) * m_tokens: from
+// w >= 512 (and from 256 when nb >= 256), 4 waves per workgroup from w >= 1024
+// and 2 below, so that there are >= 256 workgroups.  14336x4096 14.8 us (a
+// loader/chain kernel with a shared LDS ring and one barrier per chunk: 17.6;
+// k_q8_0_gemv_T<16,4>: 19.8), 4096x14336 19.1 (20.5; k_q8_0_gemv_TP: 24.1),
+// 4096x4096 7.9 (TP: 8.6), 14336x4096 x 4 tokens 36.1 (50.3); at 2048x4096 and
+// below the kernels of dispatch_T are faster.
+// Returns false when the shape or W's alignment does not fit.
 static bool launch_wide(const uint8_t* Wq, const uint8_t* Xq, float* out, int m_weight, int m_tokens, int nb,
                         hipStream_t s) {
-    if (nb % kWChunk != 0 || (reinterpret_cast<uintptr_t>(Wq) & 15) != 0) return false;
-    const bool big = m_weight >= 8192;
-    if (!big && !(m_weight >= 2048 && nb >= 256)) return false;
-    const void* f = big ? wide_kernel<32, 2>(nb) : wide_kernel<16, 4>(nb);
-    const int nt = big ? WShape<32>::NT : WShape<16>::NT;
-    const size_t lds = (size_t)nb * 36 + (big ? WShape<32>::RING : WShape<16>::RING);
-    if (f == nullptr || nb > kWXD * nt || lds > 160 * 1024) return false;
+    if (nb % kVChunk != 0 || (reinterpret_cast<uintptr_t>(Wq) & 15) != 0) return false;
+    const int64_t waves = (int64_t)((m_weight + 7) / 8) * m_tokens;
+    if (!(waves >= 512 || (waves >= 256 && nb >= 256))) return false;
+    int nw = waves >= 1024 ? 4 : 2;
+    const void* f = nw == 4 ? v_kernel<4>(nb) : v_kernel<2>(nb);
+    if (f == nullptr && nw == 2) {
+        nw = 4;
+        f = v_kernel<4>(nb);
+    }
+    const size_t lds = v_lds_bytes(nb, nw);
+    if (f == nullptr || lds > 160 * 1024) return false;
     // more than 64 KB of dynamic LDS is asked for once per process and kernel
     static std::once_flag once;
     static bool lds_ok = false;
     std::call_once(once, [] {
         lds_ok = true;
-        for (int n : {64, 128, 256, 512, 1024})
-            for (const void* k : {wide_kernel<32, 2>(n), wide_kernel<16, 4>(n)})
+        for (int n : {32, 64, 128, 256, 512, 1024})
+            for (const void* k : {v_kernel<2>(n), v_kernel<4>(n)})
                 if (k != nullptr && hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) !=
                                         hipSuccess)
                     lds_ok = false;
         (void)hipGetLastError();
     });
     if (!lds_ok) return false;
-    const int rows = big ? 32 : 16;
+    const int rows = 8 * nw;
     void* args[] = {const_cast<uint8_t**>(&Wq), const_cast<uint8_t**>(&Xq), &out, &m_weight, &nb};
-    (void)hipLaunchKernel(f, dim3((m_weight + rows - 1) / rows, m_tokens), dim3(nt), args, lds, s);
+    (void)hipLaunchKernel(f, dim3((m_weight + rows - 1) / rows, m_tokens), dim3(64 * nw), args, lds, s);
     return true;
 }
 

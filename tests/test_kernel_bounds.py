@@ -107,59 +107,83 @@ def test_dequant_in_bounds(nb):
 
 # ---------------------------------------------------------------- Q8_0 tile-order GEMV
 
-def q8_wide_config(mw, nb):
-    """(R, AHEAD, XR) of k_q8_0_gemv_W as launch_wide() in q8_0.hip picks it for a
+V_PITCH, V_SCP = 1248, 36
+V_SLOT = 8 * V_PITCH + 8 * V_SCP * 4
+
+
+def v_lds(nb, nw):
+    return (8 * (nb + 4) + nb) * 4 + nw * V_SLOT
+
+
+def q8_wide_config(mw, mt, nb):
+    """(NW, XR) of k_q8_0_gemv_V as launch_wide() in q8_0.hip picks it for a
     16-byte aligned W, or None."""
     if nb == 0 or nb % 32 != 0:
         return None
-    big = mw >= 8192
-    if not big and not (mw >= 2048 and nb >= 256):
+    waves = (mw + 7) // 8 * mt
+    if not (waves >= 512 or (waves >= 256 and nb >= 256)):
         return None
-    R, AHEAD = (32, 2) if big else (16, 4)
-    NT = 128 * (R // 8)
-    XR = next((x for x in ((2, 4, 8, 16) if R == 32 else (4, 8, 16)) if nb * 8 <= x * NT), None)
-    if XR is None or nb > 2 * NT or nb * 36 + 2 * R * 1104 > 160 * 1024:
+    xr = lambda nw: next((x for x in (2, 4, 8, 16, 32) if nb * 8 <= x * 64 * nw), None)
+    nw = 4 if waves >= 1024 else 2
+    XR = xr(nw)
+    if XR is None and nw == 2:
+        nw, XR = 4, xr(4)
+    if XR is None or v_lds(nb, nw) > 160 * 1024:
         return None
-    return R, AHEAD, XR
+    return nw, XR
 
 
 def check_wide_q8(mw, mt, nb, w_size, x_size, out_size):
-    """k_q8_0_gemv_W: loader thread lt of workgroup g reads 16-byte piece
-    f = min(lt + k*LT, R*68 - 1) -- row f/68, bytes 1088c + 16(f%68) of that row
-    (rows past mw re-read row mw-1) -- for chunks c < nb/32 and writes it at
-    (f/68)*1104 + 16(f%68) of a ring slot; chain lane (row, L) reads the row
-    chunk's bytes [34bb+2+4L, +4) (even bb: [34bb+4L, 34bb+4L+8)) and the scale at
-    34bb; the activation is quant dword min(i, 8nb-1) and scale min(j, nb-1)."""
-    R, AHEAD, XR = q8_wide_config(mw, nb)
-    NT, LT, PIECES = 128 * (R // 8), 64 * (R // 8), R * 68
-    PER = -(-PIECES // LT)
-    bpr, nch = nb * Q80, nb // 32
-    lt = np.arange(LT)
-    groups = -(-mw // R)
+    """k_q8_0_gemv_V: lane l of wave w in workgroup g (rows row0 = 8(g*NW + w) ..)
+    reads 16-byte piece f = min(l + 64k, 543) (k < 9; k = 8 on lanes < 32 only)
+    -- row f/68, bytes 1088c + 16(f%68) of that row (rows past mw re-read row
+    mw-1) -- for chunks c < nb/32 and writes it at (f/68)*1248 + 16(f%68) of the
+    wave's slot; the scale pass reads the 16-bit scale at r*1248 + 34bb and
+    writes sc[r*36 + bb] (r < 8, bb < 32); chain lane (row, L) reads the row
+    chunk's bytes [34bb+2+4L, +4) (even bb: [34bb+4L, 34bb+4L+8)), four x dwords
+    at L*(nb+4) + 32c + 4i and four products at row*36 + 4i; the activation is
+    quant dword min(i, 8nb-1) and scale min(j, nb-1)."""
+    NW, XR = q8_wide_config(mw, mt, nb)
+    NT, bpr, nch, xp = 64 * NW, nb * Q80, nb // 32, nb + 4
+    l = np.arange(64)
+    groups = -(-mw // (8 * NW))
     for g in sorted({0, groups - 1}):
-        row0 = g * R
-        row0c = min(row0, mw - 1)
-        for k in range(PER):
-            f = np.minimum(lt + k * LT, PIECES - 1)
-            r, pc = f // 68, f % 68
-            off = (np.minimum(row0 + r, mw - 1) - row0c) * bpr + 16 * pc
-            for c in (0, nch - 1):
-                a = row0c * bpr + off + c * 1088
-                assert a.min() >= 0 and (a + 16).max() <= w_size
-            dst = r * 1104 + 16 * pc
-            assert (dst + 16).max() <= R * 1104
+        for w in range(NW):
+            row0 = (g * NW + w) * 8
+            row0c = min(row0, mw - 1)
+            for k in range(9):
+                f = np.minimum(l + 64 * k, 543)
+                if k == 8:
+                    f = f[l < 32]
+                r, pc = f // 68, f % 68
+                off = (np.minimum(row0 + r, mw - 1) - row0c) * bpr + 16 * pc
+                for c in (0, nch - 1):
+                    a = row0c * bpr + off + c * 1088
+                    assert a.min() >= 0 and (a + 16).max() <= w_size
+                assert (r * V_PITCH + 16 * pc + 16).max() <= 8 * V_PITCH
+    j = np.arange(256)
+    r, bb = j // 32, j % 32
+    assert (r * V_PITCH + 34 * bb + 2).max() <= 8 * V_PITCH and (r * V_SCP + bb).max() < 8 * V_SCP
     L = np.arange(8)
     for bb in range(32):
         o = 34 * bb + 2 + 4 * L
         lo, hi = (o - 2, o + 6) if bb % 2 == 0 else (o, o + 4)
-        assert lo.min() >= 0 and hi.max() <= 1088 and 34 * bb + 2 <= 1088
+        assert lo.min() >= 0 and hi.max() <= 1088 <= V_PITCH
+    assert 7 * xp + 32 * (nch - 1) + 28 + 4 <= 8 * xp and 7 * V_SCP + 28 + 4 <= 8 * V_SCP
     i = np.minimum(np.arange(XR * NT), nb * 8 - 1)
-    j = np.minimum(np.arange(2 * NT), nb - 1)
+    jd = np.minimum(np.arange(-(-XR // 8) * NT), nb - 1)
+    assert nb <= -(-XR // 8) * NT
     for tok in range(mt):
         assert tok * bpr + ((i >> 3) * Q80 + 2 + 4 * (i & 7) + 4).max() <= x_size
-        assert tok * bpr + (j * Q80 + 2).max() <= x_size
+        assert tok * bpr + (jd * Q80 + 2).max() <= x_size
+    st = np.arange(XR * NT)
+    st = st[st < nb * 8]
+    assert ((st & 7) * xp + (st >> 3)).max() < 8 * xp
+    # 16-byte alignment of every vector LDS access: slots, x rows, product rows
+    assert ((8 * xp + nb) * 4) % 16 == 0 and V_SLOT % 16 == 0 and (8 * V_PITCH) % 16 == 0
+    assert (xp * 4) % 16 == 0 and (V_SCP * 4) % 16 == 0
     assert (mt - 1) * mw * 4 + mw * 4 <= out_size
-    assert nb * 36 + 2 * R * 1104 <= 160 * 1024
+    assert v_lds(nb, NW) <= 160 * 1024
 
 
 def q8_gemv_config(mw, mt, K):
@@ -167,7 +191,7 @@ def q8_gemv_config(mw, mt, K):
     waves = (mw + 7) // 8
     if nb == 0:
         return None
-    if q8_wide_config(mw, nb) is not None:
+    if q8_wide_config(mw, mt, nb) is not None:
         return ("wide", 0, 0)
     if nb * 36 > 64 * 1024:
         return ("plain", 4, 1)
@@ -207,7 +231,9 @@ def check_producer(mw, mt, nb, layout, w_size):
                                      (2048, 2, 2048), (1, 1, 32), (13, 3, 4128), (64, 4, 256), (6, 3, 96),
                                      (3, 1, 64), (17, 1, 32), (15, 1, 256), (23, 1, 256), (7, 1, 256),
                                      (8192, 2, 1024), (8200, 3, 8192), (2048, 1, 8192), (9000, 1, 2048),
-                                     (14336, 4, 4096), (2056, 1, 16384), (8192, 1, 32768)])
+                                     (14336, 4, 4096), (2056, 1, 16384), (8192, 1, 32768), (2048, 1, 32768),
+                                     (4096, 4, 4096), (4096, 2, 14336), (512, 1, 8192),
+                                     (4100, 1, 4096), (1024, 1, 14336), (2048, 1, 4096)])
 def test_q8_0_gemv_T_in_bounds(mw, mt, K):
     cfg = q8_gemv_config(mw, mt, K)
     nb = K // 32
