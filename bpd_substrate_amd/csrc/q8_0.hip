@@ -7,8 +7,8 @@
 //                         (bench/bpd_gemm_q8_0_cpu.c:32-86), pipelined chains
 //   k_q8_0_gemv_TP        the same cells, block products by producer waves and the
 //                         chains from LDS (few rows, long rows)
-//   k_q8_0_gemv_V         the same cells, each wave streaming its 8 rows as 16-byte
-//                         lanes through its own LDS slot (cfg2 shapes)
+//   k_q8_0_gemv_V         the same cells, each wave streaming its 4 rows as 16-byte
+//                         lanes through its own LDS slot, two lanes per chain
 //   k_q8_0_gemm_T         the same cells, plain, for rows too long to stage
 //   k_q8_pad64            fp32 -> the padded Q8 layout (inference/llamatov_c_inference.py:88-100)
 //   k_q8_0_gemm_S(H)      the scalar order S on int8 MFMA (prefill)
@@ -358,40 +358,47 @@ __global__ __launch_bounds__(320) void k_q8_0_gemv_TP(const uint8_t* __restrict_
 }
 
 // ----------------------------------------------------------------------------
-// The same order T for 34-byte rows read as 16-byte lanes, one wave per 8 rows
-// with nothing shared between the waves but the activation row.  The loads of
-// k_q8_0_gemv_T (a dword and a 16-bit word per lane and block) reach 3.6 TB/s
-// at the cfg2 shapes even without arithmetic; 16-byte lanes over the same
-// bytes reach 5.9.  Each wave streams its 8 rows in chunks of 32 blocks (1088
-// bytes of a row, 68 aligned 16-byte pieces, 544 pieces for the 8 rows: 9
-// loads per lane, the 9th on lanes 0..31) with AHEAD chunks in flight in
-// registers, and stages the current chunk in a private LDS slot (rows at a
-// 1248-byte pitch, 312 dwords = 56 mod 64, so the 8 rows' dword windows fall
-// in disjoint banks).  The wave then forms the chunk's 8 x 32 scale products
-// RN(Ad*Bd) once (4 per lane) and lane (row, L) runs k_q8_0_gemv_T's chain
-// acc_L = RN(RN(RN(Ad*Bd) * float(p_L)) + acc_L) over the 32 blocks in order:
-// quant dword at byte 34b + 2 + 4L (two aligned LDS dwords and v_alignbit for
-// even b), the activation dwords four blocks at a time from an L-major copy.
-// A wave only waits for its own loads and LDS writes (in-order LDS queue), so
-// the one workgroup barrier is the one after the activation row is staged.
-// The products, their order and the final combine are k_q8_0_gemv_T's, so the
-// bits are too.  Needs nb % 32 == 0 and W 16-byte aligned.
+// The same order T for 34-byte rows read as 16-byte lanes, one wave per 4 rows
+// and two lanes per chain, with nothing shared between the waves but the
+// activation row.  The loads of k_q8_0_gemv_T (a dword and a 16-bit word per
+// lane and block) reach 3.6 TB/s at the cfg2 shapes even without arithmetic;
+// 16-byte lanes over the same bytes reach 5.9.
+// Each wave streams its 4 rows in chunks of 32 blocks (1088 bytes of a row, 68
+// aligned 16-byte pieces, 272 pieces for the 4 rows: 5 loads per lane, the 5th
+// on lanes 0..15) with 2 chunks in flight in registers, and stages the current
+// chunk in a private LDS slot (1248-byte row pitch).  It then forms the
+// chunk's 4 x 32 scale products RN(Ad*Bd) once (2 per lane).
+// Lane (row, L, h), lane index 16 row + 2L + h, computes the products
+// RN(RN(Ad*Bd) * float(p_L)) of the blocks b with b % 2 == h: the quant dword at
+// byte 34b + 2 + 4L (two aligned LDS dwords and v_alignbit), the activation
+// dwords and scale products four blocks at a time from copies split by block
+// parity.  Both lanes of a pair then extend the same chain
+//   acc_L = RN(p_L(b) + acc_L),  acc_L = RN(p_L(b+1) + acc_L)
+// taking the even block's product from lane 2L and the odd one's from lane
+// 2L+1 (DPP quad_perm in the adds), so they hold identical accumulators.
+// A wave waits only for its own loads and its own LDS writes (the LDS queue is
+// in order per wave): the one workgroup barrier is the one after the
+// activation row is staged.  The products, their order and the final combine
+// are k_q8_0_gemv_T's, so the bits are too.  Needs nb % 32 == 0 and W 16-byte
+// aligned.
 // ----------------------------------------------------------------------------
 typedef uint32_t v_u32x4 __attribute__((ext_vector_type(4)));  // native vectors: stay in VGPRs
 typedef float v_f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kVChunk = 32;                  // blocks per chunk
 constexpr int kVRowB = kVChunk * kQ80Bytes;  // 1088 bytes of a row per chunk
 constexpr int kVPieces = kVRowB / 16;        // 68 aligned 16-byte pieces
+constexpr int kVRows = 4;                    // rows per wave
 constexpr int kVPitch = 1248;                // LDS row pitch, bytes
-constexpr int kVWavePieces = 8 * kVPieces;   // 544 pieces per wave and chunk
+constexpr int kVWavePieces = kVRows * kVPieces;  // 272 pieces per wave and chunk
 constexpr int kVPer = (kVWavePieces + 63) / 64;  // loads per lane and chunk
-constexpr int kVScP = kVChunk + 4;           // scale-product row pitch, floats
-constexpr int kVSlot = 8 * kVPitch + 8 * kVScP * 4;  // LDS bytes per wave
+constexpr int kVScP = 20;                    // (row, parity) pitch of the scale products, floats
+constexpr int kVSlot = kVRows * kVPitch + 2 * kVRows * kVScP * 4;  // LDS bytes per wave
 constexpr int kVAhead = 2;                   // chunks in flight per wave
 
-__host__ __device__ constexpr int v_xpitch(int nb) { return nb + 4; }  // dwords: the 8 L rows 4 banks apart
+// activation quant dwords: [L][parity][nb/2 + 4] (the 16 rows of a read 4 banks apart)
+__host__ __device__ constexpr int v_xpitch(int nb) { return nb / 2 + 4; }
 __host__ __device__ constexpr size_t v_lds_bytes(int nb, int nw) {
-    return (size_t)(8 * v_xpitch(nb) + nb) * 4 + (size_t)nw * kVSlot;
+    return (size_t)(16 * v_xpitch(nb) + nb) * 4 + (size_t)nw * kVSlot;
 }
 
 // the wave's own LDS writes complete before its later reads (and the compiler
@@ -407,13 +414,11 @@ __device__ __forceinline__ void v_load(v_u32x4 (&v)[kVPer], const uint8_t* __res
         if (v_piece(lane, k)) v[k] = *reinterpret_cast<const v_u32x4*>(wbase + off[k] + (uint32_t)c * kVRowB);
 }
 
-// dword at byte 34 bb + 2 + 4L of a row's chunk in LDS: 4-aligned for odd bb, 2 mod 4 for even bb
-__device__ __forceinline__ uint32_t v_quants(const uint8_t* rowp, int bb, int L) {
-    const int o = bb * kQ80Bytes + 2 + 4 * L;
-    if (bb & 1) return *reinterpret_cast<const uint32_t*>(rowp + o);
-    const uint32_t lo = *reinterpret_cast<const uint32_t*>(rowp + o - 2);
-    const uint32_t hi = *reinterpret_cast<const uint32_t*>(rowp + o + 2);
-    return __builtin_amdgcn_alignbit(hi, lo, 16);
+// v read from lane (lane & ~3) + SEL and lane (lane & ~3) + 2 + SEL of each quad
+template <int SEL>
+__device__ __forceinline__ float v_pair(float v) {
+    constexpr int ctrl = SEL | (SEL << 2) | ((2 + SEL) << 4) | ((2 + SEL) << 6);  // quad_perm
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), ctrl, 0xF, 0xF, true));
 }
 
 // Chunk c = c0 + U (register slot U holds it; U is a template argument so that
@@ -433,30 +438,36 @@ __device__ __forceinline__ void v_step(v_u32x4 (&pf)[kVAhead][kVPer], uint8_t* s
     if (c + kVAhead < nch) v_load(pf[U], wbase, off, c + kVAhead, lane);
     v_lds_order();
 #pragma unroll
-    for (int t = 0; t < 8 * kVChunk / 64; t++) {
+    for (int t = 0; t < kVRows * kVChunk / 64; t++) {
         const int j = lane + 64 * t, r = j / kVChunk, bb = j % kVChunk;
         const uint32_t ad = *reinterpret_cast<const uint16_t*>(slot + r * kVPitch + bb * kQ80Bytes);
-        sc[r * kVScP + bb] = f16_ieee(ad) * xd[c * kVChunk + bb];
+        sc[(2 * r + (bb & 1)) * kVScP + (bb >> 1)] = f16_ieee(ad) * xd[c * kVChunk + bb];
     }
     v_lds_order();
-    const int L = lane & 7, rr = lane >> 3;
+    const int h = lane & 1, L = (lane >> 1) & 7, rr = lane >> 4;
     const uint8_t* rowp = slot + rr * kVPitch;
-    const uint32_t* xl = xs + L * xp + c * kVChunk;
-    const float* sr = sc + rr * kVScP;
+    const uint32_t* xl = xs + (2 * L + h) * xp + c * (kVChunk / 2);
+    const float* sr = sc + (2 * rr + h) * kVScP;
+    // this lane's quant dword in block bb + h (bb even) is at 34 bb + ob; 34 bb = 0 mod 4
+    const int ob = 34 * h + 2 + 4 * L, oa = ob & ~3, sh = (ob & 3) * 8;
 #pragma unroll
-    for (int b4 = 0; b4 < kVChunk; b4 += 4) {
-        const v_u32x4 xq = *reinterpret_cast<const v_u32x4*>(xl + b4);
-        const v_f32x4 s4 = *reinterpret_cast<const v_f32x4*>(sr + b4);
+    for (int b8 = 0; b8 < kVChunk; b8 += 8) {
+        const v_u32x4 xq = *reinterpret_cast<const v_u32x4*>(xl + b8 / 2);  // blocks b8+h, b8+2+h, ...
+        const v_f32x4 s4 = *reinterpret_cast<const v_f32x4*>(sr + b8 / 2);
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const int p = sdot4(v_quants(rowp, b4 + j, L), xq[j], 0);
-            const float prod = s4[j] * (float)p;
-            acc = prod + acc;
+            const int bb = b8 + 2 * j;
+            const uint32_t lo = *reinterpret_cast<const uint32_t*>(rowp + 34 * bb + oa);
+            const uint32_t hi = *reinterpret_cast<const uint32_t*>(rowp + 34 * bb + oa + 4);
+            const int p = sdot4(__builtin_amdgcn_alignbit(hi, lo, sh), xq[j], 0);
+            const float mine = s4[j] * (float)p;
+            acc = v_pair<0>(mine) + acc;  // block bb
+            acc = v_pair<1>(mine) + acc;  // block bb + 1
         }
     }
 }
 
-// NW waves of 8 rows per workgroup; x quants in XR dwords per thread (nb*8 <= XR*64*NW).
+// NW waves of 4 rows per workgroup; x quants in XR dwords per thread (nb*8 <= XR*64*NW).
 template <int NW, int XR>
 __global__ __launch_bounds__(64 * NW) void k_q8_0_gemv_V(const uint8_t* __restrict__ W,
                                                         const uint8_t* __restrict__ Xq, float* __restrict__ out,
@@ -465,13 +476,13 @@ __global__ __launch_bounds__(64 * NW) void k_q8_0_gemv_V(const uint8_t* __restri
     constexpr int NT = 64 * NW;
     extern __shared__ __align__(16) uint32_t lds[];
     const int xp = v_xpitch(nb);
-    uint32_t* xs = lds;                                          // [8][xp]: quant dword L of block b at L*xp + b
-    float* xd = reinterpret_cast<float*>(lds + 8 * xp);          // [nb] activation scales
+    uint32_t* xs = lds;                                          // quant dword L of block b at (2L + b%2)*xp + b/2
+    float* xd = reinterpret_cast<float*>(lds + 16 * xp);         // [nb] activation scales
     const int tid = threadIdx.x, lane = tid & 63, tok = blockIdx.y;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    uint8_t* slot = reinterpret_cast<uint8_t*>(lds + 8 * xp + nb) + wave * kVSlot;
-    float* sc = reinterpret_cast<float*>(slot + 8 * kVPitch);    // [8][kVScP] scale products
-    const int row0 = (blockIdx.x * NW + wave) * 8, nch = nb / kVChunk;
+    uint8_t* slot = reinterpret_cast<uint8_t*>(lds + 16 * xp + nb) + wave * kVSlot;
+    float* sc = reinterpret_cast<float*>(slot + kVRows * kVPitch);  // [row][parity][kVScP]
+    const int row0 = (blockIdx.x * NW + wave) * kVRows, nch = nb / kVChunk;
     const int64_t bpr = (int64_t)nb * kQ80Bytes;
     // rows past m_weight re-read row m_weight-1 (their cells are not written)
     const int row0c = min(row0, m_weight - 1);
@@ -500,8 +511,10 @@ __global__ __launch_bounds__(64 * NW) void k_q8_0_gemv_V(const uint8_t* __restri
     for (int a = 0; a < kVAhead; a++)
         if (a < nch) v_load(pf[a], wbase, off, a, lane);
 #pragma unroll
-    for (int u = 0; u < XR; u++)
-        if (tid + u * NT < nb * 8) xs[((tid + u * NT) & 7) * xp + ((tid + u * NT) >> 3)] = xq[u];
+    for (int u = 0; u < XR; u++) {
+        const int i = tid + u * NT, b = i >> 3;
+        if (i < nb * 8) xs[(2 * (i & 7) + (b & 1)) * xp + (b >> 1)] = xq[u];
+    }
 #pragma unroll
     for (int u = 0; u < XD; u++)
         if (tid + u * NT < nb) xd[tid + u * NT] = f16_ieee(xh[u]);
@@ -511,11 +524,12 @@ __global__ __launch_bounds__(64 * NW) void k_q8_0_gemv_V(const uint8_t* __restri
         v_step<0>(pf, slot, sc, wbase, off, dst, lane, c0, nch, xs, xd, xp, acc);
         v_step<1>(pf, slot, sc, wbase, off, dst, lane, c0, nch, xs, xd, xp, acc);
     }
+    // lanes 2L and 2L+1 hold the same acc_L: k_q8_0_gemv_T's combine over L
+    acc = acc + xor_f(acc, 8);
     acc = acc + xor_f(acc, 4);
     acc = acc + xor_f(acc, 2);
-    acc = acc + xor_f(acc, 1);
-    const int row = row0 + (lane >> 3);
-    if ((lane & 7) == 0 && row < m_weight) out[(int64_t)tok * m_weight + row] = acc;
+    const int row = row0 + (lane >> 4);
+    if ((lane & 15) == 0 && row < m_weight) out[(int64_t)tok * m_weight + row] = acc;
 }
 
 // Plain form of the same order for activation rows too long to stage in LDS.
@@ -573,26 +587,25 @@ static const void* v_kernel(int nb) {
     return nullptr;
 }
 
+static const void* v_kernel_nw(int nw, int nb) {
+    return nw == 8 ? v_kernel<8>(nb) : nw == 4 ? v_kernel<4>(nb) : v_kernel<2>(nb);
+}
+
 // The wide-load kernel where it is measured faster (MI355X, graph, weights
-// beyond the MALL), by 8-row waves w = ceil(m_weight/8) * m_tokens: from
-// w >= 512 (and from 256 when nb >= 256), 4 waves per workgroup from w >= 1024
-// and 2 below, so that there are >= 256 workgroups.  14336x4096 14.8 us (a
-// loader/chain kernel with a shared LDS ring and one barrier per chunk: 17.6;
-// k_q8_0_gemv_T<16,4>: 19.8), 4096x14336 19.1 (20.5; k_q8_0_gemv_TP: 24.1),
-// 4096x4096 7.9 (TP: 8.6), 14336x4096 x 4 tokens 36.1 (50.3); at 2048x4096 and
-// below the kernels of dispatch_T are faster.
-// Returns false when the shape or W's alignment does not fit.
+// beyond the MALL), by 4-row waves w = ceil(m_weight/4) * m_tokens: from
+// w >= 128, with 2 waves per workgroup, 4 from w >= 1024 and 8 from w >= 2048.
+// Against the dword kernels of dispatch_T: 14336x4096 14.7 us (19.8),
+// 4096x14336 15.8 (24.1), 4096x4096 6.6 (8.6), 2048x14336 13.6, 1024x4096 5.4
+// (6.3), 512x4096 5.0 (6.0).  Returns false when the shape or W's alignment
+// does not fit.
 static bool launch_wide(const uint8_t* Wq, const uint8_t* Xq, float* out, int m_weight, int m_tokens, int nb,
                         hipStream_t s) {
     if (nb % kVChunk != 0 || (reinterpret_cast<uintptr_t>(Wq) & 15) != 0) return false;
-    const int64_t waves = (int64_t)((m_weight + 7) / 8) * m_tokens;
-    if (!(waves >= 512 || (waves >= 256 && nb >= 256))) return false;
-    int nw = waves >= 1024 ? 4 : 2;
-    const void* f = nw == 4 ? v_kernel<4>(nb) : v_kernel<2>(nb);
-    if (f == nullptr && nw == 2) {
-        nw = 4;
-        f = v_kernel<4>(nb);
-    }
+    const int64_t waves = (int64_t)((m_weight + kVRows - 1) / kVRows) * m_tokens;
+    if (waves < 128) return false;
+    int nw = waves >= 2048 ? 8 : waves >= 1024 ? 4 : 2;
+    const void* f = v_kernel_nw(nw, nb);
+    for (; f == nullptr && nw < 8; nw *= 2) f = v_kernel_nw(nw * 2, nb);  // more threads for a long x row
     const size_t lds = v_lds_bytes(nb, nw);
     if (f == nullptr || lds > 160 * 1024) return false;
     // more than 64 KB of dynamic LDS is asked for once per process and kernel
@@ -600,15 +613,17 @@ static bool launch_wide(const uint8_t* Wq, const uint8_t* Xq, float* out, int m_
     static bool lds_ok = false;
     std::call_once(once, [] {
         lds_ok = true;
-        for (int n : {32, 64, 128, 256, 512, 1024})
-            for (const void* k : {v_kernel<2>(n), v_kernel<4>(n)})
-                if (k != nullptr && hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) !=
-                                        hipSuccess)
+        for (int n : {32, 64, 128, 256, 512, 1024, 2048})
+            for (int w : {2, 4, 8}) {
+                const void* k = v_kernel_nw(w, n);
+                if (k != nullptr &&
+                    hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
                     lds_ok = false;
+            }
         (void)hipGetLastError();
     });
     if (!lds_ok) return false;
-    const int rows = 8 * nw;
+    const int rows = kVRows * nw;
     void* args[] = {const_cast<uint8_t**>(&Wq), const_cast<uint8_t**>(&Xq), &out, &m_weight, &nb};
     (void)hipLaunchKernel(f, dim3((m_weight + rows - 1) / rows, m_tokens), dim3(64 * nw), args, lds, s);
     return true;

@@ -107,12 +107,16 @@ def test_dequant_in_bounds(nb):
 
 # ---------------------------------------------------------------- Q8_0 tile-order GEMV
 
-V_PITCH, V_SCP = 1248, 36
-V_SLOT = 8 * V_PITCH + 8 * V_SCP * 4
+V_PITCH, V_SCP, V_ROWS = 1248, 20, 4
+V_SLOT = V_ROWS * V_PITCH + 2 * V_ROWS * V_SCP * 4
+
+
+def v_xpitch(nb):
+    return nb // 2 + 4
 
 
 def v_lds(nb, nw):
-    return (8 * (nb + 4) + nb) * 4 + nw * V_SLOT
+    return (16 * v_xpitch(nb) + nb) * 4 + nw * V_SLOT
 
 
 def q8_wide_config(mw, mt, nb):
@@ -120,56 +124,64 @@ def q8_wide_config(mw, mt, nb):
     16-byte aligned W, or None."""
     if nb == 0 or nb % 32 != 0:
         return None
-    waves = (mw + 7) // 8 * mt
-    if not (waves >= 512 or (waves >= 256 and nb >= 256)):
+    waves = -(-mw // V_ROWS) * mt
+    if waves < 128:
         return None
     xr = lambda nw: next((x for x in (2, 4, 8, 16, 32) if nb * 8 <= x * 64 * nw), None)
-    nw = 4 if waves >= 1024 else 2
+    nw = 8 if waves >= 2048 else 4 if waves >= 1024 else 2
     XR = xr(nw)
-    if XR is None and nw == 2:
-        nw, XR = 4, xr(4)
+    while XR is None and nw < 8:
+        nw *= 2
+        XR = xr(nw)
     if XR is None or v_lds(nb, nw) > 160 * 1024:
         return None
     return nw, XR
 
 
 def check_wide_q8(mw, mt, nb, w_size, x_size, out_size):
-    """k_q8_0_gemv_V: lane l of wave w in workgroup g (rows row0 = 8(g*NW + w) ..)
-    reads 16-byte piece f = min(l + 64k, 543) (k < 9; k = 8 on lanes < 32 only)
+    """k_q8_0_gemv_V: lane l of wave w in workgroup g (rows row0 = 4(g*NW + w) ..)
+    reads 16-byte piece f = min(l + 64k, 271) (k < 5; k = 4 on lanes < 16 only)
     -- row f/68, bytes 1088c + 16(f%68) of that row (rows past mw re-read row
     mw-1) -- for chunks c < nb/32 and writes it at (f/68)*1248 + 16(f%68) of the
-    wave's slot; the scale pass reads the 16-bit scale at r*1248 + 34bb and
-    writes sc[r*36 + bb] (r < 8, bb < 32); chain lane (row, L) reads the row
-    chunk's bytes [34bb+2+4L, +4) (even bb: [34bb+4L, 34bb+4L+8)), four x dwords
-    at L*(nb+4) + 32c + 4i and four products at row*36 + 4i; the activation is
-    quant dword min(i, 8nb-1) and scale min(j, nb-1)."""
+    wave's slot; the scale pass reads the 16-bit scale at r*1248 + 34bb and writes
+    sc[(2r + bb%2)*20 + bb/2] (r < 4, bb < 32); lane (row, L, h) reads the dwords
+    at 34bb + oa and 34bb + oa + 4 of its row's chunk (bb even, oa = (34h + 2 +
+    4L) & ~3), four x dwords at (2L + h)*(nb/2 + 4) + 16c + b8/2 and four products
+    at (2row + h)*20 + b8/2; the activation is quant dword min(i, 8nb-1) and
+    scale min(j, nb-1)."""
     NW, XR = q8_wide_config(mw, mt, nb)
-    NT, bpr, nch, xp = 64 * NW, nb * Q80, nb // 32, nb + 4
+    NT, bpr, nch, xp = 64 * NW, nb * Q80, nb // 32, v_xpitch(nb)
     l = np.arange(64)
-    groups = -(-mw // (8 * NW))
+    groups = -(-mw // (V_ROWS * NW))
     for g in sorted({0, groups - 1}):
         for w in range(NW):
-            row0 = (g * NW + w) * 8
+            row0 = (g * NW + w) * V_ROWS
             row0c = min(row0, mw - 1)
-            for k in range(9):
-                f = np.minimum(l + 64 * k, 543)
-                if k == 8:
-                    f = f[l < 32]
+            for k in range(5):
+                f = np.minimum(l + 64 * k, 271)
+                if k == 4:
+                    f = f[l < 16]
                 r, pc = f // 68, f % 68
                 off = (np.minimum(row0 + r, mw - 1) - row0c) * bpr + 16 * pc
                 for c in (0, nch - 1):
                     a = row0c * bpr + off + c * 1088
                     assert a.min() >= 0 and (a + 16).max() <= w_size
-                assert (r * V_PITCH + 16 * pc + 16).max() <= 8 * V_PITCH
-    j = np.arange(256)
+                assert (r * V_PITCH + 16 * pc + 16).max() <= V_ROWS * V_PITCH
+    j = np.arange(128)
     r, bb = j // 32, j % 32
-    assert (r * V_PITCH + 34 * bb + 2).max() <= 8 * V_PITCH and (r * V_SCP + bb).max() < 8 * V_SCP
-    L = np.arange(8)
-    for bb in range(32):
-        o = 34 * bb + 2 + 4 * L
-        lo, hi = (o - 2, o + 6) if bb % 2 == 0 else (o, o + 4)
-        assert lo.min() >= 0 and hi.max() <= 1088 <= V_PITCH
-    assert 7 * xp + 32 * (nch - 1) + 28 + 4 <= 8 * xp and 7 * V_SCP + 28 + 4 <= 8 * V_SCP
+    assert (r * V_PITCH + 34 * bb + 2).max() <= V_ROWS * V_PITCH
+    assert ((2 * r + bb % 2) * V_SCP + bb // 2).max() < 2 * V_ROWS * V_SCP
+    h, L, rr = l & 1, (l >> 1) & 7, l >> 4
+    oa = (34 * h + 2 + 4 * L) & ~3
+    for bb in range(0, 32, 2):
+        a = rr * V_PITCH + 34 * bb + oa
+        assert a.min() >= 0 and (a + 8).max() <= rr.max() * V_PITCH + V_PITCH
+        assert (34 * bb + oa + 8).max() <= V_PITCH
+    for b8 in range(0, 32, 8):
+        xi = (2 * L + h) * xp + 16 * (nch - 1) + b8 // 2
+        assert (xi + 4).max() <= 16 * xp
+        si = (2 * rr + h) * V_SCP + b8 // 2
+        assert (si + 4).max() <= 2 * V_ROWS * V_SCP
     i = np.minimum(np.arange(XR * NT), nb * 8 - 1)
     jd = np.minimum(np.arange(-(-XR // 8) * NT), nb - 1)
     assert nb <= -(-XR // 8) * NT
@@ -178,10 +190,11 @@ def check_wide_q8(mw, mt, nb, w_size, x_size, out_size):
         assert tok * bpr + (jd * Q80 + 2).max() <= x_size
     st = np.arange(XR * NT)
     st = st[st < nb * 8]
-    assert ((st & 7) * xp + (st >> 3)).max() < 8 * xp
+    b = st >> 3
+    assert ((2 * (st & 7) + (b & 1)) * xp + (b >> 1)).max() < 16 * xp
     # 16-byte alignment of every vector LDS access: slots, x rows, product rows
-    assert ((8 * xp + nb) * 4) % 16 == 0 and V_SLOT % 16 == 0 and (8 * V_PITCH) % 16 == 0
-    assert (xp * 4) % 16 == 0 and (V_SCP * 4) % 16 == 0
+    assert ((16 * xp + nb) * 4) % 16 == 0 and V_SLOT % 16 == 0 and (V_ROWS * V_PITCH) % 16 == 0
+    assert (xp * 4) % 16 == 0 and (V_SCP * 4) % 16 == 0 and (16 * (nch - 1) * 4) % 16 == 0
     assert (mt - 1) * mw * 4 + mw * 4 <= out_size
     assert v_lds(nb, NW) <= 160 * 1024
 
