@@ -112,8 +112,9 @@ __device__ __forceinline__ void q8_0_lane_store(float v, uint8_t* __restrict__ y
 // 2-byte aligned: the quants go out as two 16-bit stores per lane.
 __device__ __forceinline__ void q8_0_quad_store(float4 v, uint8_t* __restrict__ yb, int g) {
     float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-#pragma unroll
-    for (int mask = 1; mask < 8; mask <<= 1) amax = fmaxf(amax, xor_f(amax, mask));
+    amax = fmaxf(amax, dpp_f<0xB1>(amax));   // quad_perm [1,0,3,2]
+    amax = fmaxf(amax, dpp_f<0x4E>(amax));   // quad_perm [2,3,0,1]
+    amax = fmaxf(amax, dpp_f<0x141>(amax));  // row_half_mirror: the other quad of the 8
     const float d = amax / 127.0f;
     const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
     const uint32_t q0 = (uint32_t)(int)__builtin_rintf(v.x * id) & 0xFFu;
@@ -132,8 +133,11 @@ __device__ __forceinline__ void q8_0_quad_store(float4 v, uint8_t* __restrict__ 
 // 16 consecutive q.  yb is 4-byte aligned.
 __device__ __forceinline__ void q8k_wave_store(float4 v, uint8_t* __restrict__ yb, int lane) {
     float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-#pragma unroll
-    for (int mask = 1; mask < 64; mask <<= 1) amax = fmaxf(amax, xor_f(amax, mask));
+    amax = fmaxf(amax, dpp_f<0xB1>(amax));   // quad_perm [1,0,3,2]
+    amax = fmaxf(amax, dpp_f<0x4E>(amax));   // quad_perm [2,3,0,1]
+    amax = fmaxf(amax, dpp_f<0x141>(amax));  // row_half_mirror
+    amax = fmaxf(amax, dpp_f<0x140>(amax));  // row_mirror: every lane holds its 16-lane row's max
+    amax = fmaxf(fmaxf(readlane_f(amax, 0), readlane_f(amax, 16)), fmaxf(readlane_f(amax, 32), readlane_f(amax, 48)));
     const float d = amax / 127.0f;
     const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
     const int q0 = (int)__builtin_rintf(v.x * id), q1 = (int)__builtin_rintf(v.y * id);
