@@ -407,11 +407,15 @@ __device__ __forceinline__ void v_lds_order() { asm volatile("s_waitcnt lgkmcnt(
 
 __device__ __forceinline__ bool v_piece(int lane, int k) { return k < kVPer - 1 || lane + 64 * k < kVWavePieces; }
 
+// Non-temporal: each weight byte is read once, and every 16-byte piece of a
+// 128-byte line is loaded by the same instruction (cfg2 14336x4096 14.4 ->
+// 13.2 us, 4096x14336 15.4 -> 14.8 us against plain loads).
 __device__ __forceinline__ void v_load(v_u32x4 (&v)[kVPer], const uint8_t* __restrict__ wbase,
                                        const uint32_t (&off)[kVPer], int c, int lane) {
 #pragma unroll
     for (int k = 0; k < kVPer; k++)
-        if (v_piece(lane, k)) v[k] = *reinterpret_cast<const v_u32x4*>(wbase + off[k] + (uint32_t)c * kVRowB);
+        if (v_piece(lane, k))
+            v[k] = __builtin_nontemporal_load(reinterpret_cast<const v_u32x4*>(wbase + off[k] + (uint32_t)c * kVRowB));
 }
 
 // v read from lane (lane & ~3) + SEL and lane (lane & ~3) + 2 + SEL of each quad
