@@ -493,6 +493,111 @@ __global__ __launch_bounds__(64 * WPB) void k_q4k_q8k_gemv(const uint8_t* __rest
     rows<KIND, ORDER, R, G>(w, xq, y, M, nb, row0, unused);
 }
 
+// ----------------------------------------------------------------------------
+// Q4_K x Q8_K GEMV for K = 256*NB (NB a multiple of 16) and 16-byte aligned
+// weights, with each wave's R rows read as one contiguous span: R*NB*9 aligned
+// 16-byte pieces (288 for two rows at K = 4096), lane l loading pieces l,
+// l+64, ..., so that every load instruction covers whole 128-byte lines; the
+// loads are non-temporal (every byte is read once).  The wave writes the span
+// to its own LDS slot and reads it back in gemv4_rows's mapping: lane (bl, c4)
+// takes qs chunks c4 and c4+4 and the 16-byte header of super-block 16t+bl, so
+// a pass covers 16 super-blocks of a row and the header, the scale decode and
+// the fp32 combine are shared by 4 lanes.  Passes run in span order (row 0's,
+// then row 1's), each as soon as the loads covering it are in.  Operands,
+// integer sums and fp32 order are gemv4_rows's, and so gemv_rows's: the bits
+// are the same.
+// Measured at 14336x4096 (graph of back-to-back launches over weights beyond
+// the MALL): 6.73 us against 7.36 for gemv_rows with per-lane chunk loads; the
+// same span in gemv_rows's 8-lane mapping 6.98; R = 1, 3, 4 rows or 2 and 8
+// waves per workgroup were slower.
+// ----------------------------------------------------------------------------
+template <int NB, int R>
+struct SpanShape {
+    static constexpr int kRows = R;
+    static constexpr int kPieces = kRows * NB * 9;
+    static constexpr int kLoads = (kPieces + 63) / 64;
+    static constexpr int kSlot = kLoads * 64 * 16;     // LDS bytes per wave (whole loads)
+};
+
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+
+// The wave's LDS writes are complete before its later LDS reads are issued (and
+// the compiler keeps the accesses in that order).
+__device__ __forceinline__ void lds_wave_order() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+template <int ORDER, int NB, int R, int WPB>
+__global__ __launch_bounds__(64 * WPB) void k_q4k_q8k_gemv_span(const uint8_t* __restrict__ w,
+                                                                 const uint8_t* __restrict__ xq,
+                                                                 float* __restrict__ y, int M) {
+    using S = SpanShape<NB, R>;
+    static_assert(NB % 16 == 0, "whole 16-block passes");
+    constexpr int NT = NB / 16;
+    __shared__ __align__(16) uint8_t slots[WPB][S::kSlot];
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int lane = threadIdx.x & 63, bl = lane >> 2, c4 = lane & 3;
+    const int row0 = (blockIdx.x * WPB + wave) * R;
+    if (row0 >= M) return;
+    // pieces inside the tensor: rows past M repeat the last piece of the last row
+    // (their results are not stored)
+    const int np = min(R, M - row0) * NB * 9;
+    XOps x0[NT], x1[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        x0[t] = load_x<ORDER>(xq + (int64_t)(16 * t + bl) * kQ8KBytes, c4);
+        x1[t] = load_x<ORDER>(xq + (int64_t)(16 * t + bl) * kQ8KBytes, c4 + 4);
+    }
+    const uint8_t* span = w + (int64_t)row0 * (NB * kQ4KBytes);
+    u32x4v v[S::kLoads];
+#pragma unroll
+    for (int u = 0; u < S::kLoads; u++) {
+        const int p = min(lane + 64 * u, np - 1);
+        v[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4v*>(span + 16 * p));
+    }
+    uint8_t* slot = slots[wave];
+    float s[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) s[r] = 0.0f;
+    int written = 0;  // loads already in the slot (compile-time after unrolling)
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            const int last = (r * NB + 16 * t + 16) * 9 - 1;
+#pragma unroll
+            for (int u = 0; u < S::kLoads; u++) {
+                // lanes past the span write their (repeated) piece to the slot's tail
+                if (u >= written && 64 * u <= last)
+                    *reinterpret_cast<u32x4v*>(slot + 16 * (lane + 64 * u)) = v[u];
+            }
+#pragma unroll
+            for (int u = 0; u < S::kLoads; u++)
+                if (u >= written && 64 * u <= last) written = u + 1;
+            lds_wave_order();
+            const uint8_t* blk = slot + (r * NB + 16 * t + bl) * kQ4KBytes;
+            const uint4 hdr = *reinterpret_cast<const uint4*>(blk);
+            const uint4 qa = *reinterpret_cast<const uint4*>(blk + 16 + 16 * c4);
+            const uint4 qb = *reinterpret_cast<const uint4*>(blk + 80 + 16 * c4);
+            const uint32_t qd0[4] = {qa.x, qa.y, qa.z, qa.w};
+            const uint32_t qd1[4] = {qb.x, qb.y, qb.z, qb.w};
+            const float c = block4_contrib<ORDER>(hdr, qd0, qd1, x0[t], x1[t], c4);
+            uint32_t c_lo = __float_as_uint(c), c_hi = c_lo;
+            swap32(c_lo, c_hi);  // lanes 0-31: c_hi = contribution of block b+8
+            // NB % 16 == 0: every block 16t+bl is in the row, and so is 16t+bl+8 for lanes 0-31
+            // (the lanes that hold the slot sums)
+            s[r] = (s[r] + c) + __uint_as_float(c_hi);
+        }
+    }
+    // gemv4_rows's combine
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        float t = s[r];
+        t = t + dpp_f<0x141>(t);
+        t = t + dpp_f<0x140>(t);
+        const float lo = readlane_f(t, 0), hi = readlane_f(t, 16);
+        if (lane == 0 && row0 + r < M) y[row0 + r] = lo + hi;
+    }
+}
+
 // Up to kMulti matrices that share one activation vector (Q/K/V, gate/up) in
 // one launch: waves are numbered across the matrices, matrix i owning waves
 // [first[i], first[i+1]).  Each row is computed exactly as the single-matrix
@@ -548,7 +653,15 @@ static void launch_gemv(const uint8_t* w, const uint8_t* xq, float* y, int M, in
 
 template <int ORDER>
 static void launch_gemv_order(const uint8_t* w, const uint8_t* xq, float* y, int M, int nb, hipStream_t s) {
-    switch (choose_shape(M, nb)) {
+    const GemvShape sh = choose_shape(M, nb);
+    if (sh == kWide && nb == 16 && (reinterpret_cast<uintptr_t>(w) & 15) == 0) {
+        constexpr int R = 2, WPB = 4;
+        const int waves = (M + R - 1) / R;
+        hipLaunchKernelGGL((k_q4k_q8k_gemv_span<ORDER, 16, R, WPB>), dim3((waves + WPB - 1) / WPB), dim3(64 * WPB), 0,
+                           s, w, xq, y, M);
+        return;
+    }
+    switch (sh) {
         case kWide: launch_gemv<0, ORDER, 2, 2, 4>(w, xq, y, M, nb, s); break;
         case k4Row1: launch_gemv<1, ORDER, 1, 1, 8>(w, xq, y, M, nb, s); break;
         case k4Row2: launch_gemv<1, ORDER, 2, 1, 4>(w, xq, y, M, nb, s); break;

@@ -105,7 +105,7 @@ def test_quant_q8_k_edge_values(dev):
 
 @pytest.mark.parametrize("order", [formats.ORDER_BPD, formats.ORDER_GGUF])
 @pytest.mark.parametrize("M,K", [(4096, 4096), (14336, 4096), (4096, 14336), (1024, 4096),
-                                 (1, 256), (5, 512), (13, 2304), (9, 2048 + 256)])
+                                 (1, 256), (5, 512), (13, 2304), (9, 2048 + 256), (8193, 4096)])
 def test_qmatmul_q4k_q8k(dev, order, M, K):
     import torch
 

@@ -19,10 +19,13 @@ def lanes():
 # ---------------------------------------------------------------- Q4_K x Q8_K GEMV
 
 def q4k_gemv_shape(rows, nb):
-    """(kind, R, G, WPB) as chosen by choose_shape() in q4k.hip."""
+    """(kind, R, G, WPB) as launch_gemv_order() in q4k.hip picks it for 16-byte
+    aligned weights (kind 2: k_q4k_q8k_gemv_span)."""
     if nb > 16:
         return (1, 2, 1, 4)
-    return (1, 1, 1, 8) if rows <= 8192 else (0, 2, 2, 4)
+    if rows <= 8192:
+        return (1, 1, 1, 8)
+    return (2, 2, 2, 4) if nb == 16 else (0, 2, 2, 4)
 
 
 def x_accesses(c):
@@ -45,6 +48,35 @@ def check_wide(M, nb, row0, R, G):
                 assert (base + 4 * (c & 3) + 4).max() <= w_size
             for off, size in x_accesses(c):
                 assert np.max(bb * Q8K + off + size) <= x_size and np.min(bb * Q8K + off) >= 0
+
+
+def check_span(M, nb, row0):
+    """k_q4k_q8k_gemv_span<ORDER, NB=nb, R=2, WPB>: the wave's two rows as 16-byte
+    pieces (clamped to the tensor), its LDS slot of whole loads, the 4-lane
+    mapping's LDS reads and gemv4_rows's x reads."""
+    assert nb % 16 == 0
+    w_size, x_size = M * nb * Q4K, nb * Q8K
+    pieces = 2 * nb * 9
+    loads = (pieces + 63) // 64
+    slot = loads * 64 * 16
+    np_ = min(2, M - row0) * nb * 9
+    l = lanes()
+    bl, c4 = l >> 2, l & 3
+    span = row0 * nb * Q4K
+    for u in range(loads):
+        p = np.minimum(l + 64 * u, np_ - 1)
+        assert (span + 16 * p).min() >= 0 and (span + 16 * p + 16).max() <= w_size
+        assert (16 * (l + 64 * u) + 16).max() <= slot
+    for r in range(2):
+        for t in range(nb // 16):
+            blk = (r * nb + 16 * t + bl) * Q4K
+            assert (blk + 16).max() <= slot
+            assert (blk + 16 + 16 * c4 + 16).max() <= slot and (blk + 80 + 16 * c4 + 16).max() <= slot
+    for t in range(nb // 16):
+        b = 16 * t + bl
+        for c in (c4, c4 + 4):
+            for off, size in x_accesses(c):
+                assert np.max(b * Q8K + off + size) <= x_size and np.min(b * Q8K + off) >= 0
 
 
 def check_four(M, nb, row0, R):
@@ -71,11 +103,13 @@ def check_four(M, nb, row0, R):
 @pytest.mark.parametrize("M,K", [(4096, 4096), (14336, 4096), (4096, 14336), (1024, 4096), (1, 256), (5, 512),
                                  (13, 2304), (9, 2304), (3, 0), (64, 1024), (77, 512), (6144, 4096), (28672, 4096),
                                  (8193, 4096), (17, 4352), (2, 14336)])
-@pytest.mark.parametrize("force", [None, (0, 2, 2, 4), (1, 1, 1, 8), (1, 2, 1, 4), (1, 1, 1, 16)])
+@pytest.mark.parametrize("force", [None, (0, 2, 2, 4), (1, 1, 1, 8), (1, 2, 1, 4), (1, 1, 1, 16), (2, 2, 2, 4)])
 def test_q4k_q8k_gemv_in_bounds(M, K, force):
     nb = K // 256
     if nb == 0:
         return  # no block-group pass runs: the kernels read nothing and write y = +0.0
+    if force is not None and force[0] == 2 and nb != 16:
+        return  # the span kernel is instantiated for K = 4096 only
     kind, R, G, WPB = force or q4k_gemv_shape(M, nb)
     waves = (M + R - 1) // R
     grid = (waves + WPB - 1) // WPB
@@ -84,7 +118,12 @@ def test_q4k_q8k_gemv_in_bounds(M, K, force):
             row0 = (blk * WPB + wave) * R
             if row0 >= M:
                 continue
-            (check_wide(M, nb, row0, R, G) if kind == 0 else check_four(M, nb, row0, R))
+            if kind == 0:
+                check_wide(M, nb, row0, R, G)
+            elif kind == 1:
+                check_four(M, nb, row0, R)
+            else:
+                check_span(M, nb, row0)
             for r in range(R):
                 if row0 + r < M:
                     assert (row0 + r) * 4 + 4 <= M * 4
