@@ -494,29 +494,40 @@ __global__ __launch_bounds__(64 * WPB) void k_q4k_q8k_gemv(const uint8_t* __rest
 }
 
 // ----------------------------------------------------------------------------
-// Q4_K x Q8_K GEMV for K = 256*NB (NB a multiple of 16) and 16-byte aligned
-// weights, with each wave's R rows read as one contiguous span: R*NB*9 aligned
-// 16-byte pieces (288 for two rows at K = 4096), lane l loading pieces l,
-// l+64, ..., so that every load instruction covers whole 128-byte lines; the
-// loads are non-temporal (every byte is read once).  The wave writes the span
-// to its own LDS slot and reads it back in gemv4_rows's mapping: lane (bl, c4)
-// takes qs chunks c4 and c4+4 and the 16-byte header of super-block 16t+bl, so
-// a pass covers 16 super-blocks of a row and the header, the scale decode and
-// the fp32 combine are shared by 4 lanes.  Passes run in span order (row 0's,
-// then row 1's), each as soon as the loads covering it are in.  Operands,
-// integer sums and fp32 order are gemv4_rows's, and so gemv_rows's: the bits
-// are the same.
+// Span GEMV: gemv4_rows's arithmetic with the weights read as contiguous spans.
+// A wave owns R rows of K = 256*NB.  Its weight bytes are read as aligned
+// 16-byte pieces of one span (JOINT: R consecutive rows of one matrix,
+// R*NB*9 pieces) or of R spans (one row each, rows of different matrices),
+// lane l loading pieces l, l+64, ..., so that every load instruction covers
+// whole 128-byte lines; the loads are non-temporal (every byte is read once)
+// and all of them are issued before any compute.  The wave writes the pieces
+// to its own LDS slot and reads them back in gemv4_rows's mapping: lane
+// (bl, c4) takes qs chunks c4 and c4+4 and the 16-byte header of super-block
+// 16t+bl, so a pass covers 16 super-blocks of a row and the header, the scale
+// decode and the fp32 combine are shared by 4 lanes.  Passes run row by row,
+// each as soon as the loads holding it are in.  Operands, integer sums, the
+// valid-block rule and the fp32 order are gemv4_rows's (and so gemv_rows's):
+// the bits are the same.  Weights must be 16-byte aligned (rows are then too:
+// 144*NB is a multiple of 16 for even NB).
 // Measured at 14336x4096 (graph of back-to-back launches over weights beyond
 // the MALL): 6.73 us against 7.36 for gemv_rows with per-lane chunk loads; the
-// same span in gemv_rows's 8-lane mapping 6.98; R = 1, 3, 4 rows or 2 and 8
-// waves per workgroup were slower.
+// same span in gemv_rows's 8-lane mapping 6.98.
 // ----------------------------------------------------------------------------
-template <int NB, int R>
-struct SpanShape {
-    static constexpr int kRows = R;
-    static constexpr int kPieces = kRows * NB * 9;
-    static constexpr int kLoads = (kPieces + 63) / 64;
-    static constexpr int kSlot = kLoads * 64 * 16;     // LDS bytes per wave (whole loads)
+template <int NB, int R, bool JOINT>
+struct Span {
+    static constexpr int kSegs = JOINT ? 1 : R;
+    static constexpr int kSegPieces = (JOINT ? R : 1) * NB * 9;
+    static constexpr int kSegLoads = (kSegPieces + 63) / 64;
+    static constexpr int kLoads = kSegs * kSegLoads;
+    static constexpr int kSlot = kLoads * 1024;  // LDS bytes per wave (whole loads)
+    static constexpr int kNT = (NB + 15) / 16;   // passes per row
+    // loads, in issue order, that hold every piece of pass t of row r
+    static constexpr int covering(int r, int t) {
+        const int end = 16 * t + 16 < NB ? 16 * t + 16 : NB;
+        return JOINT ? ((r * NB + end) * 9 + 63) / 64 : r * kSegLoads + (end * 9 + 63) / 64;
+    }
+    // LDS offset of row r's first super-block
+    static constexpr int row_offset(int r) { return JOINT ? r * NB * kQ4KBytes : r * kSegLoads * 1024; }
 };
 
 typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
@@ -525,35 +536,43 @@ typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
 // the compiler keeps the accesses in that order).
 __device__ __forceinline__ void lds_wave_order() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
-template <int ORDER, int NB, int R, int WPB>
-__global__ __launch_bounds__(64 * WPB) void k_q4k_q8k_gemv_span(const uint8_t* __restrict__ w,
-                                                                 const uint8_t* __restrict__ xq,
-                                                                 float* __restrict__ y, int M) {
-    using S = SpanShape<NB, R>;
-    static_assert(NB % 16 == 0, "whole 16-block passes");
-    constexpr int NT = NB / 16;
-    __shared__ __align__(16) uint8_t slots[WPB][S::kSlot];
-    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+// Every load of the wave's span(s): segment g starts at seg[g] and has np[g] >= 1
+// pieces inside the tensor; lanes past them repeat its last piece.
+template <class S>
+__device__ __forceinline__ void span_issue(u32x4v (&v)[S::kLoads], const uint8_t* const (&seg)[S::kSegs],
+                                           const int (&np)[S::kSegs]) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int g = 0; g < S::kSegs; g++)
+#pragma unroll
+        for (int u = 0; u < S::kSegLoads; u++) {
+            const uint32_t p = (uint32_t)min(lane + 64 * u, np[g] - 1);
+            v[g * S::kSegLoads + u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4v*>(seg[g] + 16u * p));
+        }
+}
+
+// x operands of every pass from the Q8_K vector in global memory (issue these
+// before the span loads: the first pass then waits for no weight bytes it does
+// not use).
+template <int ORDER, int NB>
+__device__ __forceinline__ void span_load_x(XOps (&xr)[(NB + 15) / 16][2], const uint8_t* __restrict__ xq) {
     const int lane = threadIdx.x & 63, bl = lane >> 2, c4 = lane & 3;
-    const int row0 = (blockIdx.x * WPB + wave) * R;
-    if (row0 >= M) return;
-    // pieces inside the tensor: rows past M repeat the last piece of the last row
-    // (their results are not stored)
-    const int np = min(R, M - row0) * NB * 9;
-    XOps x0[NT], x1[NT];
 #pragma unroll
-    for (int t = 0; t < NT; t++) {
-        x0[t] = load_x<ORDER>(xq + (int64_t)(16 * t + bl) * kQ8KBytes, c4);
-        x1[t] = load_x<ORDER>(xq + (int64_t)(16 * t + bl) * kQ8KBytes, c4 + 4);
+    for (int t = 0; t < (NB + 15) / 16; t++) {
+        const uint8_t* xb = xq + (int64_t)min(16 * t + bl, NB - 1) * kQ8KBytes;
+        xr[t][0] = load_x<ORDER>(xb, c4);
+        xr[t][1] = load_x<ORDER>(xb, c4 + 4);
     }
-    const uint8_t* span = w + (int64_t)row0 * (NB * kQ4KBytes);
-    u32x4v v[S::kLoads];
-#pragma unroll
-    for (int u = 0; u < S::kLoads; u++) {
-        const int p = min(lane + 64 * u, np - 1);
-        v[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4v*>(span + 16 * p));
-    }
-    uint8_t* slot = slots[wave];
+}
+
+// The R row results (wave-uniform) from the staged loads; x from xr (LX false)
+// or from the workgroup's LDS copy xl (LX true).
+template <int ORDER, int NB, int R, bool JOINT, bool LX>
+__device__ __forceinline__ void span_rows(const u32x4v (&v)[Span<NB, R, JOINT>::kLoads], uint8_t* __restrict__ slot,
+                                          const uint8_t* __restrict__ xl, const XOps (&xr)[(NB + 15) / 16][2],
+                                          float (&out)[R]) {
+    using S = Span<NB, R, JOINT>;
+    const int lane = threadIdx.x & 63, bl = lane >> 2, c4 = lane & 3;
     float s[R];
 #pragma unroll
     for (int r = 0; r < R; r++) s[r] = 0.0f;
@@ -561,41 +580,67 @@ __global__ __launch_bounds__(64 * WPB) void k_q4k_q8k_gemv_span(const uint8_t* _
 #pragma unroll
     for (int r = 0; r < R; r++) {
 #pragma unroll
-        for (int t = 0; t < NT; t++) {
-            const int last = (r * NB + 16 * t + 16) * 9 - 1;
-#pragma unroll
-            for (int u = 0; u < S::kLoads; u++) {
-                // lanes past the span write their (repeated) piece to the slot's tail
-                if (u >= written && 64 * u <= last)
-                    *reinterpret_cast<u32x4v*>(slot + 16 * (lane + 64 * u)) = v[u];
-            }
+        for (int t = 0; t < S::kNT; t++) {
+            const int need = S::covering(r, t);
 #pragma unroll
             for (int u = 0; u < S::kLoads; u++)
-                if (u >= written && 64 * u <= last) written = u + 1;
+                if (u >= written && u < need) *reinterpret_cast<u32x4v*>(slot + 16 * (lane + 64 * u)) = v[u];
+            written = need > written ? need : written;
             lds_wave_order();
-            const uint8_t* blk = slot + (r * NB + 16 * t + bl) * kQ4KBytes;
+            const int b = 16 * t + bl, bb = min(b, NB - 1);
+            const uint8_t* blk = slot + S::row_offset(r) + bb * kQ4KBytes;
             const uint4 hdr = *reinterpret_cast<const uint4*>(blk);
             const uint4 qa = *reinterpret_cast<const uint4*>(blk + 16 + 16 * c4);
             const uint4 qb = *reinterpret_cast<const uint4*>(blk + 80 + 16 * c4);
             const uint32_t qd0[4] = {qa.x, qa.y, qa.z, qa.w};
             const uint32_t qd1[4] = {qb.x, qb.y, qb.z, qb.w};
-            const float c = block4_contrib<ORDER>(hdr, qd0, qd1, x0[t], x1[t], c4);
+            float c;
+            if constexpr (LX)
+                c = block4_contrib<ORDER>(hdr, qd0, qd1, get_x<ORDER, true>(xl, bb, c4),
+                                          get_x<ORDER, true>(xl, bb, c4 + 4), c4);
+            else
+                c = block4_contrib<ORDER>(hdr, qd0, qd1, xr[t][0], xr[t][1], c4);
             uint32_t c_lo = __float_as_uint(c), c_hi = c_lo;
             swap32(c_lo, c_hi);  // lanes 0-31: c_hi = contribution of block b+8
-            // NB % 16 == 0: every block 16t+bl is in the row, and so is 16t+bl+8 for lanes 0-31
-            // (the lanes that hold the slot sums)
-            s[r] = (s[r] + c) + __uint_as_float(c_hi);
+            float acc = s[r];
+            if (b < NB) acc = acc + c;
+            if (b + 8 < NB) acc = acc + __uint_as_float(c_hi);
+            s[r] = acc;
         }
     }
-    // gemv4_rows's combine
+    // slot q lives in lanes 4q..4q+3 (q < 8): row_half_mirror pairs slots q and
+    // q^1, row_mirror the pairs, and lanes 0 and 16 hold the two halves
 #pragma unroll
     for (int r = 0; r < R; r++) {
         float t = s[r];
         t = t + dpp_f<0x141>(t);
         t = t + dpp_f<0x140>(t);
-        const float lo = readlane_f(t, 0), hi = readlane_f(t, 16);
-        if (lane == 0 && row0 + r < M) y[row0 + r] = lo + hi;
+        out[r] = readlane_f(t, 0) + readlane_f(t, 16);
     }
+}
+
+// Single matrix, R consecutive rows per wave, x as Q8_K in global memory.
+template <int ORDER, int NB, int R, int WPB>
+__global__ __launch_bounds__(64 * WPB) void k_q4k_q8k_gemv_span(const uint8_t* __restrict__ w,
+                                                                const uint8_t* __restrict__ xq,
+                                                                float* __restrict__ y, int M) {
+    using S = Span<NB, R, true>;
+    __shared__ __align__(16) uint8_t slots[WPB][S::kSlot];
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int row0 = (blockIdx.x * WPB + wave) * R;
+    if (row0 >= M) return;
+    XOps xr[S::kNT][2];
+    span_load_x<ORDER, NB>(xr, xq);
+    // rows past M repeat the last piece of row M-1 (their results are not stored)
+    const uint8_t* seg[1] = {w + (int64_t)row0 * (NB * kQ4KBytes)};
+    const int np[1] = {min(R, M - row0) * NB * 9};
+    u32x4v v[S::kLoads];
+    span_issue<S>(v, seg, np);
+    float out[R];
+    span_rows<ORDER, NB, R, true, false>(v, slots[wave], nullptr, xr, out);
+#pragma unroll
+    for (int r = 0; r < R; r++)
+        if ((threadIdx.x & 63) == 0 && row0 + r < M) y[row0 + r] = out[r];
 }
 
 // Up to kMulti matrices that share one activation vector (Q/K/V, gate/up) in
@@ -651,17 +696,27 @@ static void launch_gemv(const uint8_t* w, const uint8_t* xq, float* y, int M, in
                        s, w, xq, y, M, nb);
 }
 
+// Span kernels where they apply (K = 4096, 16-byte aligned weights): two rows
+// per wave, one up to 2048 rows (measured: 4096x4096 3.54 us against 3.85 for
+// k4Row1, 1024x4096 2.40 against 2.86), 4 waves per workgroup.
+static bool span16(int nb, const void* w) { return nb == 16 && (reinterpret_cast<uintptr_t>(w) & 15) == 0; }
+static int span_rows_per_wave(int rows) { return rows <= 2048 ? 1 : 2; }
+
+template <int ORDER, int R>
+static void launch_span(const uint8_t* w, const uint8_t* xq, float* y, int M, hipStream_t s) {
+    constexpr int WPB = 4;
+    const int waves = (M + R - 1) / R;
+    hipLaunchKernelGGL((k_q4k_q8k_gemv_span<ORDER, 16, R, WPB>), dim3((waves + WPB - 1) / WPB), dim3(64 * WPB), 0, s,
+                       w, xq, y, M);
+}
+
 template <int ORDER>
 static void launch_gemv_order(const uint8_t* w, const uint8_t* xq, float* y, int M, int nb, hipStream_t s) {
-    const GemvShape sh = choose_shape(M, nb);
-    if (sh == kWide && nb == 16 && (reinterpret_cast<uintptr_t>(w) & 15) == 0) {
-        constexpr int R = 2, WPB = 4;
-        const int waves = (M + R - 1) / R;
-        hipLaunchKernelGGL((k_q4k_q8k_gemv_span<ORDER, 16, R, WPB>), dim3((waves + WPB - 1) / WPB), dim3(64 * WPB), 0,
-                           s, w, xq, y, M);
+    if (span16(nb, w)) {
+        if (span_rows_per_wave(M) == 1) launch_span<ORDER, 1>(w, xq, y, M, s); else launch_span<ORDER, 2>(w, xq, y, M, s);
         return;
     }
-    switch (sh) {
+    switch (choose_shape(M, nb)) {
         case kWide: launch_gemv<0, ORDER, 2, 2, 4>(w, xq, y, M, nb, s); break;
         case k4Row1: launch_gemv<1, ORDER, 1, 1, 8>(w, xq, y, M, nb, s); break;
         case k4Row2: launch_gemv<1, ORDER, 2, 1, 4>(w, xq, y, M, nb, s); break;
@@ -718,18 +773,6 @@ static MultiArgs make_multi_args(const uint8_t* const* w, float* const* y, const
     }
     a.first[kMulti] = waves;
     return a;
-}
-
-void launch_qmatmul_q4k_q8k_multi(const uint8_t* const* w, float* const* y, const int* M, int n, const uint8_t* xq,
-                                  int K, int order, hipStream_t s) {
-    const int nb = K / 256;
-    const GemvShape sh = choose_shape(total_rows(M, n), nb);
-    const MultiArgs a = make_multi_args(w, y, M, n, shape_rows_per_wave(sh));
-    if (a.first[kMulti] == 0) return;
-    if (order == 0)
-        launch_multi_order<0>(a, sh, xq, nb, s);
-    else
-        launch_multi_order<1>(a, sh, xq, nb, s);
 }
 
 // ----------------------------------------------------------------------------
@@ -887,11 +930,139 @@ static void launch_swiglu(const uint8_t* wg, const uint8_t* wu, float* y, int M,
                        (size_t)nb * kXS, s, wg, wu, y, M, x, nullptr, nb);
 }
 
+// ----------------------------------------------------------------------------
+// Span forms (see span_rows) of the multi-matrix, fused-quantization and
+// Q8_K gate/up SwiGLU launches, for K = 4096 and 16-byte aligned weights.
+// Waves, rows and outputs are numbered as in the kernels above, and so are the
+// bits.
+// ----------------------------------------------------------------------------
+template <int ORDER, int NB, int R, int WPB>
+__global__ __launch_bounds__(64 * WPB) void k_q4k_q8k_multi_span(MultiArgs a, const uint8_t* __restrict__ xq) {
+    using S = Span<NB, R, true>;
+    __shared__ __align__(16) uint8_t slots[WPB][S::kSlot];
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    int i, row0;
+    if (!wave_rows(a, blockIdx.x * WPB + wave, R, i, row0)) return;
+    XOps xr[S::kNT][2];
+    span_load_x<ORDER, NB>(xr, xq);
+    const uint8_t* seg[1] = {a.w[i] + (int64_t)row0 * (NB * kQ4KBytes)};
+    const int np[1] = {min(R, a.M[i] - row0) * NB * 9};
+    u32x4v v[S::kLoads];
+    span_issue<S>(v, seg, np);
+    float out[R];
+    span_rows<ORDER, NB, R, true, false>(v, slots[wave], nullptr, xr, out);
+#pragma unroll
+    for (int r = 0; r < R; r++)
+        if ((threadIdx.x & 63) == 0 && row0 + r < a.M[i]) a.y[i][row0 + r] = out[r];
+}
+
+// Fused quantization: the workgroup quantizes x into LDS (x32_load /
+// x32_quantize, issued before and run after the span loads), then every wave
+// runs its rows with x from LDS.
+template <int ORDER, int NB, int R, int WPB>
+__global__ __launch_bounds__(64 * WPB) void k_q4k_fused_span(MultiArgs a, const float* __restrict__ x) {
+    using S = Span<NB, R, true>;
+    constexpr int IT = (NB + 4 * WPB - 1) / (4 * WPB);
+    __shared__ __align__(16) uint8_t slots[WPB][S::kSlot];
+    __shared__ __align__(16) uint8_t xl[NB * kXS];
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    int i, row0;
+    const bool has = wave_rows(a, blockIdx.x * WPB + wave, R, i, row0);
+    XPre<IT> P;
+    x32_load<WPB, IT>(P, x, NB);
+    const uint8_t* seg[1] = {a.w[i] + (int64_t)row0 * (NB * kQ4KBytes)};
+    const int np[1] = {min(R, a.M[i] - row0) * NB * 9};
+    u32x4v v[S::kLoads];
+    span_issue<S>(v, seg, np);
+    __builtin_amdgcn_sched_barrier(0);
+    x32_quantize<WPB, IT>(P, xl, NB);
+    __syncthreads();
+    if (!has) return;
+    XOps unused[S::kNT][2];
+    float out[R];
+    span_rows<ORDER, NB, R, true, true>(v, slots[wave], xl, unused, out);
+#pragma unroll
+    for (int r = 0; r < R; r++)
+        if ((threadIdx.x & 63) == 0 && row0 + r < a.M[i]) a.y[i][row0 + r] = out[r];
+}
+
+// Gate row r and up row r per wave (two spans) from the Q8_K activation xq,
+// y[r] = silu(gate_r) * up_r (k_q4k_fused_swiglu<..., QX = true>'s bits).
+template <int ORDER, int NB, int WPB>
+__global__ __launch_bounds__(64 * WPB) void k_q4k_swiglu_span(const uint8_t* __restrict__ wg,
+                                                             const uint8_t* __restrict__ wu, float* __restrict__ y,
+                                                             int M, const uint8_t* __restrict__ xq) {
+    using S = Span<NB, 2, false>;
+    __shared__ __align__(16) uint8_t slots[WPB][S::kSlot];
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int row = blockIdx.x * WPB + wave;
+    if (row >= M) return;
+    XOps xr[S::kNT][2];
+    span_load_x<ORDER, NB>(xr, xq);
+    const int64_t off = (int64_t)row * (NB * kQ4KBytes);
+    const uint8_t* seg[2] = {wg + off, wu + off};
+    const int np[2] = {NB * 9, NB * 9};
+    u32x4v v[S::kLoads];
+    span_issue<S>(v, seg, np);
+    float out[2];
+    span_rows<ORDER, NB, 2, false, false>(v, slots[wave], nullptr, xr, out);
+    if ((threadIdx.x & 63) == 0) y[row] = silu_mul(out[0], out[1]);
+}
+
+static bool all_aligned16(const uint8_t* const* w, int n) {
+    for (int i = 0; i < n; i++)
+        if (reinterpret_cast<uintptr_t>(w[i]) & 15) return false;
+    return true;
+}
+
+template <int ORDER, int R>
+static void launch_multi_span(const MultiArgs& a, const uint8_t* xq, hipStream_t s) {
+    constexpr int WPB = 4;
+    const int waves = a.first[kMulti];
+    hipLaunchKernelGGL((k_q4k_q8k_multi_span<ORDER, 16, R, WPB>), dim3((waves + WPB - 1) / WPB), dim3(64 * WPB), 0,
+                       s, a, xq);
+}
+
+void launch_qmatmul_q4k_q8k_multi(const uint8_t* const* w, float* const* y, const int* M, int n, const uint8_t* xq,
+                                  int K, int order, hipStream_t s) {
+    const int nb = K / 256;
+    if (nb == 16 && all_aligned16(w, n)) {
+        const int R = span_rows_per_wave(total_rows(M, n));
+        const MultiArgs a = make_multi_args(w, y, M, n, R);
+        if (a.first[kMulti] == 0) return;
+        if (order == 0)
+            R == 1 ? launch_multi_span<0, 1>(a, xq, s) : launch_multi_span<0, 2>(a, xq, s);
+        else
+            R == 1 ? launch_multi_span<1, 1>(a, xq, s) : launch_multi_span<1, 2>(a, xq, s);
+        return;
+    }
+    const GemvShape sh = choose_shape(total_rows(M, n), nb);
+    const MultiArgs a = make_multi_args(w, y, M, n, shape_rows_per_wave(sh));
+    if (a.first[kMulti] == 0) return;
+    if (order == 0)
+        launch_multi_order<0>(a, sh, xq, nb, s);
+    else
+        launch_multi_order<1>(a, sh, xq, nb, s);
+}
+
 // Gate and up from a Q8_K activation (K <= 4096), as launch_qmatmul_q4k_fused_swiglu
 // computes them after quantizing.
+template <int ORDER>
+static void launch_swiglu_span(const uint8_t* wg, const uint8_t* wu, float* y, int M, const uint8_t* xq,
+                               hipStream_t s) {
+    constexpr int WPB = 4;
+    hipLaunchKernelGGL((k_q4k_swiglu_span<ORDER, 16, WPB>), dim3((M + WPB - 1) / WPB), dim3(64 * WPB), 0, s, wg, wu, y,
+                       M, xq);
+}
+
 void launch_qmatmul_q4k_swiglu_q8k(const uint8_t* wg, const uint8_t* wu, float* y, int M, const uint8_t* xq, int K,
                                    int order, hipStream_t s) {
     const int nb = K / 256;
+    const uint8_t* wgu[2] = {wg, wu};
+    if (nb == 16 && all_aligned16(wgu, 2)) {
+        if (order == 0) launch_swiglu_span<0>(wg, wu, y, M, xq, s); else launch_swiglu_span<1>(wg, wu, y, M, xq, s);
+        return;
+    }
     if (order == 0)
         hipLaunchKernelGGL((k_q4k_fused_swiglu<0, 2, 4, true>), dim3((M + 3) / 4), dim3(256), 0, s, wg, wu, y, M,
                            nullptr, xq, nb);
@@ -920,9 +1091,27 @@ void launch_qmatmul_q4k_fused_swiglu(const uint8_t* wg, const uint8_t* wu, float
 // 8 waves).  IT = 1: 4*WPB Q8_K blocks per quantization pass cover nb.
 int fused_max_k() { return 64 * 256; }
 
+template <int ORDER, int R>
+static void launch_fused_span(const MultiArgs& a, const float* x, hipStream_t s) {
+    constexpr int WPB = 4;
+    const int waves = a.first[kMulti];
+    hipLaunchKernelGGL((k_q4k_fused_span<ORDER, 16, R, WPB>), dim3((waves + WPB - 1) / WPB), dim3(64 * WPB), 0, s, a,
+                       x);
+}
+
 void launch_qmatmul_q4k_fused_multi(const uint8_t* const* w, float* const* y, const int* M, int n, const float* x,
                                     int K, int order, hipStream_t s) {
     const int nb = K / 256;
+    if (nb == 16 && all_aligned16(w, n)) {
+        const int R = span_rows_per_wave(total_rows(M, n));
+        const MultiArgs a = make_multi_args(w, y, M, n, R);
+        if (a.first[kMulti] == 0) return;
+        if (order == 0)
+            R == 1 ? launch_fused_span<0, 1>(a, x, s) : launch_fused_span<0, 2>(a, x, s);
+        else
+            R == 1 ? launch_fused_span<1, 1>(a, x, s) : launch_fused_span<1, 2>(a, x, s);
+        return;
+    }
     const bool wide = nb <= 16;
     const MultiArgs a = make_multi_args(w, y, M, n, wide ? 2 : 1);
     if (a.first[kMulti] == 0) return;

@@ -125,6 +125,22 @@ def test_step_equals_restatement(dev, fmt, variant):
         _check_step(m, tok, want, (ko, vo), pos, f"fmt {fmt} {variant}")
 
 
+@pytest.mark.parametrize("fmt", [llama.W_Q4K, llama.W_Q4K_GGUF])
+def test_step_wide_embedding(dev, fmt):
+    """n_embd = 4096: Q/K/V from the norm's Q8_K, O and gate/up + SwiGLU take the
+    K = 4096 span kernels."""
+    cfg = LM.config(E=4096, H=32, HKV=8, D=128, F=512, L=1, vocab=300, max_seq=8)
+    layers, head = LM.make(cfg, fmt, seed=6)
+    m = _gpu_model(cfg, layers, head, fmt, dev)
+    ko, vo = LM.caches(cfg)
+    for pos, e in enumerate(LM.embeddings(cfg, 2, seed=9)):
+        print(f"step fmt={fmt} n_embd=4096 position {pos}", flush=True)
+        want = O.llama_step(fmt, layers, cfg, ko, vo, pos, e, head["out_norm"], head["lm"], head["lm_f32"],
+                            cfg["vocab_size"])
+        tok = m.step(_d(e, dev), pos)
+        _check_step(m, tok, want, (ko, vo), pos, f"fmt {fmt} n_embd=4096")
+
+
 @pytest.mark.parametrize("D,pos,H,HKV,bias", [
     (64, 63, 4, 2, False), (64, 64, 4, 2, False), (64, 255, 4, 2, False), (64, 2047, 4, 2, False),
     (128, 63, 4, 2, False), (128, 300, 4, 2, False), (256, 40, 4, 2, False), (32, 1000, 4, 2, False),

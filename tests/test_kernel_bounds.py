@@ -18,14 +18,19 @@ def lanes():
 
 # ---------------------------------------------------------------- Q4_K x Q8_K GEMV
 
+def span_rows_per_wave(rows):
+    """span_rows_per_wave() in q4k.hip."""
+    return 1 if rows <= 2048 else 2
+
+
 def q4k_gemv_shape(rows, nb):
     """(kind, R, G, WPB) as launch_gemv_order() in q4k.hip picks it for 16-byte
     aligned weights (kind 2: k_q4k_q8k_gemv_span)."""
+    if nb == 16:
+        return (2, span_rows_per_wave(rows), 1, 4)
     if nb > 16:
         return (1, 2, 1, 4)
-    if rows <= 8192:
-        return (1, 1, 1, 8)
-    return (2, 2, 2, 4) if nb == 16 else (0, 2, 2, 4)
+    return (1, 1, 1, 8) if rows <= 8192 else (0, 2, 2, 4)
 
 
 def x_accesses(c):
@@ -50,30 +55,42 @@ def check_wide(M, nb, row0, R, G):
                 assert np.max(bb * Q8K + off + size) <= x_size and np.min(bb * Q8K + off) >= 0
 
 
-def check_span(M, nb, row0):
-    """k_q4k_q8k_gemv_span<ORDER, NB=nb, R=2, WPB>: the wave's two rows as 16-byte
-    pieces (clamped to the tensor), its LDS slot of whole loads, the 4-lane
-    mapping's LDS reads and gemv4_rows's x reads."""
-    assert nb % 16 == 0
+def check_span(M, nb, row0, R, joint=True):
+    """span_issue / span_rows of Span<NB=nb, R, JOINT> in q4k.hip for the wave
+    whose first row is row0 of an M-row matrix (joint: R consecutive rows as one
+    span; otherwise R one-row spans of different matrices, here rows row0 of R
+    matrices of M rows): the 16-byte pieces (clamped to the tensor), the slot of
+    whole loads, the 4-lane mapping's LDS reads (block clamped to nb-1), the
+    load count each pass waits for, and span_load_x's Q8_K reads."""
     w_size, x_size = M * nb * Q4K, nb * Q8K
-    pieces = 2 * nb * 9
-    loads = (pieces + 63) // 64
+    segs = 1 if joint else R
+    seg_pieces = (R if joint else 1) * nb * 9
+    seg_loads = (seg_pieces + 63) // 64
+    loads = segs * seg_loads
     slot = loads * 64 * 16
-    np_ = min(2, M - row0) * nb * 9
     l = lanes()
     bl, c4 = l >> 2, l & 3
-    span = row0 * nb * Q4K
-    for u in range(loads):
-        p = np.minimum(l + 64 * u, np_ - 1)
-        assert (span + 16 * p).min() >= 0 and (span + 16 * p + 16).max() <= w_size
-        assert (16 * (l + 64 * u) + 16).max() <= slot
-    for r in range(2):
-        for t in range(nb // 16):
-            blk = (r * nb + 16 * t + bl) * Q4K
+    for g in range(segs):
+        np_ = min(R, M - row0) * nb * 9 if joint else nb * 9
+        span = row0 * nb * Q4K
+        for u in range(seg_loads):
+            p = np.minimum(l + 64 * u, np_ - 1)
+            assert (span + 16 * p).min() >= 0 and (span + 16 * p + 16).max() <= w_size
+            assert (16 * (l + 64 * (g * seg_loads + u)) + 16).max() <= slot
+    for r in range(R):
+        for t in range((nb + 15) // 16):
+            end = min(16 * t + 16, nb)
+            need = ((r * nb + end) * 9 + 63) // 64 if joint else r * seg_loads + (end * 9 + 63) // 64
+            assert need <= loads
+            row_off = r * nb * Q4K if joint else r * seg_loads * 1024
+            bb = np.minimum(16 * t + bl, nb - 1)
+            blk = row_off + bb * Q4K
+            # every piece the pass reads lies in a load it waited for
+            assert ((blk + 144) <= need * 1024).all()
             assert (blk + 16).max() <= slot
             assert (blk + 16 + 16 * c4 + 16).max() <= slot and (blk + 80 + 16 * c4 + 16).max() <= slot
-    for t in range(nb // 16):
-        b = 16 * t + bl
+    for t in range((nb + 15) // 16):
+        b = np.minimum(16 * t + bl, nb - 1)
         for c in (c4, c4 + 4):
             for off, size in x_accesses(c):
                 assert np.max(b * Q8K + off + size) <= x_size and np.min(b * Q8K + off) >= 0
@@ -103,7 +120,8 @@ def check_four(M, nb, row0, R):
 @pytest.mark.parametrize("M,K", [(4096, 4096), (14336, 4096), (4096, 14336), (1024, 4096), (1, 256), (5, 512),
                                  (13, 2304), (9, 2304), (3, 0), (64, 1024), (77, 512), (6144, 4096), (28672, 4096),
                                  (8193, 4096), (17, 4352), (2, 14336)])
-@pytest.mark.parametrize("force", [None, (0, 2, 2, 4), (1, 1, 1, 8), (1, 2, 1, 4), (1, 1, 1, 16), (2, 2, 2, 4)])
+@pytest.mark.parametrize("force", [None, (0, 2, 2, 4), (1, 1, 1, 8), (1, 2, 1, 4), (1, 1, 1, 16), (2, 2, 1, 4),
+                                   (2, 1, 1, 4)])
 def test_q4k_q8k_gemv_in_bounds(M, K, force):
     nb = K // 256
     if nb == 0:
@@ -123,10 +141,29 @@ def test_q4k_q8k_gemv_in_bounds(M, K, force):
             elif kind == 1:
                 check_four(M, nb, row0, R)
             else:
-                check_span(M, nb, row0)
+                check_span(M, nb, row0, R)
             for r in range(R):
                 if row0 + r < M:
                     assert (row0 + r) * 4 + 4 <= M * 4
+
+
+@pytest.mark.parametrize("Ms", [[4096, 1024, 1024], [4096, 1024, 1024, 13], [1], [7, 2048], [14336, 14336]])
+def test_q4k_multi_span_in_bounds(Ms):
+    """k_q4k_q8k_multi_span / k_q4k_fused_span at K = 4096: every wave of every
+    matrix (waves past the last row read row 0 of a non-empty matrix)."""
+    nb = 16
+    R = span_rows_per_wave(sum(Ms))
+    for M in Ms:
+        for row0 in range(0, M, R):
+            check_span(M, nb, row0, R)
+        check_span(M, nb, 0, R)
+
+
+@pytest.mark.parametrize("M", [1, 5, 512, 14336])
+def test_q4k_swiglu_span_in_bounds(M):
+    """k_q4k_swiglu_span: row r of gate and of up as two one-row spans."""
+    for row in sorted({0, M - 1, M // 2}):
+        check_span(M, 16, row, 2, joint=False)
 
 
 # ---------------------------------------------------------------- dequant
