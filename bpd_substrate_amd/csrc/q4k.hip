@@ -513,14 +513,21 @@ __global__ __launch_bounds__(64 * WPB) void k_q4k_q8k_gemv(const uint8_t* __rest
 // the MALL): 6.73 us against 7.36 for gemv_rows with per-lane chunk loads; the
 // same span in gemv_rows's 8-lane mapping 6.98.
 // ----------------------------------------------------------------------------
-template <int NB, int R, bool JOINT>
+// PB (pass buffer): instead of a slot holding every load, the wave's LDS holds
+// one pass (16 super-blocks, 2,304 bytes), refilled from the staged loads
+// before each pass; for long rows, whose spans would not fit LDS at full
+// occupancy.
+template <int NB, int R, bool JOINT, bool PB = false>
 struct Span {
     static constexpr int kSegs = JOINT ? 1 : R;
     static constexpr int kSegPieces = (JOINT ? R : 1) * NB * 9;
     static constexpr int kSegLoads = (kSegPieces + 63) / 64;
     static constexpr int kLoads = kSegs * kSegLoads;
-    static constexpr int kSlot = kLoads * 1024;  // LDS bytes per wave (whole loads)
+    static constexpr int kSlot = PB ? 16 * kQ4KBytes : kLoads * 1024;  // LDS bytes per wave
     static constexpr int kNT = (NB + 15) / 16;   // passes per row
+    // first piece of pass t of row r inside its segment, and the pass's pieces
+    static constexpr int pass_first(int r, int t) { return ((JOINT ? r * NB : 0) + 16 * t) * 9; }
+    static constexpr int pass_pieces(int t) { return (16 * t + 16 < NB ? 16 : NB - 16 * t) * 9; }
     // loads, in issue order, that hold every piece of pass t of row r
     static constexpr int covering(int r, int t) {
         const int end = 16 * t + 16 < NB ? 16 * t + 16 : NB;
@@ -567,11 +574,11 @@ __device__ __forceinline__ void span_load_x(XOps (&xr)[(NB + 15) / 16][2], const
 
 // The R row results (wave-uniform) from the staged loads; x from xr (LX false)
 // or from the workgroup's LDS copy xl (LX true).
-template <int ORDER, int NB, int R, bool JOINT, bool LX>
-__device__ __forceinline__ void span_rows(const u32x4v (&v)[Span<NB, R, JOINT>::kLoads], uint8_t* __restrict__ slot,
-                                          const uint8_t* __restrict__ xl, const XOps (&xr)[(NB + 15) / 16][2],
-                                          float (&out)[R]) {
-    using S = Span<NB, R, JOINT>;
+template <int ORDER, int NB, int R, bool JOINT, bool LX, bool PB = false>
+__device__ __forceinline__ void span_rows(const u32x4v (&v)[Span<NB, R, JOINT, PB>::kLoads],
+                                          uint8_t* __restrict__ slot, const uint8_t* __restrict__ xl,
+                                          const XOps (&xr)[(NB + 15) / 16][2], float (&out)[R]) {
+    using S = Span<NB, R, JOINT, PB>;
     const int lane = threadIdx.x & 63, bl = lane >> 2, c4 = lane & 3;
     float s[R];
 #pragma unroll
@@ -581,14 +588,29 @@ __device__ __forceinline__ void span_rows(const u32x4v (&v)[Span<NB, R, JOINT>::
     for (int r = 0; r < R; r++) {
 #pragma unroll
         for (int t = 0; t < S::kNT; t++) {
-            const int need = S::covering(r, t);
-#pragma unroll
-            for (int u = 0; u < S::kLoads; u++)
-                if (u >= written && u < need) *reinterpret_cast<u32x4v*>(slot + 16 * (lane + 64 * u)) = v[u];
-            written = need > written ? need : written;
-            lds_wave_order();
             const int b = 16 * t + bl, bb = min(b, NB - 1);
-            const uint8_t* blk = slot + S::row_offset(r) + bb * kQ4KBytes;
+            const uint8_t* blk;
+            if constexpr (PB) {
+                // the pass's pieces, in order, from the loads of its segment that hold
+                // any (the previous pass's reads were consumed before these writes)
+                const int g = JOINT ? 0 : r, p0 = S::pass_first(r, t), n = S::pass_pieces(t);
+#pragma unroll
+                for (int u = 0; u < S::kSegLoads; u++) {
+                    if (64 * u + 63 < p0 || 64 * u >= p0 + n) continue;
+                    const int q = lane + 64 * u - p0;
+                    if (q >= 0 && q < n) *reinterpret_cast<u32x4v*>(slot + 16 * q) = v[g * S::kSegLoads + u];
+                }
+                lds_wave_order();
+                blk = slot + (bb - 16 * t) * kQ4KBytes;
+            } else {
+                const int need = S::covering(r, t);
+#pragma unroll
+                for (int u = 0; u < S::kLoads; u++)
+                    if (u >= written && u < need) *reinterpret_cast<u32x4v*>(slot + 16 * (lane + 64 * u)) = v[u];
+                written = need > written ? need : written;
+                lds_wave_order();
+                blk = slot + S::row_offset(r) + bb * kQ4KBytes;
+            }
             const uint4 hdr = *reinterpret_cast<const uint4*>(blk);
             const uint4 qa = *reinterpret_cast<const uint4*>(blk + 16 + 16 * c4);
             const uint4 qb = *reinterpret_cast<const uint4*>(blk + 80 + 16 * c4);
@@ -959,9 +981,9 @@ __global__ __launch_bounds__(64 * WPB) void k_q4k_q8k_multi_span(MultiArgs a, co
 // Fused quantization: the workgroup quantizes x into LDS (x32_load /
 // x32_quantize, issued before and run after the span loads), then every wave
 // runs its rows with x from LDS.
-template <int ORDER, int NB, int R, int WPB>
+template <int ORDER, int NB, int R, int WPB, bool PB = false>
 __global__ __launch_bounds__(64 * WPB) void k_q4k_fused_span(MultiArgs a, const float* __restrict__ x) {
-    using S = Span<NB, R, true>;
+    using S = Span<NB, R, true, PB>;
     constexpr int IT = (NB + 4 * WPB - 1) / (4 * WPB);
     __shared__ __align__(16) uint8_t slots[WPB][S::kSlot];
     __shared__ __align__(16) uint8_t xl[NB * kXS];
@@ -980,7 +1002,7 @@ __global__ __launch_bounds__(64 * WPB) void k_q4k_fused_span(MultiArgs a, const 
     if (!has) return;
     XOps unused[S::kNT][2];
     float out[R];
-    span_rows<ORDER, NB, R, true, true>(v, slots[wave], xl, unused, out);
+    span_rows<ORDER, NB, R, true, true, PB>(v, slots[wave], xl, unused, out);
 #pragma unroll
     for (int r = 0; r < R; r++)
         if ((threadIdx.x & 63) == 0 && row0 + r < a.M[i]) a.y[i][row0 + r] = out[r];
@@ -1110,6 +1132,17 @@ void launch_qmatmul_q4k_fused_multi(const uint8_t* const* w, float* const* y, co
             R == 1 ? launch_fused_span<0, 1>(a, x, s) : launch_fused_span<0, 2>(a, x, s);
         else
             R == 1 ? launch_fused_span<1, 1>(a, x, s) : launch_fused_span<1, 2>(a, x, s);
+        return;
+    }
+    if (nb == 56 && all_aligned16(w, n)) {  // K = 14336: one row per wave through a pass buffer
+        constexpr int WPB = 8;
+        const MultiArgs a = make_multi_args(w, y, M, n, 1);
+        if (a.first[kMulti] == 0) return;
+        const dim3 grid((a.first[kMulti] + WPB - 1) / WPB);
+        if (order == 0)
+            hipLaunchKernelGGL((k_q4k_fused_span<0, 56, 1, WPB, true>), grid, dim3(64 * WPB), 0, s, a, x);
+        else
+            hipLaunchKernelGGL((k_q4k_fused_span<1, 56, 1, WPB, true>), grid, dim3(64 * WPB), 0, s, a, x);
         return;
     }
     const bool wide = nb <= 16;
