@@ -1,32 +1,44 @@
 // diag.hip — measurement helpers (no counterpart in the reference).
 //
-// k_stream_read: the simplest full-rate HBM read of n16 16-byte chunks (one
-// 16-byte load per lane, grid covering the buffer once, one store per wave that
-// only happens if the data XORs to a magic value).  It gives the streaming-read
-// floor of a single launch of a given size on this device, and a kernel of
-// exactly known traffic for calibrating the FETCH_SIZE counter.
+// k_stream_read: the fastest plain HBM read of n16 16-byte pieces found on this
+// device for a single launch: each wave reads a contiguous run of 288 pieces
+// (4,608 bytes, lane l taking pieces l, l+64, ...) with non-temporal loads, the
+// load pattern of the span GEMV without its arithmetic, and stores once per wave
+// only if the data XORs to a magic value.  It gives the streaming-read floor of
+// a single launch of a given size, and a kernel of exactly known traffic for
+// calibrating the FETCH_SIZE counter.  Measured for 33.0 MB: 5.87 us, against
+// 6.38 us for one plain 16-byte load per lane and 6.02 us for the same with
+// the non-temporal hint.
 #include "bpdq_device.h"
 #include "bpdq_launch.h"
 
 namespace bpdq {
 
+constexpr int kReadRun = 288;                  // pieces per wave
+constexpr int kReadLoads = (kReadRun + 63) / 64;
+
 __global__ __launch_bounds__(256) void k_stream_read(const uint4* __restrict__ p, int64_t n16,
                                                      uint32_t* __restrict__ sink) {
-    const int64_t i = (int64_t)blockIdx.x * 1024 + threadIdx.x;
-    uint4 v[4];
+    typedef uint32_t v4 __attribute__((ext_vector_type(4)));
+    const int lane = threadIdx.x & 63;
+    const int64_t run = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * kReadRun;
+    v4 v[kReadLoads];
+    // lanes past the run or the buffer repeat its last piece (the same line: no
+    // extra traffic), so that every load is unconditional
 #pragma unroll
-    for (int u = 0; u < 4; u++) {
-        const int64_t j = i + 256 * u;
-        v[u] = j < n16 ? p[j] : make_uint4(0, 0, 0, 0);
+    for (int u = 0; u < kReadLoads; u++) {
+        const int64_t j = min(run + min(lane + 64 * u, kReadRun - 1), n16 - 1);
+        v[u] = __builtin_nontemporal_load(reinterpret_cast<const v4*>(p + j));
     }
     uint32_t acc = 0;
 #pragma unroll
-    for (int u = 0; u < 4; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    for (int u = 0; u < kReadLoads; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
     if (acc == 0x9E3779B9u) sink[0] = acc;
 }
 
 void launch_stream_read(const uint8_t* p, int64_t n16, uint32_t* sink, hipStream_t s) {
-    hipLaunchKernelGGL(k_stream_read, dim3((unsigned)((n16 + 1023) / 1024)), dim3(256), 0, s,
+    const int64_t runs = (n16 + kReadRun - 1) / kReadRun;
+    hipLaunchKernelGGL(k_stream_read, dim3((unsigned)((runs + 3) / 4)), dim3(256), 0, s,
                        reinterpret_cast<const uint4*>(p), n16, sink);
 }
 

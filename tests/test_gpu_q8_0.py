@@ -98,6 +98,26 @@ def test_dispatch_scalar_order(dev, mw, mt, K):
     assert_bits_equal(got, O.dispatch_q8_0(W, Xq, mw, mt, K, "S", nthreads=8), f"S-order {mw}x{mt}x{K}")
 
 
+@pytest.mark.parametrize("mw,mt,K", [(130, 129, 512), (40, 9, 224)])
+def test_dispatch_scalar_order_special_scales(dev, mw, mt, K):
+    """Zero, subnormal, infinite and NaN block scales in W and X: the scale products
+    come from an MFMA, and each must equal the fp32 product RN(Ad*Bd) (NaNs compared
+    as NaN)."""
+    nb = K // 32
+    W = synth.q8_0(mw, K, synth.key(43, 11)).reshape(mw, nb, 34).copy()
+    X = synth.normal_f32(mt * K, synth.key(43, 12))
+    Xq = O.quant_q8_0(X).reshape(mt, nb, 34).copy()
+    special = [0x0000, 0x8000, 0x0001, 0x83FF, 0x7C00, 0xFC00, 0x7E00, 0x7BFF]
+    for i, h in enumerate(special):
+        W[(7 * i) % mw, (3 * i) % nb, 0:2] = np.array([h & 0xFF, h >> 8], np.uint8)
+        Xq[(5 * i + 1) % mt, (2 * i + 1) % nb, 0:2] = np.array([h & 0xFF, h >> 8], np.uint8)
+    W, Xq = W.ravel(), Xq.ravel()
+    got = to_np(gpu.qmatmul_q8_0_dispatch_s(_d(W, dev), _d(Xq, dev), mw, mt, K))
+    want = O.dispatch_q8_0(W, Xq, mw, mt, K, "S", nthreads=8)
+    assert np.isnan(want).any() and np.isinf(want).any()
+    assert_bits_equal(got, want, f"S-order special scales {mw}x{mt}x{K}", nan_equal=True)
+
+
 def test_llamafile_scalar_build_path(dev):
     mw, mt, K = 96, 40, 512
     W = synth.q8_0(mw, K, synth.key(43, 9))
