@@ -299,7 +299,7 @@ def main():
         "pct_of_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(value / HBM_PEAK_GBS, 4), "traffic": load_traffic(),
-                     "kernel": "k_q4k_q8k_gemv", "alg_bytes_per_launch": ALG_BYTES,
+                     "kernel": "k_q4k_q8k_gemv_span", "alg_bytes_per_launch": ALG_BYTES,
                      "launch_us": round(us, 3),
                      "stream_read_floor": {"us": round(rd_us, 3), "gb_s": round(rd_gbs, 1),
                                            "frac_of_floor": round(rd_us / us, 4)}},
