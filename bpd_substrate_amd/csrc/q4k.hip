@@ -1113,10 +1113,20 @@ void launch_qmatmul_q4k_fused_swiglu(const uint8_t* wg, const uint8_t* wu, float
 // 8 waves).  IT = 1: 4*WPB Q8_K blocks per quantization pass cover nb.
 int fused_max_k() { return 64 * 256; }
 
+// K = 4096: 4 waves per workgroup; from 16,384 rows (gate + up) 8 waves with the
+// pass buffer, which halves the workgroups that each quantize x (measured:
+// gate+up 2x14336 12.98 us against 13.35; Q/K/V and O 4.9 and 4.1 us against 5.4
+// and 4.3 with 8 waves).
 template <int ORDER, int R>
 static void launch_fused_span(const MultiArgs& a, const float* x, hipStream_t s) {
-    constexpr int WPB = 4;
     const int waves = a.first[kMulti];
+    if (R == 2 && a.rows >= 16384) {
+        constexpr int WPB = 8;
+        hipLaunchKernelGGL((k_q4k_fused_span<ORDER, 16, 2, WPB, true>), dim3((waves + WPB - 1) / WPB), dim3(64 * WPB),
+                           0, s, a, x);
+        return;
+    }
+    constexpr int WPB = 4;
     hipLaunchKernelGGL((k_q4k_fused_span<ORDER, 16, R, WPB>), dim3((waves + WPB - 1) / WPB), dim3(64 * WPB), 0, s, a,
                        x);
 }

@@ -159,27 +159,30 @@ def test_q4k_multi_span_in_bounds(Ms):
         check_span(M, nb, 0, R)
 
 
-@pytest.mark.parametrize("M", [1, 7, 4096])
-def test_q4k_fused_span_pass_buffer_in_bounds(M):
-    """k_q4k_fused_span<ORDER, 56, 1, 8, PB = true> (K = 14336): the row's pieces as
-    loads, each pass's pieces copied into a 16-block buffer and read back there."""
-    nb, buf = 56, 16 * Q4K
-    for row0 in sorted({0, M - 1}):
-        check_span(M, nb, row0, 1)  # global reads and x reads are those of the slot form
+@pytest.mark.parametrize("nb,R,M", [(56, 1, 1), (56, 1, 7), (56, 1, 4096), (16, 2, 16384), (16, 2, 28672),
+                                    (16, 2, 16385)])
+def test_q4k_fused_span_pass_buffer_in_bounds(nb, R, M):
+    """k_q4k_fused_span<ORDER, NB, R, WPB, PB = true> (K = 14336 one row per wave; K = 4096
+    from 16,384 rows, two rows per wave): the rows' pieces as loads, each pass's pieces
+    copied into a 16-block buffer and read back there."""
+    buf = 16 * Q4K
+    for row0 in sorted({0, ((M - 1) // R) * R}):
+        check_span(M, nb, row0, R)  # global reads and x reads are those of the slot form
         l = lanes()
-        bl, c4 = l >> 2, l & 3
-        pieces = nb * 9
+        bl = l >> 2
+        pieces = R * nb * 9
         covered = np.zeros(pieces, bool)
-        for t in range((nb + 15) // 16):
-            p0, n = 16 * t * 9, min(16, nb - 16 * t) * 9
-            for u in range((pieces + 63) // 64):
-                q = l + 64 * u - p0
-                ok = (q >= 0) & (q < n)
-                assert (16 * q[ok] + 16 <= buf).all()
-                covered[(l + 64 * u)[ok & (l + 64 * u < pieces)]] = True
-            bb = np.minimum(16 * t + bl, nb - 1) - 16 * t
-            assert (bb >= 0).all() and ((bb * Q4K + 144) <= buf).all()
-            assert ((bb * Q4K + 144) <= n * 16).all()  # only the pass's own pieces are read
+        for r in range(R):
+            for t in range((nb + 15) // 16):
+                p0, n = (r * nb + 16 * t) * 9, min(16, nb - 16 * t) * 9
+                for u in range((pieces + 63) // 64):
+                    q = l + 64 * u - p0
+                    ok = (q >= 0) & (q < n)
+                    assert (16 * q[ok] + 16 <= buf).all()
+                    covered[(l + 64 * u)[ok & (l + 64 * u < pieces)]] = True
+                bb = np.minimum(16 * t + bl, nb - 1) - 16 * t
+                assert (bb >= 0).all() and ((bb * Q4K + 144) <= buf).all()
+                assert ((bb * Q4K + 144) <= n * 16).all()  # only the pass's own pieces are read
         assert covered.all()
 
 
