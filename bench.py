@@ -12,8 +12,8 @@ launch rate cannot hide or inflate kernel time.  `value` and
 `roofline.achieved` are the algorithmic bytes of one GEMV divided by the timed
 region / K.  The same method times, on the same rotating copies, a plain
 streaming read of the weight's bytes (the single-launch HBM read floor of this
-size on this device), the cfg0 dequant and the cfg2 Q8_0 GEMVs.  Prints ONE
-JSON line.
+size on this device), the cfg0 dequant, the cfg1 GEMV and the cfg2 Q8_0 GEMVs.
+Prints ONE JSON line.
 """
 import argparse
 import json
@@ -318,6 +318,19 @@ def main():
         del dq_q, dq_o, dq_in
         q_us = T.us_per_launch([(lambda: L.bpd_quant_q8_k_gpu(x.data_ptr(), xq.data_ptr(), K))] * 200)
         result["quant_q8_k_4096_us"] = round(q_us, 3)
+        # cfg1: the cfg0 weight as a 4096x4096 GEMV against x -> Q8_K (rows of 16 blocks)
+        w1 = torch.from_numpy(synth.q4k(4096, 4096, synth.key(42, synth.STREAM["cfg0_w"]))).to(dev)
+        g1 = [w1] + [w1.clone() for _ in range(-(-512 * 2**20 // w1.numel()) - 1)]
+        y1 = torch.empty(4096, dtype=torch.float32, device=dev)
+        torch.cuda.synchronize()
+        c1_us = T.us_per_launch([(lambda i=i: L.bpd_qmatmul_q4k_q8k_gpu(g1[i % len(g1)].data_ptr(), xq.data_ptr(),
+                                                                       y1.data_ptr(), 4096, 4096))
+                                 for i in range(1000)])
+        c1_bytes = 4096 * 16 * 144 + X_BYTES + 4096 * 4
+        result["q4k_q8k_gemv_cfg1_4096x4096"] = {"us": round(c1_us, 3), "gb_s": round(c1_bytes / c1_us / 1e3, 1),
+                                                 "frac_hbm": round(c1_bytes / c1_us / 1e3 / HBM_PEAK_GBS, 4),
+                                                 "copies": len(g1)}
+        del g1, w1, y1
         for name, (rows, k) in Q80_SHAPES.items():
             W = torch.from_numpy(synth.q8_0(rows, k, synth.key(42, synth.STREAM[f"cfg2_{name}"]))).to(dev)
             n_c = max(16, -(-512 * 2**20 // W.numel()))
