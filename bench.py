@@ -281,6 +281,7 @@ def main():
                              for i in range(a.steps)])
     rd_gbs = W_BYTES / (rd_us * 1e-6) / 1e9
 
+
     result = {
         "metric": "Q4_K GEMV HBM GB/s (% of peak) at 14336x4096; dequant Gelem/s; ULP vs ref",
         "value": round(value, 1),
@@ -306,6 +307,22 @@ def main():
     }
 
     if not a.no_extra:
+        # the same kernel family with the launch cost shared: two 14336x4096 matrices of one
+        # Q8_K x in one multi-matrix launch (the decode step's gate + up), same rotating copies
+        import ctypes
+        y2 = torch.empty(M, dtype=torch.float32, device=dev)
+        y_arr = (ctypes.c_void_p * 2)(y.data_ptr(), y2.data_ptr())
+        m_arr = (ctypes.c_int * 2)(M, M)
+        w_arrs = [(ctypes.c_void_p * 2)(wp[i % copies], wp[(i + 1) % copies]) for i in range(copies)]
+        pair_us = T.us_per_launch([(lambda i=i: L.bpd_qmatmul_q4k_q8k_multi_gpu(
+            ctypes.addressof(w_arrs[(2 * i) % copies]), ctypes.addressof(y_arr), ctypes.addressof(m_arr), 2,
+            xq.data_ptr(), K)) for i in range(a.steps // 2)])
+        gpu.check()
+        pair_bytes = 2 * W_BYTES + X_BYTES + 2 * Y_BYTES
+        result["two_matrix_launch_2x14336x4096"] = {
+            "us": round(pair_us, 3), "gb_s": round(pair_bytes / pair_us / 1e3, 1),
+            "frac_hbm": round(pair_bytes / pair_us / 1e3 / HBM_PEAK_GBS, 4),
+            "note": "not the metric: two GEMVs of one x per launch, as the decode step's gate + up"}
         log("dequant 4096x4096 (cfg0) and Q8_0 GEMVs (cfg2)")
         dq_in = torch.from_numpy(synth.q4k(DQ_BLOCKS, 256, synth.key(42, synth.STREAM["cfg0_w"]))).to(dev)
         dq_q = [dq_in] + [dq_in.clone() for _ in range(7)]
