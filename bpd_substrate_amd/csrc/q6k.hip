@@ -183,7 +183,183 @@ __global__ __launch_bounds__(64 * WPB) void k_q6k_q8k_gemv(const uint8_t* __rest
     }
 }
 
+// ----------------------------------------------------------------------------
+// The same GEMV for K = 4096 (16 super-blocks a row) and 16-byte aligned
+// weights, with each wave's two rows read as one contiguous span: 420 aligned
+// 16-byte pieces, lane l loading pieces l, l+64, ..., non-temporal, all issued
+// before any compute.  Eight super-blocks are 1,680 bytes = 105 whole pieces, so
+// before each pass (8 blocks of one row) the wave copies that pass's pieces
+// into its own 1,680-byte LDS buffer and the lanes read their operands there in
+// k_q6k_q8k_gemv's mapping.  Blocks sit at 210-byte offsets, so odd blocks are
+// only 2-byte aligned: words are assembled from aligned dwords with v_alignbit.
+// x operands of both passes are loaded before the span.  Integer sums, c_b and
+// the fp32 order are k_q6k_q8k_gemv's, so the bits are the same.
+// ----------------------------------------------------------------------------
+constexpr int kQ6Pass = 8 * kQ6KBytes;    // 1,680 bytes = 105 pieces
+constexpr int kQ6Buf = kQ6Pass + 16;      // tail room for the last aligned dword reads
+
+typedef uint32_t q6u32x4 __attribute__((ext_vector_type(4)));
+
+struct Q6X {
+    uint32_t xs[8];  // the 32 q8 values that meet this lane's 32 six-bit values
+    int bs0, bs1;    // bsums of its two groups
+    float dy;
+};
+
+template <int ORDER>
+__device__ __forceinline__ Q6X load_q6x(const uint8_t* __restrict__ xb, int c) {
+    Q6X o;
+    __builtin_memcpy(&o.dy, xb, 4);
+    int g0, e0, e1;
+    if (ORDER == 0) {
+        g0 = 2 * c;
+        e0 = 32 * c;
+        e1 = e0 + 16;
+    } else {
+        const int h = c >> 2, p = c & 3;
+        g0 = 8 * h + p;
+        e0 = 128 * h + 16 * p;
+        e1 = e0 + 64;
+    }
+    const int g1 = ORDER == 0 ? g0 + 1 : g0 + 4;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        o.xs[k] = ld_u32(xb + 4 + e0 + 4 * k);
+        o.xs[4 + k] = ld_u32(xb + 4 + e1 + 4 * k);
+    }
+    int16_t b0, b1;
+    __builtin_memcpy(&b0, xb + 260 + 2 * g0, 2);
+    __builtin_memcpy(&b1, xb + 260 + 2 * g1, 2);
+    o.bs0 = b0;
+    o.bs1 = b1;
+    return o;
+}
+
+// N consecutive words starting at LDS address p, p % 4 in {0, 2}.
+template <int N>
+__device__ __forceinline__ void lds_words_a2(const uint8_t* p, uint32_t (&out)[N]) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    const uint32_t* base = reinterpret_cast<const uint32_t*>(a & ~(uintptr_t)3);
+    const uint32_t sh = 8u * (uint32_t)(a & 3);
+    uint32_t d[N + 1];
+#pragma unroll
+    for (int i = 0; i <= N; i++) d[i] = base[i];
+#pragma unroll
+    for (int i = 0; i < N; i++) out[i] = __builtin_amdgcn_alignbit(d[i + 1], d[i], sh);
+}
+
+template <int ORDER>
+__device__ __forceinline__ int q6k_lane_isum_lds(const uint8_t* blk, const Q6X& x, int c) {
+    int S0 = 0, S1 = 0, g0, g1;
+    if (ORDER == 0) {
+        g0 = 2 * c;
+        g1 = 2 * c + 1;
+        uint32_t qlw[4], qhw[2];
+        lds_words_a2<4>(blk + 16 * c, qlw);
+        lds_words_a2<2>(blk + 128 + 8 * c, qhw);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const uint32_t two = (qlw[j >> 1] >> (16 * (j & 1))) & 0xFFFFu;
+            const uint32_t hb = (qhw[j >> 2] >> (8 * (j & 3))) & 0xFFu;
+            const uint32_t qv = q6_bytes(spread_nibbles(two), spread_pairs(hb));
+            if (j < 4)
+                S0 = sdot4(qv, x.xs[j], S0);
+            else
+                S1 = sdot4(qv, x.xs[j], S1);
+        }
+    } else {
+        const int h = c >> 2, p = c & 3, sh = 2 * (p >> 1);
+        g0 = 8 * h + p;
+        g1 = g0 + 4;
+        uint32_t qlw[4], qhw[4];
+        lds_words_a2<4>(blk + 64 * h + 16 * p, qlw);
+        lds_words_a2<4>(blk + 128 + 32 * h + 16 * (p & 1), qhw);
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint32_t lo = q6_bytes(qlw[k], qhw[k] >> sh);
+            const uint32_t hi = q6_bytes(qlw[k] >> 4, qhw[k] >> (sh + 4));
+            S0 = sdot4(lo, x.xs[k], S0);
+            S1 = sdot4(hi, x.xs[4 + k], S1);
+        }
+    }
+    const int sc0 = (int8_t)blk[192 + g0], sc1 = (int8_t)blk[192 + g1];
+    return sc0 * (S0 - 32 * x.bs0) + sc1 * (S1 - 32 * x.bs1);
+}
+
+template <int ORDER, int WPB>
+__global__ __launch_bounds__(64 * WPB) void k_q6k_q8k_gemv_span(const uint8_t* __restrict__ w,
+                                                               const uint8_t* __restrict__ xq, float* __restrict__ y,
+                                                               int M) {
+    constexpr int NB = 16, R = 2, NT = NB / 8;
+    constexpr int kPieces = R * NB * kQ6KBytes / 16;  // 420
+    constexpr int kLoads = (kPieces + 63) / 64;       // 7
+    __shared__ __align__(16) uint8_t bufs[WPB][kQ6Buf];
+    const int lane = threadIdx.x & 63;
+    const int q = lane >> 3, c = lane & 7;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int row0 = (blockIdx.x * WPB + wave) * R;
+    if (row0 >= M) return;
+    Q6X x[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) x[t] = load_q6x<ORDER>(xq + (int64_t)(8 * t + q) * kQ8KBytes, c);
+    // rows past M repeat the last piece of row M-1 (their results are not stored)
+    const uint8_t* span = w + (int64_t)row0 * (NB * kQ6KBytes);
+    const int np = min(R, M - row0) * NB * kQ6KBytes / 16;
+    q6u32x4 v[kLoads];
+#pragma unroll
+    for (int u = 0; u < kLoads; u++) {
+        const uint32_t p = (uint32_t)min(lane + 64 * u, np - 1);
+        v[u] = __builtin_nontemporal_load(reinterpret_cast<const q6u32x4*>(span + 16u * p));
+    }
+    uint8_t* buf = bufs[wave];
+    float s[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) s[r] = 0.0f;
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            // the pass's 105 pieces, in order (the previous pass's reads were consumed
+            // before these writes)
+            const int p0 = (r * NB + 8 * t) * kQ6KBytes / 16, n = kQ6Pass / 16;
+#pragma unroll
+            for (int u = 0; u < kLoads; u++) {
+                if (64 * u + 63 < p0 || 64 * u >= p0 + n) continue;
+                const int k = lane + 64 * u - p0;
+                if (k >= 0 && k < n) *reinterpret_cast<q6u32x4*>(buf + 16 * k) = v[u];
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            const uint8_t* blk = buf + q * kQ6KBytes;
+            int isum = q6k_lane_isum_lds<ORDER>(blk, x[t], c);
+            isum = sum8_i(isum);
+            uint16_t dh;
+            __builtin_memcpy(&dh, blk + 208, 2);
+            const float dd = f16_ieee(dh) * x[t].dy;
+            s[r] = s[r] + dd * (float)isum;
+        }
+    }
+    // k_q6k_q8k_gemv's combine
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        float tv = s[r];
+        tv = tv + dpp_f<0x140>(tv);
+        const float p01 = readlane_f(tv, 0), p23 = readlane_f(tv, 16);
+        const float p45 = readlane_f(tv, 32), p67 = readlane_f(tv, 48);
+        if (lane == 0 && row0 + r < M) y[row0 + r] = (p01 + p23) + (p45 + p67);
+    }
+}
+
 void launch_qmatmul_q6k_q8k(const uint8_t* w, const uint8_t* xq, float* y, int M, int K, int order, hipStream_t s) {
+    if (K == 4096 && (reinterpret_cast<uintptr_t>(w) & 15) == 0) {
+        constexpr int WPB = 4;
+        const int waves = (M + 1) / 2;
+        const dim3 grid((waves + WPB - 1) / WPB);
+        if (order == 0)
+            hipLaunchKernelGGL((k_q6k_q8k_gemv_span<0, WPB>), grid, dim3(64 * WPB), 0, s, w, xq, y, M);
+        else
+            hipLaunchKernelGGL((k_q6k_q8k_gemv_span<1, WPB>), grid, dim3(64 * WPB), 0, s, w, xq, y, M);
+        return;
+    }
     constexpr int R = 2, WPB = 4;
     const int nb = K / 256;
     const int waves = (M + R - 1) / R;

@@ -44,7 +44,8 @@ def test_dequant_q6k_random_bytes(dev, order, o):
 
 
 @pytest.mark.parametrize("order,o", ORDERS)
-@pytest.mark.parametrize("M,K", [(1, 256), (5, 512), (64, 4096), (4096, 4096), (17, 14336), (1024, 14336), (3, 2304)])
+@pytest.mark.parametrize("M,K", [(1, 256), (5, 512), (64, 4096), (4096, 4096), (7, 4096), (14336, 4096), (17, 14336),
+                                 (1024, 14336), (3, 2304)])
 def test_qmatmul_q6k_q8k(dev, order, o, M, K):
     w = q6k_blocks(M * K // 256, M + K)
     x = synth.normal_f32(K, synth.key(70, K))

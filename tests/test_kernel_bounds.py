@@ -193,6 +193,58 @@ def test_q4k_swiglu_span_in_bounds(M):
         check_span(M, 16, row, 2, joint=False)
 
 
+@pytest.mark.parametrize("M", [1, 7, 64, 14336])
+def test_q6k_span_in_bounds(M):
+    """k_q6k_q8k_gemv_span (K = 4096, two rows per wave): the span pieces (clamped to
+    the tensor), each pass's 105 pieces in the 1,680-byte buffer, the 2-byte-aligned
+    operand words read as whole aligned dwords inside the buffer, the Q8_K reads."""
+    Q6, nb, R, buf = 210, 16, 2, 8 * 210 + 16
+    w_size, x_size = M * nb * Q6, nb * Q8K
+    pieces = R * nb * Q6 // 16
+    loads = (pieces + 63) // 64
+    l = lanes()
+    q, c = l >> 3, l & 7
+    for row0 in sorted({0, ((M - 1) // R) * R}):
+        np_ = min(R, M - row0) * nb * Q6 // 16
+        span = row0 * nb * Q6
+        for u in range(loads):
+            p = np.minimum(l + 64 * u, np_ - 1)
+            assert (span + 16 * p).min() >= 0 and (span + 16 * p + 16).max() <= w_size
+        covered = np.zeros(pieces, bool)
+        for r in range(R):
+            for t in range(nb // 8):
+                p0, n = (r * nb + 8 * t) * Q6 // 16, 8 * Q6 // 16
+                assert (r * nb + 8 * t) * Q6 % 16 == 0
+                for u in range(loads):
+                    k = l + 64 * u - p0
+                    ok = (k >= 0) & (k < n)
+                    assert (16 * k[ok] + 16 <= buf).all()
+                    covered[(l + 64 * u)[ok & (l + 64 * u < pieces)]] = True
+        assert covered.all()
+    blk = q * Q6
+    for order in (0, 1):
+        if order == 0:
+            spans = [(blk + 16 * c, 4), (blk + 128 + 8 * c, 2)]
+            groups = (2 * c, 2 * c + 1)
+        else:
+            h, pp = c >> 2, c & 3
+            spans = [(blk + 64 * h + 16 * pp, 4), (blk + 128 + 32 * h + 16 * (pp & 1), 4)]
+            groups = (8 * h + pp, 8 * h + pp + 4)
+        for addr, nw in spans:
+            assert ((addr & 3) % 2 == 0).all()
+            assert (((addr & ~3) + 4 * (nw + 1)) <= buf).all()   # nw + 1 aligned dwords
+            assert ((addr + 4 * nw) <= 8 * Q6).all()              # the words themselves lie in the pass
+        for g in groups:
+            assert ((blk + 192 + g + 1) <= 8 * Q6).all()
+        assert ((blk + 210) <= 8 * Q6).all()
+        for t in range(nb // 8):
+            xb = (8 * t + q) * Q8K
+            for off, size in x_accesses(c):
+                assert np.max(xb + off + size) <= x_size
+            for g in groups:
+                assert np.max(xb + 260 + 2 * g + 2) <= x_size
+
+
 # ---------------------------------------------------------------- dequant
 
 @pytest.mark.parametrize("nb", [1, 7, 33, 65536, 4096])
