@@ -371,7 +371,7 @@ def main():
         out = torch.empty(512 * 14336, dtype=torch.float32, device=dev)
         torch.cuda.synchronize()
         u = T.us_per_launch([(lambda: L.bpd_qmatmul_q8_0_dispatch_s_gpu(W.data_ptr(), Xq.data_ptr(), out.data_ptr(),
-                                                                         14336, 512, 4096))] * 20)
+                                                                         14336, 512, 4096))] * 50)
         ops = 2.0 * 512 * 4096 * 14336
         result["prefill_q8_0_cfg4"] = {"us": round(u, 2), "tops": round(ops / u / 1e6, 1),
                                        "frac_int8_mfma": round(ops / u / 1e6 / 5000.0, 4),
