@@ -192,7 +192,8 @@ __global__ __launch_bounds__(64 * WPB) void k_q6k_q8k_gemv(const uint8_t* __rest
 // into its own 1,680-byte LDS buffer and the lanes read their operands there in
 // k_q6k_q8k_gemv's mapping.  Blocks sit at 210-byte offsets, so odd blocks are
 // only 2-byte aligned: words are assembled from aligned dwords with v_alignbit.
-// x operands of both passes are loaded before the span.  Integer sums, c_b and
+// x operands of both passes are loaded (and, in the reference map, regrouped)
+// before the span.  Integer sums, c_b and
 // the fp32 order are k_q6k_q8k_gemv's, so the bits are the same.
 // ----------------------------------------------------------------------------
 constexpr int kQ6Pass = 8 * kQ6KBytes;    // 1,680 bytes = 105 pieces
@@ -200,15 +201,22 @@ constexpr int kQ6Buf = kQ6Pass + 16;      // tail room for the last aligned dwor
 
 typedef uint32_t q6u32x4 __attribute__((ext_vector_type(4)));
 
+// The 32 q8 values that meet this lane's 32 six-bit values, the bsums of its two
+// groups and the block scale.  Reference map: the q8 bytes regrouped to match
+// the nibble and 2-bit fields as they sit in ql and qh (see q6k_lane_isum_lds):
+// xs[2m], xs[2m+1] = the even / odd elements of 8m..8m+7 (m < 4), and
+// xs[8+4n+k] = elements 16n+k, 16n+4+k, 16n+8+k, 16n+12+k (n < 2, k < 4).
+// GGUF map: xs[0..7] = elements e0.. and e1.. as loaded.
+template <int ORDER>
 struct Q6X {
-    uint32_t xs[8];  // the 32 q8 values that meet this lane's 32 six-bit values
-    int bs0, bs1;    // bsums of its two groups
+    uint32_t xs[ORDER == 0 ? 16 : 8];
+    int bs0, bs1;
     float dy;
 };
 
 template <int ORDER>
-__device__ __forceinline__ Q6X load_q6x(const uint8_t* __restrict__ xb, int c) {
-    Q6X o;
+__device__ __forceinline__ Q6X<ORDER> load_q6x(const uint8_t* __restrict__ xb, int c) {
+    Q6X<ORDER> o;
     __builtin_memcpy(&o.dy, xb, 4);
     int g0, e0, e1;
     if (ORDER == 0) {
@@ -222,10 +230,30 @@ __device__ __forceinline__ Q6X load_q6x(const uint8_t* __restrict__ xb, int c) {
         e1 = e0 + 64;
     }
     const int g1 = ORDER == 0 ? g0 + 1 : g0 + 4;
+    uint32_t raw[8];
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-        o.xs[k] = ld_u32(xb + 4 + e0 + 4 * k);
-        o.xs[4 + k] = ld_u32(xb + 4 + e1 + 4 * k);
+        raw[k] = ld_u32(xb + 4 + e0 + 4 * k);
+        raw[4 + k] = ld_u32(xb + 4 + e1 + 4 * k);
+    }
+    if constexpr (ORDER == 0) {
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            o.xs[2 * m] = __builtin_amdgcn_perm(raw[2 * m + 1], raw[2 * m], 0x06040200u);      // even elements
+            o.xs[2 * m + 1] = __builtin_amdgcn_perm(raw[2 * m + 1], raw[2 * m], 0x07050301u);  // odd elements
+        }
+#pragma unroll
+        for (int n = 0; n < 2; n++)
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const uint32_t sel = (uint32_t)k | ((uint32_t)(k + 4) << 8);  // byte k of S1, byte k of S0
+                const uint32_t t1 = __builtin_amdgcn_perm(raw[4 * n + 1], raw[4 * n], sel);
+                const uint32_t t2 = __builtin_amdgcn_perm(raw[4 * n + 3], raw[4 * n + 2], sel);
+                o.xs[8 + 4 * n + k] = __builtin_amdgcn_perm(t2, t1, 0x05040100u);
+            }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 8; k++) o.xs[k] = raw[k];
     }
     int16_t b0, b1;
     __builtin_memcpy(&b0, xb + 260 + 2 * g0, 2);
@@ -249,24 +277,33 @@ __device__ __forceinline__ void lds_words_a2(const uint8_t* p, uint32_t (&out)[N
 }
 
 template <int ORDER>
-__device__ __forceinline__ int q6k_lane_isum_lds(const uint8_t* blk, const Q6X& x, int c) {
+__device__ __forceinline__ int q6k_lane_isum_lds(const uint8_t* blk, const Q6X<ORDER>& x, int c) {
     int S0 = 0, S1 = 0, g0, g1;
-    if (ORDER == 0) {
+    if constexpr (ORDER == 0) {
+        // elements 32c+e: ql byte e/2 holds e (low nibble) and e+1 (high), qh byte e/4
+        // holds bits 2(e%4).. of e.  The sum over a group is exact in any order, so
+        // dot the fields where they sit against the regrouped x:
+        //   S = sum_m [low nibbles of ql dword m . even x] + [high nibbles . odd x]
+        //     + 16 * sum_{n,k} [bits 2k..2k+1 of the qh dword n bytes . xs[8+4n+k]]
         g0 = 2 * c;
         g1 = 2 * c + 1;
         uint32_t qlw[4], qhw[2];
         lds_words_a2<4>(blk + 16 * c, qlw);
         lds_words_a2<2>(blk + 128 + 8 * c, qhw);
+        int H0 = 0, H1 = 0;
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const uint32_t two = (qlw[j >> 1] >> (16 * (j & 1))) & 0xFFFFu;
-            const uint32_t hb = (qhw[j >> 2] >> (8 * (j & 3))) & 0xFFu;
-            const uint32_t qv = q6_bytes(spread_nibbles(two), spread_pairs(hb));
-            if (j < 4)
-                S0 = sdot4(qv, x.xs[j], S0);
-            else
-                S1 = sdot4(qv, x.xs[j], S1);
+        for (int m = 0; m < 4; m++) {
+            int& S = m < 2 ? S0 : S1;
+            S = sdot4(qlw[m] & 0x0F0F0F0Fu, x.xs[2 * m], S);
+            S = sdot4((qlw[m] >> 4) & 0x0F0F0F0Fu, x.xs[2 * m + 1], S);
         }
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            H0 = sdot4((qhw[0] >> (2 * k)) & 0x03030303u, x.xs[8 + k], H0);
+            H1 = sdot4((qhw[1] >> (2 * k)) & 0x03030303u, x.xs[12 + k], H1);
+        }
+        S0 += 16 * H0;
+        S1 += 16 * H1;
     } else {
         const int h = c >> 2, p = c & 3, sh = 2 * (p >> 1);
         g0 = 8 * h + p;
@@ -299,7 +336,7 @@ __global__ __launch_bounds__(64 * WPB) void k_q6k_q8k_gemv_span(const uint8_t* _
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int row0 = (blockIdx.x * WPB + wave) * R;
     if (row0 >= M) return;
-    Q6X x[NT];
+    Q6X<ORDER> x[NT];
 #pragma unroll
     for (int t = 0; t < NT; t++) x[t] = load_q6x<ORDER>(xq + (int64_t)(8 * t + q) * kQ8KBytes, c);
     // rows past M repeat the last piece of row M-1 (their results are not stored)
