@@ -348,6 +348,24 @@ def main():
                                                  "frac_hbm": round(c1_bytes / c1_us / 1e3 / HBM_PEAK_GBS, 4),
                                                  "copies": len(g1)}
         del g1, w1, y1
+        # Q6_K x Q8_K (GGUF element map) at the 32,000 x 4096 head of a Q4_K_M model: random
+        # quant bytes with a finite f16 scale per block (seeded)
+        nq6 = 32000 * 16
+        q6 = synth.random_bytes(nq6 * 210, synth.key(42, 700)).reshape(nq6, 210)
+        q6[:, 208:210] = (np.abs(synth.normal_f32(nq6, synth.key(42, 701))) * 0.02).astype(np.float16) \
+            .view(np.uint8).reshape(nq6, 2)
+        w6 = torch.from_numpy(q6.reshape(-1)).to(dev)
+        g6 = [w6] + [w6.clone() for _ in range(-(-512 * 2**20 // w6.numel()) - 1)]
+        y6 = torch.empty(32000, dtype=torch.float32, device=dev)
+        torch.cuda.synchronize()
+        q6_us = T.us_per_launch([(lambda i=i: L.bpd_qmatmul_q6k_q8k_gguf_gpu(g6[i % len(g6)].data_ptr(), xq.data_ptr(),
+                                                                            y6.data_ptr(), 32000, 4096))
+                                 for i in range(400)])
+        q6_bytes = nq6 * 210 + X_BYTES + 32000 * 4
+        result["q6k_q8k_gemv_gguf_32000x4096"] = {"us": round(q6_us, 3), "gb_s": round(q6_bytes / q6_us / 1e3, 1),
+                                                  "frac_hbm": round(q6_bytes / q6_us / 1e3 / HBM_PEAK_GBS, 4),
+                                                  "copies": len(g6)}
+        del g6, w6, y6, q6
         for name, (rows, k) in Q80_SHAPES.items():
             W = torch.from_numpy(synth.q8_0(rows, k, synth.key(42, synth.STREAM[f"cfg2_{name}"]))).to(dev)
             n_c = max(16, -(-512 * 2**20 // W.numel()))
