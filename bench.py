@@ -1,5 +1,5 @@
 #!/usr/bin/env python3
-"""Benchmark of the MI355X quantized path at BASELINE.json's metric shape.
+"""Benchmark of the MI355X quantized path at the headline metric shape (Q4_K x Q8_K, 14336x4096).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
 
@@ -152,7 +152,7 @@ def cfg3_layers(torch, dev, synth, n_layers=32):
 
 
 def decode_chain(torch, L, T, dev, gpu, layers, acts, tokens=10):
-    """BASELINE cfg3: the GEMV portion of a 32-layer Mistral-7B-shaped decode step,
+    """cfg3: the GEMV portion of a 32-layer Mistral-7B-shaped decode step,
     Q4_K weights, activations N(0,1) -> Q8_K."""
     from bpd_substrate_amd import decode
 
@@ -183,7 +183,7 @@ def decode_chain(torch, L, T, dev, gpu, layers, acts, tokens=10):
 
 
 def decode_step(torch, L, T, dev, gpu, synth, layers, tokens=10, max_seq=4096, vocab=32000):
-    """BASELINE cfg3 as a whole decode step (bpd_llama_step_gpu): the chain's
+    """cfg3 as a whole decode step (bpd_llama_step_gpu): the chain's
     Q4_K weights plus RMSNorm, RoPE, the fp32 K/V cache, GQA attention,
     SwiGLU, a Q4_K head of `vocab` rows and argmax, one token at a time.
     Timed at short context (positions 0..tokens-1) and after 2048 cached rows."""
@@ -294,8 +294,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8 dot4 / fp32 (Q4_K x Q8_K)",
-        "data": "synthetic (seeded splitmix64 Q4_K blocks per BASELINE config; x ~ N(0,1) -> Q8_K)",
-        "config": {"workload": "Q4_K x Q8_K GEMV, M=14336, K=4096, batch 1 (BASELINE metric shape)",
+        "data": "synthetic (seeded splitmix64 Q4_K blocks per benchmark config; x ~ N(0,1) -> Q8_K)",
+        "config": {"workload": "Q4_K x Q8_K GEMV, M=14336, K=4096, batch 1 (the headline metric shape)",
                    "weight_copies": copies, "timing": "HIP graph of `steps` launches, events on its stream"},
         "pct_of_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",

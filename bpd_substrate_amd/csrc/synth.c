@@ -8,7 +8,7 @@
  * transcendental whose last bit may vary between CPUs or glibc ifunc variants
  * enters the data.  Build with -ffp-contract=off.
  *
- * Distributions (the BASELINE configs):
+ * Distributions (the benchmark configurations):
  *   Q4_K block: d = f16(|N(0, d_sigma)|), dmin = f16(|N(0, dmin_sigma)|),
  *               16 six-bit scales/mins uniform 0..63 packed into scales[12],
  *               128 bytes of nibbles uniform 0..15.

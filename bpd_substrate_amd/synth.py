@@ -13,7 +13,7 @@ from ._native import load_synth
 
 _N_THREADS = max(1, min(16, os.cpu_count() or 1))
 
-# sub-seed streams, one per BASELINE config role
+# sub-seed streams, one per benchmark configuration role
 STREAM = {
     "cfg0_w": 0, "cfg1_x": 1, "metric_w": 2, "metric_x": 3,
     "cfg2_up": 4, "cfg2_down": 5, "cfg2_x_up": 6, "cfg2_x_down": 7,

@@ -99,7 +99,7 @@ def test_round_trip(tmp_path, alignment):
 
 
 def test_exact_sizes_of_the_path_types():
-    assert gguf.tensor_nbytes((4096, 14336), gguf.Q4_K) == 33030144   # BASELINE metric shape
+    assert gguf.tensor_nbytes((4096, 14336), gguf.Q4_K) == 33030144   # the headline metric shape
     assert gguf.tensor_nbytes((4096, 14336), gguf.Q8_0) == 62390272   # cfg2
     assert gguf.tensor_nbytes((4096, 4096), gguf.Q6_K) == 4096 * 16 * 210
     with pytest.raises(gguf.GGUFError):

@@ -127,7 +127,7 @@ def test_llamafile_scalar_build_path(dev):
 
 
 def test_prefill_cfg4_full_size_matches_reference_hash(dev):
-    # BASELINE cfg4: W = cfg2 up (14336 x 4096), X = 512 x 4096 N(0,1) -> Q8_0; the expected
+    # cfg4: W = cfg2 up (14336 x 4096), X = 512 x 4096 N(0,1) -> Q8_0; the expected
     # SHA-256 is that of the reference's scalar-build dispatcher output (tests/golden/make_golden.py)
     import hashlib
     import json

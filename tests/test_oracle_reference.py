@@ -2,7 +2,7 @@
 
 1. Golden vectors (tests/golden/*.npz, written by tests/golden/make_golden.py
    from the reference C compiled from source): always run.
-2. SHA-256 of the reference's outputs at the BASELINE config sizes
+2. SHA-256 of the reference's outputs at the benchmark config sizes
    (tests/golden/hashes.json): always run.
 3. Direct comparison with oracle/_ref/*.so on fresh inputs, including the
    AVX1 sign/maddubs quirk on int8 = -128: run where oracle/_ref is built.
