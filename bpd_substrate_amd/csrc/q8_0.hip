@@ -955,6 +955,8 @@ __global__ __launch_bounds__(128 * RT) void k_q8_0_gemm_SH(const uint8_t* __rest
 
     uint32_t raw[17];
     const int nh = nb / kGH;
+    // the f16 scale operands: only element 0 changes per block, the zeros stay in place
+    h16x8 a16 = {}, b16[2] = {};
     half_load<RT>(raw, W, X, m0, n0, m_weight, m_tokens, 0, bpr);
     half_store<RT>(s, 0, raw);
     __syncthreads();
@@ -972,19 +974,17 @@ __global__ __launch_bounds__(128 * RT) void k_q8_0_gemm_SH(const uint8_t* __rest
             // fp32 form of the same product, v_mfma_f32_32x32x2f32, takes twice the
             // passes: 134 -> 123 us at cfg4.)
             const float av = __uint_as_float(__float_as_uint(s.da[slot][u][ra]) & kmask);
-            h16x8 a16 = {};
             a16[0] = (_Float16)av;  // exact: av is an f16 value or 0
 #pragma unroll
             for (int ct = 0; ct < 2; ct++) {
                 const int cb = wc * 64 + ct * 32 + col;
                 const i32x4 fb = *reinterpret_cast<const i32x4*>(&s.qb[slot][u][cb][16 * half]);
                 const float bv = __uint_as_float(__float_as_uint(s.db[slot][u][cb]) & kmask);
-                h16x8 b16 = {};
-                b16[0] = (_Float16)bv;
+                b16[ct][0] = (_Float16)bv;
                 const i32x16 zero = {0};
                 const f32x16 fzero = {0.0f};
                 const i32x16 sb = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa, fb, zero, 0, 0, 0);
-                const f32x16 delta = __builtin_amdgcn_mfma_f32_32x32x16_f16(a16, b16, fzero, 0, 0, 0);
+                const f32x16 delta = __builtin_amdgcn_mfma_f32_32x32x16_f16(a16, b16[ct], fzero, 0, 0, 0);
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
                     const float prod = (float)sb[r] * delta[r];
