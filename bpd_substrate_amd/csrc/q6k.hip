@@ -386,7 +386,81 @@ __global__ __launch_bounds__(64 * WPB) void k_q6k_q8k_gemv_span(const uint8_t* _
     }
 }
 
+// K = 14336 (56 super-blocks): one row per wave (735 pieces, 12 loads per lane)
+// in the same 8-block passes.  The x operands of 7 passes would not fit the
+// registers, so the workgroup first copies the Q8_K vector (16,352 bytes) into
+// LDS: its loads are issued before the span loads, the copy and one barrier
+// follow, and each pass reads its x operands from LDS.
+template <int ORDER, int WPB>
+__global__ __launch_bounds__(64 * WPB) void k_q6k_q8k_gemv_span_long(const uint8_t* __restrict__ w,
+                                                                    const uint8_t* __restrict__ xq,
+                                                                    float* __restrict__ y, int M) {
+    constexpr int NB = 56, NT = NB / 8;
+    constexpr int kPieces = NB * kQ6KBytes / 16;  // 735
+    constexpr int kLoads = (kPieces + 63) / 64;   // 12
+    constexpr int XD = NB * kQ8KBytes / 4;        // 4,088 dwords of x
+    constexpr int XU = (XD + 64 * WPB - 1) / (64 * WPB);
+    __shared__ __align__(16) uint8_t bufs[WPB][kQ6Buf];
+    __shared__ __align__(16) uint32_t xl[XD];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int q = lane >> 3, c = lane & 7;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int row = blockIdx.x * WPB + wave;
+    const bool has = row < M;
+    uint32_t xv[XU];
+#pragma unroll
+    for (int u = 0; u < XU; u++) xv[u] = reinterpret_cast<const uint32_t*>(xq)[min(tid + 64 * WPB * u, XD - 1)];
+    // waves past the last row read row M-1 (nothing is stored for them)
+    const uint8_t* span = w + (int64_t)(has ? row : M - 1) * (NB * kQ6KBytes);
+    q6u32x4 v[kLoads];
+#pragma unroll
+    for (int u = 0; u < kLoads; u++) {
+        const uint32_t p = (uint32_t)min(lane + 64 * u, kPieces - 1);
+        v[u] = __builtin_nontemporal_load(reinterpret_cast<const q6u32x4*>(span + 16u * p));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < XU; u++)
+        if (tid + 64 * WPB * u < XD) xl[tid + 64 * WPB * u] = xv[u];
+    __syncthreads();
+    if (!has) return;
+    uint8_t* buf = bufs[wave];
+    const uint8_t* xs = reinterpret_cast<const uint8_t*>(xl);
+    float s = 0.0f;
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        const int p0 = 8 * t * kQ6KBytes / 16, n = kQ6Pass / 16;
+#pragma unroll
+        for (int u = 0; u < kLoads; u++) {
+            if (64 * u + 63 < p0 || 64 * u >= p0 + n) continue;
+            const int k = lane + 64 * u - p0;
+            if (k >= 0 && k < n) *reinterpret_cast<q6u32x4*>(buf + 16 * k) = v[u];
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        const Q6X<ORDER> x = load_q6x<ORDER>(xs + (8 * t + q) * kQ8KBytes, c);
+        const uint8_t* blk = buf + q * kQ6KBytes;
+        int isum = q6k_lane_isum_lds<ORDER>(blk, x, c);
+        isum = sum8_i(isum);
+        uint16_t dh;
+        __builtin_memcpy(&dh, blk + 208, 2);
+        s = s + (f16_ieee(dh) * x.dy) * (float)isum;
+    }
+    s = s + dpp_f<0x140>(s);
+    const float p01 = readlane_f(s, 0), p23 = readlane_f(s, 16);
+    const float p45 = readlane_f(s, 32), p67 = readlane_f(s, 48);
+    if (lane == 0) y[row] = (p01 + p23) + (p45 + p67);
+}
+
 void launch_qmatmul_q6k_q8k(const uint8_t* w, const uint8_t* xq, float* y, int M, int K, int order, hipStream_t s) {
+    if (K == 14336 && (reinterpret_cast<uintptr_t>(w) & 15) == 0) {
+        constexpr int WPB = 8;
+        const dim3 grid((M + WPB - 1) / WPB);
+        if (order == 0)
+            hipLaunchKernelGGL((k_q6k_q8k_gemv_span_long<0, WPB>), grid, dim3(64 * WPB), 0, s, w, xq, y, M);
+        else
+            hipLaunchKernelGGL((k_q6k_q8k_gemv_span_long<1, WPB>), grid, dim3(64 * WPB), 0, s, w, xq, y, M);
+        return;
+    }
     if (K == 4096 && (reinterpret_cast<uintptr_t>(w) & 15) == 0) {
         constexpr int WPB = 4;
         const int waves = (M + 1) / 2;
