@@ -70,31 +70,83 @@ struct Check {
     }
 };
 
-// Device workspace for the quantized activations of the llamafile path (the
-// reference mallocs it per call, bench/bpd_cpu.c:4441).  Grown on demand;
-// calls that overlap on different streams must not share it.
-std::mutex g_ws_mu;
-void* g_ws = nullptr;
-size_t g_ws_bytes = 0;
+// Device workspaces for the quantized activations of the fp32-input entry
+// points (the reference mallocs one per call, bench/bpd_cpu.c:4300,4441).
+// There is one per (device, stream): calls on one stream run in order and may
+// share a buffer, calls on different streams get different buffers.  A caller
+// keeps the entry locked (WsLease) from its request until its launches are
+// enqueued, so two host threads on one stream cannot interleave their quantize
+// and GEMM launches over one buffer.  A buffer is replaced only when a request
+// outgrows it: the stream is drained first (only that stream uses it), so no
+// pending launch reads freed memory.  Inside graph capture nothing is
+// allocated or drained: a request that does not fit fails with
+// BPDQ_ERR_CAPTURE (run the call once outside capture first).
+struct WsEntry {
+    int dev;
+    hipStream_t stream;
+    std::mutex mu;
+    void* p = nullptr;
+    size_t bytes = 0;
+};
+std::mutex g_ws_table_mu;
+WsEntry* g_ws_table[64];
+int g_ws_count = 0;
 
-void* workspace(size_t bytes, const char* fn) {
-    std::lock_guard<std::mutex> lk(g_ws_mu);
-    if (bytes <= g_ws_bytes) return g_ws;
-    if (g_ws) {
-        if (!hip_ok(hipDeviceSynchronize(), fn)) return nullptr;
-        (void)hipFree(g_ws);
-        g_ws = nullptr;
-        g_ws_bytes = 0;
-    }
-    if (hipMalloc(&g_ws, bytes) != hipSuccess) {
-        (void)hipGetLastError();
-        set_err(BPDQ_ERR_ALLOC, fn, "workspace allocation failed");
-        g_ws = nullptr;
+WsEntry* ws_entry(int dev, hipStream_t s, const char* fn) {
+    std::lock_guard<std::mutex> lk(g_ws_table_mu);
+    for (int i = 0; i < g_ws_count; i++)
+        if (g_ws_table[i]->dev == dev && g_ws_table[i]->stream == s) return g_ws_table[i];
+    if (g_ws_count == (int)(sizeof g_ws_table / sizeof g_ws_table[0])) {
+        set_err(BPDQ_ERR_ALLOC, fn, "more than 64 (device, stream) workspaces");
         return nullptr;
     }
-    g_ws_bytes = bytes;
-    return g_ws;
+    WsEntry* e = new WsEntry;  // lives until the process ends
+    e->dev = dev;
+    e->stream = s;
+    g_ws_table[g_ws_count++] = e;
+    return e;
 }
+
+}  // namespace
+
+namespace bpdq {
+WsLease workspace(size_t bytes, hipStream_t s, const char* fn) {
+    WsLease L;
+    int dev = 0;
+    if (!hip_ok(hipGetDevice(&dev), fn)) return L;
+    WsEntry* e = ws_entry(dev, s, fn);
+    if (!e) return L;
+    L.lock = std::unique_lock<std::mutex>(e->mu);
+    if (bytes <= e->bytes) {
+        L.ptr = e->p;
+        return L;
+    }
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (!hip_ok(hipStreamIsCapturing(s, &cs), fn)) return L;
+    if (cs != hipStreamCaptureStatusNone) {
+        set_err(BPDQ_ERR_CAPTURE, fn, "the workspace must grow, which cannot happen during stream capture");
+        return L;
+    }
+    if (e->p) {
+        if (!hip_ok(hipStreamSynchronize(s), fn)) return L;
+        (void)hipFree(e->p);
+        e->p = nullptr;
+        e->bytes = 0;
+    }
+    const size_t want = (bytes + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);  // whole MiB
+    if (hipMalloc(&e->p, want) != hipSuccess) {
+        (void)hipGetLastError();
+        set_err(BPDQ_ERR_ALLOC, fn, "workspace allocation failed");
+        e->p = nullptr;
+        return L;
+    }
+    e->bytes = want;
+    L.ptr = e->p;
+    return L;
+}
+}  // namespace bpdq
+
+namespace {
 
 void dequant_q4k(const uint8_t* q, float* out, int nb, int order, const char* fn) {
     Check c(fn);
@@ -193,7 +245,8 @@ void fused(const uint8_t* const* w_list, float* const* y_list, const int* M_list
     } else if (K <= bpdq::fused_max_k()) {
         bpdq::launch_qmatmul_q4k_fused_multi(w_list, y_list, M_list, n, x, K, 0, g_stream);
     } else {
-        uint8_t* xq = static_cast<uint8_t*>(workspace((size_t)(K / 256) * 292, fn));
+        bpdq::WsLease ws = bpdq::workspace((size_t)(K / 256) * 292, g_stream, fn);
+        uint8_t* xq = static_cast<uint8_t*>(ws.ptr);
         if (!xq) return;
         bpdq::launch_quant_q8k(x, xq, K, g_stream);
         bpdq::launch_qmatmul_q4k_q8k_multi(w_list, y_list, M_list, n, xq, K, 0, g_stream);
@@ -412,9 +465,11 @@ void bpd_qmatmul_q8_0_llamafile_gpu(const uint8_t* W, const float* X, float* out
     if (K > 0) c.ptr(W, 1, "W_q8_0").ptr(X, 4, "X_f32");
     if (!c.ok) return;
     const size_t xq_bytes = (size_t)m_tokens * (size_t)(K / 32) * 34;
+    bpdq::WsLease ws;
     uint8_t* xq = nullptr;
     if (xq_bytes > 0) {
-        xq = static_cast<uint8_t*>(workspace(xq_bytes, fn));
+        ws = bpdq::workspace(xq_bytes, g_stream, fn);
+        xq = static_cast<uint8_t*>(ws.ptr);
         if (!xq) return;
         // K % 32 == 0, so the flat m_tokens*K array quantizes to the same blocks as row by row.
         bpdq::launch_quant_q8_0(X, xq, (int64_t)m_tokens * K, g_stream);
@@ -433,7 +488,7 @@ void bpd_qmatmul_q8_0_dispatch_s_gpu(const uint8_t* Wq, const uint8_t* Xq, float
     c.ptr(out, 4, "out");
     if (K > 0) c.ptr(Wq, 1, "W_q8_0").ptr(Xq, 1, "X_q8_0");
     if (!c.ok) return;
-    bpdq::launch_q8_0_gemm_S(Wq, Xq, out, m_weight, m_tokens, K, g_stream);
+    bpdq::launch_q8_0_gemm_S(Wq, Xq, out, m_weight, m_tokens, K, 0, g_stream);
     check_launch(fn);
 }
 
@@ -447,13 +502,15 @@ void bpd_qmatmul_q8_0_llamafile_s_gpu(const uint8_t* W, const float* X, float* o
     if (K > 0) c.ptr(W, 1, "W_q8_0").ptr(X, 4, "X_f32");
     if (!c.ok) return;
     const size_t xq_bytes = (size_t)m_tokens * (size_t)(K / 32) * 34;
+    bpdq::WsLease ws;
     uint8_t* xq = nullptr;
     if (xq_bytes > 0) {
-        xq = static_cast<uint8_t*>(workspace(xq_bytes, fn));
+        ws = bpdq::workspace(xq_bytes, g_stream, fn);
+        xq = static_cast<uint8_t*>(ws.ptr);
         if (!xq) return;
         bpdq::launch_quant_q8_0(X, xq, (int64_t)m_tokens * K, g_stream);
     }
-    bpdq::launch_q8_0_gemm_S(W, xq, out, m_weight, m_tokens, K, g_stream);
+    bpdq::launch_q8_0_gemm_S(W, xq, out, m_weight, m_tokens, K, 1, g_stream);
     check_launch(fn);
 }
 

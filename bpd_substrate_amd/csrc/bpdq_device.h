@@ -28,6 +28,57 @@ __device__ __forceinline__ float f16_h2h(uint32_t h) {
     return f16_ieee(h);
 }
 
+// ---- NaN bits of the reference builds ---------------------------------------
+// The reference's C runs on x86: an SSE operation gives a NaN operand back
+// quieted (the first operand's when both are NaN) and the default NaN
+// 0xFFC00000 for an invalid operation (Inf*0, Inf-Inf).  Its CUDA kernels run on
+// NVIDIA GPUs, whose fp32 operations return the canonical NaN 0x7FFFFFFF.  The
+// kernels below compute as usual and, only where the result is NaN (which the
+// IEEE rules make NaN on every machine alike), select those bits.
+constexpr uint32_t kX86NaN = 0xFFC00000u;
+constexpr uint32_t kCudaNaN = 0x7FFFFFFFu;
+
+__device__ __forceinline__ bool f16_is_nan(uint32_t h) { return (h & 0x7FFFu) > 0x7C00u; }
+__device__ __forceinline__ bool f16_is_inf(uint32_t h) { return (h & 0x7FFFu) == 0x7C00u; }
+__device__ __forceinline__ bool f16_exp31(uint32_t h) { return (h & 0x7C00u) == 0x7C00u; }
+
+// An f16 NaN as the magic-number decode of /root/reference/bench/bpd_cpu.c:3928-3958
+// leaves it after a multiply: sign, the payload shifted up, the quiet bit set.
+__device__ __forceinline__ float f16_nan_x86(uint32_t h) {
+    return __uint_as_float(((h & 0x8000u) << 16) | 0x7FC00000u | ((h & 0x3FFu) << 13));
+}
+
+// x86 result bits of a binary operation r = first OP second whose result is NaN.
+__device__ __forceinline__ float x86_nan_of(float first, float second) {
+    if (__builtin_isnan(first)) return __uint_as_float(__float_as_uint(first) | 0x400000u);
+    if (__builtin_isnan(second)) return __uint_as_float(__float_as_uint(second) | 0x400000u);
+    return __uint_as_float(kX86NaN);
+}
+
+// Bits of a NaN Q4_K element y = RN(d*sc*q - dmin*m) as the reference computes it
+// on x86 (/root/reference/bench/bpd_quant.c:25-38,64-71): half_to_float turns an
+// f16 NaN into +/-0x7FC00000 without payload; d*sc and then *q propagate d's NaN
+// or make the default NaN from Inf*0; the subtraction keeps the left NaN, else
+// dmin*m's.  So y's NaN is positive only when it comes from a positive NaN d, or,
+// with no NaN on the left, from a positive NaN dmin.  hd, hm: the f16 bits of d
+// and dmin.  Returns y unchanged when it is not NaN.
+__device__ __forceinline__ float q4k_bpd_nan(float y, uint32_t hd, uint32_t hm, int sc, uint32_t q) {
+    if (!__builtin_isnan(y)) return y;
+    bool pos;
+    if (f16_is_nan(hd)) pos = (hd & 0x8000u) == 0;
+    else if (f16_is_inf(hd) && (sc == 0 || q == 0)) pos = false;
+    else pos = f16_is_nan(hm) && (hm & 0x8000u) == 0;
+    return __uint_as_float(pos ? 0x7FC00000u : kX86NaN);
+}
+
+// A NaN product d*c (c an integer-valued fp32, d decoded by the magic-number
+// form): d's NaN quieted, else (Inf*0) the default NaN.  Q8_0 dequant
+// (/root/reference/bench/bpd_cpu.c:3960-3973) and Q6_K dequant.
+__device__ __forceinline__ float mul_nan_x86(float y, uint32_t hd) {
+    if (!__builtin_isnan(y)) return y;
+    return f16_is_nan(hd) ? f16_nan_x86(hd) : __uint_as_float(kX86NaN);
+}
+
 // 6-bit scale and min of sub-block j from the 12 scale bytes held in three
 // dwords s0 = bytes 0..3, s1 = bytes 4..7, s2 = bytes 8..11
 // (layout of /root/reference/bench/bpd_quant.c:56-62):

@@ -5,7 +5,20 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 namespace bpdq {
+
+// A device workspace of at least the requested size for launches on stream s,
+// locked for the caller until the lease is destroyed (after its launches are
+// enqueued).  ptr is nullptr, with the error recorded, when it cannot be had:
+// allocation failure, or growth requested during stream capture
+// (BPDQ_ERR_CAPTURE).
+struct WsLease {
+    std::unique_lock<std::mutex> lock;
+    void* ptr = nullptr;
+};
+WsLease workspace(size_t bytes, hipStream_t s, const char* fn);
 
 // Error recording (read back with bpd_gpu_last_error) and the launch stream of
 // the exported ABI, for entry points defined outside abi.hip.
@@ -46,8 +59,10 @@ void launch_q8_pad64(const float* x, uint8_t* out, int N, int K, hipStream_t s);
 void launch_q8_pad64_dispatch_T(const uint8_t* Wp, const uint8_t* Xq, float* out, int m_weight, int m_tokens, int K,
                                 hipStream_t s);
 
+// nan_mode: which reference form's NaN bits the NaN cells take: 0 = the scalar
+// tiles of the dispatcher, 1 = bpd_qdot_q8_0_q8_0_cpu (the scalar build's llamafile).
 void launch_q8_0_gemm_S(const uint8_t* Wq, const uint8_t* Xq, float* out, int m_weight, int m_tokens, int K,
-                        hipStream_t s);
+                        int nan_mode, hipStream_t s);
 void launch_stream_read(const uint8_t* p, int64_t n16, uint32_t* sink, hipStream_t s);
 
 }  // namespace bpdq

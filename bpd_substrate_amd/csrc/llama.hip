@@ -763,31 +763,6 @@ void rope_table(RopeTab& t, int pos, int head_dim, float base) {
     }
 }
 
-// Device workspace of the quantized activations (Q8_0 rows, or Q8_K when a Q4_K
-// GEMV is too long for the fused kernel).  Grown on demand.
-std::mutex g_ws_mu;
-void* g_ws = nullptr;
-size_t g_ws_bytes = 0;
-
-uint8_t* step_workspace(size_t bytes, const char* fn) {
-    std::lock_guard<std::mutex> lk(g_ws_mu);
-    if (bytes <= g_ws_bytes) return static_cast<uint8_t*>(g_ws);
-    if (g_ws) {
-        if (!abi_hip_ok(hipDeviceSynchronize(), fn)) return nullptr;
-        (void)hipFree(g_ws);
-        g_ws = nullptr;
-        g_ws_bytes = 0;
-    }
-    if (hipMalloc(&g_ws, bytes) != hipSuccess) {
-        (void)hipGetLastError();
-        abi_error(BPDQ_ERR_ALLOC, fn, "workspace allocation failed");
-        g_ws = nullptr;
-        return nullptr;
-    }
-    g_ws_bytes = bytes;
-    return static_cast<uint8_t*>(g_ws);
-}
-
 struct V {
     const char* fn;
     bool ok = true;
@@ -1033,7 +1008,10 @@ bool enqueue_step(int fmt, const LayerWeights* layers, const ModelConfig* cfg, c
     const size_t xk_bytes = !q8 && g.E <= 4096 ? ((size_t)(g.E / 256) * kQ8KBytes + 255) & ~(size_t)255 : 0;
     const size_t q8k_end = ((front + q8k + 255) & ~(size_t)255) + xk_bytes;
     const size_t sc_bytes = (size_t)g.H * cfg->max_seq * 4;
-    uint8_t* ws = step_workspace(q8k_end + sc_bytes, fn);
+    // the quantized activations (Q8_0 rows, or Q8_K when a Q4_K GEMV is too long for
+    // the fused kernel) and the attention scores, in the stream's workspace
+    const WsLease lease = workspace(q8k_end + sc_bytes, abi_stream(), fn);
+    uint8_t* ws = static_cast<uint8_t*>(lease.ptr);
     if (ws == nullptr) return false;
     const Gemv gemv{fmt, ws + front, abi_stream()};
     c.cfg = cfg;

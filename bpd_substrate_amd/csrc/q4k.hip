@@ -56,6 +56,23 @@ __global__ __launch_bounds__(256) void k_dequant_q4k(const uint8_t* __restrict__
     v.y = fmaf(s, (float)((nib >> 8) & 0xFFu), -mn);
     v.z = fmaf(s, (float)((nib >> 16) & 0xFFu), -mn);
     v.w = fmaf(s, (float)(nib >> 24), -mn);
+    // Inf or NaN d / dmin (one wave = one block, so the test is uniform): give NaN
+    // results the reference's bits (x86 rules for the bpd map, the CUDA kernel's
+    // canonical NaN for the GGUF map).
+    const uint32_t h = __builtin_amdgcn_readfirstlane(hdr.x);
+    if (f16_exp31(h) || f16_exp31(h >> 16)) {
+        if (ORDER == 0) {
+            v.x = q4k_bpd_nan(v.x, h & 0xFFFFu, h >> 16, sc, nib & 0xFFu);
+            v.y = q4k_bpd_nan(v.y, h & 0xFFFFu, h >> 16, sc, (nib >> 8) & 0xFFu);
+            v.z = q4k_bpd_nan(v.z, h & 0xFFFFu, h >> 16, sc, (nib >> 16) & 0xFFu);
+            v.w = q4k_bpd_nan(v.w, h & 0xFFFFu, h >> 16, sc, nib >> 24);
+        } else {
+            v.x = __builtin_isnan(v.x) ? __uint_as_float(kCudaNaN) : v.x;
+            v.y = __builtin_isnan(v.y) ? __uint_as_float(kCudaNaN) : v.y;
+            v.z = __builtin_isnan(v.z) ? __uint_as_float(kCudaNaN) : v.z;
+            v.w = __builtin_isnan(v.w) ? __uint_as_float(kCudaNaN) : v.w;
+        }
+    }
     __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(out + b * 256 + 4 * lane));
 }
 
@@ -65,6 +82,39 @@ void launch_dequant_q4k(const uint8_t* q, float* out, int n_blocks, int order, h
         hipLaunchKernelGGL(k_dequant_q4k<0>, grid, dim3(256), 0, s, q, out, n_blocks);
     else
         hipLaunchKernelGGL(k_dequant_q4k<1>, grid, dim3(256), 0, s, q, out, n_blocks);
+}
+
+// The x86 bits of a row of the reference-order GEMV whose sum came out NaN.  On
+// x86 the first NaN of the chain sticks: sum + p keeps sum's NaN, w*x keeps w's
+// (the reference build puts the weight first), and an invalid operation gives
+// the default NaN.  So the row's bits are those of its first NaN event, found by
+// running the chain again with those rules.  Called only for NaN rows.
+__device__ __noinline__ float chain_nan_bits(const uint8_t* __restrict__ rp, const float* __restrict__ x, int nb) {
+    float sum = 0.0f;
+    for (int b = 0; b < nb; b++) {
+        const uint8_t* blk = rp + (int64_t)b * kQ4KBytes;
+        const uint4 hdr = ld_u128(blk);
+        const float d = f16_ieee(hdr.x), dmin = f16_ieee(hdr.x >> 16);
+        const float* xb = x + (int64_t)b * 256;
+        for (int j = 0; j < 8; j++) {
+            int sc, m;
+            q4k_scale_min(hdr.y, hdr.z, hdr.w, j, sc, m);
+            const float scale = d * (float)sc, mn = dmin * (float)m;
+            const uint4 qv = ld_u128(blk + 16 + 16 * j);
+            const uint32_t qd[4] = {qv.x, qv.y, qv.z, qv.w};
+            for (int k = 0; k < 32; k++) {
+                const uint32_t q = (qd[(k & 15) >> 2] >> (8 * (k & 3) + (k >= 16 ? 4 : 0))) & 15u;
+                const float w = q4k_bpd_nan(fmaf(scale, (float)q, -mn), hdr.x & 0xFFFFu, hdr.x >> 16, sc, q);
+                const float xv = xb[32 * j + k];
+                float p = w * xv;
+                if (__builtin_isnan(p)) p = x86_nan_of(w, xv);
+                const float t = sum + p;
+                if (__builtin_isnan(t)) return x86_nan_of(sum, p);
+                sum = t;
+            }
+        }
+    }
+    return sum;
 }
 
 // ----------------------------------------------------------------------------
@@ -102,7 +152,7 @@ __global__ __launch_bounds__(64) void k_qmatmul_q4k_chain(const uint8_t* __restr
             }
         }
     }
-    y[row] = sum;
+    y[row] = __builtin_isnan(sum) ? chain_nan_bits(rp, x, nb) : sum;
 }
 
 void launch_qmatmul_q4k_chain(const uint8_t* w, const float* x, float* y, int M, int K, hipStream_t s) {

@@ -67,13 +67,22 @@ __global__ __launch_bounds__(256) void k_dequant_q6k(const uint8_t* __restrict__
         const uint32_t qh4 = ld_u32(blk + 128 + 32 * h + idx);
         qb = q6_bytes(ql4 >> (4 * (quarter >> 1)), qh4 >> (2 * quarter));
     }
-    const float d = f16_ieee(ld_u16g(blk + 208));
+    const uint32_t hd = ld_u16g(blk + 208);
+    const float d = f16_ieee(hd);
     const float ds = d * (float)(int8_t)blk[192 + (lane >> 2)];
     f32x4q6 v;
     v.x = ds * (float)((int)(qb & 0xFFu) - 32);
     v.y = ds * (float)((int)((qb >> 8) & 0xFFu) - 32);
     v.z = ds * (float)((int)((qb >> 16) & 0xFFu) - 32);
     v.w = ds * (float)((int)(qb >> 24) - 32);
+    // Inf or NaN d (uniform per wave): NaN results take the x86 bits of the
+    // reference's (d*sc)*q (numpy float32 for ORDER 0, llama.cpp's C for ORDER 1)
+    if (f16_exp31(__builtin_amdgcn_readfirstlane(hd))) {
+        v.x = mul_nan_x86(v.x, hd);
+        v.y = mul_nan_x86(v.y, hd);
+        v.z = mul_nan_x86(v.z, hd);
+        v.w = mul_nan_x86(v.w, hd);
+    }
     __builtin_nontemporal_store(v, reinterpret_cast<f32x4q6*>(out + b * 256 + 4 * lane));
 }
 

@@ -25,8 +25,8 @@ __global__ __launch_bounds__(256) void k_dequant_q8_0(const uint8_t* __restrict_
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= n_elems) return;
     const uint8_t* blk = raw + (i >> 5) * kQ80Bytes;
-    const float d = f16_ieee((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
-    out[i] = (float)(int8_t)blk[2 + (i & 31)] * d;
+    const uint32_t hd = (uint32_t)blk[0] | ((uint32_t)blk[1] << 8);
+    out[i] = mul_nan_x86((float)(int8_t)blk[2 + (i & 31)] * f16_ieee(hd), hd);
 }
 
 void launch_dequant_q8_0(const uint8_t* raw, float* out, int n_blocks, hipStream_t s) {
@@ -41,8 +41,8 @@ __global__ __launch_bounds__(256) void k_embed_q8_0(const uint8_t* __restrict__ 
     if (e >= embed_dim) return;
     const int64_t bpr = embed_dim / 32;
     const uint8_t* blk = table + ((int64_t)ids[t] * bpr + (e >> 5)) * kQ80Bytes;
-    const float d = f16_ieee((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
-    out[(int64_t)t * embed_dim + e] = (float)(int8_t)blk[2 + (e & 31)] * d;
+    const uint32_t hd = (uint32_t)blk[0] | ((uint32_t)blk[1] << 8);
+    out[(int64_t)t * embed_dim + e] = mul_nan_x86((float)(int8_t)blk[2 + (e & 31)] * f16_ieee(hd), hd);
 }
 
 void launch_embed_q8_0(const uint8_t* table, const int32_t* ids, float* out, int n_tokens, int embed_dim,
@@ -738,6 +738,57 @@ typedef int i32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef _Float16 h16x8 __attribute__((ext_vector_type(8)));
 
+// ----------------------------------------------------------------------------
+// NaN cells of the scalar order S.  The reference computes
+//   acc = acc + float(S_b) * (Ad*Bd)   over blocks b in order
+// on x86, where the first NaN of the chain sticks (acc + p keeps acc's NaN), a
+// NaN factor comes out quieted (the first operand's when both are NaN) and
+// Inf*0, Inf-Inf give the default NaN.  Two reference forms differ in their NaN
+// bits:
+//   kSNanTile (the scalar tiles, bench/bpd_gemm_q8_0_cpu.c:112-128): scales by
+//     the ldexpf decode of :13-26 (an f16 NaN becomes +/-0x7FC00000, no payload);
+//     the build puts Bd first in Ad*Bd;
+//   kSNanQdot (bpd_qdot_q8_0_q8_0_cpu's scalar form, bench/bpd_cpu.c:4263-4280,
+//     which the scalar build's llamafile entry uses): the magic-number decode
+//     (payload kept); the weight scale first.
+// A finite scale product keeps a finite accumulator finite (|S_b*Ad*Bd| < 2^51)
+// and an infinite one unchanged, so only blocks with an Inf or NaN scale can
+// change the state, and the first NaN event fixes the bits.  Called only for a
+// cell whose sum came out NaN; NaN-ness itself is the same on every IEEE machine.
+// ----------------------------------------------------------------------------
+constexpr int kSNanTile = 0;
+constexpr int kSNanQdot = 1;
+
+__device__ __forceinline__ float f16_ref(uint32_t h, int mode) {
+    if (!f16_is_nan(h)) return f16_ieee(h);
+    return mode == kSNanTile ? __uint_as_float(((h & 0x8000u) << 16) | 0x7FC00000u) : f16_nan_x86(h);
+}
+
+__device__ __noinline__ float s_order_nan_bits(const uint8_t* __restrict__ wrow, const uint8_t* __restrict__ xrow,
+                                               int nb, int mode) {
+    float acc = 0.0f;  // stands for any finite value
+    for (int b = 0; b < nb; b++) {
+        const uint8_t* wb = wrow + (int64_t)b * kQ80Bytes;
+        const uint8_t* xb = xrow + (int64_t)b * kQ80Bytes;
+        const uint32_t hw = (uint32_t)wb[0] | ((uint32_t)wb[1] << 8);
+        const uint32_t hx = (uint32_t)xb[0] | ((uint32_t)xb[1] << 8);
+        if (!f16_exp31(hw) && !f16_exp31(hx)) continue;
+        const float fw = f16_ref(hw, mode), fx = f16_ref(hx, mode);
+        const float first = mode == kSNanTile ? fx : fw, second = mode == kSNanTile ? fw : fx;
+        const float delta = first * second;
+        // a NaN product: p = float(S_b) * delta is delta's NaN, and acc + p is p's
+        if (__builtin_isnan(delta)) return x86_nan_of(first, second);
+        // delta is +/-Inf: p = +/-Inf, or the default NaN when S_b = 0
+        int sumi = 0;
+        for (int j = 0; j < 32; j++) sumi += (int)(int8_t)wb[2 + j] * (int)(int8_t)xb[2 + j];
+        if (sumi == 0) return __uint_as_float(kX86NaN);
+        const float p = sumi < 0 ? -delta : delta;
+        if (__builtin_isinf(acc) && acc != p) return __uint_as_float(kX86NaN);  // Inf - Inf
+        acc = p;
+    }
+    return acc;
+}
+
 constexpr int kGT = 128;  // tile rows = tile tokens
 constexpr int kGB = 4;    // blocks per LDS stage
 
@@ -792,7 +843,8 @@ __device__ __forceinline__ void stage_store(GemmLds& s, int buf, const BlkRegs (
 }
 
 __global__ __launch_bounds__(256) void k_q8_0_gemm_S(const uint8_t* __restrict__ W, const uint8_t* __restrict__ X,
-                                                     float* __restrict__ out, int m_weight, int m_tokens, int nb) {
+                                                     float* __restrict__ out, int m_weight, int m_tokens, int nb,
+                                                     int nan_mode) {
     __shared__ GemmLds s;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -868,7 +920,10 @@ __global__ __launch_bounds__(256) void k_q8_0_gemm_S(const uint8_t* __restrict__
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int row = m0 + wr * 64 + rt * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-                if (row < m_weight) out[(int64_t)tok * m_weight + row] = acc[rt][ct][r];
+                if (row >= m_weight) continue;
+                float v = acc[rt][ct][r];
+                if (__builtin_isnan(v)) v = s_order_nan_bits(W + row * bpr, X + tok * bpr, nb, nan_mode);
+                out[(int64_t)tok * m_weight + row] = v;
             }
         }
 }
@@ -936,7 +991,7 @@ __device__ __forceinline__ void half_store(GemmLdsH<RT>& s, int slot, const uint
 template <int RT>
 __global__ __launch_bounds__(128 * RT) void k_q8_0_gemm_SH(const uint8_t* __restrict__ W,
                                                            const uint8_t* __restrict__ X, float* __restrict__ out,
-                                                           int m_weight, int m_tokens, int nb) {
+                                                           int m_weight, int m_tokens, int nb, int nan_mode) {
     __shared__ GemmLdsH<RT> s;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -1003,6 +1058,17 @@ __global__ __launch_bounds__(128 * RT) void k_q8_0_gemm_SH(const uint8_t* __rest
     for (int ct = 0; ct < 2; ct++) {
         const int tok = n0 + wc * 64 + ct * 32 + col;
         if (tok >= m_tokens) continue;
+        // NaN cells take the reference's bits (rare: only Inf / NaN scales make them)
+        bool any_nan = false;
+#pragma unroll
+        for (int r = 0; r < 16; r++) any_nan |= __builtin_isnan(acc[ct][r]);
+        if (any_nan) {
+            for (int r = 0; r < 16; r++) {
+                const int row = m0 + wr * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+                if (row < m_weight && __builtin_isnan(acc[ct][r]))
+                    acc[ct][r] = s_order_nan_bits(W + row * bpr, X + tok * bpr, nb, nan_mode);
+            }
+        }
         float* o = out + (int64_t)tok * m_weight + m0 + wr * 32 + 4 * half;
         if (full_rows) {
 #pragma unroll
@@ -1020,7 +1086,7 @@ __global__ __launch_bounds__(128 * RT) void k_q8_0_gemm_SH(const uint8_t* __rest
 }
 
 void launch_q8_0_gemm_S(const uint8_t* Wq, const uint8_t* Xq, float* out, int m_weight, int m_tokens, int K,
-                        hipStream_t s) {
+                        int nan_mode, hipStream_t s) {
     if (K / 32 == 0) {  // the kernel indexes block nb-1
         launch_fill_zero(out, (int64_t)m_weight * m_tokens, s);
         return;
@@ -1029,13 +1095,14 @@ void launch_q8_0_gemm_S(const uint8_t* Wq, const uint8_t* Xq, float* out, int m_
     const bool aligned = K % 128 == 0 && (reinterpret_cast<uintptr_t>(Wq) & 3) == 0 &&
                          (reinterpret_cast<uintptr_t>(Xq) & 3) == 0;
     if (!aligned) {
-        hipLaunchKernelGGL(k_q8_0_gemm_S, grid, dim3(256), 0, s, Wq, Xq, out, m_weight, m_tokens, K / 32);
+        hipLaunchKernelGGL(k_q8_0_gemm_S, grid, dim3(256), 0, s, Wq, Xq, out, m_weight, m_tokens, K / 32, nan_mode);
         return;
     }
     // 128 weight rows per workgroup, two 512-thread workgroups per CU.  (224 rows,
     // one 896-thread workgroup per CU, balances cfg4's 14336 rows over 256 CUs
     // exactly but measured slower: 150.9 us vs 146.)
-    hipLaunchKernelGGL(k_q8_0_gemm_SH<4>, grid, dim3(512), 0, s, Wq, Xq, out, m_weight, m_tokens, K / 32);
+    hipLaunchKernelGGL(k_q8_0_gemm_SH<4>, grid, dim3(512), 0, s, Wq, Xq, out, m_weight, m_tokens, K / 32,
+                       nan_mode);
 }
 
 }  // namespace bpdq

@@ -44,7 +44,7 @@ TYPES = {
     24: ("I8", 1, 1), 25: ("I16", 1, 2), 26: ("I32", 1, 4), 27: ("I64", 1, 8), 28: ("F64", 1, 8), 30: ("BF16", 1, 2),
 }
 Q8_0, Q4_K, Q6_K = 8, 12, 14
-KQUANT = {10, 11, 12, 13, 14, 15}  # lib/gguf_validate.pl:144-150 lists 12..15
+KQUANT = {12, 13, 14, 15}  # Q4_K, Q5_K, Q6_K, Q8_K: the reference's kquant_type (lib/gguf_validate.pl:148-152)
 MAX_DIMS = 4
 # architectures whose blocks use rotary embeddings (lib/gguf_validate.pl:204-213)
 ROPE_ARCHS = {"llama", "falcon", "mistral", "qwen", "qwen2", "phi", "phi3", "gemma", "gemma2", "starcoder2"}
@@ -341,6 +341,8 @@ def validate(g):
     qv = g.metadata.get("general.quantization_version")
     if kq and qv is None:
         out.append(("quant_version", False, f"K-quant tensors ({', '.join(kq)}) but no general.quantization_version"))
+    elif kq and (isinstance(qv, bool) or not isinstance(qv, (int, float))):
+        out.append(("quant_version", False, f"general.quantization_version={qv!r} is not a number"))
     elif kq and qv < 3:
         out.append(("quant_version", False, f"general.quantization_version={qv}; K-quant tensors require >= 3"))
     else:

@@ -51,12 +51,45 @@ def check():
 
 
 def call(name, *args):
-    """Call an exported entry point by name; pointers may be tensors."""
+    """Call an exported entry point by name; pointers may be tensors.  Only names with a
+    declared ctypes signature are callable: without one, ctypes would pass each Python
+    int as a 32-bit C int and cut 64-bit device pointers short."""
+    from ._native import HIP_SIGNATURES
+
+    if name not in HIP_SIGNATURES:
+        raise KeyError(f"{name} has no ctypes signature in _native.HIP_SIGNATURES")
     fn = getattr(lib(), name)
     conv = [_ptr(a) if not isinstance(a, (float,)) else a for a in args]
     res = fn(*conv)
     check()
     return res
+
+
+BPDQ_ERR_SHAPE = 2  # include/bpdq.h
+
+
+def _need(t, nbytes, what):
+    """The C ABI takes bare device pointers and cannot see buffer sizes, so the tensor
+    helpers check them here: t must be contiguous and hold at least nbytes."""
+    if t is None or isinstance(t, int) or not hasattr(t, "numel"):
+        return
+    if not t.is_contiguous():
+        raise BpdqError(BPDQ_ERR_SHAPE, f"{what} is not contiguous")
+    have = t.numel() * t.element_size()
+    if have < nbytes:
+        raise BpdqError(BPDQ_ERR_SHAPE, f"{what} holds {have} bytes, the call needs {nbytes}")
+
+
+def _q4k_bytes(M, K):
+    return max(M, 0) * max(K, 0) // 256 * formats.Q4K_BYTES
+
+
+def _q8k_bytes(K):
+    return max(K, 0) // formats.Q8K_ELEMS * formats.Q8K_BYTES
+
+
+def _q8_0_bytes(rows, K):
+    return max(rows, 0) * max(K, 0) // 32 * formats.Q8_0_BYTES
 
 
 def _use_torch_stream():
@@ -79,6 +112,7 @@ def dequant_q4k(q, order=formats.ORDER_BPD, out=None):
 
     nb = q.numel() // formats.Q4K_BYTES
     out = _empty(nb * 256, torch.float32, q) if out is None else out
+    _need(out, nb * 256 * 4, "out")
     _use_torch_stream()
     call("bpd_dequant_q4k_gpu" if order == formats.ORDER_BPD else "bpd_dequant_q4k_gguf_gpu", q, out, nb)
     return out
@@ -89,6 +123,9 @@ def qmatmul_q4k(w, x, M, K, out=None):
     import torch
 
     out = _empty(M, torch.float32, x) if out is None else out
+    _need(w, _q4k_bytes(M, K), "w")
+    _need(x, max(K, 0) * 4, "x")
+    _need(out, max(M, 0) * 4, "out")
     _use_torch_stream()
     call("bpd_qmatmul_q4k_gpu", w, x, out, M, K)
     return out
@@ -99,6 +136,7 @@ def quant_q8_k(x, out=None):
 
     n = x.numel()
     out = _empty(n // formats.Q8K_ELEMS * formats.Q8K_BYTES, torch.uint8, x) if out is None else out
+    _need(out, _q8k_bytes(n), "out")
     _use_torch_stream()
     call("bpd_quant_q8_k_gpu", x, out, n)
     return out
@@ -108,6 +146,9 @@ def qmatmul_q4k_q8k(w, xq, M, K, order=formats.ORDER_BPD, out=None):
     import torch
 
     out = _empty(M, torch.float32, xq) if out is None else out
+    _need(w, _q4k_bytes(M, K), "w")
+    _need(xq, _q8k_bytes(K), "xq")
+    _need(out, max(M, 0) * 4, "out")
     _use_torch_stream()
     call("bpd_qmatmul_q4k_q8k_gpu" if order == formats.ORDER_BPD else "bpd_qmatmul_q4k_q8k_gguf_gpu",
          w, xq, out, M, K)
@@ -124,6 +165,9 @@ def qmatmul_q4k_q8k_fused(w, x, M, K, out=None):
     import torch
 
     out = _empty(M, torch.float32, x) if out is None else out
+    _need(w, _q4k_bytes(M, K), "w")
+    _need(x, max(K, 0) * 4, "x")
+    _need(out, max(M, 0) * 4, "out")
     _use_torch_stream()
     call("bpd_qmatmul_q4k_q8k_fused_gpu", w, x, out, M, K)
     return out
@@ -139,6 +183,10 @@ def _multi(name, ws, x, Ms, K, outs):
 
     n = len(ws)
     outs = [_empty(m, torch.float32, x) for m in Ms] if outs is None else outs
+    for i in range(n):
+        _need(ws[i], _q4k_bytes(Ms[i], K), f"w[{i}]")
+        _need(outs[i], max(Ms[i], 0) * 4, f"out[{i}]")
+    _need(x, max(K, 0) * 4 if "fused" in name else _q8k_bytes(K), "x")
     w_arr = (ctypes.c_void_p * n)(*[_ptr(w) for w in ws])
     y_arr = (ctypes.c_void_p * n)(*[_ptr(y) for y in outs])
     m_arr = (ctypes.c_int * n)(*Ms)
@@ -155,6 +203,8 @@ def q8_pad64(x, N, K, out=None):
     import torch
 
     out = _empty(K // 32 * N * 64, torch.uint8, x) if out is None else out
+    _need(x, max(N, 0) * max(K, 0) * 4, "x")
+    _need(out, max(K, 0) // 32 * max(N, 0) * 64, "out")
     _use_torch_stream()
     call("bpd_q8_pad64_from_f32_gpu", x, out, N, K)
     return out
@@ -164,6 +214,9 @@ def qmatmul_q8_pad64(Wp, Xq, m_weight, m_tokens, K, out=None):
     import torch
 
     out = _empty(m_tokens * m_weight, torch.float32, Xq) if out is None else out
+    _need(Wp, max(K, 0) // 32 * max(m_weight, 0) * 64, "W_pad64")
+    _need(Xq, _q8_0_bytes(m_tokens, K), "Xq")
+    _need(out, max(m_tokens * m_weight, 0) * 4, "out")
     _use_torch_stream()
     call("bpd_qmatmul_q8_pad64_gpu", Wp, Xq, out, m_weight, m_tokens, K)
     return out
@@ -178,6 +231,7 @@ def dequant_q6k(q, order=formats.ORDER_BPD, out=None):
 
     nb = q.numel() // 210
     out = _empty(nb * 256, torch.float32, q) if out is None else out
+    _need(out, nb * 256 * 4, "out")
     _use_torch_stream()
     call("bpd_dequant_q6k_gpu" if order == formats.ORDER_BPD else "bpd_dequant_q6k_gguf_gpu", q, out, nb)
     return out
@@ -187,6 +241,9 @@ def qmatmul_q6k_q8k(w, xq, M, K, order=formats.ORDER_BPD, out=None):
     import torch
 
     out = _empty(M, torch.float32, xq) if out is None else out
+    _need(w, max(M, 0) * max(K, 0) // 256 * 210, "w")
+    _need(xq, _q8k_bytes(K), "xq")
+    _need(out, max(M, 0) * 4, "out")
     _use_torch_stream()
     call("bpd_qmatmul_q6k_q8k_gpu" if order == formats.ORDER_BPD else "bpd_qmatmul_q6k_q8k_gguf_gpu",
          w, xq, out, M, K)
@@ -200,6 +257,7 @@ def dequant_q8_0(raw, out=None):
 
     nb = raw.numel() // formats.Q8_0_BYTES
     out = _empty(nb * 32, torch.float32, raw) if out is None else out
+    _need(out, nb * 32 * 4, "out")
     _use_torch_stream()
     call("bpd_dequant_q8_0_gpu", raw, out, nb)
     return out
@@ -210,6 +268,8 @@ def embed_lookup_q8_0(table, ids, embed_dim, out=None):
 
     n = ids.numel()
     out = _empty(n * embed_dim, torch.float32, table) if out is None else out
+    _need(table, _q8_0_bytes(1, embed_dim), "table")   # ids index rows on the device: 0 <= id < rows
+    _need(out, n * max(embed_dim, 0) * 4, "out")
     _use_torch_stream()
     call("bpd_embed_lookup_q8_0_gpu", table, ids, out, n, embed_dim)
     return out
@@ -220,6 +280,7 @@ def quant_q8_0(x, out=None):
 
     n = x.numel()
     out = _empty(n // 32 * 34, torch.uint8, x) if out is None else out
+    _need(out, n // 32 * 34, "out")
     _use_torch_stream()
     call("bpd_quant_q8_0_gpu", x, out, n)
     return out
@@ -230,6 +291,9 @@ def qmatmul_q8_0_dispatch(Wq, Xq, m_weight, m_tokens, K, out=None):
     import torch
 
     out = _empty(m_tokens * m_weight, torch.float32, Wq) if out is None else out
+    _need(Wq, _q8_0_bytes(m_weight, K), "Wq")
+    _need(Xq, _q8_0_bytes(m_tokens, K), "Xq")
+    _need(out, max(m_tokens * m_weight, 0) * 4, "out")
     _use_torch_stream()
     call("bpd_qmatmul_q8_0_dispatch_gpu", Wq, Xq, out, m_weight, m_tokens, K)
     return out
@@ -239,6 +303,9 @@ def qmatmul_q8_0_llamafile(W, X, m_weight, m_tokens, K, out=None):
     import torch
 
     out = _empty(m_tokens * m_weight, torch.float32, W) if out is None else out
+    _need(W, _q8_0_bytes(m_weight, K), "W")
+    _need(X, max(m_tokens, 0) * max(K, 0) * 4, "X")
+    _need(out, max(m_tokens * m_weight, 0) * 4, "out")
     _use_torch_stream()
     call("bpd_qmatmul_q8_0_llamafile_gpu", W, X, out, m_weight, m_tokens, K)
     return out
@@ -249,6 +316,9 @@ def qmatmul_q8_0_dispatch_s(Wq, Xq, m_weight, m_tokens, K, out=None):
     import torch
 
     out = _empty(m_tokens * m_weight, torch.float32, Wq) if out is None else out
+    _need(Wq, _q8_0_bytes(m_weight, K), "Wq")
+    _need(Xq, _q8_0_bytes(m_tokens, K), "Xq")
+    _need(out, max(m_tokens * m_weight, 0) * 4, "out")
     _use_torch_stream()
     call("bpd_qmatmul_q8_0_dispatch_s_gpu", Wq, Xq, out, m_weight, m_tokens, K)
     return out
@@ -258,6 +328,9 @@ def qmatmul_q8_0_llamafile_s(W, X, m_weight, m_tokens, K, out=None):
     import torch
 
     out = _empty(m_tokens * m_weight, torch.float32, W) if out is None else out
+    _need(W, _q8_0_bytes(m_weight, K), "W")
+    _need(X, max(m_tokens, 0) * max(K, 0) * 4, "X")
+    _need(out, max(m_tokens * m_weight, 0) * 4, "out")
     _use_torch_stream()
     call("bpd_qmatmul_q8_0_llamafile_s_gpu", W, X, out, m_weight, m_tokens, K)
     return out

@@ -35,6 +35,9 @@ extern "C" {
 #define BPDQ_ERR_ALIGN 3  /* pointer alignment below what the kernel loads with */
 #define BPDQ_ERR_HIP 4    /* the HIP runtime reported an error (launch, copy, sync) */
 #define BPDQ_ERR_ALLOC 5  /* device allocation failed */
+#define BPDQ_ERR_CAPTURE 6 /* the stream's workspace would have to grow during stream capture:
+                              make the same call once outside capture, on the same stream */
+#define BPDQ_ERR_LIMIT 7   /* the call needs more than a fixed-size buffer holds */
 /* First error recorded on the calling thread since the previous call; clears it. */
 int bpd_gpu_last_error(void);
 /* Text of the most recent error on the calling thread ("" if none). */
@@ -144,7 +147,10 @@ void bpd_quant_q8_0_gpu(const float* x_dev, uint8_t* y_dev, int n_elements);    
  * bpd_qmatmul_q8_0_dispatch_cpu of the -mavx build (bench/bpd_gemm_q8_0_cpu.c:159). */
 void bpd_qmatmul_q8_0_dispatch_gpu(const uint8_t* Wq_dev, const uint8_t* Xq_dev, float* out_dev, int m_weight,
                                    int m_tokens, int K);
-/* quantize X (fp32, m_tokens x K) then the dispatcher (bench/bpd_cpu.c:4429-4452). */
+/* quantize X (fp32, m_tokens x K) then the dispatcher (bench/bpd_cpu.c:4429-4452).
+ * The Q8_0 rows of X go to a device workspace owned by the library, one per
+ * (device, stream), grown on demand; growth fails with BPDQ_ERR_CAPTURE during
+ * stream capture.  Calls on one stream may come from several host threads. */
 void bpd_qmatmul_q8_0_llamafile_gpu(const uint8_t* W_dev, const float* X_dev, float* out_dev, int m_weight,
                                     int m_tokens, int K);
 

@@ -103,6 +103,39 @@ uint16_t bpdq_o_f32_to_f16(float f) {
 
 static inline uint16_t rd16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
 
+/* ------------------------------------------------------- x86 NaN rules --- */
+
+/* The reference's compiled C runs on x86, whose SSE arithmetic gives a NaN
+ * operand back quieted (the first operand's when both are NaN) and the default
+ * NaN 0xFFC00000 for an invalid operation (Inf*0, Inf-Inf).  For a product or
+ * sum whose two operands can both be NaN, the output bits therefore depend on
+ * which operand the compiler put first.  These helpers fix that choice in the
+ * source; each call site names the operand the reference build puts first
+ * (measured on oracle/_ref and pinned by tests/test_oracle_reference.py). */
+static inline uint32_t f32_bits(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    return u;
+}
+static inline float bits_f32(uint32_t u) {
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+static inline float x86_nan_of(float a, float b) {
+    if (isnan(a)) return bits_f32(f32_bits(a) | 0x400000u);
+    if (isnan(b)) return bits_f32(f32_bits(b) | 0x400000u);
+    return bits_f32(0xFFC00000u);
+}
+static inline float x86_mul(float first, float second) {
+    float r = first * second;
+    return isnan(r) ? x86_nan_of(first, second) : r;
+}
+static inline float x86_add(float first, float second) {
+    float r = first + second;
+    return isnan(r) ? x86_nan_of(first, second) : r;
+}
+
 /* ---------------------------------------------------------------- Q4_K --- */
 
 /* 6-bit scale/min of sub-block j: bench/bpd_quant.c:56-62. */
@@ -138,6 +171,12 @@ void bpdq_o_dequant_q4k(const uint8_t* q, float* out, int n_blocks) {
     for (int b = 0; b < n_blocks; b++) dq_block_bpd(q + (size_t)b * 144, out + (size_t)b * 256);
 }
 
+/* The GGUF-map dequant exists in the reference only as a CUDA kernel, so its
+ * NaN outputs are the NVIDIA GPU's: every fp32 operation that yields a NaN
+ * there returns the canonical NaN 0x7FFFFFFF (PTX ISA, floating-point
+ * instructions: NaN payloads are not propagated). */
+static inline float cuda_nan(float y) { return isnan(y) ? bits_f32(0x7FFFFFFFu) : y; }
+
 /* bench/bench_dequant_gpu_h2h.cu:27-48: for i in 0..3, l in 0..31:
  * element 64i+l <- low(qs[32i+l]) with sub-block 2i,
  * element 64i+32+l <- high(qs[32i+l]) with sub-block 2i+1; h2h f16 decode. */
@@ -154,8 +193,8 @@ void bpdq_o_dequant_q4k_gguf(const uint8_t* q, float* out, int n_blocks) {
             float d2 = dall * (float)sc, m2 = dmin * (float)m;
             const uint8_t* qs = blk + 16 + 32 * i;
             for (int l = 0; l < 32; l++) {
-                y[64 * i + l] = d1 * (float)(qs[l] & 15) - m1;
-                y[64 * i + 32 + l] = d2 * (float)(qs[l] >> 4) - m2;
+                y[64 * i + l] = cuda_nan(d1 * (float)(qs[l] & 15) - m1);
+                y[64 * i + 32 + l] = cuda_nan(d2 * (float)(qs[l] >> 4) - m2);
             }
         }
     }
@@ -171,7 +210,8 @@ void bpdq_o_qmatmul_q4k(const uint8_t* w, const float* x, float* y, int M, int K
         for (int b = 0; b < nb; b++) {
             dq_block_bpd(row + (size_t)b * 144, buf);
             const float* xp = x + (size_t)b * 256;
-            for (int k = 0; k < 256; k++) sum = sum + buf[k] * xp[k];
+            /* the reference build multiplies with the weight first and adds onto sum */
+            for (int k = 0; k < 256; k++) sum = x86_add(sum, x86_mul(buf[k], xp[k]));
         }
         y[r] = sum;
     }
@@ -189,7 +229,8 @@ void bpdq_o_qmm_q4k(const uint8_t* A, const float* B, float* C, int M, int N, in
             for (int k = 0; k < 256; k++) {
                 float a = buf[k];
                 const float* brow = B + ((size_t)b * 256 + k) * N;
-                for (int c = 0; c < N; c++) C[(size_t)r * N + c] = C[(size_t)r * N + c] + a * brow[c];
+                /* the reference build puts B first in the product and the product first in the sum */
+                for (int c = 0; c < N; c++) C[(size_t)r * N + c] = x86_add(x86_mul(brow[c], a), C[(size_t)r * N + c]);
             }
         }
     }
@@ -457,14 +498,27 @@ float bpdq_o_qdot_q8_0_S(const uint8_t* w, const uint8_t* a, int n_blocks) {
         const uint8_t* wb = w + (size_t)ib * 34;
         const uint8_t* ab = a + (size_t)ib * 34;
         int32_t sumi = dot32((const int8_t*)(wb + 2), (const int8_t*)(ab + 2));
-        float delta = bpdq_o_f16_magic(rd16(wb)) * bpdq_o_f16_magic(rd16(ab));
-        sumf = sumf + (float)sumi * delta;
+        /* the reference build puts the weight scale first */
+        float delta = x86_mul(bpdq_o_f16_magic(rd16(wb)), bpdq_o_f16_magic(rd16(ab)));
+        sumf = x86_add(sumf, (float)sumi * delta);
     }
     return sumf;
 }
 
+/* Scalar tile cell: bench/bpd_gemm_q8_0_cpu.c:112-128.  The same sum as
+ * bpdq_o_qdot_q8_0_S, but its scales are decoded by the ldexpf form of
+ * bench/bpd_gemm_q8_0_cpu.c:13-26 (NaN -> +/-0x7FC00000, no payload) and the
+ * reference build puts the activation scale Bd first in Ad*Bd. */
 float bpdq_o_cell_q8_0_S(const uint8_t* w, const uint8_t* a, int n_blocks) {
-    return bpdq_o_qdot_q8_0_S(w, a, n_blocks);
+    float sumf = 0.0f;
+    for (int l = 0; l < n_blocks; l++) {
+        const uint8_t* wb = w + (size_t)l * 34;
+        const uint8_t* ab = a + (size_t)l * 34;
+        int32_t sumi = dot32((const int8_t*)(wb + 2), (const int8_t*)(ab + 2));
+        float delta = x86_mul(bpdq_o_f16_ldexp(rd16(ab)), bpdq_o_f16_ldexp(rd16(wb)));
+        sumf = x86_add(sumf, (float)sumi * delta);
+    }
+    return sumf;
 }
 
 /* AVX1 pair order P: bench/bpd_cpu.c:4208-4259. */

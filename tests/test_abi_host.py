@@ -193,3 +193,35 @@ def test_decode_step_validation_before_launch():
     assert "multiple of 32" in _err(2)
     assert L.gpu_alloc(-1) is None
     _err(2)
+
+
+def test_tensor_helpers_check_buffer_sizes():
+    """The C ABI takes bare pointers, so the torch helpers check sizes on the host and
+    raise before any launch (CPU tensors: nothing here reaches the GPU)."""
+    import torch
+
+    w = torch.zeros(4 * 144, dtype=torch.uint8)            # 4 Q4_K blocks
+    xq = torch.zeros(292, dtype=torch.uint8)               # one Q8_K block
+    with pytest.raises(gpu.BpdqError, match="w holds 576 bytes, the call needs 1152"):
+        gpu.qmatmul_q4k_q8k(w, xq, 8, 256)
+    with pytest.raises(gpu.BpdqError, match="xq holds"):
+        gpu.qmatmul_q4k_q8k(torch.zeros(8 * 2 * 144, dtype=torch.uint8), xq, 8, 512)
+    with pytest.raises(gpu.BpdqError, match="out holds"):
+        gpu.qmatmul_q4k_q8k(torch.zeros(8 * 144, dtype=torch.uint8), xq, 8, 256, out=torch.zeros(7))
+    with pytest.raises(gpu.BpdqError, match="not contiguous"):
+        gpu.qmatmul_q4k(w, torch.zeros(512)[::2], 4, 256)
+    with pytest.raises(gpu.BpdqError, match="Xq holds"):
+        gpu.qmatmul_q8_0_dispatch(torch.zeros(4 * 34, dtype=torch.uint8), torch.zeros(33, dtype=torch.uint8), 4, 1, 32)
+    with pytest.raises(gpu.BpdqError, match="X holds"):
+        gpu.qmatmul_q8_0_llamafile(torch.zeros(4 * 34, dtype=torch.uint8), torch.zeros(31), 4, 1, 32)
+    with pytest.raises(gpu.BpdqError, match=r"w\[1\] holds"):
+        gpu.qmatmul_q4k_q8k_multi([w, w], xq, [4, 5], 256)
+    with pytest.raises(gpu.BpdqError, match="w holds"):
+        gpu.qmatmul_q6k_q8k(torch.zeros(210, dtype=torch.uint8), xq, 2, 256)
+
+
+def test_call_refuses_names_without_a_signature():
+    # ctypes without argtypes passes Python ints as 32-bit C ints: a device pointer would
+    # arrive cut to its low 32 bits, so gpu.call only calls declared entry points
+    with pytest.raises(KeyError, match="no ctypes signature"):
+        gpu.call("bpd_not_declared_anywhere_gpu", 0x7F1234561000)

@@ -163,3 +163,27 @@ def test_bad_magic_version_alignment_and_duplicates(tmp_path):
     gguf.write_gguf(p, [], [("t", (4,), 0, one), ("t", (4,), 0, one)])
     with pytest.raises(gguf.GGUFError, match="duplicate tensor"):
         gguf.open_gguf(p)
+
+
+def _qv_file(path, ttype, nbytes, qv):
+    meta = [("general.architecture", gguf.T_STR, "llama"), ("llama.rope.freq_base", gguf.T_F32, 10000.0)]
+    if qv is not None:
+        meta.append(("general.quantization_version",) + qv)
+    gguf.write_gguf(path, meta, [("blk.0.ffn_up.weight", (256, 1), ttype, bytes(nbytes))])
+    return dict((c, (ok, d)) for c, ok, d in gguf.report(path))
+
+
+def test_quant_version_covers_exactly_the_reference_kquant_types(tmp_path):
+    # lib/gguf_validate.pl:148-152: kquant_type is 12..15.  Q2_K / Q3_K files do not need
+    # quantization_version >= 3; a Q4_K file does.
+    p = str(tmp_path / "q.gguf")
+    assert _qv_file(p, 11, 110, (gguf.T_U32, 2))["quant_version"][0]           # Q3_K, version 2
+    assert _qv_file(p, 10, 84, None)["quant_version"][0]                      # Q2_K, no version
+    assert not _qv_file(p, 12, 144, (gguf.T_U32, 2))["quant_version"][0]      # Q4_K, version 2
+    assert _qv_file(p, 15, 292, (gguf.T_U32, 3))["quant_version"][0]          # Q8_K, version 3
+
+
+def test_non_numeric_quant_version_is_a_failed_check(tmp_path):
+    p = str(tmp_path / "q.gguf")
+    ok, detail = _qv_file(p, 12, 144, (gguf.T_STR, "3"))["quant_version"]
+    assert not ok and "not a number" in detail

@@ -38,9 +38,8 @@ def test_dequant_q6k(dev, order, o, nb):
 def test_dequant_q6k_random_bytes(dev, order, o):
     b = q6k_blocks(2048, 7, realistic=False)       # every d bit pattern class, NaN/Inf included
     got, want = to_np(gpu.dequant_q6k(_d(b, dev), order)), O.dequant_q6k(b, o)
-    nan = np.isnan(want)
-    assert np.array_equal(np.isnan(got), nan)
-    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+    assert np.isnan(want).any()
+    assert_bits_equal(got, want, f"q6k random-byte dequant order {o}")   # NaN bits included
 
 
 @pytest.mark.parametrize("order,o", ORDERS)

@@ -115,7 +115,51 @@ def test_dispatch_scalar_order_special_scales(dev, mw, mt, K):
     got = to_np(gpu.qmatmul_q8_0_dispatch_s(_d(W, dev), _d(Xq, dev), mw, mt, K))
     want = O.dispatch_q8_0(W, Xq, mw, mt, K, "S", nthreads=8)
     assert np.isnan(want).any() and np.isinf(want).any()
-    assert_bits_equal(got, want, f"S-order special scales {mw}x{mt}x{K}", nan_equal=True)
+    assert_bits_equal(got, want, f"S-order special scales {mw}x{mt}x{K}")   # NaN bits included
+
+
+SPECIAL_F16 = [0x0000, 0x8000, 0x0001, 0x83FF, 0x7C00, 0xFC00, 0x7E00, 0xFE00, 0x7C01, 0xFD55, 0x7BFF]
+
+
+def _special(rows, nb, key):
+    raw = synth.q8_0(rows, nb * 32, key).reshape(rows, nb, 34).copy()
+    for i, h in enumerate(SPECIAL_F16 * 2):
+        raw[(7 * i + 3) % rows, (5 * i + 1) % nb, 0:2] = (h & 0xFF, h >> 8)
+    return raw.reshape(-1).copy()
+
+
+@pytest.mark.parametrize("mw,mt,K", [(23, 19, 32), (130, 131, 512), (40, 9, 224)])
+def test_scalar_order_nan_bits_both_forms(dev, mw, mt, K):
+    """NaN / Inf scales with and without payload in both operands, so that the first NaN
+    of a cell can come from either factor: dispatch_s takes the scalar tiles' bits,
+    llamafile_s (through fp32 activations with infinities and NaNs) bpd_qdot's."""
+    nb = K // 32
+    W, Xq = _special(mw, nb, synth.key(46, mw)), _special(mt, nb, synth.key(47, mt))
+    got = to_np(gpu.qmatmul_q8_0_dispatch_s(_d(W, dev), _d(Xq, dev), mw, mt, K))
+    want = O.dispatch_q8_0(W, Xq, mw, mt, K, "S", nthreads=8)
+    assert np.isnan(want).any()
+    assert_bits_equal(got, want, f"dispatch_s NaN bits {mw}x{mt}x{K}")
+    X = synth.normal_f32(mt * K, synth.key(48, mt))
+    X[::97] = np.inf
+    X[5::101] = -np.inf
+    X[7::89] = np.nan
+    got = to_np(gpu.qmatmul_q8_0_llamafile_s(_d(W, dev), _d(X, dev), mw, mt, K))
+    want = O.qmatmul_q8_0_llamafile(W, X, mw, mt, K, "S")
+    assert np.isnan(want).any()
+    assert_bits_equal(got, want, f"llamafile_s NaN bits {mw}x{mt}x{K}")
+
+
+def test_dequant_and_embed_q8_0_nan_bits(dev):
+    import torch
+
+    raw = synth.random_bytes(4096 * 34, synth.key(49, 1))
+    got = to_np(gpu.dequant_q8_0(_d(raw, dev)))
+    want = O.dequant_q8_0(raw)
+    assert np.isnan(want).any()
+    assert_bits_equal(got, want, "Q8_0 dequant of random bytes")
+    ids = np.arange(0, 64, 3, dtype=np.int32)
+    got = to_np(gpu.embed_lookup_q8_0(_d(raw, dev), torch.from_numpy(ids).to(dev), 2048))
+    assert_bits_equal(got, O.embed_lookup_q8_0(raw, ids, 2048), "Q8_0 embed of random bytes")
 
 
 def test_llamafile_scalar_build_path(dev):
@@ -176,3 +220,47 @@ def test_dispatch_spare_waves(dev, mw):
     Xq = O.quant_q8_0(synth.normal_f32(K, synth.key(44, 1)))
     got = to_np(gpu.qmatmul_q8_0_dispatch(_d(W, dev), _d(Xq, dev), mw, 1, K))
     assert_bits_equal(got, O.dispatch_q8_0(W, Xq, mw, 1, K, "T"), f"spare waves mw={mw}")
+
+
+def test_workspace_growth_inside_capture_is_refused(dev):
+    """The llamafile entry quantizes X into its stream's workspace.  Inside graph capture
+    it may use the workspace but never grow it (growing drains the stream and
+    allocates): a first, larger request during capture fails with BPDQ_ERR_CAPTURE and
+    enqueues nothing.  After the same call once outside capture, on the same stream, it
+    captures, and the replays give the eager bits."""
+    import torch
+
+    mw, mt, K = 64, 3, 8192 + 512          # a size no other test asks for on this new stream
+    W = torch.from_numpy(synth.q8_0(mw, K, synth.key(50, 1))).to(dev)
+    X = torch.from_numpy(synth.normal_f32(mt * K, synth.key(50, 2))).to(dev)
+    s = torch.cuda.Stream()
+    out = torch.zeros(mt * mw, device=dev)
+    bump = torch.zeros(1, device=dev)
+    g = torch.cuda.CUDAGraph()
+    code = None
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            gpu.lib().bpd_gpu_set_stream(s.cuda_stream)
+            try:
+                gpu.call("bpd_qmatmul_q8_0_llamafile_gpu", W, X, out, mw, mt, K)
+            except gpu.BpdqError as e:
+                code = e.code
+            bump.add_(1)                    # keeps the captured graph non-empty
+    assert code == 6
+    eager = to_np(gpu.qmatmul_q8_0_llamafile(W, X, mw, mt, K))
+    with torch.cuda.stream(s):
+        gpu.lib().bpd_gpu_set_stream(s.cuda_stream)
+        gpu.call("bpd_qmatmul_q8_0_llamafile_gpu", W, X, out, mw, mt, K)   # grows, outside capture
+        s.synchronize()
+        g2 = torch.cuda.CUDAGraph()
+        out2 = torch.zeros(mt * mw, device=dev)
+        with torch.cuda.graph(g2, stream=s):
+            gpu.lib().bpd_gpu_set_stream(s.cuda_stream)
+            gpu.call("bpd_qmatmul_q8_0_llamafile_gpu", W, X, out2, mw, mt, K)
+    gpu.lib().bpd_gpu_set_stream(None)
+    for _ in range(3):
+        out2.zero_()
+        torch.cuda.synchronize()
+        g2.replay()
+        torch.cuda.synchronize()
+        assert_bits_equal(to_np(out2), eager, "captured llamafile replay")

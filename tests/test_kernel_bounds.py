@@ -245,6 +245,53 @@ def test_q6k_span_in_bounds(M):
                 assert np.max(xb + 260 + 2 * g + 2) <= x_size
 
 
+@pytest.mark.parametrize("M", [1, 5, 8, 9, 17, 4096])
+def test_q6k_span_long_in_bounds(M):
+    """k_q6k_q8k_gemv_span_long (K = 14336, one row per wave, 8 waves per workgroup):
+    the Q8_K copy into LDS (clamped loads, guarded stores), the 735 pieces of a row
+    (clamped at the last piece; spare waves read row M-1 and store nothing), each of
+    the 7 passes' 105 pieces inside the 1,696-byte pass buffer and covered by the
+    loads, and the x operand reads from the LDS copy."""
+    Q6, NB, WPB, buf = 210, 56, 8, 8 * 210 + 16
+    pieces, loads = NB * Q6 // 16, (NB * Q6 // 16 + 63) // 64
+    assert pieces * 16 == NB * Q6 and (pieces, loads) == (735, 12)
+    XD = NB * Q8K // 4
+    XU = (XD + 64 * WPB - 1) // (64 * WPB)
+    tid = np.arange(64 * WPB)
+    for u in range(XU):
+        src = np.minimum(tid + 64 * WPB * u, XD - 1)
+        assert 4 * src.max() + 4 <= NB * Q8K
+        dst = tid + 64 * WPB * u
+        assert (dst[dst < XD] < XD).all()
+    assert set(np.concatenate([tid + 64 * WPB * u for u in range(XU)])) >= set(range(XD))
+    grid = (M + WPB - 1) // WPB
+    w_size = M * NB * Q6
+    l = lanes()
+    for blk in sorted({0, grid - 1}):
+        for wave in range(WPB):
+            row = blk * WPB + wave
+            span = (row if row < M else M - 1) * NB * Q6
+            for u in range(loads):
+                p = np.minimum(l + 64 * u, pieces - 1)
+                assert span + 16 * p.min() >= 0 and span + 16 * p.max() + 16 <= w_size
+    covered = np.zeros(pieces, bool)
+    for t in range(NB // 8):
+        assert 8 * t * Q6 % 16 == 0
+        p0, n = 8 * t * Q6 // 16, 8 * Q6 // 16
+        for u in range(loads):
+            k = l + 64 * u - p0
+            ok = (k >= 0) & (k < n)
+            assert (16 * k[ok] + 16 <= buf).all()
+            covered[(l + 64 * u)[ok]] = True
+        q, c = l >> 3, l & 7
+        xb = (8 * t + q) * Q8K
+        for off, size in x_accesses(c):
+            assert np.max(xb + off + size) <= XD * 4
+        for g in range(16):
+            assert np.max(xb + 260 + 2 * g + 2) <= XD * 4
+    assert covered.all()
+
+
 # ---------------------------------------------------------------- dequant
 
 @pytest.mark.parametrize("nb", [1, 7, 33, 65536, 4096])

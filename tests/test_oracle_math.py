@@ -87,6 +87,42 @@ def test_q4k_dequant_closed_form():
     assert_bits_equal(O.dequant_q4k(q), exact.astype(np.float32).ravel(), "closed form")
 
 
+def _scale_min(blk):
+    s = blk[:, 4:16].astype(np.int64)
+    sc = np.zeros((len(blk), 8), np.int64)
+    mn = np.zeros((len(blk), 8), np.int64)
+    sc[:, :4], mn[:, :4] = s[:, 0:4] & 63, s[:, 4:8] & 63
+    sc[:, 4:] = (s[:, 8:12] & 15) | ((s[:, 0:4] >> 6) << 4)
+    mn[:, 4:] = (s[:, 8:12] >> 4) | ((s[:, 4:8] >> 6) << 4)
+    return sc, mn
+
+
+def test_q4k_gguf_dequant_nan_is_the_cuda_canonical_nan():
+    # random bytes: the h2h decode turns NaN scales into +/-Inf, so NaNs come only from
+    # Inf*0 and Inf-Inf.  Every other value is numpy's float32 d1*q - m1 (exact products,
+    # one rounding), every NaN is 0x7FFFFFFF, the NaN the reference's CUDA kernel returns.
+    q = synth.random_bytes(2048 * 144, synth.key(21, 2))
+    blk = q.reshape(-1, 144)
+    h = blk[:, 0:4].copy().view(np.uint16)
+    f = h.view(np.float16).astype(np.float32)
+    f[(h & 0x7C00) == 0x7C00] = np.where(h[(h & 0x7C00) == 0x7C00] & 0x8000, -np.inf, np.inf)
+    f[(h & 0x7FFF) == 0] = 0.0
+    sc, mn = _scale_min(blk)
+    qs = blk[:, 16:].astype(np.float32).reshape(-1, 4, 32)
+    y = np.empty((len(blk), 4, 2, 32), np.float32)
+    with np.errstate(invalid="ignore", over="ignore"):
+        for i in range(4):
+            for hi in range(2):
+                j = 2 * i + hi
+                nib = np.floor(qs[:, i] / 16) if hi else qs[:, i] % 16
+                y[:, i, hi] = (f[:, 0:1] * sc[:, j:j + 1].astype(np.float32)) * nib - \
+                    f[:, 1:2] * mn[:, j:j + 1].astype(np.float32)
+    y = y.ravel()
+    assert np.isnan(y).sum() > 100
+    y.view(np.uint32)[np.isnan(y)] = 0x7FFFFFFF
+    assert_bits_equal(O.dequant_q4k_gguf(q), y, "GGUF map, random bytes")
+
+
 @pytest.mark.parametrize("order", [0, 1])
 def test_q4k_element_map_probes(order):
     # one non-zero nibble per probe block; d = 1, every scale 1, dmin = 0 -> a single 1.0

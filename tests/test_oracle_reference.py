@@ -235,3 +235,126 @@ def test_ref_qmm_q4k_random():
     C = np.empty(35, np.float32)
     f(A.ctypes.data, B.ctypes.data, C.ctypes.data, 5, 7, 512)
     assert_bits_equal(O.qmm_q4k(A, B, 5, 7, 512), C, "qmm")
+
+
+# ------------------------------------------- NaN bits (x86 rules of the reference build)
+
+def _nan_x(n, key):
+    """fp32 vector with quiet and signalling NaNs of both signs, infinities and zeros."""
+    x = synth.normal_f32(n, key)
+    special = np.array([0x7FC00001, 0xFFC00002, 0x7F800003, 0xFF812345, 0x7F800000, 0xFF800000, 0x80000000, 0],
+                       np.uint32).view(np.float32)
+    idx = synth.random_bytes(64, key ^ 0x5A).astype(np.int64) * (n // 256)
+    x[idx % n] = special[np.arange(idx.size) % special.size]
+    return x
+
+
+def test_ref_qmatmul_q4k_nan_bits():
+    # random-byte weights (NaN / Inf d and dmin of both signs) against NaN / Inf activations
+    R = _need("quant")
+    f = _bind(R, "bpd_qmatmul_q4k", [P, P, P, I, I])
+    M, K = 64, 2048
+    w = synth.random_bytes(M * K // 256 * 144, synth.key(12, 1))
+    for x in (synth.normal_f32(K, synth.key(12, 2)), _nan_x(K, synth.key(12, 3))):
+        y = np.empty(M, np.float32)
+        f(w.ctypes.data, x.ctypes.data, y.ctypes.data, M, K)
+        assert np.isnan(y).any()
+        assert_bits_equal(O.qmatmul_q4k(w, x, M, K), y, "bpd_qmatmul_q4k NaN bits")
+
+
+def test_ref_qmm_q4k_nan_bits():
+    R = _need("quant")
+    f = _bind(R, "bpd_qmm_q4k", [P, P, P, I, I, I])
+    M, N, K = 6, 5, 512
+    A = synth.random_bytes(M * K // 256 * 144, synth.key(13, 1))
+    B = _nan_x(K * N, synth.key(13, 2))
+    C = np.empty(M * N, np.float32)
+    f(A.ctypes.data, B.ctypes.data, C.ctypes.data, M, N, K)
+    assert np.isnan(C).any()
+    assert_bits_equal(O.qmm_q4k(A, B, M, N, K), C, "bpd_qmm_q4k NaN bits")
+    # both factors NaN (d = +NaN, B = -NaN with a payload) in the last product: which one
+    # comes out names the operand order
+    blk = np.zeros(144, np.uint8)
+    blk[1], blk[4:8], blk[12:16], blk[16:] = 0x7E, 1, 1, 0x11
+    B = np.ones((256, 2), np.float32)
+    B[255, :] = np.uint32(0xFFC00002).view(np.float32)
+    C = np.empty(2, np.float32)
+    f(blk.ctypes.data, B.ctypes.data, C.ctypes.data, 1, 2, 256)
+    assert_bits_equal(O.qmm_q4k(blk, B.ravel(), 1, 2, 256), C, "bpd_qmm_q4k both-NaN product")
+
+
+SPECIAL_F16 = [0x0000, 0x8000, 0x0001, 0x83FF, 0x7C00, 0xFC00, 0x7E00, 0xFE00, 0x7C01, 0xFD55, 0x7BFF]
+
+
+def _q8_special(rows, nb, key, every):
+    raw = _q8_random(rows * nb, key).reshape(rows, nb, 34)
+    for i, h in enumerate(SPECIAL_F16 * every):
+        raw[(7 * i + 3) % rows, (5 * i + 1) % nb, 0:2] = (h & 0xFF, h >> 8)
+    return raw.reshape(-1).copy()
+
+
+@pytest.mark.parametrize("nb", [1, 2, 3, 16])
+def test_ref_q8_0_scalar_order_nan_bits(nb):
+    # zero, subnormal, infinite and NaN (with and without payload) scales in both operands
+    RS = _need("scalar")
+    mw, mt, K = 23, 19, 32 * nb
+    W, X = _q8_special(mw, nb, synth.key(14, nb), 2), _q8_special(mt, nb, synth.key(15, nb), 2)
+    f = _bind(RS, "bpd_qmatmul_q8_0_dispatch_cpu", [P, P, P, I, I, I])
+    out = np.empty(mw * mt, np.float32)
+    f(W.ctypes.data, X.ctypes.data, out.ctypes.data, mw, mt, K)
+    assert np.isnan(out).any()
+    assert_bits_equal(O.dispatch_q8_0(W, X, mw, mt, K, "S"), out, "scalar tiles (S) NaN bits")
+    q = _bind(RS, "bpd_qdot_q8_0_q8_0_cpu", [P, P, I], ctypes.c_float)
+    bpr = nb * 34
+    for r in range(mw):
+        for t in range(mt):
+            want = np.float32(q(W.ctypes.data + r * bpr, X.ctypes.data + t * bpr, nb))
+            got = np.float32(O.lib().bpdq_o_qdot_q8_0_S(W.ctypes.data + r * bpr, X.ctypes.data + t * bpr, nb))
+            assert_bits_equal(got, want, f"qdot S NaN bits ({r}, {t})")
+
+
+def test_ref_llamafile_scalar_build_inf_activations():
+    # the scalar build's llamafile entry goes through bpd_qmatmul_q8_0_cpu (qdot S):
+    # infinite activations give infinite Q8_0 scales, NaN ones quantize to zeros
+    RS = _need("scalar")
+    mw, mt, K = 13, 6, 256
+    W = _q8_special(mw, K // 32, synth.key(16, 1), 1)
+    X = _nan_x(mt * K, synth.key(16, 2))
+    f = _bind(RS, "bpd_qmatmul_q8_0_llamafile_cpu", [P, P, P, I, I, I])
+    out = np.empty(mw * mt, np.float32)
+    f(W.ctypes.data, X.ctypes.data, out.ctypes.data, mw, mt, K)
+    assert np.isnan(out).any()
+    assert_bits_equal(O.qmatmul_q8_0_llamafile(W, X, mw, mt, K, "S"), out, "llamafile scalar build NaN bits")
+
+
+def test_ref_both_nan_operand_order():
+    """One product with two NaN factors of different sign / payload: the bits that come
+    out name the operand the reference build puts first (x86 keeps the first NaN)."""
+    RQ, RS = _need("quant"), _need("scalar")
+    # bpd_qmatmul_q4k: weight (d = NaN) times x = -NaN with a payload
+    f = _bind(RQ, "bpd_qmatmul_q4k", [P, P, P, I, I])
+    for dh in (0x7E01, 0xFE01):
+        blk = np.zeros(144, np.uint8)
+        blk[0], blk[1], blk[4:8], blk[12:16], blk[16:] = dh & 0xFF, dh >> 8, 1, 1, 0x11
+        for xb in (0x7FC00001, 0xFFC00002):
+            x = np.ones(256, np.float32)
+            x[0] = np.uint32(xb).view(np.float32)
+            y = np.empty(1, np.float32)
+            f(blk.ctypes.data, x.ctypes.data, y.ctypes.data, 1, 256)
+            assert_bits_equal(O.qmatmul_q4k(blk, x, 1, 256), y, f"chain d={dh:#x} x0={xb:#x}")
+
+    def q8(h):
+        b = np.full(34, 1, np.uint8)
+        b[0], b[1] = h & 0xFF, h >> 8
+        return b
+
+    q = _bind(RS, "bpd_qdot_q8_0_q8_0_cpu", [P, P, I], ctypes.c_float)
+    d = _bind(RS, "bpd_qmatmul_q8_0_dispatch_cpu", [P, P, P, I, I, I])
+    for wh, xh in ((0x7E01, 0xFE02), (0xFE02, 0x7E01), (0x7C00, 0x0000), (0x0000, 0xFC00)):
+        w, a = q8(wh), q8(xh)
+        want = np.float32(q(w.ctypes.data, a.ctypes.data, 1))
+        assert_bits_equal(np.float32(O.lib().bpdq_o_qdot_q8_0_S(w.ctypes.data, a.ctypes.data, 1)), want,
+                          f"qdot S {wh:#x} x {xh:#x}")
+        out = np.empty(1, np.float32)
+        d(w.ctypes.data, a.ctypes.data, out.ctypes.data, 1, 1, 32)
+        assert_bits_equal(O.dispatch_q8_0(w, a, 1, 1, 32, "S"), out, f"scalar tile {wh:#x} x {xh:#x}")
