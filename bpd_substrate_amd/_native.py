@@ -66,6 +66,7 @@ HIP_SIGNATURES = {
     "bpd_quant_q8_0_gpu": (None, [P, P, I]),
     "bpd_qmatmul_q8_0_dispatch_gpu": (None, [P, P, P, I, I, I]),
     "bpd_qmatmul_q8_0_llamafile_gpu": (None, [P, P, P, I, I, I]),
+    "bpd_qmatmul_q8_0_llamafile_noalloc_gpu": (None, [P, P, P, I, I, I]),
     "bpd_qmatmul_q8_0_dispatch_s_gpu": (None, [P, P, P, I, I, I]),
     "bpd_qmatmul_q8_0_llamafile_s_gpu": (None, [P, P, P, I, I, I]),
     "bpdq_stream_read_gpu": (None, [P, I, P]),

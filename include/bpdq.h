@@ -154,6 +154,16 @@ void bpd_qmatmul_q8_0_dispatch_gpu(const uint8_t* Wq_dev, const uint8_t* Xq_dev,
 void bpd_qmatmul_q8_0_llamafile_gpu(const uint8_t* W_dev, const float* X_dev, float* out_dev, int m_weight,
                                     int m_tokens, int K);
 
+/* No counterpart in the reference: bpd_qmatmul_q8_0_llamafile_gpu for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments and bits; the Q8_0 rows of X go to a fixed 8 MiB device array
+ * that each GPU holds for the life of the process, so the call allocates nothing.
+ * m_tokens * (K/32) * 34 bytes above 8 MiB are refused with BPDQ_ERR_LIMIT, nothing launched.
+ * Every call on one GPU shares that array: calls that overlap on one GPU (other streams,
+ * other host threads) race on it. */
+void bpd_qmatmul_q8_0_llamafile_noalloc_gpu(const uint8_t* W_dev, const float* X_dev, float* out_dev, int m_weight,
+                                            int m_tokens, int K);
+
 /* Same cells in the scalar order S (bench/bpd_gemm_q8_0_cpu.c:102-131): bit-identical
  * to bpd_qmatmul_q8_0_dispatch_cpu / _llamafile_cpu of the -O2 (non-AVX) build.  Runs
  * on int8 MFMA (one 32x32x32 step per Q8_0 block) with an fp32 epilogue per block:
