@@ -67,6 +67,11 @@ HIP_SIGNATURES = {
     "bpd_qmatmul_q8_0_dispatch_gpu": (None, [P, P, P, I, I, I]),
     "bpd_qmatmul_q8_0_llamafile_gpu": (None, [P, P, P, I, I, I]),
     "bpd_qmatmul_q8_0_llamafile_noalloc_gpu": (None, [P, P, P, I, I, I]),
+    "bpd_qmm_q4k_gpu": (None, [P, P, P, I, I, I]),
+    "bpd_qdot_q8_0_q8_0_grid_gpu": (None, [P, P, P, I, I, I]),
+    "bpd_qdot_q8_0_q8_0_grid_s_gpu": (None, [P, P, P, I, I, I]),
+    "bpd_qmatmul_q8_0_gpu": (None, [P, P, P, I, I, I]),
+    "bpd_qmatmul_q8_0_s_gpu": (None, [P, P, P, I, I, I]),
     "bpd_qmatmul_q8_0_dispatch_s_gpu": (None, [P, P, P, I, I, I]),
     "bpd_qmatmul_q8_0_llamafile_s_gpu": (None, [P, P, P, I, I, I]),
     "bpdq_stream_read_gpu": (None, [P, I, P]),

@@ -514,6 +514,82 @@ void bpd_qmatmul_q8_0_llamafile_s_gpu(const uint8_t* W, const float* X, float* o
     check_launch(fn);
 }
 
+// ---- bpd_qmm_q4k, the qdot grid and bpd_qmatmul_q8_0_cpu's form -----------------
+void bpd_qmm_q4k_gpu(const uint8_t* A, const float* B, float* C, int M, int N, int K) {
+    const char* fn = "bpd_qmm_q4k_gpu";
+    Check c(fn);
+    c.nonneg(M, "M").nonneg(N, "N").nonneg(K, "K").multiple(K, 256, "K");
+    if (!c.ok || M == 0 || N == 0) return;
+    c.ptr(C, 4, "C");
+    if (K > 0) c.ptr(A, 16, "A").ptr(B, 4, "B");
+    if (!c.ok) return;
+    bpdq::launch_qmm_q4k(A, B, C, M, N, K, g_stream);
+    check_launch(fn);
+}
+
+// out[m*N + n] = one qdot of weight row n and activation row m (order P or S).
+static void qdot_grid(const uint8_t* Wq, const uint8_t* Xq, float* out, int M, int N, int K, bool p_order, const char* fn) {
+    if (p_order && K > bpdq::qdot_p_max_k()) {
+        char buf[96];
+        std::snprintf(buf, sizeof buf, "K=%d is above the %d the staged activation row holds", K, bpdq::qdot_p_max_k());
+        set_err(BPDQ_ERR_LIMIT, fn, buf);
+        return;
+    }
+    if (p_order)
+        bpdq::launch_q8_0_qdot_P(Wq, Xq, out, N, M, K, g_stream);
+    else
+        bpdq::launch_q8_0_gemm_S(Wq, Xq, out, N, M, K, 1, g_stream);
+    check_launch(fn);
+}
+
+static bool check_qdot_args(Check& c, const void* W, const void* X, const float* out, int M, int N, int K, uintptr_t xa) {
+    c.nonneg(M, "M").nonneg(N, "N").nonneg(K, "K").multiple(K, 32, "K");
+    if (!c.ok || M == 0 || N == 0) return false;
+    c.ptr(out, 4, "out");
+    if (K > 0) c.ptr(W, 1, "W").ptr(X, xa, "X");
+    return c.ok;
+}
+
+void bpd_qdot_q8_0_q8_0_grid_gpu(const uint8_t* Wq, const uint8_t* Xq, float* out, int M, int N, int K) {
+    const char* fn = "bpd_qdot_q8_0_q8_0_grid_gpu";
+    Check c(fn);
+    if (check_qdot_args(c, Wq, Xq, out, M, N, K, 1)) qdot_grid(Wq, Xq, out, M, N, K, true, fn);
+}
+
+void bpd_qdot_q8_0_q8_0_grid_s_gpu(const uint8_t* Wq, const uint8_t* Xq, float* out, int M, int N, int K) {
+    const char* fn = "bpd_qdot_q8_0_q8_0_grid_s_gpu";
+    Check c(fn);
+    if (check_qdot_args(c, Wq, Xq, out, M, N, K, 1)) qdot_grid(Wq, Xq, out, M, N, K, false, fn);
+}
+
+// bpd_qmatmul_q8_0_cpu (bench/bpd_cpu.c:4295-4315): quantize the M rows of X, then the qdot grid.
+static void qmatmul_q8_0(const uint8_t* W, const float* X, float* out, int M, int N, int K, bool p_order, const char* fn) {
+    Check c(fn);
+    if (!check_qdot_args(c, W, X, out, M, N, K, 4)) return;
+    if (p_order && K > bpdq::qdot_p_max_k()) {
+        qdot_grid(nullptr, nullptr, out, M, N, K, true, fn);  // records the limit
+        return;
+    }
+    const size_t xq_bytes = (size_t)M * (size_t)(K / 32) * 34;
+    bpdq::WsLease ws;
+    uint8_t* xq = nullptr;
+    if (xq_bytes > 0) {
+        ws = bpdq::workspace(xq_bytes, g_stream, fn);
+        xq = static_cast<uint8_t*>(ws.ptr);
+        if (!xq) return;
+        bpdq::launch_quant_q8_0(X, xq, (int64_t)M * K, g_stream);
+    }
+    qdot_grid(W, xq, out, M, N, K, p_order, fn);
+}
+
+void bpd_qmatmul_q8_0_gpu(const uint8_t* W, const float* X, float* out, int M, int N, int K) {
+    qmatmul_q8_0(W, X, out, M, N, K, true, "bpd_qmatmul_q8_0_gpu");
+}
+
+void bpd_qmatmul_q8_0_s_gpu(const uint8_t* W, const float* X, float* out, int M, int N, int K) {
+    qmatmul_q8_0(W, X, out, M, N, K, false, "bpd_qmatmul_q8_0_s_gpu");
+}
+
 // ---- measurement helper ---------------------------------------------------------
 void bpdq_stream_read_gpu(const uint8_t* p, int n16, uint32_t* sink) {
     const char* fn = "bpdq_stream_read_gpu";

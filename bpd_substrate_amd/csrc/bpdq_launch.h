@@ -65,4 +65,14 @@ void launch_q8_0_gemm_S(const uint8_t* Wq, const uint8_t* Xq, float* out, int m_
                         int nan_mode, hipStream_t s);
 void launch_stream_read(const uint8_t* p, int64_t n16, uint32_t* sink, hipStream_t s);
 
+// Writes +0.0 to out[0..n).
+void launch_fill_zero(float* out, int64_t n, hipStream_t s);
+// bpd_qmm_q4k's cells: C[M][N] = deq(A[M][K]) . B[K][N], the reference's chain per cell.
+void launch_qmm_q4k(const uint8_t* A, const float* B, float* C, int M, int N, int K, hipStream_t s);
+// The AVX1 pair order P of bpd_qdot_q8_0_q8_0_cpu for every (activation row m, weight
+// row n): out[m * n_rows + n]; Q8_0 rows of K/32 blocks (K <= qdot_p_max_k()).
+int qdot_p_max_k();
+void launch_q8_0_qdot_P(const uint8_t* Wq, const uint8_t* Xq, float* out, int n_rows, int m_tokens, int K,
+                        hipStream_t s);
+
 }  // namespace bpdq

@@ -160,6 +160,97 @@ void launch_qmatmul_q4k_chain(const uint8_t* w, const float* x, float* y, int M,
 }
 
 // ----------------------------------------------------------------------------
+// bpd_qmm_q4k (bench/bpd_quant.c:114-137): C[r][c] starts at +0.0 and, for k in
+// element order, C = RN(RN(B[k][c] * deq(A)[r][k]) + C).  A workgroup takes 4
+// rows of A and 256 columns of B: for each Q4_K block its 4 waves dequantize
+// one row each into LDS (bpd map, the bits of k_dequant_q4k<0>), then thread c
+// runs the 4 chains of its column over the block's 256 k, reading B[k][c]
+// coalesced across the wave.  Cells are independent, so each is the
+// reference's chain bit for bit; a NaN cell is walked again for the x86 bits of
+// its NaN (on x86 the reference keeps the last NaN product: C + p puts p first,
+// and B[k][c] * a puts B first).
+// ----------------------------------------------------------------------------
+__device__ __noinline__ float qmm_nan_bits(const uint8_t* __restrict__ arow, const float* __restrict__ B, int N,
+                                           int col, int nb) {
+    float acc = 0.0f;
+    for (int b = 0; b < nb; b++) {
+        const uint8_t* blk = arow + (int64_t)b * kQ4KBytes;
+        const uint4 hdr = ld_u128(blk);
+        const float d = f16_ieee(hdr.x), dmin = f16_ieee(hdr.x >> 16);
+        for (int j = 0; j < 8; j++) {
+            int sc, m;
+            q4k_scale_min(hdr.y, hdr.z, hdr.w, j, sc, m);
+            const float scale = d * (float)sc, mn = dmin * (float)m;
+            for (int k = 0; k < 32; k++) {
+                const uint32_t q = (blk[16 + 16 * j + (k & 15)] >> (k >= 16 ? 4 : 0)) & 15u;
+                const float a = q4k_bpd_nan(fmaf(scale, (float)q, -mn), hdr.x & 0xFFFFu, hdr.x >> 16, sc, q);
+                const float bv = B[((int64_t)b * 256 + 32 * j + k) * N + col];
+                float p = bv * a;
+                if (__builtin_isnan(p)) p = x86_nan_of(bv, a);
+                float t = p + acc;
+                if (__builtin_isnan(t)) t = x86_nan_of(p, acc);
+                acc = t;
+            }
+        }
+    }
+    return acc;
+}
+
+__global__ __launch_bounds__(256) void k_qmm_q4k(const uint8_t* __restrict__ A, const float* __restrict__ B,
+                                                 float* __restrict__ C, int M, int N, int nb) {
+    __shared__ __align__(16) float deq[4][256];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int r0 = blockIdx.y * 4;
+    const int col = blockIdx.x * 256 + t;
+    const int cc = min(col, N - 1);  // spare columns repeat column N-1 (not stored)
+    const int64_t rowbytes = (int64_t)nb * kQ4KBytes;
+    // wave w dequantizes row r0+w (rows past M repeat row M-1); lane l: elements 4l..4l+3
+    const uint8_t* arow = A + (int64_t)min(r0 + wave, M - 1) * rowbytes;
+    const int j = lane >> 3, dw = 4 * j + (lane & 3), hi = (lane >> 2) & 1;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int b = 0; b < nb; b++) {
+        const uint8_t* blk = arow + (int64_t)b * kQ4KBytes;
+        const uint4 hdr = ld_u128(blk);
+        const uint32_t qw = ld_u32(blk + 16 + 4 * dw);
+        int sc, m;
+        q4k_scale_min(hdr.y, hdr.z, hdr.w, j, sc, m);
+        const float s = f16_ieee(hdr.x) * (float)sc, mn = f16_ieee(hdr.x >> 16) * (float)m;
+        const uint32_t nib = (hi ? (qw >> 4) : qw) & 0x0F0F0F0Fu;
+        float4 v;
+        v.x = fmaf(s, (float)(nib & 0xFFu), -mn);
+        v.y = fmaf(s, (float)((nib >> 8) & 0xFFu), -mn);
+        v.z = fmaf(s, (float)((nib >> 16) & 0xFFu), -mn);
+        v.w = fmaf(s, (float)(nib >> 24), -mn);
+        __syncthreads();  // every chain is done with the previous block
+        *reinterpret_cast<float4*>(&deq[wave][4 * lane]) = v;
+        __syncthreads();
+        const float* bp = B + (int64_t)b * 256 * N + cc;
+#pragma unroll 4
+        for (int k = 0; k < 256; k++) {
+            const float bv = bp[(int64_t)k * N];
+#pragma unroll
+            for (int r = 0; r < 4; r++) acc[r] = bv * deq[r][k] + acc[r];
+        }
+    }
+    if (col >= N) return;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        if (r0 + r >= M) break;
+        float v = acc[r];
+        if (__builtin_isnan(v)) v = qmm_nan_bits(A + (int64_t)(r0 + r) * rowbytes, B, N, col, nb);
+        C[(int64_t)(r0 + r) * N + col] = v;
+    }
+}
+
+void launch_qmm_q4k(const uint8_t* A, const float* B, float* C, int M, int N, int K, hipStream_t s) {
+    if (K / 256 == 0) {  // the empty sum: the reference leaves C at its +0.0 start
+        launch_fill_zero(C, (int64_t)M * N, s);
+        return;
+    }
+    hipLaunchKernelGGL(k_qmm_q4k, dim3((N + 255) / 256, (M + 3) / 4), dim3(256), 0, s, A, B, C, M, N, K / 256);
+}
+
+// ----------------------------------------------------------------------------
 // Q8_K quantizer: one wave per 256-element block, lane l holds elements 4l..4l+3.
 // d = RN(amax/127), id = amax ? RN(127/amax) : 0, q = rint(RN(x*id)),
 // bsums[g] = sum of q[16g..16g+15] (lanes 4g..4g+3).

@@ -758,6 +758,7 @@ typedef _Float16 h16x8 __attribute__((ext_vector_type(8)));
 // ----------------------------------------------------------------------------
 constexpr int kSNanTile = 0;
 constexpr int kSNanQdot = 1;
+static_assert(kSNanTile != kSNanQdot, "the two NaN forms");
 
 __device__ __forceinline__ float f16_ref(uint32_t h, int mode) {
     if (!f16_is_nan(h)) return f16_ieee(h);

@@ -173,6 +173,26 @@ void bpd_qmatmul_q8_0_dispatch_s_gpu(const uint8_t* Wq_dev, const uint8_t* Xq_de
 void bpd_qmatmul_q8_0_llamafile_s_gpu(const uint8_t* W_dev, const float* X_dev, float* out_dev, int m_weight,
                                       int m_tokens, int K);
 
+/* ---- the reference's other CPU forms on the GPU ----
+ * bpd_qmm_q4k (bench/bpd_quant.c:114-137): C[M][N] = dequant(A_q4k[M][K]) . B[K][N], B and C
+ * row-major fp32; each cell the reference's sequential chain from +0.0 over k in element
+ * order: bit-identical to bpd_qmm_q4k, NaN bits included.  A 16-byte aligned. */
+void bpd_qmm_q4k_gpu(const uint8_t* A_dev, const float* B_dev, float* C_dev, int M, int N, int K);
+/* bpd_qdot_q8_0_q8_0_cpu (bench/bpd_cpu.c:4208-4259, the AVX1 build's pair order P) for every
+ * (activation row m, weight row n): out[m * N + n] = qdot(Wq row n, Xq row m, K/32).  Wq: N
+ * Q8_0 rows, Xq: M Q8_0 rows, of K/32 blocks each.  Bit-identical over the whole int8 range
+ * (the SSSE3 maddubs arithmetic is reproduced for -128 quants).  K <= 52,416. */
+void bpd_qdot_q8_0_q8_0_grid_gpu(const uint8_t* Wq_dev, const uint8_t* Xq_dev, float* out_dev, int M, int N, int K);
+/* The same cells in the scalar build's order S (bench/bpd_cpu.c:4263-4280), NaN bits included. */
+void bpd_qdot_q8_0_q8_0_grid_s_gpu(const uint8_t* Wq_dev, const uint8_t* Xq_dev, float* out_dev, int M, int N,
+                                   int K);
+/* bpd_qmatmul_q8_0_cpu(W, X, out, M = tokens, N = weight rows, K) (bench/bpd_cpu.c:4295-4315):
+ * quantize the M fp32 rows of X to Q8_0 (bpd_quant_q8_0_cpu), then out[m * N + n] = qdot:
+ * order P (the -mavx build) and order S (the -O2 build).  X 4-byte aligned; the quantized rows
+ * go to the stream's workspace.  The P form needs K <= 52,416. */
+void bpd_qmatmul_q8_0_gpu(const uint8_t* W_dev, const float* X_dev, float* out_dev, int M, int N, int K);
+void bpd_qmatmul_q8_0_s_gpu(const uint8_t* W_dev, const float* X_dev, float* out_dev, int M, int N, int K);
+
 /* ---- measurement helper (no counterpart in the reference) -------------------
  * Reads n16 16-byte chunks at p once, as fast as a plain streaming kernel can,
  * and writes *sink only if the data XORs to a magic value.  bench.py uses it for

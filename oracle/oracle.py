@@ -210,6 +210,15 @@ def qmatmul_q8_0(W, X, M, N, K, order="P"):
     return out
 
 
+def qdot_grid(Wq, Xq, M, N, K, order="P"):
+    """out[m * N + n] = bpdq_o_qdot_q8_0_{P,S}(Wq row n, Xq row m, K/32)."""
+    nb = K // 32
+    bpr = nb * 34
+    f = lib().bpdq_o_qdot_q8_0_P if order == "P" else lib().bpdq_o_qdot_q8_0_S
+    w0, x0 = Wq.ctypes.data, Xq.ctypes.data
+    return np.array([f(w0 + n * bpr, x0 + m * bpr, nb) for m in range(M) for n in range(N)], np.float32)
+
+
 def qmatmul_q8_0_llamafile(W, X, m_weight, m_tokens, K, order="T"):
     out = np.empty(m_weight * m_tokens, np.float32)
     lib().bpdq_o_qmatmul_q8_0_llamafile(_p(W), _p(X), _p(out), m_weight, m_tokens, K, ord(order))

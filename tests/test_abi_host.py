@@ -225,3 +225,14 @@ def test_call_refuses_names_without_a_signature():
     # arrive cut to its low 32 bits, so gpu.call only calls declared entry points
     with pytest.raises(KeyError, match="no ctypes signature"):
         gpu.call("bpd_not_declared_anywhere_gpu", 0x7F1234561000)
+
+
+def test_p_order_k_limit_is_refused_before_launch():
+    L = _native.load_hip()
+    L.bpd_gpu_last_error()
+    L.bpd_qdot_q8_0_q8_0_grid_gpu(0x1000, 0x2000, 0x3000, 1, 8, 52416 + 32)
+    assert "52416" in _err(7)
+    L.bpd_qmatmul_q8_0_gpu(0x1000, 0x2000, 0x3000, 1, 8, 52416 + 32)
+    _err(7)
+    L.bpd_qmm_q4k_gpu(0x1000, 0x2000, 0x3000, 2, 3, 300)
+    assert "multiple of 256" in _err(2)

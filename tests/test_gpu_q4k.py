@@ -168,3 +168,31 @@ def test_qmatmul_q4k_reference_order_nan_bits(dev, M, K):
         want = O.qmatmul_q4k(w, xv, M, K)
         assert np.isnan(want).any()
         assert_bits_equal(to_np(y), want, f"reference-order GEMV NaN bits {M}x{K}")
+
+
+@pytest.mark.parametrize("M,N,K", [(3, 5, 256), (64, 64, 4096), (7, 300, 512)])
+def test_qmm_q4k_matches_the_reference_chain(dev, M, N, K):
+    import torch
+
+    A = synth.q4k(M, K, synth.key(55, M))
+    B = synth.normal_f32(K * N, synth.key(56, N))
+    C = torch.full((M * N,), float("nan"), device=dev)
+    gpu.lib().bpd_gpu_set_stream(torch.cuda.current_stream().cuda_stream)
+    gpu.call("bpd_qmm_q4k_gpu", _dev_u8(A, dev), torch.from_numpy(B).to(dev), C, M, N, K)
+    assert_bits_equal(to_np(C), O.qmm_q4k(A, B, M, N, K), f"bpd_qmm_q4k {M}x{N}x{K}")
+
+
+def test_qmm_q4k_nan_bits(dev):
+    import torch
+
+    M, N, K = 6, 5, 512
+    A = synth.random_bytes(M * K // 256 * 144, synth.key(57, 1))
+    B = synth.normal_f32(K * N, synth.key(57, 2))
+    special = np.array([0x7FC00001, 0xFFC00002, 0x7F800003, 0xFF812345, 0x7F800000, 0xFF800000], np.uint32)
+    B[np.arange(special.size) * 401 % B.size] = special.view(np.float32)
+    C = torch.full((M * N,), 0.0, device=dev)
+    gpu.lib().bpd_gpu_set_stream(torch.cuda.current_stream().cuda_stream)
+    gpu.call("bpd_qmm_q4k_gpu", _dev_u8(A, dev), torch.from_numpy(B).to(dev), C, M, N, K)
+    want = O.qmm_q4k(A, B, M, N, K)
+    assert np.isnan(want).any()
+    assert_bits_equal(to_np(C), want, "bpd_qmm_q4k NaN bits")

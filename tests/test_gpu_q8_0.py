@@ -264,3 +264,40 @@ def test_workspace_growth_inside_capture_is_refused(dev):
         g2.replay()
         torch.cuda.synchronize()
         assert_bits_equal(to_np(out2), eager, "captured llamafile replay")
+
+
+# ------------------------------------------- bpd_qmatmul_q8_0_cpu's form: orders P and S
+
+def _q8_full_range(rows, nb, key):
+    """Q8_0 rows whose quants take every int8 value, -128 included, with realistic scales."""
+    raw = synth.random_bytes(rows * nb * 34, key).reshape(rows, nb, 34)
+    raw[:, :, :2] = synth.q8_0(rows, nb * 32, key ^ 0x77).reshape(rows, nb, 34)[:, :, :2]
+    raw[0, 0, 2:6] = 0x80                               # -128 in both operands for sure
+    return raw.reshape(-1).copy()
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 14336, 4096), (1, 4096, 14336), (3, 37, 224), (2, 9, 32), (5, 17, 4128)])
+def test_qdot_grid_orders_P_and_S_full_int8_range(dev, M, N, K):
+    nb = K // 32
+    Wq, Xq = _q8_full_range(N, nb, synth.key(51, N)), _q8_full_range(M, nb, synth.key(52, M))
+    wd, xd = _d(Wq, dev), _d(Xq, dev)
+    import torch
+
+    for name, order in (("bpd_qdot_q8_0_q8_0_grid_gpu", "P"), ("bpd_qdot_q8_0_q8_0_grid_s_gpu", "S")):
+        out = torch.full((M * N,), float("nan"), device=dev)
+        gpu.lib().bpd_gpu_set_stream(torch.cuda.current_stream().cuda_stream)
+        gpu.call(name, wd, xd, out, M, N, K)
+        assert_bits_equal(to_np(out), O.qdot_grid(Wq, Xq, M, N, K, order), f"qdot {order} {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 14336, 4096), (4, 300, 4096), (3, 6, 96), (2, 11, 224)])
+def test_qmatmul_q8_0_orders_P_and_S(dev, M, N, K):
+    import torch
+
+    W = synth.q8_0(N, K, synth.key(53, N))
+    X = synth.normal_f32(M * K, synth.key(54, M))
+    for name, order in (("bpd_qmatmul_q8_0_gpu", "P"), ("bpd_qmatmul_q8_0_s_gpu", "S")):
+        out = torch.full((M * N,), float("nan"), device=dev)
+        gpu.lib().bpd_gpu_set_stream(torch.cuda.current_stream().cuda_stream)
+        gpu.call(name, _d(W, dev), _d(X, dev), out, M, N, K)
+        assert_bits_equal(to_np(out), O.qmatmul_q8_0(W, X, M, N, K, order), f"qmatmul {order} {M}x{N}x{K}")

@@ -665,3 +665,63 @@ def test_q8_pad64_conversion_in_bounds(N, K):
     assert ((rec * 32 + e) < N * K).all()
     o = (b * N + n) * 64
     assert ((o + 4 + e) < N * nb * 64).all() and ((o + 36 + np.minimum(e, 27)) < N * nb * 64).all()
+
+
+# ---------------------------------------------------------------- bpd_qmm_q4k, qdot grid P
+
+@pytest.mark.parametrize("M,N,K", [(3, 5, 256), (64, 64, 4096), (7, 300, 512), (1, 1, 256), (5, 257, 768)])
+def test_qmm_q4k_in_bounds(M, N, K):
+    """k_qmm_q4k: grid (ceil(N/256), ceil(M/4)); wave w dequantizes row min(r0+w, M-1),
+    thread c reads B[k][min(c, N-1)], stores only c < N and rows < M; the NaN re-walk
+    reads the same ranges."""
+    nb = K // 256
+    a_size, b_size = M * nb * Q4K, K * N
+    l = lanes()
+    j, dw = l >> 3, 4 * (l >> 3) + (l & 3)
+    assert (16 + 4 * dw + 4).max() <= Q4K and (4 * l + 4).max() <= 256
+    gx, gy = (N + 255) // 256, (M + 3) // 4
+    for by in sorted({0, gy - 1}):
+        r0 = by * 4
+        for wave in range(4):
+            arow = min(r0 + wave, M - 1) * nb * Q4K
+            assert arow + (nb - 1) * Q4K + Q4K <= a_size
+        for bx in sorted({0, gx - 1}):
+            col = bx * 256 + np.arange(256)
+            cc = np.minimum(col, N - 1)
+            assert ((nb * 256 - 1) * N + cc).max() < b_size and cc.min() >= 0
+            for r in range(4):
+                if r0 + r < M:
+                    assert ((r0 + r) * N + col[col < N]).max() < M * N
+    # the NaN re-walk: qs byte 16 + 16j + (k & 15) of each block
+    assert 16 + 16 * 7 + 15 < Q4K
+
+
+@pytest.mark.parametrize("n_rows,M,K", [(14336, 1, 4096), (4096, 1, 14336), (37, 3, 224), (9, 2, 32),
+                                        (17, 5, 4128), (1, 1, 64), (8, 1, 52416)])
+def test_q8_0_qdot_P_in_bounds(n_rows, M, K):
+    """k_q8_0_qdot_P<8, 4>: LDS = 40 nb bytes; lane (L = 4h + i) loads block 2*min(p, np-1)+h
+    (<= nb-1) at +2+4i and +18+4i, its scale at +0; the odd tail block's dword L; spare
+    rows and waves clamp to row n_rows-1."""
+    nb, WPB = K // 32, 4
+    np_ = nb // 2
+    bpr = nb * Q80
+    assert nb * 40 <= 64 * 1024
+    l = lanes()
+    L, i, h = l & 7, l & 3, (l & 7) >> 2
+    assert (2 + 4 * i + 16 + 4).max() <= Q80 and (2 + 4 * L + 4).max() <= Q80
+    if np_ > 0:
+        assert 2 * (np_ - 1) + 1 <= nb - 1
+    waves = (n_rows + 7) // 8
+    grid = (waves + WPB - 1) // WPB
+    for blk in sorted({0, grid - 1}):
+        for wave in range(WPB):
+            row = (blk * WPB + wave) * 8 + (l >> 3)
+            row0 = min((blk * WPB + wave) * 8, n_rows - 1)
+            doff = (np.maximum(np.minimum(row, n_rows - 1), row0) - row0) * bpr
+            assert (row0 * bpr + doff).min() >= 0
+            last = row0 * bpr + doff + (nb - 1) * Q80 + Q80
+            assert last.max() <= n_rows * bpr
+            assert ((M - 1) * n_rows + row[row < n_rows]).max(initial=0) < M * n_rows
+    # the staged activation row: dword i of element group, i <= nb*8 - 1
+    n = nb * 8
+    assert ((n - 1) >> 3) * Q80 + 2 + 4 * ((n - 1) & 7) + 4 <= bpr
