@@ -6,11 +6,12 @@
 A step is one Q4_K x Q8_K GEMV at M=14336, K=4096 (the metric workload) with
 the weight, the Q8_K activation and the output already resident in HBM.  The
 weight rotates over >= 16 distinct copies (> 512 MB) so the 256 MB MALL cannot
-serve it.  The K timed launches are captured once in a HIP graph and replayed;
-HIP events on the graph's stream bracket the timed region, so the host's
-launch rate cannot hide or inflate kernel time.  `value` and
-`roofline.achieved` are the algorithmic bytes of one GEMV divided by the timed
-region / K.  The same method times, on the same rotating copies, a plain
+serve it.  The K timed launches are captured once in a HIP graph; each timed
+replay follows a short GPU spin on the same stream (so the graph is queued
+before the start event runs) and is bracketed by HIP events on the graph's
+stream, so the host's launch rate cannot hide or inflate kernel time.  The
+median over 7 replays is kept.  `value` and `roofline.achieved` are the
+algorithmic bytes of one GEMV divided by that median / K.  The same method times, on the same rotating copies, a plain
 streaming read of the weight's bytes (the single-launch HBM read floor of this
 size on this device), the cfg0 dequant, the cfg1 GEMV and the cfg2 Q8_0 GEMVs.
 Prints ONE JSON line.
@@ -45,7 +46,7 @@ def parse():
     ap.add_argument("--copies", type=int, default=16)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="metric GEMV only")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-runs", type=int, default=10)
     return ap.parse_args()
 
 
@@ -54,12 +55,26 @@ def log(msg):
 
 
 class Timer:
-    """Capture a list of library launches into one graph and time its replay."""
+    """Capture a list of library launches into one graph and time its replay.
+
+    Each timed replay is preceded on the same stream by a short GPU spin, so the
+    host has queued the graph before the start event runs: the events then
+    bracket the kernels alone, not the host's graph submission.  The result is
+    the median over `repeats` timed replays (one untimed replay warms the graph)."""
+
+    SPIN_CYCLES = 400_000  # ~0.2 ms at the MI355X shader clock
 
     def __init__(self, torch, lib, stream):
         self.torch, self.lib, self.stream = torch, lib, stream
+        try:
+            with torch.cuda.stream(stream):
+                torch.cuda._sleep(1000)
+            torch.cuda.synchronize()
+            self.spin = True
+        except Exception:  # no spin kernel in this torch build: time without the pre-roll
+            self.spin = False
 
-    def us_per_launch(self, launches, repeats=3):
+    def us_per_launch(self, launches, repeats=7):
         torch = self.torch
         g = torch.cuda.CUDAGraph()
         with torch.cuda.stream(self.stream):
@@ -68,68 +83,159 @@ class Timer:
                 for fn in launches:
                     fn()
             self.lib.bpd_gpu_set_stream(self.stream.cuda_stream)
-        best = None
+        times = []
         for i in range(repeats + 1):
             s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             torch.cuda.synchronize()
             with torch.cuda.stream(self.stream):
+                if self.spin:
+                    torch.cuda._sleep(self.SPIN_CYCLES)
                 s.record(self.stream)
                 g.replay()
                 e.record(self.stream)
             e.synchronize()
-            ms = s.elapsed_time(e)
             if i > 0:  # the first replay warms the graph
-                best = ms if best is None else min(best, ms)
+                times.append(s.elapsed_time(e))
         del g
-        return best * 1e3 / len(launches)
+        return float(np.median(times)) * 1e3 / len(launches)
 
 
-def cpu_baseline(w_host, x_host, seconds):
-    """Reference C bpd_qmatmul_q4k (bench/bpd_quant.c:88-109) on this host's cores,
-    rows split across threads (each row's bits are unchanged)."""
-    import ctypes
+# ---------------------------------------------------------------- CPU baseline
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _pinned_parallel(n_items, nthreads, work):
+    """Run work(i0, i1) over nthreads disjoint ranges of [0, n_items), each thread pinned
+    to one CPU of this process's affinity set (ctypes releases the GIL during the C call)."""
     import threading
 
-    from oracle import oracle as O
-
-    nthreads = max(1, min(16, os.cpu_count() or 1))
-    R = O.ref("quant")
-    kind = "reference"
-    if R is not None:
-        fn = R.bpd_qmatmul_q4k
-        fn.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int] * 2
-    else:  # the in-repo restatement, identical bits
-        kind = "port"
-        fn = O.lib().bpdq_o_qmatmul_q4k
-    y = np.empty(M, np.float32)
-    rows_per = (M + nthreads - 1) // nthreads
-    row_bytes = (K // 256) * 144
+    cpus = sorted(os.sched_getaffinity(0))
+    per = -(-n_items // nthreads)
 
     def part(t):
-        r0, r1 = t * rows_per, min(M, (t + 1) * rows_per)
-        if r1 > r0:
-            fn(w_host.ctypes.data + r0 * row_bytes, x_host.ctypes.data, y.ctypes.data + 4 * r0, r1 - r0, K)
+        try:
+            os.sched_setaffinity(0, {cpus[t % len(cpus)]})  # this thread only (Linux)
+        except OSError:
+            pass
+        i0, i1 = t * per, min(n_items, (t + 1) * per)
+        if i1 > i0:
+            work(i0, i1)
 
-    def one():
-        ths = [threading.Thread(target=part, args=(t,)) for t in range(nthreads)]
-        for th in ths:
-            th.start()
-        for th in ths:
-            th.join()
+    if nthreads == 1:
+        part(0)
+        return
+    ths = [threading.Thread(target=part, args=(t,)) for t in range(nthreads)]
+    for th in ths:
+        th.start()
+    for th in ths:
+        th.join()
 
-    one()  # warm
-    n, t0 = 0, time.perf_counter()
-    while True:
-        one()
-        n += 1
-        if time.perf_counter() - t0 >= seconds:
-            break
-    dt = (time.perf_counter() - t0) / n
-    cpu_bytes = W_BYTES + K * 4 + Y_BYTES
-    return {"value": round(cpu_bytes / dt / 1e9, 3), "unit": "GB/s", "cores": nthreads, "kind": kind,
-            "sample": f"{n} full {M}x{K} fp32-x GEMVs of bpd_qmatmul_q4k (reference C, -O2, rows split over "
-                      f"{nthreads} threads) in {n * dt:.1f} s, {dt * 1e3:.2f} ms each; bytes counted as for the "
-                      f"GPU metric with fp32 x"}, y
+
+def _median_ms(run, runs):
+    run()  # warm
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        run()
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts)) * 1e3
+
+
+def cpu_baseline(w_host, x_host, runs=10):
+    """the reference C of the path on this host's cores, 1 core
+    and all cores (a pinned thread per core over disjoint rows / blocks, which leaves
+    every output's bits unchanged), median of `runs` runs per leg, full config sizes.
+    Legs: cfg0 bpd_dequant_q4k and the metric-shape bpd_qmatmul_q4k (bench/bpd_quant.c,
+    -O2); cfg2 bpd_quant_q8_0_cpu + bpd_qmatmul_q8_0_dispatch_cpu (bench/bpd_cpu.c +
+    bench/bpd_gemm_q8_0_cpu.c, -O2 -mavx -mssse3); and this build's own Q4_K x Q8_K C
+    oracle at the metric shape (no reference C exists for it).  Returns the result
+    object (its value: the metric-shape bpd_qmatmul_q4k on all cores) and that leg's
+    output for the GPU parity check."""
+    import ctypes
+
+    from bpd_substrate_amd import synth
+    from oracle import oracle as O
+
+    P, I = ctypes.c_void_p, ctypes.c_int
+    allc = max(1, min(16, len(os.sched_getaffinity(0))))  # the GPU box's CPU share is 16
+    RQ, RA = O.ref("quant"), O.ref("avx")
+    kind = "reference" if RQ is not None else "port"
+    if RQ is not None:
+        dq, mm = RQ.bpd_dequant_q4k, RQ.bpd_qmatmul_q4k
+        dq.argtypes, mm.argtypes = [P, P, I], [P, P, P, I, I]
+    else:  # the in-repo restatement, pinned bit-identical to it
+        dq, mm = O.lib().bpdq_o_dequant_q4k, O.lib().bpdq_o_qmatmul_q4k
+    legs = {}
+
+    def leg(name, run_1, run_n, work_bytes, extra):
+        r = {"1_core_ms": round(_median_ms(run_1, runs), 3), f"{allc}_cores_ms": round(_median_ms(run_n, runs), 3)}
+        r.update({"1_core_gb_s": round(work_bytes / r["1_core_ms"] / 1e6, 3),
+                  f"{allc}_cores_gb_s": round(work_bytes / r[f"{allc}_cores_ms"] / 1e6, 3)})
+        r.update(extra)
+        legs[name] = r
+        return r
+
+    # metric shape, reference order, fp32 x
+    y = np.empty(M, np.float32)
+    row_b = (K // 256) * 144
+    mm_work = lambda r0, r1: mm(w_host.ctypes.data + r0 * row_b, x_host.ctypes.data, y.ctypes.data + 4 * r0,
+                                r1 - r0, K)
+    m = leg("metric_bpd_qmatmul_q4k_14336x4096", lambda: mm_work(0, M),
+            lambda: _pinned_parallel(M, allc, mm_work), W_BYTES + K * 4 + Y_BYTES,
+            {"ref": "bench/bpd_quant.c:88-109", "flags": "-O2", "bytes": "W 33,030,144 + fp32 x + y"})
+    # cfg0 dequant
+    q0 = synth.q4k(DQ_BLOCKS, 256, synth.key(42, synth.STREAM["cfg0_w"]))
+    o0 = np.empty(DQ_BLOCKS * 256, np.float32)
+    dq_work = lambda b0, b1: dq(q0.ctypes.data + b0 * 144, o0.ctypes.data + b0 * 1024, b1 - b0)
+    r = leg("cfg0_bpd_dequant_q4k_4096x4096", lambda: dq_work(0, DQ_BLOCKS),
+            lambda: _pinned_parallel(DQ_BLOCKS, allc, dq_work), DQ_BYTES,
+            {"ref": "bench/bpd_quant.c:41-81", "flags": "-O2", "bytes": "76,546,048 (144 B in + 1 KiB out per block)"})
+    for c in ("1_core", f"{allc}_cores"):
+        r[f"{c}_gelem_s"] = round(DQ_BLOCKS * 256 / r[f"{c}_ms"] / 1e6, 3)
+    del q0, o0
+    # cfg2: quantize x, then the AVX1 build's dispatcher (tile order T)
+    if RA is not None:
+        qz, dp = RA.bpd_quant_q8_0_cpu, RA.bpd_qmatmul_q8_0_dispatch_cpu
+        qz.argtypes, dp.argtypes = [P, P, I], [P, P, P, I, I, I]
+        for name, (rows, k) in Q80_SHAPES.items():
+            W = synth.q8_0(rows, k, synth.key(42, synth.STREAM[f"cfg2_{name}"]))
+            X = synth.normal_f32(k, synth.key(42, synth.STREAM[f"cfg2_x_{name}"]))
+            Xq = np.empty(k // 32 * 34, np.uint8)
+            out = np.empty(rows, np.float32)
+            bpr = k // 32 * 34
+            d_work = lambda r0, r1, W=W, Xq=Xq, out=out, k=k, bpr=bpr: dp(
+                W.ctypes.data + r0 * bpr, Xq.ctypes.data, out.ctypes.data + 4 * r0, r1 - r0, 1, k)
+            run1 = lambda X=X, Xq=Xq, k=k, rows=rows, d_work=d_work: (qz(X.ctypes.data, Xq.ctypes.data, k),
+                                                                       d_work(0, rows))
+            runn = lambda X=X, Xq=Xq, k=k, rows=rows, d_work=d_work: (qz(X.ctypes.data, Xq.ctypes.data, k),
+                                                                       _pinned_parallel(rows, allc, d_work))
+            leg(f"cfg2_{name}_quant_q8_0+dispatch_{rows}x{k}", run1, runn, W.nbytes + k * 4 + rows * 4,
+                {"ref": "bench/bpd_cpu.c:4106-4136 + bench/bpd_gemm_q8_0_cpu.c:159-207",
+                 "flags": "-O2 -mavx -mssse3 (tile order T)"})
+            del W
+    # the build's Q4_K x Q8_K order (no reference C exists), metric shape
+    xq = O.quant_q8_k(x_host)
+    leg("metric_q4k_q8k_oracle_14336x4096", lambda: O.qmatmul_q4k_q8k(w_host, xq, M, K, 0, 1),
+        lambda: O.qmatmul_q4k_q8k(w_host, xq, M, K, 0, allc), ALG_BYTES,
+        {"ref": "none: no reference C exists for Q4_K x Q8_K; this build's C oracle", "flags": "-O2 -ffp-contract=off",
+         "threads": "unpinned pthreads over rows"})
+    mm_work(0, M)  # the output of the parity check below
+    res = {"value": m[f"{allc}_cores_gb_s"], "unit": "GB/s", "cores": allc, "kind": kind,
+           "sample": f"bpd_qmatmul_q4k (reference C, -O2) at the full 14336x4096 metric shape with fp32 x, rows "
+                     f"split over {allc} pinned threads, median of {runs} runs: {m[f'{allc}_cores_ms']} ms per "
+                     f"GEMV; bytes counted as for the GPU metric with fp32 x",
+           "cpu_model": _cpu_model(), "cpus_available": len(os.sched_getaffinity(0)), "runs_per_leg": runs,
+           "legs": legs}
+    return res, y
 
 
 def cfg3_layers(torch, dev, synth, n_layers=32):
@@ -382,6 +488,18 @@ def main():
                                               "frac_hbm": round(alg / u / 1e3 / HBM_PEAK_GBS, 4),
                                               "order": "llamafile tile (T), bit-exact"}
             del Ws, W
+        # the reference-order fp32-x GEMV (bpd_qmatmul_q4k_gpu, bit-identical to the CPU
+        # reference) at the metric shape, same rotating weight copies
+        y_c = torch.empty(M, dtype=torch.float32, device=dev)
+        rc_us = T.us_per_launch([(lambda i=i: L.bpd_qmatmul_q4k_gpu(wp[i % copies], x.data_ptr(), y_c.data_ptr(), M, K))
+                                 for i in range(100)])
+        gpu.check()
+        rc_bytes = W_BYTES + K * 4 + Y_BYTES
+        result["reference_order_gemv_14336x4096"] = {
+            "us": round(rc_us, 3), "gb_s": round(rc_bytes / rc_us / 1e3, 1),
+            "frac_hbm": round(rc_bytes / rc_us / 1e3 / HBM_PEAK_GBS, 4),
+            "order": "bpd_qmatmul_q4k's sequential fp32 chain per row (bench/bpd_quant.c:88-109), bit-exact"}
+        del y_c
         # cfg4: batched prefill, 512 tokens x 4096 x 14336 rows, order S on int8 MFMA
         W = torch.from_numpy(synth.q8_0(14336, 4096, synth.key(42, synth.STREAM["cfg2_up"]))).to(dev)
         X = torch.from_numpy(synth.normal_f32(512 * 4096, synth.key(42, synth.STREAM["cfg4_x"]))).to(dev)
@@ -402,8 +520,14 @@ def main():
         del layers, acts
 
     if not a.no_cpu:
-        log("CPU baseline (reference C bpd_qmatmul_q4k)")
-        cb, y_cpu = cpu_baseline(w_host, x_host, a.cpu_seconds)
+        log("CPU baseline (reference C, 1 core and all cores)")
+        cb, y_cpu = cpu_baseline(w_host, x_host, a.cpu_runs)
+        for name, gpu_us in (("metric_bpd_qmatmul_q4k_14336x4096", result.get("reference_order_gemv_14336x4096", {}).get("us")),
+                             ("metric_q4k_q8k_oracle_14336x4096", us),
+                             ("cfg0_bpd_dequant_q4k_4096x4096", result.get("dequant_cfg0", {}).get("us"))):
+            if gpu_us and name in cb["legs"]:
+                c = cb["legs"][name]
+                c["gpu_speedup_vs_all_cores"] = round(c[f"{cb['cores']}_cores_ms"] * 1e3 / gpu_us, 1)
         result["cpu_baseline"] = cb
         # the GPU reference-order entry point reproduces the CPU reference bit for bit
         y_chain = torch.empty(M, dtype=torch.float32, device=dev)

@@ -94,6 +94,12 @@ __device__ __forceinline__ void q4k_scale_min(uint32_t s0, uint32_t s1, uint32_t
     m = (int)(j < 4 ? (b & 63u) : m_hi);
 }
 
+// Workgroup barrier for LDS traffic only: this wave's LDS operations complete, then
+// s_barrier.  Unlike __syncthreads() it does not wait for the wave's outstanding
+// global loads, so a register prefetch stays in flight across it.  Only for
+// kernels whose waves exchange data through LDS alone.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }

@@ -4,6 +4,9 @@
 //   k_qmatmul_q4k_chain    reference-order GEMV with fp32 x (one fp32 chain per row)
 //   k_quant_q8k            fp32 -> Q8_K activation blocks
 //   k_q4k_q8k_gemv<ORDER,R> Q4_K x Q8_K GEMV, integer sub-block sums + fixed fp32 tree
+#include <mutex>
+
+#include "../../include/bpdq.h"
 #include "bpdq_device.h"
 #include "bpdq_launch.h"
 #include "bpdq_math.h"
@@ -84,11 +87,29 @@ void launch_dequant_q4k(const uint8_t* q, float* out, int n_blocks, int order, h
         hipLaunchKernelGGL(k_dequant_q4k<1>, grid, dim3(256), 0, s, q, out, n_blocks);
 }
 
-// The x86 bits of a row of the reference-order GEMV whose sum came out NaN.  On
-// x86 the first NaN of the chain sticks: sum + p keeps sum's NaN, w*x keeps w's
-// (the reference build puts the weight first), and an invalid operation gives
-// the default NaN.  So the row's bits are those of its first NaN event, found by
-// running the chain again with those rules.  Called only for NaN rows.
+// ----------------------------------------------------------------------------
+// Reference-order GEMV with fp32 x (bench/bpd_quant.c:88-109):
+//   y[r] = (((0 + w_0 x_0) + w_1 x_1) + ...) over k in bpd element order,
+// each product and each sum rounded once.  The chain is serial by definition,
+// so a row costs K dependent adds (~2.5 ns each on this GPU) however it is
+// mapped; everything else is kept off that chain.
+//
+// A workgroup owns 64 rows and has 5 waves.  Waves 1-4 (producers) turn the
+// rows' weights into products RN(w_k * x_k), half a Q4_K block (128 elements,
+// sub-blocks 4h..4h+3) per chunk: lane (s, r) = (wave-1, lane) takes sub-block
+// 4h+s of row r, i.e. one 16-byte qs load for 32 consecutive elements, the
+// block header, and x of those 32 elements (wave-uniform: scalar loads).  The
+// weight loads run kChainAhead chunks ahead in registers.  The products go to a
+// two-slot LDS ring stored [k/4][row][4], so wave 0 (consumer) lane r reads
+// its row's next 4 products as one float4 and only adds, in order.  One
+// barrier per chunk.  Rows are independent and every product and sum is the
+// reference's, so the output is bpd_qmatmul_q4k's bit for bit.
+// ----------------------------------------------------------------------------
+// The x86 bits of a row whose sum came out NaN.  On x86 the first NaN of the
+// chain sticks: sum + p keeps sum's NaN, w*x keeps w's (the reference build
+// puts the weight first), and an invalid operation gives the default NaN.  So
+// the row's bits are those of its first NaN event, found by running the chain
+// again with those rules.  Called only for NaN rows.
 __device__ __noinline__ float chain_nan_bits(const uint8_t* __restrict__ rp, const float* __restrict__ x, int nb) {
     float sum = 0.0f;
     for (int b = 0; b < nb; b++) {
@@ -117,46 +138,189 @@ __device__ __noinline__ float chain_nan_bits(const uint8_t* __restrict__ rp, con
     return sum;
 }
 
-// ----------------------------------------------------------------------------
-// Reference-order GEMV with fp32 x (bench/bpd_quant.c:88-109): one lane per row
-// runs y = (((0 + w0*x0) + w1*x1) + ...) over k in bpd element order, each
-// product and each sum rounded once.  Rows are independent, so this is
-// bit-identical to the CPU reference; the chain itself is serial by definition.
-// ----------------------------------------------------------------------------
-__global__ __launch_bounds__(64) void k_qmatmul_q4k_chain(const uint8_t* __restrict__ w, const float* __restrict__ x,
-                                                          float* __restrict__ y, int M, int nb) {
-    const int row = blockIdx.x * 64 + threadIdx.x;
-    if (row >= M) return;
-    const uint8_t* rp = w + (int64_t)row * nb * kQ4KBytes;
-    float sum = 0.0f;
-    for (int b = 0; b < nb; b++) {
-        const uint8_t* blk = rp + (int64_t)b * kQ4KBytes;
-        const uint4 hdr = ld_u128(blk);
-        const float d = f16_ieee(hdr.x), dmin = f16_ieee(hdr.x >> 16);
-        const float* xb = x + (int64_t)b * 256;
-        for (int j = 0; j < 8; j++) {
-            int sc, m;
-            q4k_scale_min(hdr.y, hdr.z, hdr.w, j, sc, m);
-            const float scale = d * (float)sc, mn = dmin * (float)m;
-            const uint4 qv = ld_u128(blk + 16 + 16 * j);
-            const uint32_t qd[4] = {qv.x, qv.y, qv.z, qv.w};
+constexpr int kChainRows = 64;          // rows per workgroup = consumer lanes
+constexpr int kChainWaves = 8;          // 0: consumer (SIMD 0); 4: helps stage x, then exits; others: producers
+constexpr int kChainSb = 6;             // sub-blocks (of 32 elements) per chunk: one per producer wave
+constexpr int kChainElems = 32 * kChainSb;                        // 192 elements per chunk
+constexpr int kChainAhead = 4;          // chunks of weight loads in flight per producer lane
+constexpr int kChainRing = 2 * (kChainElems / 4) * kChainRows;  // float4s of the product ring (96 KB)
+constexpr int kChainXMax = 16384;       // x staged in LDS up to this K (ring + x <= 160 KB)
+
+// Producer lane's registers for one chunk: its sub-block's block header and 16-byte qs slice.
+struct ChainLoad {
+    uint4 hdr, qs;
+};
+
+__device__ __forceinline__ ChainLoad chain_load(const uint8_t* __restrict__ rp, int c, int p, int nsb) {
+    const int sb = min(kChainSb * c + p, nsb - 1);  // sub-blocks past the end repeat the last one (not used)
+    const uint8_t* blk = rp + (int64_t)(sb >> 3) * kQ4KBytes;
+    return ChainLoad{ld_u128(blk), ld_u128(blk + 16 + 16 * (sb & 7))};
+}
+
+// v_cvt_f32_ubyteN: byte N of v as an fp32 (the compiler otherwise extracts it with a
+// separate v_bfe_u32 once the byte is known to hold a nibble).
+template <int N>
+__device__ __forceinline__ float cvt_ubyte(uint32_t v) {
+    float r;
+    if constexpr (N == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(v));
+    if constexpr (N == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(v));
+    if constexpr (N == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(v));
+    if constexpr (N == 3) asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(v));
+    return r;
+}
+
+// Products RN(RN(scale*q - mn) * x) of 32 elements (one sub-block) into the ring:
+// elements 4g..4g+3 take the low (g < 4) or high nibbles of qs dword g & 3.
+__device__ __forceinline__ void chain_products(float4* __restrict__ dst, const uint4 qv, const float4 (&xv)[8],
+                                               float scale, float mn) {
+    const uint32_t qd[4] = {qv.x, qv.y, qv.z, qv.w};
 #pragma unroll
-            for (int k = 0; k < 16; k++) {
-                const float v = fmaf(scale, (float)((qd[k >> 2] >> (8 * (k & 3))) & 15u), -mn);
-                sum = sum + v * xb[32 * j + k];
-            }
+    for (int g = 0; g < 8; g++) {
+        const uint32_t nib = (g < 4 ? qd[g & 3] : qd[g & 3] >> 4) & 0x0F0F0F0Fu;
+        float4 o;
+        o.x = fmaf(scale, cvt_ubyte<0>(nib), -mn) * xv[g].x;
+        o.y = fmaf(scale, cvt_ubyte<1>(nib), -mn) * xv[g].y;
+        o.z = fmaf(scale, cvt_ubyte<2>(nib), -mn) * xv[g].z;
+        o.w = fmaf(scale, cvt_ubyte<3>(nib), -mn) * xv[g].w;
+        dst[g * kChainRows] = o;
+    }
+}
+
+// XL: x staged once per workgroup in LDS (K <= kChainXMax), else read from global memory.
+template <bool XL>
+__global__ __launch_bounds__(64 * kChainWaves) void k_qmatmul_q4k_chain(const uint8_t* __restrict__ w,
+                                                                        const float* __restrict__ x,
+                                                                        float* __restrict__ y, int M, int nb) {
+    constexpr int NT = 64 * kChainWaves;
+    constexpr int E4 = kChainElems / 4;
+    extern __shared__ __align__(16) float4 chain_lds[];
+    float4(*prod)[E4][kChainRows] = reinterpret_cast<float4(*)[E4][kChainRows]>(chain_lds);
+    float* xl = reinterpret_cast<float*>(chain_lds + kChainRing);
+    const int lane = threadIdx.x & 63;
+    // waves go to SIMDs round-robin: 0 and 4 share SIMD 0, the producers take SIMDs 1-3 two each
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int row0 = blockIdx.x * kChainRows;
+    const int nsb = 8 * nb, nch = (nsb + kChainSb - 1) / kChainSb;
+    const int64_t rowbytes = (int64_t)nb * kQ4KBytes;
+    const int p = wave < 4 ? wave - 1 : wave - 2;  // producers 1,2,3,5,6,7: sub-block 6c + p of chunk c
+    const bool producer = (wave & 3) != 0;
+    const uint8_t* rp = w + (int64_t)min(row0 + lane, M - 1) * rowbytes;  // rows past M repeat row M-1
+    ChainLoad ring[kChainAhead];
+    if (producer) {
 #pragma unroll
-            for (int k = 0; k < 16; k++) {
-                const float v = fmaf(scale, (float)((qd[k >> 2] >> (8 * (k & 3) + 4)) & 15u), -mn);
-                sum = sum + v * xb[32 * j + 16 + k];
+        for (int a = 0; a < kChainAhead; a++) ring[a] = chain_load(rp, a, p, nsb);
+    }
+    if (XL) {  // every thread copies x to LDS, 4 loads in flight, while the weight loads are too
+        const float4* x4 = reinterpret_cast<const float4*>(x);
+        float4* xl4 = reinterpret_cast<float4*>(xl);
+        const int n4 = nb * 64;
+        for (int i0 = threadIdx.x; i0 < n4; i0 += 4 * NT) {
+            float4 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) v[u] = x4[min(i0 + NT * u, n4 - 1)];
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+                if (i0 + NT * u < n4) xl4[i0 + NT * u] = v[u];
+        }
+        lds_barrier();
+    }
+    if (wave == 4) return;  // a finished wave no longer takes part in s_barrier
+    if (wave == 0) {
+        // the chain: sum = RN(sum + p_k) in element order; chunk c holds elements
+        // [192c, 192c + 192) (the last chunk may hold fewer: its tail is never read).
+        // Reads go out 12 float4s ahead of the adds.
+        float sum = 0.0f;
+        for (int c = 0; c < nch; c++) {
+            lds_barrier();  // chunk c is in slot c & 1
+            const int n4 = min(kChainElems, 32 * (nsb - kChainSb * c)) / 4;
+            if (n4 == E4) {
+                float4 v[E4];
+#pragma unroll
+                for (int k4 = 0; k4 < 12; k4++) v[k4] = prod[c & 1][k4][lane];
+#pragma unroll
+                for (int g = 0; g < E4 / 12; g++) {
+                    if (g + 1 < E4 / 12) {
+#pragma unroll
+                        for (int k4 = 12 * (g + 1); k4 < 12 * (g + 2); k4++) v[k4] = prod[c & 1][k4][lane];
+                    }
+#pragma unroll
+                    for (int k4 = 12 * g; k4 < 12 * (g + 1); k4++) {
+                        sum = sum + v[k4].x;
+                        sum = sum + v[k4].y;
+                        sum = sum + v[k4].z;
+                        sum = sum + v[k4].w;
+                    }
+                }
+            } else {
+                for (int k4 = 0; k4 < n4; k4++) {
+                    const float4 v = prod[c & 1][k4][lane];
+                    sum = sum + v.x;
+                    sum = sum + v.y;
+                    sum = sum + v.z;
+                    sum = sum + v.w;
+                }
             }
         }
+        const int row = row0 + lane;
+        if (row < M) y[row] = __builtin_isnan(sum) ? chain_nan_bits(w + (int64_t)row * rowbytes, x, nb) : sum;
+        return;
     }
-    y[row] = __builtin_isnan(sum) ? chain_nan_bits(rp, x, nb) : sum;
+    for (int c0 = 0; c0 < nch; c0 += kChainAhead) {
+#pragma unroll
+        for (int a = 0; a < kChainAhead; a++) {
+            const int c = c0 + a;
+            const int sb = kChainSb * c + p;  // wave-uniform
+            if (c < nch && sb < nsb) {
+                const ChainLoad ld = ring[a];
+                // the 8 x reads before the first product write: x and the ring share LDS,
+                // so a read after a write could not be moved above it
+                const float* xs = (XL ? xl : x) + (int64_t)32 * sb;
+                float4 xv[8];
+#pragma unroll
+                for (int g = 0; g < 8; g++) xv[g] = *reinterpret_cast<const float4*>(xs + 4 * g);
+                int sc, m;
+                q4k_scale_min(ld.hdr.y, ld.hdr.z, ld.hdr.w, sb & 7, sc, m);
+                chain_products(&prod[c & 1][8 * p][lane], ld.qs, xv, f16_ieee(ld.hdr.x) * (float)sc,
+                               f16_ieee(ld.hdr.x >> 16) * (float)m);
+            }
+            // refill the slot after its last use (so the loads can take its registers), on
+            // every path, so the count of loads in flight is the same whichever chunks exist
+            ring[a] = chain_load(rp, c + kChainAhead, p, nsb);
+            // chunk c written: the consumer's barrier c.  Producers and consumer pass
+            // exactly nch barriers each; the weight loads of the next chunks stay in flight.
+            if (c < nch) lds_barrier();
+        }
+    }
 }
 
 void launch_qmatmul_q4k_chain(const uint8_t* w, const float* x, float* y, int M, int K, hipStream_t s) {
-    hipLaunchKernelGGL(k_qmatmul_q4k_chain, dim3((M + 63) / 64), dim3(64), 0, s, w, x, y, M, K / 256);
+    const int nb = K / 256;
+    if (nb == 0) {  // the empty sum
+        launch_fill_zero(y, M, s);
+        return;
+    }
+    const dim3 grid((M + kChainRows - 1) / kChainRows), block(64 * kChainWaves);
+    // more than 64 KB of dynamic LDS is asked for once per process
+    static std::once_flag once;
+    static bool lds_ok = false;
+    std::call_once(once, [] {
+        lds_ok = true;
+        for (const void* k : {reinterpret_cast<const void*>(&k_qmatmul_q4k_chain<true>),
+                              reinterpret_cast<const void*>(&k_qmatmul_q4k_chain<false>)})
+            if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
+                lds_ok = false;
+        (void)hipGetLastError();
+    });
+    if (!lds_ok) {
+        abi_error(BPDQ_ERR_HIP, "bpd_qmatmul_q4k_gpu", "the 96 KB LDS ring of the chain kernel was refused");
+        return;
+    }
+    const bool xl = K <= kChainXMax && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+    if (xl)
+        hipLaunchKernelGGL(k_qmatmul_q4k_chain<true>, grid, block, kChainRing * 16 + (size_t)K * 4, s, w, x, y, M,
+                           nb);
+    else
+        hipLaunchKernelGGL(k_qmatmul_q4k_chain<false>, grid, block, kChainRing * 16, s, w, x, y, M, nb);
 }
 
 // ----------------------------------------------------------------------------

@@ -725,3 +725,39 @@ def test_q8_0_qdot_P_in_bounds(n_rows, M, K):
     # the staged activation row: dword i of element group, i <= nb*8 - 1
     n = nb * 8
     assert ((n - 1) >> 3) * Q80 + 2 + 4 * ((n - 1) & 7) + 4 <= bpr
+
+
+@pytest.mark.parametrize("M,K", [(16, 256), (16, 4096), (77, 512), (4096, 4096), (300, 256), (14336, 4096),
+                                 (64, 2048), (1, 1536), (5, 14336), (3, 16384), (2, 16640)])
+def test_qmatmul_q4k_chain_in_bounds_and_barriers(M, K):
+    """k_qmatmul_q4k_chain: chunk c holds sub-blocks 6c..6c+5; producer p loads sub-blocks
+    min(6c + 2p + t, nsb - 1) of row min(row0+r, M-1) (header + 16-byte qs slice), reads x of
+    elements 32 sb .. 32 sb + 31 and writes prod[c&1][8(2p+t) + g][r] only for sb < nsb;
+    the consumer reads the chunk's first min(192, 32(nsb - 6c)) products, exactly what the
+    producers wrote; consumer and producers each pass nch barriers (plus the x-staging one)."""
+    nb, rows, ahead, sbc = K // 256, 64, 4, 6
+    nsb = 8 * nb
+    nch = -(-nsb // sbc)
+    rowbytes = nb * Q4K
+    for c in range(nch + ahead):
+        written = set()
+        for p in range(3):
+            for t in range(2):
+                sb = sbc * c + 2 * p + t
+                sbl = min(sb, nsb - 1)
+                assert (sbl >> 3) * Q4K + 16 + 16 * (sbl & 7) + 16 <= rowbytes
+                if c < nch and sb < nsb:
+                    assert 32 * sb + 31 < K
+                    k4 = 8 * (2 * p + t)
+                    assert k4 + 7 < 48
+                    written.update(range(k4, k4 + 8))
+        if c < nch:
+            n4 = min(192, 32 * (nsb - sbc * c)) // 4
+            assert set(range(n4)) <= written
+    assert 96 * 1024 + (K * 4 if K <= 16384 else 0) <= 160 * 1024
+    grid = (M + rows - 1) // rows
+    for bx in sorted({0, grid - 1}):
+        r = np.minimum(bx * rows + np.arange(rows), M - 1)
+        assert (r * rowbytes + rowbytes).max() <= M * rowbytes
+    producer_barriers = sum(1 for c0 in range(0, nch, ahead) for a in range(ahead) if c0 + a < nch)
+    assert producer_barriers == nch
