@@ -6,12 +6,14 @@
 A step is one Q4_K x Q8_K GEMV at M=14336, K=4096 (the metric workload) with
 the weight, the Q8_K activation and the output already resident in HBM.  The
 weight rotates over >= 16 distinct copies (> 512 MB) so the 256 MB MALL cannot
-serve it.  The K timed launches are captured once in a HIP graph; each timed
-replay follows a short GPU spin on the same stream (so the graph is queued
-before the start event runs) and is bracketed by HIP events on the graph's
-stream, so the host's launch rate cannot hide or inflate kernel time.  The
-median over 7 replays is kept.  `value` and `roofline.achieved` are the
-algorithmic bytes of one GEMV divided by that median / K.  The same method times, on the same rotating copies, a plain
+serve it.  The K timed launches go back to back on one stream behind a GPU
+spin (so the host has queued them before the start event runs): as eager
+launches after a few untimed warm-up launches for K <= 64 (the driver's
+--steps 20), as one HIP graph for longer regions.  HIP events on that stream
+bracket the K launches, so the host's launch rate cannot hide or inflate
+kernel time; the median over 7 timed regions is kept.  `value` and
+`roofline.achieved` are the algorithmic bytes of one GEMV divided by that
+median / K.  The same method times, on the same rotating copies, a plain
 streaming read of the weight's bytes (the single-launch HBM read floor of this
 size on this device), the cfg0 dequant, the cfg1 GEMV and the cfg2 Q8_0 GEMVs.
 Prints ONE JSON line.
@@ -55,14 +57,20 @@ def log(msg):
 
 
 class Timer:
-    """Capture a list of library launches into one graph and time its replay.
+    """Time K back-to-back library launches on one stream.
 
-    Each timed replay is preceded on the same stream by a short GPU spin, so the
-    host has queued the graph before the start event runs: the events then
-    bracket the kernels alone, not the host's graph submission.  The result is
-    the median over `repeats` timed replays (one untimed replay warms the graph)."""
+    Short regions (K <= EAGER_MAX, as the driver's --steps 20) are timed as eager
+    launches: a GPU spin and a few untimed warm-up launches go first on the same
+    stream, so the host has queued all K launches before the start event runs and the
+    GPU goes straight from warm-up into the timed launches.  Longer regions are one
+    HIP graph of the K launches, replayed after the same spin (a graph replay carries
+    a fixed ~8 us of its own on this GPU, which a 20-launch region would count as
+    0.4 us per launch; eager launches carry a smaller per-launch gap instead).  HIP
+    events on the stream bracket the K launches; the median over `repeats` timed
+    regions is kept."""
 
-    SPIN_CYCLES = 400_000  # ~0.2 ms at the MI355X shader clock
+    SPIN_CYCLES = 1_000_000  # ~0.4 ms at the MI355X shader clock: covers the host's queueing
+    EAGER_MAX = 64
 
     def __init__(self, torch, lib, stream):
         self.torch, self.lib, self.stream = torch, lib, stream
@@ -74,8 +82,35 @@ class Timer:
         except Exception:  # no spin kernel in this torch build: time without the pre-roll
             self.spin = False
 
-    def us_per_launch(self, launches, repeats=7):
+    def _region(self, pre, body):
         torch = self.torch
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(self.stream):
+            self.lib.bpd_gpu_set_stream(self.stream.cuda_stream)
+            if self.spin:
+                torch.cuda._sleep(self.SPIN_CYCLES)
+            pre()
+            s.record(self.stream)
+            body()
+            e.record(self.stream)
+        e.synchronize()
+        return s.elapsed_time(e)
+
+    def us_per_launch(self, launches, repeats=7, graph=None):
+        """graph: None picks by K; True always captures (for "launches" that are whole
+        decode steps of hundreds of kernels, which the host could not queue ahead)."""
+        torch = self.torch
+        if not graph and len(launches) <= self.EAGER_MAX:
+            warm = launches[-min(4, len(launches)):]
+
+            def run_all(fs):
+                for fn in fs:
+                    fn()
+
+            self._region(lambda: None, lambda: run_all(launches))  # first use: warms caches and clocks
+            times = [self._region(lambda: run_all(warm), lambda: run_all(launches)) for _ in range(repeats)]
+            return float(np.median(times)) * 1e3 / len(launches)
         g = torch.cuda.CUDAGraph()
         with torch.cuda.stream(self.stream):
             with torch.cuda.graph(g, stream=self.stream):
@@ -83,19 +118,8 @@ class Timer:
                 for fn in launches:
                     fn()
             self.lib.bpd_gpu_set_stream(self.stream.cuda_stream)
-        times = []
-        for i in range(repeats + 1):
-            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            torch.cuda.synchronize()
-            with torch.cuda.stream(self.stream):
-                if self.spin:
-                    torch.cuda._sleep(self.SPIN_CYCLES)
-                s.record(self.stream)
-                g.replay()
-                e.record(self.stream)
-            e.synchronize()
-            if i > 0:  # the first replay warms the graph
-                times.append(s.elapsed_time(e))
+        self._region(lambda: None, g.replay)  # the first replay warms the graph
+        times = [self._region(lambda: None, g.replay) for _ in range(repeats)]
         del g
         return float(np.median(times)) * 1e3 / len(launches)
 
@@ -272,7 +296,7 @@ def decode_chain(torch, L, T, dev, gpu, layers, acts, tokens=10):
         chain.step(acts)
         torch.cuda.synchronize()
         gpu.check()
-        us = T.us_per_launch([lambda: chain.step(acts)] * tokens)  # us per token
+        us = T.us_per_launch([lambda: chain.step(acts)] * tokens, graph=True)  # us per token
         wb = chain.weight_bytes()
         gpu.check()
         r = {"us_per_token": round(us, 1), "tokens_per_s": round(1e6 / us, 1), "weight_bytes": wb,
@@ -311,7 +335,7 @@ def decode_step(torch, L, T, dev, gpu, synth, layers, tokens=10, max_seq=4096, v
     wb = sum(t.numel() for lw in layers for t in (getattr(lw, n) for n in llama.MATRICES)) + lm.numel()
     out = {"weight_bytes": wb, "vocab": vocab, "max_seq": max_seq, "launches_per_token": 7 * len(layers) + 3}
     for pos0 in (0, 2048):
-        us = T.us_per_launch([(lambda t=t: m.enqueue(embs[t], pos0 + t)) for t in range(tokens)])
+        us = T.us_per_launch([(lambda t=t: m.enqueue(embs[t], pos0 + t)) for t in range(tokens)], graph=True)
         gpu.check()
         out[f"pos{pos0}"] = {"us_per_token": round(us, 1), "tokens_per_s": round(1e6 / us, 1),
                              "weight_gb_s": round(wb / us / 1e3, 1),
@@ -402,7 +426,9 @@ def main():
         "dtype": "int8 dot4 / fp32 (Q4_K x Q8_K)",
         "data": "synthetic (seeded splitmix64 Q4_K blocks per benchmark config; x ~ N(0,1) -> Q8_K)",
         "config": {"workload": "Q4_K x Q8_K GEMV, M=14336, K=4096, batch 1 (the headline metric shape)",
-                   "weight_copies": copies, "timing": "HIP graph of `steps` launches, events on its stream"},
+                   "weight_copies": copies,
+                   "timing": ("eager" if a.steps <= Timer.EAGER_MAX else "HIP graph of") +
+                             " `steps` back-to-back launches behind a GPU spin, events on their stream, median of 7"},
         "pct_of_peak": round(100 * value / HBM_PEAK_GBS, 2),
         "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(value / HBM_PEAK_GBS, 4), "traffic": load_traffic(),
