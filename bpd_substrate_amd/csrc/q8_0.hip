@@ -7,8 +7,8 @@
 //                         (bench/bpd_gemm_q8_0_cpu.c:32-86), pipelined chains
 //   k_q8_0_gemv_TP        the same cells, block products by producer waves and the
 //                         chains from LDS (few rows, long rows)
-//   k_q8_0_gemv_V         the same cells, each wave streaming its 4 rows as 16-byte
-//                         lanes through its own LDS slot, two lanes per chain
+//   k_q8_0_gemv_V         the same cells, each wave streaming its 2 rows as 16-byte
+//                         lanes through its own LDS slot, four lanes per chain
 //   k_q8_0_gemm_T         the same cells, plain, for rows too long to stage
 //   k_q8_pad64            fp32 -> the padded Q8 layout (inference/llamatov_c_inference.py:88-100)
 //   k_q8_0_gemm_S(H)      the scalar order S on int8 MFMA (prefill)
@@ -358,47 +358,55 @@ __global__ __launch_bounds__(320) void k_q8_0_gemv_TP(const uint8_t* __restrict_
 }
 
 // ----------------------------------------------------------------------------
-// The same order T for 34-byte rows read as 16-byte lanes, one wave per 4 rows
-// and two lanes per chain, with nothing shared between the waves but the
+// The same order T for 34-byte rows read as 16-byte lanes, one wave per 2 rows
+// and four lanes per chain, with nothing shared between the waves but the
 // activation row.  The loads of k_q8_0_gemv_T (a dword and a 16-bit word per
 // lane and block) reach 3.6 TB/s at the cfg2 shapes even without arithmetic;
-// 16-byte lanes over the same bytes reach 5.9.
-// Each wave streams its 4 rows in chunks of 32 blocks (1088 bytes of a row, 68
-// aligned 16-byte pieces, 272 pieces for the 4 rows: 5 loads per lane, the 5th
-// on lanes 0..15) with 2 chunks in flight in registers, and stages the current
-// chunk in a private LDS slot (1248-byte row pitch).  It then forms the
-// chunk's 4 x 32 scale products RN(Ad*Bd) once (2 per lane).
-// Lane (row, L, h), lane index 16 row + 2L + h, computes the products
-// RN(RN(Ad*Bd) * float(p_L)) of the blocks b with b % 2 == h: the quant dword at
+// 16-byte lanes over the same bytes reach 5.9, and more so with 2 rows per wave
+// than with 4 (4096x14336 read alone: 10.7 us against 12.5).
+// Each wave streams its 2 rows in chunks of 32 blocks (1088 bytes of a row, 68
+// aligned 16-byte pieces, 136 pieces for the 2 rows: 3 loads per lane, the 3rd
+// on lanes 0..7) with 2 chunks in flight in registers, and stages the current
+// chunk in a private LDS slot (1248-byte row pitch).  It then forms the chunk's
+// 2 x 32 scale products RN(Ad*Bd) once (one per lane).
+// Lane (row, L, q), lane index 32 row + 4L + q, computes the products
+// RN(RN(Ad*Bd) * float(p_L)) of the blocks b with b % 4 == q: the quant dword at
 // byte 34b + 2 + 4L (two aligned LDS dwords and v_alignbit), the activation
-// dwords and scale products four blocks at a time from copies split by block
-// parity.  Both lanes of a pair then extend the same chain
-//   acc_L = RN(p_L(b) + acc_L),  acc_L = RN(p_L(b+1) + acc_L)
-// taking the even block's product from lane 2L and the odd one's from lane
-// 2L+1 (DPP quad_perm in the adds), so they hold identical accumulators.
+// dwords and scale products four blocks at a time from copies split by b % 4.
+// The four lanes of a quad then extend the same chain
+//   acc_L = RN(p_L(b) + acc_L), ..., acc_L = RN(p_L(b+3) + acc_L)
+// taking block b+j's product from lane 4L+j (DPP quad_perm broadcast in the
+// adds), so they hold identical accumulators.
 // A wave waits only for its own loads and its own LDS writes (the LDS queue is
 // in order per wave): the one workgroup barrier is the one after the
 // activation row is staged.  The products, their order and the final combine
 // are k_q8_0_gemv_T's, so the bits are too.  Needs nb % 32 == 0 and W 16-byte
 // aligned.
+//
+// ALWAYS: every chunk step issues its 3 loads, past the last chunk a 16-byte
+// read of the wave's first row that every lane shares (discarded).  With the
+// loads unconditional the compiler's wait before a chunk's LDS writes leaves the
+// next chunk in flight; with them under a branch it waits for every load.  Each
+// form is faster on some shapes (measured, launch_wide).
 // ----------------------------------------------------------------------------
 typedef uint32_t v_u32x4 __attribute__((ext_vector_type(4)));  // native vectors: stay in VGPRs
 typedef float v_f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kVChunk = 32;                  // blocks per chunk
 constexpr int kVRowB = kVChunk * kQ80Bytes;  // 1088 bytes of a row per chunk
 constexpr int kVPieces = kVRowB / 16;        // 68 aligned 16-byte pieces
-constexpr int kVRows = 4;                    // rows per wave
+constexpr int kVRows = 2;                    // rows per wave
 constexpr int kVPitch = 1248;                // LDS row pitch, bytes
-constexpr int kVWavePieces = kVRows * kVPieces;  // 272 pieces per wave and chunk
+constexpr int kVWavePieces = kVRows * kVPieces;  // 136 pieces per wave and chunk
 constexpr int kVPer = (kVWavePieces + 63) / 64;  // loads per lane and chunk
-constexpr int kVScP = 20;                    // (row, parity) pitch of the scale products, floats
-constexpr int kVSlot = kVRows * kVPitch + 2 * kVRows * kVScP * 4;  // LDS bytes per wave
+constexpr int kVScP = kVChunk / 4 + 4;       // (row, b%4) pitch of the scale products, floats
+constexpr int kVSlot = kVRows * kVPitch + 4 * kVRows * kVScP * 4;  // LDS bytes per wave
 constexpr int kVAhead = 2;                   // chunks in flight per wave
+static_assert(kVPer == 3 && kVSlot % 16 == 0, "slot geometry");
 
-// activation quant dwords: [L][parity][nb/2 + 4] (the 16 rows of a read 4 banks apart)
-__host__ __device__ constexpr int v_xpitch(int nb) { return nb / 2 + 4; }
+// activation quant dwords: [L][b%4][nb/4 + 4] (the 32 rows of a read 4 banks apart)
+__host__ __device__ constexpr int v_xpitch(int nb) { return nb / 4 + 4; }
 __host__ __device__ constexpr size_t v_lds_bytes(int nb, int nw) {
-    return (size_t)(16 * v_xpitch(nb) + nb) * 4 + (size_t)nw * kVSlot;
+    return (size_t)(32 * v_xpitch(nb) + nb) * 4 + (size_t)nw * kVSlot;
 }
 
 // the wave's own LDS writes complete before its later reads (and the compiler
@@ -408,84 +416,93 @@ __device__ __forceinline__ void v_lds_order() { asm volatile("s_waitcnt lgkmcnt(
 __device__ __forceinline__ bool v_piece(int lane, int k) { return k < kVPer - 1 || lane + 64 * k < kVWavePieces; }
 
 // Non-temporal: each weight byte is read once, and every 16-byte piece of a
-// 128-byte line is loaded by the same instruction (cfg2 14336x4096 14.4 ->
-// 13.2 us, 4096x14336 15.4 -> 14.8 us against plain loads).
+// 128-byte line is loaded by the same instruction.  ALWAYS: lanes past the
+// wave's 136 pieces load piece 135 (off[] is clamped), an address another lane
+// of the same instruction loads; otherwise they load nothing (measured faster
+// for that form).
+template <bool ALWAYS>
 __device__ __forceinline__ void v_load(v_u32x4 (&v)[kVPer], const uint8_t* __restrict__ wbase,
-                                       const uint32_t (&off)[kVPer], int c, int lane) {
+                                       const uint32_t (&off)[kVPer], int c, bool real, int lane) {
+    const uint8_t* src = wbase + (real ? (uint32_t)c * kVRowB : 0u);
 #pragma unroll
     for (int k = 0; k < kVPer; k++)
-        if (v_piece(lane, k))
-            v[k] = __builtin_nontemporal_load(reinterpret_cast<const v_u32x4*>(wbase + off[k] + (uint32_t)c * kVRowB));
+        if (ALWAYS || v_piece(lane, k))
+            v[k] = __builtin_nontemporal_load(reinterpret_cast<const v_u32x4*>(src + (real ? off[k] : 0u)));
 }
 
-// v read from lane (lane & ~3) + SEL and lane (lane & ~3) + 2 + SEL of each quad
+// v read from lane (lane & ~3) + SEL of each quad
 template <int SEL>
-__device__ __forceinline__ float v_pair(float v) {
-    constexpr int ctrl = SEL | (SEL << 2) | ((2 + SEL) << 4) | ((2 + SEL) << 6);  // quad_perm
+__device__ __forceinline__ float v_quad(float v) {
+    constexpr int ctrl = SEL | (SEL << 2) | (SEL << 4) | (SEL << 6);  // quad_perm
     return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), ctrl, 0xF, 0xF, true));
 }
 
 // Chunk c = c0 + U (register slot U holds it; U is a template argument so that
 // the slots are indexed by constants): stage it, refill slot U with chunk
 // c + kVAhead, scale products, chains.
-template <int U>
+template <int U, bool ALWAYS>
 __device__ __forceinline__ void v_step(v_u32x4 (&pf)[kVAhead][kVPer], uint8_t* slot, float* sc,
                                        const uint8_t* __restrict__ wbase, const uint32_t (&off)[kVPer],
                                        const uint32_t (&dst)[kVPer], int lane, int c0, int nch,
                                        const uint32_t* __restrict__ xs, const float* __restrict__ xd, int xp,
                                        float& acc) {
     const int c = c0 + U;
-    if (c >= nch) return;  // uniform over the wave
+    if (!ALWAYS && c >= nch) return;  // uniform over the wave (the ALWAYS loop calls only c < nch)
 #pragma unroll
     for (int k = 0; k < kVPer; k++)
         if (v_piece(lane, k)) *reinterpret_cast<v_u32x4*>(slot + dst[k]) = pf[U][k];
-    if (c + kVAhead < nch) v_load(pf[U], wbase, off, c + kVAhead, lane);
+    if (ALWAYS)
+        v_load<true>(pf[U], wbase, off, c + kVAhead, c + kVAhead < nch, lane);
+    else if (c + kVAhead < nch)
+        v_load<false>(pf[U], wbase, off, c + kVAhead, true, lane);
     v_lds_order();
-#pragma unroll
-    for (int t = 0; t < kVRows * kVChunk / 64; t++) {
-        const int j = lane + 64 * t, r = j / kVChunk, bb = j % kVChunk;
+    {
+        const int r = lane / kVChunk, bb = lane % kVChunk;  // kVRows * kVChunk == 64
         const uint32_t ad = *reinterpret_cast<const uint16_t*>(slot + r * kVPitch + bb * kQ80Bytes);
-        sc[(2 * r + (bb & 1)) * kVScP + (bb >> 1)] = f16_ieee(ad) * xd[c * kVChunk + bb];
+        sc[(4 * r + (bb & 3)) * kVScP + (bb >> 2)] = f16_ieee(ad) * xd[c * kVChunk + bb];
     }
     v_lds_order();
-    const int h = lane & 1, L = (lane >> 1) & 7, rr = lane >> 4;
+    const int q = lane & 3, L = (lane >> 2) & 7, rr = lane >> 5;
     const uint8_t* rowp = slot + rr * kVPitch;
-    const uint32_t* xl = xs + (2 * L + h) * xp + c * (kVChunk / 2);
-    const float* sr = sc + (2 * rr + h) * kVScP;
-    // this lane's quant dword in block bb + h (bb even) is at 34 bb + ob; 34 bb = 0 mod 4
-    const int ob = 34 * h + 2 + 4 * L, oa = ob & ~3, sh = (ob & 3) * 8;
+    const uint32_t* xl = xs + (4 * L + q) * xp + c * (kVChunk / 4);
+    const float* sr = sc + (4 * rr + q) * kVScP;
+    // this lane's quant dword in block bb + q (bb % 4 == 0) is at 34 bb + ob; 34 bb = 0 mod 4
+    const int ob = 34 * q + 2 + 4 * L, oa = ob & ~3, sh = (ob & 3) * 8;
 #pragma unroll
-    for (int b8 = 0; b8 < kVChunk; b8 += 8) {
-        const v_u32x4 xq = *reinterpret_cast<const v_u32x4*>(xl + b8 / 2);  // blocks b8+h, b8+2+h, ...
-        const v_f32x4 s4 = *reinterpret_cast<const v_f32x4*>(sr + b8 / 2);
+    for (int b16 = 0; b16 < kVChunk; b16 += 16) {
+        const v_u32x4 xq = *reinterpret_cast<const v_u32x4*>(xl + b16 / 4);  // blocks b16+q, b16+4+q, ...
+        const v_f32x4 s4 = *reinterpret_cast<const v_f32x4*>(sr + b16 / 4);
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const int bb = b8 + 2 * j;
+            const int bb = b16 + 4 * j;
             const uint32_t lo = *reinterpret_cast<const uint32_t*>(rowp + 34 * bb + oa);
             const uint32_t hi = *reinterpret_cast<const uint32_t*>(rowp + 34 * bb + oa + 4);
             const int p = sdot4(__builtin_amdgcn_alignbit(hi, lo, sh), xq[j], 0);
             const float mine = s4[j] * (float)p;
-            acc = v_pair<0>(mine) + acc;  // block bb
-            acc = v_pair<1>(mine) + acc;  // block bb + 1
+            acc = v_quad<0>(mine) + acc;  // block bb
+            acc = v_quad<1>(mine) + acc;  // block bb + 1
+            acc = v_quad<2>(mine) + acc;  // block bb + 2
+            acc = v_quad<3>(mine) + acc;  // block bb + 3
         }
     }
 }
 
-// NW waves of 4 rows per workgroup; x quants in XR dwords per thread (nb*8 <= XR*64*NW).
-template <int NW, int XR>
+// NW waves of 2 rows per workgroup; x quants in XR dwords per thread (nb*8 <= XR*64*NW).
+template <int NW, int XR, bool ALWAYS>
 __global__ __launch_bounds__(64 * NW) void k_q8_0_gemv_V(const uint8_t* __restrict__ W,
                                                         const uint8_t* __restrict__ Xq, float* __restrict__ out,
                                                         int m_weight, int nb) {
     static_assert(kVAhead == 2, "one v_step call per chunk in flight");
+    static_assert(kVRows * kVChunk == 64, "one scale product per lane");
     constexpr int NT = 64 * NW;
     extern __shared__ __align__(16) uint32_t lds[];
     const int xp = v_xpitch(nb);
-    uint32_t* xs = lds;                                          // quant dword L of block b at (2L + b%2)*xp + b/2
-    float* xd = reinterpret_cast<float*>(lds + 16 * xp);         // [nb] activation scales
+    uint32_t* xs = lds;                                          // quant dword L of block b at (4L + b%4)*xp + b/4
+    float* xd = reinterpret_cast<float*>(lds + 32 * xp);         // [nb] activation scales
     const int tid = threadIdx.x, lane = tid & 63, tok = blockIdx.y;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    uint8_t* slot = reinterpret_cast<uint8_t*>(lds + 16 * xp + nb) + wave * kVSlot;
-    float* sc = reinterpret_cast<float*>(slot + kVRows * kVPitch);  // [row][parity][kVScP]
+    uint8_t* slot = reinterpret_cast<uint8_t*>(lds + 32 * xp + nb) + wave * kVSlot;
+    float* sc = reinterpret_cast<float*>(slot + kVRows * kVPitch);  // [row][b%4][kVScP]
     const int row0 = (blockIdx.x * NW + wave) * kVRows, nch = nb / kVChunk;
     const int64_t bpr = (int64_t)nb * kQ80Bytes;
     // rows past m_weight re-read row m_weight-1 (their cells are not written)
@@ -502,7 +519,7 @@ __global__ __launch_bounds__(64 * NW) void k_q8_0_gemv_V(const uint8_t* __restri
     }
 #pragma unroll
     for (int u = 0; u < XD; u++) xh[u] = ld_u16(xr + (int64_t)min(tid + u * NT, nb - 1) * kQ80Bytes);
-    // piece k of this lane: f = lane + 64k is row f/68, piece f%68 of the chunk
+    // piece k of this lane: f = min(lane + 64k, 135) is row f/68, piece f%68 of the chunk
     uint32_t off[kVPer], dst[kVPer];
 #pragma unroll
     for (int k = 0; k < kVPer; k++) {
@@ -513,27 +530,38 @@ __global__ __launch_bounds__(64 * NW) void k_q8_0_gemv_V(const uint8_t* __restri
     v_u32x4 pf[kVAhead][kVPer];
 #pragma unroll
     for (int a = 0; a < kVAhead; a++)
-        if (a < nch) v_load(pf[a], wbase, off, a, lane);
+        if (ALWAYS || a < nch) v_load<ALWAYS>(pf[a], wbase, off, a, a < nch, lane);
 #pragma unroll
     for (int u = 0; u < XR; u++) {
         const int i = tid + u * NT, b = i >> 3;
-        if (i < nb * 8) xs[(2 * (i & 7) + (b & 1)) * xp + (b >> 1)] = xq[u];
+        if (i < nb * 8) xs[(4 * (i & 7) + (b & 3)) * xp + (b >> 2)] = xq[u];
     }
 #pragma unroll
     for (int u = 0; u < XD; u++)
         if (tid + u * NT < nb) xd[tid + u * NT] = f16_ieee(xh[u]);
     __syncthreads();
     float acc = 0.0f;
-    for (int c0 = 0; c0 < nch; c0 += kVAhead) {
-        v_step<0>(pf, slot, sc, wbase, off, dst, lane, c0, nch, xs, xd, xp, acc);
-        v_step<1>(pf, slot, sc, wbase, off, dst, lane, c0, nch, xs, xd, xp, acc);
+    if (ALWAYS) {
+        // whole pairs of chunks, then an odd last one: no step of the loop body
+        // can be skipped, so every trip issues the same loads in the same order
+        int c0 = 0;
+        for (; c0 + 1 < nch; c0 += kVAhead) {
+            v_step<0, true>(pf, slot, sc, wbase, off, dst, lane, c0, nch, xs, xd, xp, acc);
+            v_step<1, true>(pf, slot, sc, wbase, off, dst, lane, c0, nch, xs, xd, xp, acc);
+        }
+        if (c0 < nch) v_step<0, true>(pf, slot, sc, wbase, off, dst, lane, c0, nch, xs, xd, xp, acc);
+    } else {
+        for (int c0 = 0; c0 < nch; c0 += kVAhead) {
+            v_step<0, false>(pf, slot, sc, wbase, off, dst, lane, c0, nch, xs, xd, xp, acc);
+            v_step<1, false>(pf, slot, sc, wbase, off, dst, lane, c0, nch, xs, xd, xp, acc);
+        }
     }
-    // lanes 2L and 2L+1 hold the same acc_L: k_q8_0_gemv_T's combine over L
+    // lanes 4L..4L+3 hold the same acc_L (L at lane bits 2-4): k_q8_0_gemv_T's combine over L
+    acc = acc + xor_f(acc, 16);
     acc = acc + xor_f(acc, 8);
     acc = acc + xor_f(acc, 4);
-    acc = acc + xor_f(acc, 2);
-    const int row = row0 + (lane >> 4);
-    if ((lane & 15) == 0 && row < m_weight) out[(int64_t)tok * m_weight + row] = acc;
+    const int row = row0 + (lane >> 5);
+    if ((lane & 31) == 0 && row < m_weight) out[(int64_t)tok * m_weight + row] = acc;
 }
 
 // Plain form of the same order for activation rows too long to stage in LDS.
@@ -580,53 +608,52 @@ void launch_fill_zero(float* out, int64_t n, hipStream_t s) {
 
 // k_q8_0_gemv_V with NW waves per workgroup for nb blocks, or NULL when the
 // activation row does not fit XR <= 32 dwords per thread.
-template <int NW>
+template <int NW, bool ALWAYS>
 static const void* v_kernel(int nb) {
     constexpr int NT = 64 * NW;
-    if (nb * 8 <= 2 * NT) return reinterpret_cast<const void*>(&k_q8_0_gemv_V<NW, 2>);
-    if (nb * 8 <= 4 * NT) return reinterpret_cast<const void*>(&k_q8_0_gemv_V<NW, 4>);
-    if (nb * 8 <= 8 * NT) return reinterpret_cast<const void*>(&k_q8_0_gemv_V<NW, 8>);
-    if (nb * 8 <= 16 * NT) return reinterpret_cast<const void*>(&k_q8_0_gemv_V<NW, 16>);
-    if (nb * 8 <= 32 * NT) return reinterpret_cast<const void*>(&k_q8_0_gemv_V<NW, 32>);
+    if (nb * 8 <= 4 * NT) return reinterpret_cast<const void*>(&k_q8_0_gemv_V<NW, 4, ALWAYS>);
+    if (nb * 8 <= 8 * NT) return reinterpret_cast<const void*>(&k_q8_0_gemv_V<NW, 8, ALWAYS>);
+    if (nb * 8 <= 16 * NT) return reinterpret_cast<const void*>(&k_q8_0_gemv_V<NW, 16, ALWAYS>);
+    if (nb * 8 <= 32 * NT) return reinterpret_cast<const void*>(&k_q8_0_gemv_V<NW, 32, ALWAYS>);
     return nullptr;
 }
 
-static const void* v_kernel_nw(int nw, int nb) {
-    return nw == 8 ? v_kernel<8>(nb) : nw == 4 ? v_kernel<4>(nb) : v_kernel<2>(nb);
-}
-
-// The wide-load kernel where it is measured faster (MI355X, graph, weights
-// beyond the MALL), by 4-row waves w = ceil(m_weight/4) * m_tokens: from
-// w >= 128, with 2 waves per workgroup, 4 from w >= 1024 and 8 from w >= 2048.
-// Against the dword kernels of dispatch_T: 14336x4096 14.7 us (19.8),
-// 4096x14336 15.8 (24.1), 4096x4096 6.6 (8.6), 2048x14336 13.6, 1024x4096 5.4
-// (6.3), 512x4096 5.0 (6.0).  Returns false when the shape or W's alignment
-// does not fit.
+// The wide-load kernel where it is measured faster (MI355X, weights beyond the
+// MALL), by 2-row waves w = ceil(m_weight/2) * m_tokens: from w >= 256, 4 waves
+// per workgroup (8 when the activation row needs them: nb > 1024).  Against the
+// 4-row form it replaces: 14336x4096 12.9 us (13.6), 4096x14336 14.0 (15.3),
+// 2048x14336 11.0 (13.4), 6144x4096 7.2 (8.5), 4096x4096 6.1 (6.9), 1024x4096
+// 4.8 (5.6), 512x4096 4.7 (5.5), 28672x4096 22.6 (23.1).  Loads unconditional
+// (ALWAYS) for rows of at most 4 chunks and w <= 8192, where that form is the
+// faster one.  Returns false when the shape or W's alignment does not fit.
 static bool launch_wide(const uint8_t* Wq, const uint8_t* Xq, float* out, int m_weight, int m_tokens, int nb,
                         hipStream_t s) {
     if (nb % kVChunk != 0 || (reinterpret_cast<uintptr_t>(Wq) & 15) != 0) return false;
     const int64_t waves = (int64_t)((m_weight + kVRows - 1) / kVRows) * m_tokens;
-    if (waves < 128) return false;
-    int nw = waves >= 2048 ? 8 : waves >= 1024 ? 4 : 2;
-    const void* f = v_kernel_nw(nw, nb);
-    for (; f == nullptr && nw < 8; nw *= 2) f = v_kernel_nw(nw * 2, nb);  // more threads for a long x row
+    if (waves < 256) return false;
+    const bool always = nb / kVChunk <= 4 && waves <= 8192;
+    int nw = 4;
+    const void* f = always ? v_kernel<4, true>(nb) : v_kernel<4, false>(nb);
+    if (f == nullptr) {  // a long activation row: 8 waves stage it
+        nw = 8;
+        f = always ? v_kernel<8, true>(nb) : v_kernel<8, false>(nb);
+    }
     const size_t lds = v_lds_bytes(nb, nw);
     if (f == nullptr || lds > 160 * 1024) return false;
-    // more than 64 KB of dynamic LDS is asked for once per process and kernel
-    static std::once_flag once;
-    static bool lds_ok = false;
-    std::call_once(once, [] {
-        lds_ok = true;
-        for (int n : {32, 64, 128, 256, 512, 1024, 2048})
-            for (int w : {2, 4, 8}) {
-                const void* k = v_kernel_nw(w, n);
-                if (k != nullptr &&
+    if (lds > 64 * 1024) {
+        // more than 64 KB of dynamic LDS is asked for once per process and kernel
+        static std::once_flag once;
+        static bool lds_ok = false;
+        std::call_once(once, [] {
+            lds_ok = true;
+            for (const void* k : {v_kernel<8, false>(2048), v_kernel<8, true>(2048)})
+                if (k == nullptr ||
                     hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
                     lds_ok = false;
-            }
-        (void)hipGetLastError();
-    });
-    if (!lds_ok) return false;
+            (void)hipGetLastError();
+        });
+        if (!lds_ok) return false;
+    }
     const int rows = kVRows * nw;
     void* args[] = {const_cast<uint8_t**>(&Wq), const_cast<uint8_t**>(&Xq), &out, &m_weight, &nb};
     (void)hipLaunchKernel(f, dim3((m_weight + rows - 1) / rows, m_tokens), dim3(64 * nw), args, lds, s);

@@ -63,13 +63,15 @@ def test_quant_q8_0_edges(dev):
 
 @pytest.mark.parametrize("mw,mt,K", [(14336, 1, 4096), (4096, 1, 14336), (4, 2, 128), (7, 5, 128),
                                      (9, 7, 128), (2048, 2, 2048), (1, 1, 32), (13, 3, 4096 + 32),
-                                     # the wide-load kernel: 8-, 4- and 2-wave workgroups, partial
-                                     # last workgroups and waves, each activation register count,
-                                     # several tokens, and 4 waves where 2 cannot hold the x row
+                                     # the wide-load kernel: both load forms, partial last
+                                     # workgroups and waves, each activation register count,
+                                     # several tokens, an odd chunk count, and 8 waves where 4
+                                     # cannot hold the x row (K = 65536, over 64 KB of LDS)
                                      (8192, 2, 1024), (8200, 3, 8192), (2048, 1, 8192), (9000, 1, 2048),
                                      (2056, 1, 16384), (4096, 4, 4096), (4100, 1, 4096), (4096, 1, 4096),
                                      (2048, 1, 32768), (4096, 2, 14336), (511, 1, 4096), (1024, 1, 14336),
-                                     (2048, 1, 4096), (514, 1, 1024)])
+                                     (2048, 1, 4096), (514, 1, 1024), (512, 1, 65536), (513, 1, 3072),
+                                     (4097, 3, 1024)])
 def test_dispatch_tile_order(dev, mw, mt, K):
     W = synth.q8_0(mw, K, synth.key(42, 7))
     X = synth.normal_f32(mt * K, synth.key(42, 8))

@@ -309,49 +309,52 @@ def test_dequant_in_bounds(nb):
 
 # ---------------------------------------------------------------- Q8_0 tile-order GEMV
 
-V_PITCH, V_SCP, V_ROWS = 1248, 20, 4
-V_SLOT = V_ROWS * V_PITCH + 2 * V_ROWS * V_SCP * 4
+V_PITCH, V_SCP, V_ROWS = 1248, 12, 2
+V_SLOT = V_ROWS * V_PITCH + 4 * V_ROWS * V_SCP * 4
 
 
 def v_xpitch(nb):
-    return nb // 2 + 4
+    return nb // 4 + 4
 
 
 def v_lds(nb, nw):
-    return (16 * v_xpitch(nb) + nb) * 4 + nw * V_SLOT
+    return (32 * v_xpitch(nb) + nb) * 4 + nw * V_SLOT
 
 
 def q8_wide_config(mw, mt, nb):
-    """(NW, XR) of k_q8_0_gemv_V as launch_wide() in q8_0.hip picks it for a
-    16-byte aligned W, or None."""
+    """(NW, XR, ALWAYS) of k_q8_0_gemv_V as launch_wide() in q8_0.hip picks it
+    for a 16-byte aligned W, or None."""
     if nb == 0 or nb % 32 != 0:
         return None
     waves = -(-mw // V_ROWS) * mt
-    if waves < 128:
+    if waves < 256:
         return None
-    xr = lambda nw: next((x for x in (2, 4, 8, 16, 32) if nb * 8 <= x * 64 * nw), None)
-    nw = 8 if waves >= 2048 else 4 if waves >= 1024 else 2
+    always = nb // 32 <= 4 and waves <= 8192
+    xr = lambda nw: next((x for x in (4, 8, 16, 32) if nb * 8 <= x * 64 * nw), None)
+    nw = 4
     XR = xr(nw)
-    while XR is None and nw < 8:
-        nw *= 2
+    if XR is None:
+        nw = 8
         XR = xr(nw)
     if XR is None or v_lds(nb, nw) > 160 * 1024:
         return None
-    return nw, XR
+    return nw, XR, always
 
 
 def check_wide_q8(mw, mt, nb, w_size, x_size, out_size):
-    """k_q8_0_gemv_V: lane l of wave w in workgroup g (rows row0 = 4(g*NW + w) ..)
-    reads 16-byte piece f = min(l + 64k, 271) (k < 5; k = 4 on lanes < 16 only)
-    -- row f/68, bytes 1088c + 16(f%68) of that row (rows past mw re-read row
-    mw-1) -- for chunks c < nb/32 and writes it at (f/68)*1248 + 16(f%68) of the
-    wave's slot; the scale pass reads the 16-bit scale at r*1248 + 34bb and writes
-    sc[(2r + bb%2)*20 + bb/2] (r < 4, bb < 32); lane (row, L, h) reads the dwords
-    at 34bb + oa and 34bb + oa + 4 of its row's chunk (bb even, oa = (34h + 2 +
-    4L) & ~3), four x dwords at (2L + h)*(nb/2 + 4) + 16c + b8/2 and four products
-    at (2row + h)*20 + b8/2; the activation is quant dword min(i, 8nb-1) and
-    scale min(j, nb-1)."""
-    NW, XR = q8_wide_config(mw, mt, nb)
+    """k_q8_0_gemv_V: lane l of wave w in workgroup g (rows row0 = 2(g*NW + w) ..)
+    reads 16-byte piece f = min(l + 64k, 135) (k < 3; k = 2 on lanes < 8 only,
+    or on every lane when ALWAYS) -- row f/68, bytes 1088c + 16(f%68) of that row
+    (rows past mw re-read row mw-1) -- for chunks c < nb/32, and when ALWAYS also
+    the first 16 bytes of row row0c; it writes piece f at (f/68)*1248 + 16(f%68)
+    of the wave's slot (lanes with f < 136); the scale pass (lane j: r = j/32,
+    bb = j%32) reads the 16-bit scale at r*1248 + 34bb and writes
+    sc[(4r + bb%4)*12 + bb/4]; lane (row, L, q) reads the dwords at 34bb + oa and
+    34bb + oa + 4 of its row's chunk (bb % 4 == 0, oa = (34q + 2 + 4L) & ~3), four
+    x dwords at (4L + q)*(nb/4 + 4) + 8c + b16/4 and four products at
+    (4row + q)*12 + b16/4; the activation is quant dword min(i, 8nb-1) and scale
+    min(j, nb-1)."""
+    NW, XR, always = q8_wide_config(mw, mt, nb)
     NT, bpr, nch, xp = 64 * NW, nb * Q80, nb // 32, v_xpitch(nb)
     l = np.arange(64)
     groups = -(-mw // (V_ROWS * NW))
@@ -359,31 +362,32 @@ def check_wide_q8(mw, mt, nb, w_size, x_size, out_size):
         for w in range(NW):
             row0 = (g * NW + w) * V_ROWS
             row0c = min(row0, mw - 1)
-            for k in range(5):
-                f = np.minimum(l + 64 * k, 271)
-                if k == 4:
-                    f = f[l < 16]
+            if always:
+                assert row0c * bpr + 16 <= w_size
+            for k in range(3):
+                f = np.minimum(l + 64 * k, 135)
+                if k == 2 and not always:
+                    f = f[l < 8]
                 r, pc = f // 68, f % 68
                 off = (np.minimum(row0 + r, mw - 1) - row0c) * bpr + 16 * pc
                 for c in (0, nch - 1):
                     a = row0c * bpr + off + c * 1088
                     assert a.min() >= 0 and (a + 16).max() <= w_size
-                assert (r * V_PITCH + 16 * pc + 16).max() <= V_ROWS * V_PITCH
-    j = np.arange(128)
-    r, bb = j // 32, j % 32
+                fw = np.minimum(l + 64 * k, 135)[l + 64 * k < 136]
+                assert ((fw // 68) * V_PITCH + 16 * (fw % 68) + 16).max() <= V_ROWS * V_PITCH
+    r, bb = l // 32, l % 32
     assert (r * V_PITCH + 34 * bb + 2).max() <= V_ROWS * V_PITCH
-    assert ((2 * r + bb % 2) * V_SCP + bb // 2).max() < 2 * V_ROWS * V_SCP
-    h, L, rr = l & 1, (l >> 1) & 7, l >> 4
-    oa = (34 * h + 2 + 4 * L) & ~3
-    for bb in range(0, 32, 2):
-        a = rr * V_PITCH + 34 * bb + oa
-        assert a.min() >= 0 and (a + 8).max() <= rr.max() * V_PITCH + V_PITCH
+    assert ((4 * r + bb % 4) * V_SCP + bb // 4).max() < 4 * V_ROWS * V_SCP
+    assert (nch - 1) * 32 + bb.max() < nb
+    q, L, rr = l & 3, (l >> 2) & 7, l >> 5
+    oa = (34 * q + 2 + 4 * L) & ~3
+    for bb in range(0, 32, 4):
         assert (34 * bb + oa + 8).max() <= V_PITCH
-    for b8 in range(0, 32, 8):
-        xi = (2 * L + h) * xp + 16 * (nch - 1) + b8 // 2
-        assert (xi + 4).max() <= 16 * xp
-        si = (2 * rr + h) * V_SCP + b8 // 2
-        assert (si + 4).max() <= 2 * V_ROWS * V_SCP
+    for b16 in (0, 16):
+        xi = (4 * L + q) * xp + 8 * (nch - 1) + b16 // 4
+        assert (xi + 4).max() <= 32 * xp
+        si = (4 * rr + q) * V_SCP + b16 // 4
+        assert (si + 4).max() <= 4 * V_ROWS * V_SCP
     i = np.minimum(np.arange(XR * NT), nb * 8 - 1)
     jd = np.minimum(np.arange(-(-XR // 8) * NT), nb - 1)
     assert nb <= -(-XR // 8) * NT
@@ -393,10 +397,10 @@ def check_wide_q8(mw, mt, nb, w_size, x_size, out_size):
     st = np.arange(XR * NT)
     st = st[st < nb * 8]
     b = st >> 3
-    assert ((2 * (st & 7) + (b & 1)) * xp + (b >> 1)).max() < 16 * xp
+    assert ((4 * (st & 7) + (b & 3)) * xp + (b >> 2)).max() < 32 * xp
     # 16-byte alignment of every vector LDS access: slots, x rows, product rows
-    assert ((16 * xp + nb) * 4) % 16 == 0 and V_SLOT % 16 == 0 and (V_ROWS * V_PITCH) % 16 == 0
-    assert (xp * 4) % 16 == 0 and (V_SCP * 4) % 16 == 0 and (16 * (nch - 1) * 4) % 16 == 0
+    assert ((32 * xp + nb) * 4) % 16 == 0 and V_SLOT % 16 == 0 and (V_ROWS * V_PITCH) % 16 == 0
+    assert (xp * 4) % 16 == 0 and (V_SCP * 4) % 16 == 0 and (8 * (nch - 1) * 4) % 16 == 0
     assert (mt - 1) * mw * 4 + mw * 4 <= out_size
     assert v_lds(nb, NW) <= 160 * 1024
 
@@ -448,7 +452,8 @@ def check_producer(mw, mt, nb, layout, w_size):
                                      (8192, 2, 1024), (8200, 3, 8192), (2048, 1, 8192), (9000, 1, 2048),
                                      (14336, 4, 4096), (2056, 1, 16384), (8192, 1, 32768), (2048, 1, 32768),
                                      (4096, 4, 4096), (4096, 2, 14336), (512, 1, 8192),
-                                     (4100, 1, 4096), (1024, 1, 14336), (2048, 1, 4096)])
+                                     (4100, 1, 4096), (1024, 1, 14336), (2048, 1, 4096), (512, 1, 65536),
+                                     (513, 1, 3072), (28672, 1, 4096), (4097, 3, 1024)])
 def test_q8_0_gemv_T_in_bounds(mw, mt, K):
     cfg = q8_gemv_config(mw, mt, K)
     nb = K // 32
