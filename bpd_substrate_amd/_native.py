@@ -11,8 +11,10 @@ import ctypes
 import os
 
 PKG = os.path.dirname(os.path.abspath(__file__))
-HIP_LIB = os.path.join(PKG, "libbpdq_hip.so")
-SYNTH_LIB = os.path.join(PKG, "libbpdq_synth.so")
+# BPDQ_HIP_LIB / BPDQ_SYNTH_LIB name other builds of the same libraries (the CPU
+# test suite's sanitized host-only build); unset, the in-tree builds are used.
+HIP_LIB = os.environ.get("BPDQ_HIP_LIB") or os.path.join(PKG, "libbpdq_hip.so")
+SYNTH_LIB = os.environ.get("BPDQ_SYNTH_LIB") or os.path.join(PKG, "libbpdq_synth.so")
 
 P, I, F = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
 

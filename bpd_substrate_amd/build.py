@@ -1,9 +1,17 @@
 """Build the native libraries in-tree.
 
-    python -m bpd_substrate_amd.build          # libbpdq_hip.so + libbpdq_synth.so
+    python -m bpd_substrate_amd.build             # libbpdq_hip.so + libbpdq_synth.so
+    python -m bpd_substrate_amd.build --sanitize  # _san/: host code under ASan + UBSan
 
 libbpdq_hip.so   hipcc --offload-arch=gfx950, one object per csrc/*.hip, then -shared
 libbpdq_synth.so gcc, the deterministic input generator (csrc/synth.c)
+
+The sanitized variants (_san/libbpdq_hip.so, _san/libbpdq_synth.so) are for the
+CPU test suite: the host pass of every HIP source is compiled with Address-
+Sanitizer and UndefinedBehaviorSanitizer (the device code is the usual one and
+is not instrumented), and synth.c with clang under the same runtime, so one
+process can load both next to the sanitized oracle (oracle/Makefile, target
+san).
 
 The built files stay next to this module so that they travel with the source
 tree to the GPU host; nothing is installed.
@@ -73,12 +81,48 @@ def build_synth():
     return SYNTH_LIB
 
 
+SAN_DIR = os.path.join(PKG, "_san")
+CLANG = os.environ.get("BPDQ_CLANG", "/opt/rocm/llvm/bin/clang")
+# each -fsanitize option goes to the host pass only
+SAN_HOST = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+            "-Xarch_host", "-fno-sanitize-recover=all", "-Xarch_host", "-fno-omit-frame-pointer"]
+SAN_C = ["-fsanitize=address,undefined", "-fno-sanitize-recover=all", "-fno-omit-frame-pointer", "-shared-libsan"]
+
+
+def asan_runtime():
+    """The clang ASan runtime the sanitized libraries need preloaded (LD_PRELOAD)."""
+    return _run([CLANG, "-print-file-name=libclang_rt.asan-x86_64.so"]).strip()
+
+
+def build_sanitized():
+    """_san/libbpdq_hip.so (the host pass of every csrc/*.hip under ASan + UBSan)
+    and _san/libbpdq_synth.so, with clang's shared sanitizer runtime."""
+    obj = os.path.join(SAN_DIR, "obj")
+    os.makedirs(obj, exist_ok=True)
+    srcs = hip_sources()
+    objs = [os.path.join(obj, os.path.basename(s)[:-4] + ".o") for s in srcs]
+    base = [HIPCC, *HIP_FLAGS, *SAN_HOST, "-g"]
+    with cf.ThreadPoolExecutor(max_workers=max(1, min(len(srcs), int(os.environ.get("MAX_JOBS", "8"))))) as ex:
+        for f in [ex.submit(_run, [*base, "-c", s, "-o", o]) for s, o in zip(srcs, objs)]:
+            f.result()
+    hip = os.path.join(SAN_DIR, "libbpdq_hip.so")
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *SAN_HOST, "-Xarch_host", "-shared-libsan",
+          "-o", hip, *objs])
+    synth = os.path.join(SAN_DIR, "libbpdq_synth.so")
+    _run([CLANG, "-O1", "-g", "-ffp-contract=off", "-fPIC", "-shared", *SAN_C, "-o", synth,
+          os.path.join(CSRC, "synth.c"), "-lm", "-lpthread"])
+    return hip, synth
+
+
 def build_all(verbose=False):
     build_synth()
     build_hip(verbose=verbose)
 
 
 if __name__ == "__main__":
-    build_all(verbose="-v" in sys.argv)
-    print(HIP_LIB)
-    print(SYNTH_LIB)
+    if "--sanitize" in sys.argv:
+        print(*build_sanitized(), sep="\n")
+    else:
+        build_all(verbose="-v" in sys.argv)
+        print(HIP_LIB)
+        print(SYNTH_LIB)

@@ -1148,9 +1148,9 @@ __device__ __forceinline__ void x32_quantize(const XPre<IT>& P, uint8_t* __restr
             e[4 * k + 2] = P.v[it][k].z;
             e[4 * k + 3] = P.v[it][k].w;
         }
-        float amax = fabsf(e[0]);
+        float amax = abs_no_nan(e[0]);
 #pragma unroll
-        for (int k = 1; k < 16; k++) amax = fmaxf(amax, fabsf(e[k]));
+        for (int k = 1; k < 16; k++) amax = fmaxf(amax, abs_no_nan(e[k]));
         amax = fmaxf(amax, dpp_f<0xB1>(amax));   // quad_perm [1,0,3,2]
         amax = fmaxf(amax, dpp_f<0x4E>(amax));   // quad_perm [2,3,0,1]
         amax = fmaxf(amax, dpp_f<0x141>(amax));  // row_half_mirror
@@ -1161,7 +1161,7 @@ __device__ __forceinline__ void x32_quantize(const XPre<IT>& P, uint8_t* __restr
         int bsum = 0;
 #pragma unroll
         for (int k = 0; k < 16; k++) {
-            const int qv = (int)__builtin_rintf(e[k] * id);
+            const int qv = x86_i8(__builtin_rintf(e[k] * id));
             bsum += qv;
             pk[k >> 2] |= (uint32_t)(qv & 0xFF) << (8 * (k & 3));
         }

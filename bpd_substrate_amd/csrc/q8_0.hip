@@ -708,6 +708,9 @@ void launch_q8_pad64_dispatch_T(const uint8_t* Wp, const uint8_t* Xq, float* out
 // q = clip(round-half-even(RN(x / d)), -128, 127), record (b, n) at byte
 // (b*N + n)*64 = {f16(d) RNE, 0, 0, q[32], 28 zero bytes}.  32 lanes per record
 // (lane = element), so the reads of consecutive records are contiguous.
+// As numpy computes it: a NaN in the block carries through max, clip and /127
+// into d (float16 0x7E00) and every quant is 0 (NaN cast to int8); with an Inf
+// (d = Inf) Inf/Inf is NaN and its quant 0.
 // ----------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_q8_pad64(const float* __restrict__ x, uint8_t* __restrict__ out, int N,
                                                   int nb) {
@@ -720,14 +723,17 @@ __global__ __launch_bounds__(256) void k_q8_pad64(const float* __restrict__ x, u
     float amax = fabsf(v);
 #pragma unroll
     for (int mask = 1; mask < 32; mask <<= 1) amax = fmaxf(amax, xor_f(amax, mask));
+    // a NaN anywhere in the record (its 32 lanes are one half of the wave)
+    const bool nan_rec = ((uint64_t)__ballot(__builtin_isnan(v)) >> (threadIdx.x & 32) & 0xFFFFFFFFull) != 0;
     amax = fmaxf(amax, 1e-10f);
     const float d = amax / 127.0f;
-    const float qf = fminf(fmaxf(__builtin_rintf(v / d), -128.0f), 127.0f);
+    const float r = __builtin_rintf(v / d);
+    const float qf = (nan_rec || __builtin_isnan(r)) ? 0.0f : fminf(fmaxf(r, -128.0f), 127.0f);
     uint8_t* o = out + (b * N + n) * 64;
     o[4 + e] = (uint8_t)(int8_t)(int)qf;
     if (e < 28) o[36 + e] = 0;
     if (e == 0) {
-        const uint16_t h = __builtin_bit_cast(uint16_t, (_Float16)d);
+        const uint16_t h = nan_rec ? (uint16_t)0x7E00 : __builtin_bit_cast(uint16_t, (_Float16)d);
         *reinterpret_cast<uint32_t*>(o) = (uint32_t)h;
     }
 }

@@ -103,6 +103,16 @@ uint16_t bpdq_o_f32_to_f16(float f) {
 
 static inline uint16_t rd16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
 
+/* (int8_t)v for a float v, as the reference's x86 build executes the cast of
+ * bench/bpd_cpu.c:4133 (also used for the Q8_K and padded-Q8 quantizers below):
+ * cvttss2si to int32, which gives 0x80000000 for NaN and for values outside the
+ * int32 range, then the low byte.  Spelled out because the C cast is undefined
+ * for such v (a NaN element, or an overflowing 127/amax). */
+static inline int8_t x86_f32_to_i8(float v) {
+    const int32_t i = (v >= -2147483648.0f && v < 2147483648.0f) ? (int32_t)v : INT32_MIN;  /* NaN: both false */
+    return (int8_t)(uint8_t)(uint32_t)i;
+}
+
 /* ------------------------------------------------------- x86 NaN rules --- */
 
 /* The reference's compiled C runs on x86, whose SSE arithmetic gives a NaN
@@ -257,7 +267,7 @@ void bpdq_o_quant_q8_k(const float* x, uint8_t* y, int n) {
         float id = amax != 0.0f ? 127.0f / amax : 0.0f;
         memcpy(yb, &d, 4);
         int8_t* qs = (int8_t*)(yb + 4);
-        for (int j = 0; j < 256; j++) qs[j] = (int8_t)rintf(xb[j] * id);
+        for (int j = 0; j < 256; j++) qs[j] = x86_f32_to_i8(rintf(xb[j] * id));
         for (int g = 0; g < 16; g++) {
             int s = 0;
             for (int j = 0; j < 16; j++) s += qs[16 * g + j];
@@ -455,7 +465,7 @@ void bpdq_o_quant_q8_0(const float* x, uint8_t* y, int n_elements) {
         yb[1] = (uint8_t)(dh >> 8);
         float id = amax != 0.0f ? 127.0f / amax : 0.0f;
         int8_t* qs = (int8_t*)(yb + 2);
-        for (int j = 0; j < 32; j++) qs[j] = (int8_t)rintf(xb[j] * id);
+        for (int j = 0; j < 32; j++) qs[j] = x86_f32_to_i8(rintf(xb[j] * id));
     }
 }
 
@@ -626,20 +636,31 @@ void bpdq_o_q8_pad64(const float* x, uint8_t* out, int N, int K) {
             const float* xb = x + (size_t)n * K + (size_t)b * 32;
             uint8_t* o = out + ((size_t)b * N + n) * 64;
             float amax = 0.0f;
+            int has_nan = 0;
             for (int j = 0; j < 32; j++) {
                 float a = fabsf(xb[j]);
-                if (a > amax) amax = a;
+                if (isnan(a)) has_nan = 1;
+                else if (a > amax) amax = a;
+            }
+            memset(o, 0, 64);
+            if (has_nan) {
+                /* numpy's max, clip and /127 carry the NaN into d, so every x/d is
+                 * NaN and casts to 0; d's float16 is 0x7E00 for the default NaN (a
+                 * payload survives numpy's SIMD max at some positions only) */
+                const uint16_t h = 0x7E00;
+                memcpy(o, &h, 2);
+                continue;
             }
             if (amax < 1e-10f) amax = 1e-10f;
             float d = amax / 127.0f;
-            memset(o, 0, 64);
             uint16_t h = bpdq_o_f32_to_f16(d);
             memcpy(o, &h, 2);
             for (int j = 0; j < 32; j++) {
                 float q = rintf(xb[j] / d);
+                if (isnan(q)) q = 0.0f;  /* Inf/Inf (amax = Inf): clip keeps the NaN, the int8 cast gives 0 */
                 if (q < -128.0f) q = -128.0f;
                 if (q > 127.0f) q = 127.0f;
-                o[4 + j] = (uint8_t)(int8_t)q;
+                o[4 + j] = (uint8_t)x86_f32_to_i8(q);
             }
         }
 }

@@ -11,7 +11,8 @@ import subprocess
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB = os.path.join(HERE, "liboracle.so")
+# BPDQ_ORACLE_LIB: another build of the same file (the sanitized one, make san)
+LIB = os.environ.get("BPDQ_ORACLE_LIB") or os.path.join(HERE, "liboracle.so")
 REF_DIR = os.path.join(HERE, "_ref")
 REF_LIBS = {
     "quant": os.path.join(REF_DIR, "bpd_quant_ref.so"),        # bench/bpd_quant.c, -O2

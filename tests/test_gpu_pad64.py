@@ -5,7 +5,7 @@ import numpy as np
 import pytest
 
 from bpd_substrate_amd import gpu, synth
-from helpers import assert_bits_equal, to_np
+from helpers import assert_bits_equal, special_f32_blocks, to_np
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -33,6 +33,14 @@ def test_pad64_conversion(dev, N, K):
     got = to_np(gpu.q8_pad64(_d(x.ravel(), dev), N, K))
     want = O.q8_pad64(x, N, K)
     assert np.array_equal(got, want), f"pad64 N={N} K={K}: {np.count_nonzero(got != want)} bytes differ"
+
+
+def test_pad64_non_finite_blocks(dev):
+    # NaN blocks (d = 0x7E00, every quant 0), Inf blocks (Inf/Inf quant 0), as numpy
+    x = special_f32_blocks(32).reshape(3, 96)
+    got = to_np(gpu.q8_pad64(_d(x.ravel(), dev), 3, 96))
+    want = O.q8_pad64(x, 3, 96)
+    assert np.array_equal(got, want), f"{np.count_nonzero(got != want)} bytes differ"
 
 
 @pytest.mark.parametrize("mw,mt,K", [(4096, 1, 14336), (14336, 1, 4096), (13, 3, 160), (8, 1, 32), (9, 2, 64)])

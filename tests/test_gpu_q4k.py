@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 
 from bpd_substrate_amd import formats, gpu, synth
-from helpers import assert_bits_equal, to_np
+from helpers import assert_bits_equal, special_f32_blocks, to_np
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -104,6 +104,29 @@ def test_quant_q8_k_edge_values(dev):
     x[768:1024] = -7.25                            # block 3: constant negative (every q = -127)
     got = to_np(gpu.quant_q8_k(torch.from_numpy(x).to(dev)))
     assert np.array_equal(got, O.quant_q8_k(x))
+
+
+def test_quant_q8_k_non_finite(dev):
+    import torch
+
+    x = special_f32_blocks(256)
+    got = to_np(gpu.quant_q8_k(torch.from_numpy(x).to(dev)))
+    want = O.quant_q8_k(x)
+    assert np.array_equal(got, want), f"Q8_K bytes differ at {np.flatnonzero(got != want)[:8]}"
+
+
+@pytest.mark.parametrize("M,K", [(512, 4096), (4096, 14336)])
+def test_fused_quantize_tiny_amax_block(dev, M, K):
+    # a block whose 127/amax overflows: the fused GEMV's in-kernel Q8_K must give
+    # the x86 cast's 0 quants (and bsums) there, as the oracle's quantizer
+    import torch
+
+    w = synth.q4k(M, K, synth.key(46, 1))
+    x = synth.normal_f32(K, synth.key(46, 2))
+    x[256:512] = np.float32(1e-38) * np.sign(np.linspace(-1, 1, 256, dtype=np.float32))
+    got = to_np(gpu.qmatmul_q4k_q8k_fused(_dev_u8(w, dev), torch.from_numpy(x).to(dev), M, K))
+    want = O.qmatmul_q4k_q8k(w, O.quant_q8_k(x), M, K, formats.ORDER_BPD)
+    assert_bits_equal(got, want, "fused, tiny-amax block")
 
 
 @pytest.mark.parametrize("order", [formats.ORDER_BPD, formats.ORDER_GGUF])

@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 from bpd_substrate_amd import gpu, synth
-from helpers import assert_bits_equal, to_np
+from helpers import assert_bits_equal, special_f32_blocks, to_np
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -47,6 +47,15 @@ def test_quant_q8_0(dev, n):
     got = to_np(gpu.quant_q8_0(_d(x, dev)))
     want = O.quant_q8_0(x)
     assert np.array_equal(got, want), f"Q8_0 bytes differ at {np.flatnonzero(got != want)[:8]}"
+
+
+def test_quant_q8_0_non_finite(dev):
+    # the x86 cast of the reference (0 for NaN and for +-Inf), which the GPU's
+    # saturating v_cvt_i32_f32 does not give for +Inf by itself
+    x = special_f32_blocks(32)
+    got = to_np(gpu.quant_q8_0(_d(x, dev)))
+    want = O.quant_q8_0(x)
+    assert np.array_equal(got, want), f"bytes differ at {np.flatnonzero(got != want)[:8]}"
 
 
 def test_quant_q8_0_edges(dev):

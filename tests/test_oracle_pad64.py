@@ -9,10 +9,16 @@ inference/llamatov_c_inference.py:88-100), CPU only:
 * an all-zero block takes d = 1e-10/127, whose binary16 rounds to +0, and
   quantizes to 0;
 * layout probes: one non-zero value per (row, block) lands in record (b, n)
-  at byte 4 + j, the scale at bytes 0-1, everything else zero.
+  at byte 4 + j, the scale at bytes 0-1, everything else zero;
+* non-finite inputs as numpy computes them: a NaN in a block carries into d
+  (float16 0x7E00 for the default NaN) and every quant is 0; an Inf makes
+  d = Inf and Inf/Inf a NaN quant, cast to 0.
 """
+import warnings
+
 import numpy as np
 
+from helpers import special_f32_blocks
 from oracle import oracle as O
 
 
@@ -61,3 +67,15 @@ def test_zero_block_and_layout_probes():
                 rec = out[b, n]
                 assert rec[4 + j].view(np.int8) == -127 and rec[0:2].view(np.float16)[0] == np.float16(3 / 127)
                 assert np.count_nonzero(out) == np.count_nonzero(rec) == 3
+
+
+def test_non_finite_blocks_match_numpy():
+    x = special_f32_blocks(32).reshape(3, 96)
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore")  # numpy warns on the NaN casts it performs
+        want = numpy_ops(x)
+    assert np.array_equal(O.q8_pad64(x, 3, 96), want)
+    rec = O.q8_pad64(x, 3, 96).reshape(3, 3, 64)   # [block][row]
+    for b in (0, 1):  # row 0, blocks 0 (one NaN) and 1 (all NaN): d = 0x7E00, every quant 0
+        assert rec[b, 0, 0:2].view(np.uint16)[0] == 0x7E00 and not rec[b, 0, 4:36].any()
+    assert rec[2, 0, 0:2].view(np.uint16)[0] == 0x7C00   # row 0, block 2 (an Inf): d = Inf

@@ -16,7 +16,7 @@ import numpy as np
 import pytest
 
 from bpd_substrate_amd import synth
-from helpers import assert_bits_equal
+from helpers import assert_bits_equal, special_f32_blocks
 from oracle import oracle as O
 
 GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
@@ -175,6 +175,27 @@ def test_ref_q8_0_quant_and_dequant_random():
     out = np.empty(4096 * 32, np.float32)
     fd(raw.ctypes.data, out.ctypes.data, 4096)
     assert_bits_equal(O.dequant_q8_0(raw), out, "dequant")
+
+
+def test_ref_q8_0_quant_out_of_range_casts():
+    # the reference's (int8_t)rintf(x0) on x86: int32 conversion (0x80000000 for NaN
+    # and overflow), low byte -- bench/bpd_cpu.c:4133
+    RS = _need("scalar")
+    fq = _bind(RS, "bpd_quant_q8_0_cpu", [P, P, I])
+    x = special_f32_blocks(32)
+    y = np.empty(x.size // 32 * 34, np.uint8)
+    fq(x.ctypes.data, y.ctypes.data, x.size)
+    assert np.array_equal(O.quant_q8_0(x), y)
+
+
+def test_q8_0_quant_out_of_range_casts_give_zero():
+    # what the reference build gives for those elements (pinned above where the
+    # reference builds): quant byte 0 for every non-finite x*id
+    x = special_f32_blocks(32)
+    q = O.quant_q8_0(x).reshape(-1, 34)[:, 2:].view(np.int8)
+    for i in (1, 2, 3, 4, 5):  # every x*id NaN, +-Inf or (id = 0) zero
+        assert (q[i] == 0).all(), i
+    assert q[0][5] == 0 and q[7][3] == 0 and (q[8] != 0).any()
 
 
 @pytest.mark.parametrize("nb", [1, 2, 7, 64, 129])
