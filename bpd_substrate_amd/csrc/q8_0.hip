@@ -383,11 +383,12 @@ __global__ __launch_bounds__(320) void k_q8_0_gemv_TP(const uint8_t* __restrict_
 // are k_q8_0_gemv_T's, so the bits are too.  Needs nb % 32 == 0 and W 16-byte
 // aligned.
 //
-// ALWAYS: every chunk step issues its 3 loads, past the last chunk a 16-byte
-// read of the wave's first row that every lane shares (discarded).  With the
-// loads unconditional the compiler's wait before a chunk's LDS writes leaves the
-// next chunk in flight; with them under a branch it waits for every load.  Each
-// form is faster on some shapes (measured, launch_wide).
+// Every chunk step issues its 3 loads (past the last chunk a 16-byte read of the
+// wave's first row that every lane shares, discarded), in a loop of whole chunk
+// pairs plus an odd tail step: with no load under a branch the compiler's wait
+// before a chunk's LDS writes leaves the next chunk in flight (vmcnt(3)-(5));
+// with the last loads skipped by a branch it waited for every load of the wave
+// once per two chunks (4096x14336: 14.0 -> 13.4 us, 2048x14336: 10.9 -> 9.4).
 // ----------------------------------------------------------------------------
 typedef uint32_t v_u32x4 __attribute__((ext_vector_type(4)));  // native vectors: stay in VGPRs
 typedef float v_f32x4 __attribute__((ext_vector_type(4)));
@@ -416,18 +417,16 @@ __device__ __forceinline__ void v_lds_order() { asm volatile("s_waitcnt lgkmcnt(
 __device__ __forceinline__ bool v_piece(int lane, int k) { return k < kVPer - 1 || lane + 64 * k < kVWavePieces; }
 
 // Non-temporal: each weight byte is read once, and every 16-byte piece of a
-// 128-byte line is loaded by the same instruction.  ALWAYS: lanes past the
-// wave's 136 pieces load piece 135 (off[] is clamped), an address another lane
-// of the same instruction loads; otherwise they load nothing (measured faster
-// for that form).
-template <bool ALWAYS>
+// 128-byte line is loaded by the same instruction.  Lanes past the wave's 136
+// pieces load piece 135 (off[] is clamped), an address another lane of the same
+// instruction loads.  real == false: the shared 16-byte read of a step past the
+// last chunk.
 __device__ __forceinline__ void v_load(v_u32x4 (&v)[kVPer], const uint8_t* __restrict__ wbase,
-                                       const uint32_t (&off)[kVPer], int c, bool real, int lane) {
+                                       const uint32_t (&off)[kVPer], int c, bool real) {
     const uint8_t* src = wbase + (real ? (uint32_t)c * kVRowB : 0u);
 #pragma unroll
     for (int k = 0; k < kVPer; k++)
-        if (ALWAYS || v_piece(lane, k))
-            v[k] = __builtin_nontemporal_load(reinterpret_cast<const v_u32x4*>(src + (real ? off[k] : 0u)));
+        v[k] = __builtin_nontemporal_load(reinterpret_cast<const v_u32x4*>(src + (real ? off[k] : 0u)));
 }
 
 // v read from lane (lane & ~3) + SEL of each quad
@@ -437,24 +436,20 @@ __device__ __forceinline__ float v_quad(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), ctrl, 0xF, 0xF, true));
 }
 
-// Chunk c = c0 + U (register slot U holds it; U is a template argument so that
-// the slots are indexed by constants): stage it, refill slot U with chunk
+// Chunk c = c0 + U < nch (register slot U holds it; U is a template argument so
+// that the slots are indexed by constants): stage it, refill slot U with chunk
 // c + kVAhead, scale products, chains.
-template <int U, bool ALWAYS>
+template <int U>
 __device__ __forceinline__ void v_step(v_u32x4 (&pf)[kVAhead][kVPer], uint8_t* slot, float* sc,
                                        const uint8_t* __restrict__ wbase, const uint32_t (&off)[kVPer],
                                        const uint32_t (&dst)[kVPer], int lane, int c0, int nch,
                                        const uint32_t* __restrict__ xs, const float* __restrict__ xd, int xp,
                                        float& acc) {
     const int c = c0 + U;
-    if (!ALWAYS && c >= nch) return;  // uniform over the wave (the ALWAYS loop calls only c < nch)
 #pragma unroll
     for (int k = 0; k < kVPer; k++)
         if (v_piece(lane, k)) *reinterpret_cast<v_u32x4*>(slot + dst[k]) = pf[U][k];
-    if (ALWAYS)
-        v_load<true>(pf[U], wbase, off, c + kVAhead, c + kVAhead < nch, lane);
-    else if (c + kVAhead < nch)
-        v_load<false>(pf[U], wbase, off, c + kVAhead, true, lane);
+    v_load(pf[U], wbase, off, c + kVAhead, c + kVAhead < nch);
     v_lds_order();
     {
         const int r = lane / kVChunk, bb = lane % kVChunk;  // kVRows * kVChunk == 64
@@ -488,8 +483,12 @@ __device__ __forceinline__ void v_step(v_u32x4 (&pf)[kVAhead][kVPer], uint8_t* s
 }
 
 // NW waves of 2 rows per workgroup; x quants in XR dwords per thread (nb*8 <= XR*64*NW).
-template <int NW, int XR, bool ALWAYS>
-__global__ __launch_bounds__(64 * NW) void k_q8_0_gemv_V(const uint8_t* __restrict__ W,
+// XR = 4 (K <= 4096): at most 72 VGPRs, 7 waves per SIMD, which the 7,168 waves
+// of 14336x4096 need to be resident at once (84 VGPRs unbounded: 13.5 -> 12.8 us;
+// the larger XR spill under that bound and are left unbounded).
+template <int NW, int XR>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(XR <= 4 ? 7 : 1)))
+void k_q8_0_gemv_V(const uint8_t* __restrict__ W,
                                                         const uint8_t* __restrict__ Xq, float* __restrict__ out,
                                                         int m_weight, int nb) {
     static_assert(kVAhead == 2, "one v_step call per chunk in flight");
@@ -530,7 +529,7 @@ __global__ __launch_bounds__(64 * NW) void k_q8_0_gemv_V(const uint8_t* __restri
     v_u32x4 pf[kVAhead][kVPer];
 #pragma unroll
     for (int a = 0; a < kVAhead; a++)
-        if (ALWAYS || a < nch) v_load<ALWAYS>(pf[a], wbase, off, a, a < nch, lane);
+        if (a < nch) v_load(pf[a], wbase, off, a, true);
 #pragma unroll
     for (int u = 0; u < XR; u++) {
         const int i = tid + u * NT, b = i >> 3;
@@ -541,21 +540,14 @@ __global__ __launch_bounds__(64 * NW) void k_q8_0_gemv_V(const uint8_t* __restri
         if (tid + u * NT < nb) xd[tid + u * NT] = f16_ieee(xh[u]);
     __syncthreads();
     float acc = 0.0f;
-    if (ALWAYS) {
-        // whole pairs of chunks, then an odd last one: no step of the loop body
-        // can be skipped, so every trip issues the same loads in the same order
-        int c0 = 0;
-        for (; c0 + 1 < nch; c0 += kVAhead) {
-            v_step<0, true>(pf, slot, sc, wbase, off, dst, lane, c0, nch, xs, xd, xp, acc);
-            v_step<1, true>(pf, slot, sc, wbase, off, dst, lane, c0, nch, xs, xd, xp, acc);
-        }
-        if (c0 < nch) v_step<0, true>(pf, slot, sc, wbase, off, dst, lane, c0, nch, xs, xd, xp, acc);
-    } else {
-        for (int c0 = 0; c0 < nch; c0 += kVAhead) {
-            v_step<0, false>(pf, slot, sc, wbase, off, dst, lane, c0, nch, xs, xd, xp, acc);
-            v_step<1, false>(pf, slot, sc, wbase, off, dst, lane, c0, nch, xs, xd, xp, acc);
-        }
+    // whole pairs of chunks, then an odd last one: no step of the loop body can be
+    // skipped, so every trip issues the same loads in the same order
+    int c0 = 0;
+    for (; c0 + 1 < nch; c0 += kVAhead) {
+        v_step<0>(pf, slot, sc, wbase, off, dst, lane, c0, nch, xs, xd, xp, acc);
+        v_step<1>(pf, slot, sc, wbase, off, dst, lane, c0, nch, xs, xd, xp, acc);
     }
+    if (c0 < nch) v_step<0>(pf, slot, sc, wbase, off, dst, lane, c0, nch, xs, xd, xp, acc);
     // lanes 4L..4L+3 hold the same acc_L (L at lane bits 2-4): k_q8_0_gemv_T's combine over L
     acc = acc + xor_f(acc, 16);
     acc = acc + xor_f(acc, 8);
@@ -608,48 +600,44 @@ void launch_fill_zero(float* out, int64_t n, hipStream_t s) {
 
 // k_q8_0_gemv_V with NW waves per workgroup for nb blocks, or NULL when the
 // activation row does not fit XR <= 32 dwords per thread.
-template <int NW, bool ALWAYS>
+template <int NW>
 static const void* v_kernel(int nb) {
     constexpr int NT = 64 * NW;
-    if (nb * 8 <= 4 * NT) return reinterpret_cast<const void*>(&k_q8_0_gemv_V<NW, 4, ALWAYS>);
-    if (nb * 8 <= 8 * NT) return reinterpret_cast<const void*>(&k_q8_0_gemv_V<NW, 8, ALWAYS>);
-    if (nb * 8 <= 16 * NT) return reinterpret_cast<const void*>(&k_q8_0_gemv_V<NW, 16, ALWAYS>);
-    if (nb * 8 <= 32 * NT) return reinterpret_cast<const void*>(&k_q8_0_gemv_V<NW, 32, ALWAYS>);
+    if (nb * 8 <= 4 * NT) return reinterpret_cast<const void*>(&k_q8_0_gemv_V<NW, 4>);
+    if (nb * 8 <= 8 * NT) return reinterpret_cast<const void*>(&k_q8_0_gemv_V<NW, 8>);
+    if (nb * 8 <= 16 * NT) return reinterpret_cast<const void*>(&k_q8_0_gemv_V<NW, 16>);
+    if (nb * 8 <= 32 * NT) return reinterpret_cast<const void*>(&k_q8_0_gemv_V<NW, 32>);
     return nullptr;
 }
 
 // The wide-load kernel where it is measured faster (MI355X, weights beyond the
 // MALL), by 2-row waves w = ceil(m_weight/2) * m_tokens: from w >= 256, 4 waves
 // per workgroup (8 when the activation row needs them: nb > 1024).  Against the
-// 4-row form it replaces: 14336x4096 12.9 us (13.6), 4096x14336 14.0 (15.3),
-// 2048x14336 11.0 (13.4), 6144x4096 7.2 (8.5), 4096x4096 6.1 (6.9), 1024x4096
-// 4.8 (5.6), 512x4096 4.7 (5.5), 28672x4096 22.6 (23.1).  Loads unconditional
-// (ALWAYS) for rows of at most 4 chunks and w <= 8192, where that form is the
-// faster one.  Returns false when the shape or W's alignment does not fit.
+// 4-row form it replaces (probe copies, eager, one box): 14336x4096 12.8 us
+// (13.6), 4096x14336 13.4 (15.2), 2048x14336 9.4 (13.4), 6144x4096 7.1 (8.5),
+// 4096x4096 5.9 (6.9), 1024x4096 4.5 (5.6), 512x4096 4.4 (5.5), 28672x4096 22.9
+// (23.1).  Returns false when the shape or W's alignment does not fit.
 static bool launch_wide(const uint8_t* Wq, const uint8_t* Xq, float* out, int m_weight, int m_tokens, int nb,
                         hipStream_t s) {
     if (nb % kVChunk != 0 || (reinterpret_cast<uintptr_t>(Wq) & 15) != 0) return false;
     const int64_t waves = (int64_t)((m_weight + kVRows - 1) / kVRows) * m_tokens;
     if (waves < 256) return false;
-    const bool always = nb / kVChunk <= 4 && waves <= 8192;
     int nw = 4;
-    const void* f = always ? v_kernel<4, true>(nb) : v_kernel<4, false>(nb);
+    const void* f = v_kernel<4>(nb);
     if (f == nullptr) {  // a long activation row: 8 waves stage it
         nw = 8;
-        f = always ? v_kernel<8, true>(nb) : v_kernel<8, false>(nb);
+        f = v_kernel<8>(nb);
     }
     const size_t lds = v_lds_bytes(nb, nw);
     if (f == nullptr || lds > 160 * 1024) return false;
     if (lds > 64 * 1024) {
-        // more than 64 KB of dynamic LDS is asked for once per process and kernel
+        // more than 64 KB of dynamic LDS is asked for once per process (only the
+        // 8-wave, 32-register form can need it)
         static std::once_flag once;
         static bool lds_ok = false;
         std::call_once(once, [] {
-            lds_ok = true;
-            for (const void* k : {v_kernel<8, false>(2048), v_kernel<8, true>(2048)})
-                if (k == nullptr ||
-                    hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess)
-                    lds_ok = false;
+            lds_ok = hipFuncSetAttribute(v_kernel<8>(2048), hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) ==
+                     hipSuccess;
             (void)hipGetLastError();
         });
         if (!lds_ok) return false;

@@ -322,14 +322,13 @@ def v_lds(nb, nw):
 
 
 def q8_wide_config(mw, mt, nb):
-    """(NW, XR, ALWAYS) of k_q8_0_gemv_V as launch_wide() in q8_0.hip picks it
-    for a 16-byte aligned W, or None."""
+    """(NW, XR) of k_q8_0_gemv_V as launch_wide() in q8_0.hip picks it for a
+    16-byte aligned W, or None."""
     if nb == 0 or nb % 32 != 0:
         return None
     waves = -(-mw // V_ROWS) * mt
     if waves < 256:
         return None
-    always = nb // 32 <= 4 and waves <= 8192
     xr = lambda nw: next((x for x in (4, 8, 16, 32) if nb * 8 <= x * 64 * nw), None)
     nw = 4
     XR = xr(nw)
@@ -338,23 +337,23 @@ def q8_wide_config(mw, mt, nb):
         XR = xr(nw)
     if XR is None or v_lds(nb, nw) > 160 * 1024:
         return None
-    return nw, XR, always
+    return nw, XR
 
 
 def check_wide_q8(mw, mt, nb, w_size, x_size, out_size):
     """k_q8_0_gemv_V: lane l of wave w in workgroup g (rows row0 = 2(g*NW + w) ..)
-    reads 16-byte piece f = min(l + 64k, 135) (k < 3; k = 2 on lanes < 8 only,
-    or on every lane when ALWAYS) -- row f/68, bytes 1088c + 16(f%68) of that row
-    (rows past mw re-read row mw-1) -- for chunks c < nb/32, and when ALWAYS also
-    the first 16 bytes of row row0c; it writes piece f at (f/68)*1248 + 16(f%68)
-    of the wave's slot (lanes with f < 136); the scale pass (lane j: r = j/32,
+    reads 16-byte piece f = min(l + 64k, 135) (k < 3, every lane) -- row f/68,
+    bytes 1088c + 16(f%68) of that row (rows past mw re-read row mw-1) -- for
+    chunks c < nb/32, and the first 16 bytes of row row0c for the steps past the
+    last chunk; it writes piece f at (f/68)*1248 + 16(f%68) of the wave's slot
+    (lanes with l + 64k < 136); the scale pass (lane j: r = j/32,
     bb = j%32) reads the 16-bit scale at r*1248 + 34bb and writes
     sc[(4r + bb%4)*12 + bb/4]; lane (row, L, q) reads the dwords at 34bb + oa and
     34bb + oa + 4 of its row's chunk (bb % 4 == 0, oa = (34q + 2 + 4L) & ~3), four
     x dwords at (4L + q)*(nb/4 + 4) + 8c + b16/4 and four products at
     (4row + q)*12 + b16/4; the activation is quant dword min(i, 8nb-1) and scale
     min(j, nb-1)."""
-    NW, XR, always = q8_wide_config(mw, mt, nb)
+    NW, XR = q8_wide_config(mw, mt, nb)
     NT, bpr, nch, xp = 64 * NW, nb * Q80, nb // 32, v_xpitch(nb)
     l = np.arange(64)
     groups = -(-mw // (V_ROWS * NW))
@@ -362,12 +361,9 @@ def check_wide_q8(mw, mt, nb, w_size, x_size, out_size):
         for w in range(NW):
             row0 = (g * NW + w) * V_ROWS
             row0c = min(row0, mw - 1)
-            if always:
-                assert row0c * bpr + 16 <= w_size
+            assert row0c * bpr + 16 <= w_size
             for k in range(3):
                 f = np.minimum(l + 64 * k, 135)
-                if k == 2 and not always:
-                    f = f[l < 8]
                 r, pc = f // 68, f % 68
                 off = (np.minimum(row0 + r, mw - 1) - row0c) * bpr + 16 * pc
                 for c in (0, nch - 1):
