@@ -206,7 +206,8 @@ __global__ __launch_bounds__(64 * WPB) void k_q6k_q8k_gemv(const uint8_t* __rest
 // the fp32 order are k_q6k_q8k_gemv's, so the bits are the same.
 // ----------------------------------------------------------------------------
 constexpr int kQ6Pass = 8 * kQ6KBytes;    // 1,680 bytes = 105 pieces
-constexpr int kQ6Buf = kQ6Pass + 16;      // tail room for the last aligned dword reads
+constexpr int kQ6Buf = kQ6Pass + 16;      // tail room for the last aligned dword reads, and the
+                                          // slot that takes a lane's out-of-pass piece write
 
 typedef uint32_t q6u32x4 __attribute__((ext_vector_type(4)));
 
@@ -272,12 +273,15 @@ __device__ __forceinline__ Q6X<ORDER> load_q6x(const uint8_t* __restrict__ xb, i
     return o;
 }
 
-// N consecutive words starting at LDS address p, p % 4 in {0, 2}.
+// N consecutive words starting at LDS address p, p % 4 in {0, 2}.  The aligned
+// base is p minus its misalignment (pointer arithmetic: a pointer rebuilt from
+// an integer loses the LDS address space, and its reads become flat loads that
+// wait on every outstanding global load too).
 template <int N>
 __device__ __forceinline__ void lds_words_a2(const uint8_t* p, uint32_t (&out)[N]) {
-    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-    const uint32_t* base = reinterpret_cast<const uint32_t*>(a & ~(uintptr_t)3);
-    const uint32_t sh = 8u * (uint32_t)(a & 3);
+    const uint32_t mis = (uint32_t)reinterpret_cast<uintptr_t>(p) & 3u;
+    const uint32_t* base = static_cast<const uint32_t*>(__builtin_assume_aligned(p - mis, 4));
+    const uint32_t sh = 8u * mis;
     uint32_t d[N + 1];
 #pragma unroll
     for (int i = 0; i <= N; i++) d[i] = base[i];
@@ -348,6 +352,9 @@ __global__ __launch_bounds__(64 * WPB) void k_q6k_q8k_gemv_span(const uint8_t* _
     Q6X<ORDER> x[NT];
 #pragma unroll
     for (int t = 0; t < NT; t++) x[t] = load_q6x<ORDER>(xq + (int64_t)(8 * t + q) * kQ8KBytes, c);
+    // x's loads go out before the span's (loads return in order: the first pass
+    // then waits for no weight bytes it does not use)
+    __builtin_amdgcn_sched_barrier(0);
     // rows past M repeat the last piece of row M-1 (their results are not stored)
     const uint8_t* span = w + (int64_t)row0 * (NB * kQ6KBytes);
     const int np = min(R, M - row0) * NB * kQ6KBytes / 16;
@@ -371,8 +378,10 @@ __global__ __launch_bounds__(64 * WPB) void k_q6k_q8k_gemv_span(const uint8_t* _
 #pragma unroll
             for (int u = 0; u < kLoads; u++) {
                 if (64 * u + 63 < p0 || 64 * u >= p0 + n) continue;
+                // pieces outside the pass go to the spare slot n: no branch around
+                // the write, so the compiler's load waits stay per load
                 const int k = lane + 64 * u - p0;
-                if (k >= 0 && k < n) *reinterpret_cast<q6u32x4*>(buf + 16 * k) = v[u];
+                *reinterpret_cast<q6u32x4*>(buf + 16 * (k >= 0 && k < n ? k : n)) = v[u];
             }
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
             const uint8_t* blk = buf + q * kQ6KBytes;
@@ -381,7 +390,11 @@ __global__ __launch_bounds__(64 * WPB) void k_q6k_q8k_gemv_span(const uint8_t* _
             uint16_t dh;
             __builtin_memcpy(&dh, blk + 208, 2);
             const float dd = f16_ieee(dh) * x[t].dy;
-            s[r] = s[r] + dd * (float)isum;
+            float acc = s[r] + dd * (float)isum;
+            // this pass's arithmetic is done before the next pass's LDS writes (which
+            // wait for their loads), not hoisted below them
+            asm volatile("" : "+v"(acc) : : "memory");
+            s[r] = acc;
         }
     }
     // k_q6k_q8k_gemv's combine
@@ -410,7 +423,7 @@ __global__ __launch_bounds__(64 * WPB) void k_q6k_q8k_gemv_span_long(const uint8
     constexpr int XD = NB * kQ8KBytes / 4;        // 4,088 dwords of x
     constexpr int XU = (XD + 64 * WPB - 1) / (64 * WPB);
     __shared__ __align__(16) uint8_t bufs[WPB][kQ6Buf];
-    __shared__ __align__(16) uint32_t xl[XD];
+    __shared__ __align__(16) uint32_t xl[XU * 64 * WPB];  // XD words and padding: every thread stores
     const int tid = threadIdx.x, lane = tid & 63;
     const int q = lane >> 3, c = lane & 7;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -429,10 +442,10 @@ __global__ __launch_bounds__(64 * WPB) void k_q6k_q8k_gemv_span_long(const uint8
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int u = 0; u < XU; u++)
-        if (tid + 64 * WPB * u < XD) xl[tid + 64 * WPB * u] = xv[u];
+    for (int u = 0; u < XU; u++) xl[tid + 64 * WPB * u] = xv[u];  // past XD: a repeat of word XD-1
     __syncthreads();
-    if (!has) return;
+    // waves past the last row run on (no early return: the compiler would sink the
+    // span loads below it, after the x copy and the barrier) and store nothing
     uint8_t* buf = bufs[wave];
     const uint8_t* xs = reinterpret_cast<const uint8_t*>(xl);
     float s = 0.0f;
@@ -442,8 +455,8 @@ __global__ __launch_bounds__(64 * WPB) void k_q6k_q8k_gemv_span_long(const uint8
 #pragma unroll
         for (int u = 0; u < kLoads; u++) {
             if (64 * u + 63 < p0 || 64 * u >= p0 + n) continue;
-            const int k = lane + 64 * u - p0;
-            if (k >= 0 && k < n) *reinterpret_cast<q6u32x4*>(buf + 16 * k) = v[u];
+            const int k = lane + 64 * u - p0;  // outside the pass: the spare slot n
+            *reinterpret_cast<q6u32x4*>(buf + 16 * (k >= 0 && k < n ? k : n)) = v[u];
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         const Q6X<ORDER> x = load_q6x<ORDER>(xs + (8 * t + q) * kQ8KBytes, c);
@@ -453,11 +466,12 @@ __global__ __launch_bounds__(64 * WPB) void k_q6k_q8k_gemv_span_long(const uint8
         uint16_t dh;
         __builtin_memcpy(&dh, blk + 208, 2);
         s = s + (f16_ieee(dh) * x.dy) * (float)isum;
+        asm volatile("" : "+v"(s) : : "memory");  // as in k_q6k_q8k_gemv_span
     }
     s = s + dpp_f<0x140>(s);
     const float p01 = readlane_f(s, 0), p23 = readlane_f(s, 16);
     const float p45 = readlane_f(s, 32), p67 = readlane_f(s, 48);
-    if (lane == 0) y[row] = (p01 + p23) + (p45 + p67);
+    if (lane == 0 && has) y[row] = (p01 + p23) + (p45 + p67);
 }
 
 void launch_qmatmul_q6k_q8k(const uint8_t* w, const uint8_t* xq, float* y, int M, int K, int order, hipStream_t s) {
