@@ -962,7 +962,6 @@ __global__ __launch_bounds__(64 * WPB) void k_q4k_q8k_gemv_span(const uint8_t* _
     if (row0 >= M) return;
     XOps xr[S::kNT][2];
     span_load_x<ORDER, NB>(xr, xq);
-    __builtin_amdgcn_sched_barrier(0);  // x's loads go out before the span's
     // rows past M repeat the last piece of row M-1 (their results are not stored)
     const uint8_t* seg[1] = {w + (int64_t)row0 * (NB * kQ4KBytes)};
     const int np[1] = {min(R, M - row0) * NB * 9};

@@ -352,9 +352,6 @@ __global__ __launch_bounds__(64 * WPB) void k_q6k_q8k_gemv_span(const uint8_t* _
     Q6X<ORDER> x[NT];
 #pragma unroll
     for (int t = 0; t < NT; t++) x[t] = load_q6x<ORDER>(xq + (int64_t)(8 * t + q) * kQ8KBytes, c);
-    // x's loads go out before the span's (loads return in order: the first pass
-    // then waits for no weight bytes it does not use)
-    __builtin_amdgcn_sched_barrier(0);
     // rows past M repeat the last piece of row M-1 (their results are not stored)
     const uint8_t* span = w + (int64_t)row0 * (NB * kQ6KBytes);
     const int np = min(R, M - row0) * NB * kQ6KBytes / 16;
