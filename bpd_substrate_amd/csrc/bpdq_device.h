@@ -145,22 +145,25 @@ __device__ __forceinline__ uint4 ld_u128(const uint8_t* p) {
     return *reinterpret_cast<const uint4*>(p);
 }
 
-// (int8_t)r for a float r, as the reference's x86 builds execute that cast
-// (/root/reference/bench/bpd_cpu.c:4133): cvttss2si to int32, which gives
-// 0x80000000 for NaN and for r outside the int32 range, then the low byte;
-// returned sign-extended.  v_cvt_i32_f32 alone differs for +Inf (it saturates
-// to 0x7FFFFFFF, low byte 0xFF), which a quantizer meets when 127/amax
-// overflows (amax < 127/FLT_MAX).  r is integral (a rint result) or not finite.
-__device__ __forceinline__ int x86_i8(float r) {
-    const int i = (r >= -2147483648.0f && r < 2147483648.0f) ? (int)r : 0;  // low byte of 0x80000000
-    return (int)(int8_t)(uint8_t)(uint32_t)i;
+// The quantizers' multiplier id = 127/amax (0 when amax is 0), made 0 where it
+// overflows to +Inf (amax < 127/FLT_MAX).  The reference's (int8_t)rintf(x*id)
+// (/root/reference/bench/bpd_cpu.c:4133) runs on x86 as cvttss2si to int32 (0x80000000
+// for NaN and out-of-range values) and keeps the low byte: every non-finite x*id
+// gives quant 0.  v_cvt_i32_f32 gives 0 for NaN and 0x80000000 for -Inf too, but
+// saturates +Inf to 0x7FFFFFFF (byte 0xFF); with a finite id, x*id is never +Inf
+// (|x| <= amax, and x = Inf makes amax = Inf and id = 0: NaN), and with id = 0 in
+// place of +Inf every quant of the block is 0 or NaN -> 0, as on x86.  So the plain
+// conversion of rint(x*q8_id(amax)) gives the reference's bytes for every input.
+__device__ __forceinline__ float q8_id(float amax) {
+    const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+    return __builtin_isinf(id) ? 0.0f : id;
 }
 
 // |v| for the quantizers' amax: the reference's scalar loop (`if (av > max)`,
 // max starting at 0) never takes a NaN, so a NaN element counts as 0 and a block
-// of NaNs keeps amax = 0.  fmaxf alone differs there (NaN when both operands
-// are NaN; a signalling NaN may win under IEEE mode).
-__device__ __forceinline__ float abs_no_nan(float v) { return __builtin_isnan(v) ? 0.0f : fabsf(v); }
+// of NaNs keeps amax = 0.  maxNum(|v|, 0) is |v|, or 0 for a NaN (the compiler
+// quiets a signalling NaN before v_max_f32), so the reduction never meets a NaN.
+__device__ __forceinline__ float abs_no_nan(float v) { return fmaxf(fabsf(v), 0.0f); }
 
 // Q8_0 quantization of one 32-element block held by 32 consecutive lanes of a
 // wave (lane = element e, all 32 active), as bpd_quant_q8_0_cpu
@@ -172,8 +175,8 @@ __device__ __forceinline__ void q8_0_lane_store(float v, uint8_t* __restrict__ y
 #pragma unroll
     for (int mask = 1; mask < 32; mask <<= 1) amax = fmaxf(amax, xor_f(amax, mask));
     const float d = amax / 127.0f;
-    const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
-    yb[2 + e] = (uint8_t)x86_i8(__builtin_rintf(v * id));
+    const float id = q8_id(amax);
+    yb[2 + e] = (uint8_t)(int8_t)(int)__builtin_rintf(v * id);
     if (e == 0) {
         const uint16_t h = __builtin_bit_cast(uint16_t, (_Float16)d);
         yb[0] = (uint8_t)(h & 0xFF);
@@ -190,11 +193,11 @@ __device__ __forceinline__ void q8_0_quad_store(float4 v, uint8_t* __restrict__ 
     amax = fmaxf(amax, dpp_f<0x4E>(amax));   // quad_perm [2,3,0,1]
     amax = fmaxf(amax, dpp_f<0x141>(amax));  // row_half_mirror: the other quad of the 8
     const float d = amax / 127.0f;
-    const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
-    const uint32_t q0 = (uint32_t)x86_i8(__builtin_rintf(v.x * id)) & 0xFFu;
-    const uint32_t q1 = (uint32_t)x86_i8(__builtin_rintf(v.y * id)) & 0xFFu;
-    const uint32_t q2 = (uint32_t)x86_i8(__builtin_rintf(v.z * id)) & 0xFFu;
-    const uint32_t q3 = (uint32_t)x86_i8(__builtin_rintf(v.w * id)) & 0xFFu;
+    const float id = q8_id(amax);
+    const uint32_t q0 = (uint32_t)(int)__builtin_rintf(v.x * id) & 0xFFu;
+    const uint32_t q1 = (uint32_t)(int)__builtin_rintf(v.y * id) & 0xFFu;
+    const uint32_t q2 = (uint32_t)(int)__builtin_rintf(v.z * id) & 0xFFu;
+    const uint32_t q3 = (uint32_t)(int)__builtin_rintf(v.w * id) & 0xFFu;
     uint16_t* p = reinterpret_cast<uint16_t*>(yb + 2 + 4 * g);
     p[0] = (uint16_t)(q0 | (q1 << 8));
     p[1] = (uint16_t)(q2 | (q3 << 8));
@@ -213,9 +216,9 @@ __device__ __forceinline__ void q8k_wave_store(float4 v, uint8_t* __restrict__ y
     amax = fmaxf(amax, dpp_f<0x140>(amax));  // row_mirror: every lane holds its 16-lane row's max
     amax = fmaxf(fmaxf(readlane_f(amax, 0), readlane_f(amax, 16)), fmaxf(readlane_f(amax, 32), readlane_f(amax, 48)));
     const float d = amax / 127.0f;
-    const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
-    const int q0 = x86_i8(__builtin_rintf(v.x * id)), q1 = x86_i8(__builtin_rintf(v.y * id));
-    const int q2 = x86_i8(__builtin_rintf(v.z * id)), q3 = x86_i8(__builtin_rintf(v.w * id));
+    const float id = q8_id(amax);
+    const int q0 = (int)__builtin_rintf(v.x * id), q1 = (int)__builtin_rintf(v.y * id);
+    const int q2 = (int)__builtin_rintf(v.z * id), q3 = (int)__builtin_rintf(v.w * id);
     const uint32_t packed = (uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) | ((uint32_t)(q2 & 0xFF) << 16) |
                             ((uint32_t)(q3 & 0xFF) << 24);
     *reinterpret_cast<uint32_t*>(yb + 4 + 4 * lane) = packed;

@@ -1160,12 +1160,12 @@ __device__ __forceinline__ void x32_quantize(const XPre<IT>& P, uint8_t* __restr
         amax = fmaxf(amax, dpp_f<0x141>(amax));  // row_half_mirror
         amax = fmaxf(amax, dpp_f<0x140>(amax));  // row_mirror: the whole 16-lane row
         const float d = amax / 127.0f;
-        const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+        const float id = q8_id(amax);
         uint32_t pk[4] = {0u, 0u, 0u, 0u};
         int bsum = 0;
 #pragma unroll
         for (int k = 0; k < 16; k++) {
-            const int qv = x86_i8(__builtin_rintf(e[k] * id));
+            const int qv = (int)__builtin_rintf(e[k] * id);
             bsum += qv;
             pk[k >> 2] |= (uint32_t)(qv & 0xFF) << (8 * (k & 3));
         }
