@@ -216,9 +216,12 @@ def test_q6k_span_in_bounds(M):
                 p0, n = (r * nb + 8 * t) * Q6 // 16, 8 * Q6 // 16
                 assert (r * nb + 8 * t) * Q6 % 16 == 0
                 for u in range(loads):
+                    if 64 * u + 63 < p0 or 64 * u >= p0 + n:
+                        continue
                     k = l + 64 * u - p0
                     ok = (k >= 0) & (k < n)
-                    assert (16 * k[ok] + 16 <= buf).all()
+                    slot = np.where(ok, k, n)            # lanes outside the pass: the spare slot n
+                    assert (16 * slot + 16 <= buf).all()
                     covered[(l + 64 * u)[ok & (l + 64 * u < pieces)]] = True
         assert covered.all()
     blk = q * Q6
@@ -248,10 +251,11 @@ def test_q6k_span_in_bounds(M):
 @pytest.mark.parametrize("M", [1, 5, 8, 9, 17, 4096])
 def test_q6k_span_long_in_bounds(M):
     """k_q6k_q8k_gemv_span_long (K = 14336, one row per wave, 8 waves per workgroup):
-    the Q8_K copy into LDS (clamped loads, guarded stores), the 735 pieces of a row
-    (clamped at the last piece; spare waves read row M-1 and store nothing), each of
-    the 7 passes' 105 pieces inside the 1,696-byte pass buffer and covered by the
-    loads, and the x operand reads from the LDS copy."""
+    the Q8_K copy into LDS (clamped loads, every thread storing into the array padded
+    to XU * 512 words), the 735 pieces of a row (clamped at the last piece; spare
+    waves read row M-1 and store nothing), each of the 7 passes' 105 pieces inside
+    the 1,696-byte pass buffer (lanes outside the pass write the spare slot 105) and
+    covered by the loads, and the x operand reads from the LDS copy."""
     Q6, NB, WPB, buf = 210, 56, 8, 8 * 210 + 16
     pieces, loads = NB * Q6 // 16, (NB * Q6 // 16 + 63) // 64
     assert pieces * 16 == NB * Q6 and (pieces, loads) == (735, 12)
@@ -262,7 +266,7 @@ def test_q6k_span_long_in_bounds(M):
         src = np.minimum(tid + 64 * WPB * u, XD - 1)
         assert 4 * src.max() + 4 <= NB * Q8K
         dst = tid + 64 * WPB * u
-        assert (dst[dst < XD] < XD).all()
+        assert dst.max() < XU * 64 * WPB                  # the padded LDS array
     assert set(np.concatenate([tid + 64 * WPB * u for u in range(XU)])) >= set(range(XD))
     grid = (M + WPB - 1) // WPB
     w_size = M * NB * Q6
@@ -279,9 +283,11 @@ def test_q6k_span_long_in_bounds(M):
         assert 8 * t * Q6 % 16 == 0
         p0, n = 8 * t * Q6 // 16, 8 * Q6 // 16
         for u in range(loads):
+            if 64 * u + 63 < p0 or 64 * u >= p0 + n:
+                continue
             k = l + 64 * u - p0
             ok = (k >= 0) & (k < n)
-            assert (16 * k[ok] + 16 <= buf).all()
+            assert (16 * np.where(ok, k, n) + 16 <= buf).all()
             covered[(l + 64 * u)[ok]] = True
         q, c = l >> 3, l & 7
         xb = (8 * t + q) * Q8K
