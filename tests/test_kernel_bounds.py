@@ -569,6 +569,44 @@ def test_q8_0_gemm_SH_in_bounds(mw, mt, K, RT):
                 src = r * bpr + (b0 + 2 * p) * Q80
                 assert (src >= 0).all() and ((src + 4 * 16 + 4) <= size).all()
                 assert ((b0 + 2 * p + 1) < nb).all()  # both staged blocks exist
+    # LDS: staged rows inside qa / qb and da / db; the scale operand rows (lanes
+    # 32-63: the zero rows 32*RT and 128, which the arrays hold as their last row)
+    lane = np.arange(64)
+    col, half = lane & 31, lane >> 5
+    for wave in range(2 * RT):
+        wr, wc = wave >> 1, wave & 1
+        ra = wr * 32 + col
+        za = np.where(half == 1, 32 * RT, ra)
+        assert za.max() <= 32 * RT and ra.max() < 32 * RT
+        for ct in range(2):
+            cb = wc * 64 + ct * 32 + col
+            assert cb.max() < 128 and np.where(half == 1, 128, cb).max() <= 128
+
+
+def h_swz(row, b):
+    return ((row >> 2) ^ (row >> 3) ^ (b >> 1)) & 1
+
+
+def test_q8_0_gemm_SH_swizzle():
+    """The quant halves' swizzle: the writer of blocks 2p, 2p+1 and the reader of
+    block u agree, and 16 consecutive lanes' 16-byte operand reads (one block,
+    rows r..r+15, one half) and 16 consecutive lanes' staging writes (rows
+    r..r+7, both parts) fall in 16 different 16-byte groups modulo 256 bytes."""
+    rows = np.arange(256)
+    for p in (0, 1):
+        assert (h_swz(rows, 2 * p) == h_swz(rows, 2 * p + 1)).all()
+    for u in range(4):
+        for half in (0, 1):
+            for r0 in range(0, 256, 16):
+                r = np.arange(r0, r0 + 16)
+                byte = (u * 128 + r) * 32 + 16 * (half ^ h_swz(r, u))
+                assert len(set((byte % 256) // 16)) == 16
+    t = np.arange(512)
+    p, row = t & 1, t >> 1
+    for h in (0, 1):
+        byte = (2 * p * 128 + row) * 32 + 16 * (h ^ h_swz(row, 2 * p))
+        for g in range(0, 512, 16):
+            assert len(set((byte[g:g + 16] % 256) // 16)) == 16
 
 
 # ---------------------------------------------------------------- Q6_K
