@@ -410,6 +410,9 @@ def main():
     rd_us = T.us_per_launch([(lambda i=i: L.bpdq_stream_read_gpu(wp[i % copies], W_BYTES // 16, sink.data_ptr()))
                              for i in range(a.steps)])
     rd_gbs = W_BYTES / (rd_us * 1e-6) / 1e9
+    # warm: one weight copy for every launch, so the 33 MB stay in the 256 MB MALL (not the metric)
+    warm_us = T.us_per_launch([gemv(0) for _ in range(a.steps)])
+    gpu.check()
 
 
     result = {
@@ -436,6 +439,9 @@ def main():
                      "launch_us": round(us, 3),
                      "stream_read_floor": {"us": round(rd_us, 3), "gb_s": round(rd_gbs, 1),
                                            "frac_of_floor": round(rd_us / us, 4)}},
+        "metric_warm_mall": {"us": round(warm_us, 3), "gb_s": round(ALG_BYTES / warm_us / 1e3, 1),
+                             "note": "one weight copy for every launch (resident in the MALL): not the metric, "
+                                     "which rotates 17 copies beyond it"},
     }
 
     if not a.no_extra:
@@ -461,9 +467,16 @@ def main():
         dq_o = [torch.empty(DQ_BLOCKS * 256, dtype=torch.float32, device=dev) for _ in range(8)]
         dq_us = T.us_per_launch([(lambda i=i: L.bpd_dequant_q4k_gpu(dq_q[i % 8].data_ptr(), dq_o[i % 8].data_ptr(),
                                                                    DQ_BLOCKS)) for i in range(400)])
+        # the write floor of one launch of the dequant's output size (67 MB), same buffers
+        wr_us = T.us_per_launch([(lambda i=i: L.bpdq_stream_write_gpu(dq_o[i % 8].data_ptr(), DQ_BLOCKS * 64, i))
+                                 for i in range(400)])
+        gpu.check()
         result["dequant_cfg0"] = {"us": round(dq_us, 3), "gelem_s": round(DQ_BLOCKS * 256 / dq_us / 1e3, 1),
                                   "gb_s": round(DQ_BYTES / dq_us / 1e3, 1),
-                                  "frac_hbm": round(DQ_BYTES / dq_us / 1e3 / HBM_PEAK_GBS, 4)}
+                                  "frac_hbm": round(DQ_BYTES / dq_us / 1e3 / HBM_PEAK_GBS, 4),
+                                  "stream_write_floor_67MB": {
+                                      "us": round(wr_us, 3), "gb_s": round(DQ_BLOCKS * 1024 / wr_us / 1e3, 1),
+                                      "note": "k_stream_write of the output bytes alone; the dequant also reads 9.4 MB"}}
         del dq_q, dq_o, dq_in
         q_us = T.us_per_launch([(lambda: L.bpd_quant_q8_k_gpu(x.data_ptr(), xq.data_ptr(), K))] * 200)
         result["quant_q8_k_4096_us"] = round(q_us, 3)
@@ -535,8 +548,19 @@ def main():
         u = T.us_per_launch([(lambda: L.bpd_qmatmul_q8_0_dispatch_s_gpu(W.data_ptr(), Xq.data_ptr(), out.data_ptr(),
                                                                          14336, 512, 4096))] * 50)
         ops = 2.0 * 512 * 4096 * 14336
+        # the device's int8 MFMA rate: register-only v_mfma_i32_32x32x32_i8 rounds, 8 waves per CU
+        probe_waves, probe_iters = 2048, 4096
+        sink = torch.zeros(4, dtype=torch.int32, device=dev)
+        pu = T.us_per_launch([(lambda: L.bpdq_mfma_i8_probe_gpu(probe_waves, probe_iters, sink.data_ptr()))] * 5)
+        gpu.check()
+        probe_tops = probe_waves * probe_iters * 4 * 32 * 32 * 32 * 2 / pu / 1e6
+        result["int8_mfma_probe"] = {"tops": round(probe_tops, 1), "frac_of_peak": round(probe_tops / 5000.0, 4),
+                                     "us": round(pu, 2),
+                                     "kernel": "k_mfma_i8_probe: 2048 waves x 4096 rounds of 4 register-only "
+                                               "v_mfma_i32_32x32x32_i8"}
         result["prefill_q8_0_cfg4"] = {"us": round(u, 2), "tops": round(ops / u / 1e6, 1),
                                        "frac_int8_mfma": round(ops / u / 1e6 / 5000.0, 4),
+                                       "frac_of_probe": round(ops / u / 1e6 / probe_tops, 4),
                                        "order": "scalar S, bit-exact vs the -O2 reference build"}
         del W, X, Xq, out
         gpu.check()

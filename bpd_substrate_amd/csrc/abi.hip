@@ -602,4 +602,27 @@ void bpdq_stream_read_gpu(const uint8_t* p, int n16, uint32_t* sink) {
     check_launch(fn);
 }
 
+void bpdq_stream_write_gpu(uint8_t* p, int n16, uint32_t value) {
+    const char* fn = "bpdq_stream_write_gpu";
+    Check c(fn);
+    c.nonneg(n16, "n16");
+    if (!c.ok || n16 == 0) return;
+    c.ptr(p, 16, "p");
+    if (!c.ok) return;
+    bpdq::launch_stream_write(p, n16, value, g_stream);
+    check_launch(fn);
+}
+
+void bpdq_mfma_i8_probe_gpu(int waves, int iters, uint32_t* sink) {
+    const char* fn = "bpdq_mfma_i8_probe_gpu";
+    Check c(fn);
+    c.nonneg(waves, "waves").nonneg(iters, "iters").multiple(waves, 4, "waves");
+    if (c.ok && waves > (1 << 20)) c.fail(BPDQ_ERR_SHAPE, "waves", "is above 2^20");
+    if (!c.ok || waves == 0) return;
+    c.ptr(sink, 4, "sink");
+    if (!c.ok) return;
+    bpdq::launch_mfma_i8_probe(waves, iters, sink, g_stream);
+    check_launch(fn);
+}
+
 }  // extern "C"

@@ -64,6 +64,8 @@ void launch_q8_pad64_dispatch_T(const uint8_t* Wp, const uint8_t* Xq, float* out
 void launch_q8_0_gemm_S(const uint8_t* Wq, const uint8_t* Xq, float* out, int m_weight, int m_tokens, int K,
                         int nan_mode, hipStream_t s);
 void launch_stream_read(const uint8_t* p, int64_t n16, uint32_t* sink, hipStream_t s);
+void launch_stream_write(uint8_t* p, int64_t n16, uint32_t value, hipStream_t s);
+void launch_mfma_i8_probe(int waves, int iters, uint32_t* sink, hipStream_t s);
 
 // Writes +0.0 to out[0..n).
 void launch_fill_zero(float* out, int64_t n, hipStream_t s);

@@ -199,6 +199,13 @@ void bpd_qmatmul_q8_0_s_gpu(const uint8_t* W_dev, const float* X_dev, float* out
  * the single-launch HBM read floor of a given size, and it is the known-traffic
  * kernel that calibrates rocprofv3's FETCH_SIZE counter. */
 void bpdq_stream_read_gpu(const uint8_t* p, int n16, uint32_t* sink);
+/* Writes n16 16-byte chunks at p once (non-temporal stores of a pattern derived
+ * from value): the single-launch HBM write floor of a given size. */
+void bpdq_stream_write_gpu(uint8_t* p, int n16, uint32_t value);
+/* waves (a multiple of 4) waves each run iters rounds of 4 register-only
+ * v_mfma_i32_32x32x32_i8 (262,144 int8 ops per round); *sink is written only
+ * if the result folds to a magic value.  The device's int8 MFMA rate. */
+void bpdq_mfma_i8_probe_gpu(int waves, int iters, uint32_t* sink);
 
 #ifdef __cplusplus
 }

@@ -80,6 +80,17 @@ def test_validation_rejects_before_launch():
     _err(3)
     L.bpd_embed_lookup_q8_0_gpu(0x1000, None, 0x3000, 2, 64)
     _err(1)
+    # measurement helpers
+    L.bpdq_stream_write_gpu(0x1000, -1, 7)
+    _err(2)
+    L.bpdq_stream_write_gpu(0x1008, 64, 7)
+    _err(3)
+    L.bpdq_mfma_i8_probe_gpu(6, 10, 0x1000)
+    assert "multiple of 4" in _err(2)
+    L.bpdq_mfma_i8_probe_gpu(8, -1, 0x1000)
+    _err(2)
+    L.bpdq_mfma_i8_probe_gpu(8, 10, None)
+    _err(1)
     # fused-quantization GEMVs: fp32 x must be 16-byte aligned, list sizes 0..4
     L.bpd_qmatmul_q4k_q8k_fused_gpu(0x1000, 0x2004, 0x3000, 4, 256)
     assert "x is not 16-byte aligned" in _err(3)
