@@ -224,11 +224,15 @@ struct Q6X {
     float dy;
 };
 
+// The Q8_K bytes a lane needs for super-block xb (load_q6x's loads).
+struct Q6XRaw {
+    uint32_t raw[8];
+    int16_t b0, b1;
+    float dy;
+};
+
 template <int ORDER>
-__device__ __forceinline__ Q6X<ORDER> load_q6x(const uint8_t* __restrict__ xb, int c) {
-    Q6X<ORDER> o;
-    __builtin_memcpy(&o.dy, xb, 4);
-    int g0, e0, e1;
+__device__ __forceinline__ void q6x_fields(int c, int& g0, int& g1, int& e0, int& e1) {
     if (ORDER == 0) {
         g0 = 2 * c;
         e0 = 32 * c;
@@ -239,13 +243,30 @@ __device__ __forceinline__ Q6X<ORDER> load_q6x(const uint8_t* __restrict__ xb, i
         e0 = 128 * h + 16 * p;
         e1 = e0 + 64;
     }
-    const int g1 = ORDER == 0 ? g0 + 1 : g0 + 4;
-    uint32_t raw[8];
+    g1 = ORDER == 0 ? g0 + 1 : g0 + 4;
+}
+
+template <int ORDER>
+__device__ __forceinline__ Q6XRaw q6x_load_raw(const uint8_t* __restrict__ xb, int c) {
+    Q6XRaw r;
+    int g0, g1, e0, e1;
+    q6x_fields<ORDER>(c, g0, g1, e0, e1);
+    __builtin_memcpy(&r.dy, xb, 4);
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-        raw[k] = ld_u32(xb + 4 + e0 + 4 * k);
-        raw[4 + k] = ld_u32(xb + 4 + e1 + 4 * k);
+        r.raw[k] = ld_u32(xb + 4 + e0 + 4 * k);
+        r.raw[4 + k] = ld_u32(xb + 4 + e1 + 4 * k);
     }
+    __builtin_memcpy(&r.b0, xb + 260 + 2 * g0, 2);
+    __builtin_memcpy(&r.b1, xb + 260 + 2 * g1, 2);
+    return r;
+}
+
+template <int ORDER>
+__device__ __forceinline__ Q6X<ORDER> q6x_regroup(const Q6XRaw& r) {
+    Q6X<ORDER> o;
+    o.dy = r.dy;
+    const uint32_t* raw = r.raw;
     if constexpr (ORDER == 0) {
 #pragma unroll
         for (int m = 0; m < 4; m++) {
@@ -265,12 +286,14 @@ __device__ __forceinline__ Q6X<ORDER> load_q6x(const uint8_t* __restrict__ xb, i
 #pragma unroll
         for (int k = 0; k < 8; k++) o.xs[k] = raw[k];
     }
-    int16_t b0, b1;
-    __builtin_memcpy(&b0, xb + 260 + 2 * g0, 2);
-    __builtin_memcpy(&b1, xb + 260 + 2 * g1, 2);
-    o.bs0 = b0;
-    o.bs1 = b1;
+    o.bs0 = r.b0;
+    o.bs1 = r.b1;
     return o;
+}
+
+template <int ORDER>
+__device__ __forceinline__ Q6X<ORDER> load_q6x(const uint8_t* __restrict__ xb, int c) {
+    return q6x_regroup<ORDER>(q6x_load_raw<ORDER>(xb, c));
 }
 
 // N consecutive words starting at LDS address p, p % 4 in {0, 2}.  The aligned
@@ -407,9 +430,12 @@ __global__ __launch_bounds__(64 * WPB) void k_q6k_q8k_gemv_span(const uint8_t* _
 
 // K = 14336 (56 super-blocks): one row per wave (735 pieces, 12 loads per lane)
 // in the same 8-block passes.  The x operands of 7 passes would not fit the
-// registers, so the workgroup first copies the Q8_K vector (16,352 bytes) into
-// LDS: its loads are issued before the span loads, the copy and one barrier
-// follow, and each pass reads its x operands from LDS.
+// registers, so the workgroup first stages them in LDS, already in the lanes'
+// form: thread t < 448 loads the Q8_K bytes of (super-block t/8, lane group t%8)
+// before the span loads are issued, regroups them after (the perm work of
+// load_q6x, done once per workgroup instead of once per wave and pass) and
+// stores one 80-byte record; one barrier; each pass reads its record with
+// aligned 16-byte LDS reads.
 template <int ORDER, int WPB>
 __global__ __launch_bounds__(64 * WPB) void k_q6k_q8k_gemv_span_long(const uint8_t* __restrict__ w,
                                                                     const uint8_t* __restrict__ xq,
@@ -417,18 +443,19 @@ __global__ __launch_bounds__(64 * WPB) void k_q6k_q8k_gemv_span_long(const uint8
     constexpr int NB = 56, NT = NB / 8;
     constexpr int kPieces = NB * kQ6KBytes / 16;  // 735
     constexpr int kLoads = (kPieces + 63) / 64;   // 12
-    constexpr int XD = NB * kQ8KBytes / 4;        // 4,088 dwords of x
-    constexpr int XU = (XD + 64 * WPB - 1) / (64 * WPB);
+    constexpr int XR = NB * 8;                    // x records: (super-block, lane group)
+    constexpr int kRec = 20;                      // dwords: xs[16], bs0, bs1, dy, pad
+    static_assert(XR <= 64 * WPB, "one record per thread");
     __shared__ __align__(16) uint8_t bufs[WPB][kQ6Buf];
-    __shared__ __align__(16) uint32_t xl[XU * 64 * WPB];  // XD words and padding: every thread stores
+    __shared__ __align__(16) uint32_t xrec[XR * kRec];
     const int tid = threadIdx.x, lane = tid & 63;
     const int q = lane >> 3, c = lane & 7;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int row = blockIdx.x * WPB + wave;
     const bool has = row < M;
-    uint32_t xv[XU];
-#pragma unroll
-    for (int u = 0; u < XU; u++) xv[u] = reinterpret_cast<const uint32_t*>(xq)[min(tid + 64 * WPB * u, XD - 1)];
+    // threads past the last record load record XR-1's bytes again (not stored)
+    const int rt = min(tid, XR - 1);
+    const Q6XRaw xr = q6x_load_raw<ORDER>(xq + (int64_t)(rt >> 3) * kQ8KBytes, rt & 7);
     // waves past the last row read row M-1 (nothing is stored for them)
     const uint8_t* span = w + (int64_t)(has ? row : M - 1) * (NB * kQ6KBytes);
     q6u32x4 v[kLoads];
@@ -438,13 +465,19 @@ __global__ __launch_bounds__(64 * WPB) void k_q6k_q8k_gemv_span_long(const uint8
         v[u] = __builtin_nontemporal_load(reinterpret_cast<const q6u32x4*>(span + 16u * p));
     }
     __builtin_amdgcn_sched_barrier(0);
+    if (tid < XR) {
+        const Q6X<ORDER> xo = q6x_regroup<ORDER>(xr);
+        uint32_t* rec = xrec + tid * kRec;
 #pragma unroll
-    for (int u = 0; u < XU; u++) xl[tid + 64 * WPB * u] = xv[u];  // past XD: a repeat of word XD-1
+        for (int k2 = 0; k2 < (ORDER == 0 ? 16 : 8); k2++) rec[k2] = xo.xs[k2];
+        rec[16] = (uint32_t)xo.bs0;
+        rec[17] = (uint32_t)xo.bs1;
+        rec[18] = __float_as_uint(xo.dy);
+    }
     __syncthreads();
     // waves past the last row run on (no early return: the compiler would sink the
     // span loads below it, after the x copy and the barrier) and store nothing
     uint8_t* buf = bufs[wave];
-    const uint8_t* xs = reinterpret_cast<const uint8_t*>(xl);
     float s = 0.0f;
 #pragma unroll
     for (int t = 0; t < NT; t++) {
@@ -456,7 +489,15 @@ __global__ __launch_bounds__(64 * WPB) void k_q6k_q8k_gemv_span_long(const uint8
             *reinterpret_cast<q6u32x4*>(buf + 16 * (k >= 0 && k < n ? k : n)) = v[u];
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        const Q6X<ORDER> x = load_q6x<ORDER>(xs + (8 * t + q) * kQ8KBytes, c);
+        Q6X<ORDER> x;
+        {
+            const uint32_t* rec = xrec + ((8 * t + q) * 8 + c) * kRec;
+#pragma unroll
+            for (int k2 = 0; k2 < (ORDER == 0 ? 16 : 8); k2++) x.xs[k2] = rec[k2];
+            x.bs0 = (int)rec[16];
+            x.bs1 = (int)rec[17];
+            x.dy = __uint_as_float(rec[18]);
+        }
         const uint8_t* blk = buf + q * kQ6KBytes;
         int isum = q6k_lane_isum_lds<ORDER>(blk, x, c);
         isum = sum8_i(isum);

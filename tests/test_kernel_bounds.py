@@ -39,6 +39,18 @@ def x_accesses(c):
             (4 + 64 * (c >> 1) + 16 * (c & 1), 16), (4 + 64 * (c >> 1) + 16 * (c & 1) + 32, 16))
 
 
+def q6x_accesses(c, order):
+    """(offset, bytes) of every Q8_K access q6x_load_raw makes for lane group c."""
+    if order == 0:
+        g0, e0 = 2 * c, 32 * c
+        g1, e1 = g0 + 1, e0 + 16
+    else:
+        h, p = c >> 2, c & 3
+        g0, e0 = 8 * h + p, 128 * h + 16 * p
+        g1, e1 = g0 + 4, e0 + 64
+    return ((0, 4), (4 + e0, 16), (4 + e1, 16), (260 + 2 * g0, 2), (260 + 2 * g1, 2))
+
+
 def check_wide(M, nb, row0, R, G):
     w_size, x_size = M * nb * Q4K, nb * Q8K
     l = lanes()
@@ -251,23 +263,25 @@ def test_q6k_span_in_bounds(M):
 @pytest.mark.parametrize("M", [1, 5, 8, 9, 17, 4096])
 def test_q6k_span_long_in_bounds(M):
     """k_q6k_q8k_gemv_span_long (K = 14336, one row per wave, 8 waves per workgroup):
-    the Q8_K copy into LDS (clamped loads, every thread storing into the array padded
-    to XU * 512 words), the 735 pieces of a row (clamped at the last piece; spare
-    waves read row M-1 and store nothing), each of the 7 passes' 105 pieces inside
-    the 1,696-byte pass buffer (lanes outside the pass write the spare slot 105) and
-    covered by the loads, and the x operand reads from the LDS copy."""
+    the x records (thread t < 448 loads the Q8_K bytes of super-block t/8, lane group
+    t%8 -- threads past them record 447's, clamped -- and stores one 20-dword record),
+    the 735 pieces of a row (clamped at the last piece; spare waves read row M-1 and
+    store nothing), each of the 7 passes' 105 pieces inside the 1,696-byte pass
+    buffer (lanes outside the pass write the spare slot 105) and covered by the
+    loads, and each pass's record read."""
     Q6, NB, WPB, buf = 210, 56, 8, 8 * 210 + 16
     pieces, loads = NB * Q6 // 16, (NB * Q6 // 16 + 63) // 64
     assert pieces * 16 == NB * Q6 and (pieces, loads) == (735, 12)
-    XD = NB * Q8K // 4
-    XU = (XD + 64 * WPB - 1) // (64 * WPB)
+    XR, REC = NB * 8, 20
+    assert XR <= 64 * WPB
     tid = np.arange(64 * WPB)
-    for u in range(XU):
-        src = np.minimum(tid + 64 * WPB * u, XD - 1)
-        assert 4 * src.max() + 4 <= NB * Q8K
-        dst = tid + 64 * WPB * u
-        assert dst.max() < XU * 64 * WPB                  # the padded LDS array
-    assert set(np.concatenate([tid + 64 * WPB * u for u in range(XU)])) >= set(range(XD))
+    rt = np.minimum(tid, XR - 1)
+    for order in (0, 1):
+        for off, size in q6x_accesses(rt & 7, order):
+            assert np.max((rt >> 3) * Q8K + off + size) <= NB * Q8K and np.min(off) >= 0
+            assert np.max(off + size) <= Q8K                  # inside the record's super-block
+    st = tid[tid < XR]
+    assert (st * REC + 18).max() < XR * REC and len(set((st * REC).tolist())) == XR
     grid = (M + WPB - 1) // WPB
     w_size = M * NB * Q6
     l = lanes()
@@ -290,11 +304,8 @@ def test_q6k_span_long_in_bounds(M):
             assert (16 * np.where(ok, k, n) + 16 <= buf).all()
             covered[(l + 64 * u)[ok]] = True
         q, c = l >> 3, l & 7
-        xb = (8 * t + q) * Q8K
-        for off, size in x_accesses(c):
-            assert np.max(xb + off + size) <= XD * 4
-        for g in range(16):
-            assert np.max(xb + 260 + 2 * g + 2) <= XD * 4
+        rec = ((8 * t + q) * 8 + c) * REC
+        assert (rec + 18).max() < XR * REC and rec.min() >= 0
     assert covered.all()
 
 
