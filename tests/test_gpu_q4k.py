@@ -75,7 +75,8 @@ def test_qgpu_memory_helpers(dev):
     assert_bits_equal(out, O.dequant_q4k(q), "qgpu_* round trip")
 
 
-@pytest.mark.parametrize("M,K", [(16, 256), (16, 4096), (77, 512), (4096, 4096), (70, 14336), (5, 16640)])
+@pytest.mark.parametrize("M,K", [(16, 256), (16, 4096), (77, 512), (4096, 4096), (70, 14336), (5, 16640),
+                                 (16, 262144), (1030, 512)])
 def test_qmatmul_q4k_reference_order(dev, M, K):
     import torch
 

@@ -784,7 +784,7 @@ def test_q8_0_qdot_P_in_bounds(n_rows, M, K):
 
 
 @pytest.mark.parametrize("M,K", [(16, 256), (16, 4096), (77, 512), (4096, 4096), (300, 256), (14336, 4096),
-                                 (64, 2048), (1, 1536), (5, 14336), (3, 16384), (2, 16640)])
+                                 (64, 2048), (1, 1536), (5, 14336), (3, 16384), (2, 16640), (16, 262144)])
 def test_qmatmul_q4k_chain_in_bounds_and_barriers(M, K):
     """k_qmatmul_q4k_chain: chunk c holds sub-blocks 6c..6c+5; producer p loads sub-blocks
     min(6c + 2p + t, nsb - 1) of row min(row0+r, M-1) (header + 16-byte qs slice), reads x of
