@@ -109,6 +109,24 @@ def test_dispatch_scalar_order(dev, mw, mt, K):
     assert_bits_equal(got, O.dispatch_q8_0(W, Xq, mw, mt, K, "S", nthreads=8), f"S-order {mw}x{mt}x{K}")
 
 
+@pytest.mark.parametrize("wo,xo", [(2, 1), (1, 3)])
+def test_dispatch_scalar_order_unaligned_operands(dev, wo, xo):
+    """W and X at byte offsets that are not multiples of 4 (tensor data in a file need
+    not be aligned): the launcher takes the kernel without dword staging, and the
+    result is the same."""
+    import torch
+
+    mw, mt, K = 130, 129, 256
+    W = synth.q8_0(mw, K, synth.key(43, 13))
+    Xq = O.quant_q8_0(synth.normal_f32(mt * K, synth.key(43, 14)))
+    wb = torch.zeros(W.size + 8, dtype=torch.uint8, device=dev)
+    xb = torch.zeros(Xq.size + 8, dtype=torch.uint8, device=dev)
+    wb[wo:wo + W.size] = _d(W, dev)
+    xb[xo:xo + Xq.size] = _d(Xq, dev)
+    got = to_np(gpu.qmatmul_q8_0_dispatch_s(wb[wo:wo + W.size], xb[xo:xo + Xq.size], mw, mt, K))
+    assert_bits_equal(got, O.dispatch_q8_0(W, Xq, mw, mt, K, "S", nthreads=8), f"S-order offsets {wo},{xo}")
+
+
 @pytest.mark.parametrize("mw,mt,K", [(130, 129, 512), (40, 9, 224)])
 def test_dispatch_scalar_order_special_scales(dev, mw, mt, K):
     """Zero, subnormal, infinite and NaN block scales in W and X: the scale products
