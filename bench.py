@@ -488,10 +488,16 @@ def main():
         c1_us = T.us_per_launch([(lambda i=i: L.bpd_qmatmul_q4k_q8k_gpu(g1[i % len(g1)].data_ptr(), xq.data_ptr(),
                                                                        y1.data_ptr(), 4096, 4096))
                                  for i in range(1000)])
+        # its single-launch read floor: k_stream_read of the same weight bytes, same copies
+        c1_rd = T.us_per_launch([(lambda i=i: L.bpdq_stream_read_gpu(g1[i % len(g1)].data_ptr(), w1.numel() // 16,
+                                                                    sink.data_ptr())) for i in range(1000)])
+        gpu.check()
         c1_bytes = 4096 * 16 * 144 + X_BYTES + 4096 * 4
         result["q4k_q8k_gemv_cfg1_4096x4096"] = {"us": round(c1_us, 3), "gb_s": round(c1_bytes / c1_us / 1e3, 1),
                                                  "frac_hbm": round(c1_bytes / c1_us / 1e3 / HBM_PEAK_GBS, 4),
-                                                 "copies": len(g1)}
+                                                 "copies": len(g1),
+                                                 "stream_read_floor": {"us": round(c1_rd, 3),
+                                                                       "frac_of_floor": round(c1_rd / c1_us, 4)}}
         del g1, w1, y1
         # Q6_K x Q8_K (GGUF element map) at the 32,000 x 4096 head of a Q4_K_M model: random
         # quant bytes with a finite f16 scale per block (seeded)
@@ -522,10 +528,15 @@ def main():
             u = T.us_per_launch([(lambda i=i: L.bpd_qmatmul_q8_0_dispatch_gpu(Ws[i % n_c].data_ptr(), Xq.data_ptr(),
                                                                              out.data_ptr(), rows, 1, k))
                                  for i in range(400)])
+            rd = T.us_per_launch([(lambda i=i: L.bpdq_stream_read_gpu(Ws[i % n_c].data_ptr(), W.numel() // 16,
+                                                                      sink.data_ptr())) for i in range(400)])
+            gpu.check()
             alg = W.numel() + Xq.numel() + rows * 4
             result[f"q8_0_gemv_{rows}x{k}"] = {"us": round(u, 3), "gb_s": round(alg / u / 1e3, 1),
                                               "frac_hbm": round(alg / u / 1e3 / HBM_PEAK_GBS, 4),
-                                              "order": "llamafile tile (T), bit-exact"}
+                                              "order": "llamafile tile (T), bit-exact",
+                                              "stream_read_floor": {"us": round(rd, 3),
+                                                                    "frac_of_floor": round(rd / u, 4)}}
             del Ws, W
         # the reference-order fp32-x GEMV (bpd_qmatmul_q4k_gpu, bit-identical to the CPU
         # reference) at the metric shape, same rotating weight copies
