@@ -132,7 +132,11 @@ def test_fused_quantize_tiny_amax_block(dev, M, K):
 
 @pytest.mark.parametrize("order", [formats.ORDER_BPD, formats.ORDER_GGUF])
 @pytest.mark.parametrize("M,K", [(4096, 4096), (14336, 4096), (4096, 14336), (1024, 4096),
-                                 (1, 256), (5, 512), (13, 2304), (9, 2048 + 256), (8193, 4096)])
+                                 (1, 256), (5, 512), (13, 2304), (9, 2048 + 256), (8193, 4096),
+                                 # dispatch boundaries: the span kernel's last one-row-per-wave
+                                 # size and its first two-row one (an odd row count), and the
+                                 # two-row wide kernel (more than 8192 rows of fewer than 16 blocks)
+                                 (2048, 4096), (2049, 4096), (8200, 2048)])
 def test_qmatmul_q4k_q8k(dev, order, M, K):
     import torch
 
