@@ -90,6 +90,81 @@ __device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) {
     return v;
 }
 
+// ----------------------------------------------------------------------------
+// NaN cells of the AVX1 tile order T (bench/bpd_gemm_q8_0_cpu.c:32-86) get the
+// bits the reference build gives them on x86, where a NaN operand comes back
+// quieted (the first operand's when both are NaN) and Inf*0, Inf-Inf give the
+// default NaN.  Which operand is first differs between the build's nine tile
+// kernels, so a cell's bits depend on the tile that computes it
+// (bench/bpd_gemm_q8_0_cpu.c:159-207: tiles of 4, then 2, then 1 rows and
+// tokens).  Measured on that build, one probe per operand pair with NaNs of both
+// signs: Ad and Bd come from the ldexpf decode of :13-26 (an f16 NaN becomes
+// +/-0x7FC00000, no payload); scale = Bd*Ad with Bd first in every tile; lane L's
+// product scale*float(p_L); its chain acc_L = prod + acc_L with the accumulator
+// first in the 1x1 tile and the product first in the others; the hsum
+// ((a0+a4)+(a2+a6))+((a1+a5)+(a3+a7)) with a per-cell mask of swapped additions
+// (t_tile_mask).  Only blocks with an Inf or NaN scale can make a lane
+// non-finite, so the others are skipped, with 0 standing in for a finite lane (a
+// finite value never decides the bits of a NaN or the sign of an infinity).
+// Called only for a cell whose sum came out NaN.  Weight block b of the row is
+// at wrow + b * bstride, its quants at +qoff.
+// ----------------------------------------------------------------------------
+__device__ __forceinline__ float x86_mul(float first, float second) {
+    const float r = first * second;
+    return __builtin_isnan(r) ? x86_nan_of(first, second) : r;
+}
+__device__ __forceinline__ float x86_add(float first, float second) {
+    const float r = first + second;
+    return __builtin_isnan(r) ? x86_nan_of(first, second) : r;
+}
+__device__ __forceinline__ float x86_add_sw(float a, float b, uint32_t sw) { return sw ? x86_add(b, a) : x86_add(a, b); }
+__device__ __forceinline__ float f16_tile(uint32_t h) {
+    if (!f16_is_nan(h)) return f16_ieee(h);
+    return __uint_as_float(((h & 0x8000u) << 16) | 0x7FC00000u);
+}
+
+// The tile of cell (row r, token t) and its hsum mask: bits 0-3 swap the pairs
+// (a0,a4), (a2,a6), (a1,a5), (a3,a7) (the right one first), bit 4 the left
+// second-level sum, bit 5 the right one, bit 6 the top addition.  *acc_first:
+// the 1x1 tile.
+__device__ __forceinline__ uint32_t t_tile_mask(int r, int t, int m_weight, int m_tokens, bool* acc_first) {
+    const int full_r = m_weight / 4 * 4, full_t = m_tokens / 4 * 4;
+    const int RM = r < full_r ? 4 : (m_weight - full_r >= 2 && r < full_r + 2) ? 2 : 1;
+    const int RN = t < full_t ? 4 : (m_tokens - full_t >= 2 && t < full_t + 2) ? 2 : 1;
+    const int i = RM == 4 ? r % 4 : RM == 2 ? r - full_r : 0;
+    const int j = RN == 4 ? t % 4 : RN == 2 ? t - full_t : 0;
+    *acc_first = RM == 1 && RN == 1;
+    if (RM == 4) return 0x12u;
+    if (RM == 2) return (RN == 1 || i == 0) ? 0u : 0x12u;
+    return RN == 4 ? 0x10u : RN == 2 ? (j == 0 ? 0x01u : 0x10u) : 0u;
+}
+
+__device__ __forceinline__ float t_order_nan_bits(const uint8_t* __restrict__ wrow, int64_t bstride, int qoff,
+                                               const uint8_t* __restrict__ xrow, int nb, int r, int t,
+                                               int m_weight, int m_tokens) {
+    bool acc_first;
+    const uint32_t m = t_tile_mask(r, t, m_weight, m_tokens, &acc_first);
+    float C[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    for (int b = 0; b < nb; b++) {
+        const uint8_t* wb = wrow + (int64_t)b * bstride;
+        const uint8_t* xb = xrow + (int64_t)b * kQ80Bytes;
+        const uint32_t hw = (uint32_t)wb[0] | ((uint32_t)wb[1] << 8);
+        const uint32_t hx = (uint32_t)xb[0] | ((uint32_t)xb[1] << 8);
+        if (!f16_exp31(hw) && !f16_exp31(hx)) continue;
+        const float scale = x86_mul(f16_tile(hx), f16_tile(hw));
+#pragma unroll
+        for (int L = 0; L < 8; L++) {
+            int p = 0;
+            for (int j = 0; j < 4; j++) p += (int)(int8_t)wb[qoff + 4 * L + j] * (int)(int8_t)xb[2 + 4 * L + j];
+            const float prod = x86_mul(scale, (float)p);
+            C[L] = acc_first ? x86_add(C[L], prod) : x86_add(prod, C[L]);
+        }
+    }
+    const float l0 = x86_add_sw(C[0], C[4], m & 1u), l1 = x86_add_sw(C[2], C[6], m & 2u);
+    const float l2 = x86_add_sw(C[1], C[5], m & 4u), l3 = x86_add_sw(C[3], C[7], m & 8u);
+    return x86_add_sw(x86_add_sw(l0, l1, m & 16u), x86_add_sw(l2, l3, m & 32u), m & 64u);
+}
+
 template <int U>
 struct WBatch {
     uint32_t q[U];   // weight bytes 2+4L..5+4L of block b
@@ -196,7 +271,12 @@ __global__ __launch_bounds__(64 * WPB) void k_q8_0_gemv_T(const uint8_t* __restr
     acc = acc + xor_f(acc, 4);
     acc = acc + xor_f(acc, 2);
     acc = acc + xor_f(acc, 1);
-    if (L == 0 && row < m_weight) out[(int64_t)tok * m_weight + row] = acc;
+    if (L == 0 && row < m_weight) {
+        if (__builtin_isnan(acc))
+            acc = t_order_nan_bits(W + (int64_t)row * wrow, bstride, LAYOUT == 0 ? 2 : 4, Xq + (int64_t)tok * bpr, nb,
+                                   row, tok, m_weight, (int)gridDim.y);
+        out[(int64_t)tok * m_weight + row] = acc;
+    }
 }
 
 // ----------------------------------------------------------------------------
@@ -353,7 +433,13 @@ __global__ __launch_bounds__(320) void k_q8_0_gemv_TP(const uint8_t* __restrict_
         acc = acc + xor_f(acc, 2);
         acc = acc + xor_f(acc, 1);
         const int orow = row0 + (tid >> 3);
-        if ((tid & 7) == 0 && orow < m_weight) out[(int64_t)tok * m_weight + orow] = acc;
+        if ((tid & 7) == 0 && orow < m_weight) {
+            if (__builtin_isnan(acc))
+                acc = t_order_nan_bits(W + (int64_t)orow * (LAYOUT == 0 ? (int64_t)nb * kQ80Bytes : 64), p.bstride,
+                                       LAYOUT == 0 ? 2 : 4, Xq + (int64_t)tok * nb * kQ80Bytes, nb, orow, tok,
+                                       m_weight, (int)gridDim.y);
+            out[(int64_t)tok * m_weight + orow] = acc;
+        }
     }
 }
 
@@ -553,7 +639,11 @@ void k_q8_0_gemv_V(const uint8_t* __restrict__ W,
     acc = acc + xor_f(acc, 8);
     acc = acc + xor_f(acc, 4);
     const int row = row0 + (lane >> 5);
-    if ((lane & 31) == 0 && row < m_weight) out[(int64_t)tok * m_weight + row] = acc;
+    if ((lane & 31) == 0 && row < m_weight) {
+        if (__builtin_isnan(acc))
+            acc = t_order_nan_bits(W + (int64_t)row * bpr, kQ80Bytes, 2, xr, nb, row, tok, m_weight, (int)gridDim.y);
+        out[(int64_t)tok * m_weight + row] = acc;
+    }
 }
 
 // Plain form of the same order for activation rows too long to stage in LDS.
@@ -585,7 +675,13 @@ __global__ __launch_bounds__(256) void k_q8_0_gemm_T(const uint8_t* __restrict__
     acc = acc + xor_f(acc, 4);
     acc = acc + xor_f(acc, 2);
     acc = acc + xor_f(acc, 1);
-    if (L == 0 && row < m_weight) out[(int64_t)tok * m_weight + row] = acc;
+    if (L == 0 && row < m_weight) {
+        if (__builtin_isnan(acc))
+            acc = t_order_nan_bits(W + (int64_t)row * (LAYOUT == 0 ? bpr : 64),
+                                   LAYOUT == 0 ? (int64_t)kQ80Bytes : (int64_t)m_weight * 64, LAYOUT == 0 ? 2 : 4,
+                                   Xq + (int64_t)tok * bpr, nb, row, tok, m_weight, (int)gridDim.y);
+        out[(int64_t)tok * m_weight + row] = acc;
+    }
 }
 
 // Every cell of an empty (K = 0) product is the empty sum, +0.0.

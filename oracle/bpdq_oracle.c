@@ -561,22 +561,60 @@ float bpdq_o_qdot_q8_0_P(const uint8_t* w, const uint8_t* a, int n_blocks) {
 }
 
 /* AVX1 llamafile tile order T, one output cell: bench/bpd_gemm_q8_0_cpu.c:32-86.
- * Lane L accumulates the 4-element partial of elements 4L..4L+3 of every block. */
-float bpdq_o_cell_q8_0_T(const uint8_t* w, const uint8_t* a, int n_blocks) {
+ * Lane L accumulates the 4-element partial of elements 4L..4L+3 of every block:
+ * scale = Ad*Bd, prod = scale*float(p_L), acc_L = prod + acc_L, then the hsum
+ * ((a0+a4)+(a2+a6))+((a1+a5)+(a3+a7)).  The values do not depend on the tile that
+ * computes the cell; the bits of a NaN do, because the reference build's code for
+ * each of the nine tile kernels puts different operands first.  Measured on that
+ * build (one probe per operand pair, NaNs of both signs):
+ *   Ad*Bd: Bd first in every tile;
+ *   prod + acc: the accumulator first in the 1x1 tile, the product first in the others;
+ *   the hsum: per cell, a mask of swapped additions, bit 0-3 for the pairs (a0,a4),
+ *   (a2,a6), (a1,a5), (a3,a7) (set: the right one first), bit 4 for the left pair
+ *   sum of the second level, bit 5 the right one, bit 6 the top addition.
+ * t_tile_spec gives the cell's tile (bench/bpd_gemm_q8_0_cpu.c:159-207: 4, then 2,
+ * then 1 rows / tokens) and its orders. */
+typedef struct { int acc_first; unsigned mask; } t_spec;
+
+static t_spec t_tile_spec(int r, int t, int m_weight, int m_tokens) {
+    /* tile size along one axis and the index inside it */
+    int full_r = m_weight / 4 * 4, full_t = m_tokens / 4 * 4;
+    int RM = r < full_r ? 4 : (m_weight - full_r >= 2 && r < full_r + 2) ? 2 : 1;
+    int RN = t < full_t ? 4 : (m_tokens - full_t >= 2 && t < full_t + 2) ? 2 : 1;
+    int i = RM == 4 ? r % 4 : RM == 2 ? r - full_r : 0;
+    int j = RN == 4 ? t % 4 : RN == 2 ? t - full_t : 0;
+    t_spec s = {RM == 1 && RN == 1, 0u};
+    if (RM == 4) s.mask = 0x12u;
+    else if (RM == 2) s.mask = (RN == 1 || i == 0) ? 0u : 0x12u;
+    else s.mask = RN == 4 ? 0x10u : RN == 2 ? (j == 0 ? 0x01u : 0x10u) : 0u;
+    return s;
+}
+
+static inline float x86_add_sw(float a, float b, unsigned sw) { return sw ? x86_add(b, a) : x86_add(a, b); }
+
+static float cell_q8_0_T(const uint8_t* w, const uint8_t* a, int n_blocks, t_spec sp) {
     float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     for (int l = 0; l < n_blocks; l++) {
         const uint8_t* ab = a + (size_t)l * 34;
         const uint8_t* wb = w + (size_t)l * 34;
         float Bd = bpdq_o_f16_ldexp(rd16(ab));
         float Ad = bpdq_o_f16_ldexp(rd16(wb));
-        float scale = Ad * Bd;
+        float scale = x86_mul(Bd, Ad);
         for (int L = 0; L < 8; L++) {
             int32_t p = sse_quad((const int8_t*)(wb + 2) + 4 * L, (const int8_t*)(ab + 2) + 4 * L);
-            float prod = scale * (float)p;
-            acc[L] = prod + acc[L];
+            float prod = x86_mul(scale, (float)p);
+            acc[L] = sp.acc_first ? x86_add(acc[L], prod) : x86_add(prod, acc[L]);
         }
     }
-    return hsum8(acc);
+    unsigned m = sp.mask;
+    float l0 = x86_add_sw(acc[0], acc[4], m & 1u), l1 = x86_add_sw(acc[2], acc[6], m & 2u);
+    float l2 = x86_add_sw(acc[1], acc[5], m & 4u), l3 = x86_add_sw(acc[3], acc[7], m & 8u);
+    return x86_add_sw(x86_add_sw(l0, l1, m & 16u), x86_add_sw(l2, l3, m & 32u), m & 64u);
+}
+
+/* The cell as the 4-row tiles compute it (the tile of every cell of a 4x4 block). */
+float bpdq_o_cell_q8_0_T(const uint8_t* w, const uint8_t* a, int n_blocks) {
+    return cell_q8_0_T(w, a, n_blocks, t_tile_spec(0, 0, 4, 4));
 }
 
 /* bench/bpd_gemm_q8_0_cpu.c:159-207: every cell of out[token * m_weight + row]
@@ -588,7 +626,8 @@ void bpdq_o_dispatch_q8_0(const uint8_t* Wq, const uint8_t* Xq, float* out, int 
         for (int r = 0; r < m_weight; r++) {
             const uint8_t* wr = Wq + (size_t)r * bpr;
             const uint8_t* xr = Xq + (size_t)t * bpr;
-            out[(size_t)t * m_weight + r] = order == 'T' ? bpdq_o_cell_q8_0_T(wr, xr, k) : bpdq_o_cell_q8_0_S(wr, xr, k);
+            out[(size_t)t * m_weight + r] = order == 'T' ? cell_q8_0_T(wr, xr, k, t_tile_spec(r, t, m_weight, m_tokens))
+                                                         : bpdq_o_cell_q8_0_S(wr, xr, k);
         }
 }
 
@@ -690,8 +729,10 @@ static void* mt_run(void* p) {
         size_t bpr = (size_t)k * 34;
         for (int t = 0; t < j->mt; t++)
             for (int r = j->r0; r < j->r1; r++)
-                j->out[(size_t)t * j->mw + r] = j->order == 'T' ? bpdq_o_cell_q8_0_T(j->a + (size_t)r * bpr, j->b + (size_t)t * bpr, k)
-                                                                : bpdq_o_cell_q8_0_S(j->a + (size_t)r * bpr, j->b + (size_t)t * bpr, k);
+                j->out[(size_t)t * j->mw + r] =
+                    j->order == 'T' ? cell_q8_0_T(j->a + (size_t)r * bpr, j->b + (size_t)t * bpr, k,
+                                                  t_tile_spec(r, t, j->mw, j->mt))
+                                    : bpdq_o_cell_q8_0_S(j->a + (size_t)r * bpr, j->b + (size_t)t * bpr, k);
     }
     return NULL;
 }

@@ -157,6 +157,55 @@ def _special(rows, nb, key):
     return raw.reshape(-1).copy()
 
 
+# each kernel of the tile-order dispatcher: the producer/consumer kernel (few waves), the
+# wide-load kernel (nb % 32 == 0, >= 256 two-row waves; 4 and 16 activation registers),
+# the pipelined kernel (>= 1024 eight-row waves) and the plain one (rows too long for LDS)
+@pytest.mark.parametrize("mw,mt,K", [(23, 19, 32), (40, 9, 224), (600, 1, 1024), (520, 3, 4096),
+                                     (600, 1, 14336), (8192, 1, 4096 + 32), (9, 2, 59392)])
+@pytest.mark.parametrize("dense", [False, True])
+def test_dispatch_tile_order_nan_bits(dev, mw, mt, K, dense):
+    """Zero, subnormal, infinite and NaN scales (with and without payload) in both
+    operands, tile order T: every cell, NaN bits included, equals the oracle, which is
+    checked against the AVX1 reference build's nine tile kernels on such inputs (each
+    tile puts different operands first).  dense: NaN / Inf scales in 40 % of the blocks
+    and zero 4-element groups (Inf * 0), several events per lane chain."""
+    nb = K // 32
+    if dense:
+        W, X = _q8_nan_heavy(mw, nb, synth.key(49, mw)), _q8_nan_heavy(mt, nb, synth.key(50, mt))
+    else:
+        W, X = _special(mw, nb, synth.key(47, mw)), _special(mt, nb, synth.key(48, mt))
+    got = to_np(gpu.qmatmul_q8_0_dispatch(_d(W, dev), _d(X, dev), mw, mt, K))
+    want = O.dispatch_q8_0(W, X, mw, mt, K, "T", nthreads=8)
+    assert np.isnan(want).any()
+    assert_bits_equal(got, want, f"tile order NaN bits {mw}x{mt}x{K}")
+
+
+@pytest.mark.parametrize("mw,mt,K", [(7, 7, 96), (5, 6, 128), (11, 3, 64), (9, 1, 160), (1, 9, 192), (2, 2, 256)])
+def test_dispatch_tile_order_nan_bits_every_tile(dev, mw, mt, K):
+    """Row and token counts whose remainders give every reference tile (4, 2 and 1 rows
+    by 4, 2 and 1 tokens), dense NaN / Inf scales."""
+    nb = K // 32
+    for seed in range(3):
+        W, X = _q8_nan_heavy(mw, nb, synth.key(51 + seed, mw)), _q8_nan_heavy(mt, nb, synth.key(54 + seed, mt))
+        got = to_np(gpu.qmatmul_q8_0_dispatch(_d(W, dev), _d(X, dev), mw, mt, K))
+        assert_bits_equal(got, O.dispatch_q8_0(W, X, mw, mt, K, "T"), f"every tile {mw}x{mt}x{K} seed {seed}")
+
+
+def _q8_nan_heavy(rows, nb, key):
+    """Q8_0 rows with 30 % of the 4-element quant groups zero and a special scale
+    (zero, subnormal, +-Inf, NaN with and without payload) in 40 % of the blocks."""
+    raw = synth.q8_0(rows, nb * 32, key).reshape(rows * nb, 34).copy()
+    rng = np.random.default_rng(key)
+    groups = raw[:, 2:].reshape(rows * nb, 8, 4)
+    groups[rng.random((rows * nb, 8)) < 0.3] = 0
+    raw[:, 2:] = groups.reshape(rows * nb, 32)
+    pick = rng.random(rows * nb) < 0.4
+    h = np.array(SPECIAL_F16, np.uint16)[rng.integers(0, len(SPECIAL_F16), rows * nb)]
+    raw[pick, 0] = (h[pick] & 0xFF).astype(np.uint8)
+    raw[pick, 1] = (h[pick] >> 8).astype(np.uint8)
+    return raw.reshape(-1).copy()
+
+
 @pytest.mark.parametrize("mw,mt,K", [(23, 19, 32), (130, 131, 512), (40, 9, 224)])
 def test_scalar_order_nan_bits_both_forms(dev, mw, mt, K):
     """NaN / Inf scales with and without payload in both operands, so that the first NaN

@@ -334,6 +334,42 @@ def test_ref_q8_0_scalar_order_nan_bits(nb):
             assert_bits_equal(got, want, f"qdot S NaN bits ({r}, {t})")
 
 
+def _q8_nan_heavy(rows, nb, key):
+    """Random quants (the whole int8 range), 30 % of the 4-element groups zero, and
+    scales drawn from the special values (zero, subnormal, +-Inf, NaN with and
+    without payload, both signs) in 40 % of the blocks: several NaN and infinity
+    events of either sign per lane chain, Inf * 0 included."""
+    raw = _q8_random(rows * nb, key).reshape(rows * nb, 34)
+    rng = np.random.default_rng(key)
+    groups = raw[:, 2:].reshape(rows * nb, 8, 4)
+    groups[rng.random((rows * nb, 8)) < 0.3] = 0
+    raw[:, 2:] = groups.reshape(rows * nb, 32)
+    pick = rng.random(rows * nb) < 0.4
+    h = np.array(SPECIAL_F16, np.uint16)[rng.integers(0, len(SPECIAL_F16), rows * nb)]
+    raw[pick, 0] = (h[pick] & 0xFF).astype(np.uint8)
+    raw[pick, 1] = (h[pick] >> 8).astype(np.uint8)
+    return raw.reshape(-1).copy()
+
+
+@pytest.mark.parametrize("mw,mt,nb", [(7, 7, 3), (5, 6, 4), (11, 3, 2), (9, 1, 5), (1, 9, 6), (2, 2, 8), (3, 5, 1)])
+def test_ref_tile_order_nan_bits_every_tile(mw, mt, nb):
+    """Order T (the AVX1 build's dispatcher): NaN bits depend on the tile kernel that
+    computes a cell, since each of the nine puts different operands first.  Shapes whose
+    row and token remainders give every tile (4, 2 and 1 rows by 4, 2 and 1 tokens),
+    dense NaN / Inf scales: every cell, NaN bits included, equals the oracle."""
+    RA = _need("avx")
+    f = _bind(RA, "bpd_qmatmul_q8_0_dispatch_cpu", [P, P, P, I, I, I])
+    n_nan = 0
+    for seed in range(6):
+        W = _q8_nan_heavy(mw, nb, synth.key(60 + seed, mw * 16 + nb))
+        X = _q8_nan_heavy(mt, nb, synth.key(70 + seed, mt * 16 + nb))
+        out = np.empty(mw * mt, np.float32)
+        f(W.ctypes.data, X.ctypes.data, out.ctypes.data, mw, mt, 32 * nb)
+        n_nan += int(np.isnan(out).sum())
+        assert_bits_equal(O.dispatch_q8_0(W, X, mw, mt, 32 * nb, "T"), out, f"tile order NaN bits seed {seed}")
+    assert n_nan > 0
+
+
 def test_ref_llamafile_scalar_build_inf_activations():
     # the scalar build's llamafile entry goes through bpd_qmatmul_q8_0_cpu (qdot S):
     # infinite activations give infinite Q8_0 scales, NaN ones quantize to zeros
