@@ -56,6 +56,58 @@ __device__ __noinline__ int ssse3_quad(uint32_t w, uint32_t a) {
     return total;
 }
 
+// NaN cells get the bits the AVX1 reference build gives them on x86, where a NaN
+// operand comes back quieted (the first operand's when both are NaN) and Inf*0,
+// Inf-Inf give the default NaN.  Operand orders measured on that build with
+// probes of two NaNs of different sign and payload per operand pair: the pair
+// deltas d = ad*wd with the activation scale first, the lane chains
+// a_L = a_L + prod with the accumulator first, the hsum as
+// ((a2+a6) + (a4+a0)) + ((a3+a7) + (a5+a1)) with the left operand of each
+// addition first; the odd block's delta with the weight scale first
+// and s = s + prod with the sum first.  Scales decode with their payload (the
+// magic-number f16 decode).  Only blocks with an Inf or NaN scale can make a lane
+// non-finite, so the pairs' other blocks are skipped, 0 standing in for a finite
+// lane.  Called only for a cell whose result came out NaN.
+__device__ __forceinline__ float p_x86_mul(float first, float second) {
+    const float r = first * second;
+    return __builtin_isnan(r) ? x86_nan_of(first, second) : r;
+}
+__device__ __forceinline__ float p_x86_add(float first, float second) {
+    const float r = first + second;
+    return __builtin_isnan(r) ? x86_nan_of(first, second) : r;
+}
+__device__ __forceinline__ float f16_magic_dec(uint32_t h) { return f16_is_nan(h) ? f16_nan_x86(h) : f16_ieee(h); }
+
+__device__ __forceinline__ float p_order_nan_bits(const uint8_t* __restrict__ wrow, const uint8_t* __restrict__ xrow,
+                                                  int nb) {
+    float a[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    for (int b = 0; b < nb / 2 * 2; b++) {  // the blocks of whole pairs
+        const uint8_t* wb = wrow + (int64_t)b * kQ80Bytes;
+        const uint8_t* xb = xrow + (int64_t)b * kQ80Bytes;
+        const uint32_t hw = ld_u16p(wb), hx = ld_u16p(xb);
+        if (!f16_exp31(hw) && !f16_exp31(hx)) continue;
+        const float d = p_x86_mul(f16_magic_dec(hx), f16_magic_dec(hw));
+        const int h = b & 1;
+        for (int i = 0; i < 4; i++) {
+            const int pi = ssse3_quad(ld_u32(wb + 2 + 4 * i), ld_u32(xb + 2 + 4 * i)) +
+                           ssse3_quad(ld_u32(wb + 18 + 4 * i), ld_u32(xb + 18 + 4 * i));
+            a[4 * h + i] = p_x86_add(a[4 * h + i], p_x86_mul(d, (float)pi));
+        }
+    }
+    const float l0 = p_x86_add(a[4], a[0]), l1 = p_x86_add(a[2], a[6]);
+    const float l2 = p_x86_add(a[5], a[1]), l3 = p_x86_add(a[3], a[7]);
+    float s = p_x86_add(p_x86_add(l1, l0), p_x86_add(l3, l2));
+    if (nb & 1) {
+        const uint8_t* wb = wrow + (int64_t)(nb - 1) * kQ80Bytes;
+        const uint8_t* xb = xrow + (int64_t)(nb - 1) * kQ80Bytes;
+        int sumi = 0;
+        for (int j = 0; j < 32; j++) sumi += (int)(int8_t)wb[2 + j] * (int)(int8_t)xb[2 + j];
+        const float d = p_x86_mul(f16_magic_dec(ld_u16p(wb)), f16_magic_dec(ld_u16p(xb)));
+        s = p_x86_add(s, p_x86_mul((float)sumi, d));
+    }
+    return s;
+}
+
 template <int U>
 struct PBatch {
     uint32_t q0[U], q1[U];  // weight dwords i and 4+i of block 2p+h
@@ -166,7 +218,10 @@ __global__ __launch_bounds__(64 * WPB) void k_q8_0_qdot_P(const uint8_t* __restr
         s += xor_i(s, 1);
         acc = acc + (float)s * (f16_ieee(ld_u16p(wl)) * xd[bl]);
     }
-    if (L == 0 && row < n_rows) out[(int64_t)tok * n_rows + row] = acc;
+    if (L == 0 && row < n_rows) {
+        if (__builtin_isnan(acc)) acc = p_order_nan_bits(W + (int64_t)row * bpr, Xq + (int64_t)tok * bpr, nb);
+        out[(int64_t)tok * n_rows + row] = acc;
+    }
 }
 
 }  // namespace

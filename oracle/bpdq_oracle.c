@@ -532,6 +532,15 @@ float bpdq_o_cell_q8_0_S(const uint8_t* w, const uint8_t* a, int n_blocks) {
 }
 
 /* AVX1 pair order P: bench/bpd_cpu.c:4208-4259. */
+/* NaN bits as the reference build gives them (measured with probes of two NaNs of
+ * different sign and payload per operand pair): the pair deltas put the activation
+ * scale first, the lane chains the accumulator first (the first NaN of a lane
+ * sticks), the odd block's delta the weight scale first and its add the running sum
+ * first; the hsum's additions, with the left operand of
+ * ((a0+a4)+(a2+a6))+((a1+a5)+(a3+a7)) first unless noted, take a4 before a0, a5 before
+ * a1, the (a2,a6) sum before the (a0,a4) one and the (a3,a7) sum before the (a1,a5)
+ * one.  (Orders within the right half that no input can tell apart are not pinned:
+ * its NaNs are always default NaNs when the left half holds none.) */
 float bpdq_o_qdot_q8_0_P(const uint8_t* w, const uint8_t* a, int n_blocks) {
     float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     int ib = 0;
@@ -541,21 +550,23 @@ float bpdq_o_qdot_q8_0_P(const uint8_t* w, const uint8_t* a, int n_blocks) {
             const uint8_t* ab = a + (size_t)(ib + h) * 34;
             const int8_t* wq = (const int8_t*)(wb + 2);
             const int8_t* aq = (const int8_t*)(ab + 2);
-            float delta = bpdq_o_f16_magic(rd16(wb)) * bpdq_o_f16_magic(rd16(ab));
+            float delta = x86_mul(bpdq_o_f16_magic(rd16(ab)), bpdq_o_f16_magic(rd16(wb)));
             for (int i = 0; i < 4; i++) {
                 int32_t p = sse_quad(wq + 4 * i, aq + 4 * i) + sse_quad(wq + 16 + 4 * i, aq + 16 + 4 * i);
-                float prod = delta * (float)p;
-                acc[4 * h + i] = prod + acc[4 * h + i];
+                float prod = x86_mul(delta, (float)p);
+                acc[4 * h + i] = x86_add(acc[4 * h + i], prod);
             }
         }
     }
-    float sumf = hsum8(acc);
+    float l0 = x86_add(acc[4], acc[0]), l1 = x86_add(acc[2], acc[6]);
+    float l2 = x86_add(acc[5], acc[1]), l3 = x86_add(acc[3], acc[7]);
+    float sumf = x86_add(x86_add(l1, l0), x86_add(l3, l2));
     for (; ib < n_blocks; ib++) {
         const uint8_t* wb = w + (size_t)ib * 34;
         const uint8_t* ab = a + (size_t)ib * 34;
         int32_t sumi = dot32((const int8_t*)(wb + 2), (const int8_t*)(ab + 2));
-        float delta = bpdq_o_f16_magic(rd16(wb)) * bpdq_o_f16_magic(rd16(ab));
-        sumf = sumf + (float)sumi * delta;
+        float delta = x86_mul(bpdq_o_f16_magic(rd16(wb)), bpdq_o_f16_magic(rd16(ab)));
+        sumf = x86_add(sumf, x86_mul((float)sumi, delta));
     }
     return sumf;
 }

@@ -368,6 +368,25 @@ def test_qdot_grid_orders_P_and_S_full_int8_range(dev, M, N, K):
         assert_bits_equal(to_np(out), O.qdot_grid(Wq, Xq, M, N, K, order), f"qdot {order} {M}x{N}x{K}")
 
 
+@pytest.mark.parametrize("M,N,K", [(3, 37, 224), (2, 9, 32), (5, 17, 4128), (1, 600, 4096), (4, 64, 96)])
+def test_qdot_grid_orders_P_and_S_nan_bits(dev, M, N, K):
+    """Dense NaN / Inf scales (with and without payload) and zero quarter sums: orders P
+    and S, every cell, NaN bits included, equals the oracle, which is checked against the
+    AVX1 and scalar reference builds on such inputs."""
+    import torch
+
+    nb = K // 32
+    Wq, Xq = _q8_nan_heavy(N, nb, synth.key(57, N)), _q8_nan_heavy(M, nb, synth.key(58, M))
+    wd, xd = _d(Wq, dev), _d(Xq, dev)
+    for name, order in (("bpd_qdot_q8_0_q8_0_grid_gpu", "P"), ("bpd_qdot_q8_0_q8_0_grid_s_gpu", "S")):
+        out = torch.full((M * N,), 1.0, device=dev)
+        gpu.lib().bpd_gpu_set_stream(torch.cuda.current_stream().cuda_stream)
+        gpu.call(name, wd, xd, out, M, N, K)
+        want = O.qdot_grid(Wq, Xq, M, N, K, order)
+        assert np.isnan(want).any()
+        assert_bits_equal(to_np(out), want, f"qdot {order} NaN bits {M}x{N}x{K}")
+
+
 @pytest.mark.parametrize("M,N,K", [(1, 14336, 4096), (4, 300, 4096), (3, 6, 96), (2, 11, 224)])
 def test_qmatmul_q8_0_orders_P_and_S(dev, M, N, K):
     import torch

@@ -370,6 +370,23 @@ def test_ref_tile_order_nan_bits_every_tile(mw, mt, nb):
     assert n_nan > 0
 
 
+@pytest.mark.parametrize("nb", [1, 2, 3, 5, 8, 13])
+def test_ref_qdot_pair_order_nan_bits(nb):
+    """Order P (the AVX1 build's bpd_qdot_q8_0_q8_0_cpu) on dense NaN / Inf scales with
+    zero quarter sums: every result, NaN bits included, equals the oracle."""
+    RA = _need("avx")
+    q = _bind(RA, "bpd_qdot_q8_0_q8_0_cpu", [P, P, I], ctypes.c_float)
+    n_nan = 0
+    for seed in range(40):
+        w = _q8_nan_heavy(1, nb, synth.key(80 + seed, nb))
+        a = _q8_nan_heavy(1, nb, synth.key(90 + seed, nb))
+        want = np.float32(q(w.ctypes.data, a.ctypes.data, nb))
+        got = np.float32(O.lib().bpdq_o_qdot_q8_0_P(w.ctypes.data, a.ctypes.data, nb))
+        n_nan += int(np.isnan(want))
+        assert_bits_equal(got, want, f"qdot P NaN bits seed {seed}")
+    assert n_nan > 0
+
+
 def test_ref_llamafile_scalar_build_inf_activations():
     # the scalar build's llamafile entry goes through bpd_qmatmul_q8_0_cpu (qdot S):
     # infinite activations give infinite Q8_0 scales, NaN ones quantize to zeros
