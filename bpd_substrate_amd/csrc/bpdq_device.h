@@ -104,6 +104,34 @@ __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
 
+// Nonzero when some byte of v is 0x80 (-128).
+__device__ __forceinline__ uint32_t has_m128(uint32_t v) {
+    const uint32_t t = v ^ 0x80808080u;
+    return (t - 0x01010101u) & ~t & 0x80808080u;
+}
+
+// The AVX1 builds' int8 products: _mm_maddubs_epi16(_mm_sign_epi8(w, w),
+// _mm_sign_epi8(a, w)) and _mm_madd_epi16 with ones, over the 4 bytes of one
+// dword: |w| read as an unsigned byte (128 for -128), a*sign(w) wrapping (-(-128)
+// is -128), each pair's sum saturated to int16, the two pairs added.  Equal to
+// the exact dot whenever no byte of a is -128 against a negative w.
+__device__ __forceinline__ int ssse3_quad_inl(uint32_t w, uint32_t a) {
+    int total = 0;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        int t = 0;
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int wi = (int8_t)(w >> (16 * h + 8 * u)), ai = (int8_t)(a >> (16 * h + 8 * u));
+            const int uw = wi < 0 ? -wi : wi;
+            const int sa = wi < 0 ? (int)(int8_t)(uint8_t)(-ai) : (wi == 0 ? 0 : ai);
+            t += uw * sa;
+        }
+        total += t > 32767 ? 32767 : (t < -32768 ? -32768 : t);
+    }
+    return total;
+}
+
 // Cross-lane moves inside a wave64.
 template <int CTRL>
 __device__ __forceinline__ int dpp_i(int v) {

@@ -91,8 +91,13 @@ __device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) {
 }
 
 // ----------------------------------------------------------------------------
-// NaN cells of the AVX1 tile order T (bench/bpd_gemm_q8_0_cpu.c:32-86) get the
-// bits the reference build gives them on x86, where a NaN operand comes back
+// Cells of the AVX1 tile order T (bench/bpd_gemm_q8_0_cpu.c:32-86) that the fast
+// kernels below cannot give bit for bit are recomputed by one lane in the
+// reference's own arithmetic (t_order_cell): NaN cells, and every cell of an
+// activation row holding a -128 quant (where SSSE3's sign/maddubs wrap: -(-128)
+// is -128 against a negative weight; the kernels use the exact dot, which the
+// Q8_0 quantizers' [-127, 127] output always gives).  NaN bits: the reference build
+// on x86 gives a NaN operand back
 // quieted (the first operand's when both are NaN) and Inf*0, Inf-Inf give the
 // default NaN.  Which operand is first differs between the build's nine tile
 // kernels, so a cell's bits depend on the tile that computes it
@@ -103,11 +108,8 @@ __device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) {
 // product scale*float(p_L); its chain acc_L = prod + acc_L with the accumulator
 // first in the 1x1 tile and the product first in the others; the hsum
 // ((a0+a4)+(a2+a6))+((a1+a5)+(a3+a7)) with a per-cell mask of swapped additions
-// (t_tile_mask).  Only blocks with an Inf or NaN scale can make a lane
-// non-finite, so the others are skipped, with 0 standing in for a finite lane (a
-// finite value never decides the bits of a NaN or the sign of an infinity).
-// Called only for a cell whose sum came out NaN.  Weight block b of the row is
-// at wrow + b * bstride, its quants at +qoff.
+// (t_tile_mask).  Weight block b of the row is at wrow + b * bstride, its quants
+// at +qoff.
 // ----------------------------------------------------------------------------
 __device__ __forceinline__ float x86_mul(float first, float second) {
     const float r = first * second;
@@ -139,9 +141,9 @@ __device__ __forceinline__ uint32_t t_tile_mask(int r, int t, int m_weight, int 
     return RN == 4 ? 0x10u : RN == 2 ? (j == 0 ? 0x01u : 0x10u) : 0u;
 }
 
-__device__ __forceinline__ float t_order_nan_bits(const uint8_t* __restrict__ wrow, int64_t bstride, int qoff,
-                                               const uint8_t* __restrict__ xrow, int nb, int r, int t,
-                                               int m_weight, int m_tokens) {
+__device__ __forceinline__ float t_order_cell(const uint8_t* __restrict__ wrow, int64_t bstride, int qoff,
+                                             const uint8_t* __restrict__ xrow, int nb, int r, int t, int m_weight,
+                                             int m_tokens) {
     bool acc_first;
     const uint32_t m = t_tile_mask(r, t, m_weight, m_tokens, &acc_first);
     float C[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
@@ -150,12 +152,10 @@ __device__ __forceinline__ float t_order_nan_bits(const uint8_t* __restrict__ wr
         const uint8_t* xb = xrow + (int64_t)b * kQ80Bytes;
         const uint32_t hw = (uint32_t)wb[0] | ((uint32_t)wb[1] << 8);
         const uint32_t hx = (uint32_t)xb[0] | ((uint32_t)xb[1] << 8);
-        if (!f16_exp31(hw) && !f16_exp31(hx)) continue;
         const float scale = x86_mul(f16_tile(hx), f16_tile(hw));
 #pragma unroll
         for (int L = 0; L < 8; L++) {
-            int p = 0;
-            for (int j = 0; j < 4; j++) p += (int)(int8_t)wb[qoff + 4 * L + j] * (int)(int8_t)xb[2 + 4 * L + j];
+            const int p = ssse3_quad_inl(ld_u32(wb + qoff + 4 * L), ld_u32(xb + 2 + 4 * L));
             const float prod = x86_mul(scale, (float)p);
             C[L] = acc_first ? x86_add(C[L], prod) : x86_add(prod, C[L]);
         }
@@ -163,6 +163,19 @@ __device__ __forceinline__ float t_order_nan_bits(const uint8_t* __restrict__ wr
     const float l0 = x86_add_sw(C[0], C[4], m & 1u), l1 = x86_add_sw(C[2], C[6], m & 2u);
     const float l2 = x86_add_sw(C[1], C[5], m & 4u), l3 = x86_add_sw(C[3], C[7], m & 8u);
     return x86_add_sw(x86_add_sw(l0, l1, m & 16u), x86_add_sw(l2, l3, m & 32u), m & 64u);
+}
+
+// Whether the activation row holds a -128 quant: the waves of the workgroup record
+// theirs in wave_m128[wave] while staging (every wave writes its entry, so no
+// clearing is needed), read after the staging barrier.
+__device__ __forceinline__ void note_m128(uint32_t* wave_m128, uint32_t any_m128) {
+    const bool w = __ballot(any_m128 != 0) != 0;
+    if ((threadIdx.x & 63) == 0) wave_m128[threadIdx.x >> 6] = w ? 1u : 0u;
+}
+__device__ __forceinline__ bool row_m128(const uint32_t* wave_m128, int nwaves) {
+    uint32_t a = 0;
+    for (int i = 0; i < nwaves; i++) a |= wave_m128[i];
+    return a != 0;
 }
 
 template <int U>
@@ -208,9 +221,10 @@ __device__ __forceinline__ float accumulate_batch(const WBatch<U>& w, const uint
 // before storing any, so staging costs one memory latency per 8*NT dwords
 // instead of one per loop trip.
 template <int NT>
-__device__ __forceinline__ void stage_x(uint32_t* __restrict__ xs, float* __restrict__ xd,
-                                        const uint8_t* __restrict__ xr, int nb) {
+__device__ __forceinline__ uint32_t stage_x(uint32_t* __restrict__ xs, float* __restrict__ xd,
+                                            const uint8_t* __restrict__ xr, int nb) {
     const int n = nb * 8;
+    uint32_t any_m128 = 0;
     for (int i0 = threadIdx.x; i0 < n; i0 += 8 * NT) {
         uint32_t v[8];
 #pragma unroll
@@ -220,7 +234,10 @@ __device__ __forceinline__ void stage_x(uint32_t* __restrict__ xs, float* __rest
         }
 #pragma unroll
         for (int u = 0; u < 8; u++)
-            if (i0 + u * NT < n) xs[i0 + u * NT] = v[u];
+            if (i0 + u * NT < n) {
+                xs[i0 + u * NT] = v[u];
+                any_m128 |= has_m128(v[u]);
+            }
     }
     for (int i0 = threadIdx.x; i0 < nb; i0 += 8 * NT) {
         uint32_t v[8];
@@ -230,6 +247,7 @@ __device__ __forceinline__ void stage_x(uint32_t* __restrict__ xs, float* __rest
         for (int u = 0; u < 8; u++)
             if (i0 + u * NT < nb) xd[i0 + u * NT] = f16_ieee(v[u]);
     }
+    return any_m128;
 }
 
 // LAYOUT 0: W is rows of 34-byte Q8_0 blocks.  LAYOUT 1: W is the padded
@@ -256,10 +274,12 @@ __global__ __launch_bounds__(64 * WPB) void k_q8_0_gemv_T(const uint8_t* __restr
     const uint32_t doff = (uint32_t)((max(min(row, m_weight - 1), row0) - row0) * wrow);
     const uint32_t voff = doff + (LAYOUT == 0 ? 2 : 4) + 4 * L;
 
+    __shared__ uint32_t wave_m128[WPB];
     WBatch<U> a, b;
     load_batch<U, LAYOUT>(a, wbase, voff, doff, 0, nb, bstride);
-    stage_x<64 * WPB>(xs, xd, Xq + (int64_t)tok * bpr, nb);
+    note_m128(wave_m128, stage_x<64 * WPB>(xs, xd, Xq + (int64_t)tok * bpr, nb));
     __syncthreads();
+    const bool xm128 = __builtin_amdgcn_readfirstlane((int)row_m128(wave_m128, WPB)) != 0;
 
     float acc = 0.0f;
     for (int b0 = 0; b0 < nb; b0 += 2 * U) {
@@ -272,9 +292,9 @@ __global__ __launch_bounds__(64 * WPB) void k_q8_0_gemv_T(const uint8_t* __restr
     acc = acc + xor_f(acc, 2);
     acc = acc + xor_f(acc, 1);
     if (L == 0 && row < m_weight) {
-        if (__builtin_isnan(acc))
-            acc = t_order_nan_bits(W + (int64_t)row * wrow, bstride, LAYOUT == 0 ? 2 : 4, Xq + (int64_t)tok * bpr, nb,
-                                   row, tok, m_weight, (int)gridDim.y);
+        if (__builtin_isnan(acc) || xm128)
+            acc = t_order_cell(W + (int64_t)row * wrow, bstride, LAYOUT == 0 ? 2 : 4, Xq + (int64_t)tok * bpr, nb,
+                               row, tok, m_weight, (int)gridDim.y);
         out[(int64_t)tok * m_weight + row] = acc;
     }
 }
@@ -403,7 +423,8 @@ __global__ __launch_bounds__(320) void k_q8_0_gemv_TP(const uint8_t* __restrict_
     // the activation row first (an L2 hit for every workgroup but the first few),
     // then the weight prefetch: loads return in order, so staging issued after
     // the prefetch would wait for all of it
-    stage_x<320>(xs, xd, Xq + (int64_t)tok * nb * kQ80Bytes, nb);
+    __shared__ uint32_t wave_m128[5];
+    note_m128(wave_m128, stage_x<320>(xs, xd, Xq + (int64_t)tok * nb * kQ80Bytes, nb));
     TpLoad regs[kTpAhead];
     if (producer) {
 #pragma unroll
@@ -411,6 +432,7 @@ __global__ __launch_bounds__(320) void k_q8_0_gemv_TP(const uint8_t* __restrict_
             if (c < nch) tp_load<LAYOUT>(regs[c], p, c);
     }
     __syncthreads();
+    const bool xm128 = __builtin_amdgcn_readfirstlane((int)row_m128(wave_m128, 5)) != 0;
     if (producer) {
         tp_products<LAYOUT>(regs[0], p, prod[0], xs, xd, 0);
         if (kTpAhead < nch) tp_load<LAYOUT>(regs[0], p, kTpAhead);
@@ -434,10 +456,10 @@ __global__ __launch_bounds__(320) void k_q8_0_gemv_TP(const uint8_t* __restrict_
         acc = acc + xor_f(acc, 1);
         const int orow = row0 + (tid >> 3);
         if ((tid & 7) == 0 && orow < m_weight) {
-            if (__builtin_isnan(acc))
-                acc = t_order_nan_bits(W + (int64_t)orow * (LAYOUT == 0 ? (int64_t)nb * kQ80Bytes : 64), p.bstride,
-                                       LAYOUT == 0 ? 2 : 4, Xq + (int64_t)tok * nb * kQ80Bytes, nb, orow, tok,
-                                       m_weight, (int)gridDim.y);
+            if (__builtin_isnan(acc) || xm128)
+                acc = t_order_cell(W + (int64_t)orow * (LAYOUT == 0 ? (int64_t)nb * kQ80Bytes : 64), p.bstride,
+                                   LAYOUT == 0 ? 2 : 4, Xq + (int64_t)tok * nb * kQ80Bytes, nb, orow, tok, m_weight,
+                                   (int)gridDim.y);
             out[(int64_t)tok * m_weight + orow] = acc;
         }
     }
@@ -616,15 +638,23 @@ void k_q8_0_gemv_V(const uint8_t* __restrict__ W,
 #pragma unroll
     for (int a = 0; a < kVAhead; a++)
         if (a < nch) v_load(pf[a], wbase, off, a, true);
+    uint32_t any_m128 = 0;
 #pragma unroll
     for (int u = 0; u < XR; u++) {
         const int i = tid + u * NT, b = i >> 3;
-        if (i < nb * 8) xs[(4 * (i & 7) + (b & 3)) * xp + (b >> 2)] = xq[u];
+        if (i < nb * 8) {
+            xs[(4 * (i & 7) + (b & 3)) * xp + (b >> 2)] = xq[u];
+            any_m128 |= has_m128(xq[u]);
+        }
     }
+    __shared__ uint32_t wave_m128[NW];
+    note_m128(wave_m128, any_m128);
 #pragma unroll
     for (int u = 0; u < XD; u++)
         if (tid + u * NT < nb) xd[tid + u * NT] = f16_ieee(xh[u]);
     __syncthreads();
+    // read once here, off the kernel's tail; wave-uniform
+    const bool xm128 = __builtin_amdgcn_readfirstlane((int)row_m128(wave_m128, NW)) != 0;
     float acc = 0.0f;
     // whole pairs of chunks, then an odd last one: no step of the loop body can be
     // skipped, so every trip issues the same loads in the same order
@@ -640,8 +670,8 @@ void k_q8_0_gemv_V(const uint8_t* __restrict__ W,
     acc = acc + xor_f(acc, 4);
     const int row = row0 + (lane >> 5);
     if ((lane & 31) == 0 && row < m_weight) {
-        if (__builtin_isnan(acc))
-            acc = t_order_nan_bits(W + (int64_t)row * bpr, kQ80Bytes, 2, xr, nb, row, tok, m_weight, (int)gridDim.y);
+        if (__builtin_isnan(acc) || xm128)
+            acc = t_order_cell(W + (int64_t)row * bpr, kQ80Bytes, 2, xr, nb, row, tok, m_weight, (int)gridDim.y);
         out[(int64_t)tok * m_weight + row] = acc;
     }
 }
@@ -660,11 +690,13 @@ __global__ __launch_bounds__(256) void k_q8_0_gemm_T(const uint8_t* __restrict__
     const uint8_t* wr = W + (int64_t)rr * (LAYOUT == 0 ? bpr : 64);
     const uint8_t* xr = Xq + (int64_t)tok * bpr;
     float acc = 0.0f;
+    uint32_t any_m128 = 0;  // the cell's 8 lanes see every activation quant
     for (int b = 0; b < nb; b++) {
         const uint8_t* wb = wr + (int64_t)b * (LAYOUT == 0 ? (int64_t)kQ80Bytes : (int64_t)m_weight * 64);
         const uint8_t* xb = xr + (int64_t)b * kQ80Bytes;
         const uint32_t wv = ld_u32(wb + (LAYOUT == 0 ? 2 : 4) + 4 * L);
         const uint32_t xv = ld_u32(xb + 2 + 4 * L);
+        any_m128 |= has_m128(xv);
         const float Ad = f16_ieee((uint32_t)wb[0] | ((uint32_t)wb[1] << 8));
         const float Bd = f16_ieee((uint32_t)xb[0] | ((uint32_t)xb[1] << 8));
         const float scale = Ad * Bd;
@@ -675,11 +707,14 @@ __global__ __launch_bounds__(256) void k_q8_0_gemm_T(const uint8_t* __restrict__
     acc = acc + xor_f(acc, 4);
     acc = acc + xor_f(acc, 2);
     acc = acc + xor_f(acc, 1);
+    any_m128 |= (uint32_t)xor_i((int)any_m128, 4);
+    any_m128 |= (uint32_t)xor_i((int)any_m128, 2);
+    any_m128 |= (uint32_t)xor_i((int)any_m128, 1);
     if (L == 0 && row < m_weight) {
-        if (__builtin_isnan(acc))
-            acc = t_order_nan_bits(W + (int64_t)row * (LAYOUT == 0 ? bpr : 64),
-                                   LAYOUT == 0 ? (int64_t)kQ80Bytes : (int64_t)m_weight * 64, LAYOUT == 0 ? 2 : 4,
-                                   Xq + (int64_t)tok * bpr, nb, row, tok, m_weight, (int)gridDim.y);
+        if (__builtin_isnan(acc) || any_m128 != 0)
+            acc = t_order_cell(W + (int64_t)row * (LAYOUT == 0 ? bpr : 64),
+                               LAYOUT == 0 ? (int64_t)kQ80Bytes : (int64_t)m_weight * 64, LAYOUT == 0 ? 2 : 4,
+                               Xq + (int64_t)tok * bpr, nb, row, tok, m_weight, (int)gridDim.y);
         out[(int64_t)tok * m_weight + row] = acc;
     }
 }

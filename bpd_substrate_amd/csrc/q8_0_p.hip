@@ -33,28 +33,8 @@ __device__ __forceinline__ uint32_t ld_u16p(const uint8_t* p) {
     return v;
 }
 
-// Nonzero when some byte of v is 0x80 (-128).
-__device__ __forceinline__ uint32_t has_m128(uint32_t v) {
-    const uint32_t t = v ^ 0x80808080u;
-    return (t - 0x01010101u) & ~t & 0x80808080u;
-}
-
-// _mm_maddubs_epi16(_mm_sign_epi8(w, w), _mm_sign_epi8(a, w)) and _mm_madd_epi16
-// with ones, over the 4 bytes of one dword: two saturated int16 pair sums, added.
-__device__ __noinline__ int ssse3_quad(uint32_t w, uint32_t a) {
-    int total = 0;
-    for (int h = 0; h < 2; h++) {
-        int t = 0;
-        for (int u = 0; u < 2; u++) {
-            const int wi = (int8_t)(w >> (16 * h + 8 * u)), ai = (int8_t)(a >> (16 * h + 8 * u));
-            const int uw = wi < 0 ? -wi : wi;  // 128 for -128, read as an unsigned byte
-            const int sa = wi < 0 ? (int)(int8_t)(uint8_t)(-ai) : (wi == 0 ? 0 : ai);
-            t += uw * sa;
-        }
-        total += t > 32767 ? 32767 : (t < -32768 ? -32768 : t);
-    }
-    return total;
-}
+// The SSSE3 arithmetic of one dword, called only for lanes that hold a -128 byte.
+__device__ __noinline__ int ssse3_quad(uint32_t w, uint32_t a) { return ssse3_quad_inl(w, a); }
 
 // NaN cells get the bits the AVX1 reference build gives them on x86, where a NaN
 // operand comes back quieted (the first operand's when both are NaN) and Inf*0,

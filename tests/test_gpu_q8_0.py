@@ -180,6 +180,20 @@ def test_dispatch_tile_order_nan_bits(dev, mw, mt, K, dense):
     assert_bits_equal(got, want, f"tile order NaN bits {mw}x{mt}x{K}")
 
 
+@pytest.mark.parametrize("mw,mt,K", [(23, 19, 224), (600, 1, 1024), (520, 3, 4096), (600, 1, 14336),
+                                     (8192, 1, 4096 + 32), (9, 2, 59392), (7, 7, 96)])
+def test_dispatch_tile_order_full_int8_range(dev, mw, mt, K):
+    """Random quant bytes over the whole int8 range in both operands: -128 activations
+    against negative weights, where SSSE3's sign/maddubs wrap, make the AVX1 build's
+    partials differ from the exact dot; every kernel of the dispatcher gives the
+    reference's bits (the activation row's -128 sends its cells to the reference-order
+    recomputation)."""
+    nb = K // 32
+    W, X = _q8_full_range(mw, nb, synth.key(59, mw)), _q8_full_range(mt, nb, synth.key(60, mt))
+    got = to_np(gpu.qmatmul_q8_0_dispatch(_d(W, dev), _d(X, dev), mw, mt, K))
+    assert_bits_equal(got, O.dispatch_q8_0(W, X, mw, mt, K, "T", nthreads=8), f"tile order int8 range {mw}x{mt}x{K}")
+
+
 @pytest.mark.parametrize("mw,mt,K", [(7, 7, 96), (5, 6, 128), (11, 3, 64), (9, 1, 160), (1, 9, 192), (2, 2, 256)])
 def test_dispatch_tile_order_nan_bits_every_tile(dev, mw, mt, K):
     """Row and token counts whose remainders give every reference tile (4, 2 and 1 rows
