@@ -127,6 +127,19 @@ def test_dispatch_scalar_order_unaligned_operands(dev, wo, xo):
     assert_bits_equal(got, O.dispatch_q8_0(W, Xq, mw, mt, K, "S", nthreads=8), f"S-order offsets {wo},{xo}")
 
 
+@pytest.mark.parametrize("mw,mt,K", [(130, 129, 512), (7, 7, 96), (256, 130, 4096), (23, 5, 224)])
+def test_dispatch_scalar_order_dense_special_scales(dev, mw, mt, K):
+    """Order S (the prefill GEMM's int8-MFMA kernels and the plain one) on dense NaN / Inf
+    scales with zero 4-element groups: every cell, NaN bits included, equals the oracle,
+    which equals the scalar reference build on such inputs."""
+    nb = K // 32
+    W, X = _q8_nan_heavy(mw, nb, synth.key(61, mw)), _q8_nan_heavy(mt, nb, synth.key(62, mt))
+    got = to_np(gpu.qmatmul_q8_0_dispatch_s(_d(W, dev), _d(X, dev), mw, mt, K))
+    want = O.dispatch_q8_0(W, X, mw, mt, K, "S", nthreads=8)
+    assert np.isnan(want).any()
+    assert_bits_equal(got, want, f"S-order dense special scales {mw}x{mt}x{K}")
+
+
 @pytest.mark.parametrize("mw,mt,K", [(130, 129, 512), (40, 9, 224)])
 def test_dispatch_scalar_order_special_scales(dev, mw, mt, K):
     """Zero, subnormal, infinite and NaN block scales in W and X: the scale products

@@ -370,6 +370,27 @@ def test_ref_tile_order_nan_bits_every_tile(mw, mt, nb):
     assert n_nan > 0
 
 
+@pytest.mark.parametrize("mw,mt,nb", [(7, 7, 3), (5, 6, 4), (11, 3, 2), (9, 1, 5), (1, 9, 6), (2, 2, 8)])
+def test_ref_scalar_order_nan_bits_dense(mw, mt, nb):
+    """Order S (the scalar build's tiles, every tile shape, and its qdot) on dense NaN /
+    Inf scales with zero 4-element groups: the oracle equals the reference build."""
+    RS = _need("scalar")
+    f = _bind(RS, "bpd_qmatmul_q8_0_dispatch_cpu", [P, P, P, I, I, I])
+    q = _bind(RS, "bpd_qdot_q8_0_q8_0_cpu", [P, P, I], ctypes.c_float)
+    bpr = nb * 34
+    for seed in range(4):
+        W = _q8_nan_heavy(mw, nb, synth.key(100 + seed, mw * 16 + nb))
+        X = _q8_nan_heavy(mt, nb, synth.key(110 + seed, mt * 16 + nb))
+        out = np.empty(mw * mt, np.float32)
+        f(W.ctypes.data, X.ctypes.data, out.ctypes.data, mw, mt, 32 * nb)
+        assert_bits_equal(O.dispatch_q8_0(W, X, mw, mt, 32 * nb, "S"), out, f"scalar tiles dense NaN seed {seed}")
+        for r in range(mw):
+            for t in range(mt):
+                want = np.float32(q(W.ctypes.data + r * bpr, X.ctypes.data + t * bpr, nb))
+                got = np.float32(O.lib().bpdq_o_qdot_q8_0_S(W.ctypes.data + r * bpr, X.ctypes.data + t * bpr, nb))
+                assert_bits_equal(got, want, f"qdot S dense NaN ({r}, {t}) seed {seed}")
+
+
 @pytest.mark.parametrize("nb", [1, 2, 3, 5, 8, 13])
 def test_ref_qdot_pair_order_nan_bits(nb):
     """Order P (the AVX1 build's bpd_qdot_q8_0_q8_0_cpu) on dense NaN / Inf scales with
