@@ -175,7 +175,7 @@ def _median_ms(run, runs):
 
 
 def cpu_baseline(w_host, x_host, runs=10):
-    """the reference C of the path on this host's cores, 1 core
+    """The CPU baseline: the reference C of the path on this host's cores, 1 core
     and all cores (a pinned thread per core over disjoint rows / blocks, which leaves
     every output's bits unchanged), median of `runs` runs per leg, full config sizes.
     Legs: cfg0 bpd_dequant_q4k and the metric-shape bpd_qmatmul_q4k (bench/bpd_quant.c,
