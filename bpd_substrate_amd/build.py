@@ -39,6 +39,11 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     # MFMA results in VGPRs: the prefill epilogue reads every one with the VALU
     "-mllvm", "-amdgpu-mfma-vgpr-form=1",
+    # kernel arguments preloaded into SGPRs at wave launch (gfx950), so a wave's first
+    # loads do not wait for scalar loads of its arguments (the code object keeps a
+    # prologue that loads them for firmware without preloading).  Measured on the metric
+    # GEMV: 6.93 -> 6.68 us per launch, same bits.
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-Wall", "-Wno-unused-result",
 ]
 
