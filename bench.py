@@ -5,11 +5,14 @@
 
 A step is one Q4_K x Q8_K GEMV at M=14336, K=4096 (the metric workload) with
 the weight, the Q8_K activation and the output already resident in HBM.  The
-weight rotates over >= 16 distinct copies (> 512 MB) so the 256 MB MALL cannot
-serve it.  The K timed launches go back to back on one stream behind a GPU
-spin (so the host has queued them before the start event runs): as eager
-launches after a few untimed warm-up launches for K <= 64 (the driver's
---steps 20), as one HIP graph for longer regions.  HIP events on that stream
+weight rotates over distinct copies so the 256 MB MALL cannot serve it: at
+least 16 (> 512 MB), and for eager regions K + 8, so that the K timed launches
+read K different copies and the 8 untimed warm-up launches before them read 8
+others (264 MB, which also push the previous region's copies out).  The K timed
+launches go back to back on one stream behind a GPU spin (so the host has
+queued them before the start event runs): as eager launches after the warm-up
+launches for K <= 64 (the driver's --steps 20), as one HIP graph for longer
+regions.  HIP events on that stream
 bracket the K launches, so the host's launch rate cannot hide or inflate
 kernel time; the median over 7 timed regions is kept.  `value` and
 `roofline.achieved` are the algorithmic bytes of one GEMV divided by that
@@ -97,12 +100,16 @@ class Timer:
         e.synchronize()
         return s.elapsed_time(e)
 
-    def us_per_launch(self, launches, repeats=7, graph=None):
+    def us_per_launch(self, launches, repeats=7, graph=None, warm=None):
         """graph: None picks by K; True always captures (for "launches" that are whole
-        decode steps of hundreds of kernels, which the host could not queue ahead)."""
+        decode steps of hundreds of kernels, which the host could not queue ahead).
+        warm: the eager regions' untimed warm-up launches (default: the last 4 timed
+        ones).  Launches that rotate weight copies pass launches of copies that the
+        first timed launches do not read, so that no timed launch finds its weights
+        in the MALL from the warm-up."""
         torch = self.torch
         if not graph and len(launches) <= self.EAGER_MAX:
-            warm = launches[-min(4, len(launches)):]
+            warm = warm if warm is not None else launches[-min(4, len(launches)):]
 
             def run_all(fs):
                 for fn in fs:
@@ -380,7 +387,10 @@ def main():
     w_host = synth.q4k(M, K, synth.key(42, synth.STREAM["metric_w"]))
     x_host = synth.normal_f32(K, synth.key(42, synth.STREAM["metric_x"]))
     w0 = torch.from_numpy(w_host).to(dev)
-    copies = max(a.copies, -(-512 * 2**20 // W_BYTES))
+    # eager regions (--steps <= 64) read `steps` distinct copies, and their warm-up 8 more, so
+    # that no timed launch reads a copy that the warm-up or the previous region left in the
+    # 256 MB MALL; graph regions cycle >= 512 MiB of copies
+    copies = max(a.copies, -(-512 * 2**20 // W_BYTES), a.steps + 8 if a.steps <= Timer.EAGER_MAX else 0)
     ws = [w0] + [w0.clone() for _ in range(copies - 1)]
     x = torch.from_numpy(x_host).to(dev)
     xq = torch.empty(X_BYTES, dtype=torch.uint8, device=dev)
@@ -401,14 +411,19 @@ def main():
     gpu.check()
 
     log(f"timing {a.steps} GEMVs over {copies} weight copies ({copies * W_BYTES / 2**20:.0f} MiB)")
-    us = T.us_per_launch([gemv(i) for i in range(a.steps)])
+    # eager warm-up on the 8 copies after the timed ones (264 MB): the first timed launches'
+    # copies were last read a whole region earlier
+    cold_warm = range(copies - 8, copies)
+    us = T.us_per_launch([gemv(i) for i in range(a.steps)], warm=[gemv(i) for i in cold_warm])
     gpu.check()
     ms_per_step = us * 1e-3
     value = ALG_BYTES / (us * 1e-6) / 1e9
 
     # single-launch streaming-read floor for the same bytes, same copies
-    rd_us = T.us_per_launch([(lambda i=i: L.bpdq_stream_read_gpu(wp[i % copies], W_BYTES // 16, sink.data_ptr()))
-                             for i in range(a.steps)])
+    def read(i):
+        return lambda: L.bpdq_stream_read_gpu(wp[i % copies], W_BYTES // 16, sink.data_ptr())
+
+    rd_us = T.us_per_launch([read(i) for i in range(a.steps)], warm=[read(i) for i in cold_warm])
     rd_gbs = W_BYTES / (rd_us * 1e-6) / 1e9
     # warm: one weight copy for every launch, so the 33 MB stay in the 256 MB MALL (not the
     # metric; skipped with --no-extra, so that a kernel trace of that run holds only the
@@ -445,7 +460,7 @@ def main():
     if warm_us is not None:
         result["metric_warm_mall"] = {"us": round(warm_us, 3), "gb_s": round(ALG_BYTES / warm_us / 1e3, 1),
                                       "note": "one weight copy for every launch (resident in the MALL): not the "
-                                              "metric, which rotates 17 copies beyond it"}
+                                              f"metric, which rotates {copies} copies beyond it"}
 
     if not a.no_extra:
         # the same kernel family with the launch cost shared: two 14336x4096 matrices of one
@@ -455,9 +470,14 @@ def main():
         y_arr = (ctypes.c_void_p * 2)(y.data_ptr(), y2.data_ptr())
         m_arr = (ctypes.c_int * 2)(M, M)
         w_arrs = [(ctypes.c_void_p * 2)(wp[i % copies], wp[(i + 1) % copies]) for i in range(copies)]
-        pair_us = T.us_per_launch([(lambda i=i: L.bpd_qmatmul_q4k_q8k_multi_gpu(
-            ctypes.addressof(w_arrs[(2 * i) % copies]), ctypes.addressof(y_arr), ctypes.addressof(m_arr), 2,
-            xq.data_ptr(), K)) for i in range(a.steps // 2)])
+        def pair(i):
+            return lambda: L.bpd_qmatmul_q4k_q8k_multi_gpu(ctypes.addressof(w_arrs[(2 * i) % copies]),
+                                                           ctypes.addressof(y_arr), ctypes.addressof(m_arr), 2,
+                                                           xq.data_ptr(), K)
+
+        # warm-up on the copies after the timed ones (the pairs of cold_warm)
+        pair_us = T.us_per_launch([pair(i) for i in range(a.steps // 2)],
+                                  warm=[pair(i) for i in range((copies - 8) // 2, copies // 2)])
         gpu.check()
         pair_bytes = 2 * W_BYTES + X_BYTES + 2 * Y_BYTES
         result["two_matrix_launch_2x14336x4096"] = {

@@ -23,6 +23,7 @@ HIP_SIGNATURES = {
     "bpd_gpu_last_error": (I, []),
     "bpd_gpu_last_error_message": (ctypes.c_char_p, []),
     "bpd_gpu_set_stream": (None, [P]),
+    "bpd_gpu_workspace_release": (None, [P]),
     "bpd_dequant_q4k_gpu": (None, [P, P, I]),
     "bpd_qmatmul_q4k_gpu": (None, [P, P, P, I, I]),
     "qgpu_alloc": (P, [I]),

@@ -76,28 +76,62 @@ struct Check {
 // share a buffer, calls on different streams get different buffers.  A caller
 // keeps the entry locked (WsLease) from its request until its launches are
 // enqueued, so two host threads on one stream cannot interleave their quantize
-// and GEMM launches over one buffer.  A buffer is replaced only when a request
-// outgrows it: the stream is drained first (only that stream uses it), so no
-// pending launch reads freed memory.  Inside graph capture nothing is
-// allocated or drained: a request that does not fit fails with
-// BPDQ_ERR_CAPTURE (run the call once outside capture first).
+// and GEMM launches over one buffer.
+//
+// A buffer is never freed while its entry lives.  When a request outgrows it, a
+// new buffer (at least twice the old size, so the buffers kept add up to less
+// than twice the largest) becomes current and the old one is kept on the
+// entry's retired list: a HIP graph captured earlier holds the old address and
+// may still be replayed, on any stream.  Only bpd_gpu_workspace_release(), which
+// the caller makes once no captured graph uses the stream's buffers, frees them.
+// Inside graph capture nothing is allocated: a request that does not fit fails
+// with BPDQ_ERR_CAPTURE (run the call once outside capture first).
+//
+// Entries are never deleted, only recycled (dev = -1 marks a free entry), so a
+// pointer taken from the table stays valid; the lease re-checks the entry's
+// owner once it holds the entry's lock.
+constexpr int kWsEntries = 64;
+constexpr int kWsRetired = 32;  // growths per entry: doubling from 1 MiB passes any device's memory first
 struct WsEntry {
-    int dev;
-    hipStream_t stream;
+    int dev = -1;
+    hipStream_t stream = nullptr;
     std::mutex mu;
     void* p = nullptr;
     size_t bytes = 0;
+    void* retired[kWsRetired] = {};
+    int n_retired = 0;
 };
 std::mutex g_ws_table_mu;
-WsEntry* g_ws_table[64];
+WsEntry* g_ws_table[kWsEntries];
 int g_ws_count = 0;
+
+WsEntry* ws_find(int dev, hipStream_t s) {
+    for (int i = 0; i < g_ws_count; i++)
+        if (g_ws_table[i]->dev == dev && g_ws_table[i]->stream == s) return g_ws_table[i];
+    return nullptr;
+}
+
+// Whether e still belongs to (dev, s); the caller holds e->mu (lock order: an
+// entry's lock, then the table's).
+bool ws_owned(WsEntry* e, int dev, hipStream_t s) {
+    std::lock_guard<std::mutex> lk(g_ws_table_mu);
+    return e->dev == dev && e->stream == s;
+}
 
 WsEntry* ws_entry(int dev, hipStream_t s, const char* fn) {
     std::lock_guard<std::mutex> lk(g_ws_table_mu);
+    if (WsEntry* e = ws_find(dev, s)) return e;
     for (int i = 0; i < g_ws_count; i++)
-        if (g_ws_table[i]->dev == dev && g_ws_table[i]->stream == s) return g_ws_table[i];
-    if (g_ws_count == (int)(sizeof g_ws_table / sizeof g_ws_table[0])) {
-        set_err(BPDQ_ERR_ALLOC, fn, "more than 64 (device, stream) workspaces");
+        if (g_ws_table[i]->dev == -1) {  // a released entry: its lock may still be held by a
+            WsEntry* e = g_ws_table[i];  // lease that re-checks the owner and retries
+            e->dev = dev;
+            e->stream = s;
+            return e;
+        }
+    if (g_ws_count == kWsEntries) {
+        set_err(BPDQ_ERR_ALLOC, fn,
+                "more than 64 (device, stream) workspaces: release those of finished streams with "
+                "bpd_gpu_workspace_release");
         return nullptr;
     }
     WsEntry* e = new WsEntry;  // lives until the process ends
@@ -114,9 +148,14 @@ WsLease workspace(size_t bytes, hipStream_t s, const char* fn) {
     WsLease L;
     int dev = 0;
     if (!hip_ok(hipGetDevice(&dev), fn)) return L;
-    WsEntry* e = ws_entry(dev, s, fn);
-    if (!e) return L;
-    L.lock = std::unique_lock<std::mutex>(e->mu);
+    WsEntry* e = nullptr;
+    for (;;) {  // the entry may be released and recycled between lookup and lock
+        e = ws_entry(dev, s, fn);
+        if (!e) return L;
+        L.lock = std::unique_lock<std::mutex>(e->mu);
+        if (ws_owned(e, dev, s)) break;
+        L.lock.unlock();
+    }
     if (bytes <= e->bytes) {
         L.ptr = e->p;
         return L;
@@ -127,19 +166,20 @@ WsLease workspace(size_t bytes, hipStream_t s, const char* fn) {
         set_err(BPDQ_ERR_CAPTURE, fn, "the workspace must grow, which cannot happen during stream capture");
         return L;
     }
-    if (e->p) {
-        if (!hip_ok(hipStreamSynchronize(s), fn)) return L;
-        (void)hipFree(e->p);
-        e->p = nullptr;
-        e->bytes = 0;
-    }
-    const size_t want = (bytes + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);  // whole MiB
-    if (hipMalloc(&e->p, want) != hipSuccess) {
-        (void)hipGetLastError();
-        set_err(BPDQ_ERR_ALLOC, fn, "workspace allocation failed");
-        e->p = nullptr;
+    if (e->p != nullptr && e->n_retired == kWsRetired) {
+        set_err(BPDQ_ERR_ALLOC, fn, "the stream's workspace grew 32 times: release it with bpd_gpu_workspace_release");
         return L;
     }
+    size_t want = (bytes + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);  // whole MiB
+    if (want < 2 * e->bytes) want = 2 * e->bytes;
+    void* p = nullptr;
+    if (hipMalloc(&p, want) != hipSuccess) {
+        (void)hipGetLastError();
+        set_err(BPDQ_ERR_ALLOC, fn, "workspace allocation failed");
+        return L;
+    }
+    if (e->p != nullptr) e->retired[e->n_retired++] = e->p;  // kept for graphs captured with it
+    e->p = p;
     e->bytes = want;
     L.ptr = e->p;
     return L;
@@ -147,6 +187,31 @@ WsLease workspace(size_t bytes, hipStream_t s, const char* fn) {
 }  // namespace bpdq
 
 namespace {
+
+// Frees every buffer of (current device, s) after the whole device is idle (a
+// graph captured on s may have been replayed on another stream), and recycles
+// the entry.
+void workspace_release(hipStream_t s, const char* fn) {
+    int dev = 0;
+    if (!hip_ok(hipGetDevice(&dev), fn)) return;
+    WsEntry* e = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(g_ws_table_mu);
+        e = ws_find(dev, s);
+    }
+    if (e == nullptr) return;  // nothing was ever allocated for it
+    std::unique_lock<std::mutex> lk(e->mu);  // waits for a lease that is enqueueing
+    if (!ws_owned(e, dev, s)) return;  // released meanwhile
+    if (!hip_ok(hipDeviceSynchronize(), fn)) return;
+    for (int i = 0; i < e->n_retired; i++) hip_ok(hipFree(e->retired[i]), fn);
+    if (e->p != nullptr) hip_ok(hipFree(e->p), fn);
+    e->n_retired = 0;
+    e->p = nullptr;
+    e->bytes = 0;
+    std::lock_guard<std::mutex> tl(g_ws_table_mu);
+    e->dev = -1;
+    e->stream = nullptr;
+}
 
 void dequant_q4k(const uint8_t* q, float* out, int nb, int order, const char* fn) {
     Check c(fn);
@@ -273,6 +338,8 @@ int bpd_gpu_last_error(void) {
 const char* bpd_gpu_last_error_message(void) { return g_msg; }
 
 void bpd_gpu_set_stream(void* s) { g_stream = static_cast<hipStream_t>(s); }
+
+void bpd_gpu_workspace_release(void* s) { workspace_release(static_cast<hipStream_t>(s), "bpd_gpu_workspace_release"); }
 
 // ---- Q4_K -------------------------------------------------------------------
 void bpd_dequant_q4k_gpu(const uint8_t* q, float* out, int n_blocks) {

@@ -1,6 +1,6 @@
 // q8_0_p.hip — the AVX1 build's pair order P of bpd_qdot_q8_0_q8_0_cpu
 // (/root/reference/bench/bpd_cpu.c:4208-4259) for a grid of cells, and the
-// entry points bpd_qdot_q8_0_q8_0_gpu / bpd_qmatmul_q8_0_gpu built on it.
+// entry points bpd_qdot_q8_0_q8_0_grid_gpu (and _grid_s_gpu) / bpd_qmatmul_q8_0_gpu built on it.
 //
 // Per output cell (weight row n, activation row m), with nb blocks:
 //   8 fp32 lanes a_L = +0.0; for each block pair (2p, 2p+1), p < nb/2:

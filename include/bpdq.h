@@ -44,6 +44,16 @@ int bpd_gpu_last_error(void);
 const char* bpd_gpu_last_error_message(void);
 /* Launch stream for every later call (a hipStream_t; NULL = the null stream). */
 void bpd_gpu_set_stream(void* hip_stream);
+/* No counterpart in the reference (its CPU functions malloc per call).  The
+ * entry points that quantize fp32 activations keep them in a device workspace
+ * owned by the library, one per (device, stream), at most 64 at once.  A
+ * workspace only grows, and a buffer it outgrows is kept, not freed: a HIP graph
+ * captured with it may still replay into it.  This call frees every buffer of
+ * (current device, hip_stream) after waiting for the whole device to go idle,
+ * and frees the stream's slot of the 64.  Call it before destroying a stream
+ * that library calls ran on, and only once no captured graph that holds
+ * library calls made on that stream will be replayed again. */
+void bpd_gpu_workspace_release(void* hip_stream);
 
 /* ---- Q4_K: bench/bpd_quant_gpu.cu:160-178 ------------------------------- */
 /* out[256 b + e] = dequant of Q4_K block b in the bpd element map
@@ -149,8 +159,10 @@ void bpd_qmatmul_q8_0_dispatch_gpu(const uint8_t* Wq_dev, const uint8_t* Xq_dev,
                                    int m_tokens, int K);
 /* quantize X (fp32, m_tokens x K) then the dispatcher (bench/bpd_cpu.c:4429-4452).
  * The Q8_0 rows of X go to a device workspace owned by the library, one per
- * (device, stream), grown on demand; growth fails with BPDQ_ERR_CAPTURE during
- * stream capture.  Calls on one stream may come from several host threads. */
+ * (device, stream), grown on demand (buffers it outgrows are kept for graphs
+ * captured with them, see bpd_gpu_workspace_release); growth fails with
+ * BPDQ_ERR_CAPTURE during stream capture.  Calls on one stream may come from
+ * several host threads. */
 void bpd_qmatmul_q8_0_llamafile_gpu(const uint8_t* W_dev, const float* X_dev, float* out_dev, int m_weight,
                                     int m_tokens, int K);
 

@@ -225,3 +225,62 @@ def test_argmax_equals_reference(dev, n):
         gpu._use_torch_stream()
         gpu.call("bpd_argmax_gpu", _d(x, dev), n, out)
         assert int(out.item()) == O.argmax(x), (n, i)
+
+
+def test_captured_step_survives_workspace_growth(dev):
+    """A decode step captured in a HIP graph holds the address of its stream's
+    workspace.  A later, larger llamafile call on the same stream grows that
+    workspace; the buffer the graph holds must stay allocated, so replays still
+    give the eager bits and write into no memory allocated since.  After
+    bpd_gpu_workspace_release the stream allocates afresh and steps as before."""
+    cfg = LM.config(L=2)
+    layers, head = LM.make(cfg, 0, seed=13)
+    m = _gpu_model(cfg, layers, head, llama.W_Q8_PAD64, dev)
+    e = _d(LM.embeddings(cfg, 1, seed=14)[0], dev)
+    mw, mt, K = 64, 64, 16384                  # X's Q8_0 rows: 1,114,112 B, above the step's 1 MiB
+    W = _d(LM.synth.q8_0(mw, K, LM.synth.key(70, 1)), dev)
+    Xh = LM.synth.normal_f32(mt * K, LM.synth.key(70, 2))
+    X = _d(Xh, dev)
+    s = torch.cuda.Stream()
+    try:
+        with torch.cuda.stream(s):
+            print("workspace growth: eager step on a new stream", flush=True)
+            m.enqueue(e, 0)
+            s.synchronize()
+            want_logits = to_np(m.buf_t["logits"]).copy()
+            want_tok = int(m.buf_t["argmax_result"][0].item())
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=s):
+                m.enqueue(e, 0)
+            print("workspace growth: larger llamafile call on the same stream", flush=True)
+            out = torch.zeros(mt * mw, device=dev)
+            gpu._use_torch_stream()
+            gpu.call("bpd_qmatmul_q8_0_llamafile_gpu", W, X, out, mw, mt, K)
+            s.synchronize()
+            assert_bits_equal(to_np(out), O.qmatmul_q8_0_llamafile(LM.synth.q8_0(mw, K, LM.synth.key(70, 1)), Xh,
+                                                                    mw, mt, K), "llamafile after growth")
+            guard = [torch.full((1 << 18,), 7.0, device=dev) for _ in range(8)]   # 8 x 1 MiB, allocated since
+            torch.cuda.synchronize()
+            for rep in range(3):
+                print(f"workspace growth: replay {rep}", flush=True)
+                m.buf_t["logits"].zero_()
+                m.buf_t["argmax_result"].fill_(-1)
+                g.replay()
+                s.synchronize()
+                assert_bits_equal(to_np(m.buf_t["logits"]), want_logits, f"replayed step {rep}")
+                assert int(m.buf_t["argmax_result"][0].item()) == want_tok
+                assert all(bool((t == 7.0).all()) for t in guard), "a replay wrote into memory allocated later"
+            del g
+        torch.cuda.synchronize()
+        gpu.lib().bpd_gpu_set_stream(None)
+        gpu.call("bpd_gpu_workspace_release", s.cuda_stream)
+        with torch.cuda.stream(s):
+            print("workspace growth: eager step after release", flush=True)
+            m.buf_t["logits"].zero_()
+            m.enqueue(e, 0)
+            s.synchronize()
+            assert_bits_equal(to_np(m.buf_t["logits"]), want_logits, "step after release")
+    finally:
+        torch.cuda.synchronize()
+        gpu.lib().bpd_gpu_set_stream(None)
+        gpu.lib().bpd_gpu_workspace_release(s.cuda_stream)
