@@ -89,6 +89,12 @@ HIP_SIGNATURES = {
     "gpu_sync": (None, []),
     "gpu_free": (None, [P]),
     "bpd_llama_step_gpu": (I, [I, P, P, P, P, I, P, P, P, P, I, I]),
+    "bpd_llama_step_ext_gpu": (I, [I, P, P, P, P, P, I, P, P, P, P, I, I]),
+    # bench/bpd_llamatov_infer.py:459-466 binds bpd_llama_forward_cpu with these argtypes
+    "bpd_llama_block_gpu": (None, [P, P, P, P, I, I, P, P, P, P, P, P]),
+    "bpd_llama_block_s_gpu": (None, [P, P, P, P, I, I, P, P, P, P, P, P]),
+    "bpd_llama_forward_gpu": (None, [P, I, P, P, P, I, P, P, P, P]),
+    "bpd_llama_forward_s_gpu": (None, [P, I, P, P, P, I, P, P, P, P]),
     "bpd_residual_rmsnorm_gpu": (None, [P, P, P, P, P, P, I, F]),
     "bpd_expf_gpu": (None, [P, P, I]),
     "bpd_argmax_gpu": (None, [P, I, P]),

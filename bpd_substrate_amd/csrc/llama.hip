@@ -30,10 +30,13 @@
 //   - the RMSNorm sum of squares is binary64 like the reference's; its
 //     parallel sum is used only when an error bound proves it gives the same
 //     fp32 mean as the reference's sequential binary64 sum.
+#include <algorithm>
 #include <climits>
 #include <cmath>
 #include <cstdio>
+#include <cstring>
 #include <mutex>
+#include <vector>
 
 #include "../../include/bpdq.h"
 #include "../../include/bpdq_llama.h"
@@ -65,7 +68,8 @@ constexpr int kMaxCtx = 32768;  // one head's scores stay in LDS (128 KB)
 // the norm weight loaded alongside.  Q8_0 blocks are 8 consecutive lanes.
 // xk (or NULL) receives Q8_K blocks of h, the bytes k_quant_q8k writes: chunk
 // c of a thread is lane c % 64 of block c / 64, so each block is one whole wave
-// (n % 256 == 0 when xk is given).
+// (n % 256 == 0 when xk is given).  Workgroup b normalizes row b of row-major
+// [rows][n] tensors (bpd_rmsnorm_llama_cpu's n_rows).
 template <int NT, int MAXC>
 __global__ __launch_bounds__(NT) void k_residual_rmsnorm(const float* x_in, const float* __restrict__ add,
                                                          float* x_out, const float* __restrict__ w,
@@ -75,6 +79,15 @@ __global__ __launch_bounds__(NT) void k_residual_rmsnorm(const float* x_in, cons
     __shared__ double wsum[NT / 64];
     __shared__ float sh_scale;
     const int tid = threadIdx.x, nc = n >> 2;
+    {
+        const int64_t row = blockIdx.x, ro = row * n;
+        x_in += ro;
+        if (add != nullptr) add += ro;
+        if (x_out != nullptr) x_out += ro;
+        if (h != nullptr) h += ro;
+        if (xq != nullptr) xq += row * (n / 32) * kQ80Bytes;
+        if (xk != nullptr) xk += row * (n / 256) * kQ8KBytes;
+    }
     const float4* x4 = reinterpret_cast<const float4*>(x_in);
     const float4* a4 = reinterpret_cast<const float4*>(add);
     const float4* w4 = reinterpret_cast<const float4*>(w);
@@ -164,21 +177,60 @@ struct RopeTab {
     float s[kMaxHeadDim / 2];
 };
 
+// K/V cache elements: fp32, or binary16 with the reference's conversions
+// (bpd_kv_cache_write_f16_cpu, bench/bpd_cpu.c:5240, stores f32_to_f16, :4049,
+// RNE with NaN payloads truncated and made nonzero; the block reads the cache
+// back through f16_to_f32, :3928, whose magic-number form keeps a NaN's
+// payload and sets the quiet bit).
+template <typename CT>
+struct Cache;
+template <>
+struct Cache<float> {
+    static __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+    static __device__ __forceinline__ void st(float* p, float v) { *p = v; }
+    static __device__ __forceinline__ float rt(float v) { return v; }  // the value as read back
+};
+__device__ __forceinline__ uint32_t f32_to_f16_ref(float v) {
+    const uint32_t u = __float_as_uint(v);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return ((u >> 16) & 0x8000u) | 0x7C00u | ((u & 0x7FFFFFu) >> 13) | 1u;
+    return __builtin_bit_cast(uint16_t, (_Float16)v);  // v_cvt_f16_f32: RNE, subnormals, overflow to Inf
+}
+__device__ __forceinline__ float f16_to_f32_ref(uint32_t h) {
+    return f16_is_nan(h) ? f16_nan_x86(h) : f16_ieee(h);
+}
+template <>
+struct Cache<uint16_t> {
+    static __device__ __forceinline__ float4 ld4(const uint16_t* p) {
+        const uint2 u = *reinterpret_cast<const uint2*>(p);
+        return make_float4(f16_to_f32_ref(u.x & 0xFFFFu), f16_to_f32_ref(u.x >> 16), f16_to_f32_ref(u.y & 0xFFFFu),
+                           f16_to_f32_ref(u.y >> 16));
+    }
+    static __device__ __forceinline__ void st(uint16_t* p, float v) { *p = (uint16_t)f32_to_f16_ref(v); }
+    static __device__ __forceinline__ float rt(float v) { return f16_to_f32_ref(f32_to_f16_ref(v)); }
+};
+
 struct AttnIn {
     const float *q, *knew, *vnew;  // projections of this token (before bias and RoPE)
     const float *bq, *bk, *bv;     // biases or NULL
-    float *kc, *vc;                // this layer's caches, [max_seq][row]
+    void *kc, *vc;                 // this layer's caches, [max_seq][row] of the cache type
     int group, row, D, pos;
     float scale;
+    int rot;                       // pairs 0..rot-1 of a head rotate, the rest pass through
 };
 
 // Bias + RoPE of query head `head` into qs (unless NULL) and, with `with_kv`,
-// of the new k row into ks and the new v row into vs (all LDS).
+// of the new k row into ks and the new v row into vs (all LDS), as the cache
+// will give them back.  With `write`, the thread that computes an element of
+// the new k or v row also stores it to cache row pos.
+template <typename CT>
 __device__ __forceinline__ void rope_rows(const AttnIn& a, const RopeTab& tab, int head, int kvh, float* qs,
-                                          float* ks, float* vs, bool with_kv) {
+                                          float* ks, float* vs, bool with_kv, bool write) {
     const int64_t qo = (int64_t)head * a.D, ko = (int64_t)kvh * a.D;
+    CT* kc = static_cast<CT*>(a.kc) + (int64_t)a.pos * a.row + ko;
+    CT* vc = static_cast<CT*>(a.vc) + (int64_t)a.pos * a.row + ko;
     for (int p = threadIdx.x; p < a.D / 2; p += blockDim.x) {
         const int i = 2 * p;
+        const bool rot = p < a.rot;
         const float c = tab.c[p], sn = tab.s[p];
         if (qs != nullptr) {
             float x0 = a.q[qo + i], x1 = a.q[qo + i + 1];
@@ -186,8 +238,8 @@ __device__ __forceinline__ void rope_rows(const AttnIn& a, const RopeTab& tab, i
                 x0 = x0 + a.bq[qo + i];
                 x1 = x1 + a.bq[qo + i + 1];
             }
-            qs[i] = x0 * c - x1 * sn;
-            qs[i + 1] = x0 * sn + x1 * c;
+            qs[i] = rot ? x0 * c - x1 * sn : x0;
+            qs[i + 1] = rot ? x0 * sn + x1 * c : x1;
         }
         if (with_kv) {
             float k0 = a.knew[ko + i], k1 = a.knew[ko + i + 1];
@@ -195,26 +247,22 @@ __device__ __forceinline__ void rope_rows(const AttnIn& a, const RopeTab& tab, i
                 k0 = k0 + a.bk[ko + i];
                 k1 = k1 + a.bk[ko + i + 1];
             }
-            ks[i] = k0 * c - k1 * sn;
-            ks[i + 1] = k0 * sn + k1 * c;
+            const float y0 = rot ? k0 * c - k1 * sn : k0, y1 = rot ? k0 * sn + k1 * c : k1;
+            ks[i] = Cache<CT>::rt(y0);
+            ks[i + 1] = Cache<CT>::rt(y1);
+            if (write) {
+                Cache<CT>::st(kc + i, y0);
+                Cache<CT>::st(kc + i + 1, y1);
+            }
         }
     }
     if (with_kv)
         for (int d = threadIdx.x; d < a.D; d += blockDim.x) {
             float vv = a.vnew[ko + d];
             if (a.bv != nullptr) vv = vv + a.bv[ko + d];
-            vs[d] = vv;
+            vs[d] = Cache<CT>::rt(vv);
+            if (write) Cache<CT>::st(vc + d, vv);
         }
-}
-
-// Cache row pos of the new k and v, written by the first query head of the group.
-__device__ __forceinline__ void write_new_row(const AttnIn& a, int head, int kvh, const float* ks, const float* vs) {
-    if (head % a.group != 0) return;
-    const int64_t o = (int64_t)a.pos * a.row + (int64_t)kvh * a.D;
-    for (int d = threadIdx.x; d < a.D; d += blockDim.x) {
-        a.kc[o + d] = ks[d];
-        a.vc[o + d] = vs[d];
-    }
 }
 
 // Sequential dot products of q with one k row: s = s + q_d * k_d, d ascending.
@@ -305,7 +353,7 @@ __host__ __device__ constexpr int pad32(int n) { return (n + 31) & ~31; }
 // ----------------------------------------------------------------------------
 constexpr int kSmallCtx = 64;
 
-template <int DT>
+template <int DT, typename CT>
 __global__ __launch_bounds__(256) void k_attn_small(AttnIn a, RopeTab tab, float* __restrict__ out,
                                                     uint8_t* __restrict__ xq) {
     constexpr int NT = 256, D4 = DT / 4, VU = (kSmallCtx * D4 + NT - 1) / NT;
@@ -316,23 +364,26 @@ __global__ __launch_bounds__(256) void k_attn_small(AttnIn a, RopeTab tab, float
     __shared__ float sh_inv;
     const int tid = threadIdx.x, head = blockIdx.x, kvh = head / a.group, pos = a.pos, n = pos + 1;
     const int64_t ko = (int64_t)kvh * DT;
+    const CT* kc = static_cast<const CT*>(a.kc);
+    const CT* vc = static_cast<const CT*>(a.vc);
     float4 kr[D4];
     if (tid < pos) {
-        const float4* p = reinterpret_cast<const float4*>(a.kc + (int64_t)tid * a.row + ko);
+        const CT* p = kc + (int64_t)tid * a.row + ko;
 #pragma unroll
-        for (int i = 0; i < D4; i++) kr[i] = p[i];
+        for (int i = 0; i < D4; i++) kr[i] = Cache<CT>::ld4(p + 4 * i);
     }
 #pragma unroll
     for (int u = 0; u < VU; u++) {
         const int f = tid + u * NT, r = f / D4;
-        if (r < pos) V4[f] = *reinterpret_cast<const float4*>(a.vc + (int64_t)r * a.row + ko + 4 * (f % D4));
+        if (r < pos) V4[f] = Cache<CT>::ld4(vc + (int64_t)r * a.row + ko + 4 * (f % D4));
     }
     float* qs = reinterpret_cast<float*>(qs4);
     float* ks = reinterpret_cast<float*>(ks4);
     float* vs = reinterpret_cast<float*>(vs4);
-    rope_rows(a, tab, head, kvh, qs, ks, vs, true);
+    // the first query head of each group writes cache row pos; every head takes
+    // row pos from its own LDS copy, so no workgroup reads a row another writes
+    rope_rows<CT>(a, tab, head, kvh, qs, ks, vs, true, head % a.group == 0);
     __syncthreads();
-    write_new_row(a, head, kvh, ks, vs);
     float m = -1e38f;
     if (tid < n) {
         const float sc = tid < pos ? dot_regs<D4>(qs4, kr) : dot_ptr(qs4, ks4, D4);
@@ -377,7 +428,7 @@ constexpr int kMaxGroup = 8;  // waves per workgroup; larger groups loop over th
 
 __host__ __device__ constexpr int score_pitch(int D) { return D + 4; }  // floats: rows 4 banks apart
 
-template <int DT>
+template <int DT, typename CT>
 __global__ __launch_bounds__(64 * kMaxGroup) void k_attn_scores(AttnIn a, RopeTab tab, float* __restrict__ sc, int ld) {
     extern __shared__ float4 sm4[];
     const int D = DT > 0 ? DT : a.D, D4 = D / 4, P4 = score_pitch(D) / 4, G = a.group;
@@ -392,9 +443,10 @@ __global__ __launch_bounds__(64 * kMaxGroup) void k_attn_scores(AttnIn a, RopeTa
     const int64_t ko = (int64_t)kvh * D;
     // k rows j0 .. min(j0+63, pos-1): float4 i of row r at kt[r*P4 + i]
     const int rows = min(kScoreRows, pos - j0);
+    const CT* kc = static_cast<const CT*>(a.kc);
     for (int f = threadIdx.x; f < rows * D4; f += blockDim.x) {
         const int r = f / D4, i = f % D4;
-        kt[r * P4 + i] = *reinterpret_cast<const float4*>(a.kc + (int64_t)(j0 + r) * a.row + ko + 4 * i);
+        kt[r * P4 + i] = Cache<CT>::ld4(kc + (int64_t)(j0 + r) * a.row + ko + 4 * i);
     }
     // bias + RoPE of the group's q heads in one pass (their loads in flight together),
     // then of the new k and v rows in the block holding row pos
@@ -409,20 +461,15 @@ __global__ __launch_bounds__(64 * kMaxGroup) void k_attn_scores(AttnIn a, RopeTa
             x1 = x1 + a.bq[qo + 1];
         }
         const float c = tab.c[pr], sn = tab.s[pr];
-        qs[h * D + i] = x0 * c - x1 * sn;
-        qs[h * D + i + 1] = x0 * sn + x1 * c;
+        const bool rot = pr < a.rot;
+        qs[h * D + i] = rot ? x0 * c - x1 * sn : x0;
+        qs[h * D + i + 1] = rot ? x0 * sn + x1 * c : x1;
     }
-    if (last) rope_rows(a, tab, kvh * G, kvh, nullptr, reinterpret_cast<float*>(ks4), reinterpret_cast<float*>(vs4), true);
+    // the block holding row pos also writes the new k and v rows to the caches
+    if (last)
+        rope_rows<CT>(a, tab, kvh * G, kvh, nullptr, reinterpret_cast<float*>(ks4), reinterpret_cast<float*>(vs4),
+                      true, true);
     __syncthreads();
-    if (last) {
-        const int64_t o = (int64_t)pos * a.row + ko;
-        const float* ks = reinterpret_cast<const float*>(ks4);
-        const float* vs = reinterpret_cast<const float*>(vs4);
-        for (int d = threadIdx.x; d < D; d += blockDim.x) {
-            a.kc[o + d] = ks[d];
-            a.vc[o + d] = vs[d];
-        }
-    }
     const int j = j0 + lane;
     if (j > pos) return;
     const float4* kr = j == pos ? ks4 : kt + lane * P4;
@@ -468,8 +515,9 @@ static_assert(kMaxCtx % 32 == 0 && 2 * 32 * PvShape<64>::LD * 4 + kMaxCtx * 4 + 
 static_assert(kPvBigMax % 32 == 0 && 2 * 32 * PvShape<128>::LD * 4 + kPvBigMax * 4 + 64 <= 160 * 1024,
               "k_attn_pv<128> LDS");
 
+template <typename CT>
 struct PvPipe {
-    const float* vbase;  // V column d0 of the head's kv row 0
+    const CT* vbase;     // V column d0 of the head's kv row 0
     int row, n, nch, tid;  // tid: producer number, or the chain lane
     const float* e;      // exps in LDS
     float inv;
@@ -478,10 +526,10 @@ struct PvPipe {
 // Load of chunk c's share of producer tid: float4 number f = tid + k*256 is
 // row c*ROWS + f/8, columns d0 + 4(f%8)..+3; rows past n repeat row n-1 (never
 // used, so every load stays in the cache rows already written).
-template <int ROWS>
-__device__ __forceinline__ float4 pv_load(const PvPipe& p, int c, int k) {
+template <int ROWS, typename CT>
+__device__ __forceinline__ float4 pv_load(const PvPipe<CT>& p, int c, int k) {
     const int f = p.tid + k * kPvProd, r = min(c * ROWS + f / 8, p.n - 1);
-    return *reinterpret_cast<const float4*>(p.vbase + (int64_t)r * p.row + 4 * (f % 8));
+    return Cache<CT>::ld4(p.vbase + (int64_t)r * p.row + 4 * (f % 8));
 }
 
 // Step c = c0 + U (pf slot U holds chunk c; U is a template argument so that pf
@@ -490,8 +538,8 @@ __device__ __forceinline__ float4 pv_load(const PvPipe& p, int c, int k) {
 // the chunk's ROWS products in row order.  Slot c&1 is written again at step
 // c+2, after the barrier of step c+1, which the chain reaches only once it has
 // added chunk c.
-template <int U, int ROWS>
-__device__ __forceinline__ void pv_chunk(const PvPipe& p, bool prod, bool chain,
+template <int U, int ROWS, typename CT>
+__device__ __forceinline__ void pv_chunk(const PvPipe<CT>& p, bool prod, bool chain,
                                          float4 (&pf)[PvShape<ROWS>::AHEAD * PvShape<ROWS>::PER], float* ring,
                                          int c0, float& acc) {
     constexpr int PER = PvShape<ROWS>::PER, LD = PvShape<ROWS>::LD;
@@ -516,7 +564,7 @@ __device__ __forceinline__ void pv_chunk(const PvPipe& p, bool prod, bool chain,
                 dst[2 * LD] = -0.0f;
                 dst[3 * LD] = -0.0f;
             }
-            pf[U * PER + k] = pv_load<ROWS>(p, c + PvShape<ROWS>::AHEAD, k);
+            pf[U * PER + k] = pv_load<ROWS, CT>(p, c + PvShape<ROWS>::AHEAD, k);
         }
     }
     __syncthreads();
@@ -535,7 +583,7 @@ __device__ __forceinline__ void pv_chunk(const PvPipe& p, bool prod, bool chain,
     }
 }
 
-template <int ROWS>
+template <int ROWS, typename CT>
 __global__ __launch_bounds__(kPvThreads) void k_attn_pv(AttnIn a, const float* __restrict__ sc, int ld,
                                                         float* __restrict__ out, uint8_t* __restrict__ xq) {
     constexpr int NT = kPvThreads, PER = PvShape<ROWS>::PER, AHEAD = PvShape<ROWS>::AHEAD;
@@ -546,7 +594,13 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(AttnIn a, const float* _
     __shared__ float red[NT / 64];
     __shared__ float sh_inv;
     const int H = a.row / a.D * a.group, head = blockIdx.x % H, d0 = 32 * (blockIdx.x / H);
-    const int tid = threadIdx.x, kvh = head / a.group, n = a.pos + 1, nch = (n + ROWS - 1) / ROWS;
+    // query token blockIdx.y of a batch: its position is a.pos + blockIdx.y, its
+    // scores and outputs follow the previous token's
+    const int tq = blockIdx.y;
+    sc += (int64_t)tq * H * ld;
+    out += (int64_t)tq * H * a.D;
+    if (xq != nullptr) xq += (int64_t)tq * (H * a.D / 32) * kQ80Bytes;
+    const int tid = threadIdx.x, kvh = head / a.group, n = a.pos + tq + 1, nch = (n + ROWS - 1) / ROWS;
     const bool prod = tid >= 64, chain = tid < 32;
     // the scores first, 8 loads in flight (loads complete in order, so anything
     // issued before them would be waited for too), then the first V chunks,
@@ -566,13 +620,14 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(AttnIn a, const float* _
             }
         }
     }
-    PvPipe pp{a.vc + (int64_t)kvh * a.D + d0, a.row, n, nch, prod ? tid - 64 : tid, e, 0.0f};
+    PvPipe<CT> pp{static_cast<const CT*>(a.vc) + (int64_t)kvh * a.D + d0, a.row, n, nch, prod ? tid - 64 : tid, e,
+                  0.0f};
     float4 pf[AHEAD * PER];
     if (prod) {
 #pragma unroll
         for (int c = 0; c < AHEAD; c++)
 #pragma unroll
-            for (int k = 0; k < PER; k++) pf[c * PER + k] = pv_load<ROWS>(pp, c, k);
+            for (int k = 0; k < PER; k++) pf[c * PER + k] = pv_load<ROWS, CT>(pp, c, k);
     }
     const float mx = block_max<NT>(m, red);
     for (int j = tid; j < pad32(n); j += NT) e[j] = j < n ? expf_libm(e[j] - mx) : -0.0f;
@@ -585,15 +640,15 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(AttnIn a, const float* _
     pp.inv = sh_inv;
     float acc = 0.0f;
     for (int c0 = 0; c0 < nch; c0 += AHEAD) {
-        pv_chunk<0, ROWS>(pp, prod, chain, pf, ring, c0, acc);
-        pv_chunk<1, ROWS>(pp, prod, chain, pf, ring, c0, acc);
-        pv_chunk<2, ROWS>(pp, prod, chain, pf, ring, c0, acc);
-        pv_chunk<3, ROWS>(pp, prod, chain, pf, ring, c0, acc);
+        pv_chunk<0, ROWS, CT>(pp, prod, chain, pf, ring, c0, acc);
+        pv_chunk<1, ROWS, CT>(pp, prod, chain, pf, ring, c0, acc);
+        pv_chunk<2, ROWS, CT>(pp, prod, chain, pf, ring, c0, acc);
+        pv_chunk<3, ROWS, CT>(pp, prod, chain, pf, ring, c0, acc);
         if constexpr (AHEAD == 8) {
-            pv_chunk<4, ROWS>(pp, prod, chain, pf, ring, c0, acc);
-            pv_chunk<5, ROWS>(pp, prod, chain, pf, ring, c0, acc);
-            pv_chunk<6, ROWS>(pp, prod, chain, pf, ring, c0, acc);
-            pv_chunk<7, ROWS>(pp, prod, chain, pf, ring, c0, acc);
+            pv_chunk<4, ROWS, CT>(pp, prod, chain, pf, ring, c0, acc);
+            pv_chunk<5, ROWS, CT>(pp, prod, chain, pf, ring, c0, acc);
+            pv_chunk<6, ROWS, CT>(pp, prod, chain, pf, ring, c0, acc);
+            pv_chunk<7, ROWS, CT>(pp, prod, chain, pf, ring, c0, acc);
         }
     }
     if (chain) {
@@ -638,11 +693,18 @@ __device__ __forceinline__ void argmax_take(float v, int i, float& best, int& id
 // Each thread scans float4 chunks t, t + NT, ... (8 loads in flight), then the
 // n % 4 tail, so it meets its indices in increasing order and keeps the first
 // of equal values; lanes and waves then combine by (value, lower index).
+// Workgroup b takes row b of [rows][n] and writes out[b] (int32) or, with out
+// NULL, out64[b] (the reference's long, bpd_argmax_dim_cpu with outer = rows).
+// Rows after the first are read as float4 only when n % 4 == 0 (16-byte
+// aligned); otherwise element by element.
 template <int NT>
-__global__ __launch_bounds__(NT) void k_argmax(const float* __restrict__ x, int n, int32_t* __restrict__ out) {
+__global__ __launch_bounds__(NT) void k_argmax(const float* __restrict__ x, int n, int32_t* __restrict__ out,
+                                               int64_t* __restrict__ out64) {
     __shared__ float bv[NT / 64];
     __shared__ int bi[NT / 64];
-    const int tid = threadIdx.x, nc = n >> 2;
+    x += (int64_t)blockIdx.x * n;
+    const bool vec = blockIdx.x == 0 || (n & 3) == 0;
+    const int tid = threadIdx.x, nc = vec ? n >> 2 : 0;
     const float4* x4 = reinterpret_cast<const float4*>(x);
     float best = 0.0f;
     int idx = INT_MAX;  // no candidate yet
@@ -664,7 +726,7 @@ __global__ __launch_bounds__(NT) void k_argmax(const float* __restrict__ x, int 
             }
         }
     }
-    if (tid < (n & 3)) argmax_take(x[4 * nc + tid], 4 * nc + tid, best, idx);
+    for (int i = 4 * nc + tid; i < n; i += NT) argmax_take(x[i], i, best, idx);
 #pragma unroll
     for (int mask = 32; mask >= 1; mask >>= 1) {
         const float ob = xor_f(best, mask);
@@ -686,7 +748,11 @@ __global__ __launch_bounds__(NT) void k_argmax(const float* __restrict__ x, int 
                 idx = bi[w];
             }
         const float x0 = x[0];
-        out[0] = (!(x0 == x0) || idx == INT_MAX) ? 0 : idx;
+        const int r = (!(x0 == x0) || idx == INT_MAX) ? 0 : idx;
+        if (out != nullptr)
+            out[blockIdx.x] = r;
+        else
+            out64[blockIdx.x] = r;
     }
 }
 
@@ -714,27 +780,126 @@ __global__ __launch_bounds__(256) void k_expf(const float* __restrict__ x, float
     if (i < n) y[i] = expf_libm(x[i]);
 }
 
+// ----------------------------------------------------------------------------
+// Several tokens through the block (bpd_llama_block_cpu with n_tokens > 1): the
+// reference ropes q and k of every token (bpd_rope_norm_freqs_cpu,
+// bench/bpd_cpu.c:5146-5184) and writes every k and v row to the caches
+// (:5204-5260) before attention reads them, so the batch takes three kernels:
+// k_rope_write, k_mt_scores, then k_attn_pv with one grid row per token.
+// ----------------------------------------------------------------------------
+// The rotation of token t, pair j: cos and sin of pos_ids[t] * theta_scale^j /
+// rope_freqs[j] (host libm), pairs j < rot.
+struct RopeCS {
+    float c, s;
+};
+
+// Workgroup t: q of token t (H heads of D, in place), k (roped) and v of its
+// kv heads to cache row pos[t].
+template <typename CT>
+__global__ __launch_bounds__(256) void k_rope_write(float* __restrict__ q, const float* __restrict__ k,
+                                                    const float* __restrict__ v, CT* __restrict__ kc,
+                                                    CT* __restrict__ vc, const int32_t* __restrict__ pos,
+                                                    const RopeCS* __restrict__ tab, int H, int HKV, int D, int rot) {
+    const int t = blockIdx.x, half = D / 2, row = HKV * D;
+    const RopeCS* tt = tab + (int64_t)t * (kMaxHeadDim / 2);
+    float* qt = q + (int64_t)t * H * D;
+    for (int pp = threadIdx.x; pp < H * half; pp += blockDim.x) {
+        const int p = pp % half, i = 2 * (pp / half) * half + 2 * p;
+        if (p >= rot) continue;
+        const float x0 = qt[i], x1 = qt[i + 1], c = tt[p].c, sn = tt[p].s;
+        qt[i] = x0 * c - x1 * sn;
+        qt[i + 1] = x0 * sn + x1 * c;
+    }
+    const int64_t ro = (int64_t)t * row, co = (int64_t)pos[t] * row;
+    for (int pp = threadIdx.x; pp < HKV * half; pp += blockDim.x) {
+        const int p = pp % half, i = 2 * pp;
+        float y0 = k[ro + i], y1 = k[ro + i + 1];
+        if (p < rot) {
+            const float x0 = y0, x1 = y1, c = tt[p].c, sn = tt[p].s;
+            y0 = x0 * c - x1 * sn;
+            y1 = x0 * sn + x1 * c;
+        }
+        Cache<CT>::st(kc + co + i, y0);
+        Cache<CT>::st(kc + co + i + 1, y1);
+    }
+    for (int d = threadIdx.x; d < row; d += blockDim.x) Cache<CT>::st(vc + co + d, v[ro + d]);
+}
+
+// Scores of the batch, grid (row blocks, kv heads, tokens): workgroup (b, kvh,
+// t) loads cache k rows 64b..64b+63 (those <= kv_pos + t, the token's causal
+// limit) once into LDS, and lane j of wave h computes row j's score for query
+// head kvh * G + h of token t: s = sum_d q_d k_d sequentially over d, times
+// scale, into sc[t][head][j].
+template <typename CT>
+__global__ __launch_bounds__(64 * kMaxGroup) void k_mt_scores(const float* __restrict__ q, const CT* __restrict__ kc,
+                                                              float* __restrict__ sc, int ld, int kv_pos, int H,
+                                                              int HKV, int D, float scale) {
+    extern __shared__ float4 sm4[];
+    const int G = H / HKV, D4 = D / 4, P4 = score_pitch(D) / 4, row = HKV * D;
+    const int j0 = blockIdx.x * kScoreRows, kvh = blockIdx.y, t = blockIdx.z, qpos = kv_pos + t;
+    if (j0 > qpos) return;  // uniform over the workgroup
+    const int nw = blockDim.x >> 6, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    float4* kt = sm4;                    // [64][P4]
+    float4* qs4 = kt + kScoreRows * P4;  // [G][D4]
+    const int rows = min(kScoreRows, qpos + 1 - j0);
+    const int64_t ko = (int64_t)kvh * D;
+    for (int f = threadIdx.x; f < rows * D4; f += blockDim.x) {
+        const int r = f / D4, i = f % D4;
+        kt[r * P4 + i] = Cache<CT>::ld4(kc + (int64_t)(j0 + r) * row + ko + 4 * i);
+    }
+    const float4* qt = reinterpret_cast<const float4*>(q + ((int64_t)t * H + kvh * G) * D);
+    for (int f = threadIdx.x; f < G * D4; f += blockDim.x) qs4[f] = qt[f];
+    __syncthreads();
+    if (lane >= rows) return;
+    const float4* kr = kt + lane * P4;
+    for (int h = wave; h < G; h += nw) {
+        const float4* qh = qs4 + h * D4;
+        float s = 0.0f;
+#pragma unroll 8
+        for (int i = 0; i < D4; i++) s = dot_step(s, qh[i], kr[i]);
+        sc[((int64_t)t * H + kvh * G + h) * ld + j0 + lane] = s * scale;
+    }
+}
+
+// x = x + y over n floats (bpd_add_f32_cpu, bench/bpd_cpu.c:5466), n % 4 == 0.
+__global__ __launch_bounds__(256) void k_add(float* __restrict__ x, const float* __restrict__ y, int64_t n4) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n4) return;
+    float4 a = reinterpret_cast<float4*>(x)[i];
+    const float4 b = reinterpret_cast<const float4*>(y)[i];
+    a = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+    reinterpret_cast<float4*>(x)[i] = a;
+}
+
 // ---------------------------------------------------------------------------- host side
 
 namespace {
+
+template <typename CT>
+hipError_t lds_limits_for() {
+    hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_pv<64, CT>),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, kMaxCtx * 4);
+    if (err == hipSuccess)
+        err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_pv<128, CT>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, kPvBigMax * 4);
+    // the scores kernels' LDS: the k tile plus q of up to n_embd / head_dim heads
+    for (const void* f : {reinterpret_cast<const void*>(&k_attn_scores<128, CT>),
+                          reinterpret_cast<const void*>(&k_attn_scores<64, CT>),
+                          reinterpret_cast<const void*>(&k_attn_scores<0, CT>),
+                          reinterpret_cast<const void*>(&k_mt_scores<CT>)})
+        if (err == hipSuccess)
+            err = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      (kScoreRows * score_pitch(kMaxHeadDim) + kMaxEmbd + 2 * kMaxHeadDim) * 4);
+    return err;
+}
 
 // The kernels that take more than 64 KB of dynamic LDS say so once per process.
 bool lds_limits_set(const char* fn) {
     static std::once_flag once;
     static hipError_t err = hipSuccess;
     std::call_once(once, [] {
-        err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_pv<64>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, kMaxCtx * 4);
-        if (err == hipSuccess)
-            err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_pv<128>),
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, kPvBigMax * 4);
-        // the scores kernel's LDS: the k tile plus q of up to n_embd / head_dim heads
-        for (const void* f : {reinterpret_cast<const void*>(&k_attn_scores<128>),
-                              reinterpret_cast<const void*>(&k_attn_scores<64>),
-                              reinterpret_cast<const void*>(&k_attn_scores<0>)})
-            if (err == hipSuccess)
-                err = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                          (kScoreRows * score_pitch(kMaxHeadDim) + kMaxEmbd + 2 * kMaxHeadDim) * 4);
+        err = lds_limits_for<float>();
+        if (err == hipSuccess) err = lds_limits_for<uint16_t>();
         if (err == hipSuccess)
             err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_residual_rmsnorm<kNormThreads, kNormChunks>),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, kMaxEmbd * 4);
@@ -743,24 +908,37 @@ bool lds_limits_set(const char* fn) {
 }
 
 void launch_norm(const float* x_in, const float* add, float* x_out, const float* w, float* h, uint8_t* xq, int n,
-                 float eps, hipStream_t s, uint8_t* xk = nullptr) {
-    hipLaunchKernelGGL((k_residual_rmsnorm<kNormThreads, kNormChunks>), dim3(1), dim3(kNormThreads), (size_t)n * 4, s,
-                       x_in, add, x_out, w, h, xq, xk, n, eps);
+                 float eps, hipStream_t s, uint8_t* xk = nullptr, int rows = 1) {
+    hipLaunchKernelGGL((k_residual_rmsnorm<kNormThreads, kNormChunks>), dim3(rows), dim3(kNormThreads), (size_t)n * 4,
+                       s, x_in, add, x_out, w, h, xq, xk, n, eps);
 }
 
-// Rotation table for `pos`: pair j turns by pos * theta_scale^j, the angle
-// accumulated in fp32 exactly as the reference's loop does
-// (theta_scale = powf(base, -2/n_dims); theta *= theta_scale after each pair).
-// sincosf through a pointer, so the compiler neither folds nor reorders it.
-void rope_table(RopeTab& t, int pos, int head_dim, float base) {
+// Rotation table for `pos`: pair j < n_dims/2 turns by pos * theta_scale^j /
+// freqs[j] (freqs NULL: no factor), the angle accumulated in fp32 exactly as
+// the reference's loop does (bpd_rope_norm_freqs_cpu, bench/bpd_cpu.c:5158-5171:
+// theta_scale = powf(base, -2/n_dims); theta_eff = theta / ff; theta *=
+// theta_scale after each pair).  sincosf through a pointer, so the compiler
+// neither folds nor reorders it.
+template <typename F>
+void rope_angles(int pos, int n_dims, float base, const float* freqs, F&& put) {
     static void (*volatile sc)(float, float*, float*) = sincosf;
     static float (*volatile pw)(float, float) = powf;
-    const float theta_scale = pw(base, -2.0f / (float)head_dim);
+    const float theta_scale = pw(base, -2.0f / (float)n_dims);
     float theta = (float)pos;
-    for (int j = 0; j < head_dim / 2; j++) {
-        sc(theta, &t.s[j], &t.c[j]);
+    for (int j = 0; j < n_dims / 2; j++) {
+        const float ff = freqs != nullptr ? freqs[j] : 1.0f;
+        const float theta_eff = theta / ff;
+        float s, c;
+        sc(theta_eff, &s, &c);
+        put(j, c, s);
         theta *= theta_scale;
     }
+}
+void rope_table(RopeTab& t, int pos, int n_dims, float base, const float* freqs) {
+    rope_angles(pos, n_dims, base, freqs, [&](int j, float c, float s) {
+        t.c[j] = c;
+        t.s[j] = s;
+    });
 }
 
 struct V {
@@ -797,17 +975,50 @@ struct Geometry {
     int E, H, HKV, D, F, L;
 };
 
-bool validate(V& v, int fmt, const LayerWeights* layers, const ModelConfig* cfg, const WorkBuffers* buf,
+// Options of the extended step (bpd_llama_step_ext_gpu); the plain entry
+// points use one format everywhere, rope_dim = head_dim, no frequency factors
+// and fp32 caches.
+struct StepOpts {
+    const int* layer_formats;  // host [n_layers][7] or NULL
+    int base_format, lm_format;
+    int rope_dim;
+    const float* rope_freqs;
+    bool f16;
+    int fmt(int layer, int m) const { return layer_formats ? layer_formats[layer * 7 + m] : base_format; }
+};
+
+bool is_q4k(int f) { return f == BPDQ_W_Q4K || f == BPDQ_W_Q4K_GGUF; }
+bool is_q6k(int f) { return f == BPDQ_W_Q6K || f == BPDQ_W_Q6K_GGUF; }
+bool known_format(int f) { return f == BPDQ_W_Q8_PAD64 || is_q4k(f) || is_q6k(f); }
+int format_order(int f) { return f == BPDQ_W_Q4K_GGUF || f == BPDQ_W_Q6K_GGUF ? 1 : 0; }
+uintptr_t format_align(int f) { return f == BPDQ_W_Q8_PAD64 ? 4 : is_q6k(f) ? 2 : 16; }
+
+bool validate(V& v, const StepOpts& o, const LayerWeights* layers, const ModelConfig* cfg, const WorkBuffers* buf,
               const KVCache* kv, int pos, const void* emb, const void* out_norm, const void* lm_w,
               const void* lm_f32, int lm_K, int lm_N, Geometry& g) {
-    v.need(fmt == BPDQ_W_Q8_PAD64 || fmt == BPDQ_W_Q4K || fmt == BPDQ_W_Q4K_GGUF, BPDQ_ERR_SHAPE,
-           "unknown weight_format");
     v.ptr(cfg, 1, "cfg");
     v.ptr(buf, 1, "buf");
     if (!v.ok) return false;
     g = Geometry{cfg->n_embd, cfg->n_head, cfg->n_head_kv, cfg->head_dim, cfg->ff_dim, cfg->n_layers};
-    const int blk = fmt == BPDQ_W_Q8_PAD64 ? 32 : 256;
     v.need(g.L >= 0, BPDQ_ERR_SHAPE, "n_layers is negative");
+    if (!v.ok) return false;
+    // every matrix in padded Q8 (Q8_0 activations), or every one a K-quant (Q8_K activations)
+    const bool q8 = o.base_format == BPDQ_W_Q8_PAD64;
+    v.need(known_format(o.base_format), BPDQ_ERR_SHAPE, "unknown weight_format");
+    for (int l = 0; l < g.L && v.ok; l++)
+        for (int m = 0; m < 7 && v.ok; m++) {
+            const int f = o.fmt(l, m);
+            v.need(known_format(f), BPDQ_ERR_SHAPE, "unknown format in layer_formats");
+            v.need((f == BPDQ_W_Q8_PAD64) == q8, BPDQ_ERR_SHAPE,
+                   "the padded Q8 layout cannot be mixed with the K-quant formats");
+        }
+    if (lm_w != nullptr) {
+        v.need(known_format(o.lm_format), BPDQ_ERR_SHAPE, "unknown lm_format");
+        v.need((o.lm_format == BPDQ_W_Q8_PAD64) == q8, BPDQ_ERR_SHAPE,
+               "the padded Q8 layout cannot be mixed with the K-quant formats");
+    }
+    if (!v.ok) return false;
+    const int blk = q8 ? 32 : 256;
     v.need(g.H > 0 && g.HKV > 0 && g.H % g.HKV == 0, BPDQ_ERR_SHAPE,
            "n_head and n_head_kv must be positive, n_head a multiple of n_head_kv");
     v.need(g.D > 0 && g.D % 32 == 0 && g.D <= kMaxHeadDim, BPDQ_ERR_SHAPE,
@@ -818,14 +1029,15 @@ bool validate(V& v, int fmt, const LayerWeights* layers, const ModelConfig* cfg,
     v.need(g.F > 0 && g.F % blk == 0, BPDQ_ERR_SHAPE, "ff_dim must be a positive multiple of the weight block length");
     v.need(cfg->max_seq > 0 && cfg->max_seq <= kMaxCtx, BPDQ_ERR_SHAPE, "max_seq must be in 1..32768");
     v.need(pos >= 0 && pos < cfg->max_seq, BPDQ_ERR_SHAPE, "position must be in 0..max_seq-1");
+    v.need(o.rope_dim >= 2 && o.rope_dim <= g.D && o.rope_dim % 2 == 0, BPDQ_ERR_SHAPE,
+           "rope_dim must be even, in 2..head_dim");
     v.need(lm_K == g.E, BPDQ_ERR_SHAPE, "lm_K must equal n_embd");
     v.need(lm_N > 0, BPDQ_ERR_SHAPE, "lm_N must be positive");
     if (!v.ok) return false;
-    const uintptr_t wal = fmt == BPDQ_W_Q8_PAD64 ? 4 : 16;
     v.ptr(emb, 16, "embedding");
     v.ptr(out_norm, 16, "output_norm_w");
     if (lm_w != nullptr)
-        v.ptr(lm_w, wal, "lm_head");
+        v.ptr(lm_w, format_align(o.lm_format), "lm_head");
     else
         v.ptr(lm_f32, 4, "lm_f32 (lm_head is NULL)");
     const void* bufs[11] = {buf->x, buf->h, buf->q, buf->k, buf->v, buf->attn_out,
@@ -853,7 +1065,7 @@ bool validate(V& v, int fmt, const LayerWeights* layers, const ModelConfig* cfg,
         v.dims(w.down_K, g.F, w.down_N, g.E, l, "down");
         const void* mats[7] = {w.q, w.k, w.v, w.o, w.gate, w.up, w.down};
         static const char* mnames[7] = {"q", "k", "v", "o", "gate", "up", "down"};
-        for (int i = 0; i < 7; i++) v.ptr(mats[i], wal, mnames[i]);
+        for (int i = 0; i < 7; i++) v.ptr(mats[i], format_align(o.fmt(l, i)), mnames[i]);
         v.ptr(w.attn_norm, 16, "attn_norm");
         v.ptr(w.ffn_norm, 16, "ffn_norm");
         if (w.q_bias) v.ptr(w.q_bias, 4, "q_bias");
@@ -865,28 +1077,46 @@ bool validate(V& v, int fmt, const LayerWeights* layers, const ModelConfig* cfg,
     return v.ok;
 }
 
-// One GEMV y[N] = W[N][K] a[K]: padded Q8 reads the Q8_0 bytes aq of a; Q4_K
-// takes fp32 a and quantizes it to Q8_K inside the kernel.
+// The GEMVs y_i[N_i] = W_i[N_i][K] a[K] of matrices that share one activation.
+// Padded Q8 reads the Q8_0 bytes aq of a.  The K-quants read a's Q8_K: xk when
+// the norm wrote it, else Q4_K quantizes inside the kernel (K <= fused_max_k())
+// and Q6_K (or a longer Q4_K) reads q8k, written here once per group.  Q4_K
+// matrices of one element map share a launch.
 struct Gemv {
-    int fmt;
-    uint8_t* q8k;  // Q8_K staging for K beyond the fused kernel
+    uint8_t* q8k;  // Q8_K staging (K-quant formats)
     hipStream_t s;
-    void run(int n, const void* const* w, float* const* y, const int* N, const float* a, const uint8_t* aq,
-             int K) const {
-        if (fmt == BPDQ_W_Q8_PAD64) {
+    void run(int n, const void* const* w, const int* fmt, float* const* y, const int* N, const float* a,
+             const uint8_t* aq, const uint8_t* xk, int K) const {
+        if (fmt[0] == BPDQ_W_Q8_PAD64) {
             for (int i = 0; i < n; i++)
                 launch_q8_pad64_dispatch_T(static_cast<const uint8_t*>(w[i]), aq, y[i], N[i], 1, K, s);
             return;
         }
-        const int order = fmt == BPDQ_W_Q4K_GGUF ? 1 : 0;
-        const uint8_t* wl[4];
-        for (int i = 0; i < n; i++) wl[i] = static_cast<const uint8_t*>(w[i]);
-        if (K <= fused_max_k()) {
-            launch_qmatmul_q4k_fused_multi(wl, y, N, n, a, K, order, s);
-        } else {
+        bool need_q8k = false;
+        for (int i = 0; i < n; i++) need_q8k |= is_q6k(fmt[i]) || (is_q4k(fmt[i]) && K > fused_max_k());
+        if (xk == nullptr && need_q8k) {
             launch_quant_q8k(a, q8k, K, s);
-            launch_qmatmul_q4k_q8k_multi(wl, y, N, n, q8k, K, order, s);
+            xk = q8k;
         }
+        for (int order = 0; order < 2; order++) {
+            const uint8_t* wl[4];
+            float* yl[4];
+            int nl[4], m = 0;
+            for (int i = 0; i < n; i++)
+                if (is_q4k(fmt[i]) && format_order(fmt[i]) == order) {
+                    wl[m] = static_cast<const uint8_t*>(w[i]);
+                    yl[m] = y[i];
+                    nl[m++] = N[i];
+                }
+            if (m == 0) continue;
+            if (xk != nullptr)
+                launch_qmatmul_q4k_q8k_multi(wl, yl, nl, m, xk, K, order, s);
+            else
+                launch_qmatmul_q4k_fused_multi(wl, yl, nl, m, a, K, order, s);
+        }
+        for (int i = 0; i < n; i++)
+            if (is_q6k(fmt[i]))
+                launch_qmatmul_q6k_q8k(static_cast<const uint8_t*>(w[i]), xk, y[i], N[i], K, format_order(fmt[i]), s);
     }
 };
 
@@ -894,6 +1124,7 @@ struct StepCtx {
     Geometry g;
     const ModelConfig* cfg;
     const KVCache* kv;
+    const StepOpts* o;
     int pos;
     hipStream_t s;
     RopeTab tab;
@@ -901,20 +1132,21 @@ struct StepCtx {
     float* scores;      // [n_head][max_seq] scaled scores of the long-context attention
     float attn_scale;   // 1 / sqrtf(head_dim), as the reference computes it
     uint8_t *xq_e, *xq_a, *xq_f;  // Q8_0 activations (padded Q8 weights only, else NULL)
-    uint8_t* xk;  // Q8_K of the normed row (Q4_K weights, n_embd <= 4096, else NULL)
+    uint8_t* xk;  // Q8_K of the normed row (K-quant weights, n_embd <= 4096, else NULL)
 };
 
 // Attention over n_ctx = pos + 1 rows: one kernel while the context is short
 // and head_dim is 32, 64 or 128, else scores and softmax/P.V as two kernels.
+template <typename CT>
 void attention(const StepCtx& c, const AttnIn& ai, int n_ctx) {
     const Geometry& g = c.g;
     if (n_ctx <= kSmallCtx && (g.D == 32 || g.D == 64 || g.D == 128)) {
         if (g.D == 128)
-            hipLaunchKernelGGL(k_attn_small<128>, dim3(g.H), dim3(256), 0, c.s, ai, c.tab, c.att, c.xq_a);
+            hipLaunchKernelGGL((k_attn_small<128, CT>), dim3(g.H), dim3(256), 0, c.s, ai, c.tab, c.att, c.xq_a);
         else if (g.D == 64)
-            hipLaunchKernelGGL(k_attn_small<64>, dim3(g.H), dim3(256), 0, c.s, ai, c.tab, c.att, c.xq_a);
+            hipLaunchKernelGGL((k_attn_small<64, CT>), dim3(g.H), dim3(256), 0, c.s, ai, c.tab, c.att, c.xq_a);
         else
-            hipLaunchKernelGGL(k_attn_small<32>, dim3(g.H), dim3(256), 0, c.s, ai, c.tab, c.att, c.xq_a);
+            hipLaunchKernelGGL((k_attn_small<32, CT>), dim3(g.H), dim3(256), 0, c.s, ai, c.tab, c.att, c.xq_a);
         return;
     }
     const int ld = c.cfg->max_seq, group = g.H / g.HKV;
@@ -922,19 +1154,19 @@ void attention(const StepCtx& c, const AttnIn& ai, int n_ctx) {
     // k tile, q of the group's heads, new k and v rows: <= (64 * 260 + 16384 + 512) * 4 bytes
     const size_t slds = ((size_t)kScoreRows * score_pitch(g.D) + (size_t)(group + 2) * g.D) * 4;
     if (g.D == 128)
-        hipLaunchKernelGGL(k_attn_scores<128>, gs, ts, slds, c.s, ai, c.tab, c.scores, ld);
+        hipLaunchKernelGGL((k_attn_scores<128, CT>), gs, ts, slds, c.s, ai, c.tab, c.scores, ld);
     else if (g.D == 64)
-        hipLaunchKernelGGL(k_attn_scores<64>, gs, ts, slds, c.s, ai, c.tab, c.scores, ld);
+        hipLaunchKernelGGL((k_attn_scores<64, CT>), gs, ts, slds, c.s, ai, c.tab, c.scores, ld);
     else
-        hipLaunchKernelGGL(k_attn_scores<0>, gs, ts, slds, c.s, ai, c.tab, c.scores, ld);
+        hipLaunchKernelGGL((k_attn_scores<0, CT>), gs, ts, slds, c.s, ai, c.tab, c.scores, ld);
     // e holds pad32(n_ctx) <= kMaxCtx floats (kMaxCtx % 32 == 0); with 128-row
     // chunks n_ctx <= kPvBigMax, so the ring and the scores fit in 160 KB
     const dim3 gp(g.H * (g.D / 32));
     const size_t lds = (size_t)pad32(n_ctx) * 4;
     if (n_ctx >= kPvBigMin && n_ctx <= kPvBigMax)
-        hipLaunchKernelGGL(k_attn_pv<128>, gp, dim3(kPvThreads), lds, c.s, ai, c.scores, ld, c.att, c.xq_a);
+        hipLaunchKernelGGL((k_attn_pv<128, CT>), gp, dim3(kPvThreads), lds, c.s, ai, c.scores, ld, c.att, c.xq_a);
     else
-        hipLaunchKernelGGL(k_attn_pv<64>, gp, dim3(kPvThreads), lds, c.s, ai, c.scores, ld, c.att, c.xq_a);
+        hipLaunchKernelGGL((k_attn_pv<64, CT>), gp, dim3(kPvThreads), lds, c.s, ai, c.scores, ld, c.att, c.xq_a);
 }
 
 // The layers.  The residual add is the first step of each RMSNorm kernel; the
@@ -944,78 +1176,81 @@ void attention(const StepCtx& c, const AttnIn& ai, int n_ctx) {
 void run_layers(const StepCtx& c, const Gemv& gemv, const LayerWeights* layers, const float*& xin,
                 const float*& add) {
     const Geometry& g = c.g;
+    const StepOpts& o = *c.o;
     const int row = g.HKV * g.D, n_ctx = c.pos + 1;
     for (int l = 0; l < g.L; l++) {
         const LayerWeights& w = layers[l];
+        int f[7];
+        for (int m = 0; m < 7; m++) f[m] = o.fmt(l, m);
         launch_norm(xin, add, c.x, static_cast<const float*>(w.attn_norm), c.h, c.xq_e, g.E, c.cfg->eps, c.s, c.xk);
         xin = c.x;
         const void* wqkv[3] = {w.q, w.k, w.v};
         float* yqkv[3] = {c.qb, c.kb, c.vb};
         const int nqkv[3] = {w.q_N, w.k_N, w.v_N};
-        if (c.xk != nullptr) {  // the norm wrote h's Q8_K once: the plain GEMV reads it
-            const uint8_t* wl[3] = {static_cast<const uint8_t*>(w.q), static_cast<const uint8_t*>(w.k),
-                                    static_cast<const uint8_t*>(w.v)};
-            launch_qmatmul_q4k_q8k_multi(wl, yqkv, nqkv, 3, c.xk, g.E, gemv.fmt == BPDQ_W_Q4K_GGUF ? 1 : 0, c.s);
-        } else {
-            gemv.run(3, wqkv, yqkv, nqkv, c.h, c.xq_e, g.E);
-        }
+        gemv.run(3, wqkv, f, yqkv, nqkv, c.h, c.xq_e, c.xk, g.E);
         const AttnIn ai{c.qb, c.kb, c.vb,
                         static_cast<const float*>(w.q_bias), static_cast<const float*>(w.k_bias),
-                        static_cast<const float*>(w.v_bias), static_cast<float*>(c.kv->k_cache[l]),
-                        static_cast<float*>(c.kv->v_cache[l]), g.H / g.HKV, row, g.D, c.pos, c.attn_scale};
-        attention(c, ai, n_ctx);
+                        static_cast<const float*>(w.v_bias), c.kv->k_cache[l], c.kv->v_cache[l], g.H / g.HKV, row,
+                        g.D, c.pos, c.attn_scale, o.rope_dim / 2};
+        if (o.f16)
+            attention<uint16_t>(c, ai, n_ctx);
+        else
+            attention<float>(c, ai, n_ctx);
         const void* wo[1] = {w.o};
         float* yo[1] = {c.ffn};
         const int no[1] = {w.o_N};
-        gemv.run(1, wo, yo, no, c.att, c.xq_a, g.H * g.D);
+        gemv.run(1, wo, f + 3, yo, no, c.att, c.xq_a, nullptr, g.H * g.D);
         launch_norm(c.x, c.ffn, c.x, static_cast<const float*>(w.ffn_norm), c.h, c.xq_e, g.E, c.cfg->eps, c.s, c.xk);
-        if (c.xk != nullptr) {
+        // gate/up with SwiGLU in the epilogue (into gate) when both are Q4_K of one map
+        const bool fused = is_q4k(f[4]) && f[4] == f[5];
+        if (fused && c.xk != nullptr) {
             launch_qmatmul_q4k_swiglu_q8k(static_cast<const uint8_t*>(w.gate), static_cast<const uint8_t*>(w.up),
-                                          c.gate, g.F, c.xk, g.E, gemv.fmt == BPDQ_W_Q4K_GGUF ? 1 : 0, c.s);
-        } else if (gemv.fmt == BPDQ_W_Q8_PAD64) {
+                                          c.gate, g.F, c.xk, g.E, format_order(f[4]), c.s);
+        } else if (fused && g.E <= fused_max_k()) {
+            launch_qmatmul_q4k_fused_swiglu(static_cast<const uint8_t*>(w.gate), static_cast<const uint8_t*>(w.up),
+                                            c.gate, g.F, c.h, g.E, format_order(f[4]), c.s);
+        } else {
             const void* wgu[2] = {w.gate, w.up};
             float* ygu[2] = {c.gate, c.up};
             const int ngu[2] = {w.gate_N, w.up_N};
-            gemv.run(2, wgu, ygu, ngu, c.h, c.xq_e, g.E);
+            gemv.run(2, wgu, f + 4, ygu, ngu, c.h, c.xq_e, c.xk, g.E);
             hipLaunchKernelGGL(k_swiglu, dim3((g.F + 255) / 256), dim3(256), 0, c.s, c.gate, c.up, c.xq_f, g.F);
-        } else {  // n_embd <= fused_max_k(): gate/up with SwiGLU in the epilogue, into gate
-            launch_qmatmul_q4k_fused_swiglu(static_cast<const uint8_t*>(w.gate), static_cast<const uint8_t*>(w.up),
-                                            c.gate, g.F, c.h, g.E, gemv.fmt == BPDQ_W_Q4K_GGUF ? 1 : 0, c.s);
         }
         const void* wd[1] = {w.down};
         float* yd[1] = {c.ffn};
         const int nd[1] = {w.down_N};
-        gemv.run(1, wd, yd, nd, c.gate, c.xq_f, g.F);
+        gemv.run(1, wd, f + 6, yd, nd, c.gate, c.xq_f, nullptr, g.F);
         add = c.ffn;
     }
 }
 
-bool enqueue_step(int fmt, const LayerWeights* layers, const ModelConfig* cfg, const WorkBuffers* buf,
+bool enqueue_step(const StepOpts& o, const LayerWeights* layers, const ModelConfig* cfg, const WorkBuffers* buf,
                   const KVCache* kv, int pos, const void* emb, const void* out_norm, const void* lm_w,
                   const void* lm_f32, int lm_K, int lm_N, const char* fn) {
     V v{fn};
     StepCtx c{};
     Geometry& g = c.g;
-    if (!validate(v, fmt, layers, cfg, buf, kv, pos, emb, out_norm, lm_w, lm_f32, lm_K, lm_N, g)) return false;
+    if (!validate(v, o, layers, cfg, buf, kv, pos, emb, out_norm, lm_w, lm_f32, lm_K, lm_N, g)) return false;
     if (!lds_limits_set(fn)) return false;
-    const bool q8 = fmt == BPDQ_W_Q8_PAD64;
+    const bool q8 = o.base_format == BPDQ_W_Q8_PAD64;
     const size_t q8e = (size_t)(g.E / 32) * kQ80Bytes, q8f = (size_t)(g.F / 32) * kQ80Bytes;
     const size_t front = q8 ? (2 * q8e + q8f + 255) & ~(size_t)255 : 0;
     const int kmax = g.F > g.E ? g.F : g.E;
-    const size_t q8k = kmax > fused_max_k() ? (size_t)(kmax / 256) * kQ8KBytes : 0;
-    // with Q4_K weights and n_embd <= 4096 the norms write h's Q8_K once for the
+    const size_t q8k = q8 ? 0 : (size_t)(kmax / 256) * kQ8KBytes;
+    // with K-quant weights and n_embd <= 4096 the norms write h's Q8_K once for the
     // Q/K/V and gate/up GEMVs (measured 1,515 -> 1,500 us/token at cfg3)
     const size_t xk_bytes = !q8 && g.E <= 4096 ? ((size_t)(g.E / 256) * kQ8KBytes + 255) & ~(size_t)255 : 0;
     const size_t q8k_end = ((front + q8k + 255) & ~(size_t)255) + xk_bytes;
     const size_t sc_bytes = (size_t)g.H * cfg->max_seq * 4;
-    // the quantized activations (Q8_0 rows, or Q8_K when a Q4_K GEMV is too long for
-    // the fused kernel) and the attention scores, in the stream's workspace
+    // the quantized activations (Q8_0 rows, or Q8_K staging for the K-quant GEMVs)
+    // and the attention scores, in the stream's workspace
     const WsLease lease = workspace(q8k_end + sc_bytes, abi_stream(), fn);
     uint8_t* ws = static_cast<uint8_t*>(lease.ptr);
     if (ws == nullptr) return false;
-    const Gemv gemv{fmt, ws + front, abi_stream()};
+    const Gemv gemv{ws + front, abi_stream()};
     c.cfg = cfg;
     c.kv = kv;
+    c.o = &o;
     c.pos = pos;
     c.scores = reinterpret_cast<float*>(ws + q8k_end);
     c.attn_scale = 1.0f / sqrtf((float)g.D);
@@ -1033,25 +1268,291 @@ bool enqueue_step(int fmt, const LayerWeights* layers, const ModelConfig* cfg, c
     c.xq_a = q8 ? ws + q8e : nullptr;
     c.xq_f = q8 ? ws + 2 * q8e : nullptr;
     c.xk = xk_bytes ? ws + q8k_end - xk_bytes : nullptr;
-    if (g.L > 0) rope_table(c.tab, pos, g.D, cfg->rope_theta);
+    if (g.L > 0) rope_table(c.tab, pos, o.rope_dim, cfg->rope_theta, o.rope_freqs);
     float* logits = static_cast<float*>(buf->logits);
 
     const float* xin = static_cast<const float*>(emb);
     const float* add = nullptr;
     run_layers(c, gemv, layers, xin, add);
-    launch_norm(xin, add, c.x, static_cast<const float*>(out_norm), c.h, c.xq_e, g.E, cfg->eps, c.s);
+    launch_norm(xin, add, c.x, static_cast<const float*>(out_norm), c.h, c.xq_e, g.E, cfg->eps, c.s, c.xk);
     if (lm_w != nullptr) {
         const void* wl[1] = {lm_w};
+        const int fl[1] = {o.lm_format};
         float* yl[1] = {logits};
         const int nl[1] = {lm_N};
-        gemv.run(1, wl, yl, nl, c.h, c.xq_e, g.E);
+        gemv.run(1, wl, fl, yl, nl, c.h, c.xq_e, c.xk, g.E);
     } else {
         hipLaunchKernelGGL(k_gemv_f32, dim3((lm_N + 3) / 4), dim3(256), 0, c.s, static_cast<const float*>(lm_f32),
                            c.h, logits, lm_N, g.E);
     }
     hipLaunchKernelGGL(k_argmax<1024>, dim3(1), dim3(1024), 0, c.s, logits, lm_N,
-                       static_cast<int32_t*>(buf->argmax_result));
+                       static_cast<int32_t*>(buf->argmax_result), nullptr);
     return abi_hip_ok(hipGetLastError(), fn);
+}
+
+StepOpts plain_opts(int fmt, const ModelConfig* cfg) {
+    return StepOpts{nullptr, fmt, fmt, cfg != nullptr ? cfg->head_dim : 0, nullptr, false};
+}
+
+
+// ---------------------------------------------------------------------------- several tokens
+// bpd_llama_block_cpu / bpd_llama_forward_cpu (bench/bpd_cpu.c:5608-5798) for
+// n_tokens >= 1.  Per layer, as the reference's block: RMSNorm of every row;
+// Q, K, V; RoPE of q and k and the cache writes of every token; attention of
+// query t over cache rows 0..kv_pos+t; O; x += O; RMSNorm; gate, up; SwiGLU;
+// down; x += down.  The Q8_0 products are the llamafile entry's (quantize the
+// rows, then the tile order T of the -mavx build, or order S of the -O2 build
+// on int8 MFMA); every other operation is shared by both builds.
+
+struct BlockGeo {
+    int E, H, HKV, D, F, S, rot;
+    bool f16;
+    float eps, base;
+};
+
+bool validate_block_cfg(V& v, const bpd_llama_config* cfg, int T, int kv_pos, const int32_t* pos_ids, BlockGeo& g) {
+    v.ptr(cfg, 1, "cfg");
+    if (!v.ok) return false;
+    g = BlockGeo{cfg->embed_dim, cfg->n_heads, cfg->n_kv_heads, cfg->head_dim, cfg->ffn_dim, cfg->max_seq_len,
+                 cfg->rope_dim / 2, cfg->kv_cache_f16 != 0, cfg->rms_eps, cfg->rope_base};
+    v.need(T >= 0, BPDQ_ERR_SHAPE, "n_tokens is negative");
+    v.need(g.H > 0 && g.HKV > 0 && g.H % g.HKV == 0, BPDQ_ERR_SHAPE,
+           "n_heads and n_kv_heads must be positive, n_heads a multiple of n_kv_heads");
+    v.need(g.D > 0 && g.D % 32 == 0 && g.D <= kMaxHeadDim, BPDQ_ERR_SHAPE,
+           "head_dim must be a multiple of 32 and at most 256");
+    v.need(g.E == g.H * g.D && g.E <= kMaxEmbd, BPDQ_ERR_SHAPE, "embed_dim must equal n_heads * head_dim, at most 16384");
+    v.need(g.F > 0 && g.F % 32 == 0, BPDQ_ERR_SHAPE, "ffn_dim must be a positive multiple of 32");
+    v.need(cfg->rope_dim >= 2 && cfg->rope_dim <= g.D && cfg->rope_dim % 2 == 0, BPDQ_ERR_SHAPE,
+           "rope_dim must be even, in 2..head_dim");
+    v.need(g.S > 0 && g.S <= kMaxCtx, BPDQ_ERR_SHAPE, "max_seq_len must be in 1..32768");
+    v.need(kv_pos >= 0 && (int64_t)kv_pos + T <= g.S, BPDQ_ERR_SHAPE, "kv_pos + n_tokens must be in 0..max_seq_len");
+    if (!v.ok || T == 0) return v.ok;
+    v.ptr(pos_ids, 4, "pos_ids");
+    for (int t = 0; t < T && v.ok; t++)
+        v.need(pos_ids[t] >= 0 && pos_ids[t] < g.S, BPDQ_ERR_SHAPE, "pos_ids[t] must be in 0..max_seq_len-1");
+    return v.ok;
+}
+
+void validate_layer(V& v, const bpd_llama_layer_weights* lw, const void* kc, const void* vc) {
+    v.ptr(lw, 1, "layer weights");
+    if (!v.ok) return;
+    v.ptr(lw->attn_norm_w, 16, "attn_norm_w");
+    v.ptr(lw->ffn_norm_w, 16, "ffn_norm_w");
+    const void* m[7] = {lw->w_q, lw->w_k, lw->w_v, lw->w_o, lw->w_gate, lw->w_up, lw->w_down};
+    static const char* names[7] = {"w_q", "w_k", "w_v", "w_o", "w_gate", "w_up", "w_down"};
+    for (int i = 0; i < 7; i++) v.ptr(m[i], 1, names[i]);
+    v.ptr(kc, 16, "k_cache");
+    v.ptr(vc, 16, "v_cache");
+}
+
+constexpr int kRopeSlots = kMaxHeadDim / 2;  // RopeCS entries per token
+
+struct MtCtx {
+    BlockGeo g;
+    int T, kv_pos;
+    bool order_s;
+    hipStream_t s;
+    const int32_t* ids;   // device copies of the host arrays
+    const int32_t* pos;
+    const RopeCS* tab;    // [T][kRopeSlots]
+    uint8_t* xq;          // Q8_0 rows of the current GEMM input, [T][max(E,F)/32][34]
+    float* scores;        // [tc][H][ld]
+    int ld, tc;           // score row length (kv_pos + T) and tokens per attention launch
+    float scale;
+};
+
+size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+size_t host_region_bytes(int T) { return 2 * align256((size_t)T * 4) + align256((size_t)T * kRopeSlots * sizeof(RopeCS)); }
+
+// Workspace: [token ids | positions | rotation table] [Q8_0 rows] [scores] [extra]
+// (extra: the forward's x and three scratch rows).  Fills c's pointers.
+uint8_t* mt_workspace(MtCtx& c, WsLease& lease, size_t extra, const char* fn) {
+    const BlockGeo& g = c.g;
+    const int kmax = g.F > g.E ? g.F : g.E;
+    c.ld = c.kv_pos + c.T;
+    const size_t per_tok = (size_t)g.H * c.ld * 4;
+    const size_t budget = (size_t)64 << 20;  // scores of at most 64 MiB per attention launch
+    c.tc = (int)std::max<size_t>(1, std::min<size_t>(std::min<size_t>((size_t)c.T, 32768), budget / per_tok));
+    const size_t hb = host_region_bytes(c.T), qb = align256((size_t)c.T * (kmax / 32) * kQ80Bytes);
+    const size_t sb = align256((size_t)c.tc * per_tok);
+    lease = workspace(hb + qb + sb + extra, c.s, fn);
+    uint8_t* ws = static_cast<uint8_t*>(lease.ptr);
+    if (ws == nullptr) return nullptr;
+    c.ids = reinterpret_cast<const int32_t*>(ws);
+    c.pos = reinterpret_cast<const int32_t*>(ws + align256((size_t)c.T * 4));
+    c.tab = reinterpret_cast<const RopeCS*>(ws + 2 * align256((size_t)c.T * 4));
+    c.xq = ws + hb;
+    c.scores = reinterpret_cast<float*>(ws + hb + qb);
+    return ws + hb + qb + sb;
+}
+
+// Copies the token ids (or none), positions and rotation angles to the head of
+// the workspace, then waits for the copy: the host arrays are the caller's.
+bool mt_upload(const MtCtx& c, const int32_t* ids, const int32_t* pos_ids, const float* freqs, const char* fn) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (!abi_hip_ok(hipStreamIsCapturing(c.s, &cs), fn)) return false;
+    if (cs != hipStreamCaptureStatusNone) {
+        abi_error(BPDQ_ERR_CAPTURE, fn, "the call uploads host arrays and waits for the copy: not under stream capture");
+        return false;
+    }
+    const int T = c.T;
+    std::vector<uint8_t> h(host_region_bytes(T), 0);
+    if (ids != nullptr) std::memcpy(h.data(), ids, (size_t)T * 4);
+    std::memcpy(h.data() + align256((size_t)T * 4), pos_ids, (size_t)T * 4);
+    RopeCS* tab = reinterpret_cast<RopeCS*>(h.data() + 2 * align256((size_t)T * 4));
+    for (int t = 0; t < T; t++)
+        rope_angles(pos_ids[t], 2 * c.g.rot, c.g.base, freqs, [&](int j, float cv, float sv) {
+            tab[(size_t)t * kRopeSlots + j] = RopeCS{cv, sv};
+        });
+    if (!abi_hip_ok(hipMemcpyAsync(const_cast<int32_t*>(c.ids), h.data(), h.size(), hipMemcpyHostToDevice, c.s), fn))
+        return false;
+    return abi_hip_ok(hipStreamSynchronize(c.s), fn);
+}
+
+// out[T][mw] = W[mw][K] . rows of c.xq (the Q8_0 rows of the input).
+void mt_gemm(const MtCtx& c, const uint8_t* W, float* out, int mw, int K) {
+    if (c.order_s)
+        launch_q8_0_gemm_S(W, c.xq, out, mw, c.T, K, 1, c.s);  // the -O2 build's llamafile: qdot S per cell
+    else
+        launch_q8_0_dispatch_T(W, c.xq, out, mw, c.T, K, c.s);
+}
+
+// Attention of the batch: out[T][H*D] and its Q8_0 rows in c.xq.
+template <typename CT>
+void mt_attention(const MtCtx& c, const float* q, const CT* kc, const CT* vc, float* out) {
+    const BlockGeo& g = c.g;
+    const int group = g.H / g.HKV;
+    const size_t slds = ((size_t)kScoreRows * score_pitch(g.D) + (size_t)group * g.D) * 4;
+    const int row = g.HKV * g.D;
+    for (int t0 = 0; t0 < c.T; t0 += c.tc) {
+        const int tn = std::min(c.tc, c.T - t0), n_max = c.kv_pos + t0 + tn;
+        const dim3 gs((n_max + kScoreRows - 1) / kScoreRows, g.HKV, tn);
+        const dim3 ts(64 * (group < kMaxGroup ? group : kMaxGroup));
+        hipLaunchKernelGGL((k_mt_scores<CT>), gs, ts, slds, c.s, q + (int64_t)t0 * g.H * g.D, kc, c.scores, c.ld,
+                           c.kv_pos + t0, g.H, g.HKV, g.D, c.scale);
+        const AttnIn ai{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, const_cast<CT*>(kc), const_cast<CT*>(vc),
+                        group, row, g.D, c.kv_pos + t0, c.scale, c.g.rot};
+        const dim3 gp(g.H * (g.D / 32), tn);
+        const size_t lds = (size_t)pad32(n_max) * 4;
+        float* o = out + (int64_t)t0 * g.H * g.D;
+        uint8_t* xq = c.xq + (int64_t)t0 * (g.H * g.D / 32) * kQ80Bytes;
+        if (n_max >= kPvBigMin && n_max <= kPvBigMax)
+            hipLaunchKernelGGL((k_attn_pv<128, CT>), gp, dim3(kPvThreads), lds, c.s, ai, c.scores, c.ld, o, xq);
+        else
+            hipLaunchKernelGGL((k_attn_pv<64, CT>), gp, dim3(kPvThreads), lds, c.s, ai, c.scores, c.ld, o, xq);
+    }
+}
+
+// One layer over the batch x[T][E], with the reference block's use of its
+// scratch rows: s1 = h, v, attention output, down output; s2 = q, O output,
+// gate, SwiGLU; s3 = k, up.
+template <typename CT>
+void mt_layer(const MtCtx& c, float* x, const bpd_llama_layer_weights& w, CT* kc, CT* vc, float* s1, float* s2,
+              float* s3) {
+    const BlockGeo& g = c.g;
+    const int T = c.T, qd = g.H * g.D, kd = g.HKV * g.D;
+    launch_norm(x, nullptr, nullptr, w.attn_norm_w, s1, c.xq, g.E, g.eps, c.s, nullptr, T);
+    mt_gemm(c, w.w_q, s2, qd, g.E);
+    mt_gemm(c, w.w_k, s3, kd, g.E);
+    mt_gemm(c, w.w_v, s1, kd, g.E);
+    hipLaunchKernelGGL((k_rope_write<CT>), dim3(T), dim3(256), 0, c.s, s2, s3, s1, kc, vc, c.pos, c.tab, g.H, g.HKV,
+                       g.D, g.rot);
+    mt_attention<CT>(c, s2, kc, vc, s1);
+    mt_gemm(c, w.w_o, s2, g.E, qd);
+    launch_norm(x, s2, x, w.ffn_norm_w, s1, c.xq, g.E, g.eps, c.s, nullptr, T);
+    mt_gemm(c, w.w_gate, s2, g.F, g.E);
+    mt_gemm(c, w.w_up, s3, g.F, g.E);
+    const int64_t tf = (int64_t)T * g.F;
+    hipLaunchKernelGGL(k_swiglu, dim3((unsigned)((tf + 255) / 256)), dim3(256), 0, c.s, s2, s3, c.xq, (int)tf);
+    mt_gemm(c, w.w_down, s1, g.E, g.F);
+    const int64_t n4 = (int64_t)T * g.E / 4;
+    hipLaunchKernelGGL(k_add, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, c.s, x, s1, n4);
+}
+
+void llama_block(bool order_s, float* x, const bpd_llama_layer_weights* lw, const bpd_llama_config* cfg,
+                 const int32_t* pos_ids, int T, int kv_pos, uint16_t* kc, uint16_t* vc, float* s1, float* s2,
+                 float* s3, const float* freqs, const char* fn) {
+    V v{fn};
+    MtCtx c{};
+    if (!validate_block_cfg(v, cfg, T, kv_pos, pos_ids, c.g) || T == 0) return;
+    v.ptr(x, 16, "x");
+    validate_layer(v, lw, kc, vc);
+    v.ptr(s1, 16, "scratch1");
+    v.ptr(s2, 16, "scratch2");
+    v.ptr(s3, 16, "scratch3");
+    if (!v.ok || !lds_limits_set(fn)) return;
+    c.T = T;
+    c.kv_pos = kv_pos;
+    c.order_s = order_s;
+    c.s = abi_stream();
+    c.scale = 1.0f / sqrtf((float)c.g.D);
+    WsLease lease;
+    if (mt_workspace(c, lease, 0, fn) == nullptr) return;
+    if (!mt_upload(c, nullptr, pos_ids, freqs, fn)) return;
+    if (c.g.f16)
+        mt_layer<uint16_t>(c, x, *lw, kc, vc, s1, s2, s3);
+    else
+        mt_layer<float>(c, x, *lw, reinterpret_cast<float*>(kc), reinterpret_cast<float*>(vc), s1, s2, s3);
+    abi_hip_ok(hipGetLastError(), fn);
+}
+
+void llama_forward(bool order_s, const int32_t* ids, int T, const bpd_llama_weights* w, const bpd_llama_config* cfg,
+                   const int32_t* pos_ids, int kv_pos, uint16_t* kc, uint16_t* vc, float* logits, int64_t* tok,
+                   const char* fn) {
+    V v{fn};
+    MtCtx c{};
+    if (!validate_block_cfg(v, cfg, T, kv_pos, pos_ids, c.g) || T == 0) return;
+    const BlockGeo& g = c.g;
+    v.ptr(w, 1, "weights");
+    if (!v.ok) return;
+    const int L = cfg->n_layers, NV = cfg->vocab_size;
+    v.need(L >= 0, BPDQ_ERR_SHAPE, "n_layers is negative");
+    v.need(NV > 0, BPDQ_ERR_SHAPE, "vocab_size must be positive");
+    v.ptr(ids, 4, "token_ids");
+    for (int t = 0; t < T && v.ok; t++) v.need(ids[t] >= 0 && ids[t] < NV, BPDQ_ERR_SHAPE, "token id outside 0..vocab_size-1");
+    v.ptr(w->token_embd, 1, "token_embd");
+    v.ptr(w->output_norm_w, 16, "output_norm_w");
+    v.ptr(w->output_w, 1, "output_w");
+    v.ptr(logits, 4, "logits_out");
+    v.ptr(tok, 8, "token_out");
+    if (L > 0) {
+        v.ptr(w->layers, 1, "layers");
+        v.ptr(kc, 16, "k_cache");
+        v.ptr(vc, 16, "v_cache");
+    }
+    const size_t layer_elems = (size_t)g.S * g.HKV * g.D;
+    const size_t esz = g.f16 ? 2 : 4;
+    for (int l = 0; l < L && v.ok; l++)
+        validate_layer(v, &w->layers[l], reinterpret_cast<uint8_t*>(kc) + l * layer_elems * esz,
+                       reinterpret_cast<uint8_t*>(vc) + l * layer_elems * esz);
+    if (!v.ok || !lds_limits_set(fn)) return;
+    c.T = T;
+    c.kv_pos = kv_pos;
+    c.order_s = order_s;
+    c.s = abi_stream();
+    c.scale = 1.0f / sqrtf((float)g.D);
+    const int kmax = g.F > g.E ? g.F : g.E;
+    const size_t xb = align256((size_t)T * g.E * 4), sb = align256((size_t)T * kmax * 4);
+    WsLease lease;
+    uint8_t* extra = mt_workspace(c, lease, xb + 3 * sb, fn);
+    if (extra == nullptr) return;
+    if (!mt_upload(c, ids, pos_ids, w->rope_freqs, fn)) return;
+    float* x = reinterpret_cast<float*>(extra);
+    float* s1 = reinterpret_cast<float*>(extra + xb);
+    float* s2 = reinterpret_cast<float*>(extra + xb + sb);
+    float* s3 = reinterpret_cast<float*>(extra + xb + 2 * sb);
+    launch_embed_q8_0(w->token_embd, c.ids, x, T, g.E, c.s);
+    for (int l = 0; l < L; l++) {
+        if (g.f16)
+            mt_layer<uint16_t>(c, x, w->layers[l], kc + l * layer_elems, vc + l * layer_elems, s1, s2, s3);
+        else
+            mt_layer<float>(c, x, w->layers[l], reinterpret_cast<float*>(kc) + l * layer_elems,
+                            reinterpret_cast<float*>(vc) + l * layer_elems, s1, s2, s3);
+    }
+    launch_norm(x, nullptr, nullptr, w->output_norm_w, s1, c.xq, g.E, g.eps, c.s, nullptr, T);
+    mt_gemm(c, w->output_w, logits, NV, g.E);
+    hipLaunchKernelGGL(k_argmax<1024>, dim3(T), dim3(1024), 0, c.s, logits, NV, nullptr, tok);
+    abi_hip_ok(hipGetLastError(), fn);
 }
 
 }  // namespace
@@ -1063,8 +1564,8 @@ int generate_token(const LayerWeights* layers, const ModelConfig* cfg, const Wor
                    int position, const void* embedding, const void* output_norm_w, const void* lm_head,
                    const void* lm_f32, int lm_K, int lm_N) {
     const char* fn = "generate_token";
-    if (!bpdq::enqueue_step(BPDQ_W_Q8_PAD64, layers, cfg, buf, kv, position, embedding, output_norm_w, lm_head,
-                            lm_f32, lm_K, lm_N, fn))
+    if (!bpdq::enqueue_step(bpdq::plain_opts(BPDQ_W_Q8_PAD64, cfg), layers, cfg, buf, kv, position, embedding,
+                            output_norm_w, lm_head, lm_f32, lm_K, lm_N, fn))
         return -1;
     int32_t tok = -1;
     const hipStream_t s = bpdq::abi_stream();
@@ -1076,8 +1577,27 @@ int generate_token(const LayerWeights* layers, const ModelConfig* cfg, const Wor
 int bpd_llama_step_gpu(int weight_format, const LayerWeights* layers, const ModelConfig* cfg,
                        const WorkBuffers* buf, const KVCache* kv, int position, const void* embedding,
                        const void* output_norm_w, const void* lm_head, const void* lm_f32, int lm_K, int lm_N) {
-    return bpdq::enqueue_step(weight_format, layers, cfg, buf, kv, position, embedding, output_norm_w, lm_head,
-                              lm_f32, lm_K, lm_N, "bpd_llama_step_gpu")
+    return bpdq::enqueue_step(bpdq::plain_opts(weight_format, cfg), layers, cfg, buf, kv, position, embedding,
+                              output_norm_w, lm_head, lm_f32, lm_K, lm_N, "bpd_llama_step_gpu")
+               ? 0
+               : -1;
+}
+
+int bpd_llama_step_ext_gpu(int weight_format, const bpd_llama_step_opts* opts, const LayerWeights* layers,
+                           const ModelConfig* cfg, const WorkBuffers* buf, const KVCache* kv, int position,
+                           const void* embedding, const void* output_norm_w, const void* lm_head, const void* lm_f32,
+                           int lm_K, int lm_N) {
+    const char* fn = "bpd_llama_step_ext_gpu";
+    bpdq::StepOpts o = bpdq::plain_opts(weight_format, cfg);
+    if (opts != nullptr) {
+        o.layer_formats = opts->layer_formats;
+        o.lm_format = opts->lm_format < 0 ? weight_format : opts->lm_format;
+        o.rope_dim = opts->rope_dim == 0 ? o.rope_dim : opts->rope_dim;
+        o.rope_freqs = opts->rope_freqs;
+        o.f16 = opts->kv_cache_f16 != 0;
+    }
+    return bpdq::enqueue_step(o, layers, cfg, buf, kv, position, embedding, output_norm_w, lm_head, lm_f32, lm_K,
+                              lm_N, fn)
                ? 0
                : -1;
 }
@@ -1095,6 +1615,31 @@ void* gpu_alloc(int bytes) {
         return nullptr;
     }
     return p;
+}
+
+void bpd_llama_block_gpu(float* x, const bpd_llama_layer_weights* lw, const bpd_llama_config* cfg,
+                         const int32_t* pos_ids, int n_tokens, int kv_pos, uint16_t* k_cache, uint16_t* v_cache,
+                         float* scratch1, float* scratch2, float* scratch3, const float* rope_freqs) {
+    bpdq::llama_block(false, x, lw, cfg, pos_ids, n_tokens, kv_pos, k_cache, v_cache, scratch1, scratch2, scratch3,
+                      rope_freqs, "bpd_llama_block_gpu");
+}
+void bpd_llama_block_s_gpu(float* x, const bpd_llama_layer_weights* lw, const bpd_llama_config* cfg,
+                           const int32_t* pos_ids, int n_tokens, int kv_pos, uint16_t* k_cache, uint16_t* v_cache,
+                           float* scratch1, float* scratch2, float* scratch3, const float* rope_freqs) {
+    bpdq::llama_block(true, x, lw, cfg, pos_ids, n_tokens, kv_pos, k_cache, v_cache, scratch1, scratch2, scratch3,
+                      rope_freqs, "bpd_llama_block_s_gpu");
+}
+void bpd_llama_forward_gpu(const int32_t* token_ids, int n_tokens, const bpd_llama_weights* weights,
+                           const bpd_llama_config* cfg, const int32_t* pos_ids, int kv_pos, uint16_t* k_cache,
+                           uint16_t* v_cache, float* logits_out, int64_t* token_out) {
+    bpdq::llama_forward(false, token_ids, n_tokens, weights, cfg, pos_ids, kv_pos, k_cache, v_cache, logits_out,
+                        token_out, "bpd_llama_forward_gpu");
+}
+void bpd_llama_forward_s_gpu(const int32_t* token_ids, int n_tokens, const bpd_llama_weights* weights,
+                             const bpd_llama_config* cfg, const int32_t* pos_ids, int kv_pos, uint16_t* k_cache,
+                             uint16_t* v_cache, float* logits_out, int64_t* token_out) {
+    bpdq::llama_forward(true, token_ids, n_tokens, weights, cfg, pos_ids, kv_pos, k_cache, v_cache, logits_out,
+                        token_out, "bpd_llama_forward_s_gpu");
 }
 
 void gpu_free(void* p) {
@@ -1145,7 +1690,7 @@ void bpd_argmax_gpu(const float* x, int n, int32_t* out) {
     v.ptr(x, 16, "x");
     v.ptr(out, 4, "out");
     if (!v.ok) return;
-    hipLaunchKernelGGL(bpdq::k_argmax<1024>, dim3(1), dim3(1024), 0, bpdq::abi_stream(), x, n, out);
+    hipLaunchKernelGGL(bpdq::k_argmax<1024>, dim3(1), dim3(1024), 0, bpdq::abi_stream(), x, n, out, nullptr);
     bpdq::abi_hip_ok(hipGetLastError(), fn);
 }
 

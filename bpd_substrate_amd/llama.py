@@ -17,7 +17,7 @@ import ctypes
 
 from . import gpu
 
-W_Q8_PAD64, W_Q4K, W_Q4K_GGUF = 0, 1, 2
+W_Q8_PAD64, W_Q4K, W_Q4K_GGUF, W_Q6K, W_Q6K_GGUF = 0, 1, 2, 3, 4
 
 
 class LayerWeights(ctypes.Structure):
@@ -67,6 +67,14 @@ class WorkBuffers(ctypes.Structure):
     ]
 
 
+class StepOpts(ctypes.Structure):    # include/bpdq_llama.h bpd_llama_step_opts
+    _fields_ = [
+        ("layer_formats", ctypes.POINTER(ctypes.c_int)), ("lm_format", ctypes.c_int),
+        ("rope_dim", ctypes.c_int), ("rope_freqs", ctypes.POINTER(ctypes.c_float)),
+        ("kv_cache_f16", ctypes.c_int),
+    ]
+
+
 MATRICES = ("q", "k", "v", "o", "gate", "up", "down")
 
 
@@ -79,12 +87,30 @@ class DecodeModel:
          q, k, v, o, gate, up, down (uint8, in `fmt`), optional q_bias,
          k_bias, v_bias (fp32).
     lm_head: uint8 device tensor in `fmt`, or None with lm_f32 (fp32 [lm_N, n_embd]).
+    The extended step (bpd_llama_step_ext_gpu) is used when any of these is given:
+    formats: per layer, a dict {matrix name: W_*} for matrices not in `fmt`
+         (a Q4_K_M file keeps attn_v and ffn_down in Q6_K);
+    lm_format: the head's format (default `fmt`);
+    rope_dim, rope_freqs (numpy float32 [rope_dim/2], kept on the host);
+    kv_cache_f16: binary16 caches (torch.int16 tensors holding the bits).
     """
 
-    def __init__(self, cfg, layers, out_norm, lm_head=None, lm_f32=None, lm_N=None, fmt=W_Q8_PAD64, device=None):
+    def __init__(self, cfg, layers, out_norm, lm_head=None, lm_f32=None, lm_N=None, fmt=W_Q8_PAD64, device=None,
+                 formats=None, lm_format=None, rope_dim=None, rope_freqs=None, kv_cache_f16=False):
+        import numpy as np
         import torch
 
         self.fmt = fmt
+        self.ext = (formats is not None or lm_format is not None or rope_dim is not None or rope_freqs is not None
+                    or kv_cache_f16)
+        nl = max(1, cfg["n_layers"])
+        fm = [[(formats[l] if formats else {}).get(m, fmt) for m in MATRICES] for l in range(cfg["n_layers"])]
+        self._fmts = (ctypes.c_int * (7 * nl))(*[f for row in fm for f in row])
+        self._freqs = None if rope_freqs is None else np.ascontiguousarray(rope_freqs, np.float32)
+        self.opts = StepOpts(ctypes.cast(self._fmts, ctypes.POINTER(ctypes.c_int)) if formats else None,
+                             -1 if lm_format is None else lm_format, rope_dim or 0,
+                             None if self._freqs is None else self._freqs.ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
+                             1 if kv_cache_f16 else 0)
         self.cfg_d = dict(cfg)
         E, H, HKV, D, F = (cfg["n_embd"], cfg["n_head"], cfg["n_head_kv"], cfg["head_dim"], cfg["ff_dim"])
         L, S = cfg["n_layers"], cfg["max_seq"]
@@ -110,8 +136,9 @@ class DecodeModel:
                       "attn_out": z(H * D), "gate": z(F), "up": z(F), "ffn": z(E),
                       "logits": z(self.lm_N), "argmax_result": z(4, torch.int32)}
         self.buf = WorkBuffers(**{k: v.data_ptr() for k, v in self.buf_t.items()})
-        self.k_cache = [z(S * HKV * D) for _ in range(L)]
-        self.v_cache = [z(S * HKV * D) for _ in range(L)]
+        cdt = torch.int16 if kv_cache_f16 else torch.float32
+        self.k_cache = [z(S * HKV * D, cdt) for _ in range(L)]
+        self.v_cache = [z(S * HKV * D, cdt) for _ in range(L)]
         self._kp = (ctypes.c_void_p * max(1, L))(*[t.data_ptr() for t in self.k_cache])
         self._vp = (ctypes.c_void_p * max(1, L))(*[t.data_ptr() for t in self.v_cache])
         self.kv = KVCache(ctypes.cast(self._kp, ctypes.POINTER(ctypes.c_void_p)),
@@ -127,7 +154,7 @@ class DecodeModel:
     def step(self, emb, pos):
         """One token through every layer; returns the argmax token (waits)."""
         gpu._use_torch_stream()
-        if self.fmt == W_Q8_PAD64:
+        if self.fmt == W_Q8_PAD64 and not self.ext:
             tok = gpu.call("generate_token", *self._args(emb, pos))
             if tok < 0:
                 gpu.check()
@@ -142,6 +169,99 @@ class DecodeModel:
         """The same step, launched on torch's current stream without waiting;
         the token is left in buf_t['argmax_result']."""
         gpu._use_torch_stream()
-        rc = gpu.call("bpd_llama_step_gpu", self.fmt, *self._args(emb, pos))
+        if self.ext:
+            rc = gpu.call("bpd_llama_step_ext_gpu", self.fmt, ctypes.addressof(self.opts), *self._args(emb, pos))
+        else:
+            rc = gpu.call("bpd_llama_step_gpu", self.fmt, *self._args(emb, pos))
         if rc != 0:
             gpu.check()
+
+
+# ---- the reference's CPU transformer ABI (bench/bpd_cpu.c:5556-5604), on the GPU ----
+# Field for field the ctypes structs of the reference's CPU driver
+# (bench/bpd_llamatov_infer.py:45-83), so its build_model() output binds unchanged.
+_fp = ctypes.POINTER(ctypes.c_float)
+_u8p = ctypes.POINTER(ctypes.c_uint8)
+
+
+class BpdLlamaConfig(ctypes.Structure):
+    _fields_ = [
+        ("n_layers", ctypes.c_int), ("n_heads", ctypes.c_int), ("n_kv_heads", ctypes.c_int),
+        ("head_dim", ctypes.c_int), ("embed_dim", ctypes.c_int), ("ffn_dim", ctypes.c_int),
+        ("vocab_size", ctypes.c_int), ("max_seq_len", ctypes.c_int),
+        ("rms_eps", ctypes.c_float), ("rope_base", ctypes.c_float),
+        ("rope_dim", ctypes.c_int), ("kv_cache_f16", ctypes.c_int),
+    ]
+
+
+class BpdLlamaLayerWeights(ctypes.Structure):
+    _fields_ = [
+        ("attn_norm_w", _fp), ("w_q", _u8p), ("w_k", _u8p), ("w_v", _u8p), ("w_o", _u8p),
+        ("ffn_norm_w", _fp), ("w_gate", _u8p), ("w_up", _u8p), ("w_down", _u8p),
+    ]
+
+
+class BpdLlamaWeights(ctypes.Structure):
+    _fields_ = [
+        ("token_embd", _u8p), ("layers", ctypes.POINTER(BpdLlamaLayerWeights)),
+        ("output_norm_w", _fp), ("output_w", _u8p), ("rope_freqs", _fp),
+    ]
+
+
+_REF_LAYER = ("attn_norm_w", "w_q", "w_k", "w_v", "w_o", "ffn_norm_w", "w_gate", "w_up", "w_down")
+
+
+def layer_struct(lw):
+    """BpdLlamaLayerWeights of device tensors keyed by the struct's field names."""
+    s = BpdLlamaLayerWeights()
+    for n, t in BpdLlamaLayerWeights._fields_:
+        setattr(s, n, ctypes.cast(lw[n].data_ptr(), t))
+    return s
+
+
+class Forward:
+    """A model in the reference CPU ABI's layout on the device: Q8_0 weights
+    (GGUF bytes), fp32 norms, caches of n_layers * max_seq_len rows in
+    binary16 (torch.int16 bits) or fp32.  forward() is bpd_llama_forward_gpu
+    (or the _s_ form with order="S"):
+
+        f = Forward(cfg, layers, token_embd, output_norm, output_w, rope_freqs=None)
+        logits, tokens = f.forward(token_ids, pos_ids, kv_pos)
+
+    cfg: dict with BpdLlamaConfig's field names; layers: dicts of device tensors
+    with BpdLlamaLayerWeights' field names."""
+
+    def __init__(self, cfg, layers, token_embd, output_norm, output_w, rope_freqs=None, device=None):
+        import numpy as np
+        import torch
+
+        self.cfg = BpdLlamaConfig(*(cfg[n] for n, _ in BpdLlamaConfig._fields_))
+        L, S, HKV, D = cfg["n_layers"], cfg["max_seq_len"], cfg["n_kv_heads"], cfg["head_dim"]
+        dev = device if device is not None else output_norm.device
+        self.keep = [layers, token_embd, output_norm, output_w]
+        self.layers = (BpdLlamaLayerWeights * max(1, L))(*[layer_struct(lw) for lw in layers])
+        self._freqs = None if rope_freqs is None else np.ascontiguousarray(rope_freqs, np.float32)
+        self.w = BpdLlamaWeights(ctypes.cast(token_embd.data_ptr(), _u8p),
+                                 ctypes.cast(self.layers, ctypes.POINTER(BpdLlamaLayerWeights)),
+                                 ctypes.cast(output_norm.data_ptr(), _fp), ctypes.cast(output_w.data_ptr(), _u8p),
+                                 None if self._freqs is None else self._freqs.ctypes.data_as(_fp))
+        cdt = torch.int16 if cfg["kv_cache_f16"] else torch.float32
+        self.k_cache = torch.zeros(max(1, L) * S * HKV * D, dtype=cdt, device=dev)
+        self.v_cache = torch.zeros(max(1, L) * S * HKV * D, dtype=cdt, device=dev)
+        self.device = dev
+
+    def forward(self, token_ids, pos_ids, kv_pos, order="T"):
+        """Returns device tensors (logits [n][vocab_size] fp32, tokens [n] int64)."""
+        import numpy as np
+        import torch
+
+        ids = np.ascontiguousarray(token_ids, np.int32)
+        pos = np.ascontiguousarray(pos_ids, np.int32)
+        n = ids.size
+        logits = torch.empty(max(1, n) * self.cfg.vocab_size, dtype=torch.float32, device=self.device)
+        toks = torch.empty(max(1, n), dtype=torch.int64, device=self.device)
+        gpu._use_torch_stream()
+        gpu.call("bpd_llama_forward_s_gpu" if order == "S" else "bpd_llama_forward_gpu", ids.ctypes.data, n,
+                 ctypes.addressof(self.w), ctypes.addressof(self.cfg), pos.ctypes.data, int(kv_pos), self.k_cache,
+                 self.v_cache, logits, toks)
+        return logits[: n * self.cfg.vocab_size], toks[:n]

@@ -33,8 +33,13 @@
  *   - q/k/v biases (the qwen2 fields) are added to the projection before RoPE,
  *     as in llama.cpp's qwen2 graph; the reference block has no biases.
  * Calls run on the stream of bpd_gpu_set_stream() (include/bpdq.h); errors are
- * recorded for bpd_gpu_last_error().  The library keeps one device workspace
- * for the quantized activations: steps that overlap on different streams race.
+ * recorded for bpd_gpu_last_error().  The quantized activations and attention
+ * scores live in the library's workspace of (device, stream): steps on one
+ * stream run in order over it, steps on different streams use different
+ * buffers.  It grows only outside stream capture (a step that would need it to
+ * grow during capture fails with BPDQ_ERR_CAPTURE: run one step on that stream
+ * first), and buffers it outgrows stay allocated for graphs captured with them
+ * until bpd_gpu_workspace_release().
  */
 #ifndef BPDQ_LLAMA_H
 #define BPDQ_LLAMA_H
@@ -129,9 +134,119 @@ void gpu_free(void* p);
 #define BPDQ_W_Q8_PAD64 0
 #define BPDQ_W_Q4K 1
 #define BPDQ_W_Q4K_GGUF 2
+#define BPDQ_W_Q6K 3      /* Q6_K GGUF bytes [N][K/256][210], the reference's element map */
+#define BPDQ_W_Q6K_GGUF 4 /* Q6_K, GGUF (llama.cpp) element map */
 int bpd_llama_step_gpu(int weight_format, const LayerWeights* layers, const ModelConfig* cfg,
                        const WorkBuffers* buf, const KVCache* kv, int position, const void* embedding,
                        const void* output_norm_w, const void* lm_head, const void* lm_f32, int lm_K, int lm_N);
+
+/* No counterpart in the reference's GPU ABI, whose ModelConfig has no room for
+ * them; the reference's CPU block has each (bench/bpd_cpu.c:5556-5604).  The
+ * same step with:
+ *   layer_formats  host [n_layers][7] formats of q, k, v, o, gate, up, down
+ *                  (NULL: weight_format everywhere).  A Q4_K_M file mixes
+ *                  Q6_K into attn_v and ffn_down (inference/llamatov_helpers.py
+ *                  dispatches per tensor type, :195-222).  Either every
+ *                  matrix is BPDQ_W_Q8_PAD64 or none is (the K-quants take
+ *                  Q8_K activations, the padded layout Q8_0 ones);
+ *   lm_format      format of lm_head (-1: weight_format);
+ *   rope_dim       elements of each head that rotate (0: head_dim), the
+ *                  reference's cfg->rope_dim;
+ *   rope_freqs     host [rope_dim / 2] frequency factors (Llama 3's
+ *                  rope_freqs.weight) or NULL, read during the call;
+ *   kv_cache_f16   1: the caches hold binary16 [max_seq][n_head_kv * head_dim]
+ *                  (cfg->kv_cache_f16 of the reference; its f32_to_f16 bits on
+ *                  write, f16_to_f32 on read).
+ * A Q6_K gate/up pair, or one of two element maps, runs as two GEMVs and
+ * SwiGLU; a Q6_K matrix reads the Q8_K of its activation. */
+typedef struct {
+    const int* layer_formats;
+    int lm_format;
+    int rope_dim;
+    const float* rope_freqs;
+    int kv_cache_f16;
+} bpd_llama_step_opts;
+int bpd_llama_step_ext_gpu(int weight_format, const bpd_llama_step_opts* opts, const LayerWeights* layers,
+                           const ModelConfig* cfg, const WorkBuffers* buf, const KVCache* kv, int position,
+                           const void* embedding, const void* output_norm_w, const void* lm_head, const void* lm_f32,
+                           int lm_K, int lm_N);
+
+/* ---- the reference's CPU transformer ABI, on the GPU ----
+ * The structs and entry points of bench/bpd_cpu.c:5556-5798, argument for
+ * argument, for n_tokens >= 1 (prefill, or one token at a time):
+ * bpd_llama_block_gpu replaces bpd_llama_block_cpu (:5608-5737) and
+ * bpd_llama_forward_gpu replaces bpd_llama_forward_cpu (:5740-5798).  Weights
+ * are Q8_0 rows [N][K/32][34] (GGUF bytes unchanged); the caches are
+ * [max_seq_len][n_kv_heads * head_dim] per layer, binary16 when
+ * cfg->kv_cache_f16 (the reference's f32_to_f16 / f16_to_f32 bits) and fp32
+ * otherwise.  RoPE follows bpd_rope_norm_freqs_cpu (:5146-5184): the first
+ * rope_dim elements of each head rotate in pairs, pair j by pos_ids[t] *
+ * theta_scale^j / rope_freqs[j], the rest pass through.
+ *
+ * Memory: every tensor is a device pointer (fp32 ones 16-byte aligned);
+ * the structs, the layers array, token_ids, pos_ids and rope_freqs are host
+ * memory, read before the call returns (the rotation angles are taken with
+ * the host's libm, as the reference's cosf/sinf).  scratch1..3 hold at least
+ * n_tokens * max(embed_dim, ffn_dim) floats each, as in the reference.
+ * token_out is int64 (the reference's long).  The calls enqueue on the
+ * stream of bpd_gpu_set_stream() after one synchronization for the upload
+ * of token ids, positions and angles; results are ready when that stream is.
+ *
+ * Order: bpd_llama_block_gpu / bpd_llama_forward_gpu give the bits of the
+ * reference built with -mavx -mssse3 (its correctness build: Q8_0 products in
+ * the llamafile tile order); the _s_ forms give those of its -O2 scalar build
+ * (qdot order S, run on int8 MFMA).  Every other operation is shared.
+ * Conditions: head_dim a multiple of 32, at most 256; embed_dim = n_heads *
+ * head_dim, at most 16384; ffn_dim a multiple of 32; n_heads a multiple of
+ * n_kv_heads; rope_dim even, 2 <= rope_dim <= head_dim; max_seq_len <= 32768;
+ * kv_pos >= 0, kv_pos + n_tokens <= max_seq_len; every pos_ids[t] in
+ * [0, max_seq_len); finite activations and cache contents.
+ * Differences from the reference, by design:
+ *   - attention reads cache rows 0..kv_pos+t for query t; the reference
+ *     scores all max_seq_len rows and masks the rest to weight 0, which adds
+ *     exact zeros when those rows hold finite values;
+ *   - with fp32 caches, bpd_llama_forward_cpu steps from one layer's cache to
+ *     the next by max_seq_len * n_kv_heads * head_dim uint16_t (:5771-5773),
+ *     half an fp32 layer, so its layers overlap; bpd_llama_forward_gpu gives
+ *     each layer a whole fp32 layer (the same bits while positions stay below
+ *     max_seq_len / 2).  With binary16 caches (the reference driver's default,
+ *     bench/bpd_llamatov_infer.py:453) the layouts are the same. */
+typedef struct { /* bench/bpd_cpu.c:5556-5570 */
+    int n_layers, n_heads, n_kv_heads, head_dim, embed_dim, ffn_dim, vocab_size, max_seq_len;
+    float rms_eps, rope_base;
+    int rope_dim, kv_cache_f16;
+} bpd_llama_config;
+
+typedef struct { /* :5585-5595, Q8_0 device tensors */
+    const float* attn_norm_w;
+    const uint8_t *w_q, *w_k, *w_v, *w_o;
+    const float* ffn_norm_w;
+    const uint8_t *w_gate, *w_up, *w_down;
+} bpd_llama_layer_weights;
+
+typedef struct { /* :5598-5604 */
+    const uint8_t* token_embd;               /* Q8_0 [vocab_size][embed_dim] */
+    const bpd_llama_layer_weights* layers;   /* host array of n_layers */
+    const float* output_norm_w;              /* [embed_dim] */
+    const uint8_t* output_w;                 /* Q8_0 [vocab_size][embed_dim] */
+    const float* rope_freqs;                 /* host [rope_dim / 2], or NULL */
+} bpd_llama_weights;
+
+/* x: [n_tokens][embed_dim] in/out; k_cache, v_cache: this layer's caches. */
+void bpd_llama_block_gpu(float* x, const bpd_llama_layer_weights* lw, const bpd_llama_config* cfg,
+                         const int32_t* pos_ids, int n_tokens, int kv_pos, uint16_t* k_cache, uint16_t* v_cache,
+                         float* scratch1, float* scratch2, float* scratch3, const float* rope_freqs);
+void bpd_llama_block_s_gpu(float* x, const bpd_llama_layer_weights* lw, const bpd_llama_config* cfg,
+                           const int32_t* pos_ids, int n_tokens, int kv_pos, uint16_t* k_cache, uint16_t* v_cache,
+                           float* scratch1, float* scratch2, float* scratch3, const float* rope_freqs);
+/* k_cache, v_cache: n_layers caches back to back; logits_out [n_tokens][vocab_size];
+ * token_out [n_tokens] (the argmax of each row, bpd_argmax_dim_cpu). */
+void bpd_llama_forward_gpu(const int32_t* token_ids, int n_tokens, const bpd_llama_weights* weights,
+                           const bpd_llama_config* cfg, const int32_t* pos_ids, int kv_pos, uint16_t* k_cache,
+                           uint16_t* v_cache, float* logits_out, int64_t* token_out);
+void bpd_llama_forward_s_gpu(const int32_t* token_ids, int n_tokens, const bpd_llama_weights* weights,
+                             const bpd_llama_config* cfg, const int32_t* pos_ids, int kv_pos, uint16_t* k_cache,
+                             uint16_t* v_cache, float* logits_out, int64_t* token_out);
 
 /* ---- single steps of the decode step, for parity tests ----
  * x_out = x_in (+ add); h = rmsnorm(x_out) * w; xq = Q8_0(h) when xq != NULL

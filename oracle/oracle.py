@@ -376,3 +376,67 @@ def ref_llama_step(layers, cfg, k_cache, v_cache, pos, emb, out_norm, lm, lm_N, 
     tok = np.zeros(1, np.int64)
     R.bpd_argmax_dim_cpu(_p(logits), _p(tok), 1, lm_N, 1)
     return int(tok[0]), x, h, logits
+
+
+def _ref_sigs(R):
+    for name, args in (("bpd_llama_block_cpu", [P, P, P, P, I, I, P, P, P, P, P, P]),
+                       ("bpd_llama_forward_cpu", [P, I, P, P, P, I, P, P, P, P])):
+        f = getattr(R, name)
+        f.argtypes, f.restype = args, None
+
+
+class RefLlamaWeights(ctypes.Structure):     # bench/bpd_cpu.c:5598-5604
+    _fields_ = [("token_embd", P), ("layers", P), ("output_norm_w", P), ("output_w", P), ("rope_freqs", P)]
+
+
+_REF_LAYER = ("attn_norm_w", "w_q", "w_k", "w_v", "w_o", "ffn_norm_w", "w_gate", "w_up", "w_down")
+
+
+def ref_block(layer, cfg, x, pos_ids, kv_pos, k_cache, v_cache, rope_freqs=None, kind="avx"):
+    """The reference's own bpd_llama_block_cpu (bench/bpd_cpu.c:5608-5737) from
+    oracle/_ref on host arrays: layer is a dict of numpy arrays keyed by
+    bpd_llama_layer_weights' field names (Q8_0 rows, fp32 norms); cfg a dict keyed
+    by bpd_llama_config's; x fp32 [n_tokens * embed_dim], k_cache / v_cache this
+    layer's caches (uint16 bits when cfg["kv_cache_f16"], else fp32), all updated
+    in place.  Returns False when oracle/_ref is not built."""
+    R = ref(kind)
+    if R is None:
+        return False
+    _ref_sigs(R)
+    c = RefLlamaConfig(*(cfg[n] for n, _ in RefLlamaConfig._fields_))
+    w = RefLayerWeights(*(_addr(layer[n]) for n in _REF_LAYER))
+    T = len(pos_ids)
+    big = T * max(cfg["embed_dim"], cfg["ffn_dim"])
+    s1, s2, s3 = (np.zeros(big, np.float32) for _ in range(3))
+    pos = np.ascontiguousarray(pos_ids, np.int32)
+    fr = None if rope_freqs is None else np.ascontiguousarray(rope_freqs, np.float32)
+    R.bpd_llama_block_cpu(_p(x), ctypes.addressof(w), ctypes.addressof(c), _p(pos), T, kv_pos, _p(k_cache),
+                          _p(v_cache), _p(s1), _p(s2), _p(s3), _addr(fr))
+    return True
+
+
+def ref_forward(weights, cfg, token_ids, pos_ids, kv_pos, k_cache, v_cache, kind="avx"):
+    """The reference's own bpd_llama_forward_cpu (bench/bpd_cpu.c:5740-5798) from
+    oracle/_ref: weights is a dict {token_embd, layers (list of layer dicts as for
+    ref_block), output_norm_w, output_w, rope_freqs (or None)}; the caches hold
+    n_layers layers and are updated in place.  Returns (logits [n][vocab], tokens
+    int64 [n]), or None when oracle/_ref is not built."""
+    R = ref(kind)
+    if R is None:
+        return None
+    _ref_sigs(R)
+    c = RefLlamaConfig(*(cfg[n] for n, _ in RefLlamaConfig._fields_))
+    lws = (RefLayerWeights * max(1, len(weights["layers"])))(
+        *[RefLayerWeights(*(_addr(lw[n]) for n in _REF_LAYER)) for lw in weights["layers"]])
+    fr = weights.get("rope_freqs")
+    fr = None if fr is None else np.ascontiguousarray(fr, np.float32)
+    W = RefLlamaWeights(_addr(weights["token_embd"]), ctypes.addressof(lws), _addr(weights["output_norm_w"]),
+                        _addr(weights["output_w"]), _addr(fr))
+    ids = np.ascontiguousarray(token_ids, np.int32)
+    pos = np.ascontiguousarray(pos_ids, np.int32)
+    n = ids.size
+    logits = np.zeros(n * cfg["vocab_size"], np.float32)
+    toks = np.zeros(n, np.int64)
+    R.bpd_llama_forward_cpu(_p(ids), n, ctypes.addressof(W), ctypes.addressof(c), _p(pos), kv_pos, _p(k_cache),
+                            _p(v_cache), _p(logits), _p(toks))
+    return logits.reshape(n, cfg["vocab_size"]), toks
