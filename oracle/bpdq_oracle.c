@@ -1008,18 +1008,41 @@ static void step_gemv(int fmt, const uint8_t* W, const float* a, float* y, int N
     } else {
         uint8_t* aq = (uint8_t*)malloc((size_t)(K / 256) * 292);
         bpdq_o_quant_q8_k(a, aq, K);
-        bpdq_o_qmatmul_q4k_q8k(W, aq, y, N, K, fmt == 2 ? 1 : 0);
+        if (fmt == 3 || fmt == 4)
+            bpdq_o_qmatmul_q6k_q8k(W, aq, y, N, K, fmt == 4 ? 1 : 0);
+        else
+            bpdq_o_qmatmul_q4k_q8k(W, aq, y, N, K, fmt == 2 ? 1 : 0);
         free(aq);
+    }
+}
+
+/* bench/bpd_cpu.c:5146-5184, one token */
+void bpdq_o_rope_norm_freqs(float* t, int n_heads, int head_dim, int pos, float base, int n_dims,
+                            const float* freqs) {
+    const float theta_scale = powf(base, -2.0f / (float)n_dims);
+    for (int hh = 0; hh < n_heads; hh++) {
+        float* p = t + (size_t)hh * head_dim;
+        float theta = (float)pos;
+        for (int i0 = 0; i0 < n_dims; i0 += 2) {
+            const float ff = freqs ? freqs[i0 / 2] : 1.0f;
+            const float te = theta / ff;
+            const float c = cosf(te), s = sinf(te);
+            const float x0 = p[i0], x1 = p[i0 + 1];
+            p[i0] = x0 * c - x1 * s;
+            p[i0 + 1] = x0 * s + x1 * c;
+            theta *= theta_scale;
+        }
     }
 }
 
 /* The composition of bpd_llama_block_cpu (bench/bpd_cpu.c:5611-5737) over the
  * layers and the head of bpd_llama_forward_cpu (:5779-5792) for one token. */
-int bpdq_o_llama_step(int fmt, const bpdq_o_layer* layers, const bpdq_o_cfg* cfg, float* const* k_cache,
-                      float* const* v_cache, int pos, const float* emb, const float* out_norm, const uint8_t* lm,
-                      const float* lm_f32, int lm_N, float* x, float* h, float* logits) {
+int bpdq_o_llama_step_ext(const bpdq_o_step_opts* o, const bpdq_o_layer* layers, const bpdq_o_cfg* cfg,
+                          void* const* k_cache, void* const* v_cache, int pos, const float* emb,
+                          const float* out_norm, const uint8_t* lm, const float* lm_f32, int lm_N, float* x,
+                          float* h, float* logits) {
     const int E = cfg->n_embd, H = cfg->n_head, HKV = cfg->n_head_kv, D = cfg->head_dim, F = cfg->ff_dim;
-    const int row = HKV * D;
+    const int row = HKV * D, S = cfg->max_seq;
     float* q = (float*)malloc(sizeof(float) * (size_t)H * D);
     float* k = (float*)malloc(sizeof(float) * (size_t)row);
     float* v = (float*)malloc(sizeof(float) * (size_t)row);
@@ -1027,36 +1050,68 @@ int bpdq_o_llama_step(int fmt, const bpdq_o_layer* layers, const bpdq_o_cfg* cfg
     float* t = (float*)malloc(sizeof(float) * (size_t)E);
     float* g = (float*)malloc(sizeof(float) * (size_t)F);
     float* u = (float*)malloc(sizeof(float) * (size_t)F);
+    float* kf = o->kv_f16 ? (float*)malloc(sizeof(float) * (size_t)S * row) : NULL;
+    float* vf = o->kv_f16 ? (float*)malloc(sizeof(float) * (size_t)S * row) : NULL;
     memcpy(x, emb, sizeof(float) * (size_t)E);
     const float scale = 1.0f / sqrtf((float)D);
     for (int l = 0; l < cfg->n_layers; l++) {
         const bpdq_o_layer* w = &layers[l];
+        const int* f = o->fmts + 7 * l;
         bpdq_o_rmsnorm(x, w->attn_norm, h, E, cfg->eps);
-        step_gemv(fmt, w->q, h, q, H * D, E);
-        step_gemv(fmt, w->k, h, k, row, E);
-        step_gemv(fmt, w->v, h, v, row, E);
+        step_gemv(f[0], w->q, h, q, H * D, E);
+        step_gemv(f[1], w->k, h, k, row, E);
+        step_gemv(f[2], w->v, h, v, row, E);
         if (w->q_bias) for (int i = 0; i < H * D; i++) q[i] = q[i] + w->q_bias[i];
         if (w->k_bias) for (int i = 0; i < row; i++) k[i] = k[i] + w->k_bias[i];
         if (w->v_bias) for (int i = 0; i < row; i++) v[i] = v[i] + w->v_bias[i];
-        bpdq_o_rope_norm(q, H, D, pos, cfg->rope_theta);
-        bpdq_o_rope_norm(k, HKV, D, pos, cfg->rope_theta);
-        memcpy(k_cache[l] + (size_t)pos * row, k, sizeof(float) * (size_t)row);
-        memcpy(v_cache[l] + (size_t)pos * row, v, sizeof(float) * (size_t)row);
-        bpdq_o_gqa_attn(q, k_cache[l], v_cache[l], att, cfg->max_seq, pos, H, HKV, D, scale);
-        step_gemv(fmt, w->o, att, t, E, H * D);
+        bpdq_o_rope_norm_freqs(q, H, D, pos, cfg->rope_theta, o->rope_dim, o->rope_freqs);
+        bpdq_o_rope_norm_freqs(k, HKV, D, pos, cfg->rope_theta, o->rope_dim, o->rope_freqs);
+        if (o->kv_f16) {
+            uint16_t* kc = (uint16_t*)k_cache[l];
+            uint16_t* vc = (uint16_t*)v_cache[l];
+            for (int i = 0; i < row; i++) {
+                kc[(size_t)pos * row + i] = bpdq_o_f32_to_f16(k[i]);
+                vc[(size_t)pos * row + i] = bpdq_o_f32_to_f16(v[i]);
+            }
+            for (size_t i = 0; i < (size_t)S * row; i++) {
+                kf[i] = bpdq_o_f16_magic(kc[i]);
+                vf[i] = bpdq_o_f16_magic(vc[i]);
+            }
+            bpdq_o_gqa_attn(q, kf, vf, att, S, pos, H, HKV, D, scale);
+        } else {
+            float* kc = (float*)k_cache[l];
+            float* vc = (float*)v_cache[l];
+            memcpy(kc + (size_t)pos * row, k, sizeof(float) * (size_t)row);
+            memcpy(vc + (size_t)pos * row, v, sizeof(float) * (size_t)row);
+            bpdq_o_gqa_attn(q, kc, vc, att, S, pos, H, HKV, D, scale);
+        }
+        step_gemv(f[3], w->o, att, t, E, H * D);
         for (int i = 0; i < E; i++) x[i] = x[i] + t[i];
         bpdq_o_rmsnorm(x, w->ffn_norm, h, E, cfg->eps);
-        step_gemv(fmt, w->gate, h, g, F, E);
-        step_gemv(fmt, w->up, h, u, F, E);
+        step_gemv(f[4], w->gate, h, g, F, E);
+        step_gemv(f[5], w->up, h, u, F, E);
         bpdq_o_swiglu(g, u, g, F);
-        step_gemv(fmt, w->down, g, t, E, F);
+        step_gemv(f[6], w->down, g, t, E, F);
         for (int i = 0; i < E; i++) x[i] = x[i] + t[i];
     }
     bpdq_o_rmsnorm(x, out_norm, h, E, cfg->eps);
     if (lm)
-        step_gemv(fmt, lm, h, logits, lm_N, E);
+        step_gemv(o->lm_fmt, lm, h, logits, lm_N, E);
     else
         bpdq_o_gemv_f32_wave(lm_f32, h, logits, lm_N, E);
-    free(q); free(k); free(v); free(att); free(t); free(g); free(u);
+    free(q); free(k); free(v); free(att); free(t); free(g); free(u); free(kf); free(vf);
     return bpdq_o_argmax(logits, lm_N);
+}
+
+int bpdq_o_llama_step(int fmt, const bpdq_o_layer* layers, const bpdq_o_cfg* cfg, float* const* k_cache,
+                      float* const* v_cache, int pos, const float* emb, const float* out_norm, const uint8_t* lm,
+                      const float* lm_f32, int lm_N, float* x, float* h, float* logits) {
+    const int L = cfg->n_layers > 0 ? cfg->n_layers : 1;
+    int* fmts = (int*)malloc(sizeof(int) * 7 * (size_t)L);
+    for (int i = 0; i < 7 * L; i++) fmts[i] = fmt;
+    const bpdq_o_step_opts o = {fmts, fmt, cfg->head_dim, NULL, 0};
+    const int tok = bpdq_o_llama_step_ext(&o, layers, cfg, (void* const*)k_cache, (void* const*)v_cache, pos, emb,
+                                          out_norm, lm, lm_f32, lm_N, x, h, logits);
+    free(fmts);
+    return tok;
 }

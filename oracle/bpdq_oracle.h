@@ -86,6 +86,29 @@ int bpdq_o_llama_step(int fmt, const bpdq_o_layer* layers, const bpdq_o_cfg* cfg
                       float* const* v_cache, int pos, const float* emb, const float* out_norm, const uint8_t* lm,
                       const float* lm_f32, int lm_N, float* x, float* h, float* logits);
 
+/* bpd_rope_norm_freqs_cpu (bench/bpd_cpu.c:5146-5184) for one token: the first n_dims
+ * elements of each head rotate in pairs, pair j by pos * theta_scale^j / freqs[j]
+ * (freqs NULL: factor 1); the rest pass through. */
+void bpdq_o_rope_norm_freqs(float* t, int n_heads, int head_dim, int pos, float base, int n_dims,
+                            const float* freqs);
+/* The step with per-matrix formats (fmts [n_layers][7] for q k v o gate up down, lm_fmt
+ * for the head: 0 Q8_0 rows in tile order T, 1 / 2 Q4_K, 3 / 4 Q6_K in the bpd / GGUF
+ * map, each K-quant against the Q8_K of its activation), rope_dim and frequency
+ * factors (bpd_rope_norm_freqs_cpu), and binary16 caches (kv_f16: the caches are
+ * uint16 arrays written with f32_to_f16 and read back with the magic-number
+ * f16_to_f32, as bench/bpd_cpu.c:5659-5695 does). */
+typedef struct {
+    const int* fmts;
+    int lm_fmt;
+    int rope_dim;
+    const float* rope_freqs;
+    int kv_f16;
+} bpdq_o_step_opts;
+int bpdq_o_llama_step_ext(const bpdq_o_step_opts* o, const bpdq_o_layer* layers, const bpdq_o_cfg* cfg,
+                          void* const* k_cache, void* const* v_cache, int pos, const float* emb,
+                          const float* out_norm, const uint8_t* lm, const float* lm_f32, int lm_N, float* x,
+                          float* h, float* logits);
+
 /* Row-range parallel wrappers for the CPU baseline: every row's bits are those of
  * the single-threaded function. */
 void bpdq_o_dequant_q4k_mt(const uint8_t* q, float* out, int n_blocks, int nthreads);

@@ -64,6 +64,8 @@ _SIGS = {
     "bpdq_o_argmax": (I, [P, I]),
     "bpdq_o_gemv_f32_wave": (None, [P, P, P, I, I]),
     "bpdq_o_llama_step": (I, [I, P, P, P, P, I, P, P, P, P, I, P, P, P]),
+    "bpdq_o_llama_step_ext": (I, [P, P, P, P, P, I, P, P, P, P, I, P, P, P]),
+    "bpdq_o_rope_norm_freqs": (None, [P, I, I, I, F, I, P]),
 }
 
 _lib = None
@@ -328,6 +330,33 @@ def llama_step(fmt, layers, cfg, k_cache, v_cache, pos, emb, out_norm, lm, lm_f3
     return tok, x, h, logits
 
 
+class _OStepOpts(ctypes.Structure):
+    _fields_ = [("fmts", P), ("lm_fmt", I), ("rope_dim", I), ("rope_freqs", P), ("kv_f16", I)]
+
+
+def llama_step_ext(fmts, lm_fmt, layers, cfg, k_cache, v_cache, pos, emb, out_norm, lm, lm_f32, lm_N, rope_dim=None,
+                   rope_freqs=None, kv_f16=False):
+    """bpdq_o_llama_step_ext: fmts [n_layers][7] (q k v o gate up down), lm_fmt, rope_dim
+    (default head_dim), rope_freqs, binary16 caches (uint16 arrays) with kv_f16.
+    Returns (token, x, h, logits)."""
+    E = cfg["n_embd"]
+    arr = (_OLayer * max(1, len(layers)))()
+    for i, lw in enumerate(layers):
+        for n, _ in _OLayer._fields_:
+            setattr(arr[i], n, _addr(lw.get(n)))
+    c = _OCfg(*(cfg[n] for n, _ in _OCfg._fields_))
+    f = np.ascontiguousarray(np.array(fmts, np.int32).reshape(-1) if len(layers) else np.zeros(7, np.int32))
+    fr = None if rope_freqs is None else np.ascontiguousarray(rope_freqs, np.float32)
+    o = _OStepOpts(_p(f), lm_fmt, rope_dim or cfg["head_dim"], _addr(fr), 1 if kv_f16 else 0)
+    kp = (P * max(1, len(k_cache)))(*[_p(t) for t in k_cache])
+    vp = (P * max(1, len(v_cache)))(*[_p(t) for t in v_cache])
+    x, h, logits = np.empty(E, np.float32), np.empty(E, np.float32), np.empty(lm_N, np.float32)
+    tok = lib().bpdq_o_llama_step_ext(ctypes.addressof(o), ctypes.addressof(arr), ctypes.addressof(c), kp, vp, pos,
+                                      _p(emb), _p(out_norm), _addr(lm), _addr(lm_f32), lm_N, _p(x), _p(h),
+                                      _p(logits))
+    return tok, x, h, logits
+
+
 # The reference's own block, compiled from bench/bpd_cpu.c into oracle/_ref.
 class RefLlamaConfig(ctypes.Structure):      # bench/bpd_cpu.c:5556-5570
     _fields_ = [(n, I) for n in ("n_layers", "n_heads", "n_kv_heads", "head_dim", "embed_dim", "ffn_dim",
@@ -340,7 +369,8 @@ class RefLayerWeights(ctypes.Structure):     # bench/bpd_cpu.c:5585-5595
                                  "w_down")]
 
 
-def ref_llama_step(layers, cfg, k_cache, v_cache, pos, emb, out_norm, lm, lm_N, kind="avx"):
+def ref_llama_step(layers, cfg, k_cache, v_cache, pos, emb, out_norm, lm, lm_N, kind="avx", rope_dim=None,
+                   rope_freqs=None, kv_f16=False):
     """One token through the reference's bpd_llama_block_cpu per layer
     (bench/bpd_cpu.c:5611-5737), then the head of bpd_llama_forward_cpu
     (:5779-5792: bpd_rmsnorm_llama_cpu, bpd_qmatmul_q8_0_llamafile_cpu,
@@ -359,7 +389,8 @@ def ref_llama_step(layers, cfg, k_cache, v_cache, pos, emb, out_norm, lm, lm_N, 
         f.argtypes, f.restype = args, None
     E, H, HKV, D, F_ = (cfg[n] for n in ("n_embd", "n_head", "n_head_kv", "head_dim", "ff_dim"))
     c = RefLlamaConfig(cfg["n_layers"], H, HKV, D, E, F_, lm_N, cfg["max_seq"], cfg["eps"], cfg["rope_theta"],
-                       D, 0)
+                       rope_dim or D, 1 if kv_f16 else 0)
+    fr = None if rope_freqs is None else np.ascontiguousarray(rope_freqs, np.float32)
     x = np.array(emb, np.float32)
     big = max(E, F_, H * D)
     s1, s2, s3 = (np.zeros(big, np.float32) for _ in range(3))
@@ -368,7 +399,7 @@ def ref_llama_step(layers, cfg, k_cache, v_cache, pos, emb, out_norm, lm, lm_N, 
         w = RefLayerWeights(*(_addr(lw[n]) for n in ("attn_norm", "q", "k", "v", "o", "ffn_norm", "gate", "up",
                                                      "down")))
         R.bpd_llama_block_cpu(_p(x), ctypes.addressof(w), ctypes.addressof(c), _p(pos_ids), 1, pos, _p(k_cache[l]),
-                              _p(v_cache[l]), _p(s1), _p(s2), _p(s3), None)
+                              _p(v_cache[l]), _p(s1), _p(s2), _p(s3), _addr(fr))
     h = np.empty(E, np.float32)
     R.bpd_rmsnorm_llama_cpu(_p(x), _p(out_norm), _p(h), 1, E, cfg["eps"])
     logits = np.empty(lm_N, np.float32)

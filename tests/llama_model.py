@@ -20,22 +20,34 @@ def _norm_w(n, k):
     return (1.0 + 0.1 * synth.normal_f32(n, k)).astype(np.float32)
 
 
-def make(cfg, fmt=0, seed=1, bias=False, f32_head=False):
+def q6k(n, k, key, d_sigma=0.0001):
+    """Q6_K rows [n][k/256][210]: random quant and scale bytes, f16 d ~ |N(0, d_sigma)|."""
+    nb = n * (k // 256)
+    b = synth.random_bytes(nb * 210, key).reshape(nb, 210)
+    b[:, 208:210] = (np.abs(synth.normal_f32(nb, key ^ 0x5A5A)) * d_sigma).astype(np.float16).view(np.uint8) \
+        .reshape(nb, 2)
+    return b.reshape(-1)
+
+
+def make(cfg, fmt=0, seed=1, bias=False, f32_head=False, formats=None, lm_fmt=None):
+    """formats: per layer, {matrix: format} for matrices not in `fmt` (3/4: Q6_K)."""
     E, H, HKV, D, F = (cfg[n] for n in ("n_embd", "n_head", "n_head_kv", "head_dim", "ff_dim"))
     shapes = {"q": (H * D, E), "k": (HKV * D, E), "v": (HKV * D, E), "o": (E, H * D),
               "gate": (F, E), "up": (F, E), "down": (E, F)}
     s = 1000 * seed
 
-    def mat(n, k, key):
-        if fmt == 0:
+    def mat(n, k, key, f=fmt):
+        if f == 0:
             return synth.q8_0(n, k, key, d_sigma=0.002)
+        if f in (3, 4):
+            return q6k(n, k, key)
         return synth.q4k(n, k, key, d_sigma=0.0005, dmin_sigma=0.0003)
 
     layers = []
     for l in range(cfg["n_layers"]):
         lw = {"attn_norm": _norm_w(E, synth.key(s + l, 1)), "ffn_norm": _norm_w(E, synth.key(s + l, 2))}
         for i, m in enumerate(MATS):
-            lw[m] = mat(*shapes[m], synth.key(s + l, 10 + i))
+            lw[m] = mat(*shapes[m], synth.key(s + l, 10 + i), (formats[l] if formats else {}).get(m, fmt))
         if bias:
             lw["q_bias"] = 0.1 * synth.normal_f32(H * D, synth.key(s + l, 30))
             lw["k_bias"] = 0.1 * synth.normal_f32(HKV * D, synth.key(s + l, 31))
@@ -47,7 +59,7 @@ def make(cfg, fmt=0, seed=1, bias=False, f32_head=False):
         head["lm"] = None
         head["lm_f32"] = (0.05 * synth.normal_f32(vocab * E, synth.key(s + 99, 2))).astype(np.float32)
     else:
-        head["lm"] = mat(vocab, E, synth.key(s + 99, 3))
+        head["lm"] = mat(vocab, E, synth.key(s + 99, 3), fmt if lm_fmt is None else lm_fmt)
         head["lm_f32"] = None
     return layers, head
 
@@ -83,7 +95,8 @@ def to_device(cfg, layers, head, fmt, dev):
     return dl, t(head["out_norm"]), lm, lm_f32
 
 
-def caches(cfg):
+def caches(cfg, f16=False):
     n = cfg["max_seq"] * cfg["n_head_kv"] * cfg["head_dim"]
-    return ([np.zeros(n, np.float32) for _ in range(cfg["n_layers"])],
-            [np.zeros(n, np.float32) for _ in range(cfg["n_layers"])])
+    dt = np.uint16 if f16 else np.float32
+    return ([np.zeros(n, dt) for _ in range(cfg["n_layers"])],
+            [np.zeros(n, dt) for _ in range(cfg["n_layers"])])

@@ -284,3 +284,117 @@ def test_captured_step_survives_workspace_growth(dev):
         torch.cuda.synchronize()
         gpu.lib().bpd_gpu_set_stream(None)
         gpu.lib().bpd_gpu_workspace_release(s.cuda_stream)
+
+
+# ---------------------------------------------------------------- the extended step
+
+def _ext_model(cfg, layers, head, fmt, dev, **kw):
+    dl, on, lm, lmf = LM.to_device(cfg, layers, head, fmt, dev)
+    return llama.DecodeModel(cfg, dl, on, lm_head=lm, lm_f32=lmf, fmt=fmt, device=dev, **kw)
+
+
+def _cache_np(t, f16):
+    a = to_np(t)
+    return a.view(np.uint16) if f16 else a
+
+
+@pytest.mark.parametrize("f16", [True, False])
+@pytest.mark.parametrize("rope", ["full", "half_freqs"])
+@pytest.mark.parametrize("shape", [dict(), dict(H=8, HKV=8, D=32), dict(H=4, HKV=1, D=128, E=512, F=256)])
+def test_step_ext_equals_reference_block(dev, f16, rope, shape):
+    """bpd_llama_step_ext_gpu with padded Q8 weights against the reference's own
+    bpd_llama_block_cpu (oracle/_ref, AVX build) with cfg->kv_cache_f16, rope_dim
+    and rope_freqs: token, logits, residual, normed row and both caches, 6 steps."""
+    cfg = LM.config(**shape)
+    D = cfg["head_dim"]
+    rd = D // 2 if rope == "half_freqs" else None
+    fr = (1.0 + 5.0 * np.abs(LM.synth.normal_f32((rd or D) // 2, LM.synth.key(80, D)))).astype(np.float32) \
+        if rope == "half_freqs" else None
+    layers, head = LM.make(cfg, 0, seed=15)
+    m = _ext_model(cfg, layers, head, llama.W_Q8_PAD64, dev, rope_dim=rd, rope_freqs=fr, kv_cache_f16=f16)
+    kr, vr = LM.caches(cfg, f16)
+    for pos, e in enumerate(LM.embeddings(cfg, 6, seed=16)):
+        print(f"step ext {shape} f16={f16} {rope} position {pos}", flush=True)
+        want = O.ref_llama_step(layers, cfg, kr, vr, pos, e, head["out_norm"], head["lm"], cfg["vocab_size"],
+                                rope_dim=rd, rope_freqs=fr, kv_f16=f16)
+        if want is None:
+            pytest.skip("oracle/_ref not built")
+        tok = m.step(_d(e, dev), pos)
+        tk, x, h, logits = want
+        assert tok == tk, f"token at {pos}"
+        assert_bits_equal(to_np(m.buf_t["logits"]), logits, f"logits at {pos}")
+        assert_bits_equal(to_np(m.buf_t["x"]), x, f"x at {pos}")
+        assert_bits_equal(to_np(m.buf_t["h"]), h, f"h at {pos}")
+        for l in range(cfg["n_layers"]):
+            assert np.array_equal(_cache_np(m.k_cache[l], f16), kr[l]), f"K cache layer {l} at {pos}"
+            assert np.array_equal(_cache_np(m.v_cache[l], f16), vr[l]), f"V cache layer {l} at {pos}"
+
+
+@pytest.mark.parametrize("D,pos", [(64, 63), (64, 200), (128, 1100), (32, 3000)])
+def test_step_ext_long_context_f16(dev, D, pos):
+    """Binary16 caches at every attention regime (one-kernel up to 64 rows, scores +
+    P.V with 64- and 128-row chunks): rows 0..pos-1 hold the same random binary16
+    data on both sides, one step at pos against the reference block."""
+    H, HKV = 4, 2
+    cfg = LM.config(L=1, max_seq=max(2048, pos + 1), E=H * D, H=H, HKV=HKV, D=D)
+    layers, head = LM.make(cfg, 0, seed=17)
+    m = _ext_model(cfg, layers, head, llama.W_Q8_PAD64, dev, kv_cache_f16=True)
+    kr, vr = LM.caches(cfg, True)
+    row = HKV * D
+    for l in range(cfg["n_layers"]):
+        kr[l][:pos * row] = LM.synth.normal_f32(pos * row, LM.synth.key(81, l)).astype(np.float16).view(np.uint16)
+        vr[l][:pos * row] = LM.synth.normal_f32(pos * row, LM.synth.key(82, l)).astype(np.float16).view(np.uint16)
+        m.k_cache[l].copy_(_d(kr[l].view(np.int16), dev))
+        m.v_cache[l].copy_(_d(vr[l].view(np.int16), dev))
+    e = LM.embeddings(cfg, 1, seed=18)[0]
+    want = O.ref_llama_step(layers, cfg, kr, vr, pos, e, head["out_norm"], head["lm"], cfg["vocab_size"], kv_f16=True)
+    if want is None:
+        pytest.skip("oracle/_ref not built")
+    tok = m.step(_d(e, dev), pos)
+    assert tok == want[0]
+    assert_bits_equal(to_np(m.buf_t["logits"]), want[3], "logits")
+    assert np.array_equal(_cache_np(m.k_cache[0], True), kr[0]) and np.array_equal(_cache_np(m.v_cache[0], True), vr[0])
+
+
+Q4KM = {"v": llama.W_Q6K_GGUF, "down": llama.W_Q6K_GGUF}           # what llama.cpp's Q4_K_M keeps in Q6_K
+
+
+@pytest.mark.parametrize("case", ["q4k_m", "q4k_m_bpd", "q6k_gate", "wide", "f16_rope"])
+def test_step_mixed_formats(dev, case):
+    """Per-matrix formats: Q4_K with Q6_K attn_v / ffn_down and a Q6_K head (a
+    Q4_K_M file), both element maps, a Q6_K gate (gate/up as two GEMVs and
+    SwiGLU), n_embd = 8192 (no normed Q8_K row: Q6_K matrices quantize their
+    input), and with binary16 caches and rope_freqs; against the restatement
+    bpdq_o_llama_step_ext, 3 steps, bit for bit."""
+    base, lm_fmt, fm, kw, shape = llama.W_Q4K_GGUF, llama.W_Q6K_GGUF, dict(Q4KM), {}, dict()
+    if case == "q4k_m_bpd":
+        base, lm_fmt, fm = llama.W_Q4K, llama.W_Q6K, {"v": llama.W_Q6K, "down": llama.W_Q6K}
+    elif case == "q6k_gate":
+        fm = {"gate": llama.W_Q6K_GGUF, "o": llama.W_Q6K_GGUF}
+    elif case == "wide":
+        shape = dict(E=8192, H=64, HKV=8, D=128, F=512, L=1, vocab=300, max_seq=8)
+    elif case == "f16_rope":
+        kw = dict(kv_cache_f16=True, rope_dim=32,
+                  rope_freqs=(1.0 + np.arange(16, dtype=np.float32) / 3).astype(np.float32))
+    cfg = LM.config(**shape)
+    L = cfg["n_layers"]
+    formats = [dict(fm) for _ in range(L)]
+    if case == "q4k_m" and L > 1:
+        formats[1] = {}                      # Q4_K_M keeps Q6_K in some layers only
+    layers, head = LM.make(cfg, base, seed=19, formats=formats, lm_fmt=lm_fmt)
+    m = _ext_model(cfg, layers, head, base, dev, formats=formats, lm_format=lm_fmt, **kw)
+    f16 = kw.get("kv_cache_f16", False)
+    ko, vo = LM.caches(cfg, f16)
+    fmts = [[formats[l].get(n, base) for n in LM.MATS] for l in range(L)]
+    for pos, e in enumerate(LM.embeddings(cfg, 3, seed=20)):
+        print(f"mixed formats {case} position {pos}", flush=True)
+        want = O.llama_step_ext(fmts, lm_fmt, layers, cfg, ko, vo, pos, e, head["out_norm"], head["lm"], None,
+                                cfg["vocab_size"], rope_dim=kw.get("rope_dim"), rope_freqs=kw.get("rope_freqs"),
+                                kv_f16=f16)
+        tok = m.step(_d(e, dev), pos)
+        assert tok == want[0], f"token at {pos}"
+        assert_bits_equal(to_np(m.buf_t["logits"]), want[3], f"{case} logits at {pos}")
+        assert_bits_equal(to_np(m.buf_t["x"]), want[1], f"{case} x at {pos}")
+        for l in range(L):
+            assert np.array_equal(_cache_np(m.k_cache[l], f16), ko[l]), f"K cache layer {l}"
+            assert np.array_equal(_cache_np(m.v_cache[l], f16), vo[l]), f"V cache layer {l}"

@@ -89,6 +89,28 @@ def test_rope_equals_reference(D, pos):
 
 
 @NEEDS_REF
+@pytest.mark.parametrize("D,n_dims,pos,freqs", [(64, 32, 17, True), (128, 64, 1000, True), (128, 128, 4000, True),
+                                                 (64, 2, 31000, False), (256, 200, 77, True)])
+def test_rope_freqs_partial_equals_reference(D, n_dims, pos, freqs):
+    """bpdq_o_rope_norm_freqs against bpd_rope_norm_freqs_cpu with frequency factors
+    and n_dims < head_dim (the tail of each head passes through)."""
+    rope = _ref_fn("bpd_rope_norm_freqs_cpu", [P, P, P, P, I, I, I, I, F])
+    H = 3
+    t = LM.synth.normal_f32(H * D, LM.synth.key(5, D + pos + n_dims))
+    ff = (1.0 + 9.0 * np.abs(LM.synth.normal_f32(n_dims // 2, LM.synth.key(9, n_dims)))).astype(np.float32) \
+        if freqs else None
+    want = np.empty_like(t)
+    p = np.array([pos], np.int32)
+    rope(t.ctypes.data, want.ctypes.data, p.ctypes.data, None if ff is None else ff.ctypes.data, 1, H, D, n_dims,
+         500000.0)
+    got = t.copy()
+    O.lib().bpdq_o_rope_norm_freqs(got.ctypes.data, H, D, pos, 500000.0, n_dims,
+                                   None if ff is None else ff.ctypes.data)
+    assert_bits_equal(got, want, "rope with freqs")
+    assert np.array_equal(got.reshape(H, D)[:, n_dims:], t.reshape(H, D)[:, n_dims:])   # the tail unchanged
+
+
+@NEEDS_REF
 @pytest.mark.parametrize("H,HKV,D,S,pos", [(4, 2, 64, 16, 0), (4, 2, 64, 16, 9), (8, 8, 32, 40, 39),
                                            (6, 1, 128, 33, 20)])
 def test_attention_equals_reference(H, HKV, D, S, pos):
@@ -147,6 +169,52 @@ def test_step_equals_reference_block(shape):
         for l in range(cfg["n_layers"]):
             assert_bits_equal(ko[l], kr[l], "K cache")
             assert_bits_equal(vo[l], vr[l], "V cache")
+
+
+@NEEDS_REF
+@pytest.mark.parametrize("f16,rope", [(True, "full"), (True, "half_freqs"), (False, "half_freqs")])
+def test_step_ext_equals_reference_block(f16, rope):
+    """The restatement's binary16 caches, rope_dim and frequency factors
+    (bpdq_o_llama_step_ext, padded-Q8 weights) against the reference's own
+    bpd_llama_block_cpu with cfg->kv_cache_f16, rope_dim and rope_freqs."""
+    cfg = LM.config()
+    D = cfg["head_dim"]
+    rd = D // 2 if rope == "half_freqs" else None
+    fr = (1.0 + np.arange((rd or D) // 2, dtype=np.float32) / 2).astype(np.float32) if rd else None
+    layers, head = LM.make(cfg, 0, seed=2)
+    kr, vr = LM.caches(cfg, f16)
+    ko, vo = LM.caches(cfg, f16)
+    fm = [[0] * 7 for _ in range(cfg["n_layers"])]
+    for pos, e in enumerate(LM.embeddings(cfg, 5)):
+        r = O.ref_llama_step(layers, cfg, kr, vr, pos, e, head["out_norm"], head["lm"], cfg["vocab_size"],
+                             rope_dim=rd, rope_freqs=fr, kv_f16=f16)
+        o = O.llama_step_ext(fm, 0, layers, cfg, ko, vo, pos, e, head["out_norm"], head["lm"], None,
+                             cfg["vocab_size"], rope_dim=rd, rope_freqs=fr, kv_f16=f16)
+        assert r[0] == o[0]
+        for a, b, what in zip(o[1:], r[1:], ("x", "h", "logits")):
+            assert_bits_equal(a, b, f"{what} at position {pos}")
+        for l in range(cfg["n_layers"]):
+            assert np.array_equal(ko[l], kr[l]) and np.array_equal(vo[l], vr[l]), "caches"
+
+
+def test_step_ext_q6k_matrices_are_the_q6k_gemv():
+    """A K-quant step whose v and down are Q6_K equals, layer by layer, the plain
+    composition with bpdq_o_qmatmul_q6k_q8k of the Q8_K activation in those two
+    places: the restatement's format dispatch picks the Q6_K product."""
+    cfg = LM.config(L=1)
+    fm = {"v": 4, "down": 4}
+    layers, head = LM.make(cfg, 2, seed=21, formats=[fm], lm_fmt=4)
+    e = LM.embeddings(cfg, 1, seed=22)[0]
+    ko, vo = LM.caches(cfg)
+    tok, x, h, logits = O.llama_step_ext([[fm.get(n, 2) for n in LM.MATS]], 4, layers, cfg, ko, vo, 0, e,
+                                         head["out_norm"], head["lm"], None, cfg["vocab_size"])
+    lw = layers[0]
+    E, F, row = cfg["n_embd"], cfg["ff_dim"], cfg["n_head_kv"] * cfg["head_dim"]
+    hh = O.rmsnorm(e, lw["attn_norm"], cfg["eps"])
+    v = O.qmatmul_q6k_q8k(lw["v"], O.quant_q8_k(hh), row, E, order=1)
+    assert_bits_equal(vo[0][:row], v, "V row 0 = the Q6_K GEMV of the normed embedding")
+    assert_bits_equal(logits, O.qmatmul_q6k_q8k(head["lm"], O.quant_q8_k(h), cfg["vocab_size"], E, order=1),
+                      "Q6_K head")
 
 
 def test_gemv_f32_order_pins():
