@@ -265,3 +265,182 @@ class Forward:
                  ctypes.addressof(self.w), ctypes.addressof(self.cfg), pos.ctypes.data, int(kv_pos), self.k_cache,
                  self.v_cache, logits, toks)
         return logits[: n * self.cfg.vocab_size], toks[:n]
+
+
+# ---- a decode model straight from a GGUF file ----
+# The reference driver's loader (inference/llamatov_c_inference.py:114-182) reads
+# the {arch}.* metadata into ModelConfig and every blk.N.* tensor into
+# LayerWeights, dequantizing each tensor type on the host
+# (inference/llamatov_helpers.py:195-222) and re-quantizing to the padded Q8
+# layout.  Here the bytes go to the device unchanged and each matrix keeps its
+# own format: Q4_K and Q6_K run as themselves (GGUF element map), an all-Q8_0
+# model takes the padded Q8 layout.
+
+_GGUF_MATS = (("q", "attn_q"), ("k", "attn_k"), ("v", "attn_v"), ("o", "attn_output"),
+              ("gate", "ffn_gate"), ("up", "ffn_up"), ("down", "ffn_down"))
+
+
+def _gguf_format(t):
+    from . import gguf
+
+    if t.type == gguf.Q4_K:
+        return W_Q4K_GGUF
+    if t.type == gguf.Q6_K:
+        return W_Q6K_GGUF
+    if t.type == gguf.Q8_0:
+        return W_Q8_PAD64
+    raise gguf.GGUFError(f"{t.name}: type {t.type_name} is not a decode-step weight format (Q4_K, Q6_K, Q8_0)")
+
+
+def gguf_plan(g, max_seq=2048):
+    """Host-side reading of a parsed GGUF (gguf.GGUF) as a decode model: returns
+    dict(cfg, layers=[{matrix: (tensor, format), norms, biases}], head=(tensor, format or
+    None for fp32), embd=tensor, out_norm=tensor, rope_dim, rope_freqs=tensor or None).
+    Raises gguf.GGUFError for a missing tensor, a shape that does not match the
+    metadata, or formats the step cannot combine."""
+    from . import gguf
+
+    md = g.metadata
+    arch = md.get("general.architecture", "llama")
+
+    def meta(key, default=None):
+        v = md.get(f"{arch}.{key}", default)
+        if v is None:
+            raise gguf.GGUFError(f"metadata {arch}.{key} is missing")
+        return v
+
+    def need(name, dims=None):
+        if name not in g.by_name:
+            raise gguf.GGUFError(f"tensor {name} is missing")
+        t = g.by_name[name]
+        if dims is not None and tuple(t.dims) != tuple(dims):
+            raise gguf.GGUFError(f"tensor {name} has dims {t.dims}, expected {tuple(dims)}")
+        return t
+
+    L, E, H = int(meta("block_count")), int(meta("embedding_length")), int(meta("attention.head_count"))
+    HKV = int(md.get(f"{arch}.attention.head_count_kv", H))
+    if H <= 0 or E % H:
+        raise gguf.GGUFError(f"embedding_length {E} is not a multiple of head_count {H}")
+    D = E // H
+    F = int(need("blk.0.ffn_gate.weight").dims[1]) if L > 0 else int(md.get(f"{arch}.feed_forward_length", 0))
+    head_t = g.by_name.get("output.weight") or need("token_embd.weight")
+    V = int(md.get(f"{arch}.vocab_size", head_t.dims[1]))
+    cfg = dict(n_layers=L, n_embd=E, n_head=H, n_head_kv=HKV, head_dim=D, ff_dim=F, vocab_size=V, max_seq=max_seq,
+               eps=float(md.get(f"{arch}.attention.layer_norm_rms_epsilon", 1e-5)),
+               rope_theta=float(md.get(f"{arch}.rope.freq_base", 500000.0)))
+    rope_dim = int(md.get(f"{arch}.rope.dimension_count", D))
+    rdims = {"q": (E, H * D), "k": (E, HKV * D), "v": (E, HKV * D), "o": (H * D, E), "gate": (E, F), "up": (E, F),
+             "down": (F, E)}
+    layers = []
+    for l in range(L):
+        p = f"blk.{l}"
+        lw = {"attn_norm": need(f"{p}.attn_norm.weight", (E,)), "ffn_norm": need(f"{p}.ffn_norm.weight", (E,))}
+        for m, gname in _GGUF_MATS:
+            t = need(f"{p}.{gname}.weight", rdims[m])
+            lw[m] = (t, _gguf_format(t))
+        for b, gname, n in (("q_bias", "attn_q", H * D), ("k_bias", "attn_k", HKV * D), ("v_bias", "attn_v", HKV * D)):
+            key = f"{p}.{gname}.bias"
+            lw[b] = need(key, (n,)) if key in g.by_name else None
+        layers.append(lw)
+    need(head_t.name, (E, V))
+    head_fmt = None if head_t.type in (0, 1) else _gguf_format(head_t)
+    fmts = {f for lw in layers for m, _ in _GGUF_MATS for f in [lw[m][1]]} | ({head_fmt} - {None})
+    if W_Q8_PAD64 in fmts and len(fmts) > 1:
+        raise gguf.GGUFError("Q8_0 matrices cannot be combined with K-quant ones in one decode step")
+    rf = g.by_name.get("rope_freqs.weight")
+    if rf is not None and tuple(rf.dims) != (rope_dim // 2,):
+        raise gguf.GGUFError(f"rope_freqs.weight has dims {rf.dims}, expected ({rope_dim // 2},)")
+    return dict(cfg=cfg, layers=layers, head=(head_t, head_fmt), embd=need("token_embd.weight", (E, V)),
+                out_norm=need("output_norm.weight", (E,)), rope_dim=rope_dim, rope_freqs=rf)
+
+
+def _f32_tensor(g, t, device):
+    import numpy as np
+    import torch
+
+    raw = np.frombuffer(g.tensor_bytes(t.name), np.uint8)
+    if t.type == 0:
+        a = raw.view(np.float32)
+    elif t.type == 1:
+        a = raw.view(np.float16).astype(np.float32)
+    else:
+        raise ValueError(f"{t.name}: expected F32 or F16, found {t.type_name}")
+    return torch.from_numpy(a.copy()).to(device)
+
+
+def from_gguf(path, device, max_seq=2048, kv_cache_f16=False):
+    """A DecodeModel of the GGUF file at `path` (see gguf_plan), with
+    .embed(token_id) -> the token's fp32 embedding row on the device."""
+    import numpy as np
+
+    from . import formats as fm
+    from . import gguf
+
+    g = gguf.open_gguf(path)
+    plan = gguf_plan(g, max_seq)
+    cfg = plan["cfg"]
+    E = cfg["n_embd"]
+
+    def weight(t, f):
+        if f != W_Q8_PAD64:
+            return g.to_device(t.name, device)
+        import torch   # Q8_0 rows -> the padded layout of the padded-Q8 step
+
+        host = np.frombuffer(g.tensor_bytes(t.name), np.uint8)
+        return torch.from_numpy(fm.q8_0_rows_to_pad64(host, t.dims[1], t.dims[0])).to(device)
+
+    layers, formats = [], []
+    for lw in plan["layers"]:
+        d = {"attn_norm": _f32_tensor(g, lw["attn_norm"], device), "ffn_norm": _f32_tensor(g, lw["ffn_norm"], device)}
+        for m, _ in _GGUF_MATS:
+            d[m] = weight(*lw[m])
+        for b in ("q_bias", "k_bias", "v_bias"):
+            d[b] = None if lw[b] is None else _f32_tensor(g, lw[b], device)
+        layers.append(d)
+        formats.append({m: lw[m][1] for m, _ in _GGUF_MATS})
+    head_t, head_fmt = plan["head"]
+    base = formats[0]["q"] if formats else (head_fmt if head_fmt is not None else W_Q4K_GGUF)
+    lm = None if head_fmt is None else weight(head_t, head_fmt)
+    lm_f32 = _f32_tensor(g, head_t, device) if head_fmt is None else None
+    freqs = None
+    if plan["rope_freqs"] is not None:
+        freqs = np.frombuffer(g.tensor_bytes(plan["rope_freqs"].name), np.uint8).view(np.float32).copy()
+    m = DecodeModel(cfg, layers, _f32_tensor(g, plan["out_norm"], device), lm_head=lm, lm_f32=lm_f32,
+                    lm_N=head_t.dims[1], fmt=base, device=device, formats=formats,
+                    lm_format=head_fmt if head_fmt is not None else base, rope_dim=plan["rope_dim"],
+                    rope_freqs=freqs, kv_cache_f16=kv_cache_f16)
+    m.gguf, m.plan = g, plan
+    m._embd = g.to_device(plan["embd"].name, device)
+    return m
+
+
+def _embed(self, token):
+    """The fp32 embedding row of `token` on the device, as the GPU entry points compute
+    it: the Q8_0 lookup, or the GGUF-map dequant of the row's Q4_K / Q6_K blocks."""
+    import torch
+
+    from . import gguf
+
+    t = self.plan["embd"]
+    E = self.cfg.n_embd
+    if not 0 <= token < t.dims[1]:
+        raise ValueError(f"token {token} outside 0..{t.dims[1] - 1}")
+    gpu._use_torch_stream()
+    out = torch.empty(E, dtype=torch.float32, device=self._embd.device)
+    if t.type == gguf.Q8_0:
+        ids = torch.tensor([token], dtype=torch.int32, device=self._embd.device)
+        gpu.call("bpd_embed_lookup_q8_0_gpu", self._embd, ids, out, 1, E)
+    elif t.type in (gguf.Q4_K, gguf.Q6_K):
+        bpb = 144 if t.type == gguf.Q4_K else 210
+        nb = E // 256
+        row = self._embd[token * nb * bpb:(token + 1) * nb * bpb]   # 16-byte (Q4_K) / 2-byte (Q6_K) aligned
+        gpu.call("bpd_dequant_q4k_gguf_gpu" if t.type == gguf.Q4_K else "bpd_dequant_q6k_gguf_gpu", row, out, nb)
+    elif t.type == 0:
+        out.copy_(self._embd.view(torch.float32)[token * E:(token + 1) * E])
+    else:
+        raise ValueError(f"token_embd type {t.type_name} has no embedding lookup")
+    return out
+
+
+DecodeModel.from_gguf = staticmethod(from_gguf)
+DecodeModel.embed = _embed

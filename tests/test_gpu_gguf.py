@@ -42,3 +42,58 @@ def test_gguf_tensors_feed_the_abi(dev, tmp_path):
     host_e = np.frombuffer(g.tensor_bytes(e.name), np.uint8).copy()
     want = O.embed_lookup_q8_0(host_e, np.array([0, 7, V - 1, 7], np.int32), E)
     assert_bits_equal(to_np(out).ravel(), want.ravel(), "gguf Q8_0 embedding rows")
+
+
+# ---------------------------------------------------------------- whole models from GGUF
+
+@pytest.mark.parametrize("case", ["q4k_m", "tied", "q8_0"])
+def test_decode_model_from_gguf(dev, tmp_path, case):
+    """DecodeModel.from_gguf on a synthetic llama file: a Q4_K_M layout (Q6_K
+    attn_v / ffn_down in layer 0 and a Q6_K output.weight, rope_dim and
+    rope_freqs.weight), a tied head (token_embd as the head), and an all-Q8_0
+    file (padded layout, checked against the reference's own block).  Three
+    tokens stepped from their embeddings, bit for bit."""
+    import gguf_model as GM
+    import llama_model as LM
+    from bpd_substrate_amd import llama
+
+    cfg = LM.config(L=2, vocab=300, max_seq=16)
+    E, V = cfg["n_embd"], cfg["vocab_size"]
+    if case == "q8_0":
+        layers, head = LM.make(cfg, 0, seed=33)
+        embd = (LM.synth.q8_0(V, E, LM.synth.key(33, 5), d_sigma=0.02), gguf.Q8_0)
+        fm, base, lm_fmt, rd, fr = None, 0, 0, None, None
+    else:
+        fm = [{"v": 4, "down": 4}, {}]
+        base, lm_fmt = 2, (2 if case == "tied" else 4)
+        layers, head = LM.make(cfg, 2, seed=33, formats=fm, lm_fmt=lm_fmt)
+        embd = (LM.synth.q4k(V, E, LM.synth.key(33, 5)), gguf.Q4_K)
+        rd, fr = 32, np.linspace(1, 4, 16).astype(np.float32)
+        if case == "tied":
+            head["lm"] = embd[0]
+    path = str(tmp_path / f"{case}.gguf")
+    GM.write_model(path, cfg, layers, head, embd, base, fm, lm_fmt, rope_dim=rd, rope_freqs=fr,
+                   tied=case == "tied")
+    m = llama.DecodeModel.from_gguf(path, dev, max_seq=cfg["max_seq"])
+    ko, vo = LM.caches(cfg)
+    fmts = [[(fm[l] if fm else {}).get(n, base) for n in LM.MATS] for l in range(cfg["n_layers"])]
+    for pos, tok_in in enumerate([5, 17, 299]):
+        print(f"from_gguf {case} position {pos}", flush=True)
+        emb = m.embed(tok_in)
+        nb = E // (256 if embd[1] == gguf.Q4_K else 32)
+        bpb = 144 if embd[1] == gguf.Q4_K else 34
+        row = embd[0][tok_in * nb * bpb:(tok_in + 1) * nb * bpb]
+        want_emb = O.dequant_q4k_gguf(row) if embd[1] == gguf.Q4_K else O.dequant_q8_0(row)
+        assert_bits_equal(to_np(emb), want_emb, "embedding row")
+        if case == "q8_0":
+            want = O.ref_llama_step(layers, cfg, ko, vo, pos, want_emb, head["out_norm"], head["lm"], V)
+            if want is None:
+                pytest.skip("oracle/_ref not built")
+        else:
+            want = O.llama_step_ext(fmts, lm_fmt, layers, cfg, ko, vo, pos, want_emb, head["out_norm"], head["lm"],
+                                    None, V, rope_dim=rd, rope_freqs=fr)
+        tok = m.step(emb, pos)
+        assert tok == want[0], f"token at {pos}"
+        assert_bits_equal(to_np(m.buf_t["logits"]), want[3], f"{case} logits at {pos}")
+        for l in range(cfg["n_layers"]):
+            assert_bits_equal(to_np(m.k_cache[l]), ko[l], f"K cache layer {l}")
