@@ -32,7 +32,10 @@ static __constant__ uint64_t kExp2fTab[32] = {
     0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull,
 };
 
-__device__ __forceinline__ float expf_libm(float x) {
+// tab: the 32 entries of kExp2fTab, wherever the caller keeps them (a kernel
+// with many exps per lane copies them to LDS: a per-lane index into constant
+// memory is a vector load from the cache hierarchy for every call).
+__device__ __forceinline__ float expf_libm(float x, const uint64_t* tab = kExp2fTab) {
     constexpr double kN = 32.0;
     constexpr double kInvLn2N = 0x1.71547652b82fep+0 * kN;
     constexpr double kShift = 0x1.8p+52;
@@ -52,7 +55,7 @@ __device__ __forceinline__ float expf_libm(float x) {
     const uint64_t ki = (uint64_t)__double_as_longlong(kd);
     kd -= kShift;
     const double r = __builtin_fma(kInvLn2N, xd, -kd);
-    const uint64_t t = kExp2fTab[ki & 31] + (ki << 47);
+    const uint64_t t = tab[ki & 31] + (ki << 47);
     const double s = __longlong_as_double((long long)t);
     const double z = __builtin_fma(kC0, r, kC1);
     const double r2 = r * r;

@@ -184,8 +184,13 @@ struct RopeTab {
 // payload and sets the quiet bit).
 template <typename CT>
 struct Cache;
+// ldr loads 4 consecutive elements raw and cvt turns them into fp32, so a
+// prefetch can hold raw loads in flight and convert them only when used.
 template <>
 struct Cache<float> {
+    using Raw = float4;
+    static __device__ __forceinline__ Raw ldr(const float* p) { return *reinterpret_cast<const float4*>(p); }
+    static __device__ __forceinline__ float4 cvt(Raw r) { return r; }
     static __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
     static __device__ __forceinline__ void st(float* p, float v) { *p = v; }
     static __device__ __forceinline__ float rt(float v) { return v; }  // the value as read back
@@ -200,11 +205,13 @@ __device__ __forceinline__ float f16_to_f32_ref(uint32_t h) {
 }
 template <>
 struct Cache<uint16_t> {
-    static __device__ __forceinline__ float4 ld4(const uint16_t* p) {
-        const uint2 u = *reinterpret_cast<const uint2*>(p);
+    using Raw = uint2;
+    static __device__ __forceinline__ Raw ldr(const uint16_t* p) { return *reinterpret_cast<const uint2*>(p); }
+    static __device__ __forceinline__ float4 cvt(Raw u) {
         return make_float4(f16_to_f32_ref(u.x & 0xFFFFu), f16_to_f32_ref(u.x >> 16), f16_to_f32_ref(u.y & 0xFFFFu),
                            f16_to_f32_ref(u.y >> 16));
     }
+    static __device__ __forceinline__ float4 ld4(const uint16_t* p) { return cvt(ldr(p)); }
     static __device__ __forceinline__ void st(uint16_t* p, float v) { *p = (uint16_t)f32_to_f16_ref(v); }
     static __device__ __forceinline__ float rt(float v) { return f16_to_f32_ref(f32_to_f16_ref(v)); }
 };
@@ -287,62 +294,72 @@ __device__ __forceinline__ float dot_ptr(const float4* qs4, const float4* k, int
 }
 
 // Block-wide max of the scaled scores, as the reference's scan keeps it
-// (start at -1e38, take v when v > max): exact in any order.
+// (start at -1e38, take v when v > max): exact in any order.  No value is NaN
+// (a scan that starts below every score never takes one).  Inside a wave the
+// reduction runs on DPP moves (quad_perm, row_half_mirror, row_mirror: the
+// max of each 16-lane row) and four readlanes.
+__device__ __forceinline__ float max_gt(float a, float b) { return b > a ? b : a; }
 template <int NT>
 __device__ __forceinline__ float block_max(float m, float* red) {
-#pragma unroll
-    for (int mask = 32; mask >= 1; mask >>= 1) {
-        const float o = xor_f(m, mask);
-        m = o > m ? o : m;
-    }
+    m = max_gt(m, dpp_f<0xB1>(m));   // quad_perm [1,0,3,2]
+    m = max_gt(m, dpp_f<0x4E>(m));   // quad_perm [2,3,0,1]
+    m = max_gt(m, dpp_f<0x141>(m));  // row_half_mirror
+    m = max_gt(m, dpp_f<0x140>(m));  // row_mirror
+    m = max_gt(max_gt(readlane_f(m, 0), readlane_f(m, 16)), max_gt(readlane_f(m, 32), readlane_f(m, 48)));
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
     __syncthreads();
     float mx = red[0];
 #pragma unroll
-    for (int w = 1; w < NT / 64; w++) mx = red[w] > mx ? red[w] : mx;
+    for (int w = 1; w < NT / 64; w++) mx = max_gt(mx, red[w]);
     return mx;
 }
 
-// The softmax denominator in one lane: sum = sum + e_j for j = 0..n-1.  The
-// caller pads e with -0.0 up to n32 = a multiple of 32; sum + -0.0 == sum for
-// every sum (signed zeros and NaN included), so the padding changes no bit.
-// e is read from LDS in groups of 32 (8 float4, e 16-byte aligned), the next
-// group's reads issued before the current group's adds; sched_barrier keeps the
-// compiler from sinking those reads below the adds.
-__device__ __forceinline__ void sum_group(float& sum, const float4 (&v)[8]) {
+// Sequential fp32 sums read from LDS in groups of G float4, the next group's
+// reads issued before the current group's adds (sched_barrier keeps the
+// compiler from sinking them below the adds).  A wave's VALU issue is the
+// limit here: a dependent add from registers takes ~4.4 cycles and each LDS
+// read instruction ~10, so 16-float4 groups (one read per 4 adds, few waits)
+// run at ~8.3 cycles per element against ~10 for 8-float4 groups (measured,
+// one wave, 2,048 elements).
+template <int G>
+__device__ __forceinline__ void sum_group(float& sum, const float4 (&v)[G]) {
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
+    for (int i = 0; i < G; i++) {
         sum = sum + v[i].x;
         sum = sum + v[i].y;
         sum = sum + v[i].z;
         sum = sum + v[i].w;
     }
 }
-__device__ __forceinline__ void read_group(float4 (&v)[8], const float4* e4, int g) {
+template <int G>
+__device__ __forceinline__ void read_group(float4 (&v)[G], const float4* e4, int g) {
 #pragma unroll
-    for (int i = 0; i < 8; i++) v[i] = e4[g * 8 + i];
+    for (int i = 0; i < G; i++) v[i] = e4[g * G + i];
 }
-__device__ __forceinline__ float seq_sum(const float* __restrict__ e, int n32) {
+// The softmax denominator in one lane: sum = sum + e_j for j = 0..n-1.  The
+// caller pads e with -0.0 up to n64 = a multiple of 64; sum + -0.0 == sum for
+// every sum (signed zeros and NaN included), so the padding changes no bit.
+__device__ __forceinline__ float seq_sum(const float* __restrict__ e, int n64) {
     const float4* e4 = reinterpret_cast<const float4*>(e);
-    const int ng = n32 / 32;
+    const int ng = n64 / 64;
     float sum = 0.0f;
     if (ng == 0) return sum;
-    float4 a[8], b[8];
-    read_group(a, e4, 0);
+    float4 a[16], b[16];
+    read_group<16>(a, e4, 0);
     for (int g = 0; g < ng; g += 2) {
-        read_group(b, e4, g + 1 < ng ? g + 1 : g);  // past the end: a re-read, never added
+        read_group<16>(b, e4, g + 1 < ng ? g + 1 : g);  // past the end: a re-read, never added
         __builtin_amdgcn_sched_barrier(0);
-        sum_group(sum, a);
+        sum_group<16>(sum, a);
         __builtin_amdgcn_sched_barrier(0);
         if (g + 1 >= ng) break;
-        read_group(a, e4, g + 2 < ng ? g + 2 : g + 1);
+        read_group<16>(a, e4, g + 2 < ng ? g + 2 : g + 1);
         __builtin_amdgcn_sched_barrier(0);
-        sum_group(sum, b);
+        sum_group<16>(sum, b);
         __builtin_amdgcn_sched_barrier(0);
     }
     return sum;
 }
-__host__ __device__ constexpr int pad32(int n) { return (n + 31) & ~31; }
+__host__ __device__ constexpr int pad64(int n) { return (n + 63) & ~63; }
 
 // ----------------------------------------------------------------------------
 // Short contexts (pos < 64, head_dim DT <= 128): one workgroup per query head.
@@ -394,11 +411,11 @@ __global__ __launch_bounds__(256) void k_attn_small(AttnIn a, RopeTab tab, float
     const float mx = block_max<NT>(m, red);
     if (tid < n)
         e[tid] = expf_libm(e[tid] - mx);
-    else if (tid < pad32(n))
+    else if (tid < pad64(n))
         e[tid] = -0.0f;
     __syncthreads();
     if (tid == 0) {
-        const float sum = seq_sum(e, pad32(n));
+        const float sum = seq_sum(e, pad64(n));
         sh_inv = sum == 0.0f ? 0.0f : 1.0f / sum;
     }
     __syncthreads();
@@ -428,6 +445,34 @@ constexpr int kMaxGroup = 8;  // waves per workgroup; larger groups loop over th
 
 __host__ __device__ constexpr int score_pitch(int D) { return D + 4; }  // floats: rows 4 banks apart
 
+// Cache rows j0 .. j0+rows-1 (kv head at float offset ko of a row) into LDS at
+// kt[r * P4 + i], float4 i of row r.  Each thread issues up to 8 loads before
+// its first LDS write: a write right after each load would wait for that load,
+// and the rows would arrive one memory latency after another.  Every write
+// happens (past the end into `spare`, a float4 of LDS nobody reads): a write
+// under a branch lets the compiler sink its load into the branch, behind the
+// previous writes.
+template <typename CT>
+__device__ __forceinline__ void rows_to_lds(float4* kt, float4* spare, const CT* kc, int j0, int rows, int64_t row,
+                                            int64_t ko, int D4, int P4) {
+    constexpr int B = 8;
+    const int n = rows * D4;
+    for (int f0 = threadIdx.x; f0 < n; f0 += B * (int)blockDim.x) {
+        typename Cache<CT>::Raw t[B];
+#pragma unroll
+        for (int u = 0; u < B; u++) {
+            const int f = min(f0 + u * (int)blockDim.x, n - 1);  // past the end: a re-read, never stored
+            t[u] = Cache<CT>::ldr(kc + (int64_t)(j0 + f / D4) * row + ko + 4 * (f % D4));
+        }
+#pragma unroll
+        for (int u = 0; u < B; u++) {
+            const int f = f0 + u * (int)blockDim.x;
+            float4* dst = f < n ? kt + (f / D4) * P4 + f % D4 : spare;
+            *dst = Cache<CT>::cvt(t[u]);
+        }
+    }
+}
+
 template <int DT, typename CT>
 __global__ __launch_bounds__(64 * kMaxGroup) void k_attn_scores(AttnIn a, RopeTab tab, float* __restrict__ sc, int ld) {
     extern __shared__ float4 sm4[];
@@ -439,23 +484,30 @@ __global__ __launch_bounds__(64 * kMaxGroup) void k_attn_scores(AttnIn a, RopeTa
     float4* qs4 = kt + kScoreRows * P4;      // [G][D4] q of the group's heads
     float4* ks4 = qs4 + G * D4;              // the new k row
     float4* vs4 = ks4 + D4;                  // the new v row
+    float4* spare = vs4 + D4;                // writes past the tile
     const bool last = yb == nb - 1;          // the block holding row pos
     const int64_t ko = (int64_t)kvh * D;
-    // k rows j0 .. min(j0+63, pos-1): float4 i of row r at kt[r*P4 + i]
-    const int rows = min(kScoreRows, pos - j0);
-    const CT* kc = static_cast<const CT*>(a.kc);
-    for (int f = threadIdx.x; f < rows * D4; f += blockDim.x) {
-        const int r = f / D4, i = f % D4;
-        kt[r * P4 + i] = Cache<CT>::ld4(kc + (int64_t)(j0 + r) * a.row + ko + 4 * i);
-    }
-    // bias + RoPE of the group's q heads in one pass (their loads in flight together),
-    // then of the new k and v rows in the block holding row pos
+    // bias + RoPE of the group's q heads in one pass; the q loads of a thread's
+    // first pair go out before the k tile's, so both arrive in one memory round trip
     float* qs = reinterpret_cast<float*>(qs4);
     const int half = D / 2;
-    for (int pp = threadIdx.x; pp < G * half; pp += blockDim.x) {
+    const int pp0 = threadIdx.x;
+    float2 q0 = make_float2(0.0f, 0.0f);
+    if (pp0 < G * half) q0 = *reinterpret_cast<const float2*>(a.q + (int64_t)(kvh * G + pp0 / half) * D + 2 * (pp0 % half));
+    // k rows j0 .. min(j0+63, pos-1): float4 i of row r at kt[r*P4 + i]
+    const int rows = min(kScoreRows, pos - j0);
+    rows_to_lds<CT>(kt, spare, static_cast<const CT*>(a.kc), j0, rows, a.row, ko, D4, P4);
+    for (int pp = pp0; pp < G * half; pp += blockDim.x) {
         const int h = pp / half, pr = pp % half, i = 2 * pr;
         const int64_t qo = (int64_t)(kvh * G + h) * D + i;
-        float x0 = a.q[qo], x1 = a.q[qo + 1];
+        float x0, x1;
+        if (pp == pp0) {
+            x0 = q0.x;
+            x1 = q0.y;
+        } else {
+            x0 = a.q[qo];
+            x1 = a.q[qo + 1];
+        }
         if (a.bq != nullptr) {
             x0 = x0 + a.bq[qo];
             x1 = x1 + a.bq[qo + 1];
@@ -486,7 +538,7 @@ __global__ __launch_bounds__(64 * kMaxGroup) void k_attn_scores(AttnIn a, RopeTa
     }
 }
 
-// k_attn_pv, grid (heads * head_dim/32): softmax and P.V for 32 output columns
+// k_attn_pv, grid (heads * head_dim/32, query tokens): softmax and P.V for 32 output columns
 // d0..d0+31 of one head, in the reference's order.  The scores go to LDS; max,
 // exps and the weights w_j = e_j * inv are parallel; the softmax sum runs in
 // lane 0 and each output's chain acc = RN(acc + RN(v_jd * w_j)) in lane d - d0
@@ -510,9 +562,9 @@ struct PvShape {
     static constexpr int AHEAD = 512 / ROWS;        // chunks in flight: 64 KB per workgroup
 };
 // LDS: the ring, the padded scores and a few words
-static_assert(kMaxCtx % 32 == 0 && 2 * 32 * PvShape<64>::LD * 4 + kMaxCtx * 4 + 64 <= 160 * 1024,
+static_assert(kMaxCtx % 64 == 0 && 2 * 32 * PvShape<64>::LD * 4 + kMaxCtx * 4 + 256 + 64 <= 160 * 1024,
               "k_attn_pv<64> LDS");
-static_assert(kPvBigMax % 32 == 0 && 2 * 32 * PvShape<128>::LD * 4 + kPvBigMax * 4 + 64 <= 160 * 1024,
+static_assert(kPvBigMax % 64 == 0 && 2 * 32 * PvShape<128>::LD * 4 + kPvBigMax * 4 + 256 + 64 <= 160 * 1024,
               "k_attn_pv<128> LDS");
 
 template <typename CT>
@@ -527,9 +579,9 @@ struct PvPipe {
 // row c*ROWS + f/8, columns d0 + 4(f%8)..+3; rows past n repeat row n-1 (never
 // used, so every load stays in the cache rows already written).
 template <int ROWS, typename CT>
-__device__ __forceinline__ float4 pv_load(const PvPipe<CT>& p, int c, int k) {
+__device__ __forceinline__ typename Cache<CT>::Raw pv_load(const PvPipe<CT>& p, int c, int k) {
     const int f = p.tid + k * kPvProd, r = min(c * ROWS + f / 8, p.n - 1);
-    return Cache<CT>::ld4(p.vbase + (int64_t)r * p.row + 4 * (f % 8));
+    return Cache<CT>::ldr(p.vbase + (int64_t)r * p.row + 4 * (f % 8));
 }
 
 // Step c = c0 + U (pf slot U holds chunk c; U is a template argument so that pf
@@ -540,7 +592,8 @@ __device__ __forceinline__ float4 pv_load(const PvPipe<CT>& p, int c, int k) {
 // added chunk c.
 template <int U, int ROWS, typename CT>
 __device__ __forceinline__ void pv_chunk(const PvPipe<CT>& p, bool prod, bool chain,
-                                         float4 (&pf)[PvShape<ROWS>::AHEAD * PvShape<ROWS>::PER], float* ring,
+                                         typename Cache<CT>::Raw (&pf)[PvShape<ROWS>::AHEAD * PvShape<ROWS>::PER],
+                                         float* ring,
                                          int c0, float& acc) {
     constexpr int PER = PvShape<ROWS>::PER, LD = PvShape<ROWS>::LD;
     const int c = c0 + U;
@@ -550,7 +603,7 @@ __device__ __forceinline__ void pv_chunk(const PvPipe<CT>& p, bool prod, bool ch
 #pragma unroll
         for (int k = 0; k < PER; k++) {
             const int f = p.tid + k * kPvProd, rr = f / 8, r = c * ROWS + rr;
-            const float4 v = pf[U * PER + k];
+            const float4 v = Cache<CT>::cvt(pf[U * PER + k]);
             float* dst = slot + 4 * (f % 8) * LD + rr;
             if (r < p.n) {
                 const float w = p.e[r] * p.inv;  // the reference's scores[j] *= inv_sum
@@ -569,16 +622,18 @@ __device__ __forceinline__ void pv_chunk(const PvPipe<CT>& p, bool prod, bool ch
     }
     __syncthreads();
     if (chain) {
+        // the chunk's products as 16-float4 groups (sum_group), the second
+        // group's reads issued before the first group's adds
         const float4* col = reinterpret_cast<const float4*>(slot + p.tid * LD);
-        float4 t[ROWS / 4];
-#pragma unroll
-        for (int i = 0; i < ROWS / 4; i++) t[i] = col[i];
-#pragma unroll
-        for (int i = 0; i < ROWS / 4; i++) {
-            acc = acc + t[i].x;
-            acc = acc + t[i].y;
-            acc = acc + t[i].z;
-            acc = acc + t[i].w;
+        static_assert(ROWS == 64 || ROWS == 128, "one or two 16-float4 groups per chunk");
+        float4 a[16], b[16];
+        read_group<16>(a, col, 0);
+        if constexpr (ROWS == 128) read_group<16>(b, col, 1);
+        __builtin_amdgcn_sched_barrier(0);
+        sum_group<16>(acc, a);
+        if constexpr (ROWS == 128) {
+            __builtin_amdgcn_sched_barrier(0);
+            sum_group<16>(acc, b);
         }
     }
 }
@@ -589,8 +644,9 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(AttnIn a, const float* _
     constexpr int NT = kPvThreads, PER = PvShape<ROWS>::PER, AHEAD = PvShape<ROWS>::AHEAD;
     static_assert(AHEAD == 4 || AHEAD == 8, "one pv_chunk call per chunk in flight");
     extern __shared__ float4 e4dyn[];
-    float* e = reinterpret_cast<float*>(e4dyn);  // pad32(n) floats
+    float* e = reinterpret_cast<float*>(e4dyn);  // pad64(n) floats
     __shared__ __align__(16) float ring[2 * 32 * PvShape<ROWS>::LD];
+    __shared__ uint64_t etab[32];
     __shared__ float red[NT / 64];
     __shared__ float sh_inv;
     const int H = a.row / a.D * a.group, head = blockIdx.x % H, d0 = 32 * (blockIdx.x / H);
@@ -602,6 +658,7 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(AttnIn a, const float* _
     if (xq != nullptr) xq += (int64_t)tq * (H * a.D / 32) * kQ80Bytes;
     const int tid = threadIdx.x, kvh = head / a.group, n = a.pos + tq + 1, nch = (n + ROWS - 1) / ROWS;
     const bool prod = tid >= 64, chain = tid < 32;
+    if (tid < 32) etab[tid] = kExp2fTab[tid];  // published by block_max's barrier
     // the scores first, 8 loads in flight (loads complete in order, so anything
     // issued before them would be waited for too), then the first V chunks,
     // which stream in while the softmax runs
@@ -622,7 +679,7 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(AttnIn a, const float* _
     }
     PvPipe<CT> pp{static_cast<const CT*>(a.vc) + (int64_t)kvh * a.D + d0, a.row, n, nch, prod ? tid - 64 : tid, e,
                   0.0f};
-    float4 pf[AHEAD * PER];
+    typename Cache<CT>::Raw pf[AHEAD * PER];
     if (prod) {
 #pragma unroll
         for (int c = 0; c < AHEAD; c++)
@@ -630,10 +687,13 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(AttnIn a, const float* _
             for (int k = 0; k < PER; k++) pf[c * PER + k] = pv_load<ROWS, CT>(pp, c, k);
     }
     const float mx = block_max<NT>(m, red);
-    for (int j = tid; j < pad32(n); j += NT) e[j] = j < n ? expf_libm(e[j] - mx) : -0.0f;
+    // the exps with the table in LDS (a per-lane index into constant memory is a
+    // load from the cache hierarchy per call)
+    const int n64 = pad64(n);
+    for (int j = tid; j < n64; j += NT) e[j] = j < n ? expf_libm(e[j] - mx, etab) : -0.0f;
     __syncthreads();
     if (tid == 0) {
-        const float sum = seq_sum(e, pad32(n));
+        const float sum = seq_sum(e, n64);
         sh_inv = sum == 0.0f ? 0.0f : 1.0f / sum;
     }
     __syncthreads();
@@ -841,12 +901,10 @@ __global__ __launch_bounds__(64 * kMaxGroup) void k_mt_scores(const float* __res
     const int nw = blockDim.x >> 6, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     float4* kt = sm4;                    // [64][P4]
     float4* qs4 = kt + kScoreRows * P4;  // [G][D4]
+    float4* spare = qs4 + G * D4;        // writes past the tile
     const int rows = min(kScoreRows, qpos + 1 - j0);
     const int64_t ko = (int64_t)kvh * D;
-    for (int f = threadIdx.x; f < rows * D4; f += blockDim.x) {
-        const int r = f / D4, i = f % D4;
-        kt[r * P4 + i] = Cache<CT>::ld4(kc + (int64_t)(j0 + r) * row + ko + 4 * i);
-    }
+    rows_to_lds<CT>(kt, spare, kc, j0, rows, row, ko, D4, P4);
     const float4* qt = reinterpret_cast<const float4*>(q + ((int64_t)t * H + kvh * G) * D);
     for (int f = threadIdx.x; f < G * D4; f += blockDim.x) qs4[f] = qt[f];
     __syncthreads();
@@ -889,7 +947,7 @@ hipError_t lds_limits_for() {
                           reinterpret_cast<const void*>(&k_mt_scores<CT>)})
         if (err == hipSuccess)
             err = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                      (kScoreRows * score_pitch(kMaxHeadDim) + kMaxEmbd + 2 * kMaxHeadDim) * 4);
+                                      (kScoreRows * score_pitch(kMaxHeadDim) + kMaxEmbd + 2 * kMaxHeadDim + 4) * 4);
     return err;
 }
 
@@ -1151,18 +1209,18 @@ void attention(const StepCtx& c, const AttnIn& ai, int n_ctx) {
     }
     const int ld = c.cfg->max_seq, group = g.H / g.HKV;
     const dim3 gs(g.HKV * ((n_ctx + kScoreRows - 1) / kScoreRows)), ts(64 * (group < kMaxGroup ? group : kMaxGroup));
-    // k tile, q of the group's heads, new k and v rows: <= (64 * 260 + 16384 + 512) * 4 bytes
-    const size_t slds = ((size_t)kScoreRows * score_pitch(g.D) + (size_t)(group + 2) * g.D) * 4;
+    // k tile, q of the group's heads, new k and v rows, a spare float4: <= (64 * 260 + 16384 + 516) * 4 bytes
+    const size_t slds = ((size_t)kScoreRows * score_pitch(g.D) + (size_t)(group + 2) * g.D + 4) * 4;
     if (g.D == 128)
         hipLaunchKernelGGL((k_attn_scores<128, CT>), gs, ts, slds, c.s, ai, c.tab, c.scores, ld);
     else if (g.D == 64)
         hipLaunchKernelGGL((k_attn_scores<64, CT>), gs, ts, slds, c.s, ai, c.tab, c.scores, ld);
     else
         hipLaunchKernelGGL((k_attn_scores<0, CT>), gs, ts, slds, c.s, ai, c.tab, c.scores, ld);
-    // e holds pad32(n_ctx) <= kMaxCtx floats (kMaxCtx % 32 == 0); with 128-row
+    // e holds pad64(n_ctx) <= kMaxCtx floats (kMaxCtx % 64 == 0); with 128-row
     // chunks n_ctx <= kPvBigMax, so the ring and the scores fit in 160 KB
     const dim3 gp(g.H * (g.D / 32));
-    const size_t lds = (size_t)pad32(n_ctx) * 4;
+    const size_t lds = (size_t)pad64(n_ctx) * 4;
     if (n_ctx >= kPvBigMin && n_ctx <= kPvBigMax)
         hipLaunchKernelGGL((k_attn_pv<128, CT>), gp, dim3(kPvThreads), lds, c.s, ai, c.scores, ld, c.att, c.xq_a);
     else
@@ -1422,7 +1480,7 @@ template <typename CT>
 void mt_attention(const MtCtx& c, const float* q, const CT* kc, const CT* vc, float* out) {
     const BlockGeo& g = c.g;
     const int group = g.H / g.HKV;
-    const size_t slds = ((size_t)kScoreRows * score_pitch(g.D) + (size_t)group * g.D) * 4;
+    const size_t slds = ((size_t)kScoreRows * score_pitch(g.D) + (size_t)group * g.D + 4) * 4;
     const int row = g.HKV * g.D;
     for (int t0 = 0; t0 < c.T; t0 += c.tc) {
         const int tn = std::min(c.tc, c.T - t0), n_max = c.kv_pos + t0 + tn;
@@ -1433,7 +1491,7 @@ void mt_attention(const MtCtx& c, const float* q, const CT* kc, const CT* vc, fl
         const AttnIn ai{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, const_cast<CT*>(kc), const_cast<CT*>(vc),
                         group, row, g.D, c.kv_pos + t0, c.scale, c.g.rot};
         const dim3 gp(g.H * (g.D / 32), tn);
-        const size_t lds = (size_t)pad32(n_max) * 4;
+        const size_t lds = (size_t)pad64(n_max) * 4;
         float* o = out + (int64_t)t0 * g.H * g.D;
         uint8_t* xq = c.xq + (int64_t)t0 * (g.H * g.D / 32) * kQ80Bytes;
         if (n_max >= kPvBigMin && n_max <= kPvBigMax)
