@@ -232,6 +232,26 @@ __device__ __forceinline__ void q8_0_quad_store(float4 v, uint8_t* __restrict__ 
     if (g == 0) *reinterpret_cast<uint16_t*>(yb) = __builtin_bit_cast(uint16_t, (_Float16)d);
 }
 
+// RMSNorm's scale 1 / sqrtf(mean + eps) (bpd_rmsnorm_llama_cpu,
+// bench/bpd_cpu.c:4959-4986: a sequential binary64 sum of (double)x^2, mean =
+// (float)(sum / n)) from S, the binary64 sum of the same n squares in another
+// order.  Any order of n non-negative terms is within (n - 1) 2^-53 S of the
+// exact sum, as is the sequential one, so when (S - E)/n and (S + E)/n, E =
+// 4 n 2^-53 S, round to the same float, rounding monotonicity pins the
+// reference's mean to it; otherwise the sequential sum is redone over x.
+__device__ __forceinline__ float rms_scale(double S, const float* x, int n, float eps) {
+    const double dn = (double)n;
+    const double err = S * (4.0 * dn * 0x1p-53);
+    const float lo = (float)((S - err) / dn), hi = (float)((S + err) / dn);
+    float mean = lo;
+    if (!(lo == hi)) {
+        double q = 0.0;
+        for (int i = 0; i < n; i++) q += (double)x[i] * (double)x[i];
+        mean = (float)(q / dn);
+    }
+    return 1.0f / sqrtf(mean + eps);
+}
+
 // One Q8_K block {f32 d, i8 qs[256], i16 bsums[16]} from one whole wave, lane l
 // holding elements 4l..4l+3: amax over the block (exact in any order), d =
 // amax / 127, id = 127 / amax (0 when amax is 0), q = rint(x * id), bsums of

@@ -46,6 +46,29 @@ void launch_qmatmul_q4k_fused_swiglu(const uint8_t* w_gate, const uint8_t* w_up,
 void launch_qmatmul_q4k_swiglu_q8k(const uint8_t* w_gate, const uint8_t* w_up, float* y, int M, const uint8_t* xq,
                                    int K, int order, hipStream_t s);
 
+// The decode step's RMSNorm folded into its GEMVs (n_embd = 4096, ff 4096 or
+// 14336, Q4_K weights 16-byte aligned; norm_fusion_fits): the producer (O,
+// down) adds its rows into the residual row x and writes one binary64 partial
+// sum of squares per workgroup; the consumer turns them into the norm's scale:
+// the Q/K/V GEMV quantizes h = (x * scale) * w itself, the gate/up GEMV reads
+// the Q8_K of h that one small kernel writes (a 14336-row GEMV repeating the
+// norm in each of its 3584 workgroups measured 19.7 us against 11.0 + 4.6).
+struct NormIn {
+    const float* x;
+    const float* w;
+    const double* part;
+    int npart;
+    float eps;
+};
+struct ResOut {
+    float* x;
+    double* part;
+};
+bool norm_fusion_fits(int n_embd, int ff);
+void launch_q4k_norm_multi(const uint8_t* const* w, float* const* y, const int* M, int n, const NormIn& nin,
+                           int order, hipStream_t s);
+int launch_q4k_res(const uint8_t* w, int M, const float* x, int K, const ResOut& ro, int order, hipStream_t s);
+
 void launch_dequant_q6k(const uint8_t* q, float* out, int n_blocks, int order, hipStream_t s);
 void launch_qmatmul_q6k_q8k(const uint8_t* w, const uint8_t* xq, float* y, int M, int K, int order, hipStream_t s);
 

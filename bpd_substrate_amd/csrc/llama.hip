@@ -122,17 +122,7 @@ __global__ __launch_bounds__(NT) void k_residual_rmsnorm(const float* x_in, cons
     if (tid == 0) {
         double S = 0.0;
         for (int i = 0; i < NT / 64; i++) S += wsum[i];
-        const double dn = (double)n;
-        const double err = S * (4.0 * dn * 0x1p-53);
-        const float lo = (float)((S - err) / dn), hi = (float)((S + err) / dn);
-        float mean = lo;
-        if (!(lo == hi)) {
-            const float* xs = reinterpret_cast<const float*>(xs4);
-            double q = 0.0;
-            for (int i = 0; i < n; i++) q += (double)xs[i] * (double)xs[i];
-            mean = (float)(q / dn);
-        }
-        sh_scale = 1.0f / sqrtf(mean + eps);
+        sh_scale = rms_scale(S, reinterpret_cast<const float*>(xs4), n, eps);
     }
     __syncthreads();
     const float scale = sh_scale;
@@ -149,6 +139,29 @@ __global__ __launch_bounds__(NT) void k_residual_rmsnorm(const float* x_in, cons
             if (xk != nullptr) q8k_wave_store(y, xk + (int64_t)(c >> 6) * kQ8KBytes, c & 63);
         }
     }
+}
+
+// The FFN norm of a step whose O GEMV added its rows into the residual row x
+// and left binary64 partial sums of squares (launch_q4k_res): wave b quantizes
+// block b of h = (x * scale) * w to Q8_K for the gate/up GEMV, the scale from
+// the partials (rms_scale), so xk holds k_residual_rmsnorm's bytes.
+constexpr int kNormParts = 16;  // partials per lane held in registers (producers write <= 1024)
+__global__ __launch_bounds__(64) void k_norm_q8k(NormIn nin, uint8_t* __restrict__ xk) {
+    const int lane = threadIdx.x, c = blockIdx.x * 64 + lane;
+    double pp[kNormParts];
+#pragma unroll
+    for (int k = 0; k < kNormParts; k++) pp[k] = lane + 64 * k < nin.npart ? nin.part[lane + 64 * k] : 0.0;
+    const float4 x = reinterpret_cast<const float4*>(nin.x)[c];
+    const float4 w = reinterpret_cast<const float4*>(nin.w)[c];
+    double s = 0.0;
+#pragma unroll
+    for (int k = 0; k < kNormParts; k++) s += pp[k];
+    for (int i = lane + 64 * kNormParts; i < nin.npart; i += 64) s += nin.part[i];
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m, 64);  // the same S in every lane
+    const float scale = rms_scale(s, nin.x, gridDim.x * 256, nin.eps);
+    const float4 y = make_float4((x.x * scale) * w.x, (x.y * scale) * w.y, (x.z * scale) * w.z, (x.w * scale) * w.w);
+    q8k_wave_store(y, xk + (int64_t)blockIdx.x * kQ8KBytes, lane);
 }
 
 // ----------------------------------------------------------------------------
@@ -1191,7 +1204,24 @@ struct StepCtx {
     float attn_scale;   // 1 / sqrtf(head_dim), as the reference computes it
     uint8_t *xq_e, *xq_a, *xq_f;  // Q8_0 activations (padded Q8 weights only, else NULL)
     uint8_t* xk;  // Q8_K of the normed row (K-quant weights, n_embd <= 4096, else NULL)
+    double *part_o, *part_d;  // partial sums of squares of the O and down epilogues (norm folding)
+    bool fold;                // RMSNorms folded into the GEMVs (see fold_norms)
 };
+
+// Whether every layer's norms can fold into its GEMVs (launch_q4k_res /
+// launch_q4k_norm_*): n_embd 4096, ff_dim 4096 or 14336, all seven matrices Q4_K
+// of one element map, 16-byte aligned, n_head * head_dim = n_embd.  Measured at cfg3: the two norm launches
+// took 9.1 us of a 46 us layer at position 0.
+bool fold_norms(const StepOpts& o, const Geometry& g, const LayerWeights* layers) {
+    if (!norm_fusion_fits(g.E, g.F) || g.H * g.D != g.E || !is_q4k(o.base_format)) return false;
+    for (int l = 0; l < g.L; l++) {
+        const void* m[7] = {layers[l].q, layers[l].k, layers[l].v, layers[l].o, layers[l].gate, layers[l].up,
+                            layers[l].down};
+        for (int i = 0; i < 7; i++)
+            if (o.fmt(l, i) != o.base_format || (reinterpret_cast<uintptr_t>(m[i]) & 15) != 0) return false;
+    }
+    return true;
+}
 
 // Attention over n_ctx = pos + 1 rows: one kernel while the context is short
 // and head_dim is 32, 64 or 128, else scores and softmax/P.V as two kernels.
@@ -1236,16 +1266,25 @@ void run_layers(const StepCtx& c, const Gemv& gemv, const LayerWeights* layers, 
     const Geometry& g = c.g;
     const StepOpts& o = *c.o;
     const int row = g.HKV * g.D, n_ctx = c.pos + 1;
+    int npart_d = 0;  // partials of the previous layer's down epilogue
     for (int l = 0; l < g.L; l++) {
         const LayerWeights& w = layers[l];
         int f[7];
         for (int m = 0; m < 7; m++) f[m] = o.fmt(l, m);
-        launch_norm(xin, add, c.x, static_cast<const float*>(w.attn_norm), c.h, c.xq_e, g.E, c.cfg->eps, c.s, c.xk);
-        xin = c.x;
         const void* wqkv[3] = {w.q, w.k, w.v};
         float* yqkv[3] = {c.qb, c.kb, c.vb};
         const int nqkv[3] = {w.q_N, w.k_N, w.v_N};
-        gemv.run(3, wqkv, f, yqkv, nqkv, c.h, c.xq_e, c.xk, g.E);
+        if (c.fold && l > 0) {  // the norm from the residual row and the down epilogue's partials
+            const uint8_t* wl[3] = {static_cast<const uint8_t*>(w.q), static_cast<const uint8_t*>(w.k),
+                                    static_cast<const uint8_t*>(w.v)};
+            const NormIn nin{c.x, static_cast<const float*>(w.attn_norm), c.part_d, npart_d, c.cfg->eps};
+            launch_q4k_norm_multi(wl, yqkv, nqkv, 3, nin, format_order(f[0]), c.s);
+        } else {
+            launch_norm(xin, add, c.x, static_cast<const float*>(w.attn_norm), c.h, c.xq_e, g.E, c.cfg->eps, c.s,
+                        c.xk);
+            gemv.run(3, wqkv, f, yqkv, nqkv, c.h, c.xq_e, c.xk, g.E);
+        }
+        xin = c.x;
         const AttnIn ai{c.qb, c.kb, c.vb,
                         static_cast<const float*>(w.q_bias), static_cast<const float*>(w.k_bias),
                         static_cast<const float*>(w.v_bias), c.kv->k_cache[l], c.kv->v_cache[l], g.H / g.HKV, row,
@@ -1254,6 +1293,19 @@ void run_layers(const StepCtx& c, const Gemv& gemv, const LayerWeights* layers, 
             attention<uint16_t>(c, ai, n_ctx);
         else
             attention<float>(c, ai, n_ctx);
+        if (c.fold) {  // O into the residual row, gate/up with the norm, down into the residual row
+            const int ord = format_order(f[0]);
+            const int npart_o = launch_q4k_res(static_cast<const uint8_t*>(w.o), w.o_N, c.att, g.H * g.D,
+                                               ResOut{c.x, c.part_o}, ord, c.s);
+            const NormIn nin{c.x, static_cast<const float*>(w.ffn_norm), c.part_o, npart_o, c.cfg->eps};
+            hipLaunchKernelGGL(k_norm_q8k, dim3(g.E / 256), dim3(64), 0, c.s, nin, c.xk);
+            launch_qmatmul_q4k_swiglu_q8k(static_cast<const uint8_t*>(w.gate), static_cast<const uint8_t*>(w.up),
+                                          c.gate, g.F, c.xk, g.E, ord, c.s);
+            npart_d = launch_q4k_res(static_cast<const uint8_t*>(w.down), w.down_N, c.gate, g.F, ResOut{c.x, c.part_d},
+                                     ord, c.s);
+            add = nullptr;
+            continue;
+        }
         const void* wo[1] = {w.o};
         float* yo[1] = {c.ffn};
         const int no[1] = {w.o_N};
@@ -1299,10 +1351,14 @@ bool enqueue_step(const StepOpts& o, const LayerWeights* layers, const ModelConf
     // Q/K/V and gate/up GEMVs (measured 1,515 -> 1,500 us/token at cfg3)
     const size_t xk_bytes = !q8 && g.E <= 4096 ? ((size_t)(g.E / 256) * kQ8KBytes + 255) & ~(size_t)255 : 0;
     const size_t q8k_end = ((front + q8k + 255) & ~(size_t)255) + xk_bytes;
-    const size_t sc_bytes = (size_t)g.H * cfg->max_seq * 4;
-    // the quantized activations (Q8_0 rows, or Q8_K staging for the K-quant GEMVs)
-    // and the attention scores, in the stream's workspace
-    const WsLease lease = workspace(q8k_end + sc_bytes, abi_stream(), fn);
+    const size_t sc_bytes = ((size_t)g.H * cfg->max_seq * 4 + 255) & ~(size_t)255;
+    // two sets of per-workgroup partials (a producer workgroup has at least 4
+    // waves of at least one row of n_embd)
+    c.fold = xk_bytes != 0 && fold_norms(o, g, layers);
+    const size_t part_bytes = c.fold ? 2 * ((((size_t)g.E / 4 + 1) * 8 + 255) & ~(size_t)255) : 0;
+    // the quantized activations (Q8_0 rows, or Q8_K staging for the K-quant GEMVs),
+    // the attention scores and the partials, in the stream's workspace
+    const WsLease lease = workspace(q8k_end + sc_bytes + part_bytes, abi_stream(), fn);
     uint8_t* ws = static_cast<uint8_t*>(lease.ptr);
     if (ws == nullptr) return false;
     const Gemv gemv{ws + front, abi_stream()};
@@ -1326,6 +1382,10 @@ bool enqueue_step(const StepOpts& o, const LayerWeights* layers, const ModelConf
     c.xq_a = q8 ? ws + q8e : nullptr;
     c.xq_f = q8 ? ws + 2 * q8e : nullptr;
     c.xk = xk_bytes ? ws + q8k_end - xk_bytes : nullptr;
+    if (c.fold) {
+        c.part_o = reinterpret_cast<double*>(ws + q8k_end + sc_bytes);
+        c.part_d = reinterpret_cast<double*>(ws + q8k_end + sc_bytes + part_bytes / 2);
+    }
     if (g.L > 0) rope_table(c.tab, pos, o.rope_dim, cfg->rope_theta, o.rope_freqs);
     float* logits = static_cast<float*>(buf->logits);
 

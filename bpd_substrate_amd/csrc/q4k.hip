@@ -1474,4 +1474,212 @@ void launch_qmatmul_q4k_fused_multi(const uint8_t* const* w, float* const* y, co
     }
 }
 
+
+// ----------------------------------------------------------------------------
+// RMSNorm folded into the decode step's GEMVs (n_embd = 4096).  The reference
+// runs x = x + y, then h = rmsnorm(x) * w (bpd_add_f32_cpu, bench/bpd_cpu.c:5466;
+// bpd_rmsnorm_llama_cpu, :4959-4986) between the O / down projections and the
+// Q/K/V / gate-up projections.  Here:
+//   - the producer GEMV (O, down) adds each of its rows into the residual row,
+//     x[r] = x[r] + y_r, and each workgroup stores the binary64 sum of
+//     (double)x[r]^2 over its rows, in row order, as one partial;
+//   - the consumer GEMV (Q/K/V, gate/up) sums the partials in a fixed order (so
+//     every workgroup gets the same S), and takes mean = (float)(S / n) when
+//     (S - E)/n and (S + E)/n, E = 4 n 2^-53 S, round to the same float: any
+//     summation order of n non-negative terms is within (n - 1) 2^-53 S of the
+//     exact sum, so rounding monotonicity pins the reference's sequential mean
+//     to that float; otherwise thread 0 redoes the reference's sequential sum
+//     over the row.  Then scale = 1 / sqrtf(mean + eps), h = (x * scale) * w,
+//     quantized to Q8_K in LDS exactly as the fused kernels quantize x.
+// The arithmetic is k_residual_rmsnorm's, so the Q8_K bytes and every output
+// are the same bits as the separate norm launch followed by the GEMV.
+// ----------------------------------------------------------------------------
+
+// A thread's first kPartRegs strided partials, loaded before the weight span so
+// that waiting for them does not wait for the span (vector loads complete in
+// issue order).  The producers write at most 1024 partials (n_embd 4096 rows).
+constexpr int kPartRegs = 4;
+template <int WPB>
+__device__ __forceinline__ void part_load(double (&pp)[kPartRegs], const NormIn& nin) {
+#pragma unroll
+    for (int k = 0; k < kPartRegs; k++) {
+        const int i = threadIdx.x + k * 64 * WPB;
+        pp[k] = i < nin.npart ? nin.part[i] : 0.0;
+    }
+}
+
+// Binary64 sum of the partials (a thread's strided terms in order, then the
+// wave's lanes by xor steps, then the waves in order), the mean and the scale.
+// Any order serves: the mean is either pinned by the error bound or recomputed
+// sequentially.  Every thread returns the scale.  red: LDS, one double per wave + 1.
+template <int WPB>
+__device__ __forceinline__ float norm_scale(const double (&pp)[kPartRegs], const NormIn& nin, int n, double* red) {
+    const int tid = threadIdx.x;
+    double s = 0.0;
+#pragma unroll
+    for (int k = 0; k < kPartRegs; k++) s += pp[k];
+    for (int i = tid + kPartRegs * 64 * WPB; i < nin.npart; i += 64 * WPB) s += nin.part[i];
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m, 64);
+    if ((tid & 63) == 0) red[tid >> 6] = s;
+    __syncthreads();
+    if (tid == 0) {
+        double S = 0.0;
+        for (int i = 0; i < WPB; i++) S += red[i];
+        reinterpret_cast<float*>(red)[2 * WPB] = rms_scale(S, nin.x, n, nin.eps);
+    }
+    __syncthreads();
+    return reinterpret_cast<const float*>(red)[2 * WPB];
+}
+
+// The norm weight of x32_load's elements.
+template <int WPB, int IT>
+__device__ __forceinline__ void w32_load(XPre<IT>& P, const float* __restrict__ w, int nb) {
+    x32_load<WPB, IT>(P, w, nb);
+}
+
+// h = (x * scale) * w in place of x.
+template <int IT>
+__device__ __forceinline__ void x32_normalize(XPre<IT>& P, const XPre<IT>& W, float scale) {
+#pragma unroll
+    for (int it = 0; it < IT; it++)
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const float4 x = P.v[it][k], w = W.v[it][k];
+            P.v[it][k] = make_float4((x.x * scale) * w.x, (x.y * scale) * w.y, (x.z * scale) * w.z,
+                                     (x.w * scale) * w.w);
+        }
+}
+
+// The producer's epilogue: lane 0 of each wave adds its rows into x and squares
+// them; the workgroup's partial goes to part[blockIdx.x].  Every wave calls it
+// (has = false: no rows).  red: LDS, one double per wave.
+template <int R, int WPB>
+__device__ __forceinline__ void res_epilogue(const ResOut& ro, const float (&out)[R], int row0, int M, bool has,
+                                             double* red) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    double sq = 0.0;
+    if (lane == 0 && has) {
+#pragma unroll
+        for (int r = 0; r < R; r++)
+            if (row0 + r < M) {
+                const float xn = ro.x[row0 + r] + out[r];
+                ro.x[row0 + r] = xn;
+                sq += (double)xn * (double)xn;
+            }
+    }
+    if (lane == 0) red[wave] = sq;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double p = 0.0;
+        for (int i = 0; i < WPB; i++) p += red[i];
+        ro.part[blockIdx.x] = p;
+    }
+}
+
+// Q/K/V (MultiArgs over up to 4 matrices) with the norm in the quantization
+// prologue; k_q4k_fused_span otherwise.
+template <int ORDER, int R, int WPB>
+__global__ __launch_bounds__(64 * WPB) void k_q4k_norm_span(MultiArgs a, NormIn nin) {
+    constexpr int NB = 16, IT = (NB + 4 * WPB - 1) / (4 * WPB);
+    using S = Span<NB, R, true>;
+    __shared__ __align__(16) uint8_t slots[WPB][S::kSlot];
+    __shared__ __align__(16) uint8_t xl[NB * kXS];
+    __shared__ double red[WPB + 1];
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    int i, row0;
+    const bool has = wave_rows(a, blockIdx.x * WPB + wave, R, i, row0);
+    XPre<IT> P, Wn;
+    double pp[kPartRegs];
+    part_load<WPB>(pp, nin);
+    x32_load<WPB, IT>(P, nin.x, NB);
+    w32_load<WPB, IT>(Wn, nin.w, NB);
+    const uint8_t* seg[1] = {a.w[i] + (int64_t)row0 * (NB * kQ4KBytes)};
+    const int np[1] = {min(R, a.M[i] - row0) * NB * 9};
+    u32x4v v[S::kLoads];
+    span_issue<S>(v, seg, np);
+    __builtin_amdgcn_sched_barrier(0);
+    const float scale = norm_scale<WPB>(pp, nin, NB * 256, red);
+    x32_normalize<IT>(P, Wn, scale);
+    x32_quantize<WPB, IT>(P, xl, NB);
+    __syncthreads();
+    if (!has) return;
+    XOps unused[S::kNT][2];
+    float out[R];
+    span_rows<ORDER, NB, R, true, true>(v, slots[wave], xl, unused, out);
+#pragma unroll
+    for (int r = 0; r < R; r++)
+        if ((threadIdx.x & 63) == 0 && row0 + r < a.M[i]) a.y[i][row0 + r] = out[r];
+}
+
+// O and down: k_q4k_fused_span's rows with the residual epilogue in place of
+// the y stores.
+template <int ORDER, int NB, int R, int WPB, bool PB>
+__global__ __launch_bounds__(64 * WPB) void k_q4k_res_span(const uint8_t* __restrict__ w, int M,
+                                                          const float* __restrict__ x, ResOut ro) {
+    using S = Span<NB, R, true, PB>;
+    constexpr int IT = (NB + 4 * WPB - 1) / (4 * WPB);
+    __shared__ __align__(16) uint8_t slots[WPB][S::kSlot];
+    __shared__ __align__(16) uint8_t xl[NB * kXS];
+    __shared__ double red[WPB];
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int row0w = (blockIdx.x * WPB + wave) * R;
+    const bool has = row0w < M;
+    const int row0 = has ? row0w : 0;
+    XPre<IT> P;
+    x32_load<WPB, IT>(P, x, NB);
+    const uint8_t* seg[1] = {w + (int64_t)row0 * (NB * kQ4KBytes)};
+    const int np[1] = {min(R, M - row0) * NB * 9};
+    u32x4v v[S::kLoads];
+    span_issue<S>(v, seg, np);
+    __builtin_amdgcn_sched_barrier(0);
+    x32_quantize<WPB, IT>(P, xl, NB);
+    __syncthreads();
+    float out[R];
+    if (has) {
+        XOps unused[S::kNT][2];
+        span_rows<ORDER, NB, R, true, true, PB>(v, slots[wave], xl, unused, out);
+    }
+    res_epilogue<R, WPB>(ro, out, row0, M, has, red);
+}
+
+// Launch shapes: Q/K/V and O as launch_fused_span picks them (4 waves, R rows per
+// wave), gate/up as launch_swiglu_span (4 waves), down (K = 14336) as
+// launch_qmatmul_q4k_fused_multi (8 waves, one row per wave through a pass buffer).
+bool norm_fusion_fits(int n_embd, int ff) { return n_embd == 4096 && (ff == 4096 || ff == 14336); }
+
+template <int ORDER, int R>
+static void launch_norm_span(const MultiArgs& a, const NormIn& nin, hipStream_t s) {
+    constexpr int WPB = 4;
+    hipLaunchKernelGGL((k_q4k_norm_span<ORDER, R, WPB>), dim3((a.first[kMulti] + WPB - 1) / WPB), dim3(64 * WPB), 0,
+                       s, a, nin);
+}
+
+void launch_q4k_norm_multi(const uint8_t* const* w, float* const* y, const int* M, int n, const NormIn& nin,
+                           int order, hipStream_t s) {
+    const int R = span_rows_per_wave(total_rows(M, n));
+    const MultiArgs a = make_multi_args(w, y, M, n, R);
+    if (a.first[kMulti] == 0) return;
+    if (order == 0) {
+        if (R == 1) launch_norm_span<0, 1>(a, nin, s); else launch_norm_span<0, 2>(a, nin, s);
+    } else {
+        if (R == 1) launch_norm_span<1, 1>(a, nin, s); else launch_norm_span<1, 2>(a, nin, s);
+    }
+}
+
+template <int ORDER, int NB, int R, int WPB, bool PB>
+static int launch_res(const uint8_t* w, int M, const float* x, const ResOut& ro, hipStream_t s) {
+    const int g = ((M + R - 1) / R + WPB - 1) / WPB;
+    hipLaunchKernelGGL((k_q4k_res_span<ORDER, NB, R, WPB, PB>), dim3(g), dim3(64 * WPB), 0, s, w, M, x, ro);
+    return g;
+}
+
+// Returns the number of partials written (the grid size).
+int launch_q4k_res(const uint8_t* w, int M, const float* x, int K, const ResOut& ro, int order, hipStream_t s) {
+    if (K / 256 == 56)
+        return order == 0 ? launch_res<0, 56, 1, 8, true>(w, M, x, ro, s) : launch_res<1, 56, 1, 8, true>(w, M, x, ro, s);
+    if (span_rows_per_wave(M) == 1)
+        return order == 0 ? launch_res<0, 16, 1, 4, false>(w, M, x, ro, s) : launch_res<1, 16, 1, 4, false>(w, M, x, ro, s);
+    return order == 0 ? launch_res<0, 16, 2, 4, false>(w, M, x, ro, s) : launch_res<1, 16, 2, 4, false>(w, M, x, ro, s);
+}
 }  // namespace bpdq

@@ -398,3 +398,49 @@ def test_step_mixed_formats(dev, case):
         for l in range(L):
             assert np.array_equal(_cache_np(m.k_cache[l], f16), ko[l]), f"K cache layer {l}"
             assert np.array_equal(_cache_np(m.v_cache[l], f16), vo[l]), f"V cache layer {l}"
+
+
+# ---------------------------------------------------------------- RMSNorm folded into the GEMVs
+
+@pytest.mark.parametrize("fmt,F,L", [(llama.W_Q4K, 4096, 3), (llama.W_Q4K_GGUF, 4096, 3),
+                                     (llama.W_Q4K_GGUF, 14336, 2)])
+def test_step_folded_norms(dev, fmt, F, L):
+    """n_embd = 4096, all matrices Q4_K: the O and down GEMVs add into the residual
+    row and write partial sums of squares, and the Q/K/V and gate/up GEMVs compute
+    the norm themselves (layer 0's attention norm stays a launch of its own).
+    Against the restatement bpdq_o_llama_step, 3 steps, bit for bit."""
+    cfg = LM.config(E=4096, H=32, HKV=8, D=128, F=F, L=L, vocab=300, max_seq=8)
+    layers, head = LM.make(cfg, fmt, seed=23)
+    m = _gpu_model(cfg, layers, head, fmt, dev)
+    ko, vo = LM.caches(cfg)
+    for pos, e in enumerate(LM.embeddings(cfg, 3, seed=24)):
+        print(f"folded norms fmt={fmt} F={F} position {pos}", flush=True)
+        want = O.llama_step(fmt, layers, cfg, ko, vo, pos, e, head["out_norm"], head["lm"], None, cfg["vocab_size"])
+        tok = m.step(_d(e, dev), pos)
+        _check_step(m, tok, want, (ko, vo), pos, f"folded norms fmt {fmt} F {F}")
+
+
+def test_step_folded_norm_fallback(dev):
+    """Layer 0's matrices are all zero (d = dmin = 0), so the residual row entering
+    layer 1's folded attention norm, and layer 0's folded FFN norm, is the embedding
+    itself: a row whose binary64 sum of squares straddles an fp32 rounding boundary
+    of the mean, so the folded norms must take the sequential fallback."""
+    cfg = LM.config(E=4096, H=32, HKV=8, D=128, F=4096, L=2, vocab=300, max_seq=8)
+    n = cfg["n_embd"]
+    e = np.full(n, 2.0 ** -27, np.float32)
+    e[0] = 1 + 2.0 ** -12
+    S = float(np.sum(e.astype(np.float64) ** 2))
+    E = S * 4 * n * 2.0 ** -53
+    assert np.float32((S - E) / n) != np.float32((S + E) / n)
+    layers, head = LM.make(cfg, llama.W_Q4K_GGUF, seed=25)
+    for mname in LM.MATS:
+        layers[0][mname] = np.zeros_like(layers[0][mname])
+    for lw in layers:
+        lw["attn_norm"] = np.ones(n, np.float32)
+        lw["ffn_norm"] = np.ones(n, np.float32)
+    m = _gpu_model(cfg, layers, head, llama.W_Q4K_GGUF, dev)
+    ko, vo = LM.caches(cfg)
+    want = O.llama_step(llama.W_Q4K_GGUF, layers, cfg, ko, vo, 0, e, head["out_norm"], head["lm"], None,
+                        cfg["vocab_size"])
+    tok = m.step(_d(e, dev), 0)
+    _check_step(m, tok, want, (ko, vo), 0, "folded norm fallback")
