@@ -8,8 +8,8 @@
 //                       softmax, P.V and Q8_0(out)
 //   k_attn_scores       longer contexts: bias, RoPE, cache row write and the scores,
 //                       per (kv head, 64 rows), the k rows read once into LDS
-//   k_attn_pv           longer contexts: softmax and P.V per (head, 32 columns), one
-//                       wave running the chains while four stream V
+//   k_attn_pv           longer contexts: softmax and P.V per (head, 16 or 32 columns),
+//                       one wave running the chains while four stream V
 //   k_swiglu            silu(gate) * up, Q8_0 (padded Q8 weights; with Q4_K the
 //                       gate/up GEMV applies it to its own outputs)
 //   k_argmax            first index of the maximum logit
@@ -551,8 +551,8 @@ __global__ __launch_bounds__(64 * kMaxGroup) void k_attn_scores(AttnIn a, RopeTa
     }
 }
 
-// k_attn_pv, grid (heads * head_dim/32, query tokens): softmax and P.V for 32 output columns
-// d0..d0+31 of one head, in the reference's order.  The scores go to LDS; max,
+// k_attn_pv, grid (heads * head_dim/COLS, query tokens): softmax and P.V for COLS
+// output columns d0..d0+COLS-1 of one head, in the reference's order.  The scores go to LDS; max,
 // exps and the weights w_j = e_j * inv are parallel; the softmax sum runs in
 // lane 0 and each output's chain acc = RN(acc + RN(v_jd * w_j)) in lane d - d0
 // of wave 0.  Wave 0 does nothing else during P.V: waves 1-4 (the producers)
@@ -568,16 +568,21 @@ constexpr int kPvThreads = 64 + kPvProd;   // wave 0 runs the chains
 constexpr int kPvBigMin = 1024;            // 128-row chunks from here ...
 constexpr int kPvBigMax = 16384;           // ... up to here (LDS: ring + scores)
 
-template <int ROWS>
+// COLS 16 leaves twice as many workgroups each streaming half the V bytes (the
+// stream is bound by the bytes each workgroup keeps in flight); 32 when the
+// outputs' Q8_0 blocks (32 columns) are written too.  With a 132-float pitch
+// the producers' transposed writes hit 64 distinct banks at COLS 16.
+template <int ROWS, int COLS>
 struct PvShape {
-    static constexpr int LD = ROWS + 4;             // ring row pitch in floats
-    static constexpr int PER = ROWS * 8 / kPvProd;  // float4 of a chunk per producer (ROWS x 8 float4)
-    static constexpr int AHEAD = 512 / ROWS;        // chunks in flight: 64 KB per workgroup
+    static constexpr int C4 = COLS / 4;              // float4 of a V row slice
+    static constexpr int LD = ROWS + 4;              // ring row pitch in floats
+    static constexpr int PER = ROWS * C4 / kPvProd;  // float4 of a chunk per producer
+    static constexpr int AHEAD = 4096 / (ROWS * C4) < 8 ? 4096 / (ROWS * C4) : 8;  // chunks in flight (<= 64 KB)
 };
 // LDS: the ring, the padded scores and a few words
-static_assert(kMaxCtx % 64 == 0 && 2 * 32 * PvShape<64>::LD * 4 + kMaxCtx * 4 + 256 + 64 <= 160 * 1024,
+static_assert(kMaxCtx % 64 == 0 && 2 * 32 * PvShape<64, 32>::LD * 4 + kMaxCtx * 4 + 256 + 64 <= 160 * 1024,
               "k_attn_pv<64> LDS");
-static_assert(kPvBigMax % 64 == 0 && 2 * 32 * PvShape<128>::LD * 4 + kPvBigMax * 4 + 256 + 64 <= 160 * 1024,
+static_assert(kPvBigMax % 64 == 0 && 2 * 32 * PvShape<128, 32>::LD * 4 + kPvBigMax * 4 + 256 + 64 <= 160 * 1024,
               "k_attn_pv<128> LDS");
 
 template <typename CT>
@@ -589,12 +594,13 @@ struct PvPipe {
 };
 
 // Load of chunk c's share of producer tid: float4 number f = tid + k*256 is
-// row c*ROWS + f/8, columns d0 + 4(f%8)..+3; rows past n repeat row n-1 (never
+// row c*ROWS + f/C4, columns d0 + 4(f%C4)..+3; rows past n repeat row n-1 (never
 // used, so every load stays in the cache rows already written).
-template <int ROWS, typename CT>
+template <int ROWS, int COLS, typename CT>
 __device__ __forceinline__ typename Cache<CT>::Raw pv_load(const PvPipe<CT>& p, int c, int k) {
-    const int f = p.tid + k * kPvProd, r = min(c * ROWS + f / 8, p.n - 1);
-    return Cache<CT>::ldr(p.vbase + (int64_t)r * p.row + 4 * (f % 8));
+    constexpr int C4 = COLS / 4;
+    const int f = p.tid + k * kPvProd, r = min(c * ROWS + f / C4, p.n - 1);
+    return Cache<CT>::ldr(p.vbase + (int64_t)r * p.row + 4 * (f % C4));
 }
 
 // Step c = c0 + U (pf slot U holds chunk c; U is a template argument so that pf
@@ -603,21 +609,22 @@ __device__ __forceinline__ typename Cache<CT>::Raw pv_load(const PvPipe<CT>& p, 
 // the chunk's ROWS products in row order.  Slot c&1 is written again at step
 // c+2, after the barrier of step c+1, which the chain reaches only once it has
 // added chunk c.
-template <int U, int ROWS, typename CT>
-__device__ __forceinline__ void pv_chunk(const PvPipe<CT>& p, bool prod, bool chain,
-                                         typename Cache<CT>::Raw (&pf)[PvShape<ROWS>::AHEAD * PvShape<ROWS>::PER],
-                                         float* ring,
-                                         int c0, float& acc) {
-    constexpr int PER = PvShape<ROWS>::PER, LD = PvShape<ROWS>::LD;
+template <int U, int ROWS, int COLS, typename CT>
+__device__ __forceinline__ void pv_chunk(
+    const PvPipe<CT>& p, bool prod, bool chain,
+    typename Cache<CT>::Raw (&pf)[PvShape<ROWS, COLS>::AHEAD * PvShape<ROWS, COLS>::PER], float* ring, int c0,
+    float& acc) {
+    using PS = PvShape<ROWS, COLS>;
+    constexpr int PER = PS::PER, LD = PS::LD, C4 = PS::C4;
     const int c = c0 + U;
     if (c >= p.nch) return;  // uniform over the workgroup
-    float* slot = ring + (c & 1) * 32 * LD;
+    float* slot = ring + (c & 1) * COLS * LD;
     if (prod) {
 #pragma unroll
         for (int k = 0; k < PER; k++) {
-            const int f = p.tid + k * kPvProd, rr = f / 8, r = c * ROWS + rr;
+            const int f = p.tid + k * kPvProd, rr = f / C4, r = c * ROWS + rr;
             const float4 v = Cache<CT>::cvt(pf[U * PER + k]);
-            float* dst = slot + 4 * (f % 8) * LD + rr;
+            float* dst = slot + 4 * (f % C4) * LD + rr;
             if (r < p.n) {
                 const float w = p.e[r] * p.inv;  // the reference's scores[j] *= inv_sum
                 dst[0] = v.x * w;
@@ -630,7 +637,7 @@ __device__ __forceinline__ void pv_chunk(const PvPipe<CT>& p, bool prod, bool ch
                 dst[2 * LD] = -0.0f;
                 dst[3 * LD] = -0.0f;
             }
-            pf[U * PER + k] = pv_load<ROWS, CT>(p, c + PvShape<ROWS>::AHEAD, k);
+            pf[U * PER + k] = pv_load<ROWS, COLS, CT>(p, c + PS::AHEAD, k);
         }
     }
     __syncthreads();
@@ -651,18 +658,39 @@ __device__ __forceinline__ void pv_chunk(const PvPipe<CT>& p, bool prod, bool ch
     }
 }
 
-template <int ROWS, typename CT>
+// Workgroup b's head and column slice.  Workgroups go to the 8 XCDs round robin
+// (b % 8), each with its own L2: when the (kv head, slice) pairs divide into 8,
+// the `group` heads that read one V slice get workgroups of one XCD, so the
+// slice comes from HBM once per group instead of once per head.
+__device__ __forceinline__ void pv_tile(int b, int H, int group, int slices, int& head, int& slice) {
+    const int hkv = H / group;
+    if ((hkv * slices) % 8 == 0) {
+        const int i = b >> 3, pair = (i / group) * 8 + (b & 7);
+        head = (pair % hkv) * group + i % group;
+        slice = pair / hkv;
+    } else {
+        head = b % H;
+        slice = b / H;
+    }
+}
+
+template <int ROWS, int COLS, typename CT>
 __global__ __launch_bounds__(kPvThreads) void k_attn_pv(AttnIn a, const float* __restrict__ sc, int ld,
                                                         float* __restrict__ out, uint8_t* __restrict__ xq) {
-    constexpr int NT = kPvThreads, PER = PvShape<ROWS>::PER, AHEAD = PvShape<ROWS>::AHEAD;
+    using PS = PvShape<ROWS, COLS>;
+    constexpr int NT = kPvThreads, PER = PS::PER, AHEAD = PS::AHEAD;
     static_assert(AHEAD == 4 || AHEAD == 8, "one pv_chunk call per chunk in flight");
+    static_assert(COLS == 16 || COLS == 32, "16 or 32 chain lanes (32: the outputs' Q8_0 blocks)");
     extern __shared__ float4 e4dyn[];
     float* e = reinterpret_cast<float*>(e4dyn);  // pad64(n) floats
-    __shared__ __align__(16) float ring[2 * 32 * PvShape<ROWS>::LD];
+    __shared__ __align__(16) float ring[2 * COLS * PS::LD];
     __shared__ uint64_t etab[32];
     __shared__ float red[NT / 64];
     __shared__ float sh_inv;
-    const int H = a.row / a.D * a.group, head = blockIdx.x % H, d0 = 32 * (blockIdx.x / H);
+    const int H = a.row / a.D * a.group;
+    int head, slice;
+    pv_tile(blockIdx.x, H, a.group, a.D / COLS, head, slice);
+    const int d0 = COLS * slice;
     // query token blockIdx.y of a batch: its position is a.pos + blockIdx.y, its
     // scores and outputs follow the previous token's
     const int tq = blockIdx.y;
@@ -670,7 +698,7 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(AttnIn a, const float* _
     out += (int64_t)tq * H * a.D;
     if (xq != nullptr) xq += (int64_t)tq * (H * a.D / 32) * kQ80Bytes;
     const int tid = threadIdx.x, kvh = head / a.group, n = a.pos + tq + 1, nch = (n + ROWS - 1) / ROWS;
-    const bool prod = tid >= 64, chain = tid < 32;
+    const bool prod = tid >= 64, chain = tid < COLS;
     if (tid < 32) etab[tid] = kExp2fTab[tid];  // published by block_max's barrier
     // the scores first, 8 loads in flight (loads complete in order, so anything
     // issued before them would be waited for too), then the first V chunks,
@@ -697,7 +725,7 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(AttnIn a, const float* _
 #pragma unroll
         for (int c = 0; c < AHEAD; c++)
 #pragma unroll
-            for (int k = 0; k < PER; k++) pf[c * PER + k] = pv_load<ROWS, CT>(pp, c, k);
+            for (int k = 0; k < PER; k++) pf[c * PER + k] = pv_load<ROWS, COLS, CT>(pp, c, k);
     }
     const float mx = block_max<NT>(m, red);
     // the exps with the table in LDS (a per-lane index into constant memory is a
@@ -713,21 +741,22 @@ __global__ __launch_bounds__(kPvThreads) void k_attn_pv(AttnIn a, const float* _
     pp.inv = sh_inv;
     float acc = 0.0f;
     for (int c0 = 0; c0 < nch; c0 += AHEAD) {
-        pv_chunk<0, ROWS, CT>(pp, prod, chain, pf, ring, c0, acc);
-        pv_chunk<1, ROWS, CT>(pp, prod, chain, pf, ring, c0, acc);
-        pv_chunk<2, ROWS, CT>(pp, prod, chain, pf, ring, c0, acc);
-        pv_chunk<3, ROWS, CT>(pp, prod, chain, pf, ring, c0, acc);
+        pv_chunk<0, ROWS, COLS, CT>(pp, prod, chain, pf, ring, c0, acc);
+        pv_chunk<1, ROWS, COLS, CT>(pp, prod, chain, pf, ring, c0, acc);
+        pv_chunk<2, ROWS, COLS, CT>(pp, prod, chain, pf, ring, c0, acc);
+        pv_chunk<3, ROWS, COLS, CT>(pp, prod, chain, pf, ring, c0, acc);
         if constexpr (AHEAD == 8) {
-            pv_chunk<4, ROWS, CT>(pp, prod, chain, pf, ring, c0, acc);
-            pv_chunk<5, ROWS, CT>(pp, prod, chain, pf, ring, c0, acc);
-            pv_chunk<6, ROWS, CT>(pp, prod, chain, pf, ring, c0, acc);
-            pv_chunk<7, ROWS, CT>(pp, prod, chain, pf, ring, c0, acc);
+            pv_chunk<4, ROWS, COLS, CT>(pp, prod, chain, pf, ring, c0, acc);
+            pv_chunk<5, ROWS, COLS, CT>(pp, prod, chain, pf, ring, c0, acc);
+            pv_chunk<6, ROWS, COLS, CT>(pp, prod, chain, pf, ring, c0, acc);
+            pv_chunk<7, ROWS, COLS, CT>(pp, prod, chain, pf, ring, c0, acc);
         }
     }
     if (chain) {
         const int64_t o = (int64_t)head * a.D + d0 + tid;
         out[o] = acc;
-        if (xq != nullptr) q8_0_lane_store(acc, xq + (o >> 5) * kQ80Bytes, tid & 31);
+        if constexpr (COLS == 32)
+            if (xq != nullptr) q8_0_lane_store(acc, xq + (o >> 5) * kQ80Bytes, tid & 31);
     }
 }
 
@@ -948,11 +977,13 @@ namespace {
 
 template <typename CT>
 hipError_t lds_limits_for() {
-    hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_pv<64, CT>),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, kMaxCtx * 4);
-    if (err == hipSuccess)
-        err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_attn_pv<128, CT>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, kPvBigMax * 4);
+    hipError_t err = hipSuccess;
+    for (const void* f : {reinterpret_cast<const void*>(&k_attn_pv<64, 32, CT>),
+                          reinterpret_cast<const void*>(&k_attn_pv<64, 16, CT>)})
+        if (err == hipSuccess) err = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kMaxCtx * 4);
+    for (const void* f : {reinterpret_cast<const void*>(&k_attn_pv<128, 32, CT>),
+                          reinterpret_cast<const void*>(&k_attn_pv<128, 16, CT>)})
+        if (err == hipSuccess) err = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, kPvBigMax * 4);
     // the scores kernels' LDS: the k tile plus q of up to n_embd / head_dim heads
     for (const void* f : {reinterpret_cast<const void*>(&k_attn_scores<128, CT>),
                           reinterpret_cast<const void*>(&k_attn_scores<64, CT>),
@@ -1249,12 +1280,22 @@ void attention(const StepCtx& c, const AttnIn& ai, int n_ctx) {
         hipLaunchKernelGGL((k_attn_scores<0, CT>), gs, ts, slds, c.s, ai, c.tab, c.scores, ld);
     // e holds pad64(n_ctx) <= kMaxCtx floats (kMaxCtx % 64 == 0); with 128-row
     // chunks n_ctx <= kPvBigMax, so the ring and the scores fit in 160 KB
-    const dim3 gp(g.H * (g.D / 32));
+    // 16-column slices unless the output's Q8_0 bytes are wanted (head_dim % 32 == 0)
     const size_t lds = (size_t)pad64(n_ctx) * 4;
-    if (n_ctx >= kPvBigMin && n_ctx <= kPvBigMax)
-        hipLaunchKernelGGL((k_attn_pv<128, CT>), gp, dim3(kPvThreads), lds, c.s, ai, c.scores, ld, c.att, c.xq_a);
-    else
-        hipLaunchKernelGGL((k_attn_pv<64, CT>), gp, dim3(kPvThreads), lds, c.s, ai, c.scores, ld, c.att, c.xq_a);
+    const bool big = n_ctx >= kPvBigMin && n_ctx <= kPvBigMax;
+    if (c.xq_a == nullptr) {
+        const dim3 gp(g.H * (g.D / 16));
+        if (big)
+            hipLaunchKernelGGL((k_attn_pv<128, 16, CT>), gp, dim3(kPvThreads), lds, c.s, ai, c.scores, ld, c.att, nullptr);
+        else
+            hipLaunchKernelGGL((k_attn_pv<64, 16, CT>), gp, dim3(kPvThreads), lds, c.s, ai, c.scores, ld, c.att, nullptr);
+    } else {
+        const dim3 gp(g.H * (g.D / 32));
+        if (big)
+            hipLaunchKernelGGL((k_attn_pv<128, 32, CT>), gp, dim3(kPvThreads), lds, c.s, ai, c.scores, ld, c.att, c.xq_a);
+        else
+            hipLaunchKernelGGL((k_attn_pv<64, 32, CT>), gp, dim3(kPvThreads), lds, c.s, ai, c.scores, ld, c.att, c.xq_a);
+    }
 }
 
 // The layers.  The residual add is the first step of each RMSNorm kernel; the
@@ -1555,9 +1596,9 @@ void mt_attention(const MtCtx& c, const float* q, const CT* kc, const CT* vc, fl
         float* o = out + (int64_t)t0 * g.H * g.D;
         uint8_t* xq = c.xq + (int64_t)t0 * (g.H * g.D / 32) * kQ80Bytes;
         if (n_max >= kPvBigMin && n_max <= kPvBigMax)
-            hipLaunchKernelGGL((k_attn_pv<128, CT>), gp, dim3(kPvThreads), lds, c.s, ai, c.scores, c.ld, o, xq);
+            hipLaunchKernelGGL((k_attn_pv<128, 32, CT>), gp, dim3(kPvThreads), lds, c.s, ai, c.scores, c.ld, o, xq);
         else
-            hipLaunchKernelGGL((k_attn_pv<64, CT>), gp, dim3(kPvThreads), lds, c.s, ai, c.scores, c.ld, o, xq);
+            hipLaunchKernelGGL((k_attn_pv<64, 32, CT>), gp, dim3(kPvThreads), lds, c.s, ai, c.scores, c.ld, o, xq);
     }
 }
 

@@ -444,3 +444,38 @@ def test_step_folded_norm_fallback(dev):
                         cfg["vocab_size"])
     tok = m.step(_d(e, dev), 0)
     _check_step(m, tok, want, (ko, vo), 0, "folded norm fallback")
+
+
+@pytest.mark.parametrize("f16", [False, True])
+@pytest.mark.parametrize("D,pos,H,HKV", [
+    (64, 2047, 4, 2), (64, 300, 4, 2), (128, 1100, 4, 2), (128, 1023, 8, 2), (64, 200, 16, 1), (128, 4000, 8, 2)])
+def test_long_context_kquant(dev, D, pos, H, HKV, f16):
+    """K-quant weights (no Q8_0 attention output): P.V in 16-column slices, whose
+    workgroups the (kv head, slice) pairs map onto XCDs when they divide into 8
+    (every case here but the single-kv-head one).  One step at pos over
+    pos + 1 cached rows, against the reference block."""
+    cfg = LM.config(L=1, max_seq=max(2048, pos + 1), E=H * D, H=H, HKV=HKV, D=D, F=256)
+    layers, head = LM.make(cfg, llama.W_Q4K, seed=19)
+    m = _ext_model(cfg, layers, head, llama.W_Q4K, dev, kv_cache_f16=f16)
+    kr, vr = LM.caches(cfg, f16)
+    row = HKV * D
+    for l in range(cfg["n_layers"]):
+        k = LM.synth.normal_f32(pos * row, LM.synth.key(83, l))
+        v = LM.synth.normal_f32(pos * row, LM.synth.key(84, l))
+        kr[l][:pos * row] = k.astype(np.float16).view(np.uint16) if f16 else k
+        vr[l][:pos * row] = v.astype(np.float16).view(np.uint16) if f16 else v
+        m.k_cache[l].copy_(_d(kr[l].view(np.int16) if f16 else kr[l], dev))
+        m.v_cache[l].copy_(_d(vr[l].view(np.int16) if f16 else vr[l], dev))
+    e = LM.embeddings(cfg, 1, seed=20)[0]
+    print(f"long context K-quant D={D} pos={pos} H={H} HKV={HKV} f16={f16}", flush=True)
+    fmts = [[llama.W_Q4K] * 7 for _ in range(cfg["n_layers"])]
+    want = O.llama_step_ext(fmts, llama.W_Q4K, layers, cfg, kr, vr, pos, e, head["out_norm"], head["lm"], None,
+                            cfg["vocab_size"], kv_f16=f16)
+    tok = m.step(_d(e, dev), pos)
+    assert tok == want[0], f"token at {pos}"
+    assert_bits_equal(to_np(m.buf_t["logits"]), want[3], f"logits at {pos}")
+    assert_bits_equal(to_np(m.buf_t["x"]), want[1], f"x at {pos}")
+    assert_bits_equal(to_np(m.buf_t["h"]), want[2], f"h at {pos}")
+    for l in range(cfg["n_layers"]):
+        assert np.array_equal(_cache_np(m.k_cache[l], f16), kr[l]), f"K cache layer {l}"
+        assert np.array_equal(_cache_np(m.v_cache[l], f16), vr[l]), f"V cache layer {l}"
