@@ -232,6 +232,15 @@ __device__ __forceinline__ void q8_0_quad_store(float4 v, uint8_t* __restrict__ 
     if (g == 0) *reinterpret_cast<uint16_t*>(yb) = __builtin_bit_cast(uint16_t, (_Float16)d);
 }
 
+// Workgroup b of a grid of G workgroups as numbered for row order.  The
+// hardware hands workgroups to the 8 XCDs round robin (b % 8), each XCD with
+// its own L2: XCD-major numbering gives each XCD one contiguous range of rows,
+// so each 128-byte line of outputs (rows of several workgroups) is written from
+// one L2 instead of four.  When G is not a multiple of 8, b itself.
+__device__ __forceinline__ int xcd_major(int b, int G) {
+    return (G & 7) == 0 ? (b & 7) * (G >> 3) + (b >> 3) : b;
+}
+
 // RMSNorm's scale 1 / sqrtf(mean + eps) (bpd_rmsnorm_llama_cpu,
 // bench/bpd_cpu.c:4959-4986: a sequential binary64 sum of (double)x^2, mean =
 // (float)(sum / n)) from S, the binary64 sum of the same n squares in another

@@ -792,7 +792,7 @@ __global__ __launch_bounds__(64 * WPB) void k_q4k_q8k_gemv(const uint8_t* __rest
                                                            int M, int nb) {
     // the wave index is uniform across the wave; saying so keeps row offsets scalar
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int row0 = (blockIdx.x * WPB + wave) * R;
+    const int row0 = (xcd_major(blockIdx.x, gridDim.x) * WPB + wave) * R;
     if (row0 >= M) return;
     typename PassW<KIND, R, G>::type unused;
     rows<KIND, ORDER, R, G>(w, xq, y, M, nb, row0, unused);
@@ -958,7 +958,7 @@ __global__ __launch_bounds__(64 * WPB) void k_q4k_q8k_gemv_span(const uint8_t* _
     using S = Span<NB, R, true>;
     __shared__ __align__(16) uint8_t slots[WPB][S::kSlot];
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int row0 = (blockIdx.x * WPB + wave) * R;
+    const int row0 = (xcd_major(blockIdx.x, gridDim.x) * WPB + wave) * R;
     if (row0 >= M) return;
     XOps xr[S::kNT][2];
     span_load_x<ORDER, NB>(xr, xq);
@@ -991,7 +991,7 @@ struct MultiArgs {
 template <int KIND, int ORDER, int R, int G, int WPB>
 __global__ __launch_bounds__(64 * WPB) void k_q4k_q8k_gemv_multi(MultiArgs a, const uint8_t* __restrict__ xq, int nb) {
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int gw = blockIdx.x * WPB + wave;
+    const int gw = xcd_major(blockIdx.x, gridDim.x) * WPB + wave;
     int i = 0;
 #pragma unroll
     for (int k = 1; k < kMulti; k++)
@@ -1199,7 +1199,7 @@ __global__ __launch_bounds__(64 * WPB) void k_q4k_fused_gemv(MultiArgs a, const 
     extern __shared__ __align__(16) uint8_t xl[];
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     int i, row0;
-    const bool has = wave_rows(a, blockIdx.x * WPB + wave, R, i, row0);
+    const bool has = wave_rows(a, xcd_major(blockIdx.x, gridDim.x) * WPB + wave, R, i, row0);
     XPre<IT> P;
     x32_load<WPB, IT>(P, x, nb);
     typename PassW<KIND, R, G>::type pre;
@@ -1231,7 +1231,7 @@ __global__ __launch_bounds__(64 * WPB) void k_q4k_fused_swiglu(const uint8_t* __
                                                               const uint8_t* __restrict__ xq, int nb) {
     extern __shared__ __align__(16) uint8_t xl[];
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int row = blockIdx.x * WPB + wave;
+    const int row = xcd_major(blockIdx.x, gridDim.x) * WPB + wave;
     const bool has = row < M;
     const int row0 = has ? row : 0;
     if constexpr (QX) {
@@ -1273,7 +1273,7 @@ __global__ __launch_bounds__(64 * WPB) void k_q4k_q8k_multi_span(MultiArgs a, co
     __shared__ __align__(16) uint8_t slots[WPB][S::kSlot];
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     int i, row0;
-    if (!wave_rows(a, blockIdx.x * WPB + wave, R, i, row0)) return;
+    if (!wave_rows(a, xcd_major(blockIdx.x, gridDim.x) * WPB + wave, R, i, row0)) return;
     XOps xr[S::kNT][2];
     span_load_x<ORDER, NB>(xr, xq);
     const uint8_t* seg[1] = {a.w[i] + (int64_t)row0 * (NB * kQ4KBytes)};
@@ -1298,7 +1298,7 @@ __global__ __launch_bounds__(64 * WPB) void k_q4k_fused_span(MultiArgs a, const 
     __shared__ __align__(16) uint8_t xl[NB * kXS];
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     int i, row0;
-    const bool has = wave_rows(a, blockIdx.x * WPB + wave, R, i, row0);
+    const bool has = wave_rows(a, xcd_major(blockIdx.x, gridDim.x) * WPB + wave, R, i, row0);
     XPre<IT> P;
     x32_load<WPB, IT>(P, x, NB);
     const uint8_t* seg[1] = {a.w[i] + (int64_t)row0 * (NB * kQ4KBytes)};
@@ -1326,7 +1326,7 @@ __global__ __launch_bounds__(64 * WPB) void k_q4k_swiglu_span(const uint8_t* __r
     using S = Span<NB, 2, false>;
     __shared__ __align__(16) uint8_t slots[WPB][S::kSlot];
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int row = blockIdx.x * WPB + wave;
+    const int row = xcd_major(blockIdx.x, gridDim.x) * WPB + wave;
     if (row >= M) return;
     XOps xr[S::kNT][2];
     span_load_x<ORDER, NB>(xr, xq);
@@ -1588,7 +1588,7 @@ __global__ __launch_bounds__(64 * WPB) void k_q4k_norm_span(MultiArgs a, NormIn 
     __shared__ double red[WPB + 1];
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     int i, row0;
-    const bool has = wave_rows(a, blockIdx.x * WPB + wave, R, i, row0);
+    const bool has = wave_rows(a, xcd_major(blockIdx.x, gridDim.x) * WPB + wave, R, i, row0);
     XPre<IT> P, Wn;
     double pp[kPartRegs];
     part_load<WPB>(pp, nin);
@@ -1623,7 +1623,7 @@ __global__ __launch_bounds__(64 * WPB) void k_q4k_res_span(const uint8_t* __rest
     __shared__ __align__(16) uint8_t xl[NB * kXS];
     __shared__ double red[WPB];
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int row0w = (blockIdx.x * WPB + wave) * R;
+    const int row0w = (xcd_major(blockIdx.x, gridDim.x) * WPB + wave) * R;
     const bool has = row0w < M;
     const int row0 = has ? row0w : 0;
     XPre<IT> P;

@@ -157,7 +157,7 @@ __global__ __launch_bounds__(64 * WPB) void k_q6k_q8k_gemv(const uint8_t* __rest
     const int lane = threadIdx.x & 63;
     const int q = lane >> 3, c = lane & 7;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int row0 = (blockIdx.x * WPB + wave) * R;
+    const int row0 = (xcd_major(blockIdx.x, gridDim.x) * WPB + wave) * R;
     if (row0 >= M) return;
     const int64_t row_bytes = (int64_t)nb * kQ6KBytes;
     float s[R];
@@ -370,7 +370,7 @@ __global__ __launch_bounds__(64 * WPB) void k_q6k_q8k_gemv_span(const uint8_t* _
     const int lane = threadIdx.x & 63;
     const int q = lane >> 3, c = lane & 7;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int row0 = (blockIdx.x * WPB + wave) * R;
+    const int row0 = (xcd_major(blockIdx.x, gridDim.x) * WPB + wave) * R;
     if (row0 >= M) return;
     Q6X<ORDER> x[NT];
 #pragma unroll
@@ -451,7 +451,7 @@ __global__ __launch_bounds__(64 * WPB) void k_q6k_q8k_gemv_span_long(const uint8
     const int tid = threadIdx.x, lane = tid & 63;
     const int q = lane >> 3, c = lane & 7;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int row = blockIdx.x * WPB + wave;
+    const int row = xcd_major(blockIdx.x, gridDim.x) * WPB + wave;
     const bool has = row < M;
     // threads past the last record load record XR-1's bytes again (not stored)
     const int rt = min(tid, XR - 1);
