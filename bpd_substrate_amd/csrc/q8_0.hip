@@ -1198,8 +1198,10 @@ __global__ __launch_bounds__(128 * RT) void k_q8_0_gemm_SH(const uint8_t* __rest
     for (int h = 0; h < nh; h++) {
         const int slot = h & 1;
         if (h + 1 < nh) half_load<RT>(raw, W, X, m0, n0, m_weight, m_tokens, (h + 1) * kGH, bpr);
-        // block pairs: the swizzle of the operand reads changes once per pair
-#pragma unroll 1
+        // block pairs: the swizzle of the operand reads changes once per pair (the
+        // pair loop unrolled, the block loop not: 117.7 against 120.2 us at cfg4;
+        // both unrolled spill)
+#pragma unroll
         for (int pu = 0; pu < kGH / 2; pu++) {
         const int offa = 16 * (half ^ h_swz(ra, 2 * pu));
         const int offb0 = 16 * (half ^ h_swz(wc * 64 + col, 2 * pu));
