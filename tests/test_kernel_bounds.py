@@ -817,3 +817,95 @@ def test_qmatmul_q4k_chain_in_bounds_and_barriers(M, K):
         assert (r * rowbytes + rowbytes).max() <= M * rowbytes
     producer_barriers = sum(1 for c0 in range(0, nch, ahead) for a in range(ahead) if c0 + a < nch)
     assert producer_barriers == nch
+
+
+# ---------------------------------------------------------------- workgroup numbering and the decode step
+
+def xcd_major(b, G):
+    """bpdq_device.h xcd_major: hardware workgroup b of G -> its place in row order."""
+    return (b & 7) * (G >> 3) + (b >> 3) if (G & 7) == 0 else b
+
+
+@pytest.mark.parametrize("G", [1, 7, 8, 16, 257, 512, 1025, 1792, 3584])
+def test_xcd_major_is_a_permutation_with_xcd_local_ranges(G):
+    """Every workgroup gets one place in row order and every place one workgroup;
+    when G % 8 == 0 each XCD (b % 8) owns one contiguous range of places."""
+    b = np.arange(G)
+    m = np.array([xcd_major(int(i), G) for i in b])
+    assert sorted(m.tolist()) == list(range(G))
+    if G % 8 == 0:
+        for x in range(8):
+            mine = np.sort(m[b % 8 == x])
+            assert (np.diff(mine) == 1).all() and mine[0] == x * (G // 8)
+
+
+def pv_tile(b, H, group, slices):
+    """llama.hip pv_tile: workgroup b -> (head, column slice)."""
+    hkv = H // group
+    if (hkv * slices) % 8 == 0:
+        i = b >> 3
+        pair = (i // group) * 8 + (b & 7)
+        return (pair % hkv) * group + i % group, pair // hkv
+    return b % H, b // H
+
+
+@pytest.mark.parametrize("H,HKV,D", [(32, 8, 128), (4, 2, 64), (4, 2, 128), (8, 2, 128), (16, 1, 64), (4, 4, 32),
+                                     (16, 1, 32), (64, 8, 128), (2, 1, 256)])
+@pytest.mark.parametrize("cols", [16, 32])
+def test_pv_tile_covers_every_head_and_slice_once(H, HKV, D, cols):
+    """k_attn_pv's grid of H * D/cols workgroups: each (head, slice) exactly once, and
+    with the XCD numbering the heads that read one V slice share an XCD."""
+    slices, group = D // cols, H // HKV
+    seen = set()
+    xcd = {}
+    for b in range(H * slices):
+        head, s = pv_tile(b, H, group, slices)
+        assert 0 <= head < H and 0 <= s < slices
+        seen.add((head, s))
+        xcd.setdefault((head // group, s), set()).add(b % 8)
+    assert len(seen) == H * slices
+    if (HKV * slices) % 8 == 0:
+        assert all(len(v) == 1 for v in xcd.values())
+
+
+@pytest.mark.parametrize("n", [1, 63, 64, 65, 1023, 1024, 1100, 2049, 16384])
+@pytest.mark.parametrize("cols", [16, 32])
+def test_attn_pv_ring_and_loads_in_bounds(n, cols):
+    """k_attn_pv<ROWS, COLS>: producer f = tid + 256k loads V row min(c*ROWS + f/C4, n-1),
+    columns 4(f % C4).. of the slice, and writes ring slot rows 4(f % C4)..+3 at column
+    f / C4; the chain lanes read ROWS floats of ring row tid."""
+    rows = 128 if 1024 <= n <= 16384 else 64
+    c4 = cols // 4
+    ld = rows + 4
+    per = rows * c4 // 256
+    ahead = min(4096 // (rows * c4), 8)
+    assert ahead in (4, 8) and per >= 1
+    nch = (n + rows - 1) // rows
+    f = np.arange(256)[:, None] + 256 * np.arange(per)[None, :]
+    for c in sorted({0, nch - 1, nch - 1 + ahead}):  # the prefetch runs ahead of the last chunk
+        r = np.minimum(c * rows + f // c4, n - 1)
+        assert (r >= 0).all() and (r < n).all()
+        assert (4 * (f % c4) + 3 < cols).all()
+    slot_w = 4 * (f % c4) * ld + f // c4
+    assert (slot_w + 3 * ld < cols * ld).all() and (f // c4 < rows).all()
+    chain = np.arange(cols)
+    assert (chain * ld + rows <= cols * ld).all()
+
+
+@pytest.mark.parametrize("E,F", [(4096, 4096), (4096, 14336)])
+def test_folded_norm_partials_fit_their_buffers(E, F):
+    """The residual epilogues write one partial per workgroup: O (K = n_head*head_dim =
+    n_embd, span rows per wave as launch_q4k_res picks them, 4 waves) and down (K = ff:
+    56 blocks -> one row per wave, 8 waves; 16 -> as O).  The step reserves E/4 + 1
+    doubles per set, and k_norm_q8k keeps 16 per lane in registers (1,024)."""
+    def grid(M, K):
+        if K // 256 == 56:
+            return (M + 7) // 8
+        R = span_rows_per_wave(M)
+        return ((M + R - 1) // R + 3) // 4
+    for K in (E, F):
+        g = grid(E, K)
+        assert g <= E // 4 + 1
+        assert g <= 16 * 64
+    # k_norm_q8k: wave b quantizes float4s b*64 .. b*64 + 63 of x and w
+    assert (E // 256) * 64 * 4 == E
