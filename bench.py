@@ -365,6 +365,51 @@ def decode_step(torch, L, T, dev, gpu, synth, layers, tokens=10, max_seq=4096, v
     return out
 
 
+def prefill_forward(torch, dev, gpu, synth, n_layers=32, tokens=512, vocab=32000, sets=4, runs=3):
+    """The reference CPU library's forward (bpd_llama_forward_s_gpu: order S, the
+    cfg4 int8-MFMA GEMM for every projection) over a 32-layer Mistral-7B-shaped
+    Q8_0 model with binary16 caches, one prefill of `tokens` tokens from an empty
+    cache; `sets` distinct weight copies rotate over the layers (0.93 GB, beyond
+    the MALL).  Eager calls: the forward uploads its host token and position
+    arrays and waits for that copy, as the reference's CPU call reads them."""
+    from bpd_substrate_amd import llama
+
+    E, H, HKV, D, F = 4096, 32, 8, 128, 14336
+    cfg = dict(n_layers=n_layers, n_heads=H, n_kv_heads=HKV, head_dim=D, embed_dim=E, ffn_dim=F, vocab_size=vocab,
+               max_seq_len=tokens, rms_eps=1e-5, rope_base=1e6, rope_dim=D, kv_cache_f16=1)
+    shapes = {"w_q": (H * D, E), "w_k": (HKV * D, E), "w_v": (HKV * D, E), "w_o": (E, H * D),
+              "w_gate": (F, E), "w_up": (F, E), "w_down": (E, F)}
+    base = {n: torch.from_numpy(synth.q8_0(r, k, synth.key(46, i), d_sigma=0.002)).to(dev)
+            for i, (n, (r, k)) in enumerate(shapes.items())}
+    norm = lambda t: torch.from_numpy((1.0 + 0.1 * synth.normal_f32(E, synth.key(47, t))).astype(np.float32)).to(dev)
+    wsets = [base] + [{n: t.clone() for n, t in base.items()} for _ in range(sets - 1)]
+    layers = [dict(attn_norm_w=norm(2 * l), ffn_norm_w=norm(2 * l + 1), **wsets[l % sets]) for l in range(n_layers)]
+    embd = torch.from_numpy(synth.q8_0(vocab, E, synth.key(46, 90), d_sigma=0.02)).to(dev)
+    out_w = torch.from_numpy(synth.q8_0(vocab, E, synth.key(46, 91), d_sigma=0.002)).to(dev)
+    f = llama.Forward(cfg, layers, embd, norm(999), out_w, device=dev)
+    ids = (np.arange(tokens, dtype=np.int64) * 7919 % vocab).astype(np.int32)
+    pos = np.arange(tokens, dtype=np.int32)
+    f.forward(ids, pos, 0, order="S")
+    torch.cuda.synchronize()
+    gpu.check()
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        f.forward(ids, pos, 0, order="S")
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+    gpu.check()
+    ms = float(np.median(times)) * 1e3
+    gemm_ops = 2.0 * tokens * n_layers * sum(r * k for r, k in shapes.values())
+    out = {"ms_per_prefill": round(ms, 2), "tokens_per_s": round(tokens / ms * 1e3, 1),
+           "projection_tops": round(gemm_ops / ms / 1e9, 1), "tokens": tokens, "n_layers": n_layers,
+           "weights": "Q8_0", "kv_cache": "binary16",
+           "note": "bpd_llama_forward_s_gpu, host wall clock per call (launches, the token/position upload and "
+                   "the logits of every token included); projections on k_q8_0_gemm_SH"}
+    del f, layers, wsets, base, embd, out_w
+    return out
+
+
 def load_traffic():
     p = os.path.join(ROOT, "profiles", "q4k_q8k_gemv_14336x4096_traffic.json")
     if not os.path.exists(p):
@@ -608,6 +653,8 @@ def main():
         result["decode_cfg3"] = decode_chain(torch, L, T, dev, gpu, layers, acts)
         result["decode_cfg3"]["full_step"] = decode_step(torch, L, T, dev, gpu, synth, layers)
         del layers, acts
+        log("prefill forward (reference CPU library ABI, 32 layers, 512 tokens)")
+        result["prefill_forward_32_layers_512_tokens"] = prefill_forward(torch, dev, gpu, synth)
 
     if not a.no_cpu:
         log("CPU baseline (reference C, 1 core and all cores)")

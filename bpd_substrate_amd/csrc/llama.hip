@@ -961,6 +961,213 @@ __global__ __launch_bounds__(64 * kMaxGroup) void k_mt_scores(const float* __res
     }
 }
 
+// ----------------------------------------------------------------------------
+// Attention of a batch of T tokens laid out for throughput: the arithmetic of
+// k_mt_scores + k_attn_pv (the reference's per-token order), with query token t
+// attending over rows 0..n_t-1, n_t = kv_pos + t + 1.  Those kernels give each
+// (head, token) a workgroup whose chains run in one lane (the softmax sum) or 32
+// (P.V); at T = 512 that is 65,536 workgroups of mostly idle lanes.  Here lanes
+// are tokens, so one wave-instruction advances 64 tokens' chains:
+//   k_mt_scores_tile  grid (64-row blocks, kv heads, 16-token blocks): k rows and
+//                     the block's q rows in LDS; lane j of wave h runs 16 tokens'
+//                     dots with row j (sequential over d, 16 chains per lane).
+//   k_mt_softmax      grid (heads, 64-token blocks), 8 waves: the order-free max,
+//                     then per 64-row chunk waves 1-7 write e = expf(v - m) into
+//                     LDS and over the scores in place, and lane t of wave 0 adds
+//                     token t's e in row order; inv_t = S_t == 0 ? 0 : 1/S_t.
+//   k_mt_pv           grid (heads, 64-token blocks, head_dim/32 slices): per
+//                     64-row chunk the weights RN(e*inv) and the V rows in LDS;
+//                     lane t of wave w runs token t's chains for columns 8w..8w+7
+//                     (acc = RN(acc + RN(v*w)) in row order), then Q8_0(out).
+// Score rows are ld floats apart, ld a multiple of 64 (16-byte aligned rows).
+// ----------------------------------------------------------------------------
+constexpr int kMtTok = 16;  // tokens per scores workgroup
+constexpr int kMtBlk = 64;  // tokens per softmax / P.V workgroup (one per lane)
+
+__host__ __device__ constexpr size_t mt_scores_lds(int G, int D) {
+    return ((size_t)kScoreRows * score_pitch(D) + (size_t)kMtTok * G * D + 4) * 4;
+}
+
+template <typename CT>
+__global__ __launch_bounds__(64 * kMaxGroup) void k_mt_scores_tile(const float* __restrict__ q,
+                                                                   const CT* __restrict__ kc, float* __restrict__ sc,
+                                                                   int ld, int kv_pos, int T, int H, int HKV, int D,
+                                                                   float scale) {
+    extern __shared__ float4 sm4[];
+    const int G = H / HKV, D4 = D / 4, P4 = score_pitch(D) / 4, row = HKV * D;
+    const int j0 = blockIdx.x * kScoreRows, kvh = blockIdx.y, t0 = blockIdx.z * kMtTok;
+    const int nt = min(kMtTok, T - t0), n_hi = kv_pos + t0 + nt;  // rows of the block's last token
+    if (j0 >= n_hi) return;  // uniform over the workgroup
+    const int nw = blockDim.x >> 6, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    float4* kt = sm4;                    // [64][P4]
+    float4* qs4 = kt + kScoreRows * P4;  // [kMtTok][G][D4]
+    float4* spare = qs4 + kMtTok * G * D4;
+    const int rows = min(kScoreRows, n_hi - j0);
+    rows_to_lds<CT>(kt, spare, kc, j0, rows, row, (int64_t)kvh * D, D4, P4);
+    for (int f = threadIdx.x; f < kMtTok * G * D4; f += blockDim.x) {
+        const int tt = f / (G * D4), r = f % (G * D4);
+        qs4[f] = tt < nt ? reinterpret_cast<const float4*>(q + ((int64_t)(t0 + tt) * H + kvh * G) * D)[r]
+                         : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    __syncthreads();
+    if (lane >= rows) return;
+    const float4* kr = kt + lane * P4;
+    for (int h = wave; h < G; h += nw) {
+        float s[kMtTok];
+#pragma unroll
+        for (int tt = 0; tt < kMtTok; tt++) s[tt] = 0.0f;
+        for (int i = 0; i < D4; i++) {
+            const float4 k4 = kr[i];
+#pragma unroll
+            for (int tt = 0; tt < kMtTok; tt++) s[tt] = dot_step(s[tt], qs4[(tt * G + h) * D4 + i], k4);
+        }
+#pragma unroll
+        for (int tt = 0; tt < kMtTok; tt++)
+            if (tt < nt) sc[((int64_t)(t0 + tt) * H + kvh * G + h) * ld + j0 + lane] = s[tt] * scale;
+    }
+}
+
+constexpr int kMtSmThreads = 512;  // wave 0 chains, waves 1-7 produce the exps
+constexpr int kMtEP = kScoreRows + 4;  // LDS pitch of a token's chunk of e / weights
+
+template <int NT>
+__global__ __launch_bounds__(NT) void k_mt_softmax(float* __restrict__ sc, float* __restrict__ inv_out, int ld,
+                                                   int kv_pos, int T, int H) {
+    __shared__ __align__(16) float E[2][kMtBlk * kMtEP];
+    __shared__ float red[NT / 64][kMtBlk];
+    __shared__ uint64_t etab[32];
+    const int h = blockIdx.x, tb = blockIdx.y * kMtBlk, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nt = min(kMtBlk, T - tb), n_hi = kv_pos + tb + nt;
+    if (tid < 32) etab[tid] = kExp2fTab[tid];
+    // the max of token lane's row (order-free; NaN never wins), each wave a quarter
+    // ... an eighth of the rows, then across the waves
+    {
+        const int t = tb + lane, n = kv_pos + t + 1;
+        float m = -1e38f;
+        if (lane < nt) {
+            const float* r = sc + ((int64_t)t * H + h) * ld;
+            for (int j = wave; j < n; j += NT / 64) m = r[j] > m ? r[j] : m;
+        }
+        red[wave][lane] = m;
+    }
+    __syncthreads();
+    float mx = red[0][lane];
+#pragma unroll
+    for (int w = 1; w < NT / 64; w++) mx = red[w][lane] > mx ? red[w][lane] : mx;
+    __syncthreads();
+    if (wave == 0) red[0][lane] = mx;  // token lane's max, for the producers
+    __syncthreads();
+    const int nch = (n_hi + kScoreRows - 1) / kScoreRows;
+    float sum = 0.0f;
+    // chunk c: the producers fill E[c & 1] (barrier), then wave 0 adds it while
+    // they fill the other slot; E[c & 1] is written again after the barrier of
+    // step c + 1, which wave 0 reaches only when it has added chunk c
+    for (int c = 0; c < nch; c++) {
+        if (wave > 0) {
+            float* Ec = E[c & 1];
+            for (int qi = tid - 64; qi < kMtBlk * kScoreRows; qi += NT - 64) {
+                const int tt = qi / kScoreRows, jj = qi % kScoreRows, t = tb + tt, j = c * kScoreRows + jj;
+                float e = -0.0f;  // past token tt's rows: sum + -0.0 == sum
+                if (tt < nt && j <= kv_pos + t) {
+                    float* p = sc + ((int64_t)t * H + h) * ld + j;
+                    e = expf_libm(*p - red[0][tt], etab);
+                    *p = e;
+                }
+                Ec[tt * kMtEP + jj] = e;
+            }
+        }
+        __syncthreads();
+        if (wave == 0) {
+            const float4* col = reinterpret_cast<const float4*>(E[c & 1] + lane * kMtEP);
+            float4 a[16];
+            read_group<16>(a, col, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            sum_group<16>(sum, a);
+        }
+    }
+    if (wave == 0 && lane < nt) inv_out[(int64_t)(tb + lane) * H + h] = sum == 0.0f ? 0.0f : 1.0f / sum;
+}
+
+template <typename CT>
+__global__ __launch_bounds__(256) void k_mt_pv(const float* __restrict__ sc, const float* __restrict__ inv_in,
+                                                const CT* __restrict__ vc, float* __restrict__ out,
+                                                uint8_t* __restrict__ xq, int ld, int kv_pos, int T, int H, int HKV,
+                                                int D) {
+    __shared__ __align__(16) float W[kMtBlk * kMtEP];   // [token][row of the chunk]
+    __shared__ __align__(16) float Vc[kScoreRows * 32];  // [row of the chunk][column of the slice]
+    __shared__ float O[kMtBlk][33];
+    const int h = blockIdx.x, tb = blockIdx.y * kMtBlk, d0 = 32 * blockIdx.z, tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6, kvh = h / (H / HKV), row = HKV * D;
+    const int nt = min(kMtBlk, T - tb), n_hi = kv_pos + tb + nt, n_lo = kv_pos + tb + 1;
+    const int n_me = kv_pos + tb + lane + 1;  // rows of token lane
+    const int nch = (n_hi + kScoreRows - 1) / kScoreRows;
+    float acc[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) acc[k] = 0.0f;
+    for (int c = 0; c < nch; c++) {
+        const int j0 = c * kScoreRows;
+        for (int qi = tid; qi < kMtBlk * kScoreRows; qi += 256) {
+            const int tt = qi / kScoreRows, jj = qi % kScoreRows, t = tb + tt, j = j0 + jj;
+            float w = 0.0f;
+            if (tt < nt && j <= kv_pos + t)  // the reference's scores[j] *= inv_sum
+                w = sc[((int64_t)t * H + h) * ld + j] * inv_in[(int64_t)t * H + h];
+            W[tt * kMtEP + jj] = w;
+        }
+        for (int qi = tid; qi < kScoreRows * 8; qi += 256) {
+            const int jj = qi >> 3, c4 = qi & 7, j = min(j0 + jj, n_hi - 1);
+            reinterpret_cast<float4*>(Vc)[qi] = Cache<CT>::ld4(vc + (int64_t)j * row + (int64_t)kvh * D + d0 + 4 * c4);
+        }
+        __syncthreads();
+        const float* wr = W + lane * kMtEP;
+        const float4* v4 = reinterpret_cast<const float4*>(Vc) + 2 * wave;
+        if (j0 + kScoreRows <= n_lo) {  // every token of the block has all 64 rows
+            for (int jj = 0; jj < kScoreRows; jj++) {
+                const float w = wr[jj];
+                const float4 va = v4[jj * 8], vb = v4[jj * 8 + 1];
+                acc[0] = acc[0] + va.x * w;
+                acc[1] = acc[1] + va.y * w;
+                acc[2] = acc[2] + va.z * w;
+                acc[3] = acc[3] + va.w * w;
+                acc[4] = acc[4] + vb.x * w;
+                acc[5] = acc[5] + vb.y * w;
+                acc[6] = acc[6] + vb.z * w;
+                acc[7] = acc[7] + vb.w * w;
+            }
+        } else {
+            for (int jj = 0; jj < kScoreRows; jj++) {
+                if (j0 + jj >= n_me) break;  // token lane's last row
+                const float w = wr[jj];
+                const float4 va = v4[jj * 8], vb = v4[jj * 8 + 1];
+                acc[0] = acc[0] + va.x * w;
+                acc[1] = acc[1] + va.y * w;
+                acc[2] = acc[2] + va.z * w;
+                acc[3] = acc[3] + va.w * w;
+                acc[4] = acc[4] + vb.x * w;
+                acc[5] = acc[5] + vb.y * w;
+                acc[6] = acc[6] + vb.z * w;
+                acc[7] = acc[7] + vb.w * w;
+            }
+        }
+        __syncthreads();
+    }
+    if (lane < nt) {
+        float* o = out + ((int64_t)(tb + lane) * H + h) * D + d0 + 8 * wave;
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            o[k] = acc[k];
+            O[lane][8 * wave + k] = acc[k];
+        }
+    }
+    if (xq == nullptr) return;
+    __syncthreads();
+    // Q8_0 of each token's 32 columns: lanes 0-31 one token, 32-63 the next
+    const int e = lane & 31;
+    for (int tt = 2 * wave + (lane >> 5); tt < nt; tt += 8) {
+        const int64_t blk = ((int64_t)(tb + tt) * H * D + (int64_t)h * D + d0) / 32;
+        q8_0_lane_store(O[tt][e], xq + blk * kQ80Bytes, e);
+    }
+}
+
 // x = x + y over n floats (bpd_add_f32_cpu, bench/bpd_cpu.c:5466), n % 4 == 0.
 __global__ __launch_bounds__(256) void k_add(float* __restrict__ x, const float* __restrict__ y, int64_t n4) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -992,6 +1199,9 @@ hipError_t lds_limits_for() {
         if (err == hipSuccess)
             err = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize,
                                       (kScoreRows * score_pitch(kMaxHeadDim) + kMaxEmbd + 2 * kMaxHeadDim + 4) * 4);
+    if (err == hipSuccess)
+        err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_mt_scores_tile<CT>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     return err;
 }
 
@@ -1516,7 +1726,8 @@ struct MtCtx {
     const RopeCS* tab;    // [T][kRopeSlots]
     uint8_t* xq;          // Q8_0 rows of the current GEMM input, [T][max(E,F)/32][34]
     float* scores;        // [tc][H][ld]
-    int ld, tc;           // score row length (kv_pos + T) and tokens per attention launch
+    float* inv;           // [tc][H] softmax 1/S of the tile path
+    int ld, tc;           // score row pitch (kv_pos + T rounded up to 64) and tokens per attention launch
     float scale;
 };
 
@@ -1528,13 +1739,13 @@ size_t host_region_bytes(int T) { return 2 * align256((size_t)T * 4) + align256(
 uint8_t* mt_workspace(MtCtx& c, WsLease& lease, size_t extra, const char* fn) {
     const BlockGeo& g = c.g;
     const int kmax = g.F > g.E ? g.F : g.E;
-    c.ld = c.kv_pos + c.T;
+    c.ld = pad64(c.kv_pos + c.T);
     const size_t per_tok = (size_t)g.H * c.ld * 4;
     const size_t budget = (size_t)64 << 20;  // scores of at most 64 MiB per attention launch
     c.tc = (int)std::max<size_t>(1, std::min<size_t>(std::min<size_t>((size_t)c.T, 32768), budget / per_tok));
     const size_t hb = host_region_bytes(c.T), qb = align256((size_t)c.T * (kmax / 32) * kQ80Bytes);
-    const size_t sb = align256((size_t)c.tc * per_tok);
-    lease = workspace(hb + qb + sb + extra, c.s, fn);
+    const size_t sb = align256((size_t)c.tc * per_tok), ib = align256((size_t)c.tc * g.H * 4);
+    lease = workspace(hb + qb + sb + ib + extra, c.s, fn);
     uint8_t* ws = static_cast<uint8_t*>(lease.ptr);
     if (ws == nullptr) return nullptr;
     c.ids = reinterpret_cast<const int32_t*>(ws);
@@ -1542,7 +1753,8 @@ uint8_t* mt_workspace(MtCtx& c, WsLease& lease, size_t extra, const char* fn) {
     c.tab = reinterpret_cast<const RopeCS*>(ws + 2 * align256((size_t)c.T * 4));
     c.xq = ws + hb;
     c.scores = reinterpret_cast<float*>(ws + hb + qb);
-    return ws + hb + qb + sb;
+    c.inv = reinterpret_cast<float*>(ws + hb + qb + sb);
+    return ws + hb + qb + sb + ib;
 }
 
 // Copies the token ids (or none), positions and rotation angles to the head of
@@ -1576,25 +1788,41 @@ void mt_gemm(const MtCtx& c, const uint8_t* W, float* out, int mw, int K) {
         launch_q8_0_dispatch_T(W, c.xq, out, mw, c.T, K, c.s);
 }
 
-// Attention of the batch: out[T][H*D] and its Q8_0 rows in c.xq.
+// Attention of the batch: out[T][H*D] and its Q8_0 rows in c.xq.  The tile
+// kernels (k_mt_scores_tile, k_mt_softmax, k_mt_pv) when the scores tile fits in
+// LDS (G * head_dim <= 2,048 at head_dim <= 256: every llama shape), otherwise
+// the decode kernels with one grid row per token.
 template <typename CT>
 void mt_attention(const MtCtx& c, const float* q, const CT* kc, const CT* vc, float* out) {
     const BlockGeo& g = c.g;
     const int group = g.H / g.HKV;
-    const size_t slds = ((size_t)kScoreRows * score_pitch(g.D) + (size_t)group * g.D + 4) * 4;
     const int row = g.HKV * g.D;
+    const bool tile = mt_scores_lds(group, g.D) <= 160 * 1024;
+    const dim3 ts(64 * (group < kMaxGroup ? group : kMaxGroup));
     for (int t0 = 0; t0 < c.T; t0 += c.tc) {
         const int tn = std::min(c.tc, c.T - t0), n_max = c.kv_pos + t0 + tn;
+        float* o = out + (int64_t)t0 * g.H * g.D;
+        uint8_t* xq = c.xq + (int64_t)t0 * (g.H * g.D / 32) * kQ80Bytes;
+        const float* qt = q + (int64_t)t0 * g.H * g.D;
+        if (tile) {
+            const dim3 gs((n_max + kScoreRows - 1) / kScoreRows, g.HKV, (tn + kMtTok - 1) / kMtTok);
+            hipLaunchKernelGGL((k_mt_scores_tile<CT>), gs, ts, mt_scores_lds(group, g.D), c.s, qt, kc, c.scores, c.ld,
+                               c.kv_pos + t0, tn, g.H, g.HKV, g.D, c.scale);
+            const int nb = (tn + kMtBlk - 1) / kMtBlk;
+            hipLaunchKernelGGL((k_mt_softmax<kMtSmThreads>), dim3(g.H, nb), dim3(kMtSmThreads), 0, c.s, c.scores,
+                               c.inv, c.ld, c.kv_pos + t0, tn, g.H);
+            hipLaunchKernelGGL((k_mt_pv<CT>), dim3(g.H, nb, g.D / 32), dim3(256), 0, c.s, c.scores, c.inv, vc, o, xq,
+                               c.ld, c.kv_pos + t0, tn, g.H, g.HKV, g.D);
+            continue;
+        }
+        const size_t slds = ((size_t)kScoreRows * score_pitch(g.D) + (size_t)group * g.D + 4) * 4;
         const dim3 gs((n_max + kScoreRows - 1) / kScoreRows, g.HKV, tn);
-        const dim3 ts(64 * (group < kMaxGroup ? group : kMaxGroup));
-        hipLaunchKernelGGL((k_mt_scores<CT>), gs, ts, slds, c.s, q + (int64_t)t0 * g.H * g.D, kc, c.scores, c.ld,
-                           c.kv_pos + t0, g.H, g.HKV, g.D, c.scale);
+        hipLaunchKernelGGL((k_mt_scores<CT>), gs, ts, slds, c.s, qt, kc, c.scores, c.ld, c.kv_pos + t0, g.H, g.HKV,
+                           g.D, c.scale);
         const AttnIn ai{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, const_cast<CT*>(kc), const_cast<CT*>(vc),
                         group, row, g.D, c.kv_pos + t0, c.scale, c.g.rot};
         const dim3 gp(g.H * (g.D / 32), tn);
         const size_t lds = (size_t)pad64(n_max) * 4;
-        float* o = out + (int64_t)t0 * g.H * g.D;
-        uint8_t* xq = c.xq + (int64_t)t0 * (g.H * g.D / 32) * kQ80Bytes;
         if (n_max >= kPvBigMin && n_max <= kPvBigMax)
             hipLaunchKernelGGL((k_attn_pv<128, 32, CT>), gp, dim3(kPvThreads), lds, c.s, ai, c.scores, c.ld, o, xq);
         else

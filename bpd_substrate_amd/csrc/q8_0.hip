@@ -1123,25 +1123,32 @@ struct __align__(16) GemmLdsH {
     uint32_t db[2][kGH][kGT + 1];
 };
 
+// Staging passes: 64*RT + 2*kGT staging threads (a pair per W row and per
+// token) over the 128*RT threads of the workgroup.
 template <int RT>
-__device__ __forceinline__ void half_load(uint32_t (&raw)[17], const uint8_t* __restrict__ W,
+__host__ __device__ constexpr int h_passes() { return (64 * RT + 2 * kGT + 128 * RT - 1) / (128 * RT); }
+
+template <int RT>
+__device__ __forceinline__ void half_load(uint32_t (&raw)[h_passes<RT>()][17], const uint8_t* __restrict__ W,
                                           const uint8_t* __restrict__ X, int m0, int n0, int m_weight, int m_tokens,
                                           int b0, int64_t bpr) {
-    // threads past the last staged row repeat its loads (the store skips them)
-    const int t = min((int)threadIdx.x, 64 * RT + 2 * kGT - 1);
-    const int p = h_part(t), q = h_row(t);
-    const bool wrow = q < 32 * RT;
-    const int row = wrow ? q : q - 32 * RT;
-    const uint8_t* src = wrow ? W + (int64_t)min(m0 + row, m_weight - 1) * bpr
-                              : X + (int64_t)min(n0 + row, m_tokens - 1) * bpr;
-    src += (int64_t)(b0 + 2 * p) * kQ80Bytes;
 #pragma unroll
-    for (int k = 0; k < 17; k++) raw[k] = *reinterpret_cast<const uint32_t*>(src + 4 * k);
+    for (int ps = 0; ps < h_passes<RT>(); ps++) {
+        // threads past the last staged row repeat its loads (the store skips them)
+        const int t = min((int)threadIdx.x + ps * 128 * RT, 64 * RT + 2 * kGT - 1);
+        const int p = h_part(t), q = h_row(t);
+        const bool wrow = q < 32 * RT;
+        const int row = wrow ? q : q - 32 * RT;
+        const uint8_t* src = wrow ? W + (int64_t)min(m0 + row, m_weight - 1) * bpr
+                                  : X + (int64_t)min(n0 + row, m_tokens - 1) * bpr;
+        src += (int64_t)(b0 + 2 * p) * kQ80Bytes;
+#pragma unroll
+        for (int k = 0; k < 17; k++) raw[ps][k] = *reinterpret_cast<const uint32_t*>(src + 4 * k);
+    }
 }
 
 template <int RT>
-__device__ __forceinline__ void half_store(GemmLdsH<RT>& s, int slot, const uint32_t (&d)[17]) {
-    const int t = threadIdx.x;
+__device__ __forceinline__ void half_store_one(GemmLdsH<RT>& s, int slot, const uint32_t (&d)[17], int t) {
     if (t >= 64 * RT + 2 * kGT) return;
     const int p = h_part(t), rq = h_row(t);
     const bool wrow = rq < 32 * RT;
@@ -1160,6 +1167,12 @@ __device__ __forceinline__ void half_store(GemmLdsH<RT>& s, int slot, const uint
     uint32_t* ds1 = wrow ? &s.da[slot][2 * p + 1][row] : &s.db[slot][2 * p + 1][row];
     *ds0 = d[0] & 0xFFFFu;
     *ds1 = d[8] >> 16;
+}
+
+template <int RT>
+__device__ __forceinline__ void half_store(GemmLdsH<RT>& s, int slot, const uint32_t (&raw)[h_passes<RT>()][17]) {
+#pragma unroll
+    for (int ps = 0; ps < h_passes<RT>(); ps++) half_store_one<RT>(s, slot, raw[ps], threadIdx.x + ps * 128 * RT);
 }
 
 template <int RT>
@@ -1187,7 +1200,7 @@ __global__ __launch_bounds__(128 * RT) void k_q8_0_gemm_SH(const uint8_t* __rest
 #pragma unroll
         for (int r = 0; r < 16; r++) acc[ct][r] = 0.0f;
 
-    uint32_t raw[17];
+    uint32_t raw[h_passes<RT>()][17];
     const int nh = nb / kGH;
     // the f16 scale operands: only dword 0 changes per block, the zeros stay in place
     u32x4h a16 = {0u, 0u, 0u, 0u}, b16[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
@@ -1287,9 +1300,22 @@ void launch_q8_0_gemm_S(const uint8_t* Wq, const uint8_t* Xq, float* out, int m_
     }
     // 128 weight rows per workgroup, two 512-thread workgroups per CU.  (224 rows,
     // one 896-thread workgroup per CU, balances cfg4's 14336 rows over 256 CUs
-    // exactly but measured slower: 150.9 us vs 146.)
-    hipLaunchKernelGGL(k_q8_0_gemm_SH<4>, grid, dim3(512), 0, s, Wq, Xq, out, m_weight, m_tokens, K / 32,
-                       nan_mode);
+    // exactly but measured slower: 150.9 us vs 146.)  Fewer rows per workgroup
+    // when 128 leave CUs idle: the 4096-row Q, O and down projections of a
+    // 512-token prefill (75 -> 41 us and 243 -> 126 us at 128 -> 64 rows), the
+    // 1024-row K and V (70 -> 21 us at 32 rows).
+    const int tok_tiles = (m_tokens + kGT - 1) / kGT;
+    const auto wgs = [&](int rows) { return (int64_t)((m_weight + rows - 1) / rows) * tok_tiles; };
+    if (wgs(128) >= 256) {
+        hipLaunchKernelGGL(k_q8_0_gemm_SH<4>, grid, dim3(512), 0, s, Wq, Xq, out, m_weight, m_tokens, K / 32,
+                           nan_mode);
+    } else if (wgs(64) >= 256) {
+        hipLaunchKernelGGL(k_q8_0_gemm_SH<2>, dim3((m_weight + 63) / 64, tok_tiles), dim3(256), 0, s, Wq, Xq, out,
+                           m_weight, m_tokens, K / 32, nan_mode);
+    } else {
+        hipLaunchKernelGGL(k_q8_0_gemm_SH<1>, dim3((m_weight + 31) / 32, tok_tiles), dim3(128), 0, s, Wq, Xq, out,
+                           m_weight, m_tokens, K / 32, nan_mode);
+    }
 }
 
 }  // namespace bpdq

@@ -198,3 +198,17 @@ def test_prefill_equals_stepwise(order):
     assert_bits_equal(to_np(la).reshape(9, -1)[8], to_np(lb), "last logits row")
     assert int(to_np(ta)[8]) == int(to_np(tb)[0])
     assert torch.equal(a.k_cache, b.k_cache) and torch.equal(a.v_cache, b.v_cache)
+
+
+@pytest.mark.parametrize("kind", ["avx", "scalar"])
+@pytest.mark.parametrize("shape,calls,fill", [
+    (dict(S=256), [(130, 0)], 0),
+    (dict(H=8, HKV=2, D=32, S=256), [(70, 100), (1, 170)], 100),
+    (dict(L=1, E=512, H=4, HKV=1, D=128, F=512, V=200, S=256), [(65, 0)], 0)])
+def test_forward_token_blocks(kind, shape, calls, fill):
+    """Batches past one 64-token softmax / P.V block and one 16-token score tile,
+    from an empty cache and into a filled one (rows past a token's own but inside
+    its block's tile; chunks where every token of the block has all 64 rows and
+    chunks where only some have)."""
+    cfg = config(**shape)
+    _forward_case(cfg, kind, False, calls, fill=fill)

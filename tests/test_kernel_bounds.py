@@ -561,12 +561,19 @@ def test_fused_quantization_covers_x_and_stays_in_bounds(rows):
 
 @pytest.mark.parametrize("mw,mt,K", [(14336, 512, 4096), (130, 129, 4096), (1, 1, 128), (300, 17, 384), (256, 256, 128),
                                      (7, 5, 14336), (225, 3, 256)])
-@pytest.mark.parametrize("RT", [4])
+@pytest.mark.parametrize("RT", [4, 2, 1])
 def test_q8_0_gemm_SH_in_bounds(mw, mt, K, RT):
+    """k_q8_0_gemm_SH<RT>: 32*RT weight rows x 128 tokens per workgroup of 128*RT
+    threads, staged in h_passes passes of 128*RT staging threads (a thread pair per
+    weight row and per token); every staged row and part covered once."""
     assert K % 128 == 0  # the launcher's condition for this kernel
     nb = K // 32
     bpr = nb * Q80
-    t = np.minimum(np.arange(128 * RT), 64 * RT + 255)
+    passes = (64 * RT + 256 + 128 * RT - 1) // (128 * RT)
+    t_all = np.arange(passes * 128 * RT)
+    stored = t_all[t_all < 64 * RT + 256]
+    assert len(stored) == 64 * RT + 256 and len(set(stored.tolist())) == len(stored)
+    t = np.minimum(t_all, 64 * RT + 255)
     p, wrow = t & 1, t < 64 * RT
     row = np.where(wrow, t >> 1, (t - 64 * RT) >> 1)
     assert row.max() < max(32 * RT, 128)
