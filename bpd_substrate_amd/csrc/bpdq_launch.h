@@ -86,6 +86,9 @@ void launch_q8_pad64_dispatch_T(const uint8_t* Wp, const uint8_t* Xq, float* out
 // tiles of the dispatcher, 1 = bpd_qdot_q8_0_q8_0_cpu (the scalar build's llamafile).
 void launch_q8_0_gemm_S(const uint8_t* Wq, const uint8_t* Xq, float* out, int m_weight, int m_tokens, int K,
                         int nan_mode, hipStream_t s);
+// Up to 3 matrices of M[i] >= 1 rows sharing the activation rows Xq, one launch.
+void launch_q8_0_gemm_S_multi(const uint8_t* const* W, float* const* out, const int* M, int n, const uint8_t* Xq,
+                              int m_tokens, int K, int nan_mode, hipStream_t s);
 void launch_stream_read(const uint8_t* p, int64_t n16, uint32_t* sink, hipStream_t s);
 void launch_stream_write(uint8_t* p, int64_t n16, uint32_t value, hipStream_t s);
 void launch_mfma_i8_probe(int waves, int iters, uint32_t* sink, hipStream_t s);

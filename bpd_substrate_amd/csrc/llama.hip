@@ -32,6 +32,7 @@
 //     fp32 mean as the reference's sequential binary64 sum.
 #include <algorithm>
 #include <climits>
+#include <initializer_list>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -1788,6 +1789,25 @@ void mt_gemm(const MtCtx& c, const uint8_t* W, float* out, int mw, int K) {
         launch_q8_0_dispatch_T(W, c.xq, out, mw, c.T, K, c.s);
 }
 
+// n GEMMs of the same activation rows (Q/K/V, gate/up): order S in one launch,
+// order T one dispatch each.  (Q/K/V of 512 tokens of a Mistral-7B layer, 6144
+// rows in all: 76 us in one launch against 174 us in three, each of which left
+// most CUs idle.)
+void mt_gemm3(const MtCtx& c, std::initializer_list<const uint8_t*> W, std::initializer_list<float*> out,
+              std::initializer_list<int> M, int n, int K) {
+    const uint8_t* w[3];
+    float* o[3];
+    int m[3];
+    std::copy(W.begin(), W.end(), w);
+    std::copy(out.begin(), out.end(), o);
+    std::copy(M.begin(), M.end(), m);
+    if (c.order_s) {
+        launch_q8_0_gemm_S_multi(w, o, m, n, c.xq, c.T, K, 1, c.s);
+        return;
+    }
+    for (int i = 0; i < n; i++) mt_gemm(c, w[i], o[i], m[i], K);
+}
+
 // Attention of the batch: out[T][H*D] and its Q8_0 rows in c.xq.  The tile
 // kernels (k_mt_scores_tile, k_mt_softmax, k_mt_pv) when the scores tile fits in
 // LDS (G * head_dim <= 2,048 at head_dim <= 256: every llama shape), otherwise
@@ -1839,16 +1859,13 @@ void mt_layer(const MtCtx& c, float* x, const bpd_llama_layer_weights& w, CT* kc
     const BlockGeo& g = c.g;
     const int T = c.T, qd = g.H * g.D, kd = g.HKV * g.D;
     launch_norm(x, nullptr, nullptr, w.attn_norm_w, s1, c.xq, g.E, g.eps, c.s, nullptr, T);
-    mt_gemm(c, w.w_q, s2, qd, g.E);
-    mt_gemm(c, w.w_k, s3, kd, g.E);
-    mt_gemm(c, w.w_v, s1, kd, g.E);
+    mt_gemm3(c, {w.w_q, w.w_k, w.w_v}, {s2, s3, s1}, {qd, kd, kd}, 3, g.E);
     hipLaunchKernelGGL((k_rope_write<CT>), dim3(T), dim3(256), 0, c.s, s2, s3, s1, kc, vc, c.pos, c.tab, g.H, g.HKV,
                        g.D, g.rot);
     mt_attention<CT>(c, s2, kc, vc, s1);
     mt_gemm(c, w.w_o, s2, g.E, qd);
     launch_norm(x, s2, x, w.ffn_norm_w, s1, c.xq, g.E, g.eps, c.s, nullptr, T);
-    mt_gemm(c, w.w_gate, s2, g.F, g.E);
-    mt_gemm(c, w.w_up, s3, g.F, g.E);
+    mt_gemm3(c, {w.w_gate, w.w_up, w.w_up}, {s2, s3, s3}, {g.F, g.F, g.F}, 2, g.E);
     const int64_t tf = (int64_t)T * g.F;
     hipLaunchKernelGGL(k_swiglu, dim3((unsigned)((tf + 255) / 256)), dim3(256), 0, c.s, s2, s3, c.xq, (int)tf);
     mt_gemm(c, w.w_down, s1, g.E, g.F);

@@ -1124,18 +1124,22 @@ struct __align__(16) GemmLdsH {
 };
 
 // Staging passes: 64*RT + 2*kGT staging threads (a pair per W row and per
-// token) over the 128*RT threads of the workgroup.
-template <int RT>
-__host__ __device__ constexpr int h_passes() { return (64 * RT + 2 * kGT + 128 * RT - 1) / (128 * RT); }
+// token) over the NT threads of the workgroup.
+template <int RT, int NT>
+__host__ __device__ constexpr int h_passes() { return (64 * RT + 2 * kGT + NT - 1) / NT; }
 
-template <int RT>
-__device__ __forceinline__ void half_load(uint32_t (&raw)[h_passes<RT>()][17], const uint8_t* __restrict__ W,
+// A thread's staged words: 17 per pass.
+template <int RT, int NT>
+using HRaw = uint32_t[h_passes<RT, NT>()][17];
+
+template <int RT, int NT>
+__device__ __forceinline__ void half_load(HRaw<RT, NT>& raw, const uint8_t* __restrict__ W,
                                           const uint8_t* __restrict__ X, int m0, int n0, int m_weight, int m_tokens,
                                           int b0, int64_t bpr) {
 #pragma unroll
-    for (int ps = 0; ps < h_passes<RT>(); ps++) {
+    for (int ps = 0; ps < h_passes<RT, NT>(); ps++) {
         // threads past the last staged row repeat its loads (the store skips them)
-        const int t = min((int)threadIdx.x + ps * 128 * RT, 64 * RT + 2 * kGT - 1);
+        const int t = min((int)threadIdx.x + ps * NT, 64 * RT + 2 * kGT - 1);
         const int p = h_part(t), q = h_row(t);
         const bool wrow = q < 32 * RT;
         const int row = wrow ? q : q - 32 * RT;
@@ -1169,56 +1173,78 @@ __device__ __forceinline__ void half_store_one(GemmLdsH<RT>& s, int slot, const 
     *ds1 = d[8] >> 16;
 }
 
-template <int RT>
-__device__ __forceinline__ void half_store(GemmLdsH<RT>& s, int slot, const uint32_t (&raw)[h_passes<RT>()][17]) {
+template <int RT, int NT>
+__device__ __forceinline__ void half_store(GemmLdsH<RT>& s, int slot, const HRaw<RT, NT>& raw) {
 #pragma unroll
-    for (int ps = 0; ps < h_passes<RT>(); ps++) half_store_one<RT>(s, slot, raw[ps], threadIdx.x + ps * 128 * RT);
+    for (int ps = 0; ps < h_passes<RT, NT>(); ps++) half_store_one<RT>(s, slot, raw[ps], threadIdx.x + ps * NT);
 }
 
-template <int RT>
-__global__ __launch_bounds__(128 * RT) void k_q8_0_gemm_SH(const uint8_t* __restrict__ W,
-                                                           const uint8_t* __restrict__ X, float* __restrict__ out,
-                                                           int m_weight, int m_tokens, int nb, int nan_mode) {
+// Up to kGemmMulti weight matrices that share the activation rows X (a prefill's
+// Q, K and V) in one launch: workgroup column bx takes row block bx - first[i]
+// of matrix i.
+constexpr int kGemmMulti = 3;
+struct GemmW {
+    const uint8_t* w[kGemmMulti];
+    float* out[kGemmMulti];
+    int m[kGemmMulti];
+    int first[kGemmMulti + 1];  // row blocks before matrix i
+};
+
+// CT column tiles of 32 tokens per wave: 2 (waves of 32 rows x 64 tokens, the
+// cfg4 form) or 1 (32 x 32: twice the waves for launches that leave SIMDs with
+// one wave each).
+template <int RT, int CT>
+__global__ __launch_bounds__(64 * RT * (4 / CT)) void k_q8_0_gemm_SH(GemmW gw, const uint8_t* __restrict__ X,
+                                                                     int m_tokens, int nb, int nan_mode) {
+    constexpr int WCN = 4 / CT, NT = 64 * RT * WCN;  // waves per 32-row tile, threads
+    static_assert(CT == 1 || CT == 2, "one or two column tiles per wave");
     __shared__ GemmLdsH<RT> s;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int wr = wave >> 1, wc = wave & 1;
-    const int m0 = blockIdx.x * 32 * RT, n0 = blockIdx.y * kGT;
+    const int wr = wave / WCN, wc = wave % WCN;
+    const int bx = blockIdx.x, mi = (bx >= gw.first[1]) + (bx >= gw.first[2]);
+    const uint8_t* __restrict__ W = gw.w[mi];
+    float* __restrict__ out = gw.out[mi];
+    const int m_weight = gw.m[mi];
+    const int m0 = (bx - gw.first[mi]) * 32 * RT, n0 = blockIdx.y * kGT;
     const int64_t bpr = (int64_t)nb * kQ80Bytes;
     const int col = lane & 31, half = lane >> 5;
     const int ra = wr * 32 + col;
     // lanes 32-63 give K indices 8-15 of the scale MFMA: they read the zero rows
     const int za = half ? 32 * RT : ra;
-    for (int i = threadIdx.x; i < 2 * kGH; i += 128 * RT) {
+    for (int i = threadIdx.x; i < 2 * kGH; i += NT) {
         s.da[i / kGH][i % kGH][32 * RT] = 0u;
         s.db[i / kGH][i % kGH][kGT] = 0u;
     }
 
-    float acc[2][16];
+    float acc[CT][16];
 #pragma unroll
-    for (int ct = 0; ct < 2; ct++)
+    for (int ct = 0; ct < CT; ct++)
 #pragma unroll
         for (int r = 0; r < 16; r++) acc[ct][r] = 0.0f;
 
-    uint32_t raw[h_passes<RT>()][17];
+    HRaw<RT, NT> raw;
     const int nh = nb / kGH;
     // the f16 scale operands: only dword 0 changes per block, the zeros stay in place
-    u32x4h a16 = {0u, 0u, 0u, 0u}, b16[2] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
-    half_load<RT>(raw, W, X, m0, n0, m_weight, m_tokens, 0, bpr);
-    half_store<RT>(s, 0, raw);
+    u32x4h a16 = {0u, 0u, 0u, 0u}, b16[CT];
+#pragma unroll
+    for (int ct = 0; ct < CT; ct++) b16[ct] = u32x4h{0u, 0u, 0u, 0u};
+    half_load<RT, NT>(raw, W, X, m0, n0, m_weight, m_tokens, 0, bpr);
+    half_store<RT, NT>(s, 0, raw);
     __syncthreads();
 
     for (int h = 0; h < nh; h++) {
         const int slot = h & 1;
-        if (h + 1 < nh) half_load<RT>(raw, W, X, m0, n0, m_weight, m_tokens, (h + 1) * kGH, bpr);
+        if (h + 1 < nh) half_load<RT, NT>(raw, W, X, m0, n0, m_weight, m_tokens, (h + 1) * kGH, bpr);
         // block pairs: the swizzle of the operand reads changes once per pair (the
         // pair loop unrolled, the block loop not: 117.7 against 120.2 us at cfg4;
         // both unrolled spill)
 #pragma unroll
         for (int pu = 0; pu < kGH / 2; pu++) {
         const int offa = 16 * (half ^ h_swz(ra, 2 * pu));
-        const int offb0 = 16 * (half ^ h_swz(wc * 64 + col, 2 * pu));
-        const int offb1 = 16 * (half ^ h_swz(wc * 64 + 32 + col, 2 * pu));
+        int offb[CT];
+#pragma unroll
+        for (int ct = 0; ct < CT; ct++) offb[ct] = 16 * (half ^ h_swz(wc * 32 * CT + ct * 32 + col, 2 * pu));
 #pragma unroll 1
         for (int u = 2 * pu; u < 2 * pu + 2; u++) {
             const i32x4 fa = *reinterpret_cast<const i32x4*>(&s.qa[slot][u][ra][offa]);
@@ -1230,9 +1256,9 @@ __global__ __launch_bounds__(128 * RT) void k_q8_0_gemm_SH(const uint8_t* __rest
             // passes: 134 -> 123 us at cfg4.)
             a16[0] = s.da[slot][u][za];
 #pragma unroll
-            for (int ct = 0; ct < 2; ct++) {
-                const int cb = wc * 64 + ct * 32 + col;
-                const i32x4 fb = *reinterpret_cast<const i32x4*>(&s.qb[slot][u][cb][ct ? offb1 : offb0]);
+            for (int ct = 0; ct < CT; ct++) {
+                const int cb = wc * 32 * CT + ct * 32 + col;
+                const i32x4 fb = *reinterpret_cast<const i32x4*>(&s.qb[slot][u][cb][offb[ct]]);
                 b16[ct][0] = s.db[slot][u][half ? kGT : cb];
                 const i32x16 zero = {0};
                 const f32x16 fzero = {0.0f};
@@ -1248,15 +1274,15 @@ __global__ __launch_bounds__(128 * RT) void k_q8_0_gemm_SH(const uint8_t* __rest
         }
         }
         // the other slot was last read before the previous barrier
-        if (h + 1 < nh) half_store<RT>(s, slot ^ 1, raw);
+        if (h + 1 < nh) half_store<RT, NT>(s, slot ^ 1, raw);
         __syncthreads();
     }
 
     // register r of lane l is row 8(r/4) + 4(l/32) + r%4 of the tile: runs of 4 rows
     const bool full_rows = m0 + wr * 32 + 32 <= m_weight && (m_weight & 3) == 0;
 #pragma unroll
-    for (int ct = 0; ct < 2; ct++) {
-        const int tok = n0 + wc * 64 + ct * 32 + col;
+    for (int ct = 0; ct < CT; ct++) {
+        const int tok = n0 + wc * 32 * CT + ct * 32 + col;
         if (tok >= m_tokens) continue;
         // NaN cells take the reference's bits (rare: only Inf / NaN scales make them)
         bool any_nan = false;
@@ -1285,37 +1311,76 @@ __global__ __launch_bounds__(128 * RT) void k_q8_0_gemm_SH(const uint8_t* __rest
     }
 }
 
-void launch_q8_0_gemm_S(const uint8_t* Wq, const uint8_t* Xq, float* out, int m_weight, int m_tokens, int K,
-                        int nan_mode, hipStream_t s) {
-    if (K / 32 == 0) {  // the kernel indexes block nb-1
-        launch_fill_zero(out, (int64_t)m_weight * m_tokens, s);
-        return;
+template <int RT, int CT>
+static void launch_sh(const uint8_t* const* W, float* const* out, const int* M, int n, const uint8_t* Xq, int m_tokens,
+                      int K, int nan_mode, hipStream_t s) {
+    GemmW g{};
+    int blocks = 0;
+    for (int i = 0; i < kGemmMulti; i++) {
+        g.first[i] = blocks;
+        if (i < n) {
+            g.w[i] = W[i];
+            g.out[i] = out[i];
+            g.m[i] = M[i];
+            blocks += (M[i] + 32 * RT - 1) / (32 * RT);
+        } else {
+            g.w[i] = W[0];
+            g.out[i] = out[0];
+            g.m[i] = M[0];
+        }
     }
-    const dim3 grid((m_weight + kGT - 1) / kGT, (m_tokens + kGT - 1) / kGT);
-    const bool aligned = K % 128 == 0 && (reinterpret_cast<uintptr_t>(Wq) & 3) == 0 &&
-                         (reinterpret_cast<uintptr_t>(Xq) & 3) == 0;
-    if (!aligned) {
-        hipLaunchKernelGGL(k_q8_0_gemm_S, grid, dim3(256), 0, s, Wq, Xq, out, m_weight, m_tokens, K / 32, nan_mode);
+    g.first[kGemmMulti] = blocks;
+    hipLaunchKernelGGL((k_q8_0_gemm_SH<RT, CT>), dim3(blocks, (m_tokens + kGT - 1) / kGT), dim3(64 * RT * (4 / CT)),
+                       0, s, g, Xq, m_tokens, K / 32, nan_mode);
+}
+
+// n <= kGemmMulti matrices (M[i] rows each, M[i] >= 1) sharing the activation rows
+// Xq: out[i][token * M[i] + row].
+void launch_q8_0_gemm_S_multi(const uint8_t* const* W, float* const* out, const int* M, int n, const uint8_t* Xq,
+                              int m_tokens, int K, int nan_mode, hipStream_t s) {
+    bool aligned = K % 128 == 0 && (reinterpret_cast<uintptr_t>(Xq) & 3) == 0;
+    for (int i = 0; i < n; i++) aligned = aligned && (reinterpret_cast<uintptr_t>(W[i]) & 3) == 0;
+    if (K / 32 == 0 || !aligned) {
+        for (int i = 0; i < n; i++) {
+            if (K / 32 == 0) {  // the kernel indexes block nb-1
+                launch_fill_zero(out[i], (int64_t)M[i] * m_tokens, s);
+                continue;
+            }
+            const dim3 grid((M[i] + kGT - 1) / kGT, (m_tokens + kGT - 1) / kGT);
+            hipLaunchKernelGGL(k_q8_0_gemm_S, grid, dim3(256), 0, s, W[i], Xq, out[i], M[i], m_tokens, K / 32,
+                               nan_mode);
+        }
         return;
     }
     // 128 weight rows per workgroup, two 512-thread workgroups per CU.  (224 rows,
     // one 896-thread workgroup per CU, balances cfg4's 14336 rows over 256 CUs
-    // exactly but measured slower: 150.9 us vs 146.)  Fewer rows per workgroup
-    // when 128 leave CUs idle: the 4096-row Q, O and down projections of a
-    // 512-token prefill (75 -> 41 us and 243 -> 126 us at 128 -> 64 rows), the
-    // 1024-row K and V (70 -> 21 us at 32 rows).
+    // exactly but measured slower: 150.9 us vs 146.)  64 or 32 rows when 128
+    // leave CUs idle: the 4096-row and 1024-row projections of a 512-token
+    // prefill.
     const int tok_tiles = (m_tokens + kGT - 1) / kGT;
-    const auto wgs = [&](int rows) { return (int64_t)((m_weight + rows - 1) / rows) * tok_tiles; };
-    if (wgs(128) >= 256) {
-        hipLaunchKernelGGL(k_q8_0_gemm_SH<4>, grid, dim3(512), 0, s, Wq, Xq, out, m_weight, m_tokens, K / 32,
-                           nan_mode);
-    } else if (wgs(64) >= 256) {
-        hipLaunchKernelGGL(k_q8_0_gemm_SH<2>, dim3((m_weight + 63) / 64, tok_tiles), dim3(256), 0, s, Wq, Xq, out,
-                           m_weight, m_tokens, K / 32, nan_mode);
-    } else {
-        hipLaunchKernelGGL(k_q8_0_gemm_SH<1>, dim3((m_weight + 31) / 32, tok_tiles), dim3(128), 0, s, Wq, Xq, out,
-                           m_weight, m_tokens, K / 32, nan_mode);
-    }
+    const auto wgs = [&](int rows) {
+        int64_t b = 0;
+        for (int i = 0; i < n; i++) b += (M[i] + rows - 1) / rows;
+        return b * tok_tiles;
+    };
+    // Waves of 32 rows x 64 tokens at 128 rows, of 32 x 32 below it: a launch with
+    // fewer than 256 128-row workgroups has fewer than 2 such waves per SIMD.
+    // (A 512-token prefill's 4096-row O and down: 53 and 178 us in 32 x 32 waves,
+    // 63 and 221 us in 32 x 64 waves, with bit-identical outputs.)
+    if (wgs(128) >= 256)
+        launch_sh<4, 2>(W, out, M, n, Xq, m_tokens, K, nan_mode, s);
+    else if (wgs(64) >= 256)
+        launch_sh<2, 1>(W, out, M, n, Xq, m_tokens, K, nan_mode, s);
+    else
+        launch_sh<1, 1>(W, out, M, n, Xq, m_tokens, K, nan_mode, s);
+}
+
+void launch_q8_0_gemm_S(const uint8_t* Wq, const uint8_t* Xq, float* out, int m_weight, int m_tokens, int K,
+                        int nan_mode, hipStream_t s) {
+    const uint8_t* w[1] = {Wq};
+    float* o[1] = {out};
+    const int m[1] = {m_weight};
+    launch_q8_0_gemm_S_multi(w, o, m, 1, Xq, m_tokens, K, nan_mode, s);
 }
 
 }  // namespace bpdq

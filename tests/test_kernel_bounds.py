@@ -562,15 +562,19 @@ def test_fused_quantization_covers_x_and_stays_in_bounds(rows):
 @pytest.mark.parametrize("mw,mt,K", [(14336, 512, 4096), (130, 129, 4096), (1, 1, 128), (300, 17, 384), (256, 256, 128),
                                      (7, 5, 14336), (225, 3, 256)])
 @pytest.mark.parametrize("RT", [4, 2, 1])
-def test_q8_0_gemm_SH_in_bounds(mw, mt, K, RT):
-    """k_q8_0_gemm_SH<RT>: 32*RT weight rows x 128 tokens per workgroup of 128*RT
-    threads, staged in h_passes passes of 128*RT staging threads (a thread pair per
-    weight row and per token); every staged row and part covered once."""
+@pytest.mark.parametrize("CT", [2, 1])
+def test_q8_0_gemm_SH_in_bounds(mw, mt, K, RT, CT):
+    """k_q8_0_gemm_SH<RT, CT>: 32*RT weight rows x 128 tokens per workgroup of
+    NT = 64*RT*(4/CT) threads (waves of 32 rows x 32*CT tokens), staged in
+    h_passes passes of NT staging threads (a thread pair per weight row and per
+    token); every staged row and part covered once."""
     assert K % 128 == 0  # the launcher's condition for this kernel
     nb = K // 32
     bpr = nb * Q80
-    passes = (64 * RT + 256 + 128 * RT - 1) // (128 * RT)
-    t_all = np.arange(passes * 128 * RT)
+    wcn = 4 // CT
+    nt = 64 * RT * wcn
+    passes = (64 * RT + 256 + nt - 1) // nt
+    t_all = np.arange(passes * nt)
     stored = t_all[t_all < 64 * RT + 256]
     assert len(stored) == 64 * RT + 256 and len(set(stored.tolist())) == len(stored)
     t = np.minimum(t_all, 64 * RT + 255)
@@ -591,14 +595,17 @@ def test_q8_0_gemm_SH_in_bounds(mw, mt, K, RT):
     # 32-63: the zero rows 32*RT and 128, which the arrays hold as their last row)
     lane = np.arange(64)
     col, half = lane & 31, lane >> 5
-    for wave in range(2 * RT):
-        wr, wc = wave >> 1, wave & 1
+    cover = np.zeros((32 * RT, 128), dtype=int)
+    for wave in range(RT * wcn):
+        wr, wc = wave // wcn, wave % wcn
         ra = wr * 32 + col
         za = np.where(half == 1, 32 * RT, ra)
         assert za.max() <= 32 * RT and ra.max() < 32 * RT
-        for ct in range(2):
-            cb = wc * 64 + ct * 32 + col
+        for ct in range(CT):
+            cb = wc * 32 * CT + ct * 32 + col
             assert cb.max() < 128 and np.where(half == 1, 128, cb).max() <= 128
+            cover[wr * 32:(wr + 1) * 32, wc * 32 * CT + ct * 32:wc * 32 * CT + ct * 32 + 32] += 1
+    assert (cover == 1).all()  # every (row, token) of the tile computed by one wave
 
 
 def h_swz(row, b):
