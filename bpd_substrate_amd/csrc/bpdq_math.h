@@ -35,6 +35,11 @@ static __constant__ uint64_t kExp2fTab[32] = {
 // tab: the 32 entries of kExp2fTab, wherever the caller keeps them (a kernel
 // with many exps per lane copies them to LDS: a per-lane index into constant
 // memory is a vector load from the cache hierarchy for every call).
+//
+// Branch-free: the main steps run for every input (the table index is masked,
+// so any input reads inside the table), and the special results of |x| >= 88
+// replace them by selects, so a lane's exps are straight-line code that the
+// compiler can interleave (branches per exp serialize each table read).
 __device__ __forceinline__ float expf_libm(float x, const uint64_t* tab = kExp2fTab) {
     constexpr double kN = 32.0;
     constexpr double kInvLn2N = 0x1.71547652b82fep+0 * kN;
@@ -44,12 +49,6 @@ __device__ __forceinline__ float expf_libm(float x, const uint64_t* tab = kExp2f
     constexpr double kC2 = 0x1.62e42ff0c52d6p-1 / kN;
     const uint32_t ux = __float_as_uint(x);
     const uint32_t abstop = (ux >> 20) & 0x7ffu;
-    if (abstop >= 0x42bu) {                       // |x| >= 88, Inf or NaN
-        if (ux == 0xff800000u) return 0.0f;       // -Inf
-        if (abstop >= 0x7f8u) return x + x;       // +Inf, NaN
-        if (x > 0x1.62e42ep6f) return __uint_as_float(0x7f800000u);  // overflow
-        if (x < -0x1.9fe368p6f) return 0.0f;                          // underflow
-    }
     const double xd = (double)x;
     double kd = __builtin_fma(kInvLn2N, xd, kShift);
     const uint64_t ki = (uint64_t)__double_as_longlong(kd);
@@ -62,7 +61,19 @@ __device__ __forceinline__ float expf_libm(float x, const uint64_t* tab = kExp2f
     double y = __builtin_fma(kC2, r, 1.0);
     y = __builtin_fma(z, r2, y);
     y = y * s;
-    return (float)y;
+    float out = (float)y;
+    // The empty asm takes the main result and x together and hands both on, so
+    // the selects below depend on the main steps and the compiler cannot sink
+    // those steps into a branch taken only when no special case applies.
+    float xs = x;
+    asm("" : "+v"(out), "+v"(xs));
+    // |x| >= 88, Inf or NaN (each condition below implies it): underflow, overflow,
+    // +Inf and NaN (x + x), -Inf (0), in the order that lets the later one win
+    out = xs < -0x1.9fe368p6f ? 0.0f : out;
+    out = xs > 0x1.62e42ep6f ? __uint_as_float(0x7f800000u) : out;
+    out = abstop >= 0x7f8u ? xs + xs : out;
+    out = ux == 0xff800000u ? 0.0f : out;
+    return out;
 }
 
 }  // namespace bpdq

@@ -208,6 +208,7 @@ struct Cache<float> {
     static __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
     static __device__ __forceinline__ void st(float* p, float v) { *p = v; }
     static __device__ __forceinline__ float rt(float v) { return v; }  // the value as read back
+    static __device__ __forceinline__ float cvt1(float r) { return r; }
 };
 __device__ __forceinline__ uint32_t f32_to_f16_ref(float v) {
     const uint32_t u = __float_as_uint(v);
@@ -228,6 +229,7 @@ struct Cache<uint16_t> {
     static __device__ __forceinline__ float4 ld4(const uint16_t* p) { return cvt(ldr(p)); }
     static __device__ __forceinline__ void st(uint16_t* p, float v) { *p = (uint16_t)f32_to_f16_ref(v); }
     static __device__ __forceinline__ float rt(float v) { return f16_to_f32_ref(f32_to_f16_ref(v)); }
+    static __device__ __forceinline__ float cvt1(uint16_t r) { return f16_to_f32_ref(r); }
 };
 
 struct AttnIn {
@@ -989,11 +991,16 @@ __host__ __device__ constexpr size_t mt_scores_lds(int G, int D) {
     return ((size_t)kScoreRows * score_pitch(D) + (size_t)kMtTok * G * D + 4) * 4;
 }
 
-template <typename CT>
+// 8 waves in REPS = 16 / TPW token subsets: with REPS > 1 (the host keeps
+// G * REPS <= 8) wave w takes head w % G of the kv head's group and tokens
+// TPW(w / G) .. +TPW-1 of the block; with REPS = 1 wave w takes heads w, w + 8, ...
+// and all 16 tokens.
+template <typename CT, int TPW>
 __global__ __launch_bounds__(64 * kMaxGroup) void k_mt_scores_tile(const float* __restrict__ q,
                                                                    const CT* __restrict__ kc, float* __restrict__ sc,
                                                                    int ld, int kv_pos, int T, int H, int HKV, int D,
                                                                    float scale) {
+    static_assert(kMtTok % TPW == 0, "token subsets of the block");
     extern __shared__ float4 sm4[];
     const int G = H / HKV, D4 = D / 4, P4 = score_pitch(D) / 4, row = HKV * D;
     const int j0 = blockIdx.x * kScoreRows, kvh = blockIdx.y, t0 = blockIdx.z * kMtTok;
@@ -1005,167 +1012,315 @@ __global__ __launch_bounds__(64 * kMaxGroup) void k_mt_scores_tile(const float* 
     float4* spare = qs4 + kMtTok * G * D4;
     const int rows = min(kScoreRows, n_hi - j0);
     rows_to_lds<CT>(kt, spare, kc, j0, rows, row, (int64_t)kvh * D, D4, P4);
-    for (int f = threadIdx.x; f < kMtTok * G * D4; f += blockDim.x) {
-        const int tt = f / (G * D4), r = f % (G * D4);
-        qs4[f] = tt < nt ? reinterpret_cast<const float4*>(q + ((int64_t)(t0 + tt) * H + kvh * G) * D)[r]
-                         : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    // the block's q rows, 4 loads in flight per thread before any LDS write (every
+    // write happens, past the end into `spare`, so no load sinks into a branch)
+    const int nq = kMtTok * G * D4;
+    for (int f0 = threadIdx.x; f0 < nq; f0 += 4 * (int)blockDim.x) {
+        float4 t[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int f = min(f0 + u * (int)blockDim.x, nq - 1), tt = f / (G * D4), r = f % (G * D4);
+            t[u] = tt < nt ? reinterpret_cast<const float4*>(q + ((int64_t)(t0 + tt) * H + kvh * G) * D)[r]
+                           : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int f = f0 + u * (int)blockDim.x;
+            *(f < nq ? qs4 + f : spare) = t[u];
+        }
     }
     __syncthreads();
     if (lane >= rows) return;
     const float4* kr = kt + lane * P4;
-    for (int h = wave; h < G; h += nw) {
-        float s[kMtTok];
+    constexpr int REPS = kMtTok / TPW;
+    const int sub = REPS == 1 ? 0 : wave / G, ts0 = TPW * sub;
+    if (sub >= REPS) return;
+    for (int h = REPS == 1 ? wave : wave % G; h < G; h += REPS == 1 ? nw : G) {
+        float s[TPW];
 #pragma unroll
-        for (int tt = 0; tt < kMtTok; tt++) s[tt] = 0.0f;
+        for (int tt = 0; tt < TPW; tt++) s[tt] = 0.0f;
         for (int i = 0; i < D4; i++) {
             const float4 k4 = kr[i];
 #pragma unroll
-            for (int tt = 0; tt < kMtTok; tt++) s[tt] = dot_step(s[tt], qs4[(tt * G + h) * D4 + i], k4);
+            for (int tt = 0; tt < TPW; tt++) s[tt] = dot_step(s[tt], qs4[((ts0 + tt) * G + h) * D4 + i], k4);
         }
 #pragma unroll
-        for (int tt = 0; tt < kMtTok; tt++)
-            if (tt < nt) sc[((int64_t)(t0 + tt) * H + kvh * G + h) * ld + j0 + lane] = s[tt] * scale;
+        for (int tt = 0; tt < TPW; tt++)
+            if (ts0 + tt < nt) sc[((int64_t)(t0 + ts0 + tt) * H + kvh * G + h) * ld + j0 + lane] = s[tt] * scale;
     }
 }
 
-constexpr int kMtSmThreads = 512;  // wave 0 chains, waves 1-7 produce the exps
-constexpr int kMtEP = kScoreRows + 4;  // LDS pitch of a token's chunk of e / weights
+constexpr int kMtSmThreads = 512;  // thread p: row quad p % 16 of tokens p / 16 and p / 16 + 32
+constexpr int kMtSmGroup = 8;      // 64-row chunks of e in LDS at once
+constexpr int kMtEP = kScoreRows + 4;  // LDS pitch of a token's chunk of weights (P.V)
+
+// LDS pitch of a token's e rows in k_mt_softmax: a group of up to kMtSmGroup
+// chunks plus 4 floats, so the chain lanes' float4 reads (one token each, rows
+// 4 banks apart) are conflict-free.
+__host__ __device__ constexpr int mt_sm_pitch(int nch) {
+    return kScoreRows * (nch < kMtSmGroup ? nch : kMtSmGroup) + 4;
+}
+__host__ __device__ constexpr size_t mt_sm_lds(int nch) { return (size_t)kMtBlk * mt_sm_pitch(nch) * 4; }
+
+// The chunks g0 .. g0+kMtSmGroup-1 of one token row (float4 jq of each; rows
+// past the last chunk are not read).  Every load is issued before any is used.
+__device__ __forceinline__ void mt_sm_load(float4 (&v)[kMtSmGroup], const float* row, bool has, int g0, int nch) {
+#pragma unroll
+    for (int c = 0; c < kMtSmGroup; c++)
+        v[c] = has && g0 + c < nch ? *reinterpret_cast<const float4*>(row + kScoreRows * (g0 + c))
+                                   : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+}
 
 template <int NT>
-__global__ __launch_bounds__(NT) void k_mt_softmax(float* __restrict__ sc, float* __restrict__ inv_out, int ld,
-                                                   int kv_pos, int T, int H) {
-    __shared__ __align__(16) float E[2][kMtBlk * kMtEP];
-    __shared__ float red[NT / 64][kMtBlk];
+__global__ __launch_bounds__(NT) void k_mt_softmax(float* __restrict__ sc, int ld, int kv_pos, int T, int H) {
+    static_assert(NT == 512 && kMtBlk == 64, "16 threads per token row, two tokens per thread");
+    extern __shared__ float4 sm_e4[];
+    float* E = reinterpret_cast<float*>(sm_e4);  // [token][EP]: e of the group's rows, +0.0 past the token's
     __shared__ uint64_t etab[32];
-    const int h = blockIdx.x, tb = blockIdx.y * kMtBlk, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int nt = min(kMtBlk, T - tb), n_hi = kv_pos + tb + nt;
-    if (tid < 32) etab[tid] = kExp2fTab[tid];
-    // the max of token lane's row (order-free; NaN never wins), each wave a quarter
-    // ... an eighth of the rows, then across the waves
-    {
-        const int t = tb + lane, n = kv_pos + t + 1;
-        float m = -1e38f;
-        if (lane < nt) {
-            const float* r = sc + ((int64_t)t * H + h) * ld;
-            for (int j = wave; j < n; j += NT / 64) m = r[j] > m ? r[j] : m;
-        }
-        red[wave][lane] = m;
-    }
-    __syncthreads();
-    float mx = red[0][lane];
+    __shared__ float inv_s[kMtBlk];
+    const int h = blockIdx.x, tb = blockIdx.y * kMtBlk, p = threadIdx.x, jq = p & 15, lane = p & 63;
+    const int nt = min(kMtBlk, T - tb), n_hi = kv_pos + tb + nt, nch = (n_hi + kScoreRows - 1) / kScoreRows;
+    const int ng = (nch + kMtSmGroup - 1) / kMtSmGroup, EP = mt_sm_pitch(nch);
+    if (p < 32) etab[p] = kExp2fTab[p];
+    int tt[2], nrow[2];
+    bool has[2];
+    float* row[2];
 #pragma unroll
-    for (int w = 1; w < NT / 64; w++) mx = red[w][lane] > mx ? red[w][lane] : mx;
-    __syncthreads();
-    if (wave == 0) red[0][lane] = mx;  // token lane's max, for the producers
-    __syncthreads();
-    const int nch = (n_hi + kScoreRows - 1) / kScoreRows;
-    float sum = 0.0f;
-    // chunk c: the producers fill E[c & 1] (barrier), then wave 0 adds it while
-    // they fill the other slot; E[c & 1] is written again after the barrier of
-    // step c + 1, which wave 0 reaches only when it has added chunk c
-    for (int c = 0; c < nch; c++) {
-        if (wave > 0) {
-            float* Ec = E[c & 1];
-            for (int qi = tid - 64; qi < kMtBlk * kScoreRows; qi += NT - 64) {
-                const int tt = qi / kScoreRows, jj = qi % kScoreRows, t = tb + tt, j = c * kScoreRows + jj;
-                float e = -0.0f;  // past token tt's rows: sum + -0.0 == sum
-                if (tt < nt && j <= kv_pos + t) {
-                    float* p = sc + ((int64_t)t * H + h) * ld + j;
-                    e = expf_libm(*p - red[0][tt], etab);
-                    *p = e;
+    for (int k = 0; k < 2; k++) {
+        tt[k] = (p >> 4) + 32 * k;
+        has[k] = tt[k] < nt;
+        nrow[k] = kv_pos + tb + tt[k] + 1;  // rows of the token
+        row[k] = sc + ((int64_t)(tb + (has[k] ? tt[k] : 0)) * H + h) * ld + 4 * jq;
+    }
+    // the max of each token's row (order-free: every candidate is compared with >
+    // and NaN never wins), over the thread's quads, then the token's 16 lanes
+    float4 v[2][kMtSmGroup];
+    float m[2] = {-1e38f, -1e38f};
+    for (int g = 0; g < ng; g++) {
+#pragma unroll
+        for (int k = 0; k < 2; k++) mt_sm_load(v[k], row[k], has[k], kMtSmGroup * g, nch);
+#pragma unroll
+        for (int k = 0; k < 2; k++)
+#pragma unroll
+            for (int c = 0; c < kMtSmGroup; c++) {
+                const int j = kScoreRows * (kMtSmGroup * g + c) + 4 * jq;
+                const float x[4] = {v[k][c].x, v[k][c].y, v[k][c].z, v[k][c].w};
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    if (j + i < nrow[k] && has[k]) m[k] = x[i] > m[k] ? x[i] : m[k];
+            }
+    }
+#pragma unroll
+    for (int k = 0; k < 2; k++)
+#pragma unroll
+        for (int o = 8; o >= 1; o >>= 1) {
+            const float y = __shfl_xor(m[k], o, 16);
+            m[k] = y > m[k] ? y : m[k];
+        }
+    __syncthreads();  // etab
+    float sum = 0.0f;  // lane t of wave 0: token t's chain
+    for (int g = 0; g < ng; g++) {
+        if (g > 0) __syncthreads();  // the chain has read the previous group
+        if (ng > 1) {  // one group: the registers still hold it
+#pragma unroll
+            for (int k = 0; k < 2; k++) mt_sm_load(v[k], row[k], has[k], kMtSmGroup * g, nch);
+        }
+        // e = expf(v - m) over the scores in place, and into LDS; past the token's rows
+        // expf(-Inf) = +0.0, which leaves the chain unchanged (it starts at +0.0 and adds
+        // only values >= +0.0, so it is never -0.0)
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            if (!has[k]) continue;
+#pragma unroll
+            for (int c = 0; c < kMtSmGroup; c++) {
+                const int cc = kMtSmGroup * g + c, j = kScoreRows * cc + 4 * jq;
+                if (cc >= nch) break;
+                const float x[4] = {v[k][c].x, v[k][c].y, v[k][c].z, v[k][c].w};
+                float e[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) e[i] = expf_libm(j + i < nrow[k] ? x[i] - m[k] : -INFINITY, etab);
+                v[k][c] = make_float4(e[0], e[1], e[2], e[3]);
+                if (ng > 1) {  // kept for the weights pass
+                    float* dst = row[k] + kScoreRows * cc;
+                    if (j + 3 < nrow[k]) {
+                        *reinterpret_cast<float4*>(dst) = v[k][c];
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < 4; i++)
+                            if (j + i < nrow[k]) dst[i] = e[i];
+                    }
                 }
-                Ec[tt * kMtEP + jj] = e;
+                *reinterpret_cast<float4*>(E + tt[k] * EP + kScoreRows * c + 4 * jq) = v[k][c];
             }
         }
         __syncthreads();
-        if (wave == 0) {
-            const float4* col = reinterpret_cast<const float4*>(E[c & 1] + lane * kMtEP);
-            float4 a[16];
+        if (p < 64) {
+            // token lane's chain over the group's rows in order, one chunk's 16 float4
+            // read ahead of the adds
+            const float4* col = reinterpret_cast<const float4*>(E + lane * EP);
+            const int gc = min(kMtSmGroup, nch - kMtSmGroup * g);
+            float4 a[16], b[16];
             read_group<16>(a, col, 0);
-            __builtin_amdgcn_sched_barrier(0);
-            sum_group<16>(sum, a);
+            for (int c = 0; c < gc; c += 2) {
+                read_group<16>(b, col, c + 1 < gc ? c + 1 : c);  // past the group: a re-read, never added
+                __builtin_amdgcn_sched_barrier(0);
+                sum_group<16>(sum, a);
+                __builtin_amdgcn_sched_barrier(0);
+                if (c + 1 >= gc) break;
+                read_group<16>(a, col, c + 2 < gc ? c + 2 : c + 1);
+                __builtin_amdgcn_sched_barrier(0);
+                sum_group<16>(sum, b);
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
     }
-    if (wave == 0 && lane < nt) inv_out[(int64_t)(tb + lane) * H + h] = sum == 0.0f ? 0.0f : 1.0f / sum;
+    if (p < 64) inv_s[p] = sum == 0.0f ? 0.0f : 1.0f / sum;
+    __syncthreads();  // also orders each thread's e stores before its reloads
+    // the weights w = RN(e * inv) over the scores (the reference's scores[j] *=
+    // inv_sum), for the token's rows only
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        if (!has[k]) continue;
+        const float inv = inv_s[tt[k]];
+        for (int g = 0; g < ng; g++) {
+            if (ng > 1) mt_sm_load(v[k], row[k], true, kMtSmGroup * g, nch);
+#pragma unroll
+            for (int c = 0; c < kMtSmGroup; c++) {
+                const int cc = kMtSmGroup * g + c, j = kScoreRows * cc + 4 * jq;
+                if (cc >= nch) break;
+                const float4 w = make_float4(v[k][c].x * inv, v[k][c].y * inv, v[k][c].z * inv, v[k][c].w * inv);
+                float* dst = row[k] + kScoreRows * cc;
+                if (j + 3 < nrow[k]) {
+                    *reinterpret_cast<float4*>(dst) = w;
+                } else {
+                    const float wv[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+                        if (j + i < nrow[k]) dst[i] = wv[i];
+                }
+            }
+        }
+    }
+}
+
+// k_mt_pv: grid (heads, 64-token blocks, 64-column slices), 4 waves, each
+// 32 tokens x 32 columns: lane (tg, cg) = (lane / 8, lane % 8) holds tokens
+// 4tg..4tg+3 x columns 4cg..4cg+3 of its wave's tile, 16 chains
+// acc = RN(acc + RN(v * w)) in row order.  Per row a lane reads one float4 of V
+// (its 4 columns) and one of the transposed weights (its 4 tokens), so each
+// operand feeds 4 chains and LDS carries a quarter of what one token or one
+// column per lane would need.  Chunks of 64 rows are staged in two LDS slots
+// (chunk c + 1 written while c is added): the weights the softmax left over the
+// scores, transposed to [row][token], and the V rows converted to fp32.  Rows
+// past a token's count are skipped by a select, never added.  The heaviest
+// token blocks (the last) are numbered first.
+constexpr int kPvTok = 64;   // tokens per workgroup
+constexpr int kPvCols = 64;  // columns per workgroup
+
+template <typename CT>
+struct MtPvStage {
+    float4 w[4];                   // float4 f = tid + 256k: token f % 64, rows 4(f / 64)..+3
+    typename Cache<CT>::Raw v[4];  // float4 f: row f / 16, columns 4(f % 16)..+3
+};
+
+template <typename CT>
+__device__ __forceinline__ void mt_pv_load(MtPvStage<CT>& st, const float* __restrict__ wsc, const CT* __restrict__ vbase,
+                                           int j0, int tb, int nt, int h, int H, int ld, int n_hi, int row, int ncol) {
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        // consecutive lanes take consecutive tokens, so the transposed LDS writes
+        // of a wave hit 64 different banks
+        const int f = (int)threadIdx.x + 256 * k, tt = min(f & 63, nt - 1);  // past the block: its last token
+        st.w[k] = *reinterpret_cast<const float4*>(wsc + ((int64_t)(tb + tt) * H + h) * ld + j0 + 4 * (f >> 6));
+        const int j = min(j0 + (f >> 4), n_hi - 1);  // past n_hi: a re-read, never used
+        st.v[k] = Cache<CT>::ldr(vbase + (int64_t)j * row + min(4 * (f & 15), ncol - 4));
+    }
 }
 
 template <typename CT>
-__global__ __launch_bounds__(256) void k_mt_pv(const float* __restrict__ sc, const float* __restrict__ inv_in,
-                                                const CT* __restrict__ vc, float* __restrict__ out,
-                                                uint8_t* __restrict__ xq, int ld, int kv_pos, int T, int H, int HKV,
-                                                int D) {
-    __shared__ __align__(16) float W[kMtBlk * kMtEP];   // [token][row of the chunk]
-    __shared__ __align__(16) float Vc[kScoreRows * 32];  // [row of the chunk][column of the slice]
-    __shared__ float O[kMtBlk][33];
-    const int h = blockIdx.x, tb = blockIdx.y * kMtBlk, d0 = 32 * blockIdx.z, tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6, kvh = h / (H / HKV), row = HKV * D;
-    const int nt = min(kMtBlk, T - tb), n_hi = kv_pos + tb + nt, n_lo = kv_pos + tb + 1;
-    const int n_me = kv_pos + tb + lane + 1;  // rows of token lane
-    const int nch = (n_hi + kScoreRows - 1) / kScoreRows;
-    float acc[8];
+__device__ __forceinline__ void mt_pv_store(const MtPvStage<CT>& st, float* Wt, float* Vs) {
 #pragma unroll
-    for (int k = 0; k < 8; k++) acc[k] = 0.0f;
+    for (int k = 0; k < 4; k++) {
+        const int f = (int)threadIdx.x + 256 * k, tt = f & 63, r = 4 * (f >> 6);
+        Wt[(r + 0) * kPvTok + tt] = st.w[k].x;
+        Wt[(r + 1) * kPvTok + tt] = st.w[k].y;
+        Wt[(r + 2) * kPvTok + tt] = st.w[k].z;
+        Wt[(r + 3) * kPvTok + tt] = st.w[k].w;
+        reinterpret_cast<float4*>(Vs)[f] = Cache<CT>::cvt(st.v[k]);
+    }
+}
+
+__device__ __forceinline__ void pv_fma4(float (&acc)[4][4], const float4& v, const float4& w) {
+    const float wk[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        acc[k][0] = acc[k][0] + v.x * wk[k];
+        acc[k][1] = acc[k][1] + v.y * wk[k];
+        acc[k][2] = acc[k][2] + v.z * wk[k];
+        acc[k][3] = acc[k][3] + v.w * wk[k];
+    }
+}
+
+template <typename CT>
+__global__ __launch_bounds__(256) void k_mt_pv(const float* __restrict__ wsc, const CT* __restrict__ vc,
+                                                float* __restrict__ out, uint8_t* __restrict__ xq, int ld, int kv_pos,
+                                                int T, int H, int HKV, int D) {
+    __shared__ __align__(16) float Wt[2][kScoreRows * kPvTok];   // [slot][row][token]
+    __shared__ __align__(16) float Vs[2][kScoreRows * kPvCols];  // [slot][row][column]
+    const int h = blockIdx.x, tb = (gridDim.y - 1 - blockIdx.y) * kPvTok, d0 = kPvCols * blockIdx.z;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, th = wave >> 1, ch = wave & 1;
+    const int tg = lane >> 3, cg = lane & 7;
+    const int kvh = h / (H / HKV), row = HKV * D, ncol = min(kPvCols, D - d0);
+    const int nt = min(kPvTok, T - tb), n_hi = kv_pos + tb + nt, nch = (n_hi + kScoreRows - 1) / kScoreRows;
+    const CT* vbase = vc + (int64_t)kvh * D + d0;
+    const int tw = 32 * th + 4 * tg, cw = 32 * ch + 4 * cg;  // the lane's first token and column in the block
+    // rows of the wave's first token, and of the lane's 4 tokens
+    const int n_wave = kv_pos + tb + 32 * th + 1, n_lane = kv_pos + tb + tw + 1;
+    float acc[4][4];
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[k][i] = 0.0f;
+    MtPvStage<CT> st;
+    mt_pv_load<CT>(st, wsc, vbase, 0, tb, nt, h, H, ld, n_hi, row, ncol);
+    mt_pv_store<CT>(st, Wt[0], Vs[0]);
+    if (nch > 1) mt_pv_load<CT>(st, wsc, vbase, kScoreRows, tb, nt, h, H, ld, n_hi, row, ncol);
+    __syncthreads();
     for (int c = 0; c < nch; c++) {
         const int j0 = c * kScoreRows;
-        for (int qi = tid; qi < kMtBlk * kScoreRows; qi += 256) {
-            const int tt = qi / kScoreRows, jj = qi % kScoreRows, t = tb + tt, j = j0 + jj;
-            float w = 0.0f;
-            if (tt < nt && j <= kv_pos + t)  // the reference's scores[j] *= inv_sum
-                w = sc[((int64_t)t * H + h) * ld + j] * inv_in[(int64_t)t * H + h];
-            W[tt * kMtEP + jj] = w;
-        }
-        for (int qi = tid; qi < kScoreRows * 8; qi += 256) {
-            const int jj = qi >> 3, c4 = qi & 7, j = min(j0 + jj, n_hi - 1);
-            reinterpret_cast<float4*>(Vc)[qi] = Cache<CT>::ld4(vc + (int64_t)j * row + (int64_t)kvh * D + d0 + 4 * c4);
-        }
-        __syncthreads();
-        const float* wr = W + lane * kMtEP;
-        const float4* v4 = reinterpret_cast<const float4*>(Vc) + 2 * wave;
-        if (j0 + kScoreRows <= n_lo) {  // every token of the block has all 64 rows
+        const float4* v4 = reinterpret_cast<const float4*>(Vs[c & 1] + cw);
+        const float4* w4 = reinterpret_cast<const float4*>(Wt[c & 1] + tw);
+        if (j0 + kScoreRows <= n_wave) {  // every token of the wave has all 64 rows (uniform)
+#pragma unroll 4
+            for (int jj = 0; jj < kScoreRows; jj++) pv_fma4(acc, v4[jj * (kPvCols / 4)], w4[jj * (kPvTok / 4)]);
+        } else if (j0 < n_wave + 31) {  // some token of the wave has rows here
             for (int jj = 0; jj < kScoreRows; jj++) {
-                const float w = wr[jj];
-                const float4 va = v4[jj * 8], vb = v4[jj * 8 + 1];
-                acc[0] = acc[0] + va.x * w;
-                acc[1] = acc[1] + va.y * w;
-                acc[2] = acc[2] + va.z * w;
-                acc[3] = acc[3] + va.w * w;
-                acc[4] = acc[4] + vb.x * w;
-                acc[5] = acc[5] + vb.y * w;
-                acc[6] = acc[6] + vb.z * w;
-                acc[7] = acc[7] + vb.w * w;
-            }
-        } else {
-            for (int jj = 0; jj < kScoreRows; jj++) {
-                if (j0 + jj >= n_me) break;  // token lane's last row
-                const float w = wr[jj];
-                const float4 va = v4[jj * 8], vb = v4[jj * 8 + 1];
-                acc[0] = acc[0] + va.x * w;
-                acc[1] = acc[1] + va.y * w;
-                acc[2] = acc[2] + va.z * w;
-                acc[3] = acc[3] + va.w * w;
-                acc[4] = acc[4] + vb.x * w;
-                acc[5] = acc[5] + vb.y * w;
-                acc[6] = acc[6] + vb.z * w;
-                acc[7] = acc[7] + vb.w * w;
-            }
-        }
-        __syncthreads();
-    }
-    if (lane < nt) {
-        float* o = out + ((int64_t)(tb + lane) * H + h) * D + d0 + 8 * wave;
+                const float4 v = v4[jj * (kPvCols / 4)], w = w4[jj * (kPvTok / 4)];
+                const float wk[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-        for (int k = 0; k < 8; k++) {
-            o[k] = acc[k];
-            O[lane][8 * wave + k] = acc[k];
+                for (int k = 0; k < 4; k++) {
+                    const bool on = j0 + jj < n_lane + k;  // row inside token tw + k's count
+                    acc[k][0] = on ? acc[k][0] + v.x * wk[k] : acc[k][0];
+                    acc[k][1] = on ? acc[k][1] + v.y * wk[k] : acc[k][1];
+                    acc[k][2] = on ? acc[k][2] + v.z * wk[k] : acc[k][2];
+                    acc[k][3] = on ? acc[k][3] + v.w * wk[k] : acc[k][3];
+                }
+            }
         }
+        // the other slot was last read before the previous barrier
+        if (c + 1 < nch) mt_pv_store<CT>(st, Wt[(c + 1) & 1], Vs[(c + 1) & 1]);
+        if (c + 2 < nch) mt_pv_load<CT>(st, wsc, vbase, (c + 2) * kScoreRows, tb, nt, h, H, ld, n_hi, row, ncol);
+        __syncthreads();
     }
-    if (xq == nullptr) return;
-    __syncthreads();
-    // Q8_0 of each token's 32 columns: lanes 0-31 one token, 32-63 the next
-    const int e = lane & 31;
-    for (int tt = 2 * wave + (lane >> 5); tt < nt; tt += 8) {
-        const int64_t blk = ((int64_t)(tb + tt) * H * D + (int64_t)h * D + d0) / 32;
-        q8_0_lane_store(O[tt][e], xq + blk * kQ80Bytes, e);
+    if (cw >= ncol) return;  // whole 8-lane groups (ncol is a multiple of 32)
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        if (tw + k >= nt) break;
+        const int64_t o = ((int64_t)(tb + tw + k) * H + h) * D + d0 + cw;
+        const float4 r = make_float4(acc[k][0], acc[k][1], acc[k][2], acc[k][3]);
+        *reinterpret_cast<float4*>(out + o) = r;
+        // Q8_0 of the token's 32 columns of this wave: the 8 lanes of tg, 4 each
+        if (xq != nullptr) q8_0_quad_store(r, xq + (o >> 5) * kQ80Bytes, cg);
     }
 }
 
@@ -1200,10 +1355,17 @@ hipError_t lds_limits_for() {
         if (err == hipSuccess)
             err = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize,
                                       (kScoreRows * score_pitch(kMaxHeadDim) + kMaxEmbd + 2 * kMaxHeadDim + 4) * 4);
-    if (err == hipSuccess)
-        err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_mt_scores_tile<CT>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    for (const void* f : {reinterpret_cast<const void*>(&k_mt_scores_tile<CT, 16>),
+                          reinterpret_cast<const void*>(&k_mt_scores_tile<CT, 8>),
+                          reinterpret_cast<const void*>(&k_mt_scores_tile<CT, 4>),
+                          reinterpret_cast<const void*>(&k_mt_scores_tile<CT, 2>)})
+        if (err == hipSuccess) err = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     return err;
+}
+static_assert(mt_sm_lds(kMtSmGroup) <= 160 * 1024, "k_mt_softmax LDS");
+hipError_t lds_limits_softmax() {
+    return hipFuncSetAttribute(reinterpret_cast<const void*>(&k_mt_softmax<kMtSmThreads>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)mt_sm_lds(kMtSmGroup));
 }
 
 // The kernels that take more than 64 KB of dynamic LDS say so once per process.
@@ -1213,6 +1375,7 @@ bool lds_limits_set(const char* fn) {
     std::call_once(once, [] {
         err = lds_limits_for<float>();
         if (err == hipSuccess) err = lds_limits_for<uint16_t>();
+        if (err == hipSuccess) err = lds_limits_softmax();
         if (err == hipSuccess)
             err = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_residual_rmsnorm<kNormThreads, kNormChunks>),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, kMaxEmbd * 4);
@@ -1819,6 +1982,12 @@ void mt_attention(const MtCtx& c, const float* q, const CT* kc, const CT* vc, fl
     const int row = g.HKV * g.D;
     const bool tile = mt_scores_lds(group, g.D) <= 160 * 1024;
     const dim3 ts(64 * (group < kMaxGroup ? group : kMaxGroup));
+    // the tile kernel's token subsets: as many as fit group heads each in 8 waves (1, 2, 4 or 8)
+    const int reps = kMaxGroup / group >= 8 ? 8 : kMaxGroup / group >= 4 ? 4 : kMaxGroup / group >= 2 ? 2 : 1;
+    const auto tile_k = reps == 8 ? &k_mt_scores_tile<CT, 2>
+                        : reps == 4 ? &k_mt_scores_tile<CT, 4>
+                        : reps == 2 ? &k_mt_scores_tile<CT, 8>
+                                    : &k_mt_scores_tile<CT, 16>;
     for (int t0 = 0; t0 < c.T; t0 += c.tc) {
         const int tn = std::min(c.tc, c.T - t0), n_max = c.kv_pos + t0 + tn;
         float* o = out + (int64_t)t0 * g.H * g.D;
@@ -1826,13 +1995,14 @@ void mt_attention(const MtCtx& c, const float* q, const CT* kc, const CT* vc, fl
         const float* qt = q + (int64_t)t0 * g.H * g.D;
         if (tile) {
             const dim3 gs((n_max + kScoreRows - 1) / kScoreRows, g.HKV, (tn + kMtTok - 1) / kMtTok);
-            hipLaunchKernelGGL((k_mt_scores_tile<CT>), gs, ts, mt_scores_lds(group, g.D), c.s, qt, kc, c.scores, c.ld,
+            hipLaunchKernelGGL(tile_k, gs, dim3(64 * kMaxGroup), mt_scores_lds(group, g.D), c.s, qt, kc, c.scores, c.ld,
                                c.kv_pos + t0, tn, g.H, g.HKV, g.D, c.scale);
             const int nb = (tn + kMtBlk - 1) / kMtBlk;
-            hipLaunchKernelGGL((k_mt_softmax<kMtSmThreads>), dim3(g.H, nb), dim3(kMtSmThreads), 0, c.s, c.scores,
-                               c.inv, c.ld, c.kv_pos + t0, tn, g.H);
-            hipLaunchKernelGGL((k_mt_pv<CT>), dim3(g.H, nb, g.D / 32), dim3(256), 0, c.s, c.scores, c.inv, vc, o, xq,
-                               c.ld, c.kv_pos + t0, tn, g.H, g.HKV, g.D);
+            hipLaunchKernelGGL((k_mt_softmax<kMtSmThreads>), dim3(g.H, nb), dim3(kMtSmThreads),
+                               mt_sm_lds((n_max + kScoreRows - 1) / kScoreRows), c.s, c.scores, c.ld, c.kv_pos + t0,
+                               tn, g.H);
+            hipLaunchKernelGGL((k_mt_pv<CT>), dim3(g.H, (tn + kPvTok - 1) / kPvTok, (g.D + kPvCols - 1) / kPvCols),
+                               dim3(256), 0, c.s, c.scores, vc, o, xq, c.ld, c.kv_pos + t0, tn, g.H, g.HKV, g.D);
             continue;
         }
         const size_t slds = ((size_t)kScoreRows * score_pitch(g.D) + (size_t)group * g.D + 4) * 4;

@@ -29,6 +29,11 @@ def _d(a, dev):
 
 def test_expf_sweep(dev):
     u = np.arange(0, 2 ** 32, 251, dtype=np.uint64).astype(np.uint32)
+    # the special-case boundaries: +-Inf, +-0, the overflow / underflow thresholds
+    # and |x| = 88 (the start of the special range) with their neighbours
+    edges = np.array([0x7f800000, 0xff800000, 0, 0x80000000, 0x42b17218, 0xc2cff1b5, 0x42b00000, 0xc2b00000,
+                      0x7f7fffff, 0xff7fffff, 0x00000001, 0x80000001], dtype=np.int64)
+    u = np.concatenate([u, (edges[:, None] + np.arange(-2, 3)[None, :]).reshape(-1).astype(np.uint32)])
     x = u.view(np.float32)
     x = x[~np.isnan(x)]
     want = O.libm_expf(x)

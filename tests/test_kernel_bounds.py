@@ -923,3 +923,125 @@ def test_folded_norm_partials_fit_their_buffers(E, F):
         assert g <= 16 * 64
     # k_norm_q8k: wave b quantizes float4s b*64 .. b*64 + 63 of x and w
     assert (E // 256) * 64 * 4 == E
+
+
+# ---------------------------------------------------------------- multi-token softmax and P.V
+
+@pytest.mark.parametrize("T,kv_pos", [(1, 0), (3, 1100), (65, 0), (70, 100), (130, 0), (512, 0), (64, 448),
+                                      (40, 4000)])
+def test_mt_softmax_loads_cover_each_row_once(T, kv_pos):
+    """k_mt_softmax (64-token blocks, 512 threads): thread p reads float4 p % 16 of every
+    64-row chunk of tokens p / 16 and p / 16 + 32, in groups of 8 chunks; each (token,
+    row below its count) is read, exponentiated and written once; reads stay inside
+    the token's score row (ld = pad64(kv_pos + T)); the LDS e rows (pitch EP) hold the
+    group's 64-row chunks and the chain lanes read whole chunks of their own row."""
+    ld = (kv_pos + T + 63) // 64 * 64
+    p = np.arange(512)
+    jq = p & 15
+    for tb in range(0, T, 64):
+        nt = min(64, T - tb)
+        n_hi = kv_pos + tb + nt
+        nch = (n_hi + 63) // 64
+        assert 64 * nch <= ld
+        ng = (nch + 7) // 8
+        ep = 64 * min(nch, 8) + 4
+        assert 64 * ep * 4 <= 160 * 1024
+        seen = np.zeros((nt, 64 * nch), dtype=int)
+        for k in range(2):
+            tt = (p >> 4) + 32 * k
+            has = tt < nt
+            nrow = kv_pos + tb + tt + 1
+            for g in range(ng):
+                for c in range(8):
+                    cc = 8 * g + c
+                    if cc >= nch:
+                        continue
+                    j = 64 * cc + 4 * jq
+                    assert (j + 3 < ld).all()
+                    lds = tt * ep + 64 * c + 4 * jq
+                    assert (lds[has] + 3 < 64 * ep).all()
+                    for i in range(4):
+                        ok = has & (j + i < nrow)
+                        np.add.at(seen, (tt[ok], j[ok] + i), 1)
+        for t in range(nt):
+            n = kv_pos + tb + t + 1
+            assert (seen[t, :n] == 1).all() and (seen[t, n:] == 0).all()
+        # chain: lane t reads 16 float4 per chunk of the group (and one re-read)
+        for g in range(ng):
+            gc = min(8, nch - 8 * g)
+            lane = np.arange(64)
+            assert (lane * ep + 64 * gc <= 64 * ep).all()
+
+
+@pytest.mark.parametrize("T,kv_pos,S", [(1, 0, 64), (3, 1100, 2048), (65, 0, 256), (70, 100, 256), (512, 0, 512)])
+@pytest.mark.parametrize("H,HKV,D", [(32, 8, 128), (4, 1, 128), (8, 2, 32)])
+def test_mt_pv_staging_in_bounds(T, kv_pos, S, H, HKV, D):
+    """k_mt_pv (64 tokens x 64 columns per workgroup, 256 threads): thread tid stages
+    float4 f = tid + 256k (k < 4) of the chunk's weights (token min(f % 64, nt - 1), rows
+    4(f / 64)..+3, in the token's score row of ld = pad64(kv_pos + T) floats) and of V
+    (row min(j0 + f / 16, n_hi - 1), columns min(4(f % 16), ncol - 4)..+3 of the slice),
+    stored transposed to [row][token] and as [row][column]; lane (tg, cg) of wave (th, ch)
+    reads its 4 tokens' and 4 columns' float4 per row; every (token, column) of the
+    block belongs to one lane."""
+    ld = (kv_pos + T + 63) // 64 * 64
+    row = HKV * D
+    tid = np.arange(256)
+    for tb in range(0, T, 64):
+        nt = min(64, T - tb)
+        n_hi = kv_pos + tb + nt
+        assert n_hi <= S
+        nch = (n_hi + 63) // 64
+        assert 64 * nch <= ld
+        for d0 in range(0, D, 64):
+            ncol = min(64, D - d0)
+            assert ncol % 32 == 0
+            for c in range(nch):
+                j0 = 64 * c
+                for k in range(4):
+                    f = tid + 256 * k
+                    tt = np.minimum(f & 63, nt - 1)
+                    for h in (0, H - 1):
+                        off = ((tb + tt) * H + h) * ld + j0 + 4 * (f >> 6)
+                        assert (off + 3 < T * H * ld).all() and (j0 + 4 * (f >> 6) + 3 < ld).all()
+                    j = np.minimum(j0 + (f >> 4), n_hi - 1)
+                    col = np.minimum(4 * (f & 15), ncol - 4)
+                    assert (j < S).all() and (col + 3 < ncol).all()
+                    for kvh in (0, HKV - 1):
+                        assert ((j * row + kvh * D + d0 + col + 3) < S * row).all()
+                    r = 4 * (f >> 6)
+                    assert ((r + 3) * 64 + (f & 63) < 64 * 64).all() and (f < 1024).all()
+                    # every (row, token) of the transposed tile written once per chunk
+                    if k == 3:
+                        ff = tid[:, None] + 256 * np.arange(4)[None, :]
+                        cells = ((4 * (ff >> 6))[..., None] + np.arange(4)) * 64 + (ff & 63)[..., None]
+                        assert np.array_equal(np.sort(cells.reshape(-1)), np.arange(64 * 64))
+            own = np.zeros((64, 64), dtype=int)
+            for wave in range(4):
+                th, ch = wave >> 1, wave & 1
+                lane = np.arange(64)
+                tw, cw = 32 * th + 4 * (lane >> 3), 32 * ch + 4 * (lane & 7)
+                assert (63 * 16 + (cw + 3) // 4 < 1024).all() and (63 * 16 + (tw + 3) // 4 < 1024).all()
+                for k in range(4):
+                    for i in range(4):
+                        np.add.at(own, (tw + k, cw + i), 1)
+            assert (own == 1).all()
+
+
+@pytest.mark.parametrize("G", [1, 2, 3, 4, 5, 8, 12])
+def test_mt_scores_tile_waves_cover_every_head_and_token_once(G):
+    """k_mt_scores_tile<TPW>: the host picks REPS token subsets (as many as fit G heads
+    each into 8 waves, a power of two), TPW = 16 / REPS; wave w takes head w % G and
+    subset w / G (REPS > 1) or heads w, w + 8, ... with all 16 tokens (REPS = 1)."""
+    reps = 8 if 8 // G >= 8 else 4 if 8 // G >= 4 else 2 if 8 // G >= 2 else 1
+    tpw = 16 // reps
+    assert G * reps <= 8 or reps == 1
+    seen = np.zeros((G, 16), dtype=int)
+    for wave in range(8):
+        sub = 0 if reps == 1 else wave // G
+        if sub >= reps:
+            continue
+        h = wave if reps == 1 else wave % G
+        while h < G:
+            seen[h, tpw * sub:tpw * sub + tpw] += 1
+            h += 8 if reps == 1 else G
+    assert (seen == 1).all()
