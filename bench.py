@@ -52,6 +52,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="metric GEMV and its read floor only")
     ap.add_argument("--cpu-runs", type=int, default=10)
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only the 32-layer, 512-token prefill forward (for profiling); prints its JSON")
     return ap.parse_args()
 
 
@@ -431,6 +433,18 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     L = gpu.lib()
+    if a.prefill_only:
+        log("prefill forward only (reference CPU library ABI, 32 layers, 512 tokens)")
+        res = prefill_forward(torch, dev, gpu, synth)
+        # a read of known size (the metric's weight bytes), the reference for FETCH_SIZE
+        buf = torch.zeros(W_BYTES, dtype=torch.uint8, device=dev)
+        sink = torch.zeros(1, dtype=torch.int32, device=dev)
+        for _ in range(5):
+            L.bpdq_stream_read_gpu(buf.data_ptr(), W_BYTES // 16, sink.data_ptr())
+        torch.cuda.synchronize()
+        gpu.check()
+        print(json.dumps({"prefill_forward_32_layers_512_tokens": res}))
+        return
     stream = torch.cuda.Stream()
     T = Timer(torch, L, stream)
 

@@ -1190,6 +1190,24 @@ struct GemmW {
     int first[kGemmMulti + 1];  // row blocks before matrix i
 };
 
+// Workgroup b of nP * nT (row panels x token tiles) takes panel bx, token tile
+// by.  Workgroups go to the 8 XCDs round robin (b % 8), each with its own L2:
+// when nP divides into 8, panel p runs on XCD p % 8 and its nT token tiles are
+// numbered within one run of 8 nT workgroups, so they run together and read the
+// panel's weight rows from one L2 (numbered panel-major, tiles of one panel ran
+// a whole grid row apart, and a launch of more workgroups than fit at once read
+// each panel twice).
+__device__ __forceinline__ void sh_tile(int b, int nP, int nT, int& bx, int& by) {
+    if ((nP & 7) == 0) {
+        const int g = b / (8 * nT), r = b % (8 * nT);
+        by = r >> 3;
+        bx = 8 * g + (r & 7);
+    } else {
+        bx = b % nP;
+        by = b / nP;
+    }
+}
+
 // CT column tiles of 32 tokens per wave: 2 (waves of 32 rows x 64 tokens, the
 // cfg4 form) or 1 (32 x 32: twice the waves for launches that leave SIMDs with
 // one wave each).
@@ -1202,11 +1220,13 @@ __global__ __launch_bounds__(64 * RT * (4 / CT)) void k_q8_0_gemm_SH(GemmW gw, c
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int wr = wave / WCN, wc = wave % WCN;
-    const int bx = blockIdx.x, mi = (bx >= gw.first[1]) + (bx >= gw.first[2]);
+    int bx, by;
+    sh_tile(blockIdx.x, gw.first[kGemmMulti], (m_tokens + kGT - 1) / kGT, bx, by);
+    const int mi = (bx >= gw.first[1]) + (bx >= gw.first[2]);
     const uint8_t* __restrict__ W = gw.w[mi];
     float* __restrict__ out = gw.out[mi];
     const int m_weight = gw.m[mi];
-    const int m0 = (bx - gw.first[mi]) * 32 * RT, n0 = blockIdx.y * kGT;
+    const int m0 = (bx - gw.first[mi]) * 32 * RT, n0 = by * kGT;
     const int64_t bpr = (int64_t)nb * kQ80Bytes;
     const int col = lane & 31, half = lane >> 5;
     const int ra = wr * 32 + col;
@@ -1330,8 +1350,8 @@ static void launch_sh(const uint8_t* const* W, float* const* out, const int* M, 
         }
     }
     g.first[kGemmMulti] = blocks;
-    hipLaunchKernelGGL((k_q8_0_gemm_SH<RT, CT>), dim3(blocks, (m_tokens + kGT - 1) / kGT), dim3(64 * RT * (4 / CT)),
-                       0, s, g, Xq, m_tokens, K / 32, nan_mode);
+    hipLaunchKernelGGL((k_q8_0_gemm_SH<RT, CT>), dim3(blocks * ((m_tokens + kGT - 1) / kGT)),
+                       dim3(64 * RT * (4 / CT)), 0, s, g, Xq, m_tokens, K / 32, nan_mode);
 }
 
 // n <= kGemmMulti matrices (M[i] rows each, M[i] >= 1) sharing the activation rows

@@ -1045,3 +1045,21 @@ def test_mt_scores_tile_waves_cover_every_head_and_token_once(G):
             seen[h, tpw * sub:tpw * sub + tpw] += 1
             h += 8 if reps == 1 else G
     assert (seen == 1).all()
+
+
+@pytest.mark.parametrize("nP,nT", [(112, 4), (224, 4), (64, 4), (96, 4), (250, 4), (1, 1), (5, 2), (8, 3), (448, 1)])
+def test_q8_0_gemm_SH_tile_order(nP, nT):
+    """sh_tile: workgroup b of nP * nT takes (panel, token tile) once each; with nP
+    a multiple of 8, panel p runs on XCD p % 8 (b % 8) and its nT tiles sit within
+    one run of 8 nT consecutive workgroups."""
+    seen = set()
+    for b in range(nP * nT):
+        if nP % 8 == 0:
+            g, r = divmod(b, 8 * nT)
+            by, bx = r >> 3, 8 * g + (r & 7)
+            assert b % 8 == bx % 8 and b // (8 * nT) == bx // 8
+        else:
+            bx, by = b % nP, b // nP
+        assert 0 <= bx < nP and 0 <= by < nT
+        seen.add((bx, by))
+    assert len(seen) == nP * nT
