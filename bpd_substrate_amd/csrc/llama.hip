@@ -377,12 +377,34 @@ __device__ __forceinline__ float seq_sum(const float* __restrict__ e, int n64) {
 }
 __host__ __device__ constexpr int pad64(int n) { return (n + 63) & ~63; }
 
+// The same sum for n <= 64 over ceil(n/4) float4 (e padded with -0.0 to a
+// multiple of 4), every read issued before the first add.
+__device__ __forceinline__ float seq_sum_small(const float* __restrict__ e, int n) {
+    const float4* e4 = reinterpret_cast<const float4*>(e);
+    const int g = (n + 3) >> 2;
+    float4 a[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++)
+        if (i < g) a[i] = e4[i];
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++)
+        if (i < g) {
+            sum = sum + a[i].x;
+            sum = sum + a[i].y;
+            sum = sum + a[i].z;
+            sum = sum + a[i].w;
+        }
+    return sum;
+}
+
 // ----------------------------------------------------------------------------
 // Short contexts (pos < 64, head_dim DT <= 128): one workgroup per query head.
-// Every cache load is issued at entry: thread j < pos loads k row j into
-// registers, and the V rows 0..pos-1 go to LDS, so the kernel waits for memory
-// once.  Then RoPE, scores, max, exps, the sequential softmax sum (lane 0) and
-// the sequential P.V chains (lane d) from LDS.
+// Every global load is issued at entry, before any is used: the new q/k/v pair
+// (and biases, rotation factors) of thread p < DT/2, thread j < pos's k row
+// into registers, and the V rows 0..pos-1, so the kernel waits for memory once.
+// Then RoPE, the V rows and new rows into LDS, scores, max, exps, the
+// sequential softmax sum (lane 0) and the sequential P.V chains (lane d).
 // ----------------------------------------------------------------------------
 constexpr int kSmallCtx = 64;
 
@@ -399,23 +421,71 @@ __global__ __launch_bounds__(256) void k_attn_small(AttnIn a, RopeTab tab, float
     const int64_t ko = (int64_t)kvh * DT;
     const CT* kc = static_cast<const CT*>(a.kc);
     const CT* vc = static_cast<const CT*>(a.vc);
+    // the new rows of this head: pair p of q and of k (rotated), element d of v
+    const int64_t qo = (int64_t)head * DT;
+    const bool pr = tid < DT / 2;
+    const int i2 = 2 * (pr ? tid : 0);
+    float2 q2 = *reinterpret_cast<const float2*>(a.q + qo + i2);
+    float2 k2 = *reinterpret_cast<const float2*>(a.knew + ko + i2);
+    float vv = a.vnew[ko + (tid < DT ? tid : 0)];
+    float2 bq2 = make_float2(0.0f, 0.0f), bk2 = make_float2(0.0f, 0.0f);
+    float bv = 0.0f;
+    if (a.bq != nullptr) bq2 = *reinterpret_cast<const float2*>(a.bq + qo + i2);
+    if (a.bk != nullptr) bk2 = *reinterpret_cast<const float2*>(a.bk + ko + i2);
+    if (a.bv != nullptr) bv = a.bv[ko + (tid < DT ? tid : 0)];
+    const float rc = tab.c[pr ? tid : 0], rs = tab.s[pr ? tid : 0];
     float4 kr[D4];
     if (tid < pos) {
         const CT* p = kc + (int64_t)tid * a.row + ko;
 #pragma unroll
         for (int i = 0; i < D4; i++) kr[i] = Cache<CT>::ld4(p + 4 * i);
     }
+    typename Cache<CT>::Raw vr[VU];
 #pragma unroll
     for (int u = 0; u < VU; u++) {
         const int f = tid + u * NT, r = f / D4;
-        if (r < pos) V4[f] = Cache<CT>::ld4(vc + (int64_t)r * a.row + ko + 4 * (f % D4));
+        if (r < pos) vr[u] = Cache<CT>::ldr(vc + (int64_t)r * a.row + ko + 4 * (f % D4));
     }
     float* qs = reinterpret_cast<float*>(qs4);
     float* ks = reinterpret_cast<float*>(ks4);
     float* vs = reinterpret_cast<float*>(vs4);
-    // the first query head of each group writes cache row pos; every head takes
-    // row pos from its own LDS copy, so no workgroup reads a row another writes
-    rope_rows<CT>(a, tab, head, kvh, qs, ks, vs, true, head % a.group == 0);
+    // bias, RoPE (bpd_rope_norm_freqs_cpu: pairs below rot turn, the rest pass
+    // through), the new rows into LDS; the first query head of each group writes
+    // cache row pos; every head takes row pos from its own LDS copy, so no
+    // workgroup reads a row another writes
+    const bool wr = head % a.group == 0;
+    if (pr) {
+        float x0 = q2.x, x1 = q2.y, k0 = k2.x, k1 = k2.y;
+        if (a.bq != nullptr) {
+            x0 = x0 + bq2.x;
+            x1 = x1 + bq2.y;
+        }
+        if (a.bk != nullptr) {
+            k0 = k0 + bk2.x;
+            k1 = k1 + bk2.y;
+        }
+        const bool rot = tid < a.rot;
+        qs[i2] = rot ? x0 * rc - x1 * rs : x0;
+        qs[i2 + 1] = rot ? x0 * rs + x1 * rc : x1;
+        const float y0 = rot ? k0 * rc - k1 * rs : k0, y1 = rot ? k0 * rs + k1 * rc : k1;
+        ks[i2] = Cache<CT>::rt(y0);
+        ks[i2 + 1] = Cache<CT>::rt(y1);
+        if (wr) {
+            CT* kw = const_cast<CT*>(kc) + (int64_t)pos * a.row + ko;
+            Cache<CT>::st(kw + i2, y0);
+            Cache<CT>::st(kw + i2 + 1, y1);
+        }
+    }
+    if (tid < DT) {
+        if (a.bv != nullptr) vv = vv + bv;
+        vs[tid] = Cache<CT>::rt(vv);
+        if (wr) Cache<CT>::st(const_cast<CT*>(vc) + (int64_t)pos * a.row + ko + tid, vv);
+    }
+#pragma unroll
+    for (int u = 0; u < VU; u++) {
+        const int f = tid + u * NT, r = f / D4;
+        if (r < pos) V4[f] = Cache<CT>::cvt(vr[u]);
+    }
     __syncthreads();
     float m = -1e38f;
     if (tid < n) {
@@ -431,7 +501,7 @@ __global__ __launch_bounds__(256) void k_attn_small(AttnIn a, RopeTab tab, float
         e[tid] = -0.0f;
     __syncthreads();
     if (tid == 0) {
-        const float sum = seq_sum(e, pad64(n));
+        const float sum = seq_sum_small(e, n);
         sh_inv = sum == 0.0f ? 0.0f : 1.0f / sum;
     }
     __syncthreads();
