@@ -149,11 +149,16 @@ __global__ __launch_bounds__(NT) void k_residual_rmsnorm(const float* x_in, cons
 constexpr int kNormParts = 16;  // partials per lane held in registers (producers write <= 1024)
 __global__ __launch_bounds__(64) void k_norm_q8k(NormIn nin, uint8_t* __restrict__ xk) {
     const int lane = threadIdx.x, c = blockIdx.x * 64 + lane;
-    double pp[kNormParts];
-#pragma unroll
-    for (int k = 0; k < kNormParts; k++) pp[k] = lane + 64 * k < nin.npart ? nin.part[lane + 64 * k] : 0.0;
+    // every load issued before any is used: x and w, then the partials
+    // unconditionally (past npart: a re-read of the last one, then 0)
     const float4 x = reinterpret_cast<const float4*>(nin.x)[c];
     const float4 w = reinterpret_cast<const float4*>(nin.w)[c];
+    double pp[kNormParts];
+#pragma unroll
+    for (int k = 0; k < kNormParts; k++) {
+        const double v = nin.part[min(lane + 64 * k, max(nin.npart - 1, 0))];
+        pp[k] = lane + 64 * k < nin.npart ? v : 0.0;
+    }
     double s = 0.0;
 #pragma unroll
     for (int k = 0; k < kNormParts; k++) s += pp[k];

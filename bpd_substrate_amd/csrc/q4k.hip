@@ -1503,8 +1503,11 @@ template <int WPB>
 __device__ __forceinline__ void part_load(double (&pp)[kPartRegs], const NormIn& nin) {
 #pragma unroll
     for (int k = 0; k < kPartRegs; k++) {
+        // every load unconditional (past npart: a re-read of the last partial, then
+        // 0), so none is waited for before the next is issued
         const int i = threadIdx.x + k * 64 * WPB;
-        pp[k] = i < nin.npart ? nin.part[i] : 0.0;
+        const double v = nin.part[min(i, max(nin.npart - 1, 0))];
+        pp[k] = i < nin.npart ? v : 0.0;
     }
 }
 
