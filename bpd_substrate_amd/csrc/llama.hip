@@ -2098,12 +2098,16 @@ void mt_attention(const MtCtx& c, const float* q, const CT* kc, const CT* vc, fl
 // One layer over the batch x[T][E], with the reference block's use of its
 // scratch rows: s1 = h, v, attention output, down output; s2 = q, O output,
 // gate, SwiGLU; s3 = k, up.
+// add_in: the previous layer's down output, still to be added into x (the add
+// then runs inside this layer's first norm: x = x + add_in, then its norm).
+// defer_add: leave this layer's down output in s3 for the next norm instead of
+// adding it into x here (s3 holds up, which SwiGLU has consumed by then).
 template <typename CT>
 void mt_layer(const MtCtx& c, float* x, const bpd_llama_layer_weights& w, CT* kc, CT* vc, float* s1, float* s2,
-              float* s3) {
+              float* s3, const float* add_in = nullptr, bool defer_add = false) {
     const BlockGeo& g = c.g;
     const int T = c.T, qd = g.H * g.D, kd = g.HKV * g.D;
-    launch_norm(x, nullptr, nullptr, w.attn_norm_w, s1, c.xq, g.E, g.eps, c.s, nullptr, T);
+    launch_norm(x, add_in, add_in != nullptr ? x : nullptr, w.attn_norm_w, s1, c.xq, g.E, g.eps, c.s, nullptr, T);
     mt_gemm3(c, {w.w_q, w.w_k, w.w_v}, {s2, s3, s1}, {qd, kd, kd}, 3, g.E);
     hipLaunchKernelGGL((k_rope_write<CT>), dim3(T), dim3(256), 0, c.s, s2, s3, s1, kc, vc, c.pos, c.tab, g.H, g.HKV,
                        g.D, g.rot);
@@ -2113,6 +2117,10 @@ void mt_layer(const MtCtx& c, float* x, const bpd_llama_layer_weights& w, CT* kc
     mt_gemm3(c, {w.w_gate, w.w_up, w.w_up}, {s2, s3, s3}, {g.F, g.F, g.F}, 2, g.E);
     const int64_t tf = (int64_t)T * g.F;
     hipLaunchKernelGGL(k_swiglu, dim3((unsigned)((tf + 255) / 256)), dim3(256), 0, c.s, s2, s3, c.xq, (int)tf);
+    if (defer_add) {
+        mt_gemm(c, w.w_down, s3, g.E, g.F);
+        return;
+    }
     mt_gemm(c, w.w_down, s1, g.E, g.F);
     const int64_t n4 = (int64_t)T * g.E / 4;
     hipLaunchKernelGGL(k_add, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, c.s, x, s1, n4);
@@ -2191,14 +2199,19 @@ void llama_forward(bool order_s, const int32_t* ids, int T, const bpd_llama_weig
     float* s2 = reinterpret_cast<float*>(extra + xb + sb);
     float* s3 = reinterpret_cast<float*>(extra + xb + 2 * sb);
     launch_embed_q8_0(w->token_embd, c.ids, x, T, g.E, c.s);
+    // each layer's residual add of its down output runs in the next norm (the
+    // next layer's, or the final one)
     for (int l = 0; l < L; l++) {
+        const float* add_in = l > 0 ? s3 : nullptr;
         if (g.f16)
-            mt_layer<uint16_t>(c, x, w->layers[l], kc + l * layer_elems, vc + l * layer_elems, s1, s2, s3);
+            mt_layer<uint16_t>(c, x, w->layers[l], kc + l * layer_elems, vc + l * layer_elems, s1, s2, s3, add_in,
+                               true);
         else
             mt_layer<float>(c, x, w->layers[l], reinterpret_cast<float*>(kc) + l * layer_elems,
-                            reinterpret_cast<float*>(vc) + l * layer_elems, s1, s2, s3);
+                            reinterpret_cast<float*>(vc) + l * layer_elems, s1, s2, s3, add_in, true);
     }
-    launch_norm(x, nullptr, nullptr, w->output_norm_w, s1, c.xq, g.E, g.eps, c.s, nullptr, T);
+    launch_norm(x, L > 0 ? s3 : nullptr, L > 0 ? x : nullptr, w->output_norm_w, s1, c.xq, g.E, g.eps, c.s, nullptr,
+                T);
     mt_gemm(c, w->output_w, logits, NV, g.E);
     hipLaunchKernelGGL(k_argmax<1024>, dim3(T), dim3(1024), 0, c.s, logits, NV, nullptr, tok);
     abi_hip_ok(hipGetLastError(), fn);
