@@ -77,6 +77,7 @@ HIP_SIGNATURES = {
     "bpd_qmatmul_q8_0_s_gpu": (None, [P, P, P, I, I, I]),
     "bpd_qmatmul_q8_0_dispatch_s_gpu": (None, [P, P, P, I, I, I]),
     "bpd_qmatmul_q8_0_llamafile_s_gpu": (None, [P, P, P, I, I, I]),
+    "bpdq_q8_0_gemm_swiglu_s_gpu": (None, [P, P, P, P, I, I, I]),
     "bpdq_stream_read_gpu": (None, [P, I, P]),
     "bpdq_stream_write_gpu": (None, [P, I, ctypes.c_uint32]),
     "bpdq_mfma_i8_probe_gpu": (None, [I, I, P]),

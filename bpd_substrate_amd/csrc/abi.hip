@@ -629,6 +629,24 @@ void bpd_qdot_q8_0_q8_0_grid_s_gpu(const uint8_t* Wq, const uint8_t* Xq, float* 
     if (check_qdot_args(c, Wq, Xq, out, M, N, K, 1)) qdot_grid(Wq, Xq, out, M, N, K, false, fn);
 }
 
+// The prefill's gate/up with SwiGLU in the epilogue (order S), for tests and
+// measurement: yq = Q8_0(silu(Xq . Wg) * (Xq . Wu)), M token rows of F/32 blocks.
+void bpdq_q8_0_gemm_swiglu_s_gpu(const uint8_t* Wg, const uint8_t* Wu, const uint8_t* Xq, uint8_t* yq, int M, int F,
+                                 int K) {
+    const char* fn = "bpdq_q8_0_gemm_swiglu_s_gpu";
+    Check c(fn);
+    c.nonneg(M, "M").nonneg(F, "F").nonneg(K, "K").multiple(F, 64, "F").multiple(K, 128, "K");
+    if (!c.ok || M == 0 || F == 0) return;
+    c.ptr(Wg, 4, "Wg").ptr(Wu, 4, "Wu").ptr(Xq, 4, "Xq").ptr(yq, 2, "yq");
+    if (!c.ok) return;
+    if (K == 0) {
+        c.fail(BPDQ_ERR_SHAPE, "K", "must be positive");
+        return;
+    }
+    bpdq::launch_q8_0_gemm_S_swiglu(Wg, Wu, F, Xq, M, K, 1, yq, g_stream);
+    check_launch(fn);
+}
+
 // bpd_qmatmul_q8_0_cpu (bench/bpd_cpu.c:4295-4315): quantize the M rows of X, then the qdot grid.
 static void qmatmul_q8_0(const uint8_t* W, const float* X, float* out, int M, int N, int K, bool p_order, const char* fn) {
     Check c(fn);

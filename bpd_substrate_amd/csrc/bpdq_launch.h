@@ -89,6 +89,10 @@ void launch_q8_0_gemm_S(const uint8_t* Wq, const uint8_t* Xq, float* out, int m_
 // Up to 3 matrices of M[i] >= 1 rows sharing the activation rows Xq, one launch.
 void launch_q8_0_gemm_S_multi(const uint8_t* const* W, float* const* out, const int* M, int n, const uint8_t* Xq,
                               int m_tokens, int K, int nan_mode, hipStream_t s);
+// Gate and up (F rows each) with SwiGLU and its Q8_0 rows (yq, apart from Xq) in
+// the epilogue; false (nothing launched) when the shape does not fit.
+bool launch_q8_0_gemm_S_swiglu(const uint8_t* Wg, const uint8_t* Wu, int F, const uint8_t* Xq, int m_tokens, int K,
+                               int nan_mode, uint8_t* yq, hipStream_t s);
 void launch_stream_read(const uint8_t* p, int64_t n16, uint32_t* sink, hipStream_t s);
 void launch_stream_write(uint8_t* p, int64_t n16, uint32_t value, hipStream_t s);
 void launch_mfma_i8_probe(int waves, int iters, uint32_t* sink, hipStream_t s);

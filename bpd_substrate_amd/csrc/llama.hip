@@ -1044,19 +1044,19 @@ __global__ __launch_bounds__(64 * kMaxGroup) void k_mt_scores(const float* __res
 // k_mt_scores + k_attn_pv (the reference's per-token order), with query token t
 // attending over rows 0..n_t-1, n_t = kv_pos + t + 1.  Those kernels give each
 // (head, token) a workgroup whose chains run in one lane (the softmax sum) or 32
-// (P.V); at T = 512 that is 65,536 workgroups of mostly idle lanes.  Here lanes
-// are tokens, so one wave-instruction advances 64 tokens' chains:
+// (P.V); at T = 512 that is 65,536 workgroups of mostly idle lanes.  Here a
+// wave-instruction advances many tokens' chains:
 //   k_mt_scores_tile  grid (64-row blocks, kv heads, 16-token blocks): k rows and
-//                     the block's q rows in LDS; lane j of wave h runs 16 tokens'
-//                     dots with row j (sequential over d, 16 chains per lane).
-//   k_mt_softmax      grid (heads, 64-token blocks), 8 waves: the order-free max,
-//                     then per 64-row chunk waves 1-7 write e = expf(v - m) into
-//                     LDS and over the scores in place, and lane t of wave 0 adds
-//                     token t's e in row order; inv_t = S_t == 0 ? 0 : 1/S_t.
-//   k_mt_pv           grid (heads, 64-token blocks, head_dim/32 slices): per
-//                     64-row chunk the weights RN(e*inv) and the V rows in LDS;
-//                     lane t of wave w runs token t's chains for columns 8w..8w+7
-//                     (acc = RN(acc + RN(v*w)) in row order), then Q8_0(out).
+//                     the block's q rows in LDS; lane j of a wave runs TPW tokens'
+//                     dots with row j (sequential over d, TPW chains per lane).
+//   k_mt_softmax      grid (heads, 64-token blocks), 8 waves: each thread's score
+//                     quads in registers, the order-free max, e = expf(v - m) into
+//                     LDS, lane t of wave 0 adds token t's e in row order, then the
+//                     weights w = RN(e * inv), inv = S == 0 ? 0 : 1/S, over the scores.
+//   k_mt_pv           grid (heads, 64-token blocks, 64-column slices): per 64-row
+//                     chunk the weights (transposed) and the V rows in LDS; lane
+//                     (tg, cg) runs 4 tokens x 4 columns of chains
+//                     acc = RN(acc + RN(v*w)) in row order, then Q8_0(out).
 // Score rows are ld floats apart, ld a multiple of 64 (16-byte aligned rows).
 // ----------------------------------------------------------------------------
 constexpr int kMtTok = 16;  // tokens per scores workgroup
@@ -1965,7 +1965,7 @@ struct MtCtx {
     const RopeCS* tab;    // [T][kRopeSlots]
     uint8_t* xq;          // Q8_0 rows of the current GEMM input, [T][max(E,F)/32][34]
     float* scores;        // [tc][H][ld]
-    float* inv;           // [tc][H] softmax 1/S of the tile path
+    uint8_t* yq;          // Q8_0 rows of SwiGLU's y when gate/up write them, [T][F/32][34]
     int ld, tc;           // score row pitch (kv_pos + T rounded up to 64) and tokens per attention launch
     float scale;
 };
@@ -1983,7 +1983,7 @@ uint8_t* mt_workspace(MtCtx& c, WsLease& lease, size_t extra, const char* fn) {
     const size_t budget = (size_t)64 << 20;  // scores of at most 64 MiB per attention launch
     c.tc = (int)std::max<size_t>(1, std::min<size_t>(std::min<size_t>((size_t)c.T, 32768), budget / per_tok));
     const size_t hb = host_region_bytes(c.T), qb = align256((size_t)c.T * (kmax / 32) * kQ80Bytes);
-    const size_t sb = align256((size_t)c.tc * per_tok), ib = align256((size_t)c.tc * g.H * 4);
+    const size_t sb = align256((size_t)c.tc * per_tok), ib = align256((size_t)c.T * (g.F / 32) * kQ80Bytes);
     lease = workspace(hb + qb + sb + ib + extra, c.s, fn);
     uint8_t* ws = static_cast<uint8_t*>(lease.ptr);
     if (ws == nullptr) return nullptr;
@@ -1992,7 +1992,7 @@ uint8_t* mt_workspace(MtCtx& c, WsLease& lease, size_t extra, const char* fn) {
     c.tab = reinterpret_cast<const RopeCS*>(ws + 2 * align256((size_t)c.T * 4));
     c.xq = ws + hb;
     c.scores = reinterpret_cast<float*>(ws + hb + qb);
-    c.inv = reinterpret_cast<float*>(ws + hb + qb + sb);
+    c.yq = ws + hb + qb + sb;
     return ws + hb + qb + sb + ib;
 }
 
@@ -2019,12 +2019,13 @@ bool mt_upload(const MtCtx& c, const int32_t* ids, const int32_t* pos_ids, const
     return abi_hip_ok(hipStreamSynchronize(c.s), fn);
 }
 
-// out[T][mw] = W[mw][K] . rows of c.xq (the Q8_0 rows of the input).
-void mt_gemm(const MtCtx& c, const uint8_t* W, float* out, int mw, int K) {
+// out[T][mw] = W[mw][K] . rows of xq (the Q8_0 rows of the input; c.xq by default).
+void mt_gemm(const MtCtx& c, const uint8_t* W, float* out, int mw, int K, const uint8_t* xq = nullptr) {
+    if (xq == nullptr) xq = c.xq;
     if (c.order_s)
-        launch_q8_0_gemm_S(W, c.xq, out, mw, c.T, K, 1, c.s);  // the -O2 build's llamafile: qdot S per cell
+        launch_q8_0_gemm_S(W, xq, out, mw, c.T, K, 1, c.s);  // the -O2 build's llamafile: qdot S per cell
     else
-        launch_q8_0_dispatch_T(W, c.xq, out, mw, c.T, K, c.s);
+        launch_q8_0_dispatch_T(W, xq, out, mw, c.T, K, c.s);
 }
 
 // n GEMMs of the same activation rows (Q/K/V, gate/up): order S in one launch,
@@ -2097,7 +2098,8 @@ void mt_attention(const MtCtx& c, const float* q, const CT* kc, const CT* vc, fl
 
 // One layer over the batch x[T][E], with the reference block's use of its
 // scratch rows: s1 = h, v, attention output, down output; s2 = q, O output,
-// gate, SwiGLU; s3 = k, up.
+// gate, SwiGLU; s3 = k, up (order S with the SwiGLU epilogue writes no gate, up
+// or SwiGLU rows: y goes to c.yq as Q8_0 only).
 // add_in: the previous layer's down output, still to be added into x (the add
 // then runs inside this layer's first norm: x = x + add_in, then its norm).
 // defer_add: leave this layer's down output in s3 for the next norm instead of
@@ -2114,14 +2116,21 @@ void mt_layer(const MtCtx& c, float* x, const bpd_llama_layer_weights& w, CT* kc
     mt_attention<CT>(c, s2, kc, vc, s1);
     mt_gemm(c, w.w_o, s2, g.E, qd);
     launch_norm(x, s2, x, w.ffn_norm_w, s1, c.xq, g.E, g.eps, c.s, nullptr, T);
-    mt_gemm3(c, {w.w_gate, w.w_up, w.w_up}, {s2, s3, s3}, {g.F, g.F, g.F}, 2, g.E);
-    const int64_t tf = (int64_t)T * g.F;
-    hipLaunchKernelGGL(k_swiglu, dim3((unsigned)((tf + 255) / 256)), dim3(256), 0, c.s, s2, s3, c.xq, (int)tf);
+    // order S: SwiGLU and its Q8_0 rows in the gate/up GEMM's epilogue (into c.yq;
+    // s2 and s3 then keep no gate, up or SwiGLU rows); otherwise k_swiglu
+    const uint8_t* fq = nullptr;
+    if (c.order_s && launch_q8_0_gemm_S_swiglu(w.w_gate, w.w_up, g.F, c.xq, T, g.E, 1, c.yq, c.s)) {
+        fq = c.yq;
+    } else {
+        mt_gemm3(c, {w.w_gate, w.w_up, w.w_up}, {s2, s3, s3}, {g.F, g.F, g.F}, 2, g.E);
+        const int64_t tf = (int64_t)T * g.F;
+        hipLaunchKernelGGL(k_swiglu, dim3((unsigned)((tf + 255) / 256)), dim3(256), 0, c.s, s2, s3, c.xq, (int)tf);
+    }
     if (defer_add) {
-        mt_gemm(c, w.w_down, s3, g.E, g.F);
+        mt_gemm(c, w.w_down, s3, g.E, g.F, fq);
         return;
     }
-    mt_gemm(c, w.w_down, s1, g.E, g.F);
+    mt_gemm(c, w.w_down, s1, g.E, g.F, fq);
     const int64_t n4 = (int64_t)T * g.E / 4;
     hipLaunchKernelGGL(k_add, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, c.s, x, s1, n4);
 }

@@ -16,6 +16,7 @@
 
 #include "bpdq_device.h"
 #include "bpdq_launch.h"
+#include "bpdq_math.h"
 
 namespace bpdq {
 
@@ -1132,10 +1133,12 @@ __host__ __device__ constexpr int h_passes() { return (64 * RT + 2 * kGT + NT - 
 template <int RT, int NT>
 using HRaw = uint32_t[h_passes<RT, NT>()][17];
 
+// W2 (SwiGLU pairs, else null): staged weight rows 16RT..32RT-1 are rows
+// m0 .. m0 + 16RT - 1 of W2, the rows below them the same rows of W.
 template <int RT, int NT>
 __device__ __forceinline__ void half_load(HRaw<RT, NT>& raw, const uint8_t* __restrict__ W,
-                                          const uint8_t* __restrict__ X, int m0, int n0, int m_weight, int m_tokens,
-                                          int b0, int64_t bpr) {
+                                          const uint8_t* __restrict__ W2, const uint8_t* __restrict__ X, int m0,
+                                          int n0, int m_weight, int m_tokens, int b0, int64_t bpr) {
 #pragma unroll
     for (int ps = 0; ps < h_passes<RT, NT>(); ps++) {
         // threads past the last staged row repeat its loads (the store skips them)
@@ -1143,7 +1146,8 @@ __device__ __forceinline__ void half_load(HRaw<RT, NT>& raw, const uint8_t* __re
         const int p = h_part(t), q = h_row(t);
         const bool wrow = q < 32 * RT;
         const int row = wrow ? q : q - 32 * RT;
-        const uint8_t* src = wrow ? W + (int64_t)min(m0 + row, m_weight - 1) * bpr
+        const bool second = W2 != nullptr && row >= 16 * RT;
+        const uint8_t* src = wrow ? (second ? W2 : W) + (int64_t)min(m0 + (second ? row - 16 * RT : row), m_weight - 1) * bpr
                                   : X + (int64_t)min(n0 + row, m_tokens - 1) * bpr;
         src += (int64_t)(b0 + 2 * p) * kQ80Bytes;
 #pragma unroll
@@ -1188,6 +1192,7 @@ struct GemmW {
     float* out[kGemmMulti];
     int m[kGemmMulti];
     int first[kGemmMulti + 1];  // row blocks before matrix i
+    uint8_t* yq;                // SwiGLU pairs: Q8_0 rows of y = silu(gate) * up, m[0] / 32 blocks per token
 };
 
 // Workgroup b of nP * nT (row panels x token tiles) takes panel bx, token tile
@@ -1211,7 +1216,83 @@ __device__ __forceinline__ void sh_tile(int b, int nP, int nT, int& bx, int& by)
 // CT column tiles of 32 tokens per wave: 2 (waves of 32 rows x 64 tokens, the
 // cfg4 form) or 1 (32 x 32: twice the waves for launches that leave SIMDs with
 // one wave each).
+// The SwiGLU epilogue: waves wr >= RT/2 hold up rows, waves wr - RT/2 the same
+// gate rows (register r of lane l: row 8(r/4) + 4(l/32) + r%4 of the wave's 32,
+// token l%32 of column tile ct).  NaN cells first take the reference's bits, as
+// the plain epilogue's do; then the up tiles go through LDS (the staging slots,
+// free after the loop's last barrier) to the gate waves, which form y and its
+// Q8_0 block per token: 16 rows in lane l, 16 in lane l ^ 32.
 template <int RT, int CT>
+__device__ __forceinline__ void swiglu_epilogue(float (&acc)[CT][16], GemmLdsH<RT>& s, const GemmW& gw,
+                                                const uint8_t* __restrict__ W, const uint8_t* __restrict__ W2,
+                                                const uint8_t* __restrict__ X, int m0, int n0, int m_tokens, int nb,
+                                                int nan_mode, int wr, int wc, int lane) {
+    constexpr int WCN = 4 / CT, HR = RT / 2;  // waves per row tile, row tiles of each matrix
+    static_assert(sizeof(GemmLdsH<RT>) >= (size_t)HR * WCN * CT * 16 * 64 * 4, "up tiles fit the staging LDS");
+    const int col = lane & 31, half = lane >> 5;
+    const int64_t bpr = (int64_t)nb * kQ80Bytes;
+    const bool up = wr >= HR;
+    const int tr = up ? wr - HR : wr;  // the row tile within its matrix
+#pragma unroll
+    for (int ct = 0; ct < CT; ct++) {
+        const int tok = n0 + wc * 32 * CT + ct * 32 + col;
+        bool any_nan = false;
+#pragma unroll
+        for (int r = 0; r < 16; r++) any_nan |= __builtin_isnan(acc[ct][r]);
+        if (any_nan && tok < m_tokens) {
+            for (int r = 0; r < 16; r++) {
+                const int row = m0 + tr * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+                if (__builtin_isnan(acc[ct][r]))
+                    acc[ct][r] = s_order_nan_bits((up ? W2 : W) + row * bpr, X + tok * bpr, nb, nan_mode);
+            }
+        }
+    }
+    float* U = reinterpret_cast<float*>(&s);  // [tr][wc][ct][r][lane]
+    if (up) {
+#pragma unroll
+        for (int ct = 0; ct < CT; ct++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) U[(((tr * WCN + wc) * CT + ct) * 16 + r) * 64 + lane] = acc[ct][r];
+    }
+    __syncthreads();
+    if (up) return;
+    const int fq = gw.m[0] / 32;  // Q8_0 blocks per token row of y
+#pragma unroll
+    for (int ct = 0; ct < CT; ct++) {
+        const int tok = n0 + wc * 32 * CT + ct * 32 + col;
+        float y[16];
+        float amax = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const float g = acc[ct][r], u = U[(((tr * WCN + wc) * CT + ct) * 16 + r) * 64 + lane];
+            y[r] = (g / (1.0f + expf_libm(-g))) * u;
+            amax = fmaxf(amax, abs_no_nan(y[r]));
+        }
+        amax = fmaxf(amax, xor_f(amax, 32));  // the token's other 16 rows
+        if (tok >= m_tokens) continue;
+        const float d = amax / 127.0f;
+        const float id = q8_id(amax);
+        uint8_t* yb = gw.yq + ((int64_t)tok * fq + (m0 + tr * 32) / 32) * kQ80Bytes;
+#pragma unroll
+        for (int g4 = 0; g4 < 4; g4++) {
+            uint32_t q[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) q[i] = (uint32_t)(uint8_t)(int8_t)(int)__builtin_rintf(y[4 * g4 + i] * id);
+            // rows 8g4 + 4half .. +3: quants at bytes 2 + 8g4 + 4half, 2-byte aligned
+            uint16_t* p = reinterpret_cast<uint16_t*>(yb + 2 + 8 * g4 + 4 * half);
+            p[0] = (uint16_t)(q[0] | (q[1] << 8));
+            p[1] = (uint16_t)(q[2] | (q[3] << 8));
+        }
+        if (half == 0) *reinterpret_cast<uint16_t*>(yb) = __builtin_bit_cast(uint16_t, (_Float16)d);
+    }
+}
+
+// SWG: SwiGLU pairs.  w[0] = gate, w[1] = up (m[0] rows each): a workgroup's
+// 32RT staged rows are 16RT gate rows and the same up rows, the waves of the up
+// rows hand their tiles to the gate rows' waves through LDS, and those write
+// Q8_0(y), y = (g / (1 + expf(-g))) * u (bpd_swiglu_fuse_cpu, bench/bpd_cpu.c:5504),
+// as k_swiglu does, for each token's 32 consecutive rows; no fp32 output.
+template <int RT, int CT, bool SWG = false>
 __global__ __launch_bounds__(64 * RT * (4 / CT)) void k_q8_0_gemm_SH(GemmW gw, const uint8_t* __restrict__ X,
                                                                      int m_tokens, int nb, int nan_mode) {
     constexpr int WCN = 4 / CT, NT = 64 * RT * WCN;  // waves per 32-row tile, threads
@@ -1222,11 +1303,12 @@ __global__ __launch_bounds__(64 * RT * (4 / CT)) void k_q8_0_gemm_SH(GemmW gw, c
     const int wr = wave / WCN, wc = wave % WCN;
     int bx, by;
     sh_tile(blockIdx.x, gw.first[kGemmMulti], (m_tokens + kGT - 1) / kGT, bx, by);
-    const int mi = (bx >= gw.first[1]) + (bx >= gw.first[2]);
+    const int mi = SWG ? 0 : (bx >= gw.first[1]) + (bx >= gw.first[2]);
     const uint8_t* __restrict__ W = gw.w[mi];
+    const uint8_t* __restrict__ W2 = SWG ? gw.w[1] : nullptr;
     float* __restrict__ out = gw.out[mi];
     const int m_weight = gw.m[mi];
-    const int m0 = (bx - gw.first[mi]) * 32 * RT, n0 = by * kGT;
+    const int m0 = (bx - gw.first[mi]) * (SWG ? 16 : 32) * RT, n0 = by * kGT;
     const int64_t bpr = (int64_t)nb * kQ80Bytes;
     const int col = lane & 31, half = lane >> 5;
     const int ra = wr * 32 + col;
@@ -1249,13 +1331,13 @@ __global__ __launch_bounds__(64 * RT * (4 / CT)) void k_q8_0_gemm_SH(GemmW gw, c
     u32x4h a16 = {0u, 0u, 0u, 0u}, b16[CT];
 #pragma unroll
     for (int ct = 0; ct < CT; ct++) b16[ct] = u32x4h{0u, 0u, 0u, 0u};
-    half_load<RT, NT>(raw, W, X, m0, n0, m_weight, m_tokens, 0, bpr);
+    half_load<RT, NT>(raw, W, W2, X, m0, n0, m_weight, m_tokens, 0, bpr);
     half_store<RT, NT>(s, 0, raw);
     __syncthreads();
 
     for (int h = 0; h < nh; h++) {
         const int slot = h & 1;
-        if (h + 1 < nh) half_load<RT, NT>(raw, W, X, m0, n0, m_weight, m_tokens, (h + 1) * kGH, bpr);
+        if (h + 1 < nh) half_load<RT, NT>(raw, W, W2, X, m0, n0, m_weight, m_tokens, (h + 1) * kGH, bpr);
         // block pairs: the swizzle of the operand reads changes once per pair (the
         // pair loop unrolled, the block loop not: 117.7 against 120.2 us at cfg4;
         // both unrolled spill)
@@ -1298,6 +1380,10 @@ __global__ __launch_bounds__(64 * RT * (4 / CT)) void k_q8_0_gemm_SH(GemmW gw, c
         __syncthreads();
     }
 
+    if constexpr (SWG) {
+        swiglu_epilogue<RT, CT>(acc, s, gw, W, W2, X, m0, n0, m_tokens, nb, nan_mode, wr, wc, lane);
+        return;
+    }
     // register r of lane l is row 8(r/4) + 4(l/32) + r%4 of the tile: runs of 4 rows
     const bool full_rows = m0 + wr * 32 + 32 <= m_weight && (m_weight & 3) == 0;
 #pragma unroll
@@ -1329,6 +1415,30 @@ __global__ __launch_bounds__(64 * RT * (4 / CT)) void k_q8_0_gemm_SH(GemmW gw, c
             }
         }
     }
+}
+
+// y = silu(gate) * up in Q8_0 (yq: m_tokens rows of F/32 blocks, not Xq): false
+// when the shape does not fit the pair form (F % 64, K % 128, 4-byte alignment).
+bool launch_q8_0_gemm_S_swiglu(const uint8_t* Wg, const uint8_t* Wu, int F, const uint8_t* Xq, int m_tokens, int K,
+                               int nan_mode, uint8_t* yq, hipStream_t s) {
+    constexpr int RT = 4, CT = 2;
+    const auto al4 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3) == 0; };
+    if (F <= 0 || F % (16 * RT) != 0 || K <= 0 || K % 128 != 0 || m_tokens <= 0 || !al4(Wg) || !al4(Wu) ||
+        !al4(Xq))
+        return false;
+    GemmW g{};
+    const int panels = F / (16 * RT);
+    for (int i = 0; i < kGemmMulti; i++) {
+        g.w[i] = i == 1 ? Wu : Wg;
+        g.out[i] = nullptr;
+        g.m[i] = F;
+        g.first[i] = i == 0 ? 0 : panels;
+    }
+    g.first[kGemmMulti] = panels;
+    g.yq = yq;
+    hipLaunchKernelGGL((k_q8_0_gemm_SH<RT, CT, true>), dim3(panels * ((m_tokens + kGT - 1) / kGT)),
+                       dim3(64 * RT * (4 / CT)), 0, s, g, Xq, m_tokens, K / 32, nan_mode);
+    return true;
 }
 
 template <int RT, int CT>

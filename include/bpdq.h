@@ -205,6 +205,14 @@ void bpd_qdot_q8_0_q8_0_grid_s_gpu(const uint8_t* Wq_dev, const uint8_t* Xq_dev,
 void bpd_qmatmul_q8_0_gpu(const uint8_t* W_dev, const float* X_dev, float* out_dev, int M, int N, int K);
 void bpd_qmatmul_q8_0_s_gpu(const uint8_t* W_dev, const float* X_dev, float* out_dev, int M, int N, int K);
 
+/* ---- the prefill's fused gate/up (no counterpart in the reference) ----------
+ * Order S (as bpd_qdot_q8_0_q8_0_grid_s_gpu) for the M Q8_0 rows of Xq against the F rows of
+ * Wg and of Wu, then y = silu(g) * u (bpd_swiglu_fuse_cpu, bench/bpd_cpu.c:5504-5507) and its
+ * Q8_0 rows (bpd_quant_q8_0_cpu) into yq: M rows of F/32 blocks, as the multi-token block
+ * feeds its down projection.  F a multiple of 64, K of 128; Wg, Wu and Xq 4-byte aligned. */
+void bpdq_q8_0_gemm_swiglu_s_gpu(const uint8_t* Wg_dev, const uint8_t* Wu_dev, const uint8_t* Xq_dev,
+                                 uint8_t* yq_dev, int M, int F, int K);
+
 /* ---- measurement helper (no counterpart in the reference) -------------------
  * Reads n16 16-byte chunks at p once, as fast as a plain streaming kernel can,
  * and writes *sink only if the data XORs to a magic value.  bench.py uses it for

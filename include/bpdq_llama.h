@@ -187,7 +187,10 @@ int bpd_llama_step_ext_gpu(int weight_format, const bpd_llama_step_opts* opts, c
  * the structs, the layers array, token_ids, pos_ids and rope_freqs are host
  * memory, read before the call returns (the rotation angles are taken with
  * the host's libm, as the reference's cosf/sinf).  scratch1..3 hold at least
- * n_tokens * max(embed_dim, ffn_dim) floats each, as in the reference.
+ * n_tokens * max(embed_dim, ffn_dim) floats each, as in the reference; they are
+ * work space, and their contents after the call are not the reference's (the
+ * _s_ forms form SwiGLU inside the gate/up GEMM and never write the gate, up or
+ * SwiGLU rows).
  * token_out is int64 (the reference's long).  The calls enqueue on the
  * stream of bpd_gpu_set_stream() after one synchronization for the upload
  * of token ids, positions and angles; results are ready when that stream is.

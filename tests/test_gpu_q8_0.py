@@ -425,3 +425,34 @@ def test_qmatmul_q8_0_orders_P_and_S(dev, M, N, K):
         gpu.lib().bpd_gpu_set_stream(torch.cuda.current_stream().cuda_stream)
         gpu.call(name, _d(W, dev), _d(X, dev), out, M, N, K)
         assert_bits_equal(to_np(out), O.qmatmul_q8_0(W, X, M, N, K, order), f"qmatmul {order} {M}x{N}x{K}")
+
+
+@pytest.mark.parametrize("F,mt,K,kind", [(64, 1, 128, "plain"), (128, 5, 512, "plain"), (512, 130, 512, "plain"),
+                                         (1024, 256, 4096, "plain"), (256, 129, 256, "special"),
+                                         (192, 40, 384, "nan_heavy")])
+def test_gemm_swiglu_epilogue(dev, F, mt, K, kind):
+    """bpdq_q8_0_gemm_swiglu_s_gpu (the prefill's gate/up with SwiGLU and its Q8_0 rows in
+    the order-S GEMM's epilogue, the up tiles handed to the gate rows' waves through LDS):
+    every byte equals the oracle's order-S GEMM of each matrix, SwiGLU and Q8_0
+    quantization, with special and dense NaN / Inf scales too."""
+    import torch
+    nb = K // 32
+    if kind == "special":
+        Wg, Wu, Xq = _special(F, nb, synth.key(71, F)), _special(F, nb, synth.key(72, F)), _special(mt, nb, synth.key(73, mt))
+    elif kind == "nan_heavy":
+        Wg, Wu, Xq = (_q8_nan_heavy(F, nb, synth.key(74, F)), _q8_nan_heavy(F, nb, synth.key(75, F)),
+                      _q8_nan_heavy(mt, nb, synth.key(76, mt)))
+    else:
+        Wg, Wu = synth.q8_0(F, K, synth.key(77, F)), synth.q8_0(F, K, synth.key(78, F))
+        Xq = O.quant_q8_0(synth.normal_f32(mt * K, synth.key(79, mt)))
+    g = O.dispatch_q8_0(Wg, Xq, F, mt, K, "S", nthreads=8)
+    u = O.dispatch_q8_0(Wu, Xq, F, mt, K, "S", nthreads=8)
+    want = O.quant_q8_0(O.swiglu(g, u))
+    if kind != "plain":
+        assert np.isnan(g).any() or np.isinf(g).any()
+    yq = torch.full((mt * F // 32 * 34,), 0xA5, dtype=torch.uint8, device=dev)
+    gpu.call("bpdq_q8_0_gemm_swiglu_s_gpu", _d(Wg, dev), _d(Wu, dev), _d(Xq, dev), yq, mt, F, K)
+    gpu.check()
+    got = to_np(yq)
+    bad = np.nonzero(got != want)[0]
+    assert bad.size == 0, f"{bad.size} bytes differ, first at {bad[:8]}"
