@@ -2098,8 +2098,9 @@ void mt_attention(const MtCtx& c, const float* q, const CT* kc, const CT* vc, fl
 
 // One layer over the batch x[T][E], with the reference block's use of its
 // scratch rows: s1 = h, v, attention output, down output; s2 = q, O output,
-// gate, SwiGLU; s3 = k, up (order S with the SwiGLU epilogue writes no gate, up
-// or SwiGLU rows: y goes to c.yq as Q8_0 only).
+// gate, SwiGLU; s3 = k, up; except that the norms write no h rows (their GEMMs
+// read only the Q8_0 rows in c.xq) and order S with the SwiGLU epilogue writes
+// no gate, up or SwiGLU rows (y goes to c.yq as Q8_0 only).
 // add_in: the previous layer's down output, still to be added into x (the add
 // then runs inside this layer's first norm: x = x + add_in, then its norm).
 // defer_add: leave this layer's down output in s3 for the next norm instead of
@@ -2109,13 +2110,15 @@ void mt_layer(const MtCtx& c, float* x, const bpd_llama_layer_weights& w, CT* kc
               float* s3, const float* add_in = nullptr, bool defer_add = false) {
     const BlockGeo& g = c.g;
     const int T = c.T, qd = g.H * g.D, kd = g.HKV * g.D;
-    launch_norm(x, add_in, add_in != nullptr ? x : nullptr, w.attn_norm_w, s1, c.xq, g.E, g.eps, c.s, nullptr, T);
+    // the norms write only the Q8_0 rows their GEMM reads (no fp32 h rows)
+    launch_norm(x, add_in, add_in != nullptr ? x : nullptr, w.attn_norm_w, nullptr, c.xq, g.E, g.eps, c.s, nullptr,
+                T);
     mt_gemm3(c, {w.w_q, w.w_k, w.w_v}, {s2, s3, s1}, {qd, kd, kd}, 3, g.E);
     hipLaunchKernelGGL((k_rope_write<CT>), dim3(T), dim3(256), 0, c.s, s2, s3, s1, kc, vc, c.pos, c.tab, g.H, g.HKV,
                        g.D, g.rot);
     mt_attention<CT>(c, s2, kc, vc, s1);
     mt_gemm(c, w.w_o, s2, g.E, qd);
-    launch_norm(x, s2, x, w.ffn_norm_w, s1, c.xq, g.E, g.eps, c.s, nullptr, T);
+    launch_norm(x, s2, x, w.ffn_norm_w, nullptr, c.xq, g.E, g.eps, c.s, nullptr, T);
     // order S: SwiGLU and its Q8_0 rows in the gate/up GEMM's epilogue (into c.yq;
     // s2 and s3 then keep no gate, up or SwiGLU rows); otherwise k_swiglu
     const uint8_t* fq = nullptr;
@@ -2219,8 +2222,8 @@ void llama_forward(bool order_s, const int32_t* ids, int T, const bpd_llama_weig
             mt_layer<float>(c, x, w->layers[l], reinterpret_cast<float*>(kc) + l * layer_elems,
                             reinterpret_cast<float*>(vc) + l * layer_elems, s1, s2, s3, add_in, true);
     }
-    launch_norm(x, L > 0 ? s3 : nullptr, L > 0 ? x : nullptr, w->output_norm_w, s1, c.xq, g.E, g.eps, c.s, nullptr,
-                T);
+    launch_norm(x, L > 0 ? s3 : nullptr, L > 0 ? x : nullptr, w->output_norm_w, nullptr, c.xq, g.E, g.eps, c.s,
+                nullptr, T);
     mt_gemm(c, w->output_w, logits, NV, g.E);
     hipLaunchKernelGGL(k_argmax<1024>, dim3(T), dim3(1024), 0, c.s, logits, NV, nullptr, tok);
     abi_hip_ok(hipGetLastError(), fn);
