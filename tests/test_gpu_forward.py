@@ -162,6 +162,16 @@ def test_forward_long_context(kind):
     _forward_case(cfg, kind, True, [(3, 1100)], fill=1100)
 
 
+@pytest.mark.parametrize("kind", ["avx", "scalar"])
+def test_forward_attention_in_token_chunks(kind):
+    """300 tokens at positions 7,800-8,099 over a binary16 cache whose first 7,800 rows
+    hold random data: the scores of one attention launch are capped at 64 MiB (8 heads x
+    8,128 rows x 4 bytes per token: 258 tokens), so the batch's attention runs in two
+    launches of the tile kernels, the second at kv_pos + 258."""
+    cfg = config(L=1, E=256, H=8, HKV=2, D=32, F=256, V=128, S=8192)
+    _forward_case(cfg, kind, False, [(300, 7800)], fill=7800)
+
+
 def test_forward_fp32_cache_tokens():
     """fp32 caches: bpd_llama_forward_cpu steps between layers by half an fp32
     layer (its uint16_t pointer arithmetic), so only logits and tokens are
