@@ -213,7 +213,6 @@ struct Cache<float> {
     static __device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
     static __device__ __forceinline__ void st(float* p, float v) { *p = v; }
     static __device__ __forceinline__ float rt(float v) { return v; }  // the value as read back
-    static __device__ __forceinline__ float cvt1(float r) { return r; }
 };
 __device__ __forceinline__ uint32_t f32_to_f16_ref(float v) {
     const uint32_t u = __float_as_uint(v);
@@ -234,7 +233,6 @@ struct Cache<uint16_t> {
     static __device__ __forceinline__ float4 ld4(const uint16_t* p) { return cvt(ldr(p)); }
     static __device__ __forceinline__ void st(uint16_t* p, float v) { *p = (uint16_t)f32_to_f16_ref(v); }
     static __device__ __forceinline__ float rt(float v) { return f16_to_f32_ref(f32_to_f16_ref(v)); }
-    static __device__ __forceinline__ float cvt1(uint16_t r) { return f16_to_f32_ref(r); }
 };
 
 struct AttnIn {
@@ -1127,7 +1125,6 @@ __global__ __launch_bounds__(64 * kMaxGroup) void k_mt_scores_tile(const float* 
 
 constexpr int kMtSmThreads = 512;  // thread p: row quad p % 16 of tokens p / 16 and p / 16 + 32
 constexpr int kMtSmGroup = 8;      // 64-row chunks of e in LDS at once
-constexpr int kMtEP = kScoreRows + 4;  // LDS pitch of a token's chunk of weights (P.V)
 
 // LDS pitch of a token's e rows in k_mt_softmax: a group of up to kMtSmGroup
 // chunks plus 4 floats, so the chain lanes' float4 reads (one token each, rows
