@@ -100,7 +100,10 @@ def test_llamafile_path(dev, mw, mt, K):
 # ------------------------------------------------- prefill GEMM, scalar order S (int8 MFMA)
 
 @pytest.mark.parametrize("mw,mt,K", [(4, 2, 128), (7, 5, 128), (130, 129, 4096 + 32), (1, 1, 32), (256, 256, 64),
-                                     (300, 17, 224), (2048, 64, 2048)])
+                                     (300, 17, 224), (2048, 64, 2048),
+                                     # the 64-row form (one workgroup of 8 waves per CU), the last
+                                     # with a ragged row panel
+                                     (8192, 256, 512), (8192, 256, 384), (4100, 512, 768)])
 def test_dispatch_scalar_order(dev, mw, mt, K):
     W = synth.q8_0(mw, K, synth.key(43, 7))
     X = synth.normal_f32(mt * K, synth.key(43, 8))
@@ -127,7 +130,7 @@ def test_dispatch_scalar_order_unaligned_operands(dev, wo, xo):
     assert_bits_equal(got, O.dispatch_q8_0(W, Xq, mw, mt, K, "S", nthreads=8), f"S-order offsets {wo},{xo}")
 
 
-@pytest.mark.parametrize("mw,mt,K", [(130, 129, 512), (7, 7, 96), (256, 130, 4096), (23, 5, 224)])
+@pytest.mark.parametrize("mw,mt,K", [(130, 129, 512), (7, 7, 96), (256, 130, 4096), (23, 5, 224), (4100, 512, 256)])
 def test_dispatch_scalar_order_dense_special_scales(dev, mw, mt, K):
     """Order S (the prefill GEMM's int8-MFMA kernels and the plain one) on dense NaN / Inf
     scales with zero 4-element groups: every cell, NaN bits included, equals the oracle,

@@ -560,7 +560,7 @@ def test_fused_quantization_covers_x_and_stays_in_bounds(rows):
 # ---------------------------------------------------------------- Q8_0 S-order GEMM, coalesced staging
 
 @pytest.mark.parametrize("mw,mt,K", [(14336, 512, 4096), (130, 129, 4096), (1, 1, 128), (300, 17, 384), (256, 256, 128),
-                                     (7, 5, 14336), (225, 3, 256)])
+                                     (7, 5, 14336), (225, 3, 256), (4096, 512, 14336), (4100, 512, 768)])
 @pytest.mark.parametrize("RT", [4, 2, 1])
 @pytest.mark.parametrize("CT", [2, 1])
 def test_q8_0_gemm_SH_in_bounds(mw, mt, K, RT, CT):
