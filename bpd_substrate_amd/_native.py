@@ -60,6 +60,7 @@ HIP_SIGNATURES = {
     "bpd_q8_pad64_from_f32_gpu": (None, [P, P, I, I]),
     "bpd_qmatmul_q8_pad64_gpu": (None, [P, P, P, I, I, I]),
     "bpd_dequant_q6k_gpu": (None, [P, P, I]),
+    "bpd_dequant_gguf_py_gpu": (None, [P, P, ctypes.c_int64, I]),
     "bpd_dequant_q6k_gguf_gpu": (None, [P, P, I]),
     "bpd_qmatmul_q6k_q8k_gpu": (None, [P, P, P, I, I]),
     "bpd_qmatmul_q6k_q8k_gguf_gpu": (None, [P, P, P, I, I]),

@@ -3,6 +3,7 @@
 // CPU: every numeric result comes from a gfx950 kernel.
 #include <hip/hip_runtime.h>
 
+#include <climits>
 #include <cstdio>
 #include <cstring>
 #include <mutex>
@@ -413,6 +414,41 @@ void bpd_qmatmul_q6k_q8k_gpu(const uint8_t* w, const uint8_t* xq, float* y, int 
 }
 void bpd_qmatmul_q6k_q8k_gguf_gpu(const uint8_t* w, const uint8_t* xq, float* y, int M, int K) {
     q6k_q8k(w, xq, y, M, K, 1, "bpd_qmatmul_q6k_q8k_gguf_gpu");
+}
+
+// ---- the reference Python loader's per-type fp32 (load_tensor_by_type) ---------
+void bpd_dequant_gguf_py_gpu(const uint8_t* src, float* out, int64_t n_elements, int ggml_type) {
+    const char* fn = "bpd_dequant_gguf_py_gpu";
+    Check c(fn);
+    int per = 0;
+    switch (ggml_type) {
+        case 0:
+        case 1: per = 1; break;
+        case 2: per = 32; break;
+        case 10:
+        case 11:
+        case 12:
+        case 14: per = 256; break;
+        default: {
+            char buf[96];
+            std::snprintf(buf, sizeof buf, "ggml_type %d has no loader formula", ggml_type);
+            set_err(BPDQ_ERR_SHAPE, fn, buf);
+            return;
+        }
+    }
+    if (n_elements < 0) return c.fail(BPDQ_ERR_SHAPE, "n_elements", "is negative");
+    if (n_elements % per != 0) {
+        char buf[96];
+        std::snprintf(buf, sizeof buf, "n_elements=%lld is not a multiple of %d", (long long)n_elements, per);
+        set_err(BPDQ_ERR_SHAPE, fn, buf);
+        return;
+    }
+    if (ggml_type == 14 && n_elements / 256 > INT_MAX) return c.fail(BPDQ_ERR_SHAPE, "n_elements", "is too large");
+    if (n_elements == 0) return;
+    c.ptr(src, ggml_type == 14 ? 2 : 1, "src").ptr(out, 16, "out");
+    if (!c.ok) return;
+    bpdq::launch_dequant_gguf_py(src, out, n_elements, ggml_type, g_stream);
+    check_launch(fn);
 }
 
 // ---- Q8 padded 64-byte layout (the reference's dp4a weight layout) -----------

@@ -70,6 +70,9 @@ void launch_q4k_norm_multi(const uint8_t* const* w, float* const* y, const int* 
 int launch_q4k_res(const uint8_t* w, int M, const float* x, int K, const ResOut& ro, int order, hipStream_t s);
 
 void launch_dequant_q6k(const uint8_t* q, float* out, int n_blocks, int order, hipStream_t s);
+// the reference Python loader's fp32 of a GGUF tensor (gguf_py.hip); false for a
+// type it has no formula for
+bool launch_dequant_gguf_py(const uint8_t* src, float* out, int64_t n_elements, int ggml_type, hipStream_t s);
 void launch_qmatmul_q6k_q8k(const uint8_t* w, const uint8_t* xq, float* y, int M, int K, int order, hipStream_t s);
 
 void launch_dequant_q8_0(const uint8_t* raw, float* out, int n_blocks, hipStream_t s);

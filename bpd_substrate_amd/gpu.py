@@ -222,6 +222,29 @@ def qmatmul_q8_pad64(Wp, Xq, m_weight, m_tokens, K, out=None):
     return out
 
 
+# ---------------------------------------------------------------- the reference Python loader
+
+# elements and bytes per block of the types load_tensor_by_type dequantizes
+# (inference/llamatov_helpers.py:196-222)
+GGUF_PY_BLOCKS = {0: (1, 4), 1: (1, 2), 2: (32, 18), 10: (256, 84), 11: (256, 110), 12: (256, 144), 14: (256, 210)}
+
+
+def dequant_gguf_py(raw, n_elements, ggml_type, out=None):
+    """raw: uint8 device tensor of a GGUF tensor's bytes -> fp32 [n_elements] with the
+    reference Python loader's formula for ggml_type (bpd_dequant_gguf_py_gpu)."""
+    import torch
+
+    if ggml_type not in GGUF_PY_BLOCKS:
+        raise ValueError(f"ggml_type {ggml_type} has no loader formula")
+    per, size = GGUF_PY_BLOCKS[ggml_type]
+    out = _empty(n_elements, torch.float32, raw) if out is None else out
+    _need(raw, n_elements // per * size, "raw")
+    _need(out, n_elements * 4, "out")
+    _use_torch_stream()
+    call("bpd_dequant_gguf_py_gpu", raw, out, n_elements, ggml_type)
+    return out
+
+
 # ---------------------------------------------------------------- Q6_K
 
 def dequant_q6k(q, order=formats.ORDER_BPD, out=None):

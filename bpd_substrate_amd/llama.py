@@ -272,33 +272,79 @@ class Forward:
 # the {arch}.* metadata into ModelConfig and every blk.N.* tensor into
 # LayerWeights, dequantizing each tensor type on the host
 # (inference/llamatov_helpers.py:195-222) and re-quantizing to the padded Q8
-# layout.  Here the bytes go to the device unchanged and each matrix keeps its
-# own format: Q4_K and Q6_K run as themselves (GGUF element map), an all-Q8_0
-# model takes the padded Q8 layout.
+# layout.  Two loaders here:
+# * native: the bytes go to the device unchanged and each matrix keeps its own
+#   format: Q4_K and Q6_K run as themselves (GGUF element map), an all-Q8_0 model
+#   takes the padded Q8 layout;
+# * reference: the reference driver's weights, for every type its loader reads
+#   (F32, F16, Q4_0, Q2_K, Q3_K, Q4_K, Q6_K): each matrix and the head dequantized
+#   on the device with load_tensor_by_type's formulas (bpd_dequant_gguf_py_gpu),
+#   then re-quantized to the padded Q8 layout (bpd_q8_pad64_from_f32_gpu, the
+#   reference's q8_pad64_coalesced), and the token table kept in fp32.
+#   load_tensor_by_type has no Q8_0 branch (it returns zeros for it); Q8_0
+#   tensors take the reference C's Q8_0 dequant (bpd_dequant_q8_0_gpu) instead.
+# loader="auto" takes the native one when every matrix is Q4_K, Q6_K or Q8_0 in
+# a combination the step runs, else the reference one.
+
+# the GGUF types the reference loader reads (load_tensor_by_type), and Q8_0
+PY_TYPES = (0, 1, 2, 10, 11, 12, 14)
+
+
+def load_tensor_by_type(path, offset, n_elements, shape, type_code, device):
+    """inference/llamatov_helpers.py:196-222 with the dequant on `device`: the tensor of
+    `n_elements` at byte `offset` of the file as an fp32 device tensor of `shape`.  An
+    unknown type gives zeros and a warning, as the reference's does."""
+    import numpy as np
+    import torch
+
+    if type_code not in PY_TYPES:
+        print(f"  WARN: unknown type code {type_code}, using zeros")
+        return torch.zeros(shape, dtype=torch.float32, device=device)
+    per, size = gpu.GGUF_PY_BLOCKS[type_code]
+    raw = np.fromfile(path, dtype=np.uint8, count=n_elements // per * size, offset=offset)
+    out = gpu.dequant_gguf_py(torch.from_numpy(raw).to(device), n_elements, type_code)
+    return out.reshape(shape)
 
 _GGUF_MATS = (("q", "attn_q"), ("k", "attn_k"), ("v", "attn_v"), ("o", "attn_output"),
               ("gate", "ffn_gate"), ("up", "ffn_up"), ("down", "ffn_down"))
 
 
-def _gguf_format(t):
+def _gguf_format(t, loader="native"):
     from . import gguf
 
+    if loader == "reference":
+        if t.type in PY_TYPES or t.type == gguf.Q8_0:
+            return W_Q8_PAD64
+        raise gguf.GGUFError(f"{t.name}: type {t.type_name} has no loader formula "
+                             "(F32, F16, Q4_0, Q2_K, Q3_K, Q4_K, Q6_K, Q8_0)")
     if t.type == gguf.Q4_K:
         return W_Q4K_GGUF
     if t.type == gguf.Q6_K:
         return W_Q6K_GGUF
     if t.type == gguf.Q8_0:
         return W_Q8_PAD64
-    raise gguf.GGUFError(f"{t.name}: type {t.type_name} is not a decode-step weight format (Q4_K, Q6_K, Q8_0)")
+    raise gguf.GGUFError(f"{t.name}: type {t.type_name} is not a decode-step weight format (Q4_K, Q6_K, Q8_0); "
+                         "loader='reference' reads it")
 
 
-def gguf_plan(g, max_seq=2048):
+def gguf_plan(g, max_seq=2048, loader="auto"):
     """Host-side reading of a parsed GGUF (gguf.GGUF) as a decode model: returns
     dict(cfg, layers=[{matrix: (tensor, format), norms, biases}], head=(tensor, format or
-    None for fp32), embd=tensor, out_norm=tensor, rope_dim, rope_freqs=tensor or None).
-    Raises gguf.GGUFError for a missing tensor, a shape that does not match the
-    metadata, or formats the step cannot combine."""
+    None for fp32), embd=tensor, out_norm=tensor, rope_dim, rope_freqs=tensor or None,
+    loader="native" or "reference").  Raises gguf.GGUFError for a missing tensor, a shape
+    that does not match the metadata, or formats the loader cannot take."""
     from . import gguf
+
+    if loader not in ("auto", "native", "reference"):
+        raise ValueError(f"loader {loader!r}: 'auto', 'native' or 'reference'")
+    if loader == "auto":
+        try:
+            return gguf_plan(g, max_seq, "native")
+        except gguf.GGUFError as e:
+            try:
+                return gguf_plan(g, max_seq, "reference")
+            except gguf.GGUFError:
+                raise e from None
 
     md = g.metadata
     arch = md.get("general.architecture", "llama")
@@ -337,13 +383,19 @@ def gguf_plan(g, max_seq=2048):
         lw = {"attn_norm": need(f"{p}.attn_norm.weight", (E,)), "ffn_norm": need(f"{p}.ffn_norm.weight", (E,))}
         for m, gname in _GGUF_MATS:
             t = need(f"{p}.{gname}.weight", rdims[m])
-            lw[m] = (t, _gguf_format(t))
+            lw[m] = (t, _gguf_format(t, loader))
         for b, gname, n in (("q_bias", "attn_q", H * D), ("k_bias", "attn_k", HKV * D), ("v_bias", "attn_v", HKV * D)):
             key = f"{p}.{gname}.bias"
             lw[b] = need(key, (n,)) if key in g.by_name else None
         layers.append(lw)
     need(head_t.name, (E, V))
-    head_fmt = None if head_t.type in (0, 1) else _gguf_format(head_t)
+    if loader == "reference":  # the reference's head: output.weight or token_embd, in the padded layout
+        head_fmt = _gguf_format(head_t, loader)
+        emb_t = need("token_embd.weight", (E, V))
+        if emb_t.type not in PY_TYPES and emb_t.type != gguf.Q8_0:
+            raise gguf.GGUFError(f"token_embd.weight: type {emb_t.type_name} has no loader formula")
+    else:
+        head_fmt = None if head_t.type in (0, 1) else _gguf_format(head_t)
     fmts = {f for lw in layers for m, _ in _GGUF_MATS for f in [lw[m][1]]} | ({head_fmt} - {None})
     if W_Q8_PAD64 in fmts and len(fmts) > 1:
         raise gguf.GGUFError("Q8_0 matrices cannot be combined with K-quant ones in one decode step")
@@ -351,7 +403,7 @@ def gguf_plan(g, max_seq=2048):
     if rf is not None and tuple(rf.dims) != (rope_dim // 2,):
         raise gguf.GGUFError(f"rope_freqs.weight has dims {rf.dims}, expected ({rope_dim // 2},)")
     return dict(cfg=cfg, layers=layers, head=(head_t, head_fmt), embd=need("token_embd.weight", (E, V)),
-                out_norm=need("output_norm.weight", (E,)), rope_dim=rope_dim, rope_freqs=rf)
+                out_norm=need("output_norm.weight", (E,)), rope_dim=rope_dim, rope_freqs=rf, loader=loader)
 
 
 def _f32_tensor(g, t, device):
@@ -368,20 +420,35 @@ def _f32_tensor(g, t, device):
     return torch.from_numpy(a.copy()).to(device)
 
 
-def from_gguf(path, device, max_seq=2048, kv_cache_f16=False):
-    """A DecodeModel of the GGUF file at `path` (see gguf_plan), with
-    .embed(token_id) -> the token's fp32 embedding row on the device."""
+def _f32_of(g, t, device):
+    """fp32 of a GGUF tensor on the device as the reference loader computes it
+    (Q8_0: the reference C's dequant)."""
+    from . import gguf
+
+    raw = g.to_device(t.name, device)
+    n = t.n_elements
+    if t.type == gguf.Q8_0:
+        return gpu.dequant_q8_0(raw)
+    return gpu.dequant_gguf_py(raw, n, t.type)
+
+
+def from_gguf(path, device, max_seq=2048, kv_cache_f16=False, loader="auto"):
+    """A DecodeModel of the GGUF file at `path` (see gguf_plan and the loaders above),
+    with .embed(token_id) -> the token's fp32 embedding row on the device."""
     import numpy as np
 
     from . import formats as fm
     from . import gguf
 
     g = gguf.open_gguf(path)
-    plan = gguf_plan(g, max_seq)
+    plan = gguf_plan(g, max_seq, loader)
     cfg = plan["cfg"]
     E = cfg["n_embd"]
+    ref = plan["loader"] == "reference"
 
     def weight(t, f):
+        if ref:  # fp32, then the reference's q8_pad64_coalesced, rows = dims[1]
+            return gpu.q8_pad64(_f32_of(g, t, device), t.dims[1], t.dims[0])
         if f != W_Q8_PAD64:
             return g.to_device(t.name, device)
         import torch   # Q8_0 rows -> the padded layout of the padded-Q8 step
@@ -405,12 +472,16 @@ def from_gguf(path, device, max_seq=2048, kv_cache_f16=False):
     freqs = None
     if plan["rope_freqs"] is not None:
         freqs = np.frombuffer(g.tensor_bytes(plan["rope_freqs"].name), np.uint8).view(np.float32).copy()
+    # the reference loader's model is all padded Q8: the reference's own generate_token
+    # ABI unless RoPE options or binary16 caches need the extended step
     m = DecodeModel(cfg, layers, _f32_tensor(g, plan["out_norm"], device), lm_head=lm, lm_f32=lm_f32,
-                    lm_N=head_t.dims[1], fmt=base, device=device, formats=formats,
-                    lm_format=head_fmt if head_fmt is not None else base, rope_dim=plan["rope_dim"],
+                    lm_N=head_t.dims[1], fmt=base, device=device, formats=None if ref else formats,
+                    lm_format=None if ref else (head_fmt if head_fmt is not None else base),
+                    rope_dim=None if ref and plan["rope_dim"] == cfg["head_dim"] else plan["rope_dim"],
                     rope_freqs=freqs, kv_cache_f16=kv_cache_f16)
     m.gguf, m.plan = g, plan
     m._embd = g.to_device(plan["embd"].name, device)
+    m._embd_f32 = _f32_of(g, plan["embd"], device) if ref else None
     return m
 
 
@@ -427,7 +498,9 @@ def _embed(self, token):
         raise ValueError(f"token {token} outside 0..{t.dims[1] - 1}")
     gpu._use_torch_stream()
     out = torch.empty(E, dtype=torch.float32, device=self._embd.device)
-    if t.type == gguf.Q8_0:
+    if getattr(self, "_embd_f32", None) is not None:  # the reference loader's fp32 table
+        out.copy_(self._embd_f32[token * E:(token + 1) * E])
+    elif t.type == gguf.Q8_0:
         ids = torch.tensor([token], dtype=torch.int32, device=self._embd.device)
         gpu.call("bpd_embed_lookup_q8_0_gpu", self._embd, ids, out, 1, E)
     elif t.type in (gguf.Q4_K, gguf.Q6_K):

@@ -147,6 +147,17 @@ void bpd_dequant_q6k_gguf_gpu(const uint8_t* q_dev, float* out_dev, int n_blocks
 void bpd_qmatmul_q6k_q8k_gpu(const uint8_t* w_dev, const uint8_t* xq8k_dev, float* y_dev, int M, int K);
 void bpd_qmatmul_q6k_q8k_gguf_gpu(const uint8_t* w_dev, const uint8_t* xq8k_dev, float* y_dev, int M, int K);
 
+/* ---- the reference Python loader's fp32 of a GGUF tensor ----
+ * load_tensor_by_type (inference/llamatov_helpers.py:196-222) on the device: out[n_elements] in
+ * fp32 from the tensor's bytes, with the Python's formulas, element maps and float32 operation
+ * order, NaN bits as numpy gives them on x86.  ggml_type: 0 F32, 1 F16 (astype, :205-207),
+ * 2 Q4_0 (:71-98), 10 Q2_K (:25-39), 11 Q3_K (the reference's approximate form, :42-68),
+ * 12 Q4_K (its own element map, :101-158), 14 Q6_K (:161-179, as bpd_dequant_q6k_gpu).
+ * The reference returns zeros for any other type; here that is BPDQ_ERR_SHAPE, nothing written.
+ * n_elements a multiple of the type's block (1, 32 or 256); out 16-byte aligned; src any
+ * alignment (2 bytes for Q6_K). */
+void bpd_dequant_gguf_py_gpu(const uint8_t* src_dev, float* out_dev, int64_t n_elements, int ggml_type);
+
 /* ---- Q8_0 on the GPU, same signatures as the CPU functions they mirror ---- */
 void bpd_dequant_q8_0_gpu(const uint8_t* raw_dev, float* out_dev, int n_blocks);           /* bench/bpd_cpu.c:3960 */
 /* ids must index rows of the table (0 <= id < rows); bench/bpd_cpu.c:4002 */

@@ -388,6 +388,101 @@ void bpdq_o_dequant_q6k(const uint8_t* q, float* out, int n_blocks, int order) {
     }
 }
 
+/* ------------------------------------- the reference Python loader ---- */
+
+/* load_tensor_by_type (inference/llamatov_helpers.py:196-222) turns each GGUF
+ * tensor into fp32 with numpy float32 arithmetic: binary16 through astype (the
+ * exact value; a NaN keeps its payload and its signalling bit), every product
+ * and difference one float32 operation with the left operand of the Python
+ * expression first, under x86's NaN rules (x86_mul / x86_sub).  Q6_K is
+ * bpdq_o_dequant_q6k order 0. */
+static inline float x86_sub(float first, float second) {
+    float r = first - second;
+    return isnan(r) ? x86_nan_of(first, second) : r;
+}
+
+/* numpy's float16 -> float32 (astype): sign, exponent 255 and the payload
+ * shifted up for Inf / NaN, no quiet bit added; finite values exactly. */
+float bpdq_o_f16_numpy(uint16_t h) {
+    uint32_t s = (uint32_t)(h & 0x8000u) << 16, e = (h >> 10) & 31u, m = h & 1023u;
+    if (e == 31) return bits_f32(s | 0x7F800000u | (m << 13));
+    float v = e ? ldexpf((float)(m | 1024u), (int)e - 25) : ldexpf((float)m, -24);
+    return bits_f32(f32_bits(v) | s);
+}
+
+/* TYPE_F16 (:205-207). */
+void bpdq_o_dequant_f16(const uint16_t* h, float* out, int64_t n) {
+    for (int64_t i = 0; i < n; i++) out[i] = bpdq_o_f16_numpy(h[i]);
+}
+
+/* dequant_q4_0 (:71-98), 18-byte blocks {f16 d, u8 qs[16]}: element e < 16 is
+ * the low nibble of qs[e], element 16 + e the high one; y = d * (q - 8.0). */
+void bpdq_o_dequant_q4_0(const uint8_t* q, float* out, int n_blocks) {
+    for (int b = 0; b < n_blocks; b++) {
+        const uint8_t* blk = q + (size_t)b * 18;
+        const float d = bpdq_o_f16_numpy(rd16(blk));
+        for (int e = 0; e < 32; e++) {
+            const int v = e < 16 ? (blk[2 + e] & 15) : (blk[2 + e - 16] >> 4);
+            out[(size_t)b * 32 + e] = x86_mul(d, (float)v - 8.0f);
+        }
+    }
+}
+
+/* The 2-bit field of element e (0..255) in the Python loader's unpack: bits
+ * 2(e%4)..+1 of qs[e/4] (np.stack([(qs >> 2i) & 3], -1).reshape). */
+static inline int py_q2(const uint8_t* qs, int e) { return (qs[e >> 2] >> (2 * (e & 3))) & 3; }
+
+/* dequant_q2_k (:25-39), 84-byte blocks {u8 scales[16], u8 qs[64], f16 d, f16
+ * dmin}: sc = (scales[i] & 15) * d, mn = (scales[i] >> 4) * dmin, y = sc * q - mn
+ * with i = e / 16 and q the Python unpack's 2-bit field. */
+void bpdq_o_dequant_q2k_py(const uint8_t* q, float* out, int n_blocks) {
+    for (int b = 0; b < n_blocks; b++) {
+        const uint8_t* blk = q + (size_t)b * 84;
+        const float d = bpdq_o_f16_numpy(rd16(blk + 80)), dm = bpdq_o_f16_numpy(rd16(blk + 82));
+        for (int e = 0; e < 256; e++) {
+            const int sb = blk[e / 16];
+            const float sc = x86_mul((float)(sb & 15), d), mn = x86_mul((float)(sb >> 4), dm);
+            out[(size_t)b * 256 + e] = x86_sub(x86_mul(sc, (float)py_q2(blk + 16, e)), mn);
+        }
+    }
+}
+
+/* dequant_q3_k (:42-68, the approximate form the reference itself marks as
+ * such), 110-byte blocks {u8 hmask[32], u8 qs[64], u8 scales[12], f16 d}:
+ * scale i < 8 = (scales[i] & 15) - 8, scale 8 + i = (scales[i] >> 4) - 8 (bytes
+ * 8..11 unused); quant = q_lo + 4 * hbit - 4 with q_lo the 2-bit field and hbit
+ * bit e%8 of hmask[e/8]; y = (d * scale[e/16]) * quant. */
+void bpdq_o_dequant_q3k_py(const uint8_t* q, float* out, int n_blocks) {
+    for (int b = 0; b < n_blocks; b++) {
+        const uint8_t* blk = q + (size_t)b * 110;
+        const float d = bpdq_o_f16_numpy(rd16(blk + 108));
+        for (int e = 0; e < 256; e++) {
+            const int i = e / 16, sbyte = blk[96 + (i & 7)];
+            const float scale = (float)(i < 8 ? (sbyte & 15) : (sbyte >> 4)) - 8.0f;
+            const float quant = (float)py_q2(blk + 32, e) + (float)((blk[e >> 3] >> (e & 7)) & 1) * 4.0f - 4.0f;
+            out[(size_t)b * 256 + e] = x86_mul(x86_mul(d, scale), quant);
+        }
+    }
+}
+
+/* dequant_q4_k (:101-158): the 6-bit scales and mins of bench/bpd_quant.c:56-62,
+ * and the Python loader's own element map: element e < 128 is the low nibble
+ * of qs[e] in sub-block e/32, element 128 + e the high nibble of qs[e] in
+ * sub-block 4 + e/32; y = ((d * sc) * q) - (dmin * m). */
+void bpdq_o_dequant_q4k_py(const uint8_t* q, float* out, int n_blocks) {
+    for (int b = 0; b < n_blocks; b++) {
+        const uint8_t* blk = q + (size_t)b * 144;
+        const float d = bpdq_o_f16_numpy(rd16(blk)), dmin = bpdq_o_f16_numpy(rd16(blk + 2));
+        for (int e = 0; e < 256; e++) {
+            const int hi = e >= 128, i = e & 127, j = (hi ? 4 : 0) + i / 32;
+            int sc, m;
+            q4k_scale_min(blk + 4, j, &sc, &m);
+            const int v = hi ? blk[16 + i] >> 4 : blk[16 + i] & 15;
+            out[(size_t)b * 256 + e] = x86_sub(x86_mul(x86_mul(d, (float)sc), (float)v), x86_mul(dmin, (float)m));
+        }
+    }
+}
+
 /* Q6_K x Q8_K (no reference code; the reference dequantizes Q6_K to fp32 in
  * Python): I_b = sum over the 16 groups g of sc[g] * sum_{e in g} q_e * x_e,
  * exact in int32; c_b = RN(RN(d*dy) * float(I_b)); then the fixed fp32 order of

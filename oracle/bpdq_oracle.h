@@ -42,6 +42,15 @@ void bpdq_o_qmatmul_q6k_q8k(const uint8_t* w, const uint8_t* xq, float* y, int M
 
 void bpdq_o_q8_pad64(const float* x, uint8_t* out, int N, int K);   /* inference/llamatov_c_inference.py:88-100 */
 
+/* the reference Python loader's per-type fp32 dequant (inference/llamatov_helpers.py:196-222):
+ * binary16 as numpy's astype, numpy float32 arithmetic in the expressions' order, x86 NaN bits */
+float bpdq_o_f16_numpy(uint16_t h);
+void bpdq_o_dequant_f16(const uint16_t* h, float* out, int64_t n);             /* :205-207 */
+void bpdq_o_dequant_q4_0(const uint8_t* q, float* out, int n_blocks);          /* :71-98 */
+void bpdq_o_dequant_q2k_py(const uint8_t* q, float* out, int n_blocks);        /* :25-39 */
+void bpdq_o_dequant_q3k_py(const uint8_t* q, float* out, int n_blocks);        /* :42-68 */
+void bpdq_o_dequant_q4k_py(const uint8_t* q, float* out, int n_blocks);        /* :101-158 */
+
 void bpdq_o_dequant_q8_0(const uint8_t* raw, float* out, int n_blocks);                      /* bench/bpd_cpu.c:3960-3973 */
 void bpdq_o_embed_lookup_q8_0(const uint8_t* table, const int32_t* ids, float* out, int n_tokens, int embed_dim); /* :4002-4013 */
 void bpdq_o_quant_q8_0(const float* x, uint8_t* y, int n_elements);                        /* bench/bpd_cpu.c:4106-4136 */

@@ -66,6 +66,12 @@ _SIGS = {
     "bpdq_o_llama_step": (I, [I, P, P, P, P, I, P, P, P, P, I, P, P, P]),
     "bpdq_o_llama_step_ext": (I, [P, P, P, P, P, I, P, P, P, P, I, P, P, P]),
     "bpdq_o_rope_norm_freqs": (None, [P, I, I, I, F, I, P]),
+    "bpdq_o_f16_numpy": (F, [ctypes.c_uint16]),
+    "bpdq_o_dequant_f16": (None, [P, P, ctypes.c_int64]),
+    "bpdq_o_dequant_q4_0": (None, [P, P, I]),
+    "bpdq_o_dequant_q2k_py": (None, [P, P, I]),
+    "bpdq_o_dequant_q3k_py": (None, [P, P, I]),
+    "bpdq_o_dequant_q4k_py": (None, [P, P, I]),
 }
 
 _lib = None
@@ -163,6 +169,30 @@ def dequant_q6k(q, order=0):
     nb = q.size // 210
     out = np.empty(nb * 256, np.float32)
     lib().bpdq_o_dequant_q6k(_p(q), _p(out), nb, order)
+    return out
+
+
+# the reference Python loader's per-type dequant (inference/llamatov_helpers.py:196-222)
+PY_BLOCKS = {1: (1, 2), 2: (32, 18), 10: (256, 84), 11: (256, 110), 12: (256, 144), 14: (256, 210)}
+
+
+def dequant_py(raw, ggml_type):
+    """fp32 of a GGUF tensor's bytes as load_tensor_by_type computes it (F32, F16, Q4_0,
+    Q2_K, Q3_K, Q4_K, Q6_K)."""
+    raw = np.ascontiguousarray(raw, dtype=np.uint8)
+    if ggml_type == 0:
+        return raw.view(np.float32).copy()
+    per, size = PY_BLOCKS[ggml_type]
+    nb = raw.size // size
+    out = np.empty(nb * per, np.float32)
+    if ggml_type == 1:
+        lib().bpdq_o_dequant_f16(_p(raw), _p(out), nb)
+    elif ggml_type == 14:
+        lib().bpdq_o_dequant_q6k(_p(raw), _p(out), nb, 0)
+    else:
+        fn = {2: "bpdq_o_dequant_q4_0", 10: "bpdq_o_dequant_q2k_py", 11: "bpdq_o_dequant_q3k_py",
+              12: "bpdq_o_dequant_q4k_py"}[ggml_type]
+        getattr(lib(), fn)(_p(raw), _p(out), nb)
     return out
 
 

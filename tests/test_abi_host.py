@@ -108,6 +108,21 @@ def test_validation_rejects_before_launch():
     _err(2)
     L.qgpu_h2d(None, None, -1)
     _err(2)
+    # the reference Python loader's per-type dequant
+    L.bpd_dequant_gguf_py_gpu(0x1000, 0x2000, 256, 8)
+    assert "no loader formula" in _err(2)
+    L.bpd_dequant_gguf_py_gpu(0x1000, 0x2000, 300, 12)
+    assert "multiple of 256" in _err(2)
+    L.bpd_dequant_gguf_py_gpu(0x1000, 0x2000, 40, 2)
+    assert "multiple of 32" in _err(2)
+    L.bpd_dequant_gguf_py_gpu(0x1000, 0x2000, -4, 1)
+    _err(2)
+    L.bpd_dequant_gguf_py_gpu(None, 0x2000, 32, 2)
+    _err(1)
+    L.bpd_dequant_gguf_py_gpu(0x1001, 0x2008, 32, 2)
+    assert "out is not 16-byte aligned" in _err(3)
+    L.bpd_dequant_gguf_py_gpu(0x1001, 0x2000, 256, 14)
+    assert "src is not 2-byte aligned" in _err(3)
 
 
 def test_empty_calls_are_no_ops():
@@ -116,6 +131,7 @@ def test_empty_calls_are_no_ops():
     L.bpd_dequant_q4k_gpu(None, None, 0)
     L.bpd_qmatmul_q4k_q8k_gpu(None, None, None, 0, 4096)
     L.bpd_quant_q8_0_gpu(None, None, 0)
+    L.bpd_dequant_gguf_py_gpu(None, None, 0, 11)
     assert L.qgpu_alloc(0) is None
     assert L.bpd_gpu_last_error() == 0
 

@@ -55,7 +55,7 @@ def test_plan_tied_head_and_defaults(tmp_path):
     assert plan["cfg"]["max_seq"] == 2048
 
 
-@pytest.mark.parametrize("bad", ["missing", "dims", "mix", "f16_matrix", "freqs"])
+@pytest.mark.parametrize("bad", ["missing", "dims", "mix", "f16_matrix", "freqs", "q5k_matrix"])
 def test_plan_rejects(tmp_path, bad):
     cfg = LM.config(L=1, vocab=300)
     layers, head = LM.make(cfg, 2, seed=32, lm_fmt=2)
@@ -79,9 +79,11 @@ def test_plan_rejects(tmp_path, bad):
         layers[0]["o"] = LM.synth.q8_0(cfg["n_embd"], cfg["n_embd"], LM.synth.key(32, 9))
         GM.write_model(path, cfg, layers, head, embd, 2, [{"o": 0}], 2)
         match = "cannot be combined"
-    elif bad == "f16_matrix":
-        layers[0]["up"] = np.zeros(cfg["ff_dim"] * cfg["n_embd"], np.float16)
-        GM.GTYPE[99] = 1
+    elif bad in ("f16_matrix", "q5k_matrix"):
+        f16 = bad == "f16_matrix"
+        n = cfg["ff_dim"] * cfg["n_embd"]
+        layers[0]["up"] = np.zeros(n, np.float16) if f16 else np.zeros(n // 256 * 176, np.uint8)
+        GM.GTYPE[99] = 1 if f16 else 13
         try:
             GM.write_model(path, cfg, layers, head, embd, 2, [{"up": 99}], 2)
         finally:
@@ -90,5 +92,20 @@ def test_plan_rejects(tmp_path, bad):
     else:
         GM.write_model(path, cfg, layers, head, embd, 2, None, 2, rope_dim=32, rope_freqs=np.ones(8, np.float32))
         match = "rope_freqs.weight has dims"
+    g = gguf.open_gguf(path)
     with pytest.raises(gguf.GGUFError, match=match):
-        llama.gguf_plan(gguf.open_gguf(path))
+        llama.gguf_plan(g, loader="native")
+    if bad in ("mix", "f16_matrix"):
+        # the reference loader reads both (every matrix dequantized and re-quantized to
+        # the padded Q8 layout), and "auto" falls back to it
+        plan = llama.gguf_plan(g)
+        assert plan["loader"] == "reference" and plan["head"][1] == llama.W_Q8_PAD64
+        assert {f for lw in plan["layers"] for m, _ in llama._GGUF_MATS for f in [lw[m][1]]} == {llama.W_Q8_PAD64}
+    elif bad == "q5k_matrix":  # no loader reads Q5_K: "auto" reports the native loader's error
+        with pytest.raises(gguf.GGUFError, match="no loader formula"):
+            llama.gguf_plan(g, loader="reference")
+        with pytest.raises(gguf.GGUFError, match=match):
+            llama.gguf_plan(g)
+    else:
+        with pytest.raises(gguf.GGUFError, match=match):
+            llama.gguf_plan(g)

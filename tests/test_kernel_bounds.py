@@ -1063,3 +1063,49 @@ def test_q8_0_gemm_SH_tile_order(nP, nT):
         assert 0 <= bx < nP and 0 <= by < nT
         seen.add((bx, by))
     assert len(seen) == nP * nT
+
+
+# ---------------------------------------------------------------- the reference Python loader's dequant
+
+@pytest.mark.parametrize("code,per,size", [(2, 32, 18), (10, 256, 84), (11, 256, 110), (12, 256, 144)])
+@pytest.mark.parametrize("nb", [1, 3, 4099])
+def test_dequant_gguf_py_in_bounds(code, per, size, nb):
+    """k_dequant_py<TYPE>: thread t < n_quads = nb*per/4 reads only bytes of block
+    t / (per/4) and writes float4 t; every output quad written once."""
+    qpb = per // 4
+    n_quads = nb * per // 4
+    grid = (n_quads + 255) // 256 * 256
+    t = np.arange(grid)
+    t = t[t < n_quads]
+    assert np.array_equal(t, np.arange(n_quads))
+    b, e0 = t // qpb, (t % qpb) * 4
+    assert b.max() < nb
+    if code == 2:
+        offs = [np.zeros_like(e0), np.ones_like(e0)] + [np.where(e < 16, 2 + e, 2 + e - 16) for e in
+                                                        (e0, e0 + 1, e0 + 2, e0 + 3)]
+    elif code == 10:
+        offs = [np.full_like(e0, 80), np.full_like(e0, 83), e0 >> 4, 16 + (e0 >> 2)]
+    elif code == 11:
+        si = e0 >> 4
+        offs = [np.full_like(e0, 108), np.full_like(e0, 109), 96 + (si & 7), 32 + (e0 >> 2), e0 >> 3]
+    else:
+        ii = e0 & 127
+        j = np.where(e0 >= 128, 4, 0) + (ii >> 5)
+        offs = [np.full_like(e0, 0), np.full_like(e0, 3), 4 + j, 4 + j + 4, 4 + np.maximum(j - 4, 0),
+                16 + ii, 16 + ii + 3]
+    for o in offs:
+        assert o.min() >= 0 and o.max() < size
+    assert ((b * size + max(o.max() for o in offs)) < nb * size).all()
+
+
+@pytest.mark.parametrize("esize", [2, 4])
+@pytest.mark.parametrize("n", [1, 2, 3, 4, 5, 4097])
+def test_copy_f16_f32_in_bounds(esize, n):
+    """k_copy_f16_f32: thread t handles elements 4t .. 4t+cnt-1, cnt = min(4, n - 4t);
+    whole quads as one float4 store, the tail element by element; each element once."""
+    t = np.arange((n + 3) // 4)
+    cnt = np.minimum(4, n - 4 * t)
+    assert (cnt >= 1).all()
+    elems = np.concatenate([4 * tt + np.arange(c) for tt, c in zip(t, cnt)])
+    assert np.array_equal(elems, np.arange(n))
+    assert (elems * esize + esize - 1).max() < n * esize
