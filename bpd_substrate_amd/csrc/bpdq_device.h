@@ -232,6 +232,22 @@ __device__ __forceinline__ void q8_0_quad_store(float4 v, uint8_t* __restrict__ 
     if (g == 0) *reinterpret_cast<uint16_t*>(yb) = __builtin_bit_cast(uint16_t, (_Float16)d);
 }
 
+// The same bytes from 16 consecutive lanes holding 2 elements each (lane g of the
+// aligned 16-lane row holds elements 2g, 2g+1); two bytes per lane.
+__device__ __forceinline__ void q8_0_pair_store(float2 v, uint8_t* __restrict__ yb, int g) {
+    float amax = fmaxf(abs_no_nan(v.x), abs_no_nan(v.y));
+    amax = fmaxf(amax, dpp_f<0xB1>(amax));   // quad_perm [1,0,3,2]
+    amax = fmaxf(amax, dpp_f<0x4E>(amax));   // quad_perm [2,3,0,1]
+    amax = fmaxf(amax, dpp_f<0x141>(amax));  // row_half_mirror: the other quad of the 8
+    amax = fmaxf(amax, dpp_f<0x140>(amax));  // row_mirror: the other 8 of the row
+    const float d = amax / 127.0f;
+    const float id = q8_id(amax);
+    const uint32_t q0 = (uint32_t)(int)__builtin_rintf(v.x * id) & 0xFFu;
+    const uint32_t q1 = (uint32_t)(int)__builtin_rintf(v.y * id) & 0xFFu;
+    *reinterpret_cast<uint16_t*>(yb + 2 + 2 * g) = (uint16_t)(q0 | (q1 << 8));
+    if (g == 0) *reinterpret_cast<uint16_t*>(yb) = __builtin_bit_cast(uint16_t, (_Float16)d);
+}
+
 // Workgroup b of a grid of G workgroups as numbered for row order.  The
 // hardware hands workgroups to the 8 XCDs round robin (b % 8), each XCD with
 // its own L2: XCD-major numbering gives each XCD one contiguous range of rows,

@@ -1051,7 +1051,7 @@ __global__ __launch_bounds__(64 * kMaxGroup) void k_mt_scores(const float* __res
 //                     quads in registers, the order-free max, e = expf(v - m) into
 //                     LDS, lane t of wave 0 adds token t's e in row order, then the
 //                     weights w = RN(e * inv), inv = S == 0 ? 0 : 1/S, over the scores.
-//   k_mt_pv           grid (heads, 64-token blocks, 64-column slices): per 64-row
+//   k_mt_pv           grid (heads, 64-token block pairs, 64-column slices): per 64-row
 //                     chunk the weights (transposed) and the V rows in LDS; lane
 //                     (tg, cg) runs 4 tokens x 4 columns of chains
 //                     acc = RN(acc + RN(v*w)) in row order, then Q8_0(out).
@@ -1275,34 +1275,38 @@ __global__ __launch_bounds__(NT) void k_mt_softmax(float* __restrict__ sc, int l
     }
 }
 
-// k_mt_pv: grid (heads, 64-token blocks, 64-column slices), 4 waves, each
-// 32 tokens x 32 columns: lane (tg, cg) = (lane / 8, lane % 8) holds tokens
-// 4tg..4tg+3 x columns 4cg..4cg+3 of its wave's tile, 16 chains
-// acc = RN(acc + RN(v * w)) in row order.  Per row a lane reads one float4 of V
-// (its 4 columns) and one of the transposed weights (its 4 tokens), so each
-// operand feeds 4 chains and LDS carries a quarter of what one token or one
-// column per lane would need.  Chunks of 64 rows are staged in two LDS slots
-// (chunk c + 1 written while c is added): the weights the softmax left over the
-// scores, transposed to [row][token], and the V rows converted to fp32.  Rows
-// past a token's count are skipped by a select, never added.  The heaviest
-// token blocks (the last) are numbered first.
-constexpr int kPvTok = 64;   // tokens per workgroup
+// k_mt_pv: grid (heads, token-block pairs, 64-column slices), 8 waves.  Token
+// block i of a causal batch has i + 1 chunks of 64 rows, so workgroup p takes
+// block nb - 1 - p and then block p (once when they are the same): every
+// workgroup carries nb + 1 chunks of work.  Each wave holds 16 tokens x 32
+// columns of the block: lane (tg, cg) = (lane / 16, lane % 16) holds tokens
+// 4tg..4tg+3 x columns 2cg, 2cg+1, 8 chains acc = RN(acc + RN(v * w)) in row
+// order.  Per row a lane reads a float2 of V (its 2 columns) and a float4 of the
+// transposed weights (its 4 tokens).  Chunks of 64 rows are staged in two LDS
+// slots (chunk c + 1 written while c is added): the weights the softmax left over
+// the scores, transposed to [row][token], and the V rows converted to fp32.  Rows
+// past a token's count are skipped by a select, never added.  (One wave carries
+// at most half the VALU issue of its SIMD on this loop, so a block's chains are
+// spread over all 8 waves, and pairing a heavy block with a light one keeps the
+// work per workgroup even.)
+constexpr int kPvTok = 64;   // tokens per block
 constexpr int kPvCols = 64;  // columns per workgroup
+constexpr int kPvThreads2 = 512;
 
 template <typename CT>
 struct MtPvStage {
-    float4 w[4];                   // float4 f = tid + 256k: token f % 64, rows 4(f / 64)..+3
-    typename Cache<CT>::Raw v[4];  // float4 f: row f / 16, columns 4(f % 16)..+3
+    float4 w[2];                   // float4 f = tid + 512k: token f % 64, rows 4(f / 64)..+3
+    typename Cache<CT>::Raw v[2];  // float4 f: row f / 16, columns 4(f % 16)..+3
 };
 
 template <typename CT>
 __device__ __forceinline__ void mt_pv_load(MtPvStage<CT>& st, const float* __restrict__ wsc, const CT* __restrict__ vbase,
                                            int j0, int tb, int nt, int h, int H, int ld, int n_hi, int row, int ncol) {
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
+    for (int k = 0; k < 2; k++) {
         // consecutive lanes take consecutive tokens, so the transposed LDS writes
         // of a wave hit 64 different banks
-        const int f = (int)threadIdx.x + 256 * k, tt = min(f & 63, nt - 1);  // past the block: its last token
+        const int f = (int)threadIdx.x + kPvThreads2 * k, tt = min(f & 63, nt - 1);  // past the block: its last token
         st.w[k] = *reinterpret_cast<const float4*>(wsc + ((int64_t)(tb + tt) * H + h) * ld + j0 + 4 * (f >> 6));
         const int j = min(j0 + (f >> 4), n_hi - 1);  // past n_hi: a re-read, never used
         st.v[k] = Cache<CT>::ldr(vbase + (int64_t)j * row + min(4 * (f & 15), ncol - 4));
@@ -1312,8 +1316,8 @@ __device__ __forceinline__ void mt_pv_load(MtPvStage<CT>& st, const float* __res
 template <typename CT>
 __device__ __forceinline__ void mt_pv_store(const MtPvStage<CT>& st, float* Wt, float* Vs) {
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const int f = (int)threadIdx.x + 256 * k, tt = f & 63, r = 4 * (f >> 6);
+    for (int k = 0; k < 2; k++) {
+        const int f = (int)threadIdx.x + kPvThreads2 * k, tt = f & 63, r = 4 * (f >> 6);
         Wt[(r + 0) * kPvTok + tt] = st.w[k].x;
         Wt[(r + 1) * kPvTok + tt] = st.w[k].y;
         Wt[(r + 2) * kPvTok + tt] = st.w[k].z;
@@ -1322,37 +1326,32 @@ __device__ __forceinline__ void mt_pv_store(const MtPvStage<CT>& st, float* Wt, 
     }
 }
 
-__device__ __forceinline__ void pv_fma4(float (&acc)[4][4], const float4& v, const float4& w) {
+__device__ __forceinline__ void pv_fma42(float (&acc)[4][2], const float2& v, const float4& w) {
     const float wk[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
     for (int k = 0; k < 4; k++) {
         acc[k][0] = acc[k][0] + v.x * wk[k];
         acc[k][1] = acc[k][1] + v.y * wk[k];
-        acc[k][2] = acc[k][2] + v.z * wk[k];
-        acc[k][3] = acc[k][3] + v.w * wk[k];
     }
 }
 
+// Token block tb .. tb + nt - 1 of head h, columns d0 .. d0 + 63, by all 8 waves.
 template <typename CT>
-__global__ __launch_bounds__(256) void k_mt_pv(const float* __restrict__ wsc, const CT* __restrict__ vc,
-                                                float* __restrict__ out, uint8_t* __restrict__ xq, int ld, int kv_pos,
-                                                int T, int H, int HKV, int D) {
-    __shared__ __align__(16) float Wt[2][kScoreRows * kPvTok];   // [slot][row][token]
-    __shared__ __align__(16) float Vs[2][kScoreRows * kPvCols];  // [slot][row][column]
-    const int h = blockIdx.x, tb = (gridDim.y - 1 - blockIdx.y) * kPvTok, d0 = kPvCols * blockIdx.z;
+__device__ __forceinline__ void mt_pv_block(float (*Wt)[kScoreRows * kPvTok], float (*Vs)[kScoreRows * kPvCols],
+                                            const float* __restrict__ wsc, const CT* __restrict__ vc,
+                                            float* __restrict__ out, uint8_t* __restrict__ xq, int ld, int kv_pos,
+                                            int tb, int nt, int h, int H, int HKV, int D, int d0) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, th = wave >> 1, ch = wave & 1;
-    const int tg = lane >> 3, cg = lane & 7;
+    const int tg = lane >> 4, cg = lane & 15;
+    const int n_hi = kv_pos + tb + nt, nch = (n_hi + kScoreRows - 1) / kScoreRows;
     const int kvh = h / (H / HKV), row = HKV * D, ncol = min(kPvCols, D - d0);
-    const int nt = min(kPvTok, T - tb), n_hi = kv_pos + tb + nt, nch = (n_hi + kScoreRows - 1) / kScoreRows;
     const CT* vbase = vc + (int64_t)kvh * D + d0;
-    const int tw = 32 * th + 4 * tg, cw = 32 * ch + 4 * cg;  // the lane's first token and column in the block
+    const int tw = 16 * th + 4 * tg, cw = 32 * ch + 2 * cg;  // the lane's first token and column in the block
     // rows of the wave's first token, and of the lane's 4 tokens
-    const int n_wave = kv_pos + tb + 32 * th + 1, n_lane = kv_pos + tb + tw + 1;
-    float acc[4][4];
+    const int n_wave = kv_pos + tb + 16 * th + 1, n_lane = kv_pos + tb + tw + 1;
+    float acc[4][2];
 #pragma unroll
-    for (int k = 0; k < 4; k++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) acc[k][i] = 0.0f;
+    for (int k = 0; k < 4; k++) acc[k][0] = acc[k][1] = 0.0f;
     MtPvStage<CT> st;
     mt_pv_load<CT>(st, wsc, vbase, 0, tb, nt, h, H, ld, n_hi, row, ncol);
     mt_pv_store<CT>(st, Wt[0], Vs[0]);
@@ -1360,22 +1359,21 @@ __global__ __launch_bounds__(256) void k_mt_pv(const float* __restrict__ wsc, co
     __syncthreads();
     for (int c = 0; c < nch; c++) {
         const int j0 = c * kScoreRows;
-        const float4* v4 = reinterpret_cast<const float4*>(Vs[c & 1] + cw);
+        const float2* v2 = reinterpret_cast<const float2*>(Vs[c & 1] + cw);
         const float4* w4 = reinterpret_cast<const float4*>(Wt[c & 1] + tw);
         if (j0 + kScoreRows <= n_wave) {  // every token of the wave has all 64 rows (uniform)
 #pragma unroll 4
-            for (int jj = 0; jj < kScoreRows; jj++) pv_fma4(acc, v4[jj * (kPvCols / 4)], w4[jj * (kPvTok / 4)]);
-        } else if (j0 < n_wave + 31) {  // some token of the wave has rows here
+            for (int jj = 0; jj < kScoreRows; jj++) pv_fma42(acc, v2[jj * (kPvCols / 2)], w4[jj * (kPvTok / 4)]);
+        } else if (j0 < n_wave + 15) {  // some token of the wave has rows here
             for (int jj = 0; jj < kScoreRows; jj++) {
-                const float4 v = v4[jj * (kPvCols / 4)], w = w4[jj * (kPvTok / 4)];
+                const float2 v = v2[jj * (kPvCols / 2)];
+                const float4 w = w4[jj * (kPvTok / 4)];
                 const float wk[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
                     const bool on = j0 + jj < n_lane + k;  // row inside token tw + k's count
                     acc[k][0] = on ? acc[k][0] + v.x * wk[k] : acc[k][0];
                     acc[k][1] = on ? acc[k][1] + v.y * wk[k] : acc[k][1];
-                    acc[k][2] = on ? acc[k][2] + v.z * wk[k] : acc[k][2];
-                    acc[k][3] = on ? acc[k][3] + v.w * wk[k] : acc[k][3];
                 }
             }
         }
@@ -1384,16 +1382,30 @@ __global__ __launch_bounds__(256) void k_mt_pv(const float* __restrict__ wsc, co
         if (c + 2 < nch) mt_pv_load<CT>(st, wsc, vbase, (c + 2) * kScoreRows, tb, nt, h, H, ld, n_hi, row, ncol);
         __syncthreads();
     }
-    if (cw >= ncol) return;  // whole 8-lane groups (ncol is a multiple of 32)
+    if (cw >= ncol) return;  // whole 16-lane groups (ncol is a multiple of 32)
 #pragma unroll
     for (int k = 0; k < 4; k++) {
         if (tw + k >= nt) break;
         const int64_t o = ((int64_t)(tb + tw + k) * H + h) * D + d0 + cw;
-        const float4 r = make_float4(acc[k][0], acc[k][1], acc[k][2], acc[k][3]);
-        *reinterpret_cast<float4*>(out + o) = r;
-        // Q8_0 of the token's 32 columns of this wave: the 8 lanes of tg, 4 each
-        if (xq != nullptr) q8_0_quad_store(r, xq + (o >> 5) * kQ80Bytes, cg);
+        const float2 r = make_float2(acc[k][0], acc[k][1]);
+        *reinterpret_cast<float2*>(out + o) = r;
+        // Q8_0 of the token's 32 columns of this wave: the 16 lanes of tg, 2 each
+        if (xq != nullptr) q8_0_pair_store(r, xq + (o >> 5) * kQ80Bytes, cg);
     }
+}
+
+template <typename CT>
+__global__ __launch_bounds__(kPvThreads2) void k_mt_pv(const float* __restrict__ wsc, const CT* __restrict__ vc,
+                                                        float* __restrict__ out, uint8_t* __restrict__ xq, int ld,
+                                                        int kv_pos, int T, int H, int HKV, int D) {
+    __shared__ __align__(16) float Wt[2][kScoreRows * kPvTok];   // [slot][row][token]
+    __shared__ __align__(16) float Vs[2][kScoreRows * kPvCols];  // [slot][row][column]
+    const int h = blockIdx.x, p = blockIdx.y, d0 = kPvCols * blockIdx.z, nb = (T + kPvTok - 1) / kPvTok;
+    const int heavy = nb - 1 - p;
+    mt_pv_block<CT>(Wt, Vs, wsc, vc, out, xq, ld, kv_pos, heavy * kPvTok, min(kPvTok, T - heavy * kPvTok), h, H, HKV, D,
+                    d0);
+    // the last barrier of the block above ends every read of both slots
+    if (p != heavy) mt_pv_block<CT>(Wt, Vs, wsc, vc, out, xq, ld, kv_pos, p * kPvTok, kPvTok, h, H, HKV, D, d0);
 }
 
 // x = x + y over n floats (bpd_add_f32_cpu, bench/bpd_cpu.c:5466), n % 4 == 0.
@@ -2074,8 +2086,9 @@ void mt_attention(const MtCtx& c, const float* q, const CT* kc, const CT* vc, fl
             hipLaunchKernelGGL((k_mt_softmax<kMtSmThreads>), dim3(g.H, nb), dim3(kMtSmThreads),
                                mt_sm_lds((n_max + kScoreRows - 1) / kScoreRows), c.s, c.scores, c.ld, c.kv_pos + t0,
                                tn, g.H);
-            hipLaunchKernelGGL((k_mt_pv<CT>), dim3(g.H, (tn + kPvTok - 1) / kPvTok, (g.D + kPvCols - 1) / kPvCols),
-                               dim3(256), 0, c.s, c.scores, vc, o, xq, c.ld, c.kv_pos + t0, tn, g.H, g.HKV, g.D);
+            const int pairs = ((tn + kPvTok - 1) / kPvTok + 1) / 2;
+            hipLaunchKernelGGL((k_mt_pv<CT>), dim3(g.H, pairs, (g.D + kPvCols - 1) / kPvCols), dim3(kPvThreads2), 0, c.s,
+                               c.scores, vc, o, xq, c.ld, c.kv_pos + t0, tn, g.H, g.HKV, g.D);
             continue;
         }
         const size_t slds = ((size_t)kScoreRows * score_pitch(g.D) + (size_t)group * g.D + 4) * 4;

@@ -973,21 +973,33 @@ def test_mt_softmax_loads_cover_each_row_once(T, kv_pos):
             assert (lane * ep + 64 * gc <= 64 * ep).all()
 
 
-@pytest.mark.parametrize("T,kv_pos,S", [(1, 0, 64), (3, 1100, 2048), (65, 0, 256), (70, 100, 256), (512, 0, 512)])
+@pytest.mark.parametrize("T,kv_pos,S", [(1, 0, 64), (3, 1100, 2048), (65, 0, 256), (70, 100, 256), (512, 0, 512),
+                                      (130, 0, 256), (448, 64, 512)])
 @pytest.mark.parametrize("H,HKV,D", [(32, 8, 128), (4, 1, 128), (8, 2, 32)])
 def test_mt_pv_staging_in_bounds(T, kv_pos, S, H, HKV, D):
-    """k_mt_pv (64 tokens x 64 columns per workgroup, 256 threads): thread tid stages
-    float4 f = tid + 256k (k < 4) of the chunk's weights (token min(f % 64, nt - 1), rows
-    4(f / 64)..+3, in the token's score row of ld = pad64(kv_pos + T) floats) and of V
-    (row min(j0 + f / 16, n_hi - 1), columns min(4(f % 16), ncol - 4)..+3 of the slice),
-    stored transposed to [row][token] and as [row][column]; lane (tg, cg) of wave (th, ch)
-    reads its 4 tokens' and 4 columns' float4 per row; every (token, column) of the
-    block belongs to one lane."""
+    """k_mt_pv (512 threads, 64 columns per workgroup; workgroup p takes token block
+    nb - 1 - p, then block p unless it is the same one): for each block, thread tid
+    stages float4 f = tid + 512k (k < 2) of the chunk's weights (token min(f % 64,
+    nt - 1), rows 4(f / 64)..+3, in the token's score row of ld = pad64(kv_pos + T)
+    floats) and of V (row min(j0 + f / 16, n_hi - 1), columns min(4(f % 16), ncol -
+    4)..+3 of the slice), stored transposed to [row][token] and as [row][column];
+    lane (tg, cg) of wave (th, ch) reads its 4 tokens' float4 and 2 columns' float2 per
+    row; every token of the batch is one block's, every (token, column) of a block
+    one lane's, and a 32-column Q8_0 block one 16-lane row's."""
     ld = (kv_pos + T + 63) // 64 * 64
     row = HKV * D
-    tid = np.arange(256)
-    for tb in range(0, T, 64):
-        nt = min(64, T - tb)
+    tid = np.arange(512)
+    nb = (T + 63) // 64
+    token_owner = np.zeros(T, dtype=int)
+    blocks = []
+    for p in range((nb + 1) // 2):
+        heavy = nb - 1 - p
+        blocks.append((heavy * 64, min(64, T - heavy * 64)))
+        if p != heavy:
+            assert T - p * 64 >= 64  # the lighter block is whole
+            blocks.append((p * 64, 64))
+    for tb, nt in blocks:
+        token_owner[tb:tb + nt] += 1
         n_hi = kv_pos + tb + nt
         assert n_hi <= S
         nch = (n_hi + 63) // 64
@@ -997,8 +1009,8 @@ def test_mt_pv_staging_in_bounds(T, kv_pos, S, H, HKV, D):
             assert ncol % 32 == 0
             for c in range(nch):
                 j0 = 64 * c
-                for k in range(4):
-                    f = tid + 256 * k
+                for k in range(2):
+                    f = tid + 512 * k
                     tt = np.minimum(f & 63, nt - 1)
                     for h in (0, H - 1):
                         off = ((tb + tt) * H + h) * ld + j0 + 4 * (f >> 6)
@@ -1010,21 +1022,24 @@ def test_mt_pv_staging_in_bounds(T, kv_pos, S, H, HKV, D):
                         assert ((j * row + kvh * D + d0 + col + 3) < S * row).all()
                     r = 4 * (f >> 6)
                     assert ((r + 3) * 64 + (f & 63) < 64 * 64).all() and (f < 1024).all()
-                    # every (row, token) of the transposed tile written once per chunk
-                    if k == 3:
-                        ff = tid[:, None] + 256 * np.arange(4)[None, :]
-                        cells = ((4 * (ff >> 6))[..., None] + np.arange(4)) * 64 + (ff & 63)[..., None]
-                        assert np.array_equal(np.sort(cells.reshape(-1)), np.arange(64 * 64))
-            own = np.zeros((64, 64), dtype=int)
-            for wave in range(4):
-                th, ch = wave >> 1, wave & 1
-                lane = np.arange(64)
-                tw, cw = 32 * th + 4 * (lane >> 3), 32 * ch + 4 * (lane & 7)
-                assert (63 * 16 + (cw + 3) // 4 < 1024).all() and (63 * 16 + (tw + 3) // 4 < 1024).all()
-                for k in range(4):
-                    for i in range(4):
-                        np.add.at(own, (tw + k, cw + i), 1)
-            assert (own == 1).all()
+            ff = tid[:, None] + 512 * np.arange(2)[None, :]
+            cells = ((4 * (ff >> 6))[..., None] + np.arange(4)) * 64 + (ff & 63)[..., None]
+            assert np.array_equal(np.sort(cells.reshape(-1)), np.arange(64 * 64))
+    assert (token_owner == 1).all()
+    own = np.zeros((64, 64), dtype=int)
+    for wave in range(8):
+        th, ch = wave >> 1, wave & 1
+        lane = np.arange(64)
+        tw, cw = 16 * th + 4 * (lane >> 4), 32 * ch + 2 * (lane & 15)
+        assert (63 * 32 + (cw + 1) // 2 < 2048).all() and (63 * 16 + (tw + 3) // 4 < 1024).all()
+        # the 16 lanes of one tg hold one token's 32 columns 32ch .. 32ch + 31
+        for g in range(4):
+            cols = cw[lane >> 4 == g]
+            assert np.array_equal(np.sort(np.concatenate([cols, cols + 1])), np.arange(32 * ch, 32 * ch + 32))
+        for k in range(4):
+            for i in range(2):
+                np.add.at(own, (tw + k, cw + i), 1)
+    assert (own == 1).all()
 
 
 @pytest.mark.parametrize("G", [1, 2, 3, 4, 5, 8, 12])
